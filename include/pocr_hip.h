@@ -1,0 +1,217 @@
+/*
+ * pocr_hip.h — C ABI of the MI355X (gfx950) ERNIE text-decoder step.
+ *
+ * This is the drop-in boundary a `hip` implementation of RapidOCRvl's
+ * internal/backend package binds through cgo.  Plain pointers and sizes only.
+ *
+ * Conventions (mirroring internal/backend/vulkan_exec_stub.go:14-328):
+ *  - Every call returns an int status.  POCR_OK (0) on success.
+ *    POCR_ERR_ARG: shape/length/handle problem detected BEFORE any device work;
+ *      the Go caller must return the error without disabling the op
+ *      (internal/model/vulkan_fallback_test.go:167-290).
+ *    POCR_ERR_DEVICE / POCR_ERR_NOMEM / POCR_ERR_INJECTED: device-side failure;
+ *      the Go caller disables the op and falls back to the CPU kernels
+ *      (internal/model/model.go:7240-7258 disableVulkanOp).
+ *  - pocr_last_error() returns the calling thread's last message.
+ *  - Op-level calls borrow host slices for the duration of the call and are
+ *    synchronous, like the backend.Vulkan* functions.
+ *  - Weights are uploaded once, in the GGUF Q*_ROW row layout
+ *    (internal/gguf/gguf.go:446-464,506-520,544-558): rows × f32 scale, then
+ *    rows × packed row bytes.  Handles replace the Vulkan backend's
+ *    host-pointer fingerprint cache (internal/backend/vulkan_cache_windows.go:7-98).
+ *  - Thread safety: a context serialises device work on its own stream; a
+ *    sequence must not be used by two threads at once.
+ */
+#ifndef POCR_HIP_H
+#define POCR_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define POCR_ABI_VERSION 1
+
+#define POCR_OK 0
+#define POCR_ERR_ARG (-1)
+#define POCR_ERR_DEVICE (-2)
+#define POCR_ERR_NOMEM (-3)
+#define POCR_ERR_UNSUPPORTED (-4)
+#define POCR_ERR_INJECTED (-5)
+
+/* tensor types = GGUF type ids (internal/gguf/gguf.go:19-22) */
+#define POCR_F32 0
+#define POCR_Q8 1000
+#define POCR_Q4 1001
+#define POCR_Q6 1002
+
+/* row encoder tie modes */
+#define POCR_TIE_HALF_AWAY 0 /* roundToInt, internal/tensor/quant.go:436-441 */
+#define POCR_TIE_AMD64 1     /* RNE where the amd64 converter rounds with AVX2 */
+
+/* matrix roles for pocr_model_set_weight (internal/model text layer fields) */
+#define POCR_W_Q 0
+#define POCR_W_K 1
+#define POCR_W_V 2
+#define POCR_W_O 3
+#define POCR_W_GATE 4
+#define POCR_W_UP 5
+#define POCR_W_DOWN 6
+#define POCR_W_LM_HEAD 7
+/* norm roles for pocr_model_set_norm */
+#define POCR_N_LN1 0
+#define POCR_N_LN2 1
+#define POCR_N_FINAL 2
+
+typedef struct pocr_ctx pocr_ctx;
+typedef struct pocr_weight pocr_weight;
+typedef struct pocr_model pocr_model;
+typedef struct pocr_seq pocr_seq;
+
+/* decoder hyper-parameters (internal/config/config.go:31-49).  Unlike the
+ * reference loader (internal/model/model.go:647-653) heads*head_dim may
+ * differ from hidden. */
+typedef struct {
+    int32_t hidden;
+    int32_t intermediate;
+    int32_t layers;
+    int32_t heads;
+    int32_t kv_heads;
+    int32_t head_dim;
+    int32_t vocab;
+    float rms_norm_eps;
+    double rope_theta;
+    int32_t mrope_section[3]; /* zeros → default {16,24,24} (model.go:882) */
+} pocr_config;
+
+/* ---------------- library / context ---------------- */
+int pocr_abi_version(void);
+const char *pocr_last_error(void);
+/* replaces backend.Select("hip") device bring-up (internal/backend/backend.go:85-111) */
+int pocr_ctx_create(int device, pocr_ctx **out);
+void pocr_ctx_destroy(pocr_ctx *ctx);
+/* number of HIP devices visible (0 when none); never fails */
+int pocr_device_count(void);
+
+/* ---------------- formats (host) ---------------- */
+/* row bytes of one packed row: Q8 cols, Q4 (cols+1)/2, Q6 PackedQ6Cols
+ * (internal/tensor/quant.go:2882) */
+size_t pocr_row_bytes(int qtype, int cols);
+/* QuantizeQ8RowBytesInto / QuantizeQ4RowInto / QuantizeQ6RowInto
+ * (internal/tensor/quant.go:96-137, 291-354, 201-270) over rows. */
+int pocr_quantize_rows(int qtype, int tie_mode, const float *w, int rows, int cols, float *scales,
+                       uint8_t *packed);
+/* UnpackQ4Matrix / UnpackQ6Matrix / q8ValueTable (internal/tensor/quant.go:2325-2368,
+ * 2605-2656, 2314-2320): packed rows → int8 codes */
+int pocr_unpack_rows(int qtype, const uint8_t *packed, int rows, int cols, int8_t *out);
+
+/* ---------------- weights ---------------- */
+/* upload one Q*_ROW tensor (scales f32[rows] + packed rows) into HBM */
+int pocr_weight_upload(pocr_ctx *ctx, int qtype, int rows, int cols, const float *scales,
+                       const uint8_t *packed, pocr_weight **out);
+void pocr_weight_free(pocr_weight *w);
+
+/* ---------------- op level (host buffers, synchronous) ---------------- */
+/* VulkanMatVecQ{8,6,4} (vulkan_exec_stub.go:186,234,282): out[m][rows] = W·x[m].
+ * m > 1 is the batched GEMV (M rows of activations sharing one weight stream). */
+int pocr_matvec(pocr_ctx *ctx, const pocr_weight *w, const float *x, int m, float *out);
+/* VulkanMatVecArgmaxQ* (vulkan_exec_stub.go:190,238,286): greedy LM head,
+ * ties → lowest index (internal/tensor/argmax_quant.go:255-262) */
+int pocr_matvec_argmax(pocr_ctx *ctx, const pocr_weight *w, const float *x, int32_t *index,
+                       float *score);
+/* VulkanFusedMatVec3Q* (vulkan_exec_stub.go:202,250,298) */
+int pocr_fused_matvec3(pocr_ctx *ctx, const pocr_weight *a, const pocr_weight *b, const pocr_weight *c,
+                       const float *x, float *out_a, float *out_b, float *out_c);
+/* VulkanFusedMatVec3MRoPEQ* (vulkan_exec_stub.go:214,262,310): Q,K,V then
+ * rotate-half RoPE on out_a (q_heads) and out_b (kv_heads) */
+int pocr_fused_matvec3_mrope(pocr_ctx *ctx, const pocr_weight *a, const pocr_weight *b,
+                             const pocr_weight *c, const float *x, const float *cos_t,
+                             const float *sin_t, int q_heads, int kv_heads, int head_dim,
+                             float *out_a, float *out_b, float *out_c);
+/* VulkanSwiGLUGateUpQ* (vulkan_exec_stub.go:222,270,318): out = SiLU(G·x)·(U·x) */
+int pocr_swiglu_gate_up(pocr_ctx *ctx, const pocr_weight *gate, const pocr_weight *up, const float *x,
+                        float *out);
+/* VulkanMatVecAddRMSNormQ* (vulkan_exec_stub.go:198,246,294) and the OutOnly
+ * CPU variants (internal/tensor/fused_matvec2.go:339-1623):
+ * v = residual + W·x; norm_out = RMSNorm(v)·norm_w; residual = v iff in_place */
+int pocr_matvec_add_rmsnorm(pocr_ctx *ctx, const pocr_weight *w, const float *x, float *residual,
+                            const float *norm_w, float eps, int in_place, float *norm_out);
+/* VulkanRMSNormF32 (vulkan_exec_stub.go:26) */
+int pocr_rmsnorm(pocr_ctx *ctx, const float *x, const float *w, int n, float eps, float *out);
+/* VulkanMRoPEPairF32 (vulkan_exec_stub.go:42), in place */
+int pocr_mrope_pair(pocr_ctx *ctx, float *q, float *k, const float *cos_t, const float *sin_t,
+                    int q_heads, int kv_heads, int head_dim);
+/* VulkanTextAttentionF32 (vulkan_exec_stub.go:134): GQA decode attention of
+ * q[heads*dim] over cache_len rows of kv_heads*dim fp32 K/V */
+int pocr_text_attention(pocr_ctx *ctx, const float *q, const float *k_cache, const float *v_cache,
+                        int cache_len, int heads, int kv_heads, int head_dim, float *out);
+
+/* Average device time (microseconds, HIP events on the context stream) of the
+ * M=1 GEMV kernel over `iters` launches that rotate through n_weights copies of
+ * one shape, so the working set can exceed the 256 MB Infinity Cache.  Runs a
+ * separately named instance of the same kernel so profiles can attribute it.
+ * Measurement counterpart of internal/tensor/model_dims_bench_test.go. */
+int pocr_time_matvec(pocr_ctx *ctx, const pocr_weight *const *weights, int n_weights, const float *x, int iters,
+                     float *avg_us);
+
+/* ---------------- model / step level (device-resident) ---------------- */
+int pocr_model_create(pocr_ctx *ctx, const pocr_config *cfg, pocr_model **out);
+void pocr_model_destroy(pocr_model *m);
+/* borrow an uploaded weight; layer -1 with POCR_W_LM_HEAD for the head */
+int pocr_model_set_weight(pocr_model *m, int layer, int role, const pocr_weight *w);
+/* copies hidden floats to HBM; layer -1 with POCR_N_FINAL for the final norm */
+int pocr_model_set_norm(pocr_model *m, int layer, int role, const float *w);
+/* copies the f32 embed_tokens table [vocab][hidden] to HBM */
+int pocr_model_set_embed(pocr_model *m, const float *embed);
+/* reproduce the reference's Q4/Q6 attention-residual behaviour
+ * (internal/model/model.go:3895-3902, 4051-4057); default on */
+int pocr_model_set_residual_quirk(pocr_model *m, int on);
+
+/* per-sequence state: per-layer fp32 K/V in HBM preallocated for `capacity`
+ * tokens (getKVCaches, internal/model/model.go:3286-3327) */
+int pocr_seq_create(pocr_model *m, int capacity, pocr_seq **out);
+void pocr_seq_destroy(pocr_seq *s);
+int pocr_seq_reset(pocr_seq *s);
+int pocr_seq_len(const pocr_seq *s);
+/* copy layer's first len rows of K/V (len*kv_heads*head_dim floats each) */
+int pocr_seq_read_kv(pocr_seq *s, int layer, float *k, float *v);
+/* drop cache rows beyond len (0 <= len <= current length); the rows kept are
+ * untouched, like a kvCache whose len is reset (internal/model/model.go:3318) */
+int pocr_seq_truncate(pocr_seq *s, int len);
+int pocr_seq_write_kv(pocr_seq *s, int layer, const float *k, const float *v, int len);
+
+/* one token step (forwardEmbeddingForSampling, internal/model/model.go:3475-3643).
+ * need_logits=0 is a non-final prompt token.  logits (vocab floats) and token
+ * are optional outputs. */
+int pocr_step(pocr_seq *s, const float *emb, const int32_t pos3[3], int need_logits, float *logits,
+              int32_t *token);
+/* batched prompt prefill of n embeddings at positions pos3[n][3] on MFMA;
+ * same results as n sequential pocr_step calls (token-by-token prefill,
+ * internal/model/model.go:1514-1536).  logits/token of the last row. */
+int pocr_prefill(pocr_seq *s, int n, const float *emb, const int32_t *pos3, float *logits,
+                 int32_t *token);
+/* greedy decode loop kept on the device (decode loop, model.go:1538-1568):
+ * feeds first_token at position first_pos, first_pos+1, ...; writes up to
+ * max_new tokens (first_token first) and stops after an EOS id.  Returns the
+ * number of tokens written (>=0) or an error status (<0). */
+int pocr_decode_greedy(pocr_seq *s, int32_t first_token, int32_t first_pos, int max_new,
+                       const int32_t *eos, int n_eos, int32_t *out_tokens);
+/* whole greedy generation: GenerateWithOptions / generateWithImageEmbeds
+ * (internal/model/model.go:1492-1572, 1618-1711) incl. multimodal positions
+ * (1717-1783).  image rows replace ids equal to image_token_id in order.
+ * use_prefill=1 runs the MFMA batched prefill, 0 the token-by-token steps. */
+int pocr_generate(pocr_seq *s, const int32_t *ids, int n_ids, const float *image_embeds, int n_image,
+                  int32_t image_token_id, const int32_t grid[3], int32_t merge, int max_new,
+                  const int32_t *eos, int n_eos, int use_prefill, int32_t *out_tokens);
+
+/* multimodal RoPE positions (internal/model/model.go:1717-1783), host only.
+ * Returns the number of positions written, rope_delta via pointer. */
+int pocr_mm_positions(const int32_t *ids, int n, int32_t image_token_id, const int32_t grid[3],
+                      int32_t merge, int32_t *pos3, int32_t *rope_delta);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* POCR_HIP_H */

@@ -1,0 +1,129 @@
+/*
+ * pocr_oracle.h — CPU restatement of RapidOCRvl's pure-Go ERNIE text-decoder
+ * path, used ONLY as test infrastructure: the parity checker for the HIP
+ * library and the CPU baseline timed beside it.  Nothing in the product
+ * (rapidocrvl_amd/, include/) includes, links or loads this code.
+ *
+ * Every function cites the reference file:line it restates (paths relative to
+ * the RapidOCRvl repository root).  Pinning of each function (golden vectors,
+ * closed forms, brute force) lives in tests/test_oracle_*.py; functions whose
+ * exact float rounding only the Go binary could fix are tolerance-pinned and
+ * say so below ("parity unpinned" for bit-level rounding order).
+ */
+#ifndef POCR_ORACLE_H
+#define POCR_ORACLE_H
+
+#include <stdint.h>
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* quant type tags, same numbers as the GGUF tensor types
+ * (internal/gguf/gguf.go:19-22) */
+#define ORC_F32 0
+#define ORC_Q8 1000
+#define ORC_Q4 1001
+#define ORC_Q6 1002
+
+/* row-encoder tie modes */
+#define ORC_TIE_HALF_AWAY 0 /* roundToInt, quant.go:436-441 (scalar Go, Q8 converter) */
+#define ORC_TIE_AMD64 1     /* VRNDSCALEPS RNE (dot_amd64.s:5837-6005) where the
+                               amd64 converter uses AVX2: Q4 all cols (cols>=8),
+                               Q6 floor(cols/8)*8 prefix; Q8 bytes stay half-away */
+
+/* ---- formats: encoders / unpack (a2, a3) ---- */
+size_t orc_row_bytes(int qtype, int cols);
+float orc_quantize_row(int qtype, int tie_mode, const float *w, int cols, uint8_t *out);
+void orc_unpack_row(int qtype, const uint8_t *row, int cols, int8_t *out);
+int orc_round_to_int(float x);
+
+/* ---- matvec (a4, a5) ---- */
+typedef struct {
+    int qtype;           /* ORC_Q8 / ORC_Q4 / ORC_Q6 */
+    int rows, cols;
+    const float *scale;  /* [rows] */
+    const uint8_t *data; /* rows * orc_row_bytes(qtype, cols) */
+} orc_qmat;
+
+/* plain fp32-activation semantics: out[r] = dot(int q[r], x) * scale[r] */
+void orc_matvec(const orc_qmat *m, const float *x, float *out);
+/* VNNI-emulation semantics (dot_amd64.go:140-167, dot_vnni_amd64.s:434-500,1043-1080) */
+float orc_quantize_x_vnni(const float *x, int n, uint8_t *xq);
+void orc_matvec_vnni(const orc_qmat *m, const float *x, float *out);
+
+/* ---- small vector ops (a6-a13 pieces) ---- */
+float orc_fast_exp(float x);
+float orc_fast_rsqrt(float x);
+float orc_silu(float x);
+void orc_softmax(float *x, int n);
+void orc_rmsnorm(float *out, const float *x, const float *w, int n, float eps);
+void orc_add_rmsnorm(float *out, float *dst, const float *add, const float *w, int n, float eps);
+void orc_add_rmsnorm_out_only(float *out, const float *dst, const float *add, const float *w, int n, float eps);
+int orc_argmax(const float *x, int n);
+
+/* ---- RoPE (a7) ---- */
+void orc_rope_init(double theta, int head_dim, const int *sections, int n_sections,
+                   double *freq, uint8_t *axis);
+void orc_rope_table(const double *freq, const uint8_t *axis, int half, int t, int h, int w,
+                    float *cos_t, float *sin_t);
+void orc_apply_rope(float *x, const float *cos_t, const float *sin_t, int heads, int dim);
+
+/* ---- attention over an fp32 cache (a9) ---- */
+void orc_cache_attention(float *out, const float *q, const float *kcache, const float *vcache,
+                         int len, int heads, int kv_heads, int dim);
+
+/* ---- multimodal positions (a15) ---- */
+int orc_mm_positions(const int32_t *ids, int n, int image_token_id, const int32_t grid[3],
+                     int merge, int32_t *pos3 /* [n][3] */, int *rope_delta);
+
+/* ---- the model (a14, a15) ---- */
+typedef struct orc_model orc_model;
+typedef struct orc_seq orc_seq;
+
+orc_model *orc_model_create(int hidden, int inter, int layers, int heads, int kv_heads,
+                            int head_dim, int vocab, float eps, double rope_theta);
+void orc_model_free(orc_model *m);
+/* which: 0=q 1=k 2=v 3=o 4=gate 5=up 6=down; layer -1 & which 7 = lm_head */
+int orc_model_set_matrix(orc_model *m, int layer, int which, int qtype, int rows, int cols,
+                         const float *scale, const uint8_t *data);
+/* which: 0=ln1 1=ln2 ; layer -1 = final norm */
+int orc_model_set_norm(orc_model *m, int layer, int which, const float *w);
+int orc_model_set_embed(orc_model *m, const float *embed);
+/* residual quirk for Q4/Q6 (model.go:3895-3902, 4051-4057): 1 = reproduce (default) */
+void orc_model_set_quirk(orc_model *m, int on);
+/* activation mode: 0 plain (default), 1 VNNI emulation for Q4/Q6 */
+void orc_model_set_vnni(orc_model *m, int on);
+
+orc_seq *orc_seq_create(orc_model *m, int capacity);
+void orc_seq_free(orc_seq *s);
+void orc_seq_reset(orc_seq *s);
+int orc_seq_len(const orc_seq *s);
+const float *orc_seq_k(const orc_seq *s, int layer);
+const float *orc_seq_v(const orc_seq *s, int layer);
+/* copy an externally prepared cache prefix (used for isolated attention tests) */
+int orc_seq_load(orc_seq *s, int layer, const float *k, const float *v, int len);
+
+/* one token step (forwardEmbeddingForSampling, model.go:3475-3643).
+ * need_logits=0 → non-final prompt token (last layer K/V only).
+ * Writes logits (if logits!=NULL) and greedy token (if token!=NULL). */
+int orc_step(orc_model *m, orc_seq *s, const float *emb, const int32_t pos3[3], int need_logits,
+             float *logits, int32_t *token, float *final_norm_out);
+
+/* whole generation (GenerateWithOptions model.go:1492-1572 and
+ * generateWithImageEmbeds 1618-1711, greedy).  image rows replace ids equal to
+ * image_token_id in order; grid used for positions.  Returns tokens appended
+ * (prompt not included) in out_tokens, count via return value, <0 on error. */
+int orc_generate(orc_model *m, const int32_t *ids, int n_ids, const float *image_embeds,
+                 int n_image, int image_token_id, const int32_t grid[3], int merge,
+                 int max_new, const int32_t *eos, int n_eos, int32_t *out_tokens);
+
+/* thread pool for the CPU baseline (parallelForMax, ops.go:570-614) */
+void orc_set_threads(int n);
+int orc_get_threads(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,136 @@
+// internal.hpp — shared host-side definitions of the C ABI implementation.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/pocr_hip.h"
+#include "kernels.hpp"
+
+namespace pocr {
+int fail(int code, const char *fmt, ...);
+bool injected(const char *op);
+}  // namespace pocr
+
+#define HIP_TRY(expr)                                                                                     \
+    do {                                                                                                  \
+        hipError_t e_ = (expr);                                                                           \
+        if (e_ != hipSuccess) return pocr::fail(POCR_ERR_DEVICE, "%s: %s", #expr, hipGetErrorString(e_)); \
+    } while (0)
+
+#define CHECK_INJECT(op) \
+    if (pocr::injected(op)) return pocr::fail(POCR_ERR_INJECTED, "%s: injected failure (POCR_HIP_FAIL_OP)", op)
+
+#define RC(expr)                        \
+    do {                                \
+        int rc_ = (expr);               \
+        if (rc_ != POCR_OK) return rc_; \
+    } while (0)
+
+struct DevBuf {
+    void *p = nullptr;
+    size_t n = 0;
+    ~DevBuf() {
+        if (p) (void)hipFree(p);
+    }
+    int ensure(size_t bytes) {
+        if (bytes <= n) return POCR_OK;
+        if (p) (void)hipFree(p);
+        p = nullptr;
+        n = 0;
+        const size_t sz = std::max<size_t>(bytes, 256);
+        HIP_TRY(hipMalloc(&p, sz));
+        n = sz;
+        return POCR_OK;
+    }
+    template <class T> T *as() const { return reinterpret_cast<T *>(p); }
+};
+
+struct pocr_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::mutex mu;
+    // op-level staging
+    DevBuf x, out, out2, out3, res, vbuf, kc, vc, part, counter, tabs, state;
+};
+
+struct pocr_weight {
+    pocr_ctx *ctx = nullptr;
+    int qtype = 0, rows = 0, cols = 0;
+    size_t row_bytes = 0;
+    void *base = nullptr;
+    const float *scale = nullptr;
+    const uint8_t *data = nullptr;
+};
+
+struct LayerW {
+    const pocr_weight *w[7] = {nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
+    float *ln1 = nullptr, *ln2 = nullptr;
+};
+
+struct pocr_model {
+    pocr_ctx *ctx = nullptr;
+    pocr_config cfg{};
+    std::vector<LayerW> layers;
+    const pocr_weight *lm = nullptr;
+    float *final_norm = nullptr;
+    float *embed = nullptr;
+    double *freq = nullptr;
+    uint8_t *axis = nullptr;
+    std::vector<double> h_freq;
+    std::vector<uint8_t> h_axis;
+    int quirk = 1;
+};
+
+
+// prefill / batched GEMV (prefill.hip)
+struct PrefillBufs {
+    float *x = nullptr;      // [n][max(hidden, q_rows, inter)] activations
+    float *y = nullptr;      // [n][max rows] GEMM outputs
+    float *h = nullptr;      // [n][hidden] residual rows
+    float *v = nullptr;      // [n][hidden] residual + attention rows
+    int32_t *pos = nullptr;  // [n][3]
+    float *tabs = nullptr;   // [n][2][half] RoPE tables
+    int cap_rows = 0;
+};
+void prefill_free(PrefillBufs &b);
+
+struct pocr_seq {
+    pocr_model *m = nullptr;
+    int cap = 0;
+    int len = 0;  // host mirror
+    float *kv = nullptr;  // [layers][2][cap][kvd]
+    float *h = nullptr, *qkv = nullptr, *head_out = nullptr, *vbuf = nullptr, *g = nullptr, *logits = nullptr;
+    float *part = nullptr;
+    unsigned int *counter = nullptr;
+    pocr::StepState *st = nullptr;
+    int32_t *tokens = nullptr;
+    int max_tokens = 0;
+    int nsplit = 32;
+    hipGraphExec_t decode_exec = nullptr;
+    hipGraph_t decode_graph = nullptr;
+    PrefillBufs pf;
+    ~pocr_seq();
+};
+
+namespace pocr {
+DevMat dev_mat(const pocr_weight *w);
+int gemv_launch(hipStream_t s, GemvParams p, int nmat, int pro, int epi, int max_grid);
+GemvParams gemv_params_1(const pocr_weight *w);
+int step_locked(pocr_seq *s, const float *emb, const int32_t pos3[3], int need_logits, float *logits,
+                int32_t *token);
+int prefill_locked(pocr_seq *s, int n, const float *emb, const int32_t *pos3, float *logits, int32_t *token);
+int batched_gemv(hipStream_t s, const DevMat &w, const float *x, int m, float *out);
+float *layer_k(const pocr_seq *s, int layer);
+float *layer_v(const pocr_seq *s, int layer);
+int seq_set_state(pocr_seq *s, int len);
+constexpr int kBigGrid = 1024;
+}  // namespace pocr

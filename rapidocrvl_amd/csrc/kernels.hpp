@@ -1,0 +1,847 @@
+// kernels.hpp — gfx950 HIP kernels of the ERNIE text-decoder step.
+//
+// Weights stay in the GGUF Q*_ROW row layout (internal/gguf/gguf.go:446-558):
+// per tensor an f32 scale per row and the packed rows, row-major.  One
+// wavefront streams LPR×16-byte chunks of a row with coalesced 128-bit (Q6:
+// 96-bit) loads, decodes the codes in registers against an activation slice it
+// keeps in VGPRs for all rows, and reduces the row across its LPR lanes with
+// DPP/swizzle shuffles.  Row r's result is (Σ code·x)·scale[r], the plain
+// fp32-activation semantics of MatVecQ{8,4,6} (internal/tensor/quant.go:443-561).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace pocr {
+
+enum : int { QT_Q8 = 1000, QT_Q4 = 1001, QT_Q6 = 1002 };
+
+constexpr int kThreads = 256;  // 4 wavefronts per workgroup
+constexpr int kWaves = kThreads / 64;
+constexpr int kMaxHalf = 128;  // head_dim/2 upper bound for RoPE tables
+
+struct DevMat {
+    const float *scale;    // [rows]
+    const uint8_t *data;   // rows * row_bytes, 256-byte aligned base
+    int rows;
+    int cols;
+    int row_bytes;
+    int qtype;
+};
+
+// Per-sequence step state kept in HBM so one captured graph can be replayed
+// token after token.
+struct StepState {
+    int32_t len;       // cache rows after this step's append
+    int32_t clen;      // cache rows before the append (= token index)
+    int32_t cap;       // cache capacity
+    int32_t err;       // nonzero → every kernel returns immediately
+    int32_t pos[3];    // (T,H,W) position of this token
+    int32_t next_pos;  // decode position counter
+    int32_t n_out;     // tokens emitted by the device decode loop
+    int32_t has_rope;
+    int32_t half;
+    int32_t pad;
+    unsigned long long argmax_key;
+    float cos_t[kMaxHalf];
+    float sin_t[kMaxHalf];
+};
+
+// ---------------------------------------------------------------------------
+// reference numerics (internal/tensor/ops.go)
+// ---------------------------------------------------------------------------
+
+// FastExpF32 (ops.go:1099-1112).  The reference wraps for x < -87 (its integer
+// exponent add underflows); the input is clamped there, where exp() is below
+// FLT_MIN anyway.
+__device__ __forceinline__ float fast_exp_ref(float x) {
+#pragma clang fp contract(off)
+    x = fmaxf(x, -87.0f);
+    const float log2e = 1.4426950408889634f;
+    const float magic = 12582912.0f;
+    float t = x * log2e;
+    int32_t n = (int32_t)((t + magic) - magic);
+    float f = t - (float)n;
+    float f2 = f * f;
+    float poly = (1.0f + 0.6931471824645996f * f) +
+                 f2 * (0.24022650718688965f + 0.05550410971045494f * f +
+                       f2 * (0.009618128649890423f + 0.0013352063251659274f * f));
+    return __uint_as_float(__float_as_uint(poly) + ((uint32_t)n << 23));
+}
+
+// fastRsqrtF32 (ops.go:1374-1381)
+__device__ __forceinline__ float fast_rsqrt_ref(float x) {
+#pragma clang fp contract(off)
+    float half = x * 0.5f;
+    float y = __uint_as_float(0x5f3759dfu - (__float_as_uint(x) >> 1));
+    y = y * (1.5f - half * y * y);
+    return y * (1.5f - half * y * y);
+}
+
+// SiLU (ops.go:1092-1094)
+__device__ __forceinline__ float silu_ref(float x) {
+#pragma clang fp contract(off)
+    return x / (1.0f + fast_exp_ref(-x));
+}
+
+// ---------------------------------------------------------------------------
+// code decode: chunk of packed bytes → Σ u·x with unsigned codes u; the signed
+// value is u − BIAS, folded as −BIAS·Σx once per lane.
+// ---------------------------------------------------------------------------
+template <int QT> struct QTraits;
+template <> struct QTraits<QT_Q4> {  // 16 B = 32 nibbles, value = nib − 8 (quant.go:2356)
+    static constexpr int CB = 16, W = 32;
+    static constexpr float BIAS = 8.0f;
+};
+template <> struct QTraits<QT_Q8> {  // 16 B = 16 int8; u = b ^ 0x80 = b + 128
+    static constexpr int CB = 16, W = 16;
+    static constexpr float BIAS = 128.0f;
+};
+template <> struct QTraits<QT_Q6> {  // 12 B = 16 six-bit codes, value = code − 32 (quant.go:2592)
+    static constexpr int CB = 12, W = 16;
+    static constexpr float BIAS = 32.0f;
+};
+
+struct Chunk {
+    uint32_t d[4];
+};
+
+template <int QT>
+__device__ __forceinline__ Chunk load_chunk(const uint8_t *p) {
+    Chunk c;
+    if constexpr (QT == QT_Q6) {
+        struct __attribute__((aligned(4))) U3 {
+            uint32_t a, b, c;
+        };
+        U3 v = *reinterpret_cast<const U3 *>(p);
+        c.d[0] = v.a;
+        c.d[1] = v.b;
+        c.d[2] = v.c;
+        c.d[3] = 0;
+    } else {
+        uint4 v = *reinterpret_cast<const uint4 *>(p);
+        c.d[0] = v.x;
+        c.d[1] = v.y;
+        c.d[2] = v.z;
+        c.d[3] = v.w;
+    }
+    return c;
+}
+
+__device__ __forceinline__ float ubyte(uint32_t v, int i) { return (float)((v >> (8 * i)) & 0xFFu); }
+
+template <int QT>
+__device__ __forceinline__ float chunk_dot(const Chunk &c, const float *x) {
+    float a0 = 0.0f, a1 = 0.0f;
+    if constexpr (QT == QT_Q4) {
+        // byte j holds col 2j (low nibble) and col 2j+1 (high nibble) (quant.go:322-353)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            uint32_t lo = c.d[k] & 0x0F0F0F0Fu;
+            uint32_t hi = (c.d[k] >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                a0 = fmaf(ubyte(lo, m), x[8 * k + 2 * m], a0);
+                a1 = fmaf(ubyte(hi, m), x[8 * k + 2 * m + 1], a1);
+            }
+        }
+    } else if constexpr (QT == QT_Q8) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            uint32_t u = c.d[k] ^ 0x80808080u;
+            a0 = fmaf(ubyte(u, 0), x[4 * k + 0], a0);
+            a1 = fmaf(ubyte(u, 1), x[4 * k + 1], a1);
+            a0 = fmaf(ubyte(u, 2), x[4 * k + 2], a0);
+            a1 = fmaf(ubyte(u, 3), x[4 * k + 3], a1);
+        }
+    } else {
+        // little-endian 6-bit stream, col i at bits [6i, 6i+6) (quant.go:2886-2906)
+        const uint32_t d0 = c.d[0], d1 = c.d[1], d2 = c.d[2];
+        uint32_t u[16];
+#pragma unroll
+        for (int i = 0; i < 5; ++i) u[i] = __builtin_amdgcn_ubfe(d0, 6 * i, 6);
+        u[5] = __builtin_amdgcn_alignbit(d1, d0, 30) & 63u;
+#pragma unroll
+        for (int i = 6; i < 10; ++i) u[i] = __builtin_amdgcn_ubfe(d1, 6 * i - 32, 6);
+        u[10] = __builtin_amdgcn_alignbit(d2, d1, 28) & 63u;
+#pragma unroll
+        for (int i = 11; i < 16; ++i) u[i] = __builtin_amdgcn_ubfe(d2, 6 * i - 64, 6);
+#pragma unroll
+        for (int i = 0; i < 16; i += 2) {
+            a0 = fmaf((float)u[i], x[i], a0);
+            a1 = fmaf((float)u[i + 1], x[i + 1], a1);
+        }
+    }
+    return a0 + a1;
+}
+
+template <int LPR>
+__device__ __forceinline__ float lane_group_sum(float v) {
+#pragma unroll
+    for (int off = LPR / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+// ---------------------------------------------------------------------------
+// GEMV family
+// ---------------------------------------------------------------------------
+enum : int { PRO_COPY = 0, PRO_RMSNORM = 1 };
+enum : int {
+    EPI_PLAIN = 0,   // out[r] = s
+    EPI_SWIGLU = 1,  // out[r] = SiLU(s_gate)·s_up            (NMAT = 2)
+    EPI_OPROJ = 2,   // v = residual + s; vbuf = v; residual = v if in place
+    EPI_DOWN = 3,    // residual += s, or vbuf = residual + s on the last layer
+    EPI_ARGMAX = 4,  // greedy LM head (+ optional logits)
+    EPI_ADDV = 5,    // vbuf = residual + s (op-level AddRMSNorm, norm in a 2nd kernel)
+};
+
+struct GemvParams {
+    DevMat m[3];
+    int seg_end[3];  // NMAT == 1: rows [seg_end[i-1], seg_end[i]) come from m[i]
+    int rows;
+    int cols;
+    const float *x;
+    const float *norm_w;
+    float eps;
+    float *out;
+    float *residual;
+    float *vbuf;
+    StepState *st;  // may be null (op level)
+    int flag;       // EPI_OPROJ: in-place when st==null; EPI_DOWN: last layer
+    int quirk;      // EPI_OPROJ: Q4/Q6 residual behaviour on
+};
+
+__device__ __forceinline__ unsigned long long argmax_key(float v, int row) {
+    uint32_t b = __float_as_uint(v);
+    uint32_t ord = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return ((unsigned long long)ord << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)row);
+}
+
+// Block-wide sum in a fixed order (deterministic).
+__device__ __forceinline__ float block_sum(float v, float *red) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    const int wave = threadIdx.x >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[wave] = v;
+    __syncthreads();
+    float s = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) s += red[w];
+    return s;
+}
+
+// x → LDS, optionally RMSNorm'ed: out = x·fastRsqrt(Σx²/n + eps)·w (ops.go:1015-1037)
+template <int PRO>
+__device__ __forceinline__ void stage_x(float *xs, const float *x, const float *w, int n, float eps,
+                                        float *red) {
+    if constexpr (PRO == PRO_COPY) {
+        for (int i = threadIdx.x; i < n; i += kThreads) xs[i] = x[i];
+        __syncthreads();
+    } else {
+        float ss = 0.0f;
+        for (int i = threadIdx.x; i < n; i += kThreads) {
+            float v = x[i];
+            xs[i] = v;
+            ss = fmaf(v, v, ss);
+        }
+        ss = block_sum(ss, red);
+        const float scale = fast_rsqrt_ref(ss / (float)n + eps);
+        for (int i = threadIdx.x; i < n; i += kThreads) {
+#pragma clang fp contract(off)
+            xs[i] = xs[i] * scale * w[i];
+        }
+        __syncthreads();
+    }
+}
+
+__device__ __forceinline__ void gemv_epilogue(const GemvParams &p, int epi, int r, const float *s, bool in_place,
+                                              float &best_v, int &best_r) {
+#pragma clang fp contract(off)
+    switch (epi) {
+    case EPI_PLAIN: p.out[r] = s[0]; break;
+    case EPI_SWIGLU: p.out[r] = silu_ref(s[0]) * s[1]; break;
+    case EPI_OPROJ: {
+        const float v = p.residual[r] + s[0];
+        p.vbuf[r] = v;
+        if (in_place) p.residual[r] = v;
+        break;
+    }
+    case EPI_DOWN: {
+        const float v = p.residual[r] + s[0];
+        if (p.flag) p.vbuf[r] = v;
+        else p.residual[r] = v;
+        break;
+    }
+    case EPI_ADDV: p.vbuf[r] = p.residual[r] + s[0]; break;
+    default:  // EPI_ARGMAX
+        if (p.out) p.out[r] = s[0];
+        if (s[0] > best_v || (s[0] == best_v && r < best_r)) {
+            best_v = s[0];
+            best_r = r;
+        }
+    }
+}
+
+__device__ __forceinline__ bool oproj_in_place(const GemvParams &p) {
+    if (!p.st) return p.flag != 0;
+    // model.go:3895-3902 (first token) and 4051-4057 (len > 6): Q4/Q6 use the
+    // OutOnly variant; positions 1..5 go through matVecOutAddRMSNormCPU (in place).
+    const int clen = p.st->clen;
+    return !(p.quirk && (clen == 0 || clen >= 6));
+}
+
+__device__ __forceinline__ void argmax_finish(const GemvParams &p, float best_v, int best_r, float *red) {
+    unsigned long long k = best_r == 0x7FFFFFFF ? 0ull : argmax_key(best_v, best_r);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const unsigned long long o = __shfl_xor(k, off, 64);
+        k = o > k ? o : k;
+    }
+    unsigned long long *kred = reinterpret_cast<unsigned long long *>(red);
+    const int wave = threadIdx.x >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) kred[wave] = k;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        unsigned long long m = kred[0];
+        for (int w = 1; w < kWaves; ++w) m = kred[w] > m ? kred[w] : m;
+        if (m) atomicMax(&p.st->argmax_key, m);
+    }
+}
+
+// row → (segment, row within the segment's matrix), by selects (no dynamic
+// indexing of the kernel-argument array)
+__device__ __forceinline__ DevMat seg_mat(const GemvParams &p, int sg) {
+    return sg == 0 ? p.m[0] : (sg == 1 ? p.m[1] : p.m[2]);
+}
+
+// LPR lanes share one row; each lane owns CPL chunks (lane + j·LPR) of every
+// row, so its x slice (CPL·W floats) stays in VGPRs across rows.  A wave
+// handles RPW = 64/LPR rows per step and U steps per iteration (U·RPW rows,
+// U·CPL·NMAT loads in flight per lane).
+// TAG only separates instances for profiling (TAG=1: the timing entry point).
+template <int QT, int LPR, int CPL, int U, int NMAT, int TAG = 0>
+__global__ void __launch_bounds__(kThreads) k_gemv(GemvParams p, int pro, int epi) {
+    if (p.st && p.st->err) return;
+    extern __shared__ float xs[];
+    __shared__ float red[2 * kWaves];
+    using T = QTraits<QT>;
+    constexpr int RPW = 64 / LPR;
+    if (pro == PRO_RMSNORM) stage_x<PRO_RMSNORM>(xs, p.x, p.norm_w, p.cols, p.eps, red);
+    else stage_x<PRO_COPY>(xs, p.x, p.norm_w, p.cols, p.eps, red);
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int sub = lane / LPR;
+    const int l = lane % LPR;
+
+    float xr[CPL][T::W];
+    float sx = 0.0f;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+        const int c = l + j * LPR;
+#pragma unroll
+        for (int k = 0; k < T::W; ++k) {
+            xr[j][k] = xs[c * T::W + k];
+            sx += xr[j][k];
+        }
+    }
+    const float bias = T::BIAS * sx;
+    const bool in_place = epi == EPI_OPROJ ? oproj_in_place(p) : false;
+    float best_v = -INFINITY;
+    int best_r = 0x7FFFFFFF;
+
+    constexpr int RG = RPW * U;
+    const int ngroups = (p.rows + RG - 1) / RG;
+    for (int g = blockIdx.x * kWaves + wave; g < ngroups; g += gridDim.x * kWaves) {
+        const int r0 = g * RG;
+        Chunk w[U][NMAT][CPL];
+        int lrow[U];
+        int seg[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int r = r0 + u * RPW + sub;
+            int sg = 0, lr = r;
+            if (NMAT == 1) {
+                sg = (r >= p.seg_end[0]) + (r >= p.seg_end[1]);
+                lr = r - (sg == 0 ? 0 : (sg == 1 ? p.seg_end[0] : p.seg_end[1]));
+            }
+            seg[u] = sg;
+            lrow[u] = lr;
+#pragma unroll
+            for (int mi = 0; mi < NMAT; ++mi) {
+                const DevMat M = seg_mat(p, NMAT == 1 ? sg : mi);
+#pragma unroll
+                for (int j = 0; j < CPL; ++j) {
+                    if (r < p.rows) {
+                        w[u][mi][j] = load_chunk<QT>(M.data + (size_t)lr * M.row_bytes + (l + j * LPR) * T::CB);
+                    } else {
+                        w[u][mi][j] = Chunk{{0u, 0u, 0u, 0u}};
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            float s[NMAT];
+#pragma unroll
+            for (int mi = 0; mi < NMAT; ++mi) {
+                float acc = 0.0f;
+#pragma unroll
+                for (int j = 0; j < CPL; ++j) acc += chunk_dot<QT>(w[u][mi][j], xr[j]);
+                s[mi] = lane_group_sum<LPR>(acc - bias);
+            }
+            const int r = r0 + u * RPW + sub;
+            if (l == 0 && r < p.rows) {
+#pragma unroll
+                for (int mi = 0; mi < NMAT; ++mi) {
+                    const DevMat M = seg_mat(p, NMAT == 1 ? seg[u] : mi);
+                    s[mi] = s[mi] * M.scale[lrow[u]];
+                }
+                gemv_epilogue(p, epi, r, s, in_place, best_v, best_r);
+            }
+        }
+    }
+    if (epi == EPI_ARGMAX) argmax_finish(p, best_v, best_r, red);
+}
+
+// Any shape (tiny test matrices, odd column counts): one wavefront per row,
+// lanes stride over columns and decode one code at a time.
+__device__ __forceinline__ int decode_code(const DevMat &M, const uint8_t *row, int c) {
+    if (M.qtype == QT_Q8) return (int)(int8_t)row[c];
+    if (M.qtype == QT_Q4) {
+        const uint8_t b = row[c >> 1];
+        return (int)((c & 1) ? (b >> 4) : (b & 15)) - 8;
+    }
+    const int bit = c * 6, idx = bit >> 3, sh = bit & 7;
+    uint32_t v = row[idx];
+    if (idx + 1 < M.row_bytes) v |= (uint32_t)row[idx + 1] << 8;
+    return (int)((v >> sh) & 63u) - 32;
+}
+
+template <int NMAT>
+__global__ void __launch_bounds__(kThreads) k_gemv_any(GemvParams p, int pro, int epi) {
+    if (p.st && p.st->err) return;
+    extern __shared__ float xs[];
+    __shared__ float red[2 * kWaves];
+    if (pro == PRO_RMSNORM) stage_x<PRO_RMSNORM>(xs, p.x, p.norm_w, p.cols, p.eps, red);
+    else stage_x<PRO_COPY>(xs, p.x, p.norm_w, p.cols, p.eps, red);
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const bool in_place = epi == EPI_OPROJ ? oproj_in_place(p) : false;
+    float best_v = -INFINITY;
+    int best_r = 0x7FFFFFFF;
+    const int nw = gridDim.x * kWaves;
+    const int iters = (p.rows + nw - 1) / nw;
+    for (int it = 0; it < iters; ++it) {
+        const int r = it * nw + blockIdx.x * kWaves + wave;
+        const bool valid = r < p.rows;
+        int sg = 0, lr = r;
+        if (NMAT == 1) {
+            sg = (r >= p.seg_end[0]) + (r >= p.seg_end[1]);
+            lr = r - (sg == 0 ? 0 : (sg == 1 ? p.seg_end[0] : p.seg_end[1]));
+        }
+        float s[NMAT];
+#pragma unroll
+        for (int mi = 0; mi < NMAT; ++mi) {
+            const DevMat M = seg_mat(p, NMAT == 1 ? sg : mi);
+            float acc = 0.0f;
+            if (valid) {
+                const uint8_t *row = M.data + (size_t)lr * M.row_bytes;
+                for (int c = lane; c < p.cols; c += 64) acc = fmaf((float)decode_code(M, row, c), xs[c], acc);
+            }
+            s[mi] = lane_group_sum<64>(acc);
+            if (valid) {
+#pragma clang fp contract(off)
+                s[mi] = s[mi] * M.scale[lr];
+            }
+        }
+        if (lane == 0 && valid) gemv_epilogue(p, epi, r, s, in_place, best_v, best_r);
+    }
+    if (epi == EPI_ARGMAX) argmax_finish(p, best_v, best_r, red);
+}
+
+// ---------------------------------------------------------------------------
+// small vector kernels
+// ---------------------------------------------------------------------------
+
+// out = RMSNorm(x)·w (single workgroup)
+static __global__ void __launch_bounds__(kThreads) k_rmsnorm(const float *x, const float *w, int n, float eps,
+                                                        float *out) {
+    __shared__ float red[2 * kWaves];
+    float ss = 0.0f;
+    for (int i = threadIdx.x; i < n; i += kThreads) ss = fmaf(x[i], x[i], ss);
+    ss = block_sum(ss, red);
+    const float scale = fast_rsqrt_ref(ss / (float)n + eps);
+    for (int i = threadIdx.x; i < n; i += kThreads) {
+#pragma clang fp contract(off)
+        out[i] = x[i] * scale * w[i];
+    }
+}
+
+// ApplyMRoPETable (internal/tensor/weighted_sum.go:231-250) on q and k in place
+__device__ __forceinline__ void rope_pair(float &a, float &b, float cs, float sn) {
+#pragma clang fp contract(off)
+    const float na = a * cs - b * sn;
+    const float nb = b * cs + a * sn;
+    a = na;
+    b = nb;
+}
+
+static __global__ void __launch_bounds__(kThreads) k_rope(float *q, float *k, const float *cos_t, const float *sin_t,
+                                                     int q_heads, int kv_heads, int dim) {
+    const int half = dim / 2;
+    const int total = (q_heads + kv_heads) * half;
+    for (int i = blockIdx.x * kThreads + threadIdx.x; i < total; i += gridDim.x * kThreads) {
+        const int h = i / half, j = i % half;
+        float *base = h < q_heads ? q + (size_t)h * dim : k + (size_t)(h - q_heads) * dim;
+        rope_pair(base[j], base[j + half], cos_t[j], sin_t[j]);
+    }
+}
+
+// Step prologue: token/position bookkeeping, RoPE table (buildMRoPETable,
+// model.go:7318-7357: f64 angle, f64 cos/sin rounded to f32), embedding row.
+// mode 0: h and pos were written by the host.  mode 1: greedy decode — the
+// token is the previous step's argmax, its embedding row is copied into h and
+// the position is next_pos (decode position len(out)-1+ropeDelta, model.go:1695).
+static __global__ void __launch_bounds__(kThreads) k_step_begin(StepState *st, const float *embed, float *h, int hidden,
+                                                           int vocab, const double *freq, const uint8_t *axis,
+                                                           int mode, int32_t *tokens, int max_tokens) {
+    __shared__ int s_tok, s_err, s_pos[3];
+    if (threadIdx.x == 0) {
+        int err = st->err;
+        int tok = -1;
+        if (!err && st->len >= st->cap) err = 1;
+        if (!err && mode == 1) {
+            const unsigned long long key = st->argmax_key;
+            if (key == 0ull) err = 2;
+            tok = (int)(0xFFFFFFFFu - (uint32_t)(key & 0xFFFFFFFFull));
+            if (tok < 0 || tok >= vocab) err = 3;
+            if (!err && st->n_out >= max_tokens) err = 4;
+            if (!err) {
+                tokens[st->n_out] = tok;
+                st->n_out = st->n_out + 1;
+                const int p = st->next_pos;
+                st->next_pos = p + 1;
+                st->pos[0] = st->pos[1] = st->pos[2] = p;
+            }
+        }
+        if (!err) {
+            st->clen = st->len;
+            st->len = st->len + 1;
+            st->has_rope = (st->pos[0] != 0 || st->pos[1] != 0 || st->pos[2] != 0) ? 1 : 0;
+            st->argmax_key = 0ull;
+        }
+        st->err = err;
+        s_err = err;
+        s_tok = tok;
+        s_pos[0] = st->pos[0];
+        s_pos[1] = st->pos[1];
+        s_pos[2] = st->pos[2];
+    }
+    __syncthreads();
+    if (s_err) return;
+    const int half = st->half;
+    for (int i = threadIdx.x; i < half; i += kThreads) {
+        const int a = axis[i];
+        const int p = a == 0 ? s_pos[0] : (a == 1 ? s_pos[1] : s_pos[2]);
+        const double ang = (double)p * freq[i];
+        st->cos_t[i] = (float)cos(ang);
+        st->sin_t[i] = (float)sin(ang);
+    }
+    if (mode == 1) {
+        const float *src = embed + (size_t)s_tok * hidden;
+        for (int i = threadIdx.x; i < hidden; i += kThreads) h[i] = src[i];
+    }
+}
+
+// ---------------------------------------------------------------------------
+// GQA decode attention, head_dim 128, split over cache rows.
+//
+// Workgroup (g, s) owns kv head g and cache rows [s·chunk, (s+1)·chunk).  It
+// rotates the q heads of its group (and, for the split holding the newest
+// row, the new k) with the step's RoPE table, appends the new K/V row to the
+// per-layer cache (kvCache.append, model.go:5593-5612: row t at
+// t·kvDim + g·128), scores its rows for all GROUP q heads sharing each K load,
+// and keeps an LDS-resident partial softmax (max, Σexp, Σexp·V).  The last
+// workgroup of a kv head to finish merges the partials (online softmax) into
+// head_out.  Scores: dot(q,k)·f32(1/√128) (model.go:4623-4795, 7391);
+// softmax with FastExp (ops.go:1199-1363); out = Σ p·V (model.go:5201-5590).
+// ---------------------------------------------------------------------------
+constexpr int kHD = 128;
+constexpr int kMaxGroup = 8;
+constexpr int kMaxChunk = 256;  // cache rows per workgroup
+
+struct AttnParams {
+    const float *q;        // [heads*128] (unrotated if rope)
+    const float *k_new;    // [kvh*128] new row (unrotated if rope) or null
+    const float *v_new;    // [kvh*128] or null
+    float *kc;             // layer cache base [cap][kvh*128]
+    float *vc;
+    StepState *st;         // null → op level (len/rope from fields below)
+    int len;               // op level: rows in cache (no append)
+    int has_rope;          // op level
+    const float *cos_t;    // op level tables
+    const float *sin_t;
+    float *part;           // [kvh][nsplit][GROUP][130]
+    unsigned int *counter; // [kvh]
+    float *head_out;       // [heads*128]
+    int heads, kvh, nsplit;
+    float scale;
+};
+
+static __global__ void __launch_bounds__(kThreads) k_attn_decode(AttnParams p) {
+    StepState *st = p.st;
+    if (st && st->err) return;
+    __shared__ float qs[kMaxGroup][kHD];
+    __shared__ float knew[kHD];
+    __shared__ float vnew[kHD];
+    __shared__ float sc[kMaxGroup][kMaxChunk];
+    __shared__ float sm[kMaxGroup], sl[kMaxGroup];
+    __shared__ int s_last;
+
+    const int g = blockIdx.x;        // kv head
+    const int split = blockIdx.y;
+    const int group = p.heads / p.kvh;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int L = st ? st->len : p.len;
+    const int newest = st ? st->clen : -1;  // row appended by this step
+    const int rope = st ? st->has_rope : p.has_rope;
+    const float *cos_t = st ? st->cos_t : p.cos_t;
+    const float *sin_t = st ? st->sin_t : p.sin_t;
+    const int kvd = p.kvh * kHD;
+
+    int chunk = (L + p.nsplit - 1) / p.nsplit;
+    chunk = (chunk + 15) & ~15;
+    const int t0 = split * chunk;
+    const int t1 = min(L, t0 + chunk);
+
+    // q of the group's heads (rotated), 64 pairs per head
+    for (int i = tid; i < group * (kHD / 2); i += kThreads) {
+        const int h = i / (kHD / 2), j = i % (kHD / 2);
+        const float *qh = p.q + (size_t)(g * group + h) * kHD;
+        float a = qh[j], b = qh[j + kHD / 2];
+        if (rope) rope_pair(a, b, cos_t[j], sin_t[j]);
+        qs[h][j] = a;
+        qs[h][j + kHD / 2] = b;
+    }
+    const bool owns_new = newest >= 0 && newest >= t0 && newest < t1;
+    if (owns_new && tid < kHD / 2) {
+        const float *kh = p.k_new + (size_t)g * kHD;
+        float a = kh[tid], b = kh[tid + kHD / 2];
+        if (rope) rope_pair(a, b, cos_t[tid], sin_t[tid]);
+        knew[tid] = a;
+        knew[tid + kHD / 2] = b;
+        const float *vh = p.v_new + (size_t)g * kHD;
+        vnew[tid] = vh[tid];
+        vnew[tid + kHD / 2] = vh[tid + kHD / 2];
+        float *kd = p.kc + (size_t)newest * kvd + g * kHD;
+        float *vd = p.vc + (size_t)newest * kvd + g * kHD;
+        kd[tid] = a;
+        kd[tid + kHD / 2] = b;
+        vd[tid] = vh[tid];
+        vd[tid + kHD / 2] = vh[tid + kHD / 2];
+    }
+    __syncthreads();
+
+    // ---- scores: 16 lanes per row, 8 dims per lane, all group heads ----
+    const int l16 = lane & 15;
+    float qv[kMaxGroup][8];
+#pragma unroll
+    for (int h = 0; h < kMaxGroup; ++h)
+#pragma unroll
+        for (int d = 0; d < 8; ++d) qv[h][d] = h < group ? qs[h][8 * l16 + d] : 0.0f;
+
+    for (int tb = t0; tb < t1; tb += 16) {
+        const int t = tb + wave * 4 + (lane >> 4);
+        float kv[8];
+        if (t < t1) {
+            if (t == newest) {
+#pragma unroll
+                for (int d = 0; d < 8; ++d) kv[d] = knew[8 * l16 + d];
+            } else {
+                const float4 *src = reinterpret_cast<const float4 *>(p.kc + (size_t)t * kvd + g * kHD + 8 * l16);
+                float4 a = src[0], b = src[1];
+                kv[0] = a.x; kv[1] = a.y; kv[2] = a.z; kv[3] = a.w;
+                kv[4] = b.x; kv[5] = b.y; kv[6] = b.z; kv[7] = b.w;
+            }
+        } else {
+#pragma unroll
+            for (int d = 0; d < 8; ++d) kv[d] = 0.0f;
+        }
+        float part[kMaxGroup];
+#pragma unroll
+        for (int h = 0; h < kMaxGroup; ++h) {
+            float a = 0.0f;
+#pragma unroll
+            for (int d = 0; d < 8; ++d) a = fmaf(qv[h][d], kv[d], a);
+            part[h] = a;
+        }
+        // reduce-scatter over the 16 lanes: lane keeps head (b3 b2 b1) of l16
+        const bool b3 = (l16 & 8) != 0, b2 = (l16 & 4) != 0, b1 = (l16 & 2) != 0;
+        float r4[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float keep = b3 ? part[4 + i] : part[i];
+            const float send = b3 ? part[i] : part[4 + i];
+            r4[i] = keep + __shfl_xor(send, 8, 64);
+        }
+        float r2[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const float keep = b2 ? r4[2 + i] : r4[i];
+            const float send = b2 ? r4[i] : r4[2 + i];
+            r2[i] = keep + __shfl_xor(send, 4, 64);
+        }
+        float r1;
+        {
+            const float keep = b1 ? r2[1] : r2[0];
+            const float send = b1 ? r2[0] : r2[1];
+            r1 = keep + __shfl_xor(send, 2, 64);
+        }
+        r1 += __shfl_xor(r1, 1, 64);
+        const int hs = (b3 ? 4 : 0) + (b2 ? 2 : 0) + (b1 ? 1 : 0);
+        if ((l16 & 1) == 0 && t < t1 && hs < group) {
+#pragma clang fp contract(off)
+            sc[hs][t - t0] = r1 * p.scale;
+        }
+    }
+    __syncthreads();
+
+    // ---- partial softmax per head: wave w handles heads w and w+4 ----
+    const int n = t1 - t0;
+    for (int h = wave; h < group; h += kWaves) {
+        float m = -INFINITY;
+        for (int i = lane; i < n; i += 64) m = fmaxf(m, sc[h][i]);
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+        float s = 0.0f;
+        for (int i = lane; i < n; i += 64) {
+            const float e = fast_exp_ref(sc[h][i] - m);
+            sc[h][i] = e;
+            s += e;
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+        if (lane == 0) {
+            sm[h] = m;
+            sl[h] = s;
+        }
+    }
+    __syncthreads();
+
+    // ---- Σ e·V: thread owns (head tid/32, dims 4·(tid%32)..+3) ----
+    const int h = tid >> 5;
+    const int d4 = (tid & 31) * 4;
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (h < group) {
+        for (int i = 0; i < n; ++i) {
+            const int t = t0 + i;
+            float4 v;
+            if (t == newest) v = make_float4(vnew[d4], vnew[d4 + 1], vnew[d4 + 2], vnew[d4 + 3]);
+            else v = *reinterpret_cast<const float4 *>(p.vc + (size_t)t * kvd + g * kHD + d4);
+            const float e = sc[h][i];
+            acc[0] = fmaf(e, v.x, acc[0]);
+            acc[1] = fmaf(e, v.y, acc[1]);
+            acc[2] = fmaf(e, v.z, acc[2]);
+            acc[3] = fmaf(e, v.w, acc[3]);
+        }
+    }
+    // partial record: [m, l, acc[128]]
+    constexpr int REC = kHD + 2;
+    float *rec = p.part + ((size_t)(g * p.nsplit + split) * kMaxGroup) * REC;
+    if (h < group) {
+        float *rh = rec + h * REC;
+        if (d4 == 0) {
+            rh[0] = n > 0 ? sm[h] : -INFINITY;
+            rh[1] = n > 0 ? sl[h] : 0.0f;
+        }
+        rh[2 + d4] = acc[0];
+        rh[3 + d4] = acc[1];
+        rh[4 + d4] = acc[2];
+        rh[5 + d4] = acc[3];
+    }
+    __threadfence();
+    __syncthreads();
+    if (tid == 0) {
+        const unsigned int prev = atomicAdd(&p.counter[g], 1u);
+        s_last = prev == (unsigned int)(p.nsplit - 1);
+    }
+    __syncthreads();
+    if (!s_last) return;
+    __threadfence();
+
+    // ---- merge the nsplit partials of kv head g ----
+    if (h < group) {
+        const float *base = p.part + ((size_t)g * p.nsplit * kMaxGroup) * REC + h * REC;
+        float M = -INFINITY;
+        for (int s = 0; s < p.nsplit; ++s) {
+            const float ls = __hip_atomic_load(base + (size_t)s * kMaxGroup * REC + 1, __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT);
+            const float ms = __hip_atomic_load(base + (size_t)s * kMaxGroup * REC, __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT);
+            if (ls > 0.0f) M = fmaxf(M, ms);
+        }
+        float lsum = 0.0f;
+        float o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int s = 0; s < p.nsplit; ++s) {
+            const float *rs = base + (size_t)s * kMaxGroup * REC;
+            const float ls = __hip_atomic_load(rs + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (!(ls > 0.0f)) continue;
+            const float ms = __hip_atomic_load(rs, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const float f = fast_exp_ref(ms - M);
+            lsum = fmaf(ls, f, lsum);
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+                o[c] = fmaf(__hip_atomic_load(rs + 2 + d4 + c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), f, o[c]);
+        }
+        const float inv = 1.0f / lsum;
+        float *dst = p.head_out + (size_t)(g * group + h) * kHD + d4;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) dst[c] = o[c] * inv;
+    }
+    if (tid == 0) p.counter[g] = 0u;
+}
+
+// Attention for head dims other than 128 (small test shapes): one workgroup
+// per q head, serial over rows, same math.
+static __global__ void __launch_bounds__(kThreads) k_attn_small(const float *q, const float *kc, const float *vc, int len,
+                                                          int heads, int kvh, int dim, float scale, float *out) {
+    extern __shared__ float sc_dyn[];
+    __shared__ float red[2 * kWaves];
+    const int h = blockIdx.x;
+    const int g = h / (heads / kvh);
+    const int kvd = kvh * dim;
+    const float *qh = q + (size_t)h * dim;
+    for (int t = threadIdx.x; t < len; t += kThreads) {
+        float a = 0.0f;
+        for (int d = 0; d < dim; ++d) a = fmaf(qh[d], kc[(size_t)t * kvd + g * dim + d], a);
+        sc_dyn[t] = a * scale;
+    }
+    __syncthreads();
+    float m = -INFINITY;
+    for (int t = threadIdx.x; t < len; t += kThreads) m = fmaxf(m, sc_dyn[t]);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    float s = 0.0f;
+    for (int t = threadIdx.x; t < len; t += kThreads) {
+        const float e = fast_exp_ref(sc_dyn[t] - m);
+        sc_dyn[t] = e;
+        s += e;
+    }
+    s = block_sum(s, red + kWaves);
+    const float inv = 1.0f / s;
+    for (int d = threadIdx.x; d < dim; d += kThreads) {
+        float a = 0.0f;
+        for (int t = 0; t < len; ++t) a = fmaf(sc_dyn[t], vc[(size_t)t * kvd + g * dim + d], a);
+        out[(size_t)h * dim + d] = a * inv;
+    }
+}
+
+}  // namespace pocr

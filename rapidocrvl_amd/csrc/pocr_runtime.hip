@@ -1,0 +1,1154 @@
+// pocr_runtime.hip — host runtime of the C ABI in include/pocr_hip.h.
+//
+// One context per device owns a HIP stream (default priority) and a mutex;
+// weights are uploaded once in their Q*_ROW layout; a sequence owns its
+// per-layer fp32 K/V cache in HBM, its step state and its scratch vectors, and
+// a captured HIP graph of the whole greedy decode step that is replayed token
+// after token without host round trips.
+#include <cmath>
+
+#include "internal.hpp"
+
+namespace pocr {
+
+static thread_local std::string g_err;
+
+int fail(int code, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+// POCR_HIP_FAIL_OP=<op>[,<op>...] makes the named ops return POCR_ERR_INJECTED
+// before touching the device, so a caller's CPU fallback can be exercised
+// (the reference disables a failing op and uses the CPU kernel,
+// internal/model/model.go:7240-7258).
+bool injected(const char *op) {
+    const char *env = getenv("POCR_HIP_FAIL_OP");
+    if (!env || !*env) return false;
+    std::string s(env);
+    size_t start = 0;
+    while (start <= s.size()) {
+        size_t end = s.find(',', start);
+        if (end == std::string::npos) end = s.size();
+        if (s.compare(start, end - start, op) == 0 || s.compare(start, end - start, "all") == 0) return true;
+        start = end + 1;
+    }
+    return false;
+}
+
+}  // namespace pocr
+
+using namespace pocr;
+
+extern "C" int pocr_abi_version(void) { return POCR_ABI_VERSION; }
+extern "C" const char *pocr_last_error(void) { return g_err.c_str(); }
+
+extern "C" int pocr_device_count(void) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) return 0;
+    return n;
+}
+
+static void free_dev(void *p) {
+    if (p) (void)hipFree(p);
+}
+
+pocr_seq::~pocr_seq() {
+    if (decode_exec) (void)hipGraphExecDestroy(decode_exec);
+    if (decode_graph) (void)hipGraphDestroy(decode_graph);
+    free_dev(kv);
+    free_dev(h);
+    free_dev(qkv);
+    free_dev(head_out);
+    free_dev(vbuf);
+    free_dev(g);
+    free_dev(logits);
+    free_dev(part);
+    free_dev(counter);
+    free_dev(st);
+    free_dev(tokens);
+    prefill_free(pf);
+}
+
+// ---------------------------------------------------------------------------
+// context
+// ---------------------------------------------------------------------------
+extern "C" int pocr_ctx_create(int device, pocr_ctx **out) {
+    if (!out) return fail(POCR_ERR_ARG, "pocr_ctx_create: null out");
+    *out = nullptr;
+    CHECK_INJECT("ctx");
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) return fail(POCR_ERR_DEVICE, "no HIP device visible");
+    if (device < 0 || device >= n) return fail(POCR_ERR_ARG, "device %d out of range [0,%d)", device, n);
+    HIP_TRY(hipSetDevice(device));
+    hipDeviceProp_t prop;
+    HIP_TRY(hipGetDeviceProperties(&prop, device));
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(POCR_ERR_UNSUPPORTED, "device %d is %s; this library is built for gfx950", device, prop.gcnArchName);
+    pocr_ctx *c = new pocr_ctx();
+    c->device = device;
+    if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
+        delete c;
+        return fail(POCR_ERR_DEVICE, "hipStreamCreate failed");
+    }
+    *out = c;
+    return POCR_OK;
+}
+
+extern "C" void pocr_ctx_destroy(pocr_ctx *ctx) {
+    if (!ctx) return;
+    (void)hipSetDevice(ctx->device);
+    if (ctx->stream) {
+        (void)hipStreamSynchronize(ctx->stream);
+        (void)hipStreamDestroy(ctx->stream);
+    }
+    delete ctx;
+}
+
+// ---------------------------------------------------------------------------
+// weights
+// ---------------------------------------------------------------------------
+static bool valid_qtype(int q) { return q == POCR_Q8 || q == POCR_Q4 || q == POCR_Q6; }
+
+extern "C" int pocr_weight_upload(pocr_ctx *ctx, int qtype, int rows, int cols, const float *scales,
+                                  const uint8_t *packed, pocr_weight **out) {
+    if (!ctx || !out || !scales || !packed) return fail(POCR_ERR_ARG, "pocr_weight_upload: null argument");
+    *out = nullptr;
+    if (!valid_qtype(qtype)) return fail(POCR_ERR_ARG, "pocr_weight_upload: unsupported type %d", qtype);
+    if (rows <= 0 || cols <= 0) return fail(POCR_ERR_ARG, "pocr_weight_upload: bad shape %dx%d", rows, cols);
+    CHECK_INJECT("weight_upload");
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    HIP_TRY(hipSetDevice(ctx->device));
+    const size_t rb = pocr_row_bytes(qtype, cols);
+    const size_t scale_bytes = (((size_t)rows * 4) + 255) & ~(size_t)255;  // keep rows 256-B aligned
+    const size_t data_bytes = rb * (size_t)rows;
+    void *base = nullptr;
+    HIP_TRY(hipMalloc(&base, scale_bytes + data_bytes + 64));  // +64: tail chunk over-read guard
+    hipError_t e = hipMemcpy(base, scales, (size_t)rows * 4, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy((uint8_t *)base + scale_bytes, packed, data_bytes, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemset((uint8_t *)base + scale_bytes + data_bytes, 0, 64);
+    if (e != hipSuccess) {
+        (void)hipFree(base);
+        return fail(POCR_ERR_DEVICE, "weight upload copy: %s", hipGetErrorString(e));
+    }
+    pocr_weight *w = new pocr_weight();
+    w->ctx = ctx;
+    w->qtype = qtype;
+    w->rows = rows;
+    w->cols = cols;
+    w->row_bytes = rb;
+    w->base = base;
+    w->scale = (const float *)base;
+    w->data = (const uint8_t *)base + scale_bytes;
+    *out = w;
+    return POCR_OK;
+}
+
+extern "C" void pocr_weight_free(pocr_weight *w) {
+    if (!w) return;
+    (void)hipSetDevice(w->ctx->device);
+    free_dev(w->base);
+    delete w;
+}
+
+DevMat pocr::dev_mat(const pocr_weight *w) {
+    DevMat m;
+    m.scale = w->scale;
+    m.data = w->data;
+    m.rows = w->rows;
+    m.cols = w->cols;
+    m.row_bytes = (int)w->row_bytes;
+    m.qtype = w->qtype;
+    return m;
+}
+
+// ---------------------------------------------------------------------------
+// GEMV dispatch
+// ---------------------------------------------------------------------------
+template <int QT, int NMAT, int TAG = 0>
+static bool gemv_fast_kernel(int lpr, int cpl, const void **fn) {
+    constexpr int U = 2;
+#define POCR_K(L, C)                                                           \
+    if (lpr == L && cpl == C) {                                                \
+        *fn = reinterpret_cast<const void *>(&k_gemv<QT, L, C, U, NMAT, TAG>); \
+        return true;                                                           \
+    }
+    POCR_K(64, 1)
+    POCR_K(64, 2)
+    POCR_K(64, 3)
+    POCR_K(64, 4)
+    POCR_K(32, 1)
+    POCR_K(32, 2)
+    POCR_K(32, 3)
+#undef POCR_K
+    return false;
+}
+
+struct GemvPlan {
+    const void *fn = nullptr;
+    int grid = 1;
+    size_t lds = 0;
+};
+
+// Choose the kernel for `rows` outputs of matrices with `cols` columns.
+// max_grid caps the workgroup count (rows loop inside the kernel).
+static int plan_gemv(int qtype, int nmat, int rows, int cols, const DevMat *mats, int nm, int max_grid,
+                     GemvPlan *plan, int tag = 0) {
+    if (cols > 16384) return fail(POCR_ERR_UNSUPPORTED, "gemv: cols %d > 16384", cols);
+    plan->lds = (size_t)cols * 4;
+    int W = qtype == POCR_Q4 ? 32 : 16;
+    int CB = qtype == POCR_Q6 ? 12 : 16;
+    bool fast = cols % W == 0;
+    int C = cols / W;
+    for (int i = 0; i < nm && fast; ++i) {
+        if (mats[i].row_bytes != C * CB) fast = false;
+        if (((uintptr_t)mats[i].data) % 16 != 0) fast = false;
+        if (mats[i].qtype != qtype || mats[i].cols != cols) fast = false;
+    }
+    int lpr = 0, cpl = 0;
+    if (fast) {
+        if (C % 64 == 0) lpr = 64;
+        else if (C % 32 == 0) lpr = 32;
+        else fast = false;
+        if (fast) {
+            cpl = C / lpr;
+            if (cpl > 4 || (lpr == 32 && cpl > 3)) fast = false;
+        }
+    }
+    bool ok = false;
+    if (fast && tag == 1 && nmat == 1) {
+        if (qtype == POCR_Q4) ok = gemv_fast_kernel<QT_Q4, 1, 1>(lpr, cpl, &plan->fn);
+        if (qtype == POCR_Q8) ok = gemv_fast_kernel<QT_Q8, 1, 1>(lpr, cpl, &plan->fn);
+        if (qtype == POCR_Q6) ok = gemv_fast_kernel<QT_Q6, 1, 1>(lpr, cpl, &plan->fn);
+    } else if (fast) {
+        if (nmat == 1) {
+            if (qtype == POCR_Q4) ok = gemv_fast_kernel<QT_Q4, 1>(lpr, cpl, &plan->fn);
+            if (qtype == POCR_Q8) ok = gemv_fast_kernel<QT_Q8, 1>(lpr, cpl, &plan->fn);
+            if (qtype == POCR_Q6) ok = gemv_fast_kernel<QT_Q6, 1>(lpr, cpl, &plan->fn);
+        } else {
+            if (qtype == POCR_Q4) ok = gemv_fast_kernel<QT_Q4, 2>(lpr, cpl, &plan->fn);
+            if (qtype == POCR_Q8) ok = gemv_fast_kernel<QT_Q8, 2>(lpr, cpl, &plan->fn);
+            if (qtype == POCR_Q6) ok = gemv_fast_kernel<QT_Q6, 2>(lpr, cpl, &plan->fn);
+        }
+    }
+    if (ok) {
+        const int rows_per_group = (64 / lpr) * 2;
+        const int groups = (rows + rows_per_group - 1) / rows_per_group;
+        plan->grid = std::max(1, std::min((groups + kWaves - 1) / kWaves, max_grid));
+    } else {
+        plan->fn = nmat == 1 ? reinterpret_cast<const void *>(&k_gemv_any<1>)
+                             : reinterpret_cast<const void *>(&k_gemv_any<2>);
+        plan->grid = std::max(1, std::min((rows + kWaves - 1) / kWaves, max_grid));
+    }
+    return POCR_OK;
+}
+
+static int launch_gemv(hipStream_t s, const GemvPlan &plan, GemvParams p, int pro, int epi) {
+    void *args[] = {&p, &pro, &epi};
+    HIP_TRY(hipLaunchKernel(plan.fn, dim3(plan.grid), dim3(kThreads), args, plan.lds, s));
+    return POCR_OK;
+}
+
+GemvParams pocr::gemv_params_1(const pocr_weight *w) {
+    GemvParams p{};
+    p.m[0] = p.m[1] = p.m[2] = dev_mat(w);
+    p.seg_end[0] = p.seg_end[1] = p.seg_end[2] = w->rows;
+    p.rows = w->rows;
+    p.cols = w->cols;
+    return p;
+}
+
+int pocr::gemv_launch(hipStream_t s, GemvParams p, int nmat, int pro, int epi, int max_grid) {
+    GemvPlan plan;
+    const int nm = nmat == 2 ? 2 : (p.seg_end[0] == p.rows ? 1 : (p.seg_end[1] == p.rows ? 2 : 3));
+    int rc = plan_gemv(p.m[0].qtype, nmat, p.rows, p.cols, p.m, nm, max_grid, &plan);
+    if (rc) return rc;
+    return launch_gemv(s, plan, p, pro, epi);
+}
+
+
+// ---------------------------------------------------------------------------
+// op level
+// ---------------------------------------------------------------------------
+#define CTX_GUARD(ctx)                                    \
+    std::lock_guard<std::mutex> lk_((ctx)->mu);           \
+    HIP_TRY(hipSetDevice((ctx)->device))
+
+static int h2d(hipStream_t s, void *dst, const void *src, size_t n) {
+    HIP_TRY(hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, s));
+    return POCR_OK;
+}
+static int d2h(hipStream_t s, void *dst, const void *src, size_t n) {
+    HIP_TRY(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToHost, s));
+    return POCR_OK;
+}
+static int sync(hipStream_t s) {
+    HIP_TRY(hipStreamSynchronize(s));
+    return POCR_OK;
+}
+extern "C" int pocr_matvec(pocr_ctx *ctx, const pocr_weight *w, const float *x, int m, float *out) {
+    if (!ctx || !w || !x || !out || m <= 0) return fail(POCR_ERR_ARG, "pocr_matvec: bad arguments");
+    if (w->ctx != ctx) return fail(POCR_ERR_ARG, "pocr_matvec: weight from another context");
+    CHECK_INJECT("matvec");
+    CTX_GUARD(ctx);
+    hipStream_t s = ctx->stream;
+    RC(ctx->x.ensure((size_t)m * w->cols * 4));
+    RC(ctx->out.ensure((size_t)m * w->rows * 4));
+    RC(h2d(s, ctx->x.p, x, (size_t)m * w->cols * 4));
+    if (m > 1) {
+        RC(batched_gemv(s, dev_mat(w), ctx->x.as<float>(), m, ctx->out.as<float>()));
+    } else {
+        GemvParams p = gemv_params_1(w);
+        p.x = ctx->x.as<float>();
+        p.out = ctx->out.as<float>();
+        RC(gemv_launch(s, p, 1, PRO_COPY, EPI_PLAIN, kBigGrid));
+    }
+    RC(d2h(s, out, ctx->out.p, (size_t)m * w->rows * 4));
+    return sync(s);
+}
+
+static float key_value(unsigned long long key) {
+    uint32_t ord = (uint32_t)(key >> 32);
+    uint32_t b = (ord & 0x80000000u) ? (ord & 0x7FFFFFFFu) : ~ord;
+    float f;
+    std::memcpy(&f, &b, 4);
+    return f;
+}
+
+extern "C" int pocr_matvec_argmax(pocr_ctx *ctx, const pocr_weight *w, const float *x, int32_t *index,
+                                  float *score) {
+    if (!ctx || !w || !x || !index) return fail(POCR_ERR_ARG, "pocr_matvec_argmax: bad arguments");
+    CHECK_INJECT("matvec_argmax");
+    CTX_GUARD(ctx);
+    hipStream_t s = ctx->stream;
+    RC(ctx->x.ensure((size_t)w->cols * 4));
+    RC(ctx->state.ensure(sizeof(StepState)));
+    RC(h2d(s, ctx->x.p, x, (size_t)w->cols * 4));
+    HIP_TRY(hipMemsetAsync(ctx->state.p, 0, sizeof(StepState), s));
+    GemvParams p = gemv_params_1(w);
+    p.x = ctx->x.as<float>();
+    p.st = ctx->state.as<StepState>();
+    RC(gemv_launch(s, p, 1, PRO_COPY, EPI_ARGMAX, kBigGrid));
+    StepState hst;
+    RC(d2h(s, &hst, ctx->state.p, sizeof(StepState)));
+    RC(sync(s));
+    if (hst.err) return fail(POCR_ERR_DEVICE, "matvec_argmax: device error %d", hst.err);
+    if (hst.argmax_key == 0ull) return fail(POCR_ERR_DEVICE, "matvec_argmax: no finite score");
+    *index = (int32_t)(0xFFFFFFFFu - (uint32_t)(hst.argmax_key & 0xFFFFFFFFull));
+    if (score) *score = key_value(hst.argmax_key);
+    return POCR_OK;
+}
+
+static int fused3(pocr_ctx *ctx, const pocr_weight *a, const pocr_weight *b, const pocr_weight *c,
+                  const float *x) {
+    hipStream_t s = ctx->stream;
+    const int rows = a->rows + b->rows + c->rows;
+    RC(ctx->x.ensure((size_t)a->cols * 4));
+    RC(ctx->out.ensure((size_t)rows * 4));
+    RC(h2d(s, ctx->x.p, x, (size_t)a->cols * 4));
+    GemvParams p{};
+    p.m[0] = dev_mat(a);
+    p.m[1] = dev_mat(b);
+    p.m[2] = dev_mat(c);
+    p.seg_end[0] = a->rows;
+    p.seg_end[1] = a->rows + b->rows;
+    p.seg_end[2] = rows;
+    p.rows = rows;
+    p.cols = a->cols;
+    p.x = ctx->x.as<float>();
+    p.out = ctx->out.as<float>();
+    return gemv_launch(s, p, 1, PRO_COPY, EPI_PLAIN, kBigGrid);
+}
+
+static int check3(const pocr_weight *a, const pocr_weight *b, const pocr_weight *c) {
+    if (!a || !b || !c) return fail(POCR_ERR_ARG, "fused_matvec3: null weight");
+    if (a->qtype != b->qtype || b->qtype != c->qtype || a->cols != b->cols || b->cols != c->cols)
+        return fail(POCR_ERR_ARG, "fused_matvec3: weights differ in type or columns");
+    if (a->ctx != b->ctx || b->ctx != c->ctx) return fail(POCR_ERR_ARG, "fused_matvec3: mixed contexts");
+    return POCR_OK;
+}
+
+extern "C" int pocr_fused_matvec3(pocr_ctx *ctx, const pocr_weight *a, const pocr_weight *b, const pocr_weight *c,
+                                  const float *x, float *out_a, float *out_b, float *out_c) {
+    if (!ctx || !x || !out_a || !out_b || !out_c) return fail(POCR_ERR_ARG, "pocr_fused_matvec3: null argument");
+    RC(check3(a, b, c));
+    CHECK_INJECT("fused_matvec3");
+    CTX_GUARD(ctx);
+    hipStream_t s = ctx->stream;
+    RC(fused3(ctx, a, b, c, x));
+    float *o = ctx->out.as<float>();
+    RC(d2h(s, out_a, o, (size_t)a->rows * 4));
+    RC(d2h(s, out_b, o + a->rows, (size_t)b->rows * 4));
+    RC(d2h(s, out_c, o + a->rows + b->rows, (size_t)c->rows * 4));
+    return sync(s);
+}
+
+extern "C" int pocr_fused_matvec3_mrope(pocr_ctx *ctx, const pocr_weight *a, const pocr_weight *b,
+                                        const pocr_weight *c, const float *x, const float *cos_t,
+                                        const float *sin_t, int q_heads, int kv_heads, int head_dim,
+                                        float *out_a, float *out_b, float *out_c) {
+    if (!ctx || !x || !cos_t || !sin_t || !out_a || !out_b || !out_c)
+        return fail(POCR_ERR_ARG, "pocr_fused_matvec3_mrope: null argument");
+    RC(check3(a, b, c));
+    if (head_dim <= 0 || head_dim % 2 || q_heads * head_dim != a->rows || kv_heads * head_dim != b->rows)
+        return fail(POCR_ERR_ARG, "pocr_fused_matvec3_mrope: heads/head_dim do not match rows");
+    CHECK_INJECT("fused_matvec3_mrope");
+    CTX_GUARD(ctx);
+    hipStream_t s = ctx->stream;
+    RC(fused3(ctx, a, b, c, x));
+    const int half = head_dim / 2;
+    RC(ctx->tabs.ensure((size_t)half * 8));
+    RC(h2d(s, ctx->tabs.p, cos_t, (size_t)half * 4));
+    RC(h2d(s, ctx->tabs.as<float>() + half, sin_t, (size_t)half * 4));
+    float *o = ctx->out.as<float>();
+    const int total = (q_heads + kv_heads) * half;
+    hipLaunchKernelGGL(k_rope, dim3((total + kThreads - 1) / kThreads), dim3(kThreads), 0, s, o, o + a->rows,
+                       ctx->tabs.as<float>(), ctx->tabs.as<float>() + half, q_heads, kv_heads, head_dim);
+    HIP_TRY(hipGetLastError());
+    RC(d2h(s, out_a, o, (size_t)a->rows * 4));
+    RC(d2h(s, out_b, o + a->rows, (size_t)b->rows * 4));
+    RC(d2h(s, out_c, o + a->rows + b->rows, (size_t)c->rows * 4));
+    return sync(s);
+}
+
+extern "C" int pocr_swiglu_gate_up(pocr_ctx *ctx, const pocr_weight *gate, const pocr_weight *up, const float *x,
+                                   float *out) {
+    if (!ctx || !gate || !up || !x || !out) return fail(POCR_ERR_ARG, "pocr_swiglu_gate_up: null argument");
+    if (gate->rows != up->rows || gate->cols != up->cols || gate->qtype != up->qtype)
+        return fail(POCR_ERR_ARG, "pocr_swiglu_gate_up: gate/up shapes differ");
+    CHECK_INJECT("swiglu_gate_up");
+    CTX_GUARD(ctx);
+    hipStream_t s = ctx->stream;
+    RC(ctx->x.ensure((size_t)gate->cols * 4));
+    RC(ctx->out.ensure((size_t)gate->rows * 4));
+    RC(h2d(s, ctx->x.p, x, (size_t)gate->cols * 4));
+    GemvParams p = gemv_params_1(gate);
+    p.m[1] = dev_mat(up);
+    p.x = ctx->x.as<float>();
+    p.out = ctx->out.as<float>();
+    RC(gemv_launch(s, p, 2, PRO_COPY, EPI_SWIGLU, kBigGrid));
+    RC(d2h(s, out, ctx->out.p, (size_t)gate->rows * 4));
+    return sync(s);
+}
+
+extern "C" int pocr_matvec_add_rmsnorm(pocr_ctx *ctx, const pocr_weight *w, const float *x, float *residual,
+                                       const float *norm_w, float eps, int in_place, float *norm_out) {
+    if (!ctx || !w || !x || !residual || !norm_w || !norm_out)
+        return fail(POCR_ERR_ARG, "pocr_matvec_add_rmsnorm: null argument");
+    CHECK_INJECT("matvec_add_rmsnorm");
+    CTX_GUARD(ctx);
+    hipStream_t s = ctx->stream;
+    const int n = w->rows;
+    RC(ctx->x.ensure((size_t)w->cols * 4));
+    RC(ctx->res.ensure((size_t)n * 4 * 2));
+    RC(ctx->vbuf.ensure((size_t)n * 4));
+    RC(ctx->out.ensure((size_t)n * 4));
+    RC(h2d(s, ctx->x.p, x, (size_t)w->cols * 4));
+    RC(h2d(s, ctx->res.p, residual, (size_t)n * 4));
+    RC(h2d(s, ctx->res.as<float>() + n, norm_w, (size_t)n * 4));
+    GemvParams p = gemv_params_1(w);
+    p.x = ctx->x.as<float>();
+    p.residual = ctx->res.as<float>();
+    p.vbuf = ctx->vbuf.as<float>();
+    RC(gemv_launch(s, p, 1, PRO_COPY, EPI_ADDV, kBigGrid));
+    hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(kThreads), 0, s, ctx->vbuf.as<float>(), ctx->res.as<float>() + n, n,
+                       eps, ctx->out.as<float>());
+    HIP_TRY(hipGetLastError());
+    RC(d2h(s, norm_out, ctx->out.p, (size_t)n * 4));
+    if (in_place) RC(d2h(s, residual, ctx->vbuf.p, (size_t)n * 4));
+    return sync(s);
+}
+
+extern "C" int pocr_rmsnorm(pocr_ctx *ctx, const float *x, const float *w, int n, float eps, float *out) {
+    if (!ctx || !x || !w || !out || n <= 0) return fail(POCR_ERR_ARG, "pocr_rmsnorm: bad arguments");
+    CHECK_INJECT("rmsnorm");
+    CTX_GUARD(ctx);
+    hipStream_t s = ctx->stream;
+    RC(ctx->x.ensure((size_t)n * 8));
+    RC(ctx->out.ensure((size_t)n * 4));
+    RC(h2d(s, ctx->x.p, x, (size_t)n * 4));
+    RC(h2d(s, ctx->x.as<float>() + n, w, (size_t)n * 4));
+    hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(kThreads), 0, s, ctx->x.as<float>(), ctx->x.as<float>() + n, n, eps,
+                       ctx->out.as<float>());
+    HIP_TRY(hipGetLastError());
+    RC(d2h(s, out, ctx->out.p, (size_t)n * 4));
+    return sync(s);
+}
+
+extern "C" int pocr_mrope_pair(pocr_ctx *ctx, float *q, float *k, const float *cos_t, const float *sin_t,
+                               int q_heads, int kv_heads, int head_dim) {
+    if (!ctx || !q || !k || !cos_t || !sin_t || head_dim <= 0 || head_dim % 2 || q_heads <= 0 || kv_heads <= 0)
+        return fail(POCR_ERR_ARG, "pocr_mrope_pair: bad arguments");
+    CHECK_INJECT("mrope_pair");
+    CTX_GUARD(ctx);
+    hipStream_t s = ctx->stream;
+    const int half = head_dim / 2;
+    const size_t nq = (size_t)q_heads * head_dim, nk = (size_t)kv_heads * head_dim;
+    RC(ctx->x.ensure((nq + nk) * 4));
+    RC(ctx->tabs.ensure((size_t)half * 8));
+    RC(h2d(s, ctx->x.p, q, nq * 4));
+    RC(h2d(s, ctx->x.as<float>() + nq, k, nk * 4));
+    RC(h2d(s, ctx->tabs.p, cos_t, (size_t)half * 4));
+    RC(h2d(s, ctx->tabs.as<float>() + half, sin_t, (size_t)half * 4));
+    const int total = (q_heads + kv_heads) * half;
+    hipLaunchKernelGGL(k_rope, dim3((total + kThreads - 1) / kThreads), dim3(kThreads), 0, s, ctx->x.as<float>(),
+                       ctx->x.as<float>() + nq, ctx->tabs.as<float>(), ctx->tabs.as<float>() + half, q_heads,
+                       kv_heads, head_dim);
+    HIP_TRY(hipGetLastError());
+    RC(d2h(s, q, ctx->x.p, nq * 4));
+    RC(d2h(s, k, ctx->x.as<float>() + nq, nk * 4));
+    return sync(s);
+}
+
+static int attn_nsplit(int cap) { return std::max(32, (cap + kMaxChunk - 1) / kMaxChunk); }
+
+extern "C" int pocr_text_attention(pocr_ctx *ctx, const float *q, const float *k_cache, const float *v_cache,
+                                   int cache_len, int heads, int kv_heads, int head_dim, float *out) {
+    if (!ctx || !q || !k_cache || !v_cache || !out || cache_len <= 0 || heads <= 0 || kv_heads <= 0 ||
+        head_dim <= 0 || heads % kv_heads)
+        return fail(POCR_ERR_ARG, "pocr_text_attention: bad arguments");
+    CHECK_INJECT("text_attention");
+    CTX_GUARD(ctx);
+    hipStream_t s = ctx->stream;
+    const size_t kvd = (size_t)kv_heads * head_dim;
+    const size_t nq = (size_t)heads * head_dim;
+    RC(ctx->x.ensure(nq * 4));
+    RC(ctx->kc.ensure(kvd * cache_len * 4));
+    RC(ctx->vc.ensure(kvd * cache_len * 4));
+    RC(ctx->out.ensure(nq * 4));
+    RC(h2d(s, ctx->x.p, q, nq * 4));
+    RC(h2d(s, ctx->kc.p, k_cache, kvd * cache_len * 4));
+    RC(h2d(s, ctx->vc.p, v_cache, kvd * cache_len * 4));
+    const float scale = (float)(1.0 / std::sqrt((double)head_dim));  // invSqrt, model.go:7391
+    const int group = heads / kv_heads;
+    if (head_dim == kHD && group <= kMaxGroup) {
+        const int nsplit = attn_nsplit(cache_len);
+        RC(ctx->part.ensure((size_t)kv_heads * nsplit * kMaxGroup * (kHD + 2) * 4));
+        RC(ctx->counter.ensure((size_t)kv_heads * 4));
+        HIP_TRY(hipMemsetAsync(ctx->counter.p, 0, (size_t)kv_heads * 4, s));
+        AttnParams p{};
+        p.q = ctx->x.as<float>();
+        p.kc = ctx->kc.as<float>();
+        p.vc = ctx->vc.as<float>();
+        p.st = nullptr;
+        p.len = cache_len;
+        p.has_rope = 0;
+        p.part = ctx->part.as<float>();
+        p.counter = ctx->counter.as<unsigned int>();
+        p.head_out = ctx->out.as<float>();
+        p.heads = heads;
+        p.kvh = kv_heads;
+        p.nsplit = nsplit;
+        p.scale = scale;
+        hipLaunchKernelGGL(k_attn_decode, dim3(kv_heads, nsplit), dim3(kThreads), 0, s, p);
+    } else {
+        if ((size_t)cache_len * 4 > 60 * 1024) return fail(POCR_ERR_UNSUPPORTED, "text_attention: cache too long");
+        hipLaunchKernelGGL(k_attn_small, dim3(heads), dim3(kThreads), (size_t)cache_len * 4, s, ctx->x.as<float>(),
+                           ctx->kc.as<float>(), ctx->vc.as<float>(), cache_len, heads, kv_heads, head_dim, scale,
+                           ctx->out.as<float>());
+    }
+    HIP_TRY(hipGetLastError());
+    RC(d2h(s, out, ctx->out.p, nq * 4));
+    return sync(s);
+}
+
+// ---------------------------------------------------------------------------
+// model
+// ---------------------------------------------------------------------------
+extern "C" int pocr_model_create(pocr_ctx *ctx, const pocr_config *cfg, pocr_model **out) {
+    if (!ctx || !cfg || !out) return fail(POCR_ERR_ARG, "pocr_model_create: null argument");
+    *out = nullptr;
+    const pocr_config &c = *cfg;
+    if (c.hidden <= 0 || c.intermediate <= 0 || c.layers <= 0 || c.heads <= 0 || c.kv_heads <= 0 ||
+        c.head_dim <= 0 || c.vocab <= 0 || c.heads % c.kv_heads || c.head_dim % 2)
+        return fail(POCR_ERR_ARG, "pocr_model_create: invalid config");
+    if (c.head_dim != kHD || c.heads / c.kv_heads > kMaxGroup)
+        return fail(POCR_ERR_UNSUPPORTED, "pocr_model_create: step path needs head_dim 128 and group <= 8");
+    if (c.hidden > 16384 || c.intermediate > 16384 || c.heads * c.head_dim > 16384)
+        return fail(POCR_ERR_UNSUPPORTED, "pocr_model_create: width > 16384");
+    CHECK_INJECT("model");
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    HIP_TRY(hipSetDevice(ctx->device));
+    pocr_model *m = new pocr_model();
+    m->ctx = ctx;
+    m->cfg = c;
+    m->layers.resize(c.layers);
+    // initTextRoPE (model.go:877-902): freq_i = theta^(-2i/d) in f64, axis from
+    // the mrope sections (default 16,24,24), clamped to 2
+    const int half = c.head_dim / 2;
+    int sec[3] = {c.mrope_section[0], c.mrope_section[1], c.mrope_section[2]};
+    if (sec[0] == 0 && sec[1] == 0 && sec[2] == 0) {
+        sec[0] = 16;
+        sec[1] = 24;
+        sec[2] = 24;
+    }
+    m->h_freq.resize(half);
+    m->h_axis.resize(half);
+    int section_end = sec[0], ax = 0;
+    for (int i = 0; i < half; ++i) {
+        while (ax + 1 < 3 && i >= section_end) {
+            ++ax;
+            section_end += sec[ax];
+        }
+        m->h_axis[i] = (uint8_t)std::min(ax, 2);
+        m->h_freq[i] = std::pow(c.rope_theta, -(double)(2 * i) / (double)c.head_dim);
+    }
+    hipError_t e = hipMalloc(&m->freq, half * sizeof(double));
+    if (e == hipSuccess) e = hipMalloc(&m->axis, half);
+    if (e == hipSuccess) e = hipMemcpy(m->freq, m->h_freq.data(), half * sizeof(double), hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(m->axis, m->h_axis.data(), half, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        free_dev(m->freq);
+        free_dev(m->axis);
+        delete m;
+        return fail(POCR_ERR_DEVICE, "model tables: %s", hipGetErrorString(e));
+    }
+    *out = m;
+    return POCR_OK;
+}
+
+extern "C" void pocr_model_destroy(pocr_model *m) {
+    if (!m) return;
+    (void)hipSetDevice(m->ctx->device);
+    for (auto &l : m->layers) {
+        free_dev(l.ln1);
+        free_dev(l.ln2);
+    }
+    free_dev(m->final_norm);
+    free_dev(m->embed);
+    free_dev(m->freq);
+    free_dev(m->axis);
+    delete m;
+}
+
+extern "C" int pocr_model_set_weight(pocr_model *m, int layer, int role, const pocr_weight *w) {
+    if (!m || !w) return fail(POCR_ERR_ARG, "pocr_model_set_weight: null argument");
+    if (w->ctx != m->ctx) return fail(POCR_ERR_ARG, "pocr_model_set_weight: weight from another context");
+    const pocr_config &c = m->cfg;
+    const int q_rows = c.heads * c.head_dim, kv_rows = c.kv_heads * c.head_dim;
+    if (layer == -1 && role == POCR_W_LM_HEAD) {
+        if (w->rows != c.vocab || w->cols != c.hidden) return fail(POCR_ERR_ARG, "lm_head shape mismatch");
+        m->lm = w;
+        return POCR_OK;
+    }
+    if (layer < 0 || layer >= c.layers || role < 0 || role > POCR_W_DOWN)
+        return fail(POCR_ERR_ARG, "pocr_model_set_weight: bad layer/role %d/%d", layer, role);
+    static const char *names[] = {"q", "k", "v", "o", "gate", "up", "down"};
+    const int want_rows[] = {q_rows, kv_rows, kv_rows, c.hidden, c.intermediate, c.intermediate, c.hidden};
+    const int want_cols[] = {c.hidden, c.hidden, c.hidden, q_rows, c.hidden, c.hidden, c.intermediate};
+    if (w->rows != want_rows[role] || w->cols != want_cols[role])
+        return fail(POCR_ERR_ARG, "layer %d %s: shape %dx%d, want %dx%d", layer, names[role], w->rows, w->cols,
+                    want_rows[role], want_cols[role]);
+    m->layers[layer].w[role] = w;
+    return POCR_OK;
+}
+
+static int upload_floats(pocr_ctx *ctx, float **dst, const float *src, size_t n) {
+    if (!*dst) HIP_TRY(hipMalloc(dst, n * 4));
+    HIP_TRY(hipMemcpy(*dst, src, n * 4, hipMemcpyHostToDevice));
+    (void)ctx;
+    return POCR_OK;
+}
+
+extern "C" int pocr_model_set_norm(pocr_model *m, int layer, int role, const float *w) {
+    if (!m || !w) return fail(POCR_ERR_ARG, "pocr_model_set_norm: null argument");
+    std::lock_guard<std::mutex> lk(m->ctx->mu);
+    HIP_TRY(hipSetDevice(m->ctx->device));
+    const size_t n = m->cfg.hidden;
+    if (layer == -1 && role == POCR_N_FINAL) return upload_floats(m->ctx, &m->final_norm, w, n);
+    if (layer < 0 || layer >= m->cfg.layers || (role != POCR_N_LN1 && role != POCR_N_LN2))
+        return fail(POCR_ERR_ARG, "pocr_model_set_norm: bad layer/role %d/%d", layer, role);
+    return upload_floats(m->ctx, role == POCR_N_LN1 ? &m->layers[layer].ln1 : &m->layers[layer].ln2, w, n);
+}
+
+extern "C" int pocr_model_set_embed(pocr_model *m, const float *embed) {
+    if (!m || !embed) return fail(POCR_ERR_ARG, "pocr_model_set_embed: null argument");
+    std::lock_guard<std::mutex> lk(m->ctx->mu);
+    HIP_TRY(hipSetDevice(m->ctx->device));
+    return upload_floats(m->ctx, &m->embed, embed, (size_t)m->cfg.vocab * m->cfg.hidden);
+}
+
+extern "C" int pocr_model_set_residual_quirk(pocr_model *m, int on) {
+    if (!m) return fail(POCR_ERR_ARG, "pocr_model_set_residual_quirk: null model");
+    m->quirk = on ? 1 : 0;
+    return POCR_OK;
+}
+
+static int model_ready(const pocr_model *m) {
+    for (int l = 0; l < m->cfg.layers; ++l) {
+        for (int r = 0; r < 7; ++r)
+            if (!m->layers[l].w[r]) return fail(POCR_ERR_ARG, "layer %d weight %d not set", l, r);
+        if (!m->layers[l].ln1 || !m->layers[l].ln2) return fail(POCR_ERR_ARG, "layer %d norms not set", l);
+        const int qt = m->layers[l].w[0]->qtype;
+        for (int r = 1; r < 3; ++r)
+            if (m->layers[l].w[r]->qtype != qt) return fail(POCR_ERR_ARG, "layer %d q/k/v types differ", l);
+        if (m->layers[l].w[4]->qtype != m->layers[l].w[5]->qtype)
+            return fail(POCR_ERR_ARG, "layer %d gate/up types differ", l);
+    }
+    if (!m->lm || !m->final_norm || !m->embed) return fail(POCR_ERR_ARG, "lm_head/final norm/embedding not set");
+    return POCR_OK;
+}
+
+// ---------------------------------------------------------------------------
+// sequences
+// ---------------------------------------------------------------------------
+extern "C" int pocr_seq_create(pocr_model *m, int capacity, pocr_seq **out) {
+    if (!m || !out || capacity <= 0) return fail(POCR_ERR_ARG, "pocr_seq_create: bad arguments");
+    *out = nullptr;
+    CHECK_INJECT("seq");
+    std::lock_guard<std::mutex> lk(m->ctx->mu);
+    HIP_TRY(hipSetDevice(m->ctx->device));
+    const pocr_config &c = m->cfg;
+    pocr_seq *s = new pocr_seq();
+    s->m = m;
+    s->cap = capacity;
+    s->nsplit = attn_nsplit(capacity);
+    s->max_tokens = capacity + 1;
+    const size_t kvd = (size_t)c.kv_heads * c.head_dim;
+    const size_t q_rows = (size_t)c.heads * c.head_dim;
+    const size_t qkv = q_rows + 2 * kvd;
+    hipError_t e = hipMalloc(&s->kv, (size_t)c.layers * 2 * capacity * kvd * 4);
+    if (e == hipSuccess) e = hipMalloc(&s->h, (size_t)c.hidden * 4);
+    if (e == hipSuccess) e = hipMalloc(&s->qkv, qkv * 4);
+    if (e == hipSuccess) e = hipMalloc(&s->head_out, q_rows * 4);
+    if (e == hipSuccess) e = hipMalloc(&s->vbuf, (size_t)c.hidden * 4);
+    if (e == hipSuccess) e = hipMalloc(&s->g, (size_t)c.intermediate * 4);
+    if (e == hipSuccess) e = hipMalloc(&s->logits, (size_t)c.vocab * 4);
+    if (e == hipSuccess) e = hipMalloc(&s->part, (size_t)c.kv_heads * s->nsplit * kMaxGroup * (kHD + 2) * 4);
+    if (e == hipSuccess) e = hipMalloc(&s->counter, (size_t)c.kv_heads * 4);
+    if (e == hipSuccess) e = hipMalloc(&s->st, sizeof(StepState));
+    if (e == hipSuccess) e = hipMalloc(&s->tokens, (size_t)s->max_tokens * 4);
+    if (e == hipSuccess) e = hipMemset(s->counter, 0, (size_t)c.kv_heads * 4);
+    if (e == hipSuccess) e = hipMemset(s->kv, 0, (size_t)c.layers * 2 * capacity * kvd * 4);
+    if (e != hipSuccess) {
+        delete s;
+        return fail(POCR_ERR_NOMEM, "pocr_seq_create(%d): %s", capacity, hipGetErrorString(e));
+    }
+    StepState st{};
+    st.cap = capacity;
+    st.half = c.head_dim / 2;
+    e = hipMemcpy(s->st, &st, sizeof(st), hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        delete s;
+        return fail(POCR_ERR_DEVICE, "pocr_seq_create: %s", hipGetErrorString(e));
+    }
+    *out = s;
+    return POCR_OK;
+}
+
+extern "C" void pocr_seq_destroy(pocr_seq *s) {
+    if (!s) return;
+    std::lock_guard<std::mutex> lk(s->m->ctx->mu);
+    (void)hipSetDevice(s->m->ctx->device);
+    (void)hipStreamSynchronize(s->m->ctx->stream);
+    delete s;
+}
+
+float *pocr::layer_k(const pocr_seq *s, int layer) {
+    const pocr_config &c = s->m->cfg;
+    return s->kv + (size_t)layer * 2 * s->cap * c.kv_heads * c.head_dim;
+}
+float *pocr::layer_v(const pocr_seq *s, int layer) {
+    const pocr_config &c = s->m->cfg;
+    return layer_k(s, layer) + (size_t)s->cap * c.kv_heads * c.head_dim;
+}
+
+int pocr::seq_set_state(pocr_seq *s, int len) {
+    StepState st{};
+    st.len = len;
+    st.cap = s->cap;
+    st.half = s->m->cfg.head_dim / 2;
+    HIP_TRY(hipMemcpyAsync(s->st, &st, sizeof(st), hipMemcpyHostToDevice, s->m->ctx->stream));
+    HIP_TRY(hipStreamSynchronize(s->m->ctx->stream));
+    s->len = len;
+    return POCR_OK;
+}
+
+extern "C" int pocr_seq_reset(pocr_seq *s) {
+    if (!s) return fail(POCR_ERR_ARG, "pocr_seq_reset: null");
+    std::lock_guard<std::mutex> lk(s->m->ctx->mu);
+    HIP_TRY(hipSetDevice(s->m->ctx->device));
+    return seq_set_state(s, 0);
+}
+
+extern "C" int pocr_seq_len(const pocr_seq *s) { return s ? s->len : POCR_ERR_ARG; }
+
+extern "C" int pocr_seq_read_kv(pocr_seq *s, int layer, float *k, float *v) {
+    if (!s || !k || !v || layer < 0 || layer >= s->m->cfg.layers) return fail(POCR_ERR_ARG, "pocr_seq_read_kv");
+    std::lock_guard<std::mutex> lk(s->m->ctx->mu);
+    HIP_TRY(hipSetDevice(s->m->ctx->device));
+    const size_t n = (size_t)s->len * s->m->cfg.kv_heads * s->m->cfg.head_dim * 4;
+    if (n == 0) return POCR_OK;
+    HIP_TRY(hipMemcpy(k, layer_k(s, layer), n, hipMemcpyDeviceToHost));
+    HIP_TRY(hipMemcpy(v, layer_v(s, layer), n, hipMemcpyDeviceToHost));
+    return POCR_OK;
+}
+
+extern "C" int pocr_seq_write_kv(pocr_seq *s, int layer, const float *k, const float *v, int len) {
+    if (!s || !k || !v || layer < 0 || layer >= s->m->cfg.layers || len < 0 || len > s->cap)
+        return fail(POCR_ERR_ARG, "pocr_seq_write_kv: bad arguments");
+    std::lock_guard<std::mutex> lk(s->m->ctx->mu);
+    HIP_TRY(hipSetDevice(s->m->ctx->device));
+    const size_t n = (size_t)len * s->m->cfg.kv_heads * s->m->cfg.head_dim * 4;
+    if (n) {
+        HIP_TRY(hipMemcpy(layer_k(s, layer), k, n, hipMemcpyHostToDevice));
+        HIP_TRY(hipMemcpy(layer_v(s, layer), v, n, hipMemcpyHostToDevice));
+    }
+    return seq_set_state(s, len);
+}
+
+extern "C" int pocr_seq_truncate(pocr_seq *s, int len) {
+    if (!s || len < 0 || len > s->len) return fail(POCR_ERR_ARG, "pocr_seq_truncate: bad length");
+    std::lock_guard<std::mutex> lk(s->m->ctx->mu);
+    HIP_TRY(hipSetDevice(s->m->ctx->device));
+    return seq_set_state(s, len);
+}
+
+extern "C" int pocr_time_matvec(pocr_ctx *ctx, const pocr_weight *const *weights, int n_weights, const float *x,
+                                int iters, float *avg_us) {
+    if (!ctx || !weights || n_weights <= 0 || !x || iters <= 0 || !avg_us)
+        return fail(POCR_ERR_ARG, "pocr_time_matvec: bad arguments");
+    for (int i = 0; i < n_weights; ++i)
+        if (!weights[i] || weights[i]->rows != weights[0]->rows || weights[i]->cols != weights[0]->cols ||
+            weights[i]->qtype != weights[0]->qtype || weights[i]->ctx != ctx)
+            return fail(POCR_ERR_ARG, "pocr_time_matvec: weights differ in shape/type/context");
+    CHECK_INJECT("time_matvec");
+    CTX_GUARD(ctx);
+    hipStream_t s = ctx->stream;
+    const pocr_weight *w0 = weights[0];
+    RC(ctx->x.ensure((size_t)w0->cols * 4));
+    RC(ctx->out.ensure((size_t)w0->rows * 4));
+    RC(h2d(s, ctx->x.p, x, (size_t)w0->cols * 4));
+    GemvPlan plan;
+    DevMat dm = dev_mat(w0);
+    RC(plan_gemv(w0->qtype, 1, w0->rows, w0->cols, &dm, 1, kBigGrid, &plan, 1));
+    hipEvent_t e0, e1;
+    HIP_TRY(hipEventCreate(&e0));
+    HIP_TRY(hipEventCreate(&e1));
+    // warm-up pass over every copy
+    for (int i = 0; i < n_weights; ++i) {
+        GemvParams p = gemv_params_1(weights[i]);
+        p.x = ctx->x.as<float>();
+        p.out = ctx->out.as<float>();
+        RC(launch_gemv(s, plan, p, PRO_COPY, EPI_PLAIN));
+    }
+    HIP_TRY(hipEventRecord(e0, s));
+    for (int it = 0; it < iters; ++it) {
+        GemvParams p = gemv_params_1(weights[it % n_weights]);
+        p.x = ctx->x.as<float>();
+        p.out = ctx->out.as<float>();
+        RC(launch_gemv(s, plan, p, PRO_COPY, EPI_PLAIN));
+    }
+    HIP_TRY(hipEventRecord(e1, s));
+    HIP_TRY(hipEventSynchronize(e1));
+    float ms = 0.0f;
+    HIP_TRY(hipEventElapsedTime(&ms, e0, e1));
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    *avg_us = ms * 1000.0f / (float)iters;
+    return POCR_OK;
+}
+
+// ---------------------------------------------------------------------------
+// the decoder step on the device
+// ---------------------------------------------------------------------------
+
+// One layer (model.go:3492-3603 with attentionWithNorm 3850-4066 and
+// mlpDownAddRMSNormCPU 5714-5800).  last/kv_only select the final-layer
+// variants.
+static int enqueue_layer(pocr_seq *s, int li, bool last, bool kv_only) {
+    pocr_model *m = s->m;
+    const pocr_config &c = m->cfg;
+    hipStream_t st = m->ctx->stream;
+    const LayerW &L = m->layers[li];
+    const int q_rows = c.heads * c.head_dim, kv_rows = c.kv_heads * c.head_dim;
+    const float eps = c.rms_norm_eps;
+
+    // 1. x = RMSNorm(h)·ln1 (recomputed per workgroup) → q|k|v
+    GemvParams p{};
+    p.m[0] = dev_mat(L.w[POCR_W_Q]);
+    p.m[1] = dev_mat(L.w[POCR_W_K]);
+    p.m[2] = dev_mat(L.w[POCR_W_V]);
+    p.seg_end[0] = q_rows;
+    p.seg_end[1] = q_rows + kv_rows;
+    p.seg_end[2] = q_rows + 2 * kv_rows;
+    p.rows = q_rows + 2 * kv_rows;
+    p.cols = c.hidden;
+    p.x = s->h;
+    p.norm_w = L.ln1;
+    p.eps = eps;
+    p.out = s->qkv;
+    p.st = s->st;
+    RC(gemv_launch(st, p, 1, PRO_RMSNORM, EPI_PLAIN, kBigGrid));
+
+    // 2. RoPE + KV append + split-K attention → head_out
+    AttnParams a{};
+    a.q = s->qkv;
+    a.k_new = s->qkv + q_rows;
+    a.v_new = s->qkv + q_rows + kv_rows;
+    a.kc = layer_k(s, li);
+    a.vc = layer_v(s, li);
+    a.st = s->st;
+    a.part = s->part;
+    a.counter = s->counter;
+    a.head_out = s->head_out;
+    a.heads = c.heads;
+    a.kvh = c.kv_heads;
+    a.nsplit = s->nsplit;
+    a.scale = (float)(1.0 / std::sqrt((double)c.head_dim));
+    hipLaunchKernelGGL(k_attn_decode, dim3(c.kv_heads, s->nsplit), dim3(kThreads), 0, st, a);
+    HIP_TRY(hipGetLastError());
+    if (kv_only) return POCR_OK;
+
+    // 3. o_proj + residual (+quirk) → vbuf (= h + attn), h updated if in place
+    const pocr_weight *wo = L.w[POCR_W_O];
+    GemvParams o = gemv_params_1(wo);
+    o.x = s->head_out;
+    o.residual = s->h;
+    o.vbuf = s->vbuf;
+    o.st = s->st;
+    o.quirk = (m->quirk && (wo->qtype == POCR_Q4 || wo->qtype == POCR_Q6)) ? 1 : 0;
+    RC(gemv_launch(st, o, 1, PRO_COPY, EPI_OPROJ, kBigGrid));
+
+    // 4. RMSNorm(vbuf)·ln2 → gate/up → SiLU(g)·u
+    GemvParams gu = gemv_params_1(L.w[POCR_W_GATE]);
+    gu.m[1] = dev_mat(L.w[POCR_W_UP]);
+    gu.x = s->vbuf;
+    gu.norm_w = L.ln2;
+    gu.eps = eps;
+    gu.out = s->g;
+    gu.st = s->st;
+    RC(gemv_launch(st, gu, 2, PRO_RMSNORM, EPI_SWIGLU, kBigGrid));
+
+    // 5. down + residual: h += W_down·g (in place); last layer: vbuf = h + down (OutOnly)
+    GemvParams d = gemv_params_1(L.w[POCR_W_DOWN]);
+    d.x = s->g;
+    d.residual = s->h;
+    d.vbuf = s->vbuf;
+    d.st = s->st;
+    d.flag = last ? 1 : 0;
+    RC(gemv_launch(st, d, 1, PRO_COPY, EPI_DOWN, kBigGrid));
+    return POCR_OK;
+}
+
+// LM head on RMSNorm(vbuf)·final_norm, argmax into the step state
+static int enqueue_head(pocr_seq *s, bool want_logits) {
+    pocr_model *m = s->m;
+    GemvParams p = gemv_params_1(m->lm);
+    p.x = s->vbuf;
+    p.norm_w = m->final_norm;
+    p.eps = m->cfg.rms_norm_eps;
+    p.out = want_logits ? s->logits : nullptr;
+    p.st = s->st;
+    return gemv_launch(m->ctx->stream, p, 1, PRO_RMSNORM, EPI_ARGMAX, kBigGrid);
+}
+
+static int enqueue_step(pocr_seq *s, int mode, bool need_logits, bool want_logits) {
+    pocr_model *m = s->m;
+    const pocr_config &c = m->cfg;
+    hipStream_t st = m->ctx->stream;
+    hipLaunchKernelGGL(k_step_begin, dim3(1), dim3(kThreads), 0, st, s->st, m->embed, s->h, c.hidden, c.vocab,
+                       m->freq, m->axis, mode, s->tokens, s->max_tokens);
+    HIP_TRY(hipGetLastError());
+    for (int li = 0; li < c.layers; ++li) {
+        const bool last = li + 1 == c.layers;
+        RC(enqueue_layer(s, li, last, last && !need_logits));
+    }
+    if (need_logits) RC(enqueue_head(s, want_logits));
+    return POCR_OK;
+}
+
+static int read_state(pocr_seq *s, StepState *out) {
+    HIP_TRY(hipMemcpyAsync(out, s->st, sizeof(StepState), hipMemcpyDeviceToHost, s->m->ctx->stream));
+    HIP_TRY(hipStreamSynchronize(s->m->ctx->stream));
+    return POCR_OK;
+}
+
+int pocr::step_locked(pocr_seq *s, const float *emb, const int32_t pos3[3], int need_logits, float *logits,
+                       int32_t *token) {
+    pocr_model *m = s->m;
+    hipStream_t st = m->ctx->stream;
+    if (s->len >= s->cap) return fail(POCR_ERR_ARG, "pocr_step: cache full (%d rows)", s->cap);
+    RC(h2d(st, s->h, emb, (size_t)m->cfg.hidden * 4));
+    RC(h2d(st, &s->st->pos, pos3, 12));
+    RC(enqueue_step(s, 0, need_logits != 0, logits != nullptr));
+    StepState hs;
+    RC(read_state(s, &hs));
+    if (hs.err) return fail(POCR_ERR_DEVICE, "step: device state error %d", hs.err);
+    s->len = hs.len;
+    if (need_logits) {
+        if (token) {
+            if (hs.argmax_key == 0ull) return fail(POCR_ERR_DEVICE, "step: no finite logit");
+            *token = (int32_t)(0xFFFFFFFFu - (uint32_t)(hs.argmax_key & 0xFFFFFFFFull));
+        }
+        if (logits) {
+            HIP_TRY(hipMemcpy(logits, s->logits, (size_t)m->cfg.vocab * 4, hipMemcpyDeviceToHost));
+        }
+    }
+    return POCR_OK;
+}
+
+extern "C" int pocr_step(pocr_seq *s, const float *emb, const int32_t pos3[3], int need_logits, float *logits,
+                         int32_t *token) {
+    if (!s || !emb || !pos3) return fail(POCR_ERR_ARG, "pocr_step: null argument");
+    RC(model_ready(s->m));
+    CHECK_INJECT("step");
+    std::lock_guard<std::mutex> lk(s->m->ctx->mu);
+    HIP_TRY(hipSetDevice(s->m->ctx->device));
+    return step_locked(s, emb, pos3, need_logits, logits, token);
+}
+
+static int build_decode_graph(pocr_seq *s) {
+    if (s->decode_exec) return POCR_OK;
+    hipStream_t st = s->m->ctx->stream;
+    HIP_TRY(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+    int rc = enqueue_step(s, 1, true, false);
+    hipGraph_t graph = nullptr;
+    hipError_t e = hipStreamEndCapture(st, &graph);
+    if (rc != POCR_OK) {
+        if (graph) (void)hipGraphDestroy(graph);
+        return rc;
+    }
+    if (e != hipSuccess) return fail(POCR_ERR_DEVICE, "graph capture: %s", hipGetErrorString(e));
+    e = hipGraphInstantiate(&s->decode_exec, graph, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        (void)hipGraphDestroy(graph);
+        return fail(POCR_ERR_DEVICE, "graph instantiate: %s", hipGetErrorString(e));
+    }
+    s->decode_graph = graph;
+    return POCR_OK;
+}
+
+static bool is_eos(int32_t t, const int32_t *eos, int n) {
+    for (int i = 0; i < n; ++i)
+        if (eos[i] == t) return true;
+    return false;
+}
+
+// Greedy decode loop (model.go:1538-1568) with the step graph replayed on the
+// device.  Tokens are checked for EOS every `batch` steps; steps run past an
+// EOS only append rows nobody reads.
+static int decode_locked(pocr_seq *s, int32_t first_token, int32_t first_pos, int max_new, const int32_t *eos,
+                         int n_eos, int32_t *out_tokens) {
+    pocr_model *m = s->m;
+    hipStream_t st = m->ctx->stream;
+    if (max_new <= 0) return 0;
+    if (first_token < 0 || first_token >= m->cfg.vocab) return fail(POCR_ERR_ARG, "decode: token out of vocab");
+    const int steps_needed = max_new - 1;  // the last token needs no step
+    if (s->len + steps_needed > s->cap)
+        return fail(POCR_ERR_ARG, "decode: %d steps exceed capacity (%d of %d rows used)", steps_needed, s->len,
+                    s->cap);
+    RC(build_decode_graph(s));
+    StepState hs;
+    RC(read_state(s, &hs));
+    hs.err = 0;
+    hs.n_out = 0;
+    hs.next_pos = first_pos;
+    hs.argmax_key = (1ull << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)first_token);
+    HIP_TRY(hipMemcpyAsync(s->st, &hs, sizeof(hs), hipMemcpyHostToDevice, st));
+    HIP_TRY(hipStreamSynchronize(st));  // hs is reused as a read-back target below
+    int produced = 0;  // tokens known on the host
+    int launched = 0;
+    const int batch = 16;
+    std::vector<int32_t> tok;
+    while (launched < steps_needed) {
+        const int n = std::min(batch, steps_needed - launched);
+        for (int i = 0; i < n; ++i) HIP_TRY(hipGraphLaunch(s->decode_exec, st));
+        launched += n;
+        RC(read_state(s, &hs));
+        if (hs.err) return fail(POCR_ERR_DEVICE, "decode: device state error %d", hs.err);
+        tok.resize(hs.n_out);
+        HIP_TRY(hipMemcpy(tok.data(), s->tokens, (size_t)hs.n_out * 4, hipMemcpyDeviceToHost));
+        for (; produced < hs.n_out; ++produced) {
+            out_tokens[produced] = tok[produced];
+            if (is_eos(tok[produced], eos, n_eos)) {
+                s->len = hs.len;
+                return produced + 1;
+            }
+        }
+    }
+    // the token chosen by the last step
+    out_tokens[produced] = (int32_t)(0xFFFFFFFFu - (uint32_t)(hs.argmax_key & 0xFFFFFFFFull));
+    ++produced;
+    s->len = hs.len;
+    return produced;
+}
+
+extern "C" int pocr_decode_greedy(pocr_seq *s, int32_t first_token, int32_t first_pos, int max_new,
+                                  const int32_t *eos, int n_eos, int32_t *out_tokens) {
+    if (!s || !out_tokens || (n_eos > 0 && !eos)) return fail(POCR_ERR_ARG, "pocr_decode_greedy: null argument");
+    RC(model_ready(s->m));
+    CHECK_INJECT("decode");
+    std::lock_guard<std::mutex> lk(s->m->ctx->mu);
+    HIP_TRY(hipSetDevice(s->m->ctx->device));
+    return decode_locked(s, first_token, first_pos, max_new, eos, n_eos, out_tokens);
+}
+
+extern "C" int pocr_prefill(pocr_seq *s, int n, const float *emb, const int32_t *pos3, float *logits,
+                            int32_t *token) {
+    if (!s || !emb || !pos3 || n <= 0) return fail(POCR_ERR_ARG, "pocr_prefill: bad arguments");
+    RC(model_ready(s->m));
+    CHECK_INJECT("prefill");
+    std::lock_guard<std::mutex> lk(s->m->ctx->mu);
+    HIP_TRY(hipSetDevice(s->m->ctx->device));
+    if (s->len + n > s->cap) return fail(POCR_ERR_ARG, "pocr_prefill: %d rows exceed capacity", n);
+    return prefill_locked(s, n, emb, pos3, logits, token);
+}
+
+extern "C" int pocr_generate(pocr_seq *s, const int32_t *ids, int n_ids, const float *image_embeds, int n_image,
+                             int32_t image_token_id, const int32_t grid[3], int32_t merge, int max_new,
+                             const int32_t *eos, int n_eos, int use_prefill, int32_t *out_tokens) {
+    if (!s || !ids || n_ids <= 0 || !out_tokens || (n_image > 0 && (!image_embeds || !grid)))
+        return fail(POCR_ERR_ARG, "pocr_generate: bad arguments");
+    if (max_new <= 0) return 0;
+    RC(model_ready(s->m));
+    CHECK_INJECT("generate");
+    pocr_model *m = s->m;
+    const int H = m->cfg.hidden;
+    // positions (model.go:1717-1783) and embeddings (tokenEmbeddingInto 3251 /
+    // image rows substituted for placeholders 1646-1652)
+    std::vector<int32_t> pos((size_t)n_ids * 3);
+    int32_t rope_delta = 0;
+    if (n_image > 0) {
+        int np = pocr_mm_positions(ids, n_ids, image_token_id, grid, merge, pos.data(), &rope_delta);
+        if (np != n_ids) return fail(POCR_ERR_ARG, "pocr_generate: image grid does not match placeholders");
+    } else {
+        for (int i = 0; i < n_ids; ++i) pos[3 * i] = pos[3 * i + 1] = pos[3 * i + 2] = i;
+    }
+    std::vector<float> emb((size_t)n_ids * H);
+    std::vector<float> row(H);
+    int img = 0;
+    {
+        std::lock_guard<std::mutex> lk(m->ctx->mu);
+        HIP_TRY(hipSetDevice(m->ctx->device));
+        for (int i = 0; i < n_ids; ++i) {
+            if (n_image > 0 && ids[i] == image_token_id) {
+                if (img >= n_image) return fail(POCR_ERR_ARG, "too many image placeholder tokens");
+                std::memcpy(&emb[(size_t)i * H], image_embeds + (size_t)img * H, (size_t)H * 4);
+                ++img;
+            } else {
+                if (ids[i] < 0 || ids[i] >= m->cfg.vocab) return fail(POCR_ERR_ARG, "token id %d outside vocab", ids[i]);
+                HIP_TRY(hipMemcpy(&emb[(size_t)i * H], m->embed + (size_t)ids[i] * H, (size_t)H * 4,
+                                  hipMemcpyDeviceToHost));
+            }
+        }
+        if (img != n_image) return fail(POCR_ERR_ARG, "not enough image placeholder tokens: got %d need %d", img, n_image);
+        RC(seq_set_state(s, 0));
+        if (n_ids + max_new - 1 > s->cap) return fail(POCR_ERR_ARG, "pocr_generate: capacity %d too small", s->cap);
+        int32_t next = -1;
+        if (use_prefill) {
+            RC(prefill_locked(s, n_ids, emb.data(), pos.data(), nullptr, &next));
+        } else {
+            for (int i = 0; i < n_ids; ++i)
+                RC(step_locked(s, &emb[(size_t)i * H], &pos[3 * i], i == n_ids - 1, nullptr,
+                               i == n_ids - 1 ? &next : nullptr));
+        }
+        // first decode token sits at position len(out)-1+ropeDelta = n_ids+rope_delta
+        return decode_locked(s, next, n_ids + rope_delta, max_new, eos, n_eos, out_tokens);
+    }
+}

@@ -1,0 +1,413 @@
+"""ctypes binding of libpocr_hip.so (include/pocr_hip.h).
+
+This is the host-side mirror of the reference's ``internal/backend`` hip
+implementation: a thin wrapper that converts numpy arrays to pointers and
+status codes to exceptions.  Loading fails loudly if the native library is
+missing — there is no CPU fallback in this package.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import re
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "_lib", "libpocr_hip.so")
+HEADER = os.path.join(os.path.dirname(HERE), "include", "pocr_hip.h")
+
+POCR_OK = 0
+POCR_ERR_ARG = -1
+POCR_ERR_DEVICE = -2
+POCR_ERR_NOMEM = -3
+POCR_ERR_UNSUPPORTED = -4
+POCR_ERR_INJECTED = -5
+
+F32, Q8, Q4, Q6 = 0, 1000, 1001, 1002
+TIE_HALF_AWAY, TIE_AMD64 = 0, 1
+W_Q, W_K, W_V, W_O, W_GATE, W_UP, W_DOWN, W_LM_HEAD = range(8)
+N_LN1, N_LN2, N_FINAL = 0, 1, 2
+
+
+class PocrError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"[{code}] {msg}")
+        self.code = code
+
+
+class PocrConfig(C.Structure):
+    _fields_ = [
+        ("hidden", C.c_int32), ("intermediate", C.c_int32), ("layers", C.c_int32),
+        ("heads", C.c_int32), ("kv_heads", C.c_int32), ("head_dim", C.c_int32),
+        ("vocab", C.c_int32), ("rms_norm_eps", C.c_float), ("rope_theta", C.c_double),
+        ("mrope_section", C.c_int32 * 3),
+    ]
+
+
+_vp = C.c_void_p
+_i = C.c_int
+_SIGS = {
+    "pocr_abi_version": (_i, []),
+    "pocr_last_error": (C.c_char_p, []),
+    "pocr_ctx_create": (_i, [_i, C.POINTER(_vp)]),
+    "pocr_ctx_destroy": (None, [_vp]),
+    "pocr_device_count": (_i, []),
+    "pocr_row_bytes": (C.c_size_t, [_i, _i]),
+    "pocr_quantize_rows": (_i, [_i, _i, _vp, _i, _i, _vp, _vp]),
+    "pocr_unpack_rows": (_i, [_i, _vp, _i, _i, _vp]),
+    "pocr_weight_upload": (_i, [_vp, _i, _i, _i, _vp, _vp, C.POINTER(_vp)]),
+    "pocr_weight_free": (None, [_vp]),
+    "pocr_matvec": (_i, [_vp, _vp, _vp, _i, _vp]),
+    "pocr_matvec_argmax": (_i, [_vp, _vp, _vp, _vp, _vp]),
+    "pocr_fused_matvec3": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "pocr_fused_matvec3_mrope": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp, _vp, _vp]),
+    "pocr_swiglu_gate_up": (_i, [_vp, _vp, _vp, _vp, _vp]),
+    "pocr_matvec_add_rmsnorm": (_i, [_vp, _vp, _vp, _vp, _vp, C.c_float, _i, _vp]),
+    "pocr_rmsnorm": (_i, [_vp, _vp, _vp, _i, C.c_float, _vp]),
+    "pocr_mrope_pair": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i]),
+    "pocr_text_attention": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
+    "pocr_model_create": (_i, [_vp, C.POINTER(PocrConfig), C.POINTER(_vp)]),
+    "pocr_model_destroy": (None, [_vp]),
+    "pocr_model_set_weight": (_i, [_vp, _i, _i, _vp]),
+    "pocr_model_set_norm": (_i, [_vp, _i, _i, _vp]),
+    "pocr_model_set_embed": (_i, [_vp, _vp]),
+    "pocr_model_set_residual_quirk": (_i, [_vp, _i]),
+    "pocr_seq_create": (_i, [_vp, _i, C.POINTER(_vp)]),
+    "pocr_seq_destroy": (None, [_vp]),
+    "pocr_seq_reset": (_i, [_vp]),
+    "pocr_seq_len": (_i, [_vp]),
+    "pocr_seq_read_kv": (_i, [_vp, _i, _vp, _vp]),
+    "pocr_seq_truncate": (_i, [_vp, _i]),
+    "pocr_time_matvec": (_i, [_vp, _vp, _i, _vp, _i, _vp]),
+    "pocr_seq_write_kv": (_i, [_vp, _i, _vp, _vp, _i]),
+    "pocr_step": (_i, [_vp, _vp, _vp, _i, _vp, _vp]),
+    "pocr_prefill": (_i, [_vp, _i, _vp, _vp, _vp, _vp]),
+    "pocr_decode_greedy": (_i, [_vp, C.c_int32, C.c_int32, _i, _vp, _i, _vp]),
+    "pocr_generate": (_i, [_vp, _vp, _i, _vp, _i, C.c_int32, _vp, C.c_int32, _i, _vp, _i, _i, _vp]),
+    "pocr_mm_positions": (_i, [_vp, _i, C.c_int32, _vp, C.c_int32, _vp, _vp]),
+}
+
+_lib = None
+
+
+def header_symbols(path: str = HEADER):
+    """Function names declared in include/pocr_hip.h."""
+    text = open(path).read()
+    return sorted(set(re.findall(r"\b(pocr_[a-z0-9_]+)\s*\(", text)))
+
+
+def load():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise OSError(f"{LIB_PATH} is missing; run __graft_entry__.build() (or python rapidocrvl_amd/build.py)")
+        L = C.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data
+
+
+def check(rc: int):
+    if rc < 0:
+        raise PocrError(rc, load().pocr_last_error().decode(errors="replace"))
+    return rc
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def row_bytes(qtype: int, cols: int) -> int:
+    return int(load().pocr_row_bytes(qtype, cols))
+
+
+def quantize_rows(qtype: int, w, tie: int = TIE_HALF_AWAY):
+    """QuantizeQ*Row over a [rows, cols] f32 matrix → (scales, packed[rows, row_bytes])."""
+    w = _f32(w)
+    rows, cols = w.shape
+    scales = np.zeros(rows, np.float32)
+    packed = np.zeros((rows, row_bytes(qtype, cols)), np.uint8)
+    check(load().pocr_quantize_rows(qtype, tie, _ptr(w), rows, cols, _ptr(scales), _ptr(packed)))
+    return scales, packed
+
+
+def unpack_rows(qtype: int, packed, cols: int):
+    packed = np.ascontiguousarray(packed, dtype=np.uint8)
+    rows = packed.shape[0]
+    out = np.zeros((rows, cols), np.int8)
+    check(load().pocr_unpack_rows(qtype, _ptr(packed), rows, cols, _ptr(out)))
+    return out
+
+
+def mm_positions(ids, image_token_id: int, grid, merge: int = 2):
+    ids = np.ascontiguousarray(ids, dtype=np.int32)
+    pos = np.zeros((max(ids.size, 1), 3), np.int32)
+    delta = np.zeros(1, np.int32)
+    g = np.ascontiguousarray(grid, dtype=np.int32)
+    n = check(load().pocr_mm_positions(_ptr(ids), ids.size, image_token_id, _ptr(g), merge, _ptr(pos), _ptr(delta)))
+    return pos[:n], int(delta[0])
+
+
+def device_count() -> int:
+    return int(load().pocr_device_count())
+
+
+class QMatrix:
+    """Host copy of one Q*_ROW tensor (tensor.Q8Matrix/Q4Matrix/Q6Matrix, quant.go:5-29)."""
+
+    def __init__(self, qtype: int, rows: int, cols: int, scales, packed):
+        self.qtype, self.rows, self.cols = qtype, rows, cols
+        self.scales = _f32(scales)
+        self.packed = np.ascontiguousarray(packed, dtype=np.uint8).reshape(rows, row_bytes(qtype, cols))
+
+    @classmethod
+    def quantize(cls, w, qtype: int, tie: int = TIE_HALF_AWAY):
+        w = _f32(w)
+        s, p = quantize_rows(qtype, w, tie)
+        return cls(qtype, w.shape[0], w.shape[1], s, p)
+
+
+class Weight:
+    def __init__(self, ctx: "Context", q: QMatrix):
+        self.ctx, self.q = ctx, q
+        self.rows, self.cols, self.qtype = q.rows, q.cols, q.qtype
+        h = _vp()
+        check(load().pocr_weight_upload(ctx.h, q.qtype, q.rows, q.cols, _ptr(q.scales), _ptr(q.packed), C.byref(h)))
+        self.h = h
+
+    def close(self):
+        if getattr(self, "h", None):
+            load().pocr_weight_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+
+class Context:
+    """One device context: the op-level mirror of backend.Vulkan* calls."""
+
+    def __init__(self, device: int = 0):
+        h = _vp()
+        check(load().pocr_ctx_create(device, C.byref(h)))
+        self.h = h
+
+    def close(self):
+        if getattr(self, "h", None):
+            load().pocr_ctx_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def upload(self, q: QMatrix) -> Weight:
+        return Weight(self, q)
+
+    # -- op level ---------------------------------------------------------
+    def matvec(self, w: Weight, x):
+        x = _f32(x)
+        m = 1 if x.ndim == 1 else x.shape[0]
+        out = np.zeros((m, w.rows), np.float32)
+        check(load().pocr_matvec(self.h, w.h, _ptr(x), m, _ptr(out)))
+        return out[0] if x.ndim == 1 else out
+
+    def matvec_argmax(self, w: Weight, x):
+        x = _f32(x)
+        idx = np.zeros(1, np.int32)
+        sc = np.zeros(1, np.float32)
+        check(load().pocr_matvec_argmax(self.h, w.h, _ptr(x), _ptr(idx), _ptr(sc)))
+        return int(idx[0]), float(sc[0])
+
+    def fused_matvec3(self, a: Weight, b: Weight, c: Weight, x):
+        x = _f32(x)
+        oa, ob, oc = (np.zeros(w.rows, np.float32) for w in (a, b, c))
+        check(load().pocr_fused_matvec3(self.h, a.h, b.h, c.h, _ptr(x), _ptr(oa), _ptr(ob), _ptr(oc)))
+        return oa, ob, oc
+
+    def fused_matvec3_mrope(self, a, b, c, x, cos_t, sin_t, q_heads, kv_heads, head_dim):
+        x, cos_t, sin_t = _f32(x), _f32(cos_t), _f32(sin_t)
+        oa, ob, oc = (np.zeros(w.rows, np.float32) for w in (a, b, c))
+        check(load().pocr_fused_matvec3_mrope(self.h, a.h, b.h, c.h, _ptr(x), _ptr(cos_t), _ptr(sin_t), q_heads,
+                                              kv_heads, head_dim, _ptr(oa), _ptr(ob), _ptr(oc)))
+        return oa, ob, oc
+
+    def swiglu_gate_up(self, gate: Weight, up: Weight, x):
+        x = _f32(x)
+        out = np.zeros(gate.rows, np.float32)
+        check(load().pocr_swiglu_gate_up(self.h, gate.h, up.h, _ptr(x), _ptr(out)))
+        return out
+
+    def matvec_add_rmsnorm(self, w: Weight, x, residual, norm_w, eps, in_place=True):
+        """Returns (norm_out, residual_after)."""
+        x, norm_w = _f32(x), _f32(norm_w)
+        res = _f32(residual).copy()
+        out = np.zeros(w.rows, np.float32)
+        check(load().pocr_matvec_add_rmsnorm(self.h, w.h, _ptr(x), _ptr(res), _ptr(norm_w), eps, int(in_place),
+                                             _ptr(out)))
+        return out, res
+
+    def rmsnorm(self, x, w, eps):
+        x, w = _f32(x), _f32(w)
+        out = np.zeros_like(x)
+        check(load().pocr_rmsnorm(self.h, _ptr(x), _ptr(w), x.size, eps, _ptr(out)))
+        return out
+
+    def mrope_pair(self, q, k, cos_t, sin_t, q_heads, kv_heads, head_dim):
+        q, k = _f32(q).copy(), _f32(k).copy()
+        check(load().pocr_mrope_pair(self.h, _ptr(q), _ptr(k), _ptr(_f32(cos_t)), _ptr(_f32(sin_t)), q_heads,
+                                     kv_heads, head_dim))
+        return q, k
+
+    def time_matvec(self, weights, x, iters):
+        """Average µs per launch of the M=1 GEMV rotating over `weights`."""
+        x = _f32(x)
+        arr = (_vp * len(weights))(*[w.h for w in weights])
+        us = np.zeros(1, np.float32)
+        check(load().pocr_time_matvec(self.h, arr, len(weights), _ptr(x), iters, _ptr(us)))
+        return float(us[0])
+
+    def text_attention(self, q, k_cache, v_cache, cache_len, heads, kv_heads, head_dim):
+        q, kc, vc = _f32(q), _f32(k_cache), _f32(v_cache)
+        out = np.zeros(heads * head_dim, np.float32)
+        check(load().pocr_text_attention(self.h, _ptr(q), _ptr(kc), _ptr(vc), cache_len, heads, kv_heads, head_dim,
+                                         _ptr(out)))
+        return out
+
+
+class Model:
+    """Device-resident decoder (weights borrowed, norms/embedding copied)."""
+
+    def __init__(self, ctx: Context, cfg):
+        self.ctx, self.cfg = ctx, cfg
+        c = PocrConfig(cfg.hidden, cfg.inter, cfg.layers, cfg.heads, cfg.kv_heads, cfg.head_dim, cfg.vocab,
+                       cfg.eps, cfg.rope_theta, (C.c_int32 * 3)(*cfg.mrope_section))
+        h = _vp()
+        check(load().pocr_model_create(ctx.h, C.byref(c), C.byref(h)))
+        self.h = h
+        self._weights = []
+
+    def close(self):
+        if getattr(self, "h", None):
+            load().pocr_model_destroy(self.h)
+            self.h = None
+        for w in self._weights:
+            w.close()
+        self._weights = []
+
+    def __del__(self):
+        self.close()
+
+    def set_weight(self, layer: int, role: int, q: QMatrix):
+        w = self.ctx.upload(q)
+        self._weights.append(w)
+        check(load().pocr_model_set_weight(self.h, layer, role, w.h))
+        return w
+
+    def set_norm(self, layer: int, role: int, w):
+        w = _f32(w)
+        check(load().pocr_model_set_norm(self.h, layer, role, _ptr(w)))
+
+    def set_embed(self, e):
+        e = _f32(e)
+        check(load().pocr_model_set_embed(self.h, _ptr(e)))
+
+    def set_residual_quirk(self, on: bool):
+        check(load().pocr_model_set_residual_quirk(self.h, int(on)))
+
+    def load_weights(self, weights):
+        roles = {"q": W_Q, "k": W_K, "v": W_V, "o": W_O, "gate": W_GATE, "up": W_UP, "down": W_DOWN}
+        for li, lw in enumerate(weights["layers"]):
+            for name, role in roles.items():
+                qt, sc, data, cols = lw[name]
+                self.set_weight(li, role, QMatrix(qt, sc.size, cols, sc, data))
+            self.set_norm(li, N_LN1, lw["ln1"])
+            self.set_norm(li, N_LN2, lw["ln2"])
+        qt, sc, data, cols = weights["lm_head"]
+        self.set_weight(-1, W_LM_HEAD, QMatrix(qt, sc.size, cols, sc, data))
+        self.set_norm(-1, N_FINAL, weights["final_norm"])
+        self.set_embed(weights["embed"])
+
+    def seq(self, capacity: int) -> "Sequence":
+        return Sequence(self, capacity)
+
+
+class Sequence:
+    def __init__(self, model: Model, capacity: int):
+        self.model = model
+        h = _vp()
+        check(load().pocr_seq_create(model.h, capacity, C.byref(h)))
+        self.h = h
+        self.capacity = capacity
+
+    def close(self):
+        if getattr(self, "h", None):
+            load().pocr_seq_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def __len__(self):
+        return check(load().pocr_seq_len(self.h))
+
+    def reset(self):
+        check(load().pocr_seq_reset(self.h))
+
+    def read_kv(self, layer: int):
+        cfg = self.model.cfg
+        n = len(self) * cfg.kv_heads * cfg.head_dim
+        k = np.zeros(max(n, 1), np.float32)
+        v = np.zeros(max(n, 1), np.float32)
+        check(load().pocr_seq_read_kv(self.h, layer, _ptr(k), _ptr(v)))
+        return k[:n], v[:n]
+
+    def truncate(self, length: int):
+        check(load().pocr_seq_truncate(self.h, length))
+
+    def write_kv(self, layer: int, k, v, length: int):
+        check(load().pocr_seq_write_kv(self.h, layer, _ptr(_f32(k)), _ptr(_f32(v)), length))
+
+    def step(self, emb, pos3, need_logits=True, want_logits=True):
+        cfg = self.model.cfg
+        emb = _f32(emb)
+        pos = np.ascontiguousarray(pos3, dtype=np.int32)
+        logits = np.zeros(cfg.vocab, np.float32) if (need_logits and want_logits) else None
+        tok = np.zeros(1, np.int32)
+        check(load().pocr_step(self.h, _ptr(emb), _ptr(pos), int(need_logits), _ptr(logits),
+                               _ptr(tok) if need_logits else None))
+        return (int(tok[0]) if need_logits else None), logits
+
+    def prefill(self, emb, pos3, want_logits=False):
+        cfg = self.model.cfg
+        emb = _f32(emb)
+        pos = np.ascontiguousarray(pos3, dtype=np.int32)
+        logits = np.zeros(cfg.vocab, np.float32) if want_logits else None
+        tok = np.zeros(1, np.int32)
+        check(load().pocr_prefill(self.h, emb.shape[0], _ptr(emb), _ptr(pos), _ptr(logits), _ptr(tok)))
+        return int(tok[0]), logits
+
+    def decode_greedy(self, first_token: int, first_pos: int, max_new: int, eos=(2,)):
+        eos = np.ascontiguousarray(list(eos) if eos else [-(1 << 30)], dtype=np.int32)
+        out = np.zeros(max(max_new, 1), np.int32)
+        n = check(load().pocr_decode_greedy(self.h, first_token, first_pos, max_new, _ptr(eos), eos.size, _ptr(out)))
+        return out[:n]
+
+    def generate(self, ids, max_new, eos=(2,), image_embeds=None, image_token_id=-1, grid=(1, 1, 1), merge=2,
+                 use_prefill=False):
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        eos = np.ascontiguousarray(list(eos) if eos else [-(1 << 30)], dtype=np.int32)
+        out = np.zeros(max(max_new, 1), np.int32)
+        img = _f32(image_embeds) if image_embeds is not None else None
+        n_img = 0 if img is None else img.shape[0]
+        g = np.ascontiguousarray(grid, dtype=np.int32)
+        n = check(load().pocr_generate(self.h, _ptr(ids), ids.size, _ptr(img), n_img, image_token_id, _ptr(g), merge,
+                                       max_new, _ptr(eos), eos.size, int(use_prefill), _ptr(out)))
+        return out[:n]

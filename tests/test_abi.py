@@ -1,0 +1,49 @@
+"""The C-ABI library loads, exports what include/pocr_hip.h declares, and
+rejects bad input before touching a device.  No GPU needed."""
+import ctypes as C
+import os
+
+import numpy as np
+import pytest
+
+from rapidocrvl_amd import lib
+
+
+def test_library_exports_every_header_symbol():
+    L = lib.load()
+    names = lib.header_symbols()
+    assert len(names) >= 30
+    missing = [n for n in names if not hasattr(L, n)]
+    assert not missing, missing
+    assert set(names) == set(lib._SIGS), "ctypes signatures out of sync with the header"
+
+
+def test_abi_version():
+    assert lib.load().pocr_abi_version() == 1
+
+
+def test_null_arguments_are_arg_errors():
+    L = lib.load()
+    assert L.pocr_matvec(None, None, None, 1, None) == lib.POCR_ERR_ARG
+    assert L.pocr_step(None, None, None, 1, None, None) == lib.POCR_ERR_ARG
+    assert L.pocr_quantize_rows(7, 0, None, 1, 1, None, None) == lib.POCR_ERR_ARG
+    assert b"pocr_step" in L.pocr_last_error()
+
+
+def test_fault_injection_is_reported_before_device_work(monkeypatch):
+    monkeypatch.setenv("POCR_HIP_FAIL_OP", "ctx")
+    h = C.c_void_p()
+    rc = lib.load().pocr_ctx_create(0, C.byref(h))
+    assert rc == lib.POCR_ERR_INJECTED
+    assert b"injected" in lib.load().pocr_last_error()
+
+
+@pytest.mark.skipif(lib.device_count() > 0, reason="a device is visible")
+def test_no_device_is_a_device_error():
+    h = C.c_void_p()
+    assert lib.load().pocr_ctx_create(0, C.byref(h)) == lib.POCR_ERR_DEVICE
+
+
+def test_positions_reject_grid_larger_than_placeholders():
+    with pytest.raises(lib.PocrError):
+        lib.mm_positions([1, 7, 7, 2], 7, (1, 4, 4))

@@ -1,0 +1,169 @@
+"""Op-level parity of the HIP kernels against the oracle (through the C ABI)."""
+import math
+
+import numpy as np
+import pytest
+
+from rapidocrvl_amd import lib
+
+pytestmark = pytest.mark.gpu
+
+Q8, Q4, Q6 = 1000, 1001, 1002
+SHAPES = [(3072, 1024), (1024, 3072), (2560, 1024), (1024, 2048), (103424, 1024)]
+
+
+def _qmat(rng, rows, cols, qtype, std=0.02):
+    w = (rng.standard_normal((rows, cols)) * std).astype(np.float32)
+    return lib.QMatrix.quantize(w, qtype)
+
+
+def _close(got, want, rel=2e-5):
+    scale = max(1.0, float(np.max(np.abs(want))))
+    err = float(np.max(np.abs(np.asarray(got, np.float64) - want)))
+    assert err <= rel * scale, f"max err {err} vs scale {scale}"
+
+
+@pytest.mark.parametrize("qtype", [Q8, Q4, Q6], ids=["q8", "q4", "q6"])
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: f"{s[0]}x{s[1]}")
+def test_matvec_decoder_shapes(ctx, orc, rng, qtype, shape):
+    q = _qmat(rng, *shape, qtype)
+    x = rng.standard_normal(shape[1]).astype(np.float32)
+    w = ctx.upload(q)
+    got = ctx.matvec(w, x)
+    want = orc.matvec(qtype, q.scales, q.packed, x)
+    _close(got, want)
+
+
+@pytest.mark.parametrize("qtype", [Q8, Q4, Q6], ids=["q8", "q4", "q6"])
+@pytest.mark.parametrize("shape", [(1, 1), (3, 5), (7, 33), (130, 100), (65, 96), (4, 5), (2, 3), (40, 4000)])
+def test_matvec_odd_shapes(ctx, orc, rng, qtype, shape):
+    q = _qmat(rng, *shape, qtype, std=1.0)
+    x = rng.standard_normal(shape[1]).astype(np.float32)
+    got = ctx.matvec(ctx.upload(q), x)
+    _close(got, orc.matvec(qtype, q.scales, q.packed, x))
+
+
+@pytest.mark.parametrize("qtype", [Q8, Q4, Q6], ids=["q8", "q4", "q6"])
+def test_matvec_closed_form_known_answers(ctx, orc, qtype):
+    # internal/backend/vulkan_exec_test.go:1938-2160 inputs, tol 1e-4
+    cases = [
+        (np.array([[1, 0, 0, 0, 0], [0, 1, 2, 0, 0], [-1, 0, 0, 0.25, 1], [0.5] * 5], np.float32),
+         np.array([2, -1, 0.5, 4, -3], np.float32)),
+        (np.array([[1] * 5, [1, 0, 0, 0, -1], [0, 2, 0, -1, 0], [-1] * 5], np.float32),
+         np.array([1, 2, 3, 4, 5], np.float32)),
+        (np.array([[1, 2, 0], [-1, 0, 1]], np.float32), np.array([3, -2, 5], np.float32)),
+    ]
+    for w, x in cases:
+        q = lib.QMatrix.quantize(w, qtype)
+        got = ctx.matvec(ctx.upload(q), x)
+        assert np.max(np.abs(got - orc.matvec(qtype, q.scales, q.packed, x))) <= 1e-4
+
+
+@pytest.mark.parametrize("qtype", [Q8, Q4, Q6], ids=["q8", "q4", "q6"])
+@pytest.mark.parametrize("m", [2, 4, 16])
+def test_batched_matvec(ctx, orc, rng, qtype, m):
+    q = _qmat(rng, 3072, 1024, qtype)
+    x = rng.standard_normal((m, 1024)).astype(np.float32)
+    got = ctx.matvec(ctx.upload(q), x)
+    for i in range(m):
+        _close(got[i], orc.matvec(qtype, q.scales, q.packed, x[i]), rel=5e-5)
+
+
+@pytest.mark.parametrize("qtype", [Q8, Q4, Q6], ids=["q8", "q4", "q6"])
+def test_matvec_argmax(ctx, orc, rng, qtype):
+    q = _qmat(rng, 103424, 1024, qtype)
+    w = ctx.upload(q)
+    for seed in range(3):
+        x = np.random.default_rng(seed).standard_normal(1024).astype(np.float32)
+        logits = orc.matvec(qtype, q.scales, q.packed, x)
+        idx, score = ctx.matvec_argmax(w, x)
+        top2 = np.sort(logits)[-2:]
+        if top2[1] - top2[0] > 1e-4 * abs(top2[1]):
+            assert idx == int(np.argmax(logits))
+        assert abs(score - logits[idx]) <= 1e-5 * max(1, abs(score))
+
+
+def test_argmax_ties_pick_lowest_index(ctx):
+    # identical rows give bit-identical scores: ties → lowest index
+    w = np.zeros((64, 32), np.float32)
+    w[:, 0] = -1
+    w[[9, 17, 40], 0] = 1
+    x = np.ones(32, np.float32)
+    for qtype in (Q8, Q4, Q6):
+        idx, _ = ctx.matvec_argmax(ctx.upload(lib.QMatrix.quantize(w, qtype)), x)
+        assert idx == 9
+
+
+@pytest.mark.parametrize("qtype", [Q8, Q4, Q6], ids=["q8", "q4", "q6"])
+def test_fused_qkv_and_mrope(ctx, orc, rng, qtype):
+    a, b, c = (_qmat(rng, r, 1024, qtype) for r in (2048, 256, 256))
+    x = rng.standard_normal(1024).astype(np.float32)
+    wa, wb, wc = (ctx.upload(m) for m in (a, b, c))
+    oa, ob, oc = ctx.fused_matvec3(wa, wb, wc, x)
+    ra = orc.matvec(qtype, a.scales, a.packed, x)
+    rb = orc.matvec(qtype, b.scales, b.packed, x)
+    rc = orc.matvec(qtype, c.scales, c.packed, x)
+    _close(oa, ra), _close(ob, rb), _close(oc, rc)
+    freq, axis = orc.rope_init(500000.0, 128)
+    cos_t, sin_t = orc.rope_table(freq, axis, 9, 4, 13)
+    ma, mb, mc = ctx.fused_matvec3_mrope(wa, wb, wc, x, cos_t, sin_t, 16, 2, 128)
+    _close(ma, orc.apply_rope(ra, cos_t, sin_t, 16, 128))
+    _close(mb, orc.apply_rope(rb, cos_t, sin_t, 2, 128))
+    _close(mc, rc)
+
+
+@pytest.mark.parametrize("qtype", [Q8, Q4, Q6], ids=["q8", "q4", "q6"])
+def test_swiglu_gate_up(ctx, orc, rng, qtype):
+    g, u = _qmat(rng, 3072, 1024, qtype), _qmat(rng, 3072, 1024, qtype)
+    x = rng.standard_normal(1024).astype(np.float32)
+    got = ctx.swiglu_gate_up(ctx.upload(g), ctx.upload(u), x)
+    gg = orc.matvec(qtype, g.scales, g.packed, x)
+    uu = orc.matvec(qtype, u.scales, u.packed, x)
+    want = np.array([orc.silu(float(a)) for a in gg], np.float32) * uu
+    _close(got, want)
+
+
+@pytest.mark.parametrize("qtype", [Q8, Q4, Q6], ids=["q8", "q4", "q6"])
+@pytest.mark.parametrize("in_place", [True, False])
+def test_matvec_add_rmsnorm(ctx, orc, rng, qtype, in_place):
+    q = _qmat(rng, 1024, 3072, qtype)
+    x = rng.standard_normal(3072).astype(np.float32)
+    res = rng.standard_normal(1024).astype(np.float32)
+    nw = (1 + 0.02 * rng.standard_normal(1024)).astype(np.float32)
+    out, res_after = ctx.matvec_add_rmsnorm(ctx.upload(q), x, res, nw, 1e-5, in_place)
+    mv = orc.matvec(qtype, q.scales, q.packed, x)
+    want_out, want_res = orc.add_rmsnorm(res, mv, nw, 1e-5)
+    _close(out, want_out)
+    _close(res_after, want_res if in_place else res)
+
+
+def test_rmsnorm_and_rope_known_answers(ctx, orc):
+    x = np.array([1, -2, 3, -4, 5, -6, 7, -8, 9], np.float32)
+    w = np.array([1, 0.5, 1.5, 2, 0.25, 1.25, 0.75, 1, 1.1], np.float32)
+    assert np.max(np.abs(ctx.rmsnorm(x, w, 1e-6) - orc.rmsnorm(x, w, 1e-6))) < 1e-6
+    q, k = ctx.mrope_pair(np.array([1, 2, 3, 4], np.float32), np.array([1, 2, 3, 4], np.float32),
+                          [0, 0.5], [1, 0.5], 1, 1, 4)
+    assert list(k) == [-3, -1, 1, 3] and list(q) == [-3, -1, 1, 3]
+
+
+@pytest.mark.parametrize("L", [1, 2, 6, 7, 33, 300, 1024, 4096])
+def test_text_attention_head128(ctx, orc, rng, L):
+    q = rng.standard_normal(16 * 128).astype(np.float32)
+    kc = rng.standard_normal(L * 256).astype(np.float32)
+    vc = rng.standard_normal(L * 256).astype(np.float32)
+    got = ctx.text_attention(q, kc, vc, L, 16, 2, 128)
+    want = orc.cache_attention(q, kc, vc, L, 16, 2, 128)
+    assert np.max(np.abs(got - want)) < 2e-5
+    if L == 1:
+        assert np.array_equal(got.reshape(16, 128), vc.reshape(2, 128)[np.arange(16) // 8])
+
+
+def test_text_attention_small_head_known_answer(ctx):
+    # scratch_test.go:236-248 weighted value sum through softmax weights .25/.75
+    k = np.zeros((2, 8), np.float32)
+    k[1, 4] = 2 * math.log(3)
+    v = np.array([[1, 2, 3, 4, 10, 20, 30, 40], [5, 6, 7, 8, 50, 60, 70, 80]], np.float32)
+    q = np.zeros(8, np.float32)
+    q[4] = 1
+    out = ctx.text_attention(q, k, v, 2, 2, 2, 4)
+    assert np.max(np.abs(out[4:] - np.array([40, 50, 60, 70]))) < 2e-5
