@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -54,7 +55,12 @@ struct DevBuf {
     template <class T> T *as() const { return reinterpret_cast<T *>(p); }
 };
 
+// Lifetimes: every object holds a reference on its parent (weight→ctx,
+// model→ctx and its weights, seq→model), and the public destroy/free calls
+// drop the caller's reference.  Native memory is released child-before-parent
+// whatever order a caller (or a garbage collector) destroys handles in.
 struct pocr_ctx {
+    std::atomic<int> refs{1};
     int device = 0;
     hipStream_t stream = nullptr;
     std::mutex mu;
@@ -63,6 +69,7 @@ struct pocr_ctx {
 };
 
 struct pocr_weight {
+    std::atomic<int> refs{1};
     pocr_ctx *ctx = nullptr;
     int qtype = 0, rows = 0, cols = 0;
     size_t row_bytes = 0;
@@ -77,6 +84,7 @@ struct LayerW {
 };
 
 struct pocr_model {
+    std::atomic<int> refs{1};
     pocr_ctx *ctx = nullptr;
     pocr_config cfg{};
     std::vector<LayerW> layers;
@@ -122,6 +130,10 @@ struct pocr_seq {
 };
 
 namespace pocr {
+void ctx_release(pocr_ctx *c);
+void weight_retain(const pocr_weight *w);
+void weight_release(const pocr_weight *w);
+void model_release(pocr_model *m);
 DevMat dev_mat(const pocr_weight *w);
 int gemv_launch(hipStream_t s, GemvParams p, int nmat, int pro, int epi, int max_grid);
 GemvParams gemv_params_1(const pocr_weight *w);

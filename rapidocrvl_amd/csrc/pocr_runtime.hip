@@ -100,8 +100,8 @@ extern "C" int pocr_ctx_create(int device, pocr_ctx **out) {
     return POCR_OK;
 }
 
-extern "C" void pocr_ctx_destroy(pocr_ctx *ctx) {
-    if (!ctx) return;
+void pocr::ctx_release(pocr_ctx *ctx) {
+    if (!ctx || ctx->refs.fetch_sub(1) != 1) return;
     (void)hipSetDevice(ctx->device);
     if (ctx->stream) {
         (void)hipStreamSynchronize(ctx->stream);
@@ -109,6 +109,8 @@ extern "C" void pocr_ctx_destroy(pocr_ctx *ctx) {
     }
     delete ctx;
 }
+
+extern "C" void pocr_ctx_destroy(pocr_ctx *ctx) { ctx_release(ctx); }
 
 // ---------------------------------------------------------------------------
 // weights
@@ -137,6 +139,7 @@ extern "C" int pocr_weight_upload(pocr_ctx *ctx, int qtype, int rows, int cols, 
         return fail(POCR_ERR_DEVICE, "weight upload copy: %s", hipGetErrorString(e));
     }
     pocr_weight *w = new pocr_weight();
+    ctx->refs.fetch_add(1);
     w->ctx = ctx;
     w->qtype = qtype;
     w->rows = rows;
@@ -149,12 +152,25 @@ extern "C" int pocr_weight_upload(pocr_ctx *ctx, int qtype, int rows, int cols, 
     return POCR_OK;
 }
 
-extern "C" void pocr_weight_free(pocr_weight *w) {
-    if (!w) return;
-    (void)hipSetDevice(w->ctx->device);
-    free_dev(w->base);
-    delete w;
+void pocr::weight_retain(const pocr_weight *w) {
+    if (w) const_cast<pocr_weight *>(w)->refs.fetch_add(1);
 }
+
+void pocr::weight_release(const pocr_weight *cw) {
+    pocr_weight *w = const_cast<pocr_weight *>(cw);
+    if (!w || w->refs.fetch_sub(1) != 1) return;
+    pocr_ctx *ctx = w->ctx;
+    {
+        std::lock_guard<std::mutex> lk(ctx->mu);
+        (void)hipSetDevice(ctx->device);
+        (void)hipStreamSynchronize(ctx->stream);
+        free_dev(w->base);
+    }
+    delete w;
+    ctx_release(ctx);
+}
+
+extern "C" void pocr_weight_free(pocr_weight *w) { weight_release(w); }
 
 DevMat pocr::dev_mat(const pocr_weight *w) {
     DevMat m;
@@ -575,6 +591,7 @@ extern "C" int pocr_model_create(pocr_ctx *ctx, const pocr_config *cfg, pocr_mod
     std::lock_guard<std::mutex> lk(ctx->mu);
     HIP_TRY(hipSetDevice(ctx->device));
     pocr_model *m = new pocr_model();
+    ctx->refs.fetch_add(1);
     m->ctx = ctx;
     m->cfg = c;
     m->layers.resize(c.layers);
@@ -606,25 +623,37 @@ extern "C" int pocr_model_create(pocr_ctx *ctx, const pocr_config *cfg, pocr_mod
         free_dev(m->freq);
         free_dev(m->axis);
         delete m;
+        ctx->refs.fetch_sub(1);
         return fail(POCR_ERR_DEVICE, "model tables: %s", hipGetErrorString(e));
     }
     *out = m;
     return POCR_OK;
 }
 
-extern "C" void pocr_model_destroy(pocr_model *m) {
-    if (!m) return;
-    (void)hipSetDevice(m->ctx->device);
-    for (auto &l : m->layers) {
-        free_dev(l.ln1);
-        free_dev(l.ln2);
+void pocr::model_release(pocr_model *m) {
+    if (!m || m->refs.fetch_sub(1) != 1) return;
+    pocr_ctx *ctx = m->ctx;
+    {
+        std::lock_guard<std::mutex> lk(ctx->mu);
+        (void)hipSetDevice(ctx->device);
+        (void)hipStreamSynchronize(ctx->stream);
+        for (auto &l : m->layers) {
+            free_dev(l.ln1);
+            free_dev(l.ln2);
+        }
+        free_dev(m->final_norm);
+        free_dev(m->embed);
+        free_dev(m->freq);
+        free_dev(m->axis);
     }
-    free_dev(m->final_norm);
-    free_dev(m->embed);
-    free_dev(m->freq);
-    free_dev(m->axis);
+    for (auto &l : m->layers)
+        for (const pocr_weight *w : l.w) weight_release(w);
+    weight_release(m->lm);
     delete m;
+    ctx_release(ctx);
 }
+
+extern "C" void pocr_model_destroy(pocr_model *m) { model_release(m); }
 
 extern "C" int pocr_model_set_weight(pocr_model *m, int layer, int role, const pocr_weight *w) {
     if (!m || !w) return fail(POCR_ERR_ARG, "pocr_model_set_weight: null argument");
@@ -633,6 +662,8 @@ extern "C" int pocr_model_set_weight(pocr_model *m, int layer, int role, const p
     const int q_rows = c.heads * c.head_dim, kv_rows = c.kv_heads * c.head_dim;
     if (layer == -1 && role == POCR_W_LM_HEAD) {
         if (w->rows != c.vocab || w->cols != c.hidden) return fail(POCR_ERR_ARG, "lm_head shape mismatch");
+        weight_retain(w);
+        weight_release(m->lm);
         m->lm = w;
         return POCR_OK;
     }
@@ -644,6 +675,8 @@ extern "C" int pocr_model_set_weight(pocr_model *m, int layer, int role, const p
     if (w->rows != want_rows[role] || w->cols != want_cols[role])
         return fail(POCR_ERR_ARG, "layer %d %s: shape %dx%d, want %dx%d", layer, names[role], w->rows, w->cols,
                     want_rows[role], want_cols[role]);
+    weight_retain(w);
+    weight_release(m->layers[layer].w[role]);
     m->layers[layer].w[role] = w;
     return POCR_OK;
 }
@@ -705,6 +738,7 @@ extern "C" int pocr_seq_create(pocr_model *m, int capacity, pocr_seq **out) {
     HIP_TRY(hipSetDevice(m->ctx->device));
     const pocr_config &c = m->cfg;
     pocr_seq *s = new pocr_seq();
+    m->refs.fetch_add(1);
     s->m = m;
     s->cap = capacity;
     s->nsplit = attn_nsplit(capacity);
@@ -727,6 +761,7 @@ extern "C" int pocr_seq_create(pocr_model *m, int capacity, pocr_seq **out) {
     if (e == hipSuccess) e = hipMemset(s->kv, 0, (size_t)c.layers * 2 * capacity * kvd * 4);
     if (e != hipSuccess) {
         delete s;
+        m->refs.fetch_sub(1);
         return fail(POCR_ERR_NOMEM, "pocr_seq_create(%d): %s", capacity, hipGetErrorString(e));
     }
     StepState st{};
@@ -735,6 +770,7 @@ extern "C" int pocr_seq_create(pocr_model *m, int capacity, pocr_seq **out) {
     e = hipMemcpy(s->st, &st, sizeof(st), hipMemcpyHostToDevice);
     if (e != hipSuccess) {
         delete s;
+        m->refs.fetch_sub(1);
         return fail(POCR_ERR_DEVICE, "pocr_seq_create: %s", hipGetErrorString(e));
     }
     *out = s;
@@ -743,10 +779,14 @@ extern "C" int pocr_seq_create(pocr_model *m, int capacity, pocr_seq **out) {
 
 extern "C" void pocr_seq_destroy(pocr_seq *s) {
     if (!s) return;
-    std::lock_guard<std::mutex> lk(s->m->ctx->mu);
-    (void)hipSetDevice(s->m->ctx->device);
-    (void)hipStreamSynchronize(s->m->ctx->stream);
-    delete s;
+    pocr_model *m = s->m;
+    {
+        std::lock_guard<std::mutex> lk(m->ctx->mu);
+        (void)hipSetDevice(m->ctx->device);
+        (void)hipStreamSynchronize(m->ctx->stream);
+        delete s;
+    }
+    model_release(m);
 }
 
 float *pocr::layer_k(const pocr_seq *s, int layer) {

@@ -10,6 +10,7 @@ from __future__ import annotations
 import ctypes as C
 import os
 import re
+import weakref
 
 import numpy as np
 
@@ -182,6 +183,7 @@ class Weight:
         h = _vp()
         check(load().pocr_weight_upload(ctx.h, q.qtype, q.rows, q.cols, _ptr(q.scales), _ptr(q.packed), C.byref(h)))
         self.h = h
+        ctx._children.add(self)
 
     def close(self):
         if getattr(self, "h", None):
@@ -193,15 +195,24 @@ class Weight:
 
 
 class Context:
-    """One device context: the op-level mirror of backend.Vulkan* calls."""
+    """One device context: the op-level mirror of backend.Vulkan* calls.
+
+    Closing releases dependents first (sequences, models, weights), so the
+    native objects are freed child-before-parent whatever order Python's
+    garbage collector finalises them in."""
 
     def __init__(self, device: int = 0):
+        self._children = weakref.WeakSet()
         h = _vp()
         check(load().pocr_ctx_create(device, C.byref(h)))
         self.h = h
 
     def close(self):
         if getattr(self, "h", None):
+            for obj in [o for o in self._children if isinstance(o, Model)]:
+                obj.close()
+            for obj in list(self._children):
+                obj.close()
             load().pocr_ctx_destroy(self.h)
             self.h = None
 
@@ -262,8 +273,8 @@ class Context:
 
     def mrope_pair(self, q, k, cos_t, sin_t, q_heads, kv_heads, head_dim):
         q, k = _f32(q).copy(), _f32(k).copy()
-        check(load().pocr_mrope_pair(self.h, _ptr(q), _ptr(k), _ptr(_f32(cos_t)), _ptr(_f32(sin_t)), q_heads,
-                                     kv_heads, head_dim))
+        cos_t, sin_t = _f32(cos_t), _f32(sin_t)  # keep the arrays alive across the call
+        check(load().pocr_mrope_pair(self.h, _ptr(q), _ptr(k), _ptr(cos_t), _ptr(sin_t), q_heads, kv_heads, head_dim))
         return q, k
 
     def time_matvec(self, weights, x, iters):
@@ -289,16 +300,20 @@ class Model:
         self.ctx, self.cfg = ctx, cfg
         c = PocrConfig(cfg.hidden, cfg.inter, cfg.layers, cfg.heads, cfg.kv_heads, cfg.head_dim, cfg.vocab,
                        cfg.eps, cfg.rope_theta, (C.c_int32 * 3)(*cfg.mrope_section))
+        self._seqs = weakref.WeakSet()
         h = _vp()
         check(load().pocr_model_create(ctx.h, C.byref(c), C.byref(h)))
         self.h = h
         self._weights = []
+        ctx._children.add(self)
 
     def close(self):
+        for s in list(getattr(self, "_seqs", ())):
+            s.close()
         if getattr(self, "h", None):
             load().pocr_model_destroy(self.h)
             self.h = None
-        for w in self._weights:
+        for w in getattr(self, "_weights", []):
             w.close()
         self._weights = []
 
@@ -346,6 +361,7 @@ class Sequence:
         check(load().pocr_seq_create(model.h, capacity, C.byref(h)))
         self.h = h
         self.capacity = capacity
+        model._seqs.add(self)
 
     def close(self):
         if getattr(self, "h", None):
@@ -373,7 +389,8 @@ class Sequence:
         check(load().pocr_seq_truncate(self.h, length))
 
     def write_kv(self, layer: int, k, v, length: int):
-        check(load().pocr_seq_write_kv(self.h, layer, _ptr(_f32(k)), _ptr(_f32(v)), length))
+        k, v = _f32(k), _f32(v)
+        check(load().pocr_seq_write_kv(self.h, layer, _ptr(k), _ptr(v), length))
 
     def step(self, emb, pos3, need_logits=True, want_logits=True):
         cfg = self.model.cfg

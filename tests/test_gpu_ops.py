@@ -140,7 +140,8 @@ def test_matvec_add_rmsnorm(ctx, orc, rng, qtype, in_place):
 def test_rmsnorm_and_rope_known_answers(ctx, orc):
     x = np.array([1, -2, 3, -4, 5, -6, 7, -8, 9], np.float32)
     w = np.array([1, 0.5, 1.5, 2, 0.25, 1.25, 0.75, 1, 1.1], np.float32)
-    assert np.max(np.abs(ctx.rmsnorm(x, w, 1e-6) - orc.rmsnorm(x, w, 1e-6))) < 1e-6
+    want = orc.rmsnorm(x, w, 1e-6)
+    assert np.max(np.abs(ctx.rmsnorm(x, w, 1e-6) - want)) <= 2e-6 * np.max(np.abs(want))
     q, k = ctx.mrope_pair(np.array([1, 2, 3, 4], np.float32), np.array([1, 2, 3, 4], np.float32),
                           [0, 0.5], [1, 0.5], 1, 1, 4)
     assert list(k) == [-3, -1, 1, 3] and list(q) == [-3, -1, 1, 3]
