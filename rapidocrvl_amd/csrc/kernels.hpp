@@ -128,7 +128,18 @@ __device__ __forceinline__ Chunk load_chunk(const uint8_t *p) {
     return c;
 }
 
-__device__ __forceinline__ float ubyte(uint32_t v, int i) { return (float)((v >> (8 * i)) & 0xFFu); }
+// v_cvt_f32_ubyte{0..3}: one VALU op per code (the compiler otherwise emits a
+// bit-field extract before each convert once it knows the bytes are nibbles)
+__device__ __forceinline__ float ubyte(uint32_t v, int i) {
+    float r;
+    switch (i) {
+    case 0: asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(r) : "v"(v)); break;
+    case 1: asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(r) : "v"(v)); break;
+    case 2: asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(r) : "v"(v)); break;
+    default: asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(r) : "v"(v)); break;
+    }
+    return r;
+}
 
 template <int QT>
 __device__ __forceinline__ float chunk_dot(const Chunk &c, const float *x) {
@@ -180,6 +191,67 @@ __device__ __forceinline__ float lane_group_sum(float v) {
 #pragma unroll
     for (int off = LPR / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
     return v;
+}
+
+// Cross-lane exchanges used by the reduce-scatter.  Each pairs every lane with
+// a partner that differs in one chosen lane bit (and agrees on all higher
+// ones): xor 32, xor 16 (ds_swizzle), mirror within 16 (DPP row_mirror,
+// bit 3), mirror within 8 (DPP row_half_mirror, bit 2), xor 2 and xor 1 (DPP
+// quad_perm).
+enum : int { XS32 = 0, XS16 = 1, XM16 = 2, XM8 = 3, XQ2 = 4, XQ1 = 5 };
+template <int S>
+__device__ __forceinline__ float xchg(float v) {
+    const int i = __float_as_int(v);
+    if constexpr (S == XS32) return __shfl_xor(v, 32, 64);
+    else if constexpr (S == XS16) return __int_as_float(__builtin_amdgcn_ds_swizzle(i, 0x401F));
+    else if constexpr (S == XM16) return __int_as_float(__builtin_amdgcn_update_dpp(0, i, 0x140, 0xF, 0xF, false));
+    else if constexpr (S == XM8) return __int_as_float(__builtin_amdgcn_update_dpp(0, i, 0x141, 0xF, 0xF, false));
+    else if constexpr (S == XQ2) return __int_as_float(__builtin_amdgcn_update_dpp(0, i, 0x4E, 0xF, 0xF, false));
+    else return __int_as_float(__builtin_amdgcn_update_dpp(0, i, 0xB1, 0xF, 0xF, false));
+}
+
+// One reduce-scatter step over N entries of NM floats: lanes whose step bit
+// is set keep the upper half (and receive it from the partner); with one
+// entry left the step is a butterfly add.
+template <int N, int NM, int S, int BIT>
+__device__ __forceinline__ void rs_step(float (&v)[8][NM], int lane) {
+    if constexpr (N > 1) {
+        const bool hi = (lane & BIT) != 0;
+#pragma unroll
+        for (int i = 0; i < N / 2; ++i)
+#pragma unroll
+            for (int k = 0; k < NM; ++k) {
+                const float keep = hi ? v[N / 2 + i][k] : v[i][k];
+                const float send = hi ? v[i][k] : v[N / 2 + i][k];
+                v[i][k] = keep + xchg<S>(send);
+            }
+    } else {
+#pragma unroll
+        for (int k = 0; k < NM; ++k) v[0][k] += xchg<S>(v[0][k]);
+    }
+}
+
+// Sums U entries (of NM floats) over the LPR lanes of a row group.  Lane
+// u·(LPR/U) ends up with the full sum of entry u in v[0].
+template <int LPR, int U, int NM>
+__device__ __forceinline__ void reduce_scatter(float (&v)[8][NM], int lane) {
+    constexpr int N1 = U, N2 = N1 > 1 ? N1 / 2 : 1, N3 = N2 > 1 ? N2 / 2 : 1, N4 = N3 > 1 ? N3 / 2 : 1;
+    if constexpr (LPR == 64) {
+        constexpr int N5 = N4 > 1 ? N4 / 2 : 1, N6 = N5 > 1 ? N5 / 2 : 1;
+        rs_step<N1, NM, XS32, 32>(v, lane);
+        rs_step<N2, NM, XS16, 16>(v, lane);
+        rs_step<N3, NM, XM16, 8>(v, lane);
+        rs_step<N4, NM, XM8, 4>(v, lane);
+        rs_step<N5, NM, XQ2, 2>(v, lane);
+        rs_step<N6, NM, XQ1, 1>(v, lane);
+    } else {
+        constexpr int N5 = N4 > 1 ? N4 / 2 : 1;
+        rs_step<N1, NM, XS16, 16>(v, lane);
+        rs_step<N2, NM, XM16, 8>(v, lane);
+        rs_step<N3, NM, XM8, 4>(v, lane);
+        rs_step<N4, NM, XQ2, 2>(v, lane);
+        rs_step<N5, NM, XQ1, 1>(v, lane);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -255,25 +327,26 @@ __device__ __forceinline__ void stage_x(float *xs, const float *x, const float *
     }
 }
 
-__device__ __forceinline__ void gemv_epilogue(const GemvParams &p, int epi, int r, const float *s, bool in_place,
-                                              float &best_v, int &best_r) {
+// resid = residual[r], read by the caller ahead of time (EPI_OPROJ/DOWN/ADDV)
+__device__ __forceinline__ void gemv_epilogue(const GemvParams &p, int epi, int r, const float *s, float resid,
+                                              bool in_place, float &best_v, int &best_r) {
 #pragma clang fp contract(off)
     switch (epi) {
     case EPI_PLAIN: p.out[r] = s[0]; break;
     case EPI_SWIGLU: p.out[r] = silu_ref(s[0]) * s[1]; break;
     case EPI_OPROJ: {
-        const float v = p.residual[r] + s[0];
+        const float v = resid + s[0];
         p.vbuf[r] = v;
         if (in_place) p.residual[r] = v;
         break;
     }
     case EPI_DOWN: {
-        const float v = p.residual[r] + s[0];
+        const float v = resid + s[0];
         if (p.flag) p.vbuf[r] = v;
         else p.residual[r] = v;
         break;
     }
-    case EPI_ADDV: p.vbuf[r] = p.residual[r] + s[0]; break;
+    case EPI_ADDV: p.vbuf[r] = resid + s[0]; break;
     default:  // EPI_ARGMAX
         if (p.out) p.out[r] = s[0];
         if (s[0] > best_v || (s[0] == best_v && r < best_r)) {
@@ -281,6 +354,10 @@ __device__ __forceinline__ void gemv_epilogue(const GemvParams &p, int epi, int 
             best_r = r;
         }
     }
+}
+
+__device__ __forceinline__ bool epi_reads_residual(int epi) {
+    return epi == EPI_OPROJ || epi == EPI_DOWN || epi == EPI_ADDV;
 }
 
 __device__ __forceinline__ bool oproj_in_place(const GemvParams &p) {
@@ -316,10 +393,68 @@ __device__ __forceinline__ DevMat seg_mat(const GemvParams &p, int sg) {
     return sg == 0 ? p.m[0] : (sg == 1 ? p.m[1] : p.m[2]);
 }
 
+// A wave's row group never straddles a segment boundary (the host checks
+// that segment sizes are multiples of the group size), so the segment is
+// chosen once per group from wave-uniform values: scalar branches over the
+// kernel-argument pointers.
+struct SegSel {
+    const uint8_t *data0, *data1;  // matrix (NMAT==1) or gate/up (NMAT==2)
+    const float *scale0, *scale1;
+    int start;  // first global row of the segment
+};
+
+template <int NMAT>
+__device__ __forceinline__ SegSel seg_select(const GemvParams &p, int r0) {
+    SegSel s;
+    if (NMAT == 2) {
+        s.data0 = p.m[0].data;
+        s.data1 = p.m[1].data;
+        s.scale0 = p.m[0].scale;
+        s.scale1 = p.m[1].scale;
+        s.start = 0;
+    } else if (r0 >= p.seg_end[1]) {
+        s.data0 = s.data1 = p.m[2].data;
+        s.scale0 = s.scale1 = p.m[2].scale;
+        s.start = p.seg_end[1];
+    } else if (r0 >= p.seg_end[0]) {
+        s.data0 = s.data1 = p.m[1].data;
+        s.scale0 = s.scale1 = p.m[1].scale;
+        s.start = p.seg_end[0];
+    } else {
+        s.data0 = s.data1 = p.m[0].data;
+        s.scale0 = s.scale1 = p.m[0].scale;
+        s.start = 0;
+    }
+    return s;
+}
+
+// Requests one group's chunks.  Rows past the end are clamped to the last
+// row (loaded, never written back), so every lane issues the same number of
+// loads and the wait counts stay static.
+template <int QT, int LPR, int CPL, int U, int NMAT>
+__device__ __forceinline__ void load_group(const SegSel &sel, int row_bytes, int rows, int g, int sub, int l,
+                                           Chunk (&w)[U][NMAT][CPL]) {
+    using T = QTraits<QT>;
+    constexpr int RPW = 64 / LPR;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int lr = min((g * U + u) * RPW + sub, rows - 1) - sel.start;
+#pragma unroll
+        for (int mi = 0; mi < NMAT; ++mi) {
+            const uint8_t *row = (mi == 0 ? sel.data0 : sel.data1) + (size_t)lr * row_bytes;
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) w[u][mi][j] = load_chunk<QT>(row + (l + j * LPR) * T::CB);
+        }
+    }
+}
+
 // LPR lanes share one row; each lane owns CPL chunks (lane + j·LPR) of every
 // row, so its x slice (CPL·W floats) stays in VGPRs across rows.  A wave
-// handles RPW = 64/LPR rows per step and U steps per iteration (U·RPW rows,
-// U·CPL·NMAT loads in flight per lane).
+// handles groups of U·RPW rows (RPW = 64/LPR side by side): the first group's
+// weights are requested before the activation prologue, and each group's
+// successor is requested before the group is computed, so a wave always has
+// U·CPL·NMAT 16-byte loads in flight.  The U row sums are reduced together
+// with one reduce-scatter, leaving row u's sum in lane u·(LPR/U).
 // TAG only separates instances for profiling (TAG=1: the timing entry point).
 template <int QT, int LPR, int CPL, int U, int NMAT, int TAG = 0>
 __global__ void __launch_bounds__(kThreads) k_gemv(GemvParams p, int pro, int epi) {
@@ -328,13 +463,26 @@ __global__ void __launch_bounds__(kThreads) k_gemv(GemvParams p, int pro, int ep
     __shared__ float red[2 * kWaves];
     using T = QTraits<QT>;
     constexpr int RPW = 64 / LPR;
-    if (pro == PRO_RMSNORM) stage_x<PRO_RMSNORM>(xs, p.x, p.norm_w, p.cols, p.eps, red);
-    else stage_x<PRO_COPY>(xs, p.x, p.norm_w, p.cols, p.eps, red);
+    constexpr int RG = RPW * U;
 
+    const int rows = p.rows;
+    const int row_bytes = p.m[0].row_bytes;
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int sub = lane / LPR;
     const int l = lane % LPR;
+    const int ngroups = (rows + RG - 1) / RG;
+    const int gstride = gridDim.x * kWaves;
+    int g = blockIdx.x * kWaves + wave;
+
+    Chunk w[U][NMAT][CPL];
+    {
+        const int gc = min(g, ngroups - 1);
+        load_group<QT, LPR, CPL, U, NMAT>(seg_select<NMAT>(p, gc * RG), row_bytes, rows, gc, sub, l, w);
+    }
+
+    if (pro == PRO_RMSNORM) stage_x<PRO_RMSNORM>(xs, p.x, p.norm_w, p.cols, p.eps, red);
+    else stage_x<PRO_COPY>(xs, p.x, p.norm_w, p.cols, p.eps, red);
 
     float xr[CPL][T::W];
     float sx = 0.0f;
@@ -351,57 +499,49 @@ __global__ void __launch_bounds__(kThreads) k_gemv(GemvParams p, int pro, int ep
     const bool in_place = epi == EPI_OPROJ ? oproj_in_place(p) : false;
     float best_v = -INFINITY;
     int best_r = 0x7FFFFFFF;
+    constexpr int SPAN = LPR / U;  // lanes per entry after the reduce-scatter
+    const int my_u = l / SPAN;
+    const bool writer = (l % SPAN) == 0;
 
-    constexpr int RG = RPW * U;
-    const int ngroups = (p.rows + RG - 1) / RG;
-    for (int g = blockIdx.x * kWaves + wave; g < ngroups; g += gridDim.x * kWaves) {
-        const int r0 = g * RG;
-        Chunk w[U][NMAT][CPL];
-        int lrow[U];
-        int seg[U];
+    const bool need_resid = epi_reads_residual(epi);
+    for (; g < ngroups; g += gstride) {
+        const SegSel sel = seg_select<NMAT>(p, g * RG);
+        // the writer lane's epilogue operands are read before the prefetch so
+        // that waiting for them does not wait for the prefetch too
+        const int r = (g * U + my_u) * RPW + sub;
+        const int rc = min(r, rows - 1);
+        float scl[NMAT];
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int r = r0 + u * RPW + sub;
-            int sg = 0, lr = r;
-            if (NMAT == 1) {
-                sg = (r >= p.seg_end[0]) + (r >= p.seg_end[1]);
-                lr = r - (sg == 0 ? 0 : (sg == 1 ? p.seg_end[0] : p.seg_end[1]));
-            }
-            seg[u] = sg;
-            lrow[u] = lr;
+        for (int mi = 0; mi < NMAT; ++mi) scl[mi] = (mi == 0 ? sel.scale0 : sel.scale1)[rc - sel.start];
+        const float resid = need_resid ? p.residual[rc] : 0.0f;
+        Chunk wn[U][NMAT][CPL];
+        {
+            const int gn = min(g + gstride, ngroups - 1);
+            load_group<QT, LPR, CPL, U, NMAT>(seg_select<NMAT>(p, gn * RG), row_bytes, rows, gn, sub, l, wn);
+        }
+        float acc[8][NMAT];
+#pragma unroll
+        for (int u = 0; u < U; ++u)
 #pragma unroll
             for (int mi = 0; mi < NMAT; ++mi) {
-                const DevMat M = seg_mat(p, NMAT == 1 ? sg : mi);
+                float a = 0.0f;
 #pragma unroll
-                for (int j = 0; j < CPL; ++j) {
-                    if (r < p.rows) {
-                        w[u][mi][j] = load_chunk<QT>(M.data + (size_t)lr * M.row_bytes + (l + j * LPR) * T::CB);
-                    } else {
-                        w[u][mi][j] = Chunk{{0u, 0u, 0u, 0u}};
-                    }
-                }
+                for (int j = 0; j < CPL; ++j) a += chunk_dot<QT>(w[u][mi][j], xr[j]);
+                acc[u][mi] = a - bias;
             }
-        }
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
+        reduce_scatter<LPR, U, NMAT>(acc, lane);
+        if (writer && r < rows) {
             float s[NMAT];
 #pragma unroll
-            for (int mi = 0; mi < NMAT; ++mi) {
-                float acc = 0.0f;
-#pragma unroll
-                for (int j = 0; j < CPL; ++j) acc += chunk_dot<QT>(w[u][mi][j], xr[j]);
-                s[mi] = lane_group_sum<LPR>(acc - bias);
-            }
-            const int r = r0 + u * RPW + sub;
-            if (l == 0 && r < p.rows) {
-#pragma unroll
-                for (int mi = 0; mi < NMAT; ++mi) {
-                    const DevMat M = seg_mat(p, NMAT == 1 ? seg[u] : mi);
-                    s[mi] = s[mi] * M.scale[lrow[u]];
-                }
-                gemv_epilogue(p, epi, r, s, in_place, best_v, best_r);
-            }
+            for (int mi = 0; mi < NMAT; ++mi) s[mi] = acc[0][mi] * scl[mi];
+            gemv_epilogue(p, epi, r, s, resid, in_place, best_v, best_r);
         }
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int mi = 0; mi < NMAT; ++mi)
+#pragma unroll
+                for (int j = 0; j < CPL; ++j) w[u][mi][j] = wn[u][mi][j];
     }
     if (epi == EPI_ARGMAX) argmax_finish(p, best_v, best_r, red);
 }
@@ -457,7 +597,8 @@ __global__ void __launch_bounds__(kThreads) k_gemv_any(GemvParams p, int pro, in
                 s[mi] = s[mi] * M.scale[lr];
             }
         }
-        if (lane == 0 && valid) gemv_epilogue(p, epi, r, s, in_place, best_v, best_r);
+        if (lane == 0 && valid)
+            gemv_epilogue(p, epi, r, s, epi_reads_residual(epi) ? p.residual[r] : 0.0f, in_place, best_v, best_r);
     }
     if (epi == EPI_ARGMAX) argmax_finish(p, best_v, best_r, red);
 }
@@ -559,19 +700,22 @@ static __global__ void __launch_bounds__(kThreads) k_step_begin(StepState *st, c
 // ---------------------------------------------------------------------------
 // GQA decode attention, head_dim 128, split over cache rows.
 //
-// Workgroup (g, s) owns kv head g and cache rows [s·chunk, (s+1)·chunk).  It
-// rotates the q heads of its group (and, for the split holding the newest
-// row, the new k) with the step's RoPE table, appends the new K/V row to the
-// per-layer cache (kvCache.append, model.go:5593-5612: row t at
-// t·kvDim + g·128), scores its rows for all GROUP q heads sharing each K load,
-// and keeps an LDS-resident partial softmax (max, Σexp, Σexp·V).  The last
-// workgroup of a kv head to finish merges the partials (online softmax) into
-// head_out.  Scores: dot(q,k)·f32(1/√128) (model.go:4623-4795, 7391);
-// softmax with FastExp (ops.go:1199-1363); out = Σ p·V (model.go:5201-5590).
+// Workgroup (g, s) owns kv head g and cache rows [s·chunk, (s+1)·chunk),
+// chunk ≤ 64.  It requests every K and V row of its chunk up front (one
+// memory round trip: 2 + 8 16-byte loads per lane), rotates the q heads of its
+// group (and, in the split holding the newest row, the new k) with the step's
+// RoPE table and appends the new K/V row to the per-layer cache
+// (kvCache.append, model.go:5593-5612: row t at t·kvDim + g·128).  Scores for
+// all GROUP q heads share each K row (16 lanes × 8 dims per row, reduced by a
+// DPP reduce-scatter); the partial softmax (max, Σexp, Σexp·V) is written per
+// split and the last workgroup of a kv head merges the splits.  Scores:
+// dot(q,k)·f32(1/√128) (model.go:4623-4795, 7391); softmax with FastExp
+// (ops.go:1199-1363); out = Σ p·V (model.go:5201-5590).
 // ---------------------------------------------------------------------------
 constexpr int kHD = 128;
 constexpr int kMaxGroup = 8;
-constexpr int kMaxChunk = 256;  // cache rows per workgroup
+constexpr int kMaxChunk = 64;  // cache rows per workgroup
+constexpr int kRec = kHD + 2;  // partial record per head: m, l, acc[128]
 
 struct AttnParams {
     const float *q;        // [heads*128] (unrotated if rope)
@@ -584,12 +728,22 @@ struct AttnParams {
     int has_rope;          // op level
     const float *cos_t;    // op level tables
     const float *sin_t;
-    float *part;           // [kvh][nsplit][GROUP][130]
+    float *part;           // [kvh][nsplit][GROUP][kRec]
     unsigned int *counter; // [kvh]
     float *head_out;       // [heads*128]
     int heads, kvh, nsplit;
     float scale;
 };
+
+// reduce-scatter of 8 per-head partial dots over the 16 lanes of a row:
+// lane l16 with (l16 & 1) == 0 ends with head (l16 >> 1)'s full sum
+__device__ __forceinline__ float rs16_heads(float (&v)[8][1], int lane) {
+    rs_step<8, 1, XM16, 8>(v, lane);
+    rs_step<4, 1, XM8, 4>(v, lane);
+    rs_step<2, 1, XQ2, 2>(v, lane);
+    rs_step<1, 1, XQ1, 1>(v, lane);
+    return v[0][0];
+}
 
 static __global__ void __launch_bounds__(kThreads) k_attn_decode(AttnParams p) {
     StepState *st = p.st;
@@ -598,10 +752,11 @@ static __global__ void __launch_bounds__(kThreads) k_attn_decode(AttnParams p) {
     __shared__ float knew[kHD];
     __shared__ float vnew[kHD];
     __shared__ float sc[kMaxGroup][kMaxChunk];
+    __shared__ float4 pv[8][kMaxGroup][kHD / 4];
     __shared__ float sm[kMaxGroup], sl[kMaxGroup];
     __shared__ int s_last;
 
-    const int g = blockIdx.x;        // kv head
+    const int g = blockIdx.x;  // kv head
     const int split = blockIdx.y;
     const int group = p.heads / p.kvh;
     const int tid = threadIdx.x;
@@ -614,11 +769,36 @@ static __global__ void __launch_bounds__(kThreads) k_attn_decode(AttnParams p) {
     const int kvd = p.kvh * kHD;
 
     int chunk = (L + p.nsplit - 1) / p.nsplit;
-    chunk = (chunk + 15) & ~15;
+    chunk = min((chunk + 15) & ~15, kMaxChunk);
     const int t0 = split * chunk;
     const int t1 = min(L, t0 + chunk);
+    const int n = t1 - t0;  // may be <= 0: empty split
 
-    // q of the group's heads (rotated), 64 pairs per head
+    // ---- 1. request the chunk's K rows (score layout) and V rows (PV layout)
+    const int l16 = lane & 15;
+    const int ts = wave * 4 + (lane >> 4);  // row slot of this 16-lane group
+    // Rows past the chunk are clamped to the last valid row (loaded, never
+    // used); the newest row's slot is refilled from LDS below.  Every lane
+    // issues the same loads, so the wait counts stay static.
+    const int tmax = L - 1;
+    float4 ka[4][2];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int t = min(t0 + ts + 16 * j, tmax);
+        const float4 *src = reinterpret_cast<const float4 *>(p.kc + (size_t)t * kvd + g * kHD + 8 * l16);
+        ka[j][0] = src[0];
+        ka[j][1] = src[1];
+    }
+    const int tg = tid >> 5;          // PV row slot 0..7
+    const int d4 = (tid & 31) * 4;    // PV dims d4..d4+3
+    float4 va[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int t = min(t0 + tg + 8 * j, tmax);
+        va[j] = *reinterpret_cast<const float4 *>(p.vc + (size_t)t * kvd + g * kHD + d4);
+    }
+
+    // ---- 2. rotated q of the group's heads; new K/V row (owner appends it)
     for (int i = tid; i < group * (kHD / 2); i += kThreads) {
         const int h = i / (kHD / 2), j = i % (kHD / 2);
         const float *qh = p.q + (size_t)(g * group + h) * kHD;
@@ -627,7 +807,7 @@ static __global__ void __launch_bounds__(kThreads) k_attn_decode(AttnParams p) {
         qs[h][j] = a;
         qs[h][j + kHD / 2] = b;
     }
-    const bool owns_new = newest >= 0 && newest >= t0 && newest < t1;
+    const bool owns_new = newest >= t0 && newest < t1;
     if (owns_new && tid < kHD / 2) {
         const float *kh = p.k_new + (size_t)g * kHD;
         float a = kh[tid], b = kh[tid + kHD / 2];
@@ -635,133 +815,117 @@ static __global__ void __launch_bounds__(kThreads) k_attn_decode(AttnParams p) {
         knew[tid] = a;
         knew[tid + kHD / 2] = b;
         const float *vh = p.v_new + (size_t)g * kHD;
-        vnew[tid] = vh[tid];
-        vnew[tid + kHD / 2] = vh[tid + kHD / 2];
+        const float va0 = vh[tid], va1 = vh[tid + kHD / 2];
+        vnew[tid] = va0;
+        vnew[tid + kHD / 2] = va1;
         float *kd = p.kc + (size_t)newest * kvd + g * kHD;
         float *vd = p.vc + (size_t)newest * kvd + g * kHD;
         kd[tid] = a;
         kd[tid + kHD / 2] = b;
-        vd[tid] = vh[tid];
-        vd[tid + kHD / 2] = vh[tid + kHD / 2];
+        vd[tid] = va0;
+        vd[tid + kHD / 2] = va1;
     }
     __syncthreads();
-
-    // ---- scores: 16 lanes per row, 8 dims per lane, all group heads ----
-    const int l16 = lane & 15;
-    float qv[kMaxGroup][8];
+    if (owns_new) {
 #pragma unroll
-    for (int h = 0; h < kMaxGroup; ++h)
-#pragma unroll
-        for (int d = 0; d < 8; ++d) qv[h][d] = h < group ? qs[h][8 * l16 + d] : 0.0f;
-
-    for (int tb = t0; tb < t1; tb += 16) {
-        const int t = tb + wave * 4 + (lane >> 4);
-        float kv[8];
-        if (t < t1) {
-            if (t == newest) {
-#pragma unroll
-                for (int d = 0; d < 8; ++d) kv[d] = knew[8 * l16 + d];
-            } else {
-                const float4 *src = reinterpret_cast<const float4 *>(p.kc + (size_t)t * kvd + g * kHD + 8 * l16);
-                float4 a = src[0], b = src[1];
-                kv[0] = a.x; kv[1] = a.y; kv[2] = a.z; kv[3] = a.w;
-                kv[4] = b.x; kv[5] = b.y; kv[6] = b.z; kv[7] = b.w;
+        for (int j = 0; j < 4; ++j)
+            if (t0 + ts + 16 * j == newest) {
+                ka[j][0] = make_float4(knew[8 * l16], knew[8 * l16 + 1], knew[8 * l16 + 2], knew[8 * l16 + 3]);
+                ka[j][1] = make_float4(knew[8 * l16 + 4], knew[8 * l16 + 5], knew[8 * l16 + 6], knew[8 * l16 + 7]);
             }
-        } else {
 #pragma unroll
-            for (int d = 0; d < 8; ++d) kv[d] = 0.0f;
-        }
-        float part[kMaxGroup];
+        for (int j = 0; j < 8; ++j)
+            if (t0 + tg + 8 * j == newest) va[j] = make_float4(vnew[d4], vnew[d4 + 1], vnew[d4 + 2], vnew[d4 + 3]);
+    }
+
+    // ---- 3. scores
+    {
+        float qv[kMaxGroup][8];
 #pragma unroll
-        for (int h = 0; h < kMaxGroup; ++h) {
-            float a = 0.0f;
+        for (int h = 0; h < kMaxGroup; ++h)
 #pragma unroll
-            for (int d = 0; d < 8; ++d) a = fmaf(qv[h][d], kv[d], a);
-            part[h] = a;
-        }
-        // reduce-scatter over the 16 lanes: lane keeps head (b3 b2 b1) of l16
-        const bool b3 = (l16 & 8) != 0, b2 = (l16 & 4) != 0, b1 = (l16 & 2) != 0;
-        float r4[4];
+            for (int d = 0; d < 8; ++d) qv[h][d] = h < group ? qs[h][8 * l16 + d] : 0.0f;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float keep = b3 ? part[4 + i] : part[i];
-            const float send = b3 ? part[i] : part[4 + i];
-            r4[i] = keep + __shfl_xor(send, 8, 64);
-        }
-        float r2[2];
+        for (int j = 0; j < 4; ++j) {
+            if (t0 + 16 * j >= t1) break;  // uniform across the workgroup
+            const float kv[8] = {ka[j][0].x, ka[j][0].y, ka[j][0].z, ka[j][0].w,
+                                 ka[j][1].x, ka[j][1].y, ka[j][1].z, ka[j][1].w};
+            float part[8][1];
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const float keep = b2 ? r4[2 + i] : r4[i];
-            const float send = b2 ? r4[i] : r4[2 + i];
-            r2[i] = keep + __shfl_xor(send, 4, 64);
-        }
-        float r1;
-        {
-            const float keep = b1 ? r2[1] : r2[0];
-            const float send = b1 ? r2[0] : r2[1];
-            r1 = keep + __shfl_xor(send, 2, 64);
-        }
-        r1 += __shfl_xor(r1, 1, 64);
-        const int hs = (b3 ? 4 : 0) + (b2 ? 2 : 0) + (b1 ? 1 : 0);
-        if ((l16 & 1) == 0 && t < t1 && hs < group) {
-#pragma clang fp contract(off)
-            sc[hs][t - t0] = r1 * p.scale;
+            for (int h = 0; h < kMaxGroup; ++h) {
+                float a = 0.0f;
+#pragma unroll
+                for (int d = 0; d < 8; ++d) a = fmaf(qv[h][d], kv[d], a);
+                part[h][0] = a;
+            }
+            const float sdot = rs16_heads(part, lane);
+            const int hs = l16 >> 1;
+            const int t = t0 + ts + 16 * j;
+            if ((l16 & 1) == 0 && t < t1 && hs < group) sc[hs][t - t0] = sdot * p.scale;
         }
     }
     __syncthreads();
 
-    // ---- partial softmax per head: wave w handles heads w and w+4 ----
-    const int n = t1 - t0;
+    // ---- 4. partial softmax per head (wave w: heads w and w+4)
     for (int h = wave; h < group; h += kWaves) {
-        float m = -INFINITY;
-        for (int i = lane; i < n; i += 64) m = fmaxf(m, sc[h][i]);
+        const float sv = lane < n ? sc[h][lane] : -INFINITY;
+        float m = sv;
 #pragma unroll
         for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
-        float s = 0.0f;
-        for (int i = lane; i < n; i += 64) {
-            const float e = fast_exp_ref(sc[h][i] - m);
-            sc[h][i] = e;
-            s += e;
-        }
+        const float e = lane < n ? fast_exp_ref(sv - m) : 0.0f;
+        if (lane < n) sc[h][lane] = e;
+        float sum = e;
 #pragma unroll
-        for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+        for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
         if (lane == 0) {
             sm[h] = m;
-            sl[h] = s;
+            sl[h] = sum;
         }
     }
     __syncthreads();
 
-    // ---- Σ e·V: thread owns (head tid/32, dims 4·(tid%32)..+3) ----
-    const int h = tid >> 5;
-    const int d4 = (tid & 31) * 4;
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (h < group) {
-        for (int i = 0; i < n; ++i) {
-            const int t = t0 + i;
-            float4 v;
-            if (t == newest) v = make_float4(vnew[d4], vnew[d4 + 1], vnew[d4 + 2], vnew[d4 + 3]);
-            else v = *reinterpret_cast<const float4 *>(p.vc + (size_t)t * kvd + g * kHD + d4);
-            const float e = sc[h][i];
-            acc[0] = fmaf(e, v.x, acc[0]);
-            acc[1] = fmaf(e, v.y, acc[1]);
-            acc[2] = fmaf(e, v.z, acc[2]);
-            acc[3] = fmaf(e, v.w, acc[3]);
+    // ---- 5. Σ e·V over this thread's rows for every head → LDS
+#pragma unroll
+    for (int h = 0; h < kMaxGroup; ++h) {
+        if (h >= group) break;
+        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int i = tg + 8 * j;
+            if (i < n) {
+                const float e = sc[h][i];
+                acc.x = fmaf(e, va[j].x, acc.x);
+                acc.y = fmaf(e, va[j].y, acc.y);
+                acc.z = fmaf(e, va[j].z, acc.z);
+                acc.w = fmaf(e, va[j].w, acc.w);
+            }
         }
+        pv[tg][h][d4 / 4] = acc;
     }
-    // partial record: [m, l, acc[128]]
-    constexpr int REC = kHD + 2;
-    float *rec = p.part + ((size_t)(g * p.nsplit + split) * kMaxGroup) * REC;
+    __syncthreads();
+
+    // ---- 6. partial record [m, l, acc[128]] per head
+    const int h = tid >> 5;
+    float *rec = p.part + ((size_t)(g * p.nsplit + split) * kMaxGroup) * kRec;
     if (h < group) {
-        float *rh = rec + h * REC;
+        float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const float4 a = pv[k][h][d4 / 4];
+            o.x += a.x;
+            o.y += a.y;
+            o.z += a.z;
+            o.w += a.w;
+        }
+        float *rh = rec + h * kRec;
         if (d4 == 0) {
             rh[0] = n > 0 ? sm[h] : -INFINITY;
             rh[1] = n > 0 ? sl[h] : 0.0f;
         }
-        rh[2 + d4] = acc[0];
-        rh[3 + d4] = acc[1];
-        rh[4 + d4] = acc[2];
-        rh[5 + d4] = acc[3];
+        rh[2 + d4] = o.x;
+        rh[3 + d4] = o.y;
+        rh[4 + d4] = o.z;
+        rh[5 + d4] = o.w;
     }
     __threadfence();
     __syncthreads();
@@ -773,29 +937,40 @@ static __global__ void __launch_bounds__(kThreads) k_attn_decode(AttnParams p) {
     if (!s_last) return;
     __threadfence();
 
-    // ---- merge the nsplit partials of kv head g ----
+    // ---- 7. last workgroup of kv head g merges the splits (online rescale)
     if (h < group) {
-        const float *base = p.part + ((size_t)g * p.nsplit * kMaxGroup) * REC + h * REC;
-        float M = -INFINITY;
-        for (int s = 0; s < p.nsplit; ++s) {
-            const float ls = __hip_atomic_load(base + (size_t)s * kMaxGroup * REC + 1, __ATOMIC_RELAXED,
-                                               __HIP_MEMORY_SCOPE_AGENT);
-            const float ms = __hip_atomic_load(base + (size_t)s * kMaxGroup * REC, __ATOMIC_RELAXED,
-                                               __HIP_MEMORY_SCOPE_AGENT);
-            if (ls > 0.0f) M = fmaxf(M, ms);
-        }
-        float lsum = 0.0f;
-        float o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        for (int s = 0; s < p.nsplit; ++s) {
-            const float *rs = base + (size_t)s * kMaxGroup * REC;
-            const float ls = __hip_atomic_load(rs + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if (!(ls > 0.0f)) continue;
-            const float ms = __hip_atomic_load(rs, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            const float f = fast_exp_ref(ms - M);
-            lsum = fmaf(ls, f, lsum);
+        const float *base = p.part + ((size_t)g * p.nsplit * kMaxGroup + h) * kRec;
+        float M = -INFINITY, lsum = 0.0f;
+        float o[4] = {0.f, 0.f, 0.f, 0.f};
+        constexpr int B = 8;
+        for (int s0 = 0; s0 < p.nsplit; s0 += B) {
+            float ms[B], ls[B], av[B][4];
 #pragma unroll
-            for (int c = 0; c < 4; ++c)
-                o[c] = fmaf(__hip_atomic_load(rs + 2 + d4 + c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), f, o[c]);
+            for (int b = 0; b < B; ++b) {
+                const int s = s0 + b;
+                if (s < p.nsplit) {
+                    const float *rs = base + (size_t)s * kMaxGroup * kRec;
+                    ms[b] = rs[0];
+                    ls[b] = rs[1];
+                    av[b][0] = rs[2 + d4];
+                    av[b][1] = rs[3 + d4];
+                    av[b][2] = rs[4 + d4];
+                    av[b][3] = rs[5 + d4];
+                } else {
+                    ls[b] = 0.0f;
+                }
+            }
+#pragma unroll
+            for (int b = 0; b < B; ++b) {
+                if (!(ls[b] > 0.0f)) continue;
+                const float Mn = fmaxf(M, ms[b]);
+                const float fo = fast_exp_ref(M - Mn);  // M = -inf → clamps to e^-87 ≈ 0 (lsum, o are 0)
+                const float fs = fast_exp_ref(ms[b] - Mn);
+                lsum = lsum * fo + ls[b] * fs;
+#pragma unroll
+                for (int c = 0; c < 4; ++c) o[c] = o[c] * fo + av[b][c] * fs;
+                M = Mn;
+            }
         }
         const float inv = 1.0f / lsum;
         float *dst = p.head_out + (size_t)(g * group + h) * kHD + d4;

@@ -186,23 +186,34 @@ DevMat pocr::dev_mat(const pocr_weight *w) {
 // ---------------------------------------------------------------------------
 // GEMV dispatch
 // ---------------------------------------------------------------------------
-template <int QT, int NMAT, int TAG = 0>
+template <int QT, int NMAT, int U, int TAG = 0>
 static bool gemv_fast_kernel(int lpr, int cpl, const void **fn) {
-    constexpr int U = 2;
 #define POCR_K(L, C)                                                           \
     if (lpr == L && cpl == C) {                                                \
         *fn = reinterpret_cast<const void *>(&k_gemv<QT, L, C, U, NMAT, TAG>); \
         return true;                                                           \
     }
-    POCR_K(64, 1)
-    POCR_K(64, 2)
-    POCR_K(64, 3)
-    POCR_K(64, 4)
-    POCR_K(32, 1)
-    POCR_K(32, 2)
-    POCR_K(32, 3)
+    if constexpr (U == 8) {
+        POCR_K(64, 1)
+        POCR_K(32, 1)
+    } else {
+        POCR_K(64, 1)
+        POCR_K(64, 2)
+        POCR_K(64, 3)
+        POCR_K(64, 4)
+        POCR_K(32, 1)
+        POCR_K(32, 2)
+        POCR_K(32, 3)
+    }
 #undef POCR_K
     return false;
+}
+
+template <int QT>
+static bool pick_fast(int nmat, int u, int tag, int lpr, int cpl, const void **fn) {
+    if (nmat == 2) return gemv_fast_kernel<QT, 2, 2>(lpr, cpl, fn);
+    if (tag == 1) return u == 8 ? gemv_fast_kernel<QT, 1, 8, 1>(lpr, cpl, fn) : gemv_fast_kernel<QT, 1, 2, 1>(lpr, cpl, fn);
+    return u == 8 ? gemv_fast_kernel<QT, 1, 8>(lpr, cpl, fn) : gemv_fast_kernel<QT, 1, 2>(lpr, cpl, fn);
 }
 
 struct GemvPlan {
@@ -214,7 +225,7 @@ struct GemvPlan {
 // Choose the kernel for `rows` outputs of matrices with `cols` columns.
 // max_grid caps the workgroup count (rows loop inside the kernel).
 static int plan_gemv(int qtype, int nmat, int rows, int cols, const DevMat *mats, int nm, int max_grid,
-                     GemvPlan *plan, int tag = 0) {
+                     GemvPlan *plan, int tag = 0, const int *seg_end = nullptr) {
     if (cols > 16384) return fail(POCR_ERR_UNSUPPORTED, "gemv: cols %d > 16384", cols);
     plan->lds = (size_t)cols * 4;
     int W = qtype == POCR_Q4 ? 32 : 16;
@@ -237,23 +248,21 @@ static int plan_gemv(int qtype, int nmat, int rows, int cols, const DevMat *mats
         }
     }
     bool ok = false;
-    if (fast && tag == 1 && nmat == 1) {
-        if (qtype == POCR_Q4) ok = gemv_fast_kernel<QT_Q4, 1, 1>(lpr, cpl, &plan->fn);
-        if (qtype == POCR_Q8) ok = gemv_fast_kernel<QT_Q8, 1, 1>(lpr, cpl, &plan->fn);
-        if (qtype == POCR_Q6) ok = gemv_fast_kernel<QT_Q6, 1, 1>(lpr, cpl, &plan->fn);
-    } else if (fast) {
-        if (nmat == 1) {
-            if (qtype == POCR_Q4) ok = gemv_fast_kernel<QT_Q4, 1>(lpr, cpl, &plan->fn);
-            if (qtype == POCR_Q8) ok = gemv_fast_kernel<QT_Q8, 1>(lpr, cpl, &plan->fn);
-            if (qtype == POCR_Q6) ok = gemv_fast_kernel<QT_Q6, 1>(lpr, cpl, &plan->fn);
-        } else {
-            if (qtype == POCR_Q4) ok = gemv_fast_kernel<QT_Q4, 2>(lpr, cpl, &plan->fn);
-            if (qtype == POCR_Q8) ok = gemv_fast_kernel<QT_Q8, 2>(lpr, cpl, &plan->fn);
-            if (qtype == POCR_Q6) ok = gemv_fast_kernel<QT_Q6, 2>(lpr, cpl, &plan->fn);
-        }
+    // big row counts: 8 rows per lane group and step (more bytes in flight)
+    const int u = (fast && nmat == 1 && cpl == 1 && rows >= 8192) ? 8 : 2;
+    // row groups must not straddle segments
+    if (fast && nmat == 1 && seg_end) {
+        const int rg = (64 / lpr) * u;
+        for (int i = 0; i < 2; ++i)
+            if (seg_end[i] % rg != 0) fast = false;
+    }
+    if (fast) {
+        if (qtype == POCR_Q4) ok = pick_fast<QT_Q4>(nmat, u, tag, lpr, cpl, &plan->fn);
+        if (qtype == POCR_Q8) ok = pick_fast<QT_Q8>(nmat, u, tag, lpr, cpl, &plan->fn);
+        if (qtype == POCR_Q6) ok = pick_fast<QT_Q6>(nmat, u, tag, lpr, cpl, &plan->fn);
     }
     if (ok) {
-        const int rows_per_group = (64 / lpr) * 2;
+        const int rows_per_group = (64 / lpr) * u;
         const int groups = (rows + rows_per_group - 1) / rows_per_group;
         plan->grid = std::max(1, std::min((groups + kWaves - 1) / kWaves, max_grid));
     } else {
@@ -282,7 +291,7 @@ GemvParams pocr::gemv_params_1(const pocr_weight *w) {
 int pocr::gemv_launch(hipStream_t s, GemvParams p, int nmat, int pro, int epi, int max_grid) {
     GemvPlan plan;
     const int nm = nmat == 2 ? 2 : (p.seg_end[0] == p.rows ? 1 : (p.seg_end[1] == p.rows ? 2 : 3));
-    int rc = plan_gemv(p.m[0].qtype, nmat, p.rows, p.cols, p.m, nm, max_grid, &plan);
+    int rc = plan_gemv(p.m[0].qtype, nmat, p.rows, p.cols, p.m, nm, max_grid, &plan, 0, p.seg_end);
     if (rc) return rc;
     return launch_gemv(s, plan, p, pro, epi);
 }
@@ -521,7 +530,8 @@ extern "C" int pocr_mrope_pair(pocr_ctx *ctx, float *q, float *k, const float *c
     return sync(s);
 }
 
-static int attn_nsplit(int cap) { return std::max(32, (cap + kMaxChunk - 1) / kMaxChunk); }
+// one split per kMaxChunk rows of capacity
+static int attn_nsplit(int cap) { return std::max(1, (cap + kMaxChunk - 1) / kMaxChunk); }
 
 extern "C" int pocr_text_attention(pocr_ctx *ctx, const float *q, const float *k_cache, const float *v_cache,
                                    int cache_len, int heads, int kv_heads, int head_dim, float *out) {
@@ -544,7 +554,7 @@ extern "C" int pocr_text_attention(pocr_ctx *ctx, const float *q, const float *k
     const int group = heads / kv_heads;
     if (head_dim == kHD && group <= kMaxGroup) {
         const int nsplit = attn_nsplit(cache_len);
-        RC(ctx->part.ensure((size_t)kv_heads * nsplit * kMaxGroup * (kHD + 2) * 4));
+        RC(ctx->part.ensure((size_t)kv_heads * nsplit * kMaxGroup * kRec * 4));
         RC(ctx->counter.ensure((size_t)kv_heads * 4));
         HIP_TRY(hipMemsetAsync(ctx->counter.p, 0, (size_t)kv_heads * 4, s));
         AttnParams p{};
@@ -753,7 +763,7 @@ extern "C" int pocr_seq_create(pocr_model *m, int capacity, pocr_seq **out) {
     if (e == hipSuccess) e = hipMalloc(&s->vbuf, (size_t)c.hidden * 4);
     if (e == hipSuccess) e = hipMalloc(&s->g, (size_t)c.intermediate * 4);
     if (e == hipSuccess) e = hipMalloc(&s->logits, (size_t)c.vocab * 4);
-    if (e == hipSuccess) e = hipMalloc(&s->part, (size_t)c.kv_heads * s->nsplit * kMaxGroup * (kHD + 2) * 4);
+    if (e == hipSuccess) e = hipMalloc(&s->part, (size_t)c.kv_heads * s->nsplit * kMaxGroup * kRec * 4);
     if (e == hipSuccess) e = hipMalloc(&s->counter, (size_t)c.kv_heads * 4);
     if (e == hipSuccess) e = hipMalloc(&s->st, sizeof(StepState));
     if (e == hipSuccess) e = hipMalloc(&s->tokens, (size_t)s->max_tokens * 4);
@@ -1083,7 +1093,11 @@ static int decode_locked(pocr_seq *s, int32_t first_token, int32_t first_pos, in
     if (s->len + steps_needed > s->cap)
         return fail(POCR_ERR_ARG, "decode: %d steps exceed capacity (%d of %d rows used)", steps_needed, s->len,
                     s->cap);
-    RC(build_decode_graph(s));
+    // POCR_HIP_GRAPH=0 replays the same kernel sequence with direct launches
+    // (profilers that cannot follow graph launches)
+    const char *g_env = getenv("POCR_HIP_GRAPH");
+    const bool use_graph = !(g_env && g_env[0] == '0');
+    if (use_graph) RC(build_decode_graph(s));
     StepState hs;
     RC(read_state(s, &hs));
     hs.err = 0;
@@ -1098,7 +1112,10 @@ static int decode_locked(pocr_seq *s, int32_t first_token, int32_t first_pos, in
     std::vector<int32_t> tok;
     while (launched < steps_needed) {
         const int n = std::min(batch, steps_needed - launched);
-        for (int i = 0; i < n; ++i) HIP_TRY(hipGraphLaunch(s->decode_exec, st));
+        for (int i = 0; i < n; ++i) {
+            if (use_graph) HIP_TRY(hipGraphLaunch(s->decode_exec, st));
+            else RC(enqueue_step(s, 1, true, false));
+        }
         launched += n;
         RC(read_state(s, &hs));
         if (hs.err) return fail(POCR_ERR_DEVICE, "decode: device state error %d", hs.err);
