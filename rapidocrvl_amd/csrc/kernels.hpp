@@ -19,6 +19,7 @@ enum : int { QT_Q8 = 1000, QT_Q4 = 1001, QT_Q6 = 1002 };
 constexpr int kThreads = 256;  // 4 wavefronts per workgroup
 constexpr int kWaves = kThreads / 64;
 constexpr int kMaxHalf = 128;  // head_dim/2 upper bound for RoPE tables
+constexpr int kMaxCols = 4096; // widest input of the streaming GEMV kernel
 
 struct DevMat {
     const float *scale;    // [rows]
@@ -191,6 +192,177 @@ __device__ __forceinline__ float lane_group_sum(float v) {
 #pragma unroll
     for (int off = LPR / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
     return v;
+}
+
+// ---------------------------------------------------------------------------
+// Integer inner product.  Each lane turns its activation slice once into
+// three int8 digit planes: with S a power of two ≥ max|x|/127,
+//   x = S·(d0 + d1/2^7 + d2/2^14) + e,  |e| ≤ S/2^15  (≈ 2^-22·max|x|),
+// d0 ∈ [-127,127], d1,d2 ∈ [-64,64].  A row's dot product is then three exact
+// int32 accumulations of v_dot4 (4 code×digit products per instruction),
+// combined to f32 once per row.  Unsigned codes (Q4 nibble, Q6 field) are
+// fed as their raw value u and the offset is removed exactly as
+// BIAS·Σd_k per digit plane.
+// ---------------------------------------------------------------------------
+template <int QT>
+struct DigitTraits {
+    static constexpr int NDW = QT == QT_Q4 ? 8 : 4;  // digit dwords per chunk
+    static constexpr int IBIAS = QT == QT_Q4 ? 8 : (QT == QT_Q6 ? 32 : 0);
+};
+
+__device__ __forceinline__ int pack4(int a, int b, int c, int d) {
+    return (a & 0xFF) | ((b & 0xFF) << 8) | ((c & 0xFF) << 16) | ((d & 0xFF) << 24);
+}
+
+template <int QT, int CPL>
+struct XDigits {
+    int d[CPL][DigitTraits<QT>::NDW][3];
+    int bias[CPL][3];
+    float scale[CPL];
+};
+
+// column (within a chunk) of byte m of digit dword k: Q4 dword 2k' holds the
+// low nibbles of chunk dword k' (cols 8k'+0,2,4,6), dword 2k'+1 the high ones
+// (cols 8k'+1,3,5,7); Q8/Q6 dword k holds cols 4k..4k+3.
+template <int QT>
+__device__ __forceinline__ int digit_col(int k, int m) {
+    if constexpr (QT == QT_Q4) return 8 * (k >> 1) + 2 * m + (k & 1);
+    else return 4 * k + m;
+}
+
+// LDS layout after the activation prologue: x (f32[cols]), then per chunk c
+// its digit dwords dig[c][k][3] and its scale sc[c] (power of two ≥ max|x|/127
+// over the chunk's columns).
+template <int QT>
+__device__ __forceinline__ int *lds_digits(float *xs, int cols) {
+    return reinterpret_cast<int *>(xs + cols);
+}
+template <int QT>
+__device__ __forceinline__ float *lds_scales(float *xs, int cols) {
+    constexpr int W = QTraits<QT>::W, NDW = DigitTraits<QT>::NDW;
+    return xs + cols + (cols / W) * NDW * 3;
+}
+template <int QT>
+__host__ __device__ constexpr size_t gemv_lds_bytes(int cols) {
+    return (size_t)cols * 4 + (size_t)(cols / QTraits<QT>::W) * (DigitTraits<QT>::NDW * 3 + 1) * 4;
+}
+
+// Workgroup-cooperative digit planes: task (chunk c, dword k) owns 4 columns;
+// the NDW tasks of a chunk are adjacent lanes and agree on the chunk scale by
+// a max over those lanes.  Ends with a barrier.
+template <int QT>
+__device__ __forceinline__ void build_digits(float *xs, int cols) {
+    constexpr int W = QTraits<QT>::W, NDW = DigitTraits<QT>::NDW;
+    int *dig = lds_digits<QT>(xs, cols);
+    float *scl = lds_scales<QT>(xs, cols);
+    const int tasks = (cols / W) * NDW;  // multiple of NDW; NDW divides 64
+    for (int t0 = 0; t0 < tasks; t0 += kThreads) {
+        const int t = t0 + threadIdx.x;
+        const bool ok = t < tasks;
+        const int c = t / NDW, k = t % NDW;
+        float x[4];
+        float m = 0.0f;
+#pragma unroll
+        for (int mm = 0; mm < 4; ++mm) {
+            x[mm] = ok ? xs[c * W + digit_col<QT>(k, mm)] : 0.0f;
+            m = fmaxf(m, fabsf(x[mm]));
+        }
+#pragma unroll
+        for (int off = 1; off < NDW; off <<= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+        int ex = 0;
+        (void)frexpf(m * (1.0f / 127.0f), &ex);  // m/127 < 2^ex
+        const float inv = m > 0.0f ? ldexpf(1.0f, -ex) : 1.0f;
+        int d0[4], d1[4], d2[4];
+#pragma unroll
+        for (int mm = 0; mm < 4; ++mm) {
+            const float y = x[mm] * inv;  // exact: inv is a power of two
+            const float a = rintf(y);
+            const float y1 = (y - a) * 128.0f;
+            const float b = rintf(y1);
+            d0[mm] = (int)a;
+            d1[mm] = (int)b;
+            d2[mm] = (int)rintf((y1 - b) * 128.0f);
+        }
+        if (ok) {
+            int *o = dig + (c * NDW + k) * 3;
+            o[0] = pack4(d0[0], d0[1], d0[2], d0[3]);
+            o[1] = pack4(d1[0], d1[1], d1[2], d1[3]);
+            o[2] = pack4(d2[0], d2[1], d2[2], d2[3]);
+            if (k == 0) scl[c] = m > 0.0f ? ldexpf(1.0f, ex) : 1.0f;
+        }
+    }
+    __syncthreads();
+}
+
+template <int QT, int LPR, int CPL>
+__device__ __forceinline__ void load_digits(float *xs, int cols, int l, XDigits<QT, CPL> &xd) {
+    constexpr int NDW = DigitTraits<QT>::NDW;
+    const int *dig = lds_digits<QT>(xs, cols);
+    const float *scl = lds_scales<QT>(xs, cols);
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+        const int c = l + j * LPR;
+        int s0 = 0, s1 = 0, s2 = 0;
+#pragma unroll
+        for (int k = 0; k < NDW; ++k) {
+            const int *o = dig + (c * NDW + k) * 3;
+            xd.d[j][k][0] = o[0];
+            xd.d[j][k][1] = o[1];
+            xd.d[j][k][2] = o[2];
+            s0 = __builtin_amdgcn_sdot4(o[0], 0x01010101, s0, false);
+            s1 = __builtin_amdgcn_sdot4(o[1], 0x01010101, s1, false);
+            s2 = __builtin_amdgcn_sdot4(o[2], 0x01010101, s2, false);
+        }
+        xd.bias[j][0] = DigitTraits<QT>::IBIAS * s0;
+        xd.bias[j][1] = DigitTraits<QT>::IBIAS * s1;
+        xd.bias[j][2] = DigitTraits<QT>::IBIAS * s2;
+        xd.scale[j] = scl[c];
+    }
+}
+
+__device__ __forceinline__ void dot3(int code4, const int (&x)[3], int (&a)[3]) {
+    a[0] = __builtin_amdgcn_sdot4(code4, x[0], a[0], false);
+    a[1] = __builtin_amdgcn_sdot4(code4, x[1], a[1], false);
+    a[2] = __builtin_amdgcn_sdot4(code4, x[2], a[2], false);
+}
+
+// six-bit fields of one 24-bit group spread into the four bytes of a dword
+__device__ __forceinline__ int spread6(uint32_t g) {
+    uint32_t r = g & 0x3Fu;
+    r |= (g << 2) & 0x3F00u;
+    r |= (g << 4) & 0x3F0000u;
+    r |= (g << 6) & 0x3F000000u;
+    return (int)r;
+}
+
+template <int QT, int CPL>
+__device__ __forceinline__ float row_dot(const Chunk (&w)[CPL], const XDigits<QT, CPL> &xd) {
+    float r = 0.0f;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+        int a[3] = {0, 0, 0};
+        if constexpr (QT == QT_Q8) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) dot3((int)w[j].d[k], xd.d[j][k], a);
+        } else if constexpr (QT == QT_Q4) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                dot3((int)(w[j].d[k] & 0x0F0F0F0Fu), xd.d[j][2 * k], a);
+                dot3((int)((w[j].d[k] >> 4) & 0x0F0F0F0Fu), xd.d[j][2 * k + 1], a);
+            }
+        } else {
+            const uint32_t d0 = w[j].d[0], d1 = w[j].d[1], d2 = w[j].d[2];
+            dot3(spread6(d0), xd.d[j][0], a);
+            dot3(spread6(__builtin_amdgcn_alignbit(d1, d0, 24)), xd.d[j][1], a);
+            dot3(spread6(__builtin_amdgcn_alignbit(d2, d1, 16)), xd.d[j][2], a);
+            dot3(spread6(d2 >> 8), xd.d[j][3], a);
+        }
+        const float f0 = (float)(a[0] - xd.bias[j][0]);
+        const float f1 = (float)(a[1] - xd.bias[j][1]);
+        const float f2 = (float)(a[2] - xd.bias[j][2]);
+        r = fmaf(xd.scale[j], fmaf(f2, 1.0f / 16384.0f, fmaf(f1, 1.0f / 128.0f, f0)), r);
+    }
+    return r;
 }
 
 // Cross-lane exchanges used by the reduce-scatter.  Each pairs every lane with
@@ -475,27 +647,43 @@ __global__ void __launch_bounds__(kThreads) k_gemv(GemvParams p, int pro, int ep
     const int gstride = gridDim.x * kWaves;
     int g = blockIdx.x * kWaves + wave;
 
+    // activations first, so that waiting for them does not wait for weights
+    constexpr int XPT = kMaxCols / kThreads;
+    float xv[XPT], wv[XPT];
+    const int cols = p.cols;
+#pragma unroll
+    for (int i = 0; i < XPT; ++i) {
+        const int c = threadIdx.x + i * kThreads;
+        xv[i] = c < cols ? p.x[c] : 0.0f;
+        wv[i] = (pro == PRO_RMSNORM && c < cols) ? p.norm_w[c] : 0.0f;
+    }
     Chunk w[U][NMAT][CPL];
     {
         const int gc = min(g, ngroups - 1);
         load_group<QT, LPR, CPL, U, NMAT>(seg_select<NMAT>(p, gc * RG), row_bytes, rows, gc, sub, l, w);
     }
-
-    if (pro == PRO_RMSNORM) stage_x<PRO_RMSNORM>(xs, p.x, p.norm_w, p.cols, p.eps, red);
-    else stage_x<PRO_COPY>(xs, p.x, p.norm_w, p.cols, p.eps, red);
-
-    float xr[CPL][T::W];
-    float sx = 0.0f;
+    if (pro == PRO_RMSNORM) {
+        // RMSNorm (ops.go:1015-1037): x·fastRsqrt(Σx²/n + eps)·w
+        float ss = 0.0f;
 #pragma unroll
-    for (int j = 0; j < CPL; ++j) {
-        const int c = l + j * LPR;
+        for (int i = 0; i < XPT; ++i) ss = fmaf(xv[i], xv[i], ss);
+        ss = block_sum(ss, red);
+        const float scale = fast_rsqrt_ref(ss / (float)cols + p.eps);
 #pragma unroll
-        for (int k = 0; k < T::W; ++k) {
-            xr[j][k] = xs[c * T::W + k];
-            sx += xr[j][k];
+        for (int i = 0; i < XPT; ++i) {
+#pragma clang fp contract(off)
+            xv[i] = xv[i] * scale * wv[i];
         }
     }
-    const float bias = T::BIAS * sx;
+#pragma unroll
+    for (int i = 0; i < XPT; ++i) {
+        const int c = threadIdx.x + i * kThreads;
+        if (c < cols) xs[c] = xv[i];
+    }
+    __syncthreads();
+    build_digits<QT>(xs, cols);
+    XDigits<QT, CPL> xd;
+    load_digits<QT, LPR, CPL>(xs, cols, l, xd);
     const bool in_place = epi == EPI_OPROJ ? oproj_in_place(p) : false;
     float best_v = -INFINITY;
     int best_r = 0x7FFFFFFF;
@@ -523,12 +711,7 @@ __global__ void __launch_bounds__(kThreads) k_gemv(GemvParams p, int pro, int ep
 #pragma unroll
         for (int u = 0; u < U; ++u)
 #pragma unroll
-            for (int mi = 0; mi < NMAT; ++mi) {
-                float a = 0.0f;
-#pragma unroll
-                for (int j = 0; j < CPL; ++j) a += chunk_dot<QT>(w[u][mi][j], xr[j]);
-                acc[u][mi] = a - bias;
-            }
+            for (int mi = 0; mi < NMAT; ++mi) acc[u][mi] = row_dot<QT, CPL>(w[u][mi], xd);
         reduce_scatter<LPR, U, NMAT>(acc, lane);
         if (writer && r < rows) {
             float s[NMAT];

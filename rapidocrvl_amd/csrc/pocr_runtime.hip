@@ -230,7 +230,7 @@ static int plan_gemv(int qtype, int nmat, int rows, int cols, const DevMat *mats
     plan->lds = (size_t)cols * 4;
     int W = qtype == POCR_Q4 ? 32 : 16;
     int CB = qtype == POCR_Q6 ? 12 : 16;
-    bool fast = cols % W == 0;
+    bool fast = cols % W == 0 && cols <= kMaxCols;
     int C = cols / W;
     for (int i = 0; i < nm && fast; ++i) {
         if (mats[i].row_bytes != C * CB) fast = false;
@@ -262,6 +262,8 @@ static int plan_gemv(int qtype, int nmat, int rows, int cols, const DevMat *mats
         if (qtype == POCR_Q6) ok = pick_fast<QT_Q6>(nmat, u, tag, lpr, cpl, &plan->fn);
     }
     if (ok) {
+        plan->lds = qtype == POCR_Q4 ? gemv_lds_bytes<QT_Q4>(cols)
+                                     : (qtype == POCR_Q8 ? gemv_lds_bytes<QT_Q8>(cols) : gemv_lds_bytes<QT_Q6>(cols));
         const int rows_per_group = (64 / lpr) * u;
         const int groups = (rows + rows_per_group - 1) / rows_per_group;
         plan->grid = std::max(1, std::min((groups + kWaves - 1) / kWaves, max_grid));
