@@ -65,7 +65,7 @@ struct pocr_ctx {
     hipStream_t stream = nullptr;
     std::mutex mu;
     // op-level staging
-    DevBuf x, out, out2, out3, res, vbuf, kc, vc, part, counter, tabs, state;
+    DevBuf x, out, out2, out3, res, vbuf, kc, vc, part, tabs, state;
 };
 
 struct pocr_weight {
@@ -118,7 +118,6 @@ struct pocr_seq {
     float *kv = nullptr;  // [layers][2][cap][kvd]
     float *h = nullptr, *qkv = nullptr, *head_out = nullptr, *vbuf = nullptr, *g = nullptr, *logits = nullptr;
     float *part = nullptr;
-    unsigned int *counter = nullptr;
     pocr::StepState *st = nullptr;
     int32_t *tokens = nullptr;
     int max_tokens = 0;

@@ -230,94 +230,21 @@ __device__ __forceinline__ int digit_col(int k, int m) {
     else return 4 * k + m;
 }
 
-// LDS layout after the activation prologue: x (f32[cols]), then per chunk c
-// its digit dwords dig[c][k][3] and its scale sc[c] (power of two ≥ max|x|/127
-// over the chunk's columns).
+// LDS layout after the activation prologue: one record of RS ints per chunk
+// c (W columns): its digit dwords dig[k][plane] (k < NDW, plane < 3), then
+// the three bias sums IBIAS·Σd of the planes, then the chunk scale (a power
+// of two ≥ max|x|/127 over the chunk's columns, as float bits).  RS·4 is a
+// multiple of 16, so a lane reads its records with 16-byte LDS loads.
 template <int QT>
-__device__ __forceinline__ int *lds_digits(float *xs, int cols) {
-    return reinterpret_cast<int *>(xs + cols);
-}
-template <int QT>
-__device__ __forceinline__ float *lds_scales(float *xs, int cols) {
-    constexpr int W = QTraits<QT>::W, NDW = DigitTraits<QT>::NDW;
-    return xs + cols + (cols / W) * NDW * 3;
-}
+struct DigitRec {
+    static constexpr int NDW = DigitTraits<QT>::NDW;
+    static constexpr int RS = NDW * 3 + 4;
+    static constexpr int TPC = QTraits<QT>::W / 8;  // prologue threads per chunk (8 columns each)
+    static_assert((RS * 4) % 16 == 0, "record must be 16-byte aligned");
+};
 template <int QT>
 __host__ __device__ constexpr size_t gemv_lds_bytes(int cols) {
-    return (size_t)cols * 4 + (size_t)(cols / QTraits<QT>::W) * (DigitTraits<QT>::NDW * 3 + 1) * 4;
-}
-
-// Workgroup-cooperative digit planes: task (chunk c, dword k) owns 4 columns;
-// the NDW tasks of a chunk are adjacent lanes and agree on the chunk scale by
-// a max over those lanes.  Ends with a barrier.
-template <int QT>
-__device__ __forceinline__ void build_digits(float *xs, int cols) {
-    constexpr int W = QTraits<QT>::W, NDW = DigitTraits<QT>::NDW;
-    int *dig = lds_digits<QT>(xs, cols);
-    float *scl = lds_scales<QT>(xs, cols);
-    const int tasks = (cols / W) * NDW;  // multiple of NDW; NDW divides 64
-    for (int t0 = 0; t0 < tasks; t0 += kThreads) {
-        const int t = t0 + threadIdx.x;
-        const bool ok = t < tasks;
-        const int c = t / NDW, k = t % NDW;
-        float x[4];
-        float m = 0.0f;
-#pragma unroll
-        for (int mm = 0; mm < 4; ++mm) {
-            x[mm] = ok ? xs[c * W + digit_col<QT>(k, mm)] : 0.0f;
-            m = fmaxf(m, fabsf(x[mm]));
-        }
-#pragma unroll
-        for (int off = 1; off < NDW; off <<= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
-        int ex = 0;
-        (void)frexpf(m * (1.0f / 127.0f), &ex);  // m/127 < 2^ex
-        const float inv = m > 0.0f ? ldexpf(1.0f, -ex) : 1.0f;
-        int d0[4], d1[4], d2[4];
-#pragma unroll
-        for (int mm = 0; mm < 4; ++mm) {
-            const float y = x[mm] * inv;  // exact: inv is a power of two
-            const float a = rintf(y);
-            const float y1 = (y - a) * 128.0f;
-            const float b = rintf(y1);
-            d0[mm] = (int)a;
-            d1[mm] = (int)b;
-            d2[mm] = (int)rintf((y1 - b) * 128.0f);
-        }
-        if (ok) {
-            int *o = dig + (c * NDW + k) * 3;
-            o[0] = pack4(d0[0], d0[1], d0[2], d0[3]);
-            o[1] = pack4(d1[0], d1[1], d1[2], d1[3]);
-            o[2] = pack4(d2[0], d2[1], d2[2], d2[3]);
-            if (k == 0) scl[c] = m > 0.0f ? ldexpf(1.0f, ex) : 1.0f;
-        }
-    }
-    __syncthreads();
-}
-
-template <int QT, int LPR, int CPL>
-__device__ __forceinline__ void load_digits(float *xs, int cols, int l, XDigits<QT, CPL> &xd) {
-    constexpr int NDW = DigitTraits<QT>::NDW;
-    const int *dig = lds_digits<QT>(xs, cols);
-    const float *scl = lds_scales<QT>(xs, cols);
-#pragma unroll
-    for (int j = 0; j < CPL; ++j) {
-        const int c = l + j * LPR;
-        int s0 = 0, s1 = 0, s2 = 0;
-#pragma unroll
-        for (int k = 0; k < NDW; ++k) {
-            const int *o = dig + (c * NDW + k) * 3;
-            xd.d[j][k][0] = o[0];
-            xd.d[j][k][1] = o[1];
-            xd.d[j][k][2] = o[2];
-            s0 = __builtin_amdgcn_sdot4(o[0], 0x01010101, s0, false);
-            s1 = __builtin_amdgcn_sdot4(o[1], 0x01010101, s1, false);
-            s2 = __builtin_amdgcn_sdot4(o[2], 0x01010101, s2, false);
-        }
-        xd.bias[j][0] = DigitTraits<QT>::IBIAS * s0;
-        xd.bias[j][1] = DigitTraits<QT>::IBIAS * s1;
-        xd.bias[j][2] = DigitTraits<QT>::IBIAS * s2;
-        xd.scale[j] = scl[c];
-    }
+    return (size_t)(cols / QTraits<QT>::W) * DigitRec<QT>::RS * 4;
 }
 
 __device__ __forceinline__ void dot3(int code4, const int (&x)[3], int (&a)[3]) {
@@ -423,6 +350,176 @@ __device__ __forceinline__ void reduce_scatter(float (&v)[8][NM], int lane) {
         rs_step<N3, NM, XM8, 4>(v, lane);
         rs_step<N4, NM, XQ2, 2>(v, lane);
         rs_step<N5, NM, XQ1, 1>(v, lane);
+    }
+}
+
+// Sum over the 64 lanes of a wave, the same value in every lane (DPP within
+// rows of 16, then swizzle and bpermute across them).
+__device__ __forceinline__ float wave_sum(float v) {
+    v += xchg<XQ1>(v);
+    v += xchg<XQ2>(v);
+    v += xchg<XM8>(v);
+    v += xchg<XM16>(v);
+    v += xchg<XS16>(v);
+    v += xchg<XS32>(v);
+    return v;
+}
+
+// ---------------------------------------------------------------------------
+// Activation prologue.  Thread t owns 8 consecutive columns per pass (2048
+// columns a pass); the TPC threads of a chunk are adjacent lanes.  Each turns
+// its columns into its two digit dwords of the three planes and writes them
+// to the chunk's LDS record; lane 0 of the chunk adds the bias sums and the
+// scale.  Columns past cols are clamped loads, never written.
+// ---------------------------------------------------------------------------
+constexpr int kXPass = 8 * kThreads;              // columns per prologue pass
+constexpr int kXPasses = kMaxCols / kXPass;       // 2
+
+struct XRegs {
+    float4 x[kXPasses][2];
+    float4 w[kXPasses][2];
+};
+
+// Requests the activation (and RMSNorm weight) columns of this thread.
+__device__ __forceinline__ void x_load(const float *x, const float *nw, bool norm, int cols, XRegs &r) {
+#pragma unroll
+    for (int pp = 0; pp < kXPasses; ++pp) {
+        if (pp * kXPass >= cols) break;  // uniform
+        const int cb = min((pp * kThreads + (int)threadIdx.x) * 8, cols - 8);
+        const float4 *xp = reinterpret_cast<const float4 *>(x + cb);
+        r.x[pp][0] = xp[0];
+        r.x[pp][1] = xp[1];
+        if (norm) {
+            const float4 *wp = reinterpret_cast<const float4 *>(nw + cb);
+            r.w[pp][0] = wp[0];
+            r.w[pp][1] = wp[1];
+        }
+    }
+}
+
+// Digit planes of the thread's columns → LDS records; returns the RMSNorm
+// factor fastRsqrt(Σx²/n + eps) (1 without norm).  With the norm on, the
+// digits encode x·w and the row sums are scaled by the factor afterwards.
+// Ends with the workgroup's only barrier.
+template <int QT>
+__device__ __forceinline__ float x_digits(const XRegs &r, bool norm, int cols, float eps, int *lds, float *red) {
+    constexpr int NDW = DigitRec<QT>::NDW, RS = DigitRec<QT>::RS, TPC = DigitRec<QT>::TPC;
+    const int lane = threadIdx.x & 63;
+    float ss = 0.0f;
+#pragma unroll
+    for (int pp = 0; pp < kXPasses; ++pp) {
+        if (pp * kXPass >= cols) break;  // uniform
+        const int G = pp * kThreads + (int)threadIdx.x;  // 8-column group
+        const bool valid = G * 8 < cols;
+        float y[8] = {r.x[pp][0].x, r.x[pp][0].y, r.x[pp][0].z, r.x[pp][0].w,
+                      r.x[pp][1].x, r.x[pp][1].y, r.x[pp][1].z, r.x[pp][1].w};
+        if (norm) {
+            const float wv[8] = {r.w[pp][0].x, r.w[pp][0].y, r.w[pp][0].z, r.w[pp][0].w,
+                                 r.w[pp][1].x, r.w[pp][1].y, r.w[pp][1].z, r.w[pp][1].w};
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                ss = valid ? fmaf(y[i], y[i], ss) : ss;
+                y[i] = y[i] * wv[i];  // a lone product: nothing to contract
+            }
+        }
+        float m = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(y[i]));
+        m = fmaxf(m, xchg<XQ1>(m));
+        if constexpr (TPC == 4) m = fmaxf(m, xchg<XQ2>(m));
+        int ex = 0;
+        (void)frexpf(m * (1.0f / 127.0f), &ex);  // m/127 < 2^ex
+        const float inv = m > 0.0f ? ldexpf(1.0f, -ex) : 1.0f;
+        int d0[8], d1[8], d2[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float t = y[i] * inv;  // exact: inv is a power of two
+            const float a = rintf(t);
+            const float t1 = (t - a) * 128.0f;
+            const float b = rintf(t1);
+            d0[i] = (int)a;
+            d1[i] = (int)b;
+            d2[i] = (int)rintf((t1 - b) * 128.0f);
+        }
+        // digit dwords: Q4 → even columns, then odd ones (low / high nibbles);
+        // Q8/Q6 → columns 0..3, then 4..7
+        int lo[3], hi[3];
+        if constexpr (QT == QT_Q4) {
+            lo[0] = pack4(d0[0], d0[2], d0[4], d0[6]);
+            hi[0] = pack4(d0[1], d0[3], d0[5], d0[7]);
+            lo[1] = pack4(d1[0], d1[2], d1[4], d1[6]);
+            hi[1] = pack4(d1[1], d1[3], d1[5], d1[7]);
+            lo[2] = pack4(d2[0], d2[2], d2[4], d2[6]);
+            hi[2] = pack4(d2[1], d2[3], d2[5], d2[7]);
+        } else {
+            lo[0] = pack4(d0[0], d0[1], d0[2], d0[3]);
+            hi[0] = pack4(d0[4], d0[5], d0[6], d0[7]);
+            lo[1] = pack4(d1[0], d1[1], d1[2], d1[3]);
+            hi[1] = pack4(d1[4], d1[5], d1[6], d1[7]);
+            lo[2] = pack4(d2[0], d2[1], d2[2], d2[3]);
+            hi[2] = pack4(d2[4], d2[5], d2[6], d2[7]);
+        }
+        float bs[3];
+#pragma unroll
+        for (int k = 0; k < 3; ++k) {
+            const int b2 = __builtin_amdgcn_sdot4(hi[k], 0x01010101, __builtin_amdgcn_sdot4(lo[k], 0x01010101, 0, false),
+                                                  false);
+            bs[k] = (float)b2;  // |Σ| ≤ 32·127: exact in f32
+            bs[k] += xchg<XQ1>(bs[k]);
+            if constexpr (TPC == 4) bs[k] += xchg<XQ2>(bs[k]);
+        }
+        if (valid) {
+            const int c = G / TPC, q = G % TPC;
+            int *rec = lds + c * RS;
+            int2 *dp = reinterpret_cast<int2 *>(rec + 2 * q * 3);  // dwords 2q, 2q+1: 6 ints
+            dp[0] = make_int2(lo[0], lo[1]);
+            dp[1] = make_int2(lo[2], hi[0]);
+            dp[2] = make_int2(hi[1], hi[2]);
+            if (q == 0) {
+                const float sc = m > 0.0f ? ldexpf(1.0f, ex) : 1.0f;
+                *reinterpret_cast<int4 *>(rec + NDW * 3) =
+                    make_int4(DigitTraits<QT>::IBIAS * (int)bs[0], DigitTraits<QT>::IBIAS * (int)bs[1],
+                              DigitTraits<QT>::IBIAS * (int)bs[2], __float_as_int(sc));
+            }
+        }
+    }
+    if (norm) {
+        ss = wave_sum(ss);
+        if (lane == 0) red[threadIdx.x >> 6] = ss;
+    }
+    __syncthreads();
+    if (!norm) return 1.0f;
+    float tot = red[0];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) tot += red[w];
+    // RMSNorm (ops.go:1015-1037): x·fastRsqrt(Σx²/n + eps)·w
+    return fast_rsqrt_ref(tot / (float)cols + eps);
+}
+
+// The lane's CPL chunk records (chunks l + j·LPR) → registers.
+template <int QT, int LPR, int CPL>
+__device__ __forceinline__ void load_digits(const int *lds, int l, XDigits<QT, CPL> &xd) {
+    constexpr int NDW = DigitRec<QT>::NDW, RS = DigitRec<QT>::RS;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+        const int4 *rec = reinterpret_cast<const int4 *>(lds + (l + j * LPR) * RS);
+        int v[RS];
+#pragma unroll
+        for (int i = 0; i < RS / 4; ++i) {
+            const int4 t = rec[i];
+            v[4 * i] = t.x;
+            v[4 * i + 1] = t.y;
+            v[4 * i + 2] = t.z;
+            v[4 * i + 3] = t.w;
+        }
+#pragma unroll
+        for (int k = 0; k < NDW; ++k)
+#pragma unroll
+            for (int pl = 0; pl < 3; ++pl) xd.d[j][k][pl] = v[k * 3 + pl];
+        xd.bias[j][0] = v[NDW * 3];
+        xd.bias[j][1] = v[NDW * 3 + 1];
+        xd.bias[j][2] = v[NDW * 3 + 2];
+        xd.scale[j] = __int_as_float(v[NDW * 3 + 3]);
     }
 }
 
@@ -630,10 +727,12 @@ __device__ __forceinline__ void load_group(const SegSel &sel, int row_bytes, int
 // TAG only separates instances for profiling (TAG=1: the timing entry point).
 template <int QT, int LPR, int CPL, int U, int NMAT, int TAG = 0>
 __global__ void __launch_bounds__(kThreads) k_gemv(GemvParams p, int pro, int epi) {
-    if (p.st && p.st->err) return;
-    extern __shared__ float xs[];
+    // No step-state check up front: a GEMV writes only step scratch (the
+    // residual stream, q/k/v, gate) and never indexes by the step state, so a
+    // failed step needs no guard here and the first loads wait for nothing.
+    extern __shared__ int4 lds4[];
+    int *lds = reinterpret_cast<int *>(lds4);
     __shared__ float red[2 * kWaves];
-    using T = QTraits<QT>;
     constexpr int RPW = 64 / LPR;
     constexpr int RG = RPW * U;
 
@@ -646,67 +745,51 @@ __global__ void __launch_bounds__(kThreads) k_gemv(GemvParams p, int pro, int ep
     const int ngroups = (rows + RG - 1) / RG;
     const int gstride = gridDim.x * kWaves;
     int g = blockIdx.x * kWaves + wave;
-
-    // activations first, so that waiting for them does not wait for weights
-    constexpr int XPT = kMaxCols / kThreads;
-    float xv[XPT], wv[XPT];
-    const int cols = p.cols;
-#pragma unroll
-    for (int i = 0; i < XPT; ++i) {
-        const int c = threadIdx.x + i * kThreads;
-        xv[i] = c < cols ? p.x[c] : 0.0f;
-        wv[i] = (pro == PRO_RMSNORM && c < cols) ? p.norm_w[c] : 0.0f;
-    }
-    Chunk w[U][NMAT][CPL];
-    {
-        const int gc = min(g, ngroups - 1);
-        load_group<QT, LPR, CPL, U, NMAT>(seg_select<NMAT>(p, gc * RG), row_bytes, rows, gc, sub, l, w);
-    }
-    if (pro == PRO_RMSNORM) {
-        // RMSNorm (ops.go:1015-1037): x·fastRsqrt(Σx²/n + eps)·w
-        float ss = 0.0f;
-#pragma unroll
-        for (int i = 0; i < XPT; ++i) ss = fmaf(xv[i], xv[i], ss);
-        ss = block_sum(ss, red);
-        const float scale = fast_rsqrt_ref(ss / (float)cols + p.eps);
-#pragma unroll
-        for (int i = 0; i < XPT; ++i) {
-#pragma clang fp contract(off)
-            xv[i] = xv[i] * scale * wv[i];
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < XPT; ++i) {
-        const int c = threadIdx.x + i * kThreads;
-        if (c < cols) xs[c] = xv[i];
-    }
-    __syncthreads();
-    build_digits<QT>(xs, cols);
-    XDigits<QT, CPL> xd;
-    load_digits<QT, LPR, CPL>(xs, cols, l, xd);
-    const bool in_place = epi == EPI_OPROJ ? oproj_in_place(p) : false;
-    float best_v = -INFINITY;
-    int best_r = 0x7FFFFFFF;
     constexpr int SPAN = LPR / U;  // lanes per entry after the reduce-scatter
     const int my_u = l / SPAN;
     const bool writer = (l % SPAN) == 0;
-
     const bool need_resid = epi_reads_residual(epi);
-    for (; g < ngroups; g += gstride) {
-        const SegSel sel = seg_select<NMAT>(p, g * RG);
-        // the writer lane's epilogue operands are read before the prefetch so
-        // that waiting for them does not wait for the prefetch too
-        const int r = (g * U + my_u) * RPW + sub;
-        const int rc = min(r, rows - 1);
-        float scl[NMAT];
+
+    // activations first, so that waiting for them does not wait for weights
+    const int cols = p.cols;
+    const bool norm = pro == PRO_RMSNORM;
+    XRegs xr;
+    x_load(p.x, p.norm_w, norm, cols, xr);
+    // first group: weights, then the writer lane's epilogue operands (row
+    // scale, residual), all requested before the prologue's first wait
+    Chunk w[U][NMAT][CPL];
+    float scl[NMAT], resid;
+    {
+        const int gc = min(g, ngroups - 1);
+        const SegSel sel = seg_select<NMAT>(p, gc * RG);
+        load_group<QT, LPR, CPL, U, NMAT>(sel, row_bytes, rows, gc, sub, l, w);
+        const int rc = min((gc * U + my_u) * RPW + sub, rows - 1);
 #pragma unroll
         for (int mi = 0; mi < NMAT; ++mi) scl[mi] = (mi == 0 ? sel.scale0 : sel.scale1)[rc - sel.start];
-        const float resid = need_resid ? p.residual[rc] : 0.0f;
+        resid = need_resid ? p.residual[rc] : 0.0f;
+    }
+    const float xscale = x_digits<QT>(xr, norm, cols, p.eps, lds, red);
+    XDigits<QT, CPL> xd;
+    load_digits<QT, LPR, CPL>(lds, l, xd);
+    const bool in_place = epi == EPI_OPROJ ? oproj_in_place(p) : false;
+    float best_v = -INFINITY;
+    int best_r = 0x7FFFFFFF;
+
+    for (; g < ngroups; g += gstride) {
+        // the next group's weights and epilogue operands are requested before
+        // this group is computed (software pipeline of depth one)
         Chunk wn[U][NMAT][CPL];
+        float scln[NMAT], residn;
         {
             const int gn = min(g + gstride, ngroups - 1);
-            load_group<QT, LPR, CPL, U, NMAT>(seg_select<NMAT>(p, gn * RG), row_bytes, rows, gn, sub, l, wn);
+            const SegSel seln = seg_select<NMAT>(p, gn * RG);
+            load_group<QT, LPR, CPL, U, NMAT>(seln, row_bytes, rows, gn, sub, l, wn);
+            const int rn = min((gn * U + my_u) * RPW + sub, rows - 1);
+#pragma unroll
+            for (int mi = 0; mi < NMAT; ++mi) scln[mi] = (mi == 0 ? seln.scale0 : seln.scale1)[rn - seln.start];
+            residn = need_resid ? p.residual[rn] : 0.0f;
         }
+        const int r = (g * U + my_u) * RPW + sub;
         float acc[8][NMAT];
 #pragma unroll
         for (int u = 0; u < U; ++u)
@@ -716,7 +799,7 @@ __global__ void __launch_bounds__(kThreads) k_gemv(GemvParams p, int pro, int ep
         if (writer && r < rows) {
             float s[NMAT];
 #pragma unroll
-            for (int mi = 0; mi < NMAT; ++mi) s[mi] = acc[0][mi] * scl[mi];
+            for (int mi = 0; mi < NMAT; ++mi) s[mi] = acc[0][mi] * xscale * scl[mi];
             gemv_epilogue(p, epi, r, s, resid, in_place, best_v, best_r);
         }
 #pragma unroll
@@ -725,6 +808,9 @@ __global__ void __launch_bounds__(kThreads) k_gemv(GemvParams p, int pro, int ep
             for (int mi = 0; mi < NMAT; ++mi)
 #pragma unroll
                 for (int j = 0; j < CPL; ++j) w[u][mi][j] = wn[u][mi][j];
+#pragma unroll
+        for (int mi = 0; mi < NMAT; ++mi) scl[mi] = scln[mi];
+        resid = residn;
     }
     if (epi == EPI_ARGMAX) argmax_finish(p, best_v, best_r, red);
 }
@@ -891,7 +977,7 @@ static __global__ void __launch_bounds__(kThreads) k_step_begin(StepState *st, c
 // (kvCache.append, model.go:5593-5612: row t at t·kvDim + g·128).  Scores for
 // all GROUP q heads share each K row (16 lanes × 8 dims per row, reduced by a
 // DPP reduce-scatter); the partial softmax (max, Σexp, Σexp·V) is written per
-// split and the last workgroup of a kv head merges the splits.  Scores:
+// split and k_attn_merge combines the splits.  Scores:
 // dot(q,k)·f32(1/√128) (model.go:4623-4795, 7391); softmax with FastExp
 // (ops.go:1199-1363); out = Σ p·V (model.go:5201-5590).
 // ---------------------------------------------------------------------------
@@ -912,9 +998,9 @@ struct AttnParams {
     const float *cos_t;    // op level tables
     const float *sin_t;
     float *part;           // [kvh][nsplit][GROUP][kRec]
-    unsigned int *counter; // [kvh]
     float *head_out;       // [heads*128]
     int heads, kvh, nsplit;
+    int rows_cap;          // rows the splits are cut from (cache capacity)
     float scale;
 };
 
@@ -930,40 +1016,36 @@ __device__ __forceinline__ float rs16_heads(float (&v)[8][1], int lane) {
 
 static __global__ void __launch_bounds__(kThreads) k_attn_decode(AttnParams p) {
     StepState *st = p.st;
-    if (st && st->err) return;
     __shared__ float qs[kMaxGroup][kHD];
     __shared__ float knew[kHD];
     __shared__ float vnew[kHD];
     __shared__ float sc[kMaxGroup][kMaxChunk];
     __shared__ float4 pv[8][kMaxGroup][kHD / 4];
     __shared__ float sm[kMaxGroup], sl[kMaxGroup];
-    __shared__ int s_last;
 
     const int g = blockIdx.x;  // kv head
     const int split = blockIdx.y;
     const int group = p.heads / p.kvh;
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
-    const int L = st ? st->len : p.len;
-    const int newest = st ? st->clen : -1;  // row appended by this step
-    const int rope = st ? st->has_rope : p.has_rope;
     const float *cos_t = st ? st->cos_t : p.cos_t;
     const float *sin_t = st ? st->sin_t : p.sin_t;
     const int kvd = p.kvh * kHD;
 
-    int chunk = (L + p.nsplit - 1) / p.nsplit;
+    // Splits are cut from the row capacity (a launch constant), so every
+    // request below is issued before the step state has arrived.
+    int chunk = (p.rows_cap + p.nsplit - 1) / p.nsplit;
     chunk = min((chunk + 15) & ~15, kMaxChunk);
     const int t0 = split * chunk;
-    const int t1 = min(L, t0 + chunk);
-    const int n = t1 - t0;  // may be <= 0: empty split
+    const int tmax = p.rows_cap - 1;
 
     // ---- 1. request the chunk's K rows (score layout) and V rows (PV layout)
     const int l16 = lane & 15;
     const int ts = wave * 4 + (lane >> 4);  // row slot of this 16-lane group
-    // Rows past the chunk are clamped to the last valid row (loaded, never
-    // used); the newest row's slot is refilled from LDS below.  Every lane
-    // issues the same loads, so the wait counts stay static.
-    const int tmax = L - 1;
+    // Rows past the capacity are clamped to the last row (loaded, never
+    // used); rows past the step's length are masked once it is known, and
+    // the newest row's slot is refilled from LDS below.  Every lane issues
+    // the same loads, so the wait counts stay static.
     float4 ka[4][2];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -980,33 +1062,62 @@ static __global__ void __launch_bounds__(kThreads) k_attn_decode(AttnParams p) {
         const int t = min(t0 + tg + 8 * j, tmax);
         va[j] = *reinterpret_cast<const float4 *>(p.vc + (size_t)t * kvd + g * kHD + d4);
     }
-
-    // ---- 2. rotated q of the group's heads; new K/V row (owner appends it)
-    for (int i = tid; i < group * (kHD / 2); i += kThreads) {
-        const int h = i / (kHD / 2), j = i % (kHD / 2);
+    // q pairs (j, j+64) of the group's heads, the new K/V row and the RoPE
+    // table entries of pair j = tid % 64
+    constexpr int QPT = kMaxGroup * (kHD / 2) / kThreads;
+    const int pj = tid & (kHD / 2 - 1);
+    float qa[QPT], qb[QPT];
+#pragma unroll
+    for (int k = 0; k < QPT; ++k) {
+        const int h = min((tid + k * kThreads) / (kHD / 2), group - 1);
         const float *qh = p.q + (size_t)(g * group + h) * kHD;
-        float a = qh[j], b = qh[j + kHD / 2];
-        if (rope) rope_pair(a, b, cos_t[j], sin_t[j]);
-        qs[h][j] = a;
-        qs[h][j + kHD / 2] = b;
+        qa[k] = qh[pj];
+        qb[k] = qh[pj + kHD / 2];
+    }
+    const float cj = cos_t ? cos_t[pj] : 1.0f;  // op level without RoPE passes no table
+    const float sj = sin_t ? sin_t[pj] : 0.0f;
+    float kn0 = 0.0f, kn1 = 0.0f, vn0 = 0.0f, vn1 = 0.0f;
+    if (p.k_new && tid < kHD / 2) {
+        const float *kh = p.k_new + (size_t)g * kHD;
+        const float *vh = p.v_new + (size_t)g * kHD;
+        kn0 = kh[tid];
+        kn1 = kh[tid + kHD / 2];
+        vn0 = vh[tid];
+        vn1 = vh[tid + kHD / 2];
+    }
+
+    // ---- 2. step state; rotated q; the owner of the newest row appends it
+    if (st && st->err) return;  // a failed step appends nothing
+    const int L = st ? st->len : p.len;
+    const int newest = st ? st->clen : -1;  // row appended by this step
+    const int rope = st ? st->has_rope : p.has_rope;
+    const int t1 = min(L, t0 + chunk);
+    const int n = t1 - t0;
+    if (n <= 0) return;  // split past the step's rows: the merge skips it
+#pragma unroll
+    for (int k = 0; k < QPT; ++k) {
+        const int h = (tid + k * kThreads) / (kHD / 2);
+        float a = qa[k], b2 = qb[k];
+        if (rope) rope_pair(a, b2, cj, sj);
+        if (h < group) {
+            qs[h][pj] = a;
+            qs[h][pj + kHD / 2] = b2;
+        }
     }
     const bool owns_new = newest >= t0 && newest < t1;
     if (owns_new && tid < kHD / 2) {
-        const float *kh = p.k_new + (size_t)g * kHD;
-        float a = kh[tid], b = kh[tid + kHD / 2];
-        if (rope) rope_pair(a, b, cos_t[tid], sin_t[tid]);
+        float a = kn0, b2 = kn1;
+        if (rope) rope_pair(a, b2, cj, sj);
         knew[tid] = a;
-        knew[tid + kHD / 2] = b;
-        const float *vh = p.v_new + (size_t)g * kHD;
-        const float va0 = vh[tid], va1 = vh[tid + kHD / 2];
-        vnew[tid] = va0;
-        vnew[tid + kHD / 2] = va1;
+        knew[tid + kHD / 2] = b2;
+        vnew[tid] = vn0;
+        vnew[tid + kHD / 2] = vn1;
         float *kd = p.kc + (size_t)newest * kvd + g * kHD;
         float *vd = p.vc + (size_t)newest * kvd + g * kHD;
         kd[tid] = a;
-        kd[tid + kHD / 2] = b;
-        vd[tid] = va0;
-        vd[tid + kHD / 2] = va1;
+        kd[tid + kHD / 2] = b2;
+        vd[tid] = vn0;
+        vd[tid + kHD / 2] = vn1;
     }
     __syncthreads();
     if (owns_new) {
@@ -1102,65 +1213,59 @@ static __global__ void __launch_bounds__(kThreads) k_attn_decode(AttnParams p) {
         }
         float *rh = rec + h * kRec;
         if (d4 == 0) {
-            rh[0] = n > 0 ? sm[h] : -INFINITY;
-            rh[1] = n > 0 ? sl[h] : 0.0f;
+            rh[0] = sm[h];
+            rh[1] = sl[h];
         }
         rh[2 + d4] = o.x;
         rh[3 + d4] = o.y;
         rh[4 + d4] = o.z;
         rh[5 + d4] = o.w;
     }
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) {
-        const unsigned int prev = atomicAdd(&p.counter[g], 1u);
-        s_last = prev == (unsigned int)(p.nsplit - 1);
-    }
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
+}
 
-    // ---- 7. last workgroup of kv head g merges the splits (online rescale)
-    if (h < group) {
-        const float *base = p.part + ((size_t)g * p.nsplit * kMaxGroup + h) * kRec;
-        float M = -INFINITY, lsum = 0.0f;
-        float o[4] = {0.f, 0.f, 0.f, 0.f};
-        constexpr int B = 8;
-        for (int s0 = 0; s0 < p.nsplit; s0 += B) {
-            float ms[B], ls[B], av[B][4];
+// Merge of the per-split partials (online softmax rescale), one workgroup per
+// q head, thread d owns output dim d.  A separate launch: the kernel boundary
+// orders the partial writes before these reads on every XCD.  Records of the
+// first batch are requested before the step state is read; splits at or past
+// the step's length hold stale records and are skipped.
+static __global__ void __launch_bounds__(kHD) k_attn_merge(AttnParams p) {
+    const int hq = blockIdx.x;  // q head
+    const int group = p.heads / p.kvh;
+    const int g = hq / group, h = hq % group;
+    const int d = threadIdx.x;
+    int chunk = (p.rows_cap + p.nsplit - 1) / p.nsplit;
+    chunk = min((chunk + 15) & ~15, kMaxChunk);
+    const float *base = p.part + ((size_t)g * p.nsplit * kMaxGroup + h) * kRec;
+    float M = -INFINITY, lsum = 0.0f, o = 0.0f;
+    constexpr int B = 32;
+    int used = p.nsplit;
+    for (int s0 = 0; s0 < used; s0 += B) {
+        float ms[B], ls[B], av[B];
 #pragma unroll
-            for (int b = 0; b < B; ++b) {
-                const int s = s0 + b;
-                if (s < p.nsplit) {
-                    const float *rs = base + (size_t)s * kMaxGroup * kRec;
-                    ms[b] = rs[0];
-                    ls[b] = rs[1];
-                    av[b][0] = rs[2 + d4];
-                    av[b][1] = rs[3 + d4];
-                    av[b][2] = rs[4 + d4];
-                    av[b][3] = rs[5 + d4];
-                } else {
-                    ls[b] = 0.0f;
-                }
-            }
-#pragma unroll
-            for (int b = 0; b < B; ++b) {
-                if (!(ls[b] > 0.0f)) continue;
-                const float Mn = fmaxf(M, ms[b]);
-                const float fo = fast_exp_ref(M - Mn);  // M = -inf → clamps to e^-87 ≈ 0 (lsum, o are 0)
-                const float fs = fast_exp_ref(ms[b] - Mn);
-                lsum = lsum * fo + ls[b] * fs;
-#pragma unroll
-                for (int c = 0; c < 4; ++c) o[c] = o[c] * fo + av[b][c] * fs;
-                M = Mn;
-            }
+        for (int b = 0; b < B; ++b) {
+            const int sidx = min(s0 + b, p.nsplit - 1);
+            const float *rs = base + (size_t)sidx * kMaxGroup * kRec;
+            ms[b] = rs[0];
+            ls[b] = rs[1];
+            av[b] = rs[2 + d];
         }
-        const float inv = 1.0f / lsum;
-        float *dst = p.head_out + (size_t)(g * group + h) * kHD + d4;
+        if (s0 == 0) {
+            if (p.st && p.st->err) return;
+            const int L = p.st ? p.st->len : p.len;
+            used = min(p.nsplit, (L + chunk - 1) / chunk);
+        }
 #pragma unroll
-        for (int c = 0; c < 4; ++c) dst[c] = o[c] * inv;
+        for (int b = 0; b < B; ++b) {
+            if (s0 + b >= used) break;
+            const float Mn = fmaxf(M, ms[b]);
+            const float fo = fast_exp_ref(M - Mn);  // M = -inf: clamps to ~e^-87, and lsum = o = 0
+            const float fs = fast_exp_ref(ms[b] - Mn);
+            lsum = lsum * fo + ls[b] * fs;
+            o = o * fo + av[b] * fs;
+            M = Mn;
+        }
     }
-    if (tid == 0) p.counter[g] = 0u;
+    p.head_out[(size_t)hq * kHD + d] = o * (1.0f / lsum);
 }
 
 // Attention for head dims other than 128 (small test shapes): one workgroup

@@ -69,7 +69,6 @@ pocr_seq::~pocr_seq() {
     free_dev(g);
     free_dev(logits);
     free_dev(part);
-    free_dev(counter);
     free_dev(st);
     free_dev(tokens);
     prefill_free(pf);
@@ -557,8 +556,6 @@ extern "C" int pocr_text_attention(pocr_ctx *ctx, const float *q, const float *k
     if (head_dim == kHD && group <= kMaxGroup) {
         const int nsplit = attn_nsplit(cache_len);
         RC(ctx->part.ensure((size_t)kv_heads * nsplit * kMaxGroup * kRec * 4));
-        RC(ctx->counter.ensure((size_t)kv_heads * 4));
-        HIP_TRY(hipMemsetAsync(ctx->counter.p, 0, (size_t)kv_heads * 4, s));
         AttnParams p{};
         p.q = ctx->x.as<float>();
         p.kc = ctx->kc.as<float>();
@@ -567,13 +564,14 @@ extern "C" int pocr_text_attention(pocr_ctx *ctx, const float *q, const float *k
         p.len = cache_len;
         p.has_rope = 0;
         p.part = ctx->part.as<float>();
-        p.counter = ctx->counter.as<unsigned int>();
         p.head_out = ctx->out.as<float>();
         p.heads = heads;
         p.kvh = kv_heads;
         p.nsplit = nsplit;
+        p.rows_cap = cache_len;
         p.scale = scale;
         hipLaunchKernelGGL(k_attn_decode, dim3(kv_heads, nsplit), dim3(kThreads), 0, s, p);
+        hipLaunchKernelGGL(k_attn_merge, dim3(heads), dim3(kHD), 0, s, p);
     } else {
         if ((size_t)cache_len * 4 > 60 * 1024) return fail(POCR_ERR_UNSUPPORTED, "text_attention: cache too long");
         hipLaunchKernelGGL(k_attn_small, dim3(heads), dim3(kThreads), (size_t)cache_len * 4, s, ctx->x.as<float>(),
@@ -766,10 +764,8 @@ extern "C" int pocr_seq_create(pocr_model *m, int capacity, pocr_seq **out) {
     if (e == hipSuccess) e = hipMalloc(&s->g, (size_t)c.intermediate * 4);
     if (e == hipSuccess) e = hipMalloc(&s->logits, (size_t)c.vocab * 4);
     if (e == hipSuccess) e = hipMalloc(&s->part, (size_t)c.kv_heads * s->nsplit * kMaxGroup * kRec * 4);
-    if (e == hipSuccess) e = hipMalloc(&s->counter, (size_t)c.kv_heads * 4);
     if (e == hipSuccess) e = hipMalloc(&s->st, sizeof(StepState));
     if (e == hipSuccess) e = hipMalloc(&s->tokens, (size_t)s->max_tokens * 4);
-    if (e == hipSuccess) e = hipMemset(s->counter, 0, (size_t)c.kv_heads * 4);
     if (e == hipSuccess) e = hipMemset(s->kv, 0, (size_t)c.layers * 2 * capacity * kvd * 4);
     if (e != hipSuccess) {
         delete s;
@@ -947,13 +943,14 @@ static int enqueue_layer(pocr_seq *s, int li, bool last, bool kv_only) {
     a.vc = layer_v(s, li);
     a.st = s->st;
     a.part = s->part;
-    a.counter = s->counter;
     a.head_out = s->head_out;
     a.heads = c.heads;
     a.kvh = c.kv_heads;
     a.nsplit = s->nsplit;
+    a.rows_cap = s->cap;
     a.scale = (float)(1.0 / std::sqrt((double)c.head_dim));
     hipLaunchKernelGGL(k_attn_decode, dim3(c.kv_heads, s->nsplit), dim3(kThreads), 0, st, a);
+    hipLaunchKernelGGL(k_attn_merge, dim3(c.heads), dim3(kHD), 0, st, a);
     HIP_TRY(hipGetLastError());
     if (kv_only) return POCR_OK;
 
