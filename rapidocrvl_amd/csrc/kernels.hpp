@@ -44,7 +44,7 @@ struct StepState {
     int32_t half;
     int32_t pad;
     unsigned long long argmax_key;
-    float cos_t[kMaxHalf];
+    alignas(16) float cos_t[kMaxHalf];
     float sin_t[kMaxHalf];
 };
 
@@ -970,20 +970,24 @@ static __global__ void __launch_bounds__(kThreads) k_step_begin(StepState *st, c
 // GQA decode attention, head_dim 128, split over cache rows.
 //
 // Workgroup (g, s) owns kv head g and cache rows [s·chunk, (s+1)·chunk),
-// chunk ≤ 64.  It requests every K and V row of its chunk up front (one
-// memory round trip: 2 + 8 16-byte loads per lane), rotates the q heads of its
-// group (and, in the split holding the newest row, the new k) with the step's
-// RoPE table and appends the new K/V row to the per-layer cache
-// (kvCache.append, model.go:5593-5612: row t at t·kvDim + g·128).  Scores for
-// all GROUP q heads share each K row (16 lanes × 8 dims per row, reduced by a
-// DPP reduce-scatter); the partial softmax (max, Σexp, Σexp·V) is written per
-// split and k_attn_merge combines the splits.  Scores:
-// dot(q,k)·f32(1/√128) (model.go:4623-4795, 7391); softmax with FastExp
-// (ops.go:1199-1363); out = Σ p·V (model.go:5201-5590).
+// chunk ≤ 64; wave w of it owns the 16 rows from s·chunk + 16w and is a
+// softmax split of its own.  Every request (the wave's K and V rows, the q
+// heads of the group, the RoPE table entries, the new K/V row) is issued
+// before the step state is read, in one memory round trip.  q (and the new k)
+// are rotated in registers: the pair (d, d+64) of RoPE sits in lanes l and
+// l^8 of a 16-lane row, one DPP rotate apart.  Scores for all GROUP q heads
+// share each K row (16 lanes × 8 dims per row, reduced by a DPP
+// reduce-scatter); the wave's softmax uses lane exchanges only, its
+// probabilities reach the P·V lanes through a wave-private LDS slot, and one
+// barrier combines the four waves into the split's record (max, Σexp,
+// Σexp·V), which k_attn_merge combines across splits.  The owner wave of the
+// newest row appends it (kvCache.append, model.go:5593-5612: row t at
+// t·kvDim + g·128).  Scores: dot(q,k)·f32(1/√128) (model.go:4623-4795, 7391);
+// softmax with FastExp (ops.go:1199-1363); out = Σ p·V (model.go:5201-5590).
 // ---------------------------------------------------------------------------
 constexpr int kHD = 128;
 constexpr int kMaxGroup = 8;
-constexpr int kMaxChunk = 64;  // cache rows per workgroup
+constexpr int kMaxChunk = 64;  // cache rows per workgroup (16 per wave)
 constexpr int kRec = kHD + 2;  // partial record per head: m, l, acc[128]
 
 struct AttnParams {
@@ -995,7 +999,7 @@ struct AttnParams {
     StepState *st;         // null → op level (len/rope from fields below)
     int len;               // op level: rows in cache (no append)
     int has_rope;          // op level
-    const float *cos_t;    // op level tables
+    const float *cos_t;    // op level tables (null: no RoPE)
     const float *sin_t;
     float *part;           // [kvh][nsplit][GROUP][kRec]
     float *head_out;       // [heads*128]
@@ -1004,8 +1008,14 @@ struct AttnParams {
     float scale;
 };
 
+__host__ __device__ constexpr int attn_chunk(int rows_cap, int nsplit) {
+    return ((rows_cap + nsplit - 1) / nsplit + 15) / 16 * 16 < kMaxChunk
+               ? ((rows_cap + nsplit - 1) / nsplit + 15) / 16 * 16
+               : kMaxChunk;
+}
+
 // reduce-scatter of 8 per-head partial dots over the 16 lanes of a row:
-// lane l16 with (l16 & 1) == 0 ends with head (l16 >> 1)'s full sum
+// lanes 2h and 2h+1 end with head h's full sum
 __device__ __forceinline__ float rs16_heads(float (&v)[8][1], int lane) {
     rs_step<8, 1, XM16, 8>(v, lane);
     rs_step<4, 1, XM8, 4>(v, lane);
@@ -1014,207 +1024,239 @@ __device__ __forceinline__ float rs16_heads(float (&v)[8][1], int lane) {
     return v[0][0];
 }
 
+// value of lane l ^ 8 within each row of 16 (DPP row_ror:8)
+__device__ __forceinline__ float xchg8(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false));
+}
+
+// RoPE of 8 consecutive dims held by a lane (rope_pair across lanes l, l^8):
+// lower half a' = a·cos − b·sin, upper half b' = b·cos + a·sin
+__device__ __forceinline__ void rope8(float (&v)[8], const float (&cs)[8], const float (&sn)[8], bool upper) {
+#pragma clang fp contract(off)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const float partner = xchg8(v[e]);
+        const float a = v[e] * cs[e];
+        const float b = partner * sn[e];
+        v[e] = upper ? a + b : a - b;
+    }
+}
+
+__device__ __forceinline__ void f4_to(float (&d)[8], const float4 &a, const float4 &b) {
+    d[0] = a.x; d[1] = a.y; d[2] = a.z; d[3] = a.w;
+    d[4] = b.x; d[5] = b.y; d[6] = b.z; d[7] = b.w;
+}
+
 static __global__ void __launch_bounds__(kThreads) k_attn_decode(AttnParams p) {
     StepState *st = p.st;
-    __shared__ float qs[kMaxGroup][kHD];
-    __shared__ float knew[kHD];
-    __shared__ float vnew[kHD];
-    __shared__ float sc[kMaxGroup][kMaxChunk];
-    __shared__ float4 pv[8][kMaxGroup][kHD / 4];
-    __shared__ float sm[kMaxGroup], sl[kMaxGroup];
+    __shared__ float4 e_lds[kWaves][kMaxGroup][4];      // wave-private probabilities [head][16 rows]
+    __shared__ float w_m[kWaves][kMaxGroup], w_l[kWaves][kMaxGroup];
+    __shared__ float2 w_acc[kWaves][kMaxGroup][kHD / 2];
 
     const int g = blockIdx.x;  // kv head
     const int split = blockIdx.y;
     const int group = p.heads / p.kvh;
     const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int l16 = lane & 15, rg = lane >> 4;
     const float *cos_t = st ? st->cos_t : p.cos_t;
     const float *sin_t = st ? st->sin_t : p.sin_t;
     const int kvd = p.kvh * kHD;
 
     // Splits are cut from the row capacity (a launch constant), so every
     // request below is issued before the step state has arrived.
-    int chunk = (p.rows_cap + p.nsplit - 1) / p.nsplit;
-    chunk = min((chunk + 15) & ~15, kMaxChunk);
+    const int chunk = attn_chunk(p.rows_cap, p.nsplit);
     const int t0 = split * chunk;
+    const int wr0 = t0 + 16 * wave;  // first row of this wave
     const int tmax = p.rows_cap - 1;
 
-    // ---- 1. request the chunk's K rows (score layout) and V rows (PV layout)
-    const int l16 = lane & 15;
-    const int ts = wave * 4 + (lane >> 4);  // row slot of this 16-lane group
-    // Rows past the capacity are clamped to the last row (loaded, never
-    // used); rows past the step's length are masked once it is known, and
-    // the newest row's slot is refilled from LDS below.  Every lane issues
-    // the same loads, so the wait counts stay static.
-    float4 ka[4][2];
+    // ---- 1. requests.  Rows past the capacity are clamped to the last row
+    // (loaded, masked below); every lane issues the same loads.
+    float4 ka[4][2];  // K, score layout: pass j → row wr0 + 4j + rg, dims 8·l16..
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const int t = min(t0 + ts + 16 * j, tmax);
+        const int t = min(wr0 + 4 * j + rg, tmax);
         const float4 *src = reinterpret_cast<const float4 *>(p.kc + (size_t)t * kvd + g * kHD + 8 * l16);
         ka[j][0] = src[0];
         ka[j][1] = src[1];
     }
-    const int tg = tid >> 5;          // PV row slot 0..7
-    const int d4 = (tid & 31) * 4;    // PV dims d4..d4+3
-    float4 va[8];
+    float2 va[16];  // V, P·V layout: row wr0 + i, dims 2·lane, 2·lane+1
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const int t = min(t0 + tg + 8 * j, tmax);
-        va[j] = *reinterpret_cast<const float4 *>(p.vc + (size_t)t * kvd + g * kHD + d4);
+    for (int i = 0; i < 16; ++i) {
+        const int t = min(wr0 + i, tmax);
+        va[i] = *reinterpret_cast<const float2 *>(p.vc + (size_t)t * kvd + g * kHD + 2 * lane);
     }
-    // q pairs (j, j+64) of the group's heads, the new K/V row and the RoPE
-    // table entries of pair j = tid % 64
-    constexpr int QPT = kMaxGroup * (kHD / 2) / kThreads;
-    const int pj = tid & (kHD / 2 - 1);
-    float qa[QPT], qb[QPT];
+    float4 qr[kMaxGroup][2];
 #pragma unroll
-    for (int k = 0; k < QPT; ++k) {
-        const int h = min((tid + k * kThreads) / (kHD / 2), group - 1);
-        const float *qh = p.q + (size_t)(g * group + h) * kHD;
-        qa[k] = qh[pj];
-        qb[k] = qh[pj + kHD / 2];
+    for (int h = 0; h < kMaxGroup; ++h) {
+        if (h < group) {  // uniform
+            const float4 *src = reinterpret_cast<const float4 *>(p.q + (size_t)(g * group + h) * kHD + 8 * l16);
+            qr[h][0] = src[0];
+            qr[h][1] = src[1];
+        } else {
+            qr[h][0] = qr[h][1] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
     }
-    const float cj = cos_t ? cos_t[pj] : 1.0f;  // op level without RoPE passes no table
-    const float sj = sin_t ? sin_t[pj] : 0.0f;
-    float kn0 = 0.0f, kn1 = 0.0f, vn0 = 0.0f, vn1 = 0.0f;
-    if (p.k_new && tid < kHD / 2) {
-        const float *kh = p.k_new + (size_t)g * kHD;
-        const float *vh = p.v_new + (size_t)g * kHD;
-        kn0 = kh[tid];
-        kn1 = kh[tid + kHD / 2];
-        vn0 = vh[tid];
-        vn1 = vh[tid + kHD / 2];
+    float cs[8], sn[8];
+    if (cos_t) {
+        const int tb = (8 * l16) & (kHD / 2 - 1);
+        const float4 *cp = reinterpret_cast<const float4 *>(cos_t + tb);
+        const float4 *sp = reinterpret_cast<const float4 *>(sin_t + tb);
+        f4_to(cs, cp[0], cp[1]);
+        f4_to(sn, sp[0], sp[1]);
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            cs[e] = 1.0f;
+            sn[e] = 0.0f;
+        }
+    }
+    float4 kn[2] = {make_float4(0.f, 0.f, 0.f, 0.f), make_float4(0.f, 0.f, 0.f, 0.f)};
+    float2 vn = make_float2(0.f, 0.f);
+    if (p.k_new) {
+        const float4 *kp = reinterpret_cast<const float4 *>(p.k_new + (size_t)g * kHD + 8 * l16);
+        kn[0] = kp[0];
+        kn[1] = kp[1];
+        vn = *reinterpret_cast<const float2 *>(p.v_new + (size_t)g * kHD + 2 * lane);
     }
 
-    // ---- 2. step state; rotated q; the owner of the newest row appends it
+    // ---- 2. step state
     if (st && st->err) return;  // a failed step appends nothing
     const int L = st ? st->len : p.len;
     const int newest = st ? st->clen : -1;  // row appended by this step
     const int rope = st ? st->has_rope : p.has_rope;
     const int t1 = min(L, t0 + chunk);
-    const int n = t1 - t0;
-    if (n <= 0) return;  // split past the step's rows: the merge skips it
+    if (t1 <= t0) return;  // split past the step's rows: the merge skips it
+    const bool upper = l16 >= 8;
+
+    // ---- 3. rotated q; the owner wave rotates and appends the newest row
+    float q[kMaxGroup][8];
 #pragma unroll
-    for (int k = 0; k < QPT; ++k) {
-        const int h = (tid + k * kThreads) / (kHD / 2);
-        float a = qa[k], b2 = qb[k];
-        if (rope) rope_pair(a, b2, cj, sj);
-        if (h < group) {
-            qs[h][pj] = a;
-            qs[h][pj + kHD / 2] = b2;
+    for (int h = 0; h < kMaxGroup; ++h) {
+        f4_to(q[h], qr[h][0], qr[h][1]);
+        if (rope && h < group) rope8(q[h], cs, sn, upper);
+    }
+    if (newest >= wr0 && newest < wr0 + 16 && newest < t1) {  // uniform per wave
+        float k8[8];
+        f4_to(k8, kn[0], kn[1]);
+        if (rope) rope8(k8, cs, sn, upper);
+        const int i = newest - wr0;
+        if (rg == (i & 3)) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                if (j == (i >> 2)) {
+                    ka[j][0] = make_float4(k8[0], k8[1], k8[2], k8[3]);
+                    ka[j][1] = make_float4(k8[4], k8[5], k8[6], k8[7]);
+                }
         }
-    }
-    const bool owns_new = newest >= t0 && newest < t1;
-    if (owns_new && tid < kHD / 2) {
-        float a = kn0, b2 = kn1;
-        if (rope) rope_pair(a, b2, cj, sj);
-        knew[tid] = a;
-        knew[tid + kHD / 2] = b2;
-        vnew[tid] = vn0;
-        vnew[tid + kHD / 2] = vn1;
-        float *kd = p.kc + (size_t)newest * kvd + g * kHD;
-        float *vd = p.vc + (size_t)newest * kvd + g * kHD;
-        kd[tid] = a;
-        kd[tid + kHD / 2] = b2;
-        vd[tid] = vn0;
-        vd[tid + kHD / 2] = vn1;
-    }
-    __syncthreads();
-    if (owns_new) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-            if (t0 + ts + 16 * j == newest) {
-                ka[j][0] = make_float4(knew[8 * l16], knew[8 * l16 + 1], knew[8 * l16 + 2], knew[8 * l16 + 3]);
-                ka[j][1] = make_float4(knew[8 * l16 + 4], knew[8 * l16 + 5], knew[8 * l16 + 6], knew[8 * l16 + 7]);
-            }
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-            if (t0 + tg + 8 * j == newest) va[j] = make_float4(vnew[d4], vnew[d4 + 1], vnew[d4 + 2], vnew[d4 + 3]);
+        for (int ii = 0; ii < 16; ++ii)
+            if (ii == i) va[ii] = vn;
+        if (rg == 0) {
+            float4 *kd = reinterpret_cast<float4 *>(p.kc + (size_t)newest * kvd + g * kHD + 8 * l16);
+            kd[0] = make_float4(k8[0], k8[1], k8[2], k8[3]);
+            kd[1] = make_float4(k8[4], k8[5], k8[6], k8[7]);
+        }
+        *reinterpret_cast<float2 *>(p.vc + (size_t)newest * kvd + g * kHD + 2 * lane) = vn;
     }
 
-    // ---- 3. scores
-    {
-        float qv[kMaxGroup][8];
+    // ---- 4. scores; lanes 2h, 2h+1 of each 16-lane row hold head h's score
+    const int hs = l16 >> 1;  // this lane's head after the reduce-scatter
+    float sj[4];
+    bool ok[4];
 #pragma unroll
-        for (int h = 0; h < kMaxGroup; ++h)
+    for (int j = 0; j < 4; ++j) {
+        float kv[8];
+        f4_to(kv, ka[j][0], ka[j][1]);
+        float part[8][1];
 #pragma unroll
-            for (int d = 0; d < 8; ++d) qv[h][d] = h < group ? qs[h][8 * l16 + d] : 0.0f;
+        for (int h = 0; h < kMaxGroup; ++h) {
+            float a = 0.0f;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            if (t0 + 16 * j >= t1) break;  // uniform across the workgroup
-            const float kv[8] = {ka[j][0].x, ka[j][0].y, ka[j][0].z, ka[j][0].w,
-                                 ka[j][1].x, ka[j][1].y, ka[j][1].z, ka[j][1].w};
-            float part[8][1];
+            for (int d = 0; d < 8; ++d) a = fmaf(q[h][d], kv[d], a);
+            part[h][0] = a;
+        }
+        const float sdot = rs16_heads(part, lane);
+        ok[j] = wr0 + 4 * j + rg < t1;
+        sj[j] = sdot * p.scale;
+    }
+
+    // ---- 5. the wave's softmax per head (rows of head hs: 4 passes × 4 lane rows)
+    float m = -INFINITY;
 #pragma unroll
-            for (int h = 0; h < kMaxGroup; ++h) {
-                float a = 0.0f;
+    for (int j = 0; j < 4; ++j) m = ok[j] ? fmaxf(m, sj[j]) : m;
+    m = fmaxf(m, xchg<XS16>(m));
+    m = fmaxf(m, xchg<XS32>(m));
+    float ej[4], lsum = 0.0f;
 #pragma unroll
-                for (int d = 0; d < 8; ++d) a = fmaf(qv[h][d], kv[d], a);
-                part[h][0] = a;
-            }
-            const float sdot = rs16_heads(part, lane);
-            const int hs = l16 >> 1;
-            const int t = t0 + ts + 16 * j;
-            if ((l16 & 1) == 0 && t < t1 && hs < group) sc[hs][t - t0] = sdot * p.scale;
+    for (int j = 0; j < 4; ++j) {
+        ej[j] = ok[j] ? fast_exp_ref(sj[j] - m) : 0.0f;
+        lsum += ej[j];
+    }
+    lsum += xchg<XS16>(lsum);
+    lsum += xchg<XS32>(lsum);
+    float *erow = reinterpret_cast<float *>(&e_lds[wave][0][0]);
+    if ((l16 & 1) == 0 && hs < group) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) erow[hs * 16 + 4 * j + rg] = ej[j];
+        if (rg == 0) {
+            w_m[wave][hs] = m;
+            w_l[wave][hs] = lsum;
         }
     }
-    __syncthreads();
+    // the wave reads back what its own lanes wrote: LDS keeps a wave's
+    // accesses in order, the fence keeps the compiler from reordering them
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
 
-    // ---- 4. partial softmax per head (wave w: heads w and w+4)
-    for (int h = wave; h < group; h += kWaves) {
-        const float sv = lane < n ? sc[h][lane] : -INFINITY;
-        float m = sv;
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
-        const float e = lane < n ? fast_exp_ref(sv - m) : 0.0f;
-        if (lane < n) sc[h][lane] = e;
-        float sum = e;
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
-        if (lane == 0) {
-            sm[h] = m;
-            sl[h] = sum;
-        }
-    }
-    __syncthreads();
-
-    // ---- 5. Σ e·V over this thread's rows for every head → LDS
+    // ---- 6. Σ e·V for every head over the wave's 16 rows (2 dims per lane)
 #pragma unroll
     for (int h = 0; h < kMaxGroup; ++h) {
         if (h >= group) break;
-        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+        float ev[16];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int i = tg + 8 * j;
-            if (i < n) {
-                const float e = sc[h][i];
-                acc.x = fmaf(e, va[j].x, acc.x);
-                acc.y = fmaf(e, va[j].y, acc.y);
-                acc.z = fmaf(e, va[j].z, acc.z);
-                acc.w = fmaf(e, va[j].w, acc.w);
-            }
+        for (int k = 0; k < 4; ++k) {
+            const float4 t = e_lds[wave][h][k];
+            ev[4 * k] = t.x;
+            ev[4 * k + 1] = t.y;
+            ev[4 * k + 2] = t.z;
+            ev[4 * k + 3] = t.w;
         }
-        pv[tg][h][d4 / 4] = acc;
+        float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            a0 = fmaf(ev[i], va[i].x, a0);
+            a1 = fmaf(ev[i], va[i].y, a1);
+        }
+        w_acc[wave][h][lane] = make_float2(a0, a1);
     }
     __syncthreads();
 
-    // ---- 6. partial record [m, l, acc[128]] per head
-    const int h = tid >> 5;
-    float *rec = p.part + ((size_t)(g * p.nsplit + split) * kMaxGroup) * kRec;
+    // ---- 7. combine the four waves → the split's record per head
+    const int h = tid >> 5;          // head
+    const int d4 = (tid & 31) * 4;   // dims d4..d4+3
     if (h < group) {
+        float M = w_m[0][h];
+#pragma unroll
+        for (int w = 1; w < kWaves; ++w) M = fmaxf(M, w_m[w][h]);  // finite: wave 0 holds row t0
+        float lt = 0.0f;
         float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            const float4 a = pv[k][h][d4 / 4];
-            o.x += a.x;
-            o.y += a.y;
-            o.z += a.z;
-            o.w += a.w;
+        for (int w = 0; w < kWaves; ++w) {
+            const float mw = w_m[w][h];
+            const float f = mw == -INFINITY ? 0.0f : fast_exp_ref(mw - M);
+            lt = fmaf(f, w_l[w][h], lt);
+            const float2 a = w_acc[w][h][d4 / 2];
+            const float2 b = w_acc[w][h][d4 / 2 + 1];
+            o.x = fmaf(f, a.x, o.x);
+            o.y = fmaf(f, a.y, o.y);
+            o.z = fmaf(f, b.x, o.z);
+            o.w = fmaf(f, b.y, o.w);
         }
-        float *rh = rec + h * kRec;
+        float *rh = p.part + ((size_t)(g * p.nsplit + split) * kMaxGroup + h) * kRec;
         if (d4 == 0) {
-            rh[0] = sm[h];
-            rh[1] = sl[h];
+            rh[0] = M;
+            rh[1] = lt;
         }
         rh[2 + d4] = o.x;
         rh[3 + d4] = o.y;
@@ -1223,47 +1265,48 @@ static __global__ void __launch_bounds__(kThreads) k_attn_decode(AttnParams p) {
     }
 }
 
-// Merge of the per-split partials (online softmax rescale), one workgroup per
-// q head, thread d owns output dim d.  A separate launch: the kernel boundary
-// orders the partial writes before these reads on every XCD.  Records of the
-// first batch are requested before the step state is read; splits at or past
-// the step's length hold stale records and are skipped.
+// Merge of the per-split records, one workgroup per q head, thread d owns
+// output dim d: M = max m_s, out = Σ e_s·acc_s / Σ e_s·l_s with
+// e_s = FastExp(m_s − M).  A separate launch: the kernel boundary orders the
+// record writes before these reads on every XCD.  The first batch of records
+// is requested before the step state is read; splits at or past the step's
+// length hold stale records and are skipped.
 static __global__ void __launch_bounds__(kHD) k_attn_merge(AttnParams p) {
     const int hq = blockIdx.x;  // q head
     const int group = p.heads / p.kvh;
     const int g = hq / group, h = hq % group;
     const int d = threadIdx.x;
-    int chunk = (p.rows_cap + p.nsplit - 1) / p.nsplit;
-    chunk = min((chunk + 15) & ~15, kMaxChunk);
+    const int chunk = attn_chunk(p.rows_cap, p.nsplit);
     const float *base = p.part + ((size_t)g * p.nsplit * kMaxGroup + h) * kRec;
-    float M = -INFINITY, lsum = 0.0f, o = 0.0f;
     constexpr int B = 32;
-    int used = p.nsplit;
-    for (int s0 = 0; s0 < used; s0 += B) {
-        float ms[B], ls[B], av[B];
+    auto rec = [&](int sidx) { return base + (size_t)sidx * kMaxGroup * kRec; };
+    float ms[B], ls[B], av[B];
 #pragma unroll
-        for (int b = 0; b < B; ++b) {
-            const int sidx = min(s0 + b, p.nsplit - 1);
-            const float *rs = base + (size_t)sidx * kMaxGroup * kRec;
-            ms[b] = rs[0];
-            ls[b] = rs[1];
-            av[b] = rs[2 + d];
-        }
-        if (s0 == 0) {
-            if (p.st && p.st->err) return;
-            const int L = p.st ? p.st->len : p.len;
-            used = min(p.nsplit, (L + chunk - 1) / chunk);
-        }
+    for (int b = 0; b < B; ++b) {
+        const float *r = rec(min(b, p.nsplit - 1));
+        ms[b] = r[0];
+        ls[b] = r[1];
+        av[b] = r[2 + d];
+    }
+    if (p.st && p.st->err) return;
+    const int L = p.st ? p.st->len : p.len;
+    const int used = min(p.nsplit, (L + chunk - 1) / chunk);  // ≥ 1 for L ≥ 1
+    float M = -INFINITY;
 #pragma unroll
-        for (int b = 0; b < B; ++b) {
-            if (s0 + b >= used) break;
-            const float Mn = fmaxf(M, ms[b]);
-            const float fo = fast_exp_ref(M - Mn);  // M = -inf: clamps to ~e^-87, and lsum = o = 0
-            const float fs = fast_exp_ref(ms[b] - Mn);
-            lsum = lsum * fo + ls[b] * fs;
-            o = o * fo + av[b] * fs;
-            M = Mn;
-        }
+    for (int b = 0; b < B; ++b) M = b < used ? fmaxf(M, ms[b]) : M;
+    for (int s = B; s < used; ++s) M = fmaxf(M, rec(s)[0]);
+    float lsum = 0.0f, o = 0.0f;
+#pragma unroll
+    for (int b = 0; b < B; ++b) {
+        const float e = b < used ? fast_exp_ref(ms[b] - M) : 0.0f;
+        lsum = fmaf(e, ls[b], lsum);
+        o = fmaf(e, av[b], o);
+    }
+    for (int s = B; s < used; ++s) {
+        const float *r = rec(s);
+        const float e = fast_exp_ref(r[0] - M);
+        lsum = fmaf(e, r[1], lsum);
+        o = fmaf(e, r[2 + d], o);
     }
     p.head_out[(size_t)hq * kHD + d] = o * (1.0f / lsum);
 }
