@@ -775,13 +775,31 @@ __global__ void __launch_bounds__(kThreads) k_gemv(GemvParams p, int pro, int ep
     float best_v = -INFINITY;
     int best_r = 0x7FFFFFFF;
 
-    for (; g < ngroups; g += gstride) {
-        // the next group's weights and epilogue operands are requested before
-        // this group is computed (software pipeline of depth one)
+    // one group: row sums, reduce-scatter, epilogue by the writer lanes
+    auto compute = [&](int gg, const Chunk (&wc)[U][NMAT][CPL], const float (&sc)[NMAT], float rs) {
+        const int r = (gg * U + my_u) * RPW + sub;
+        float acc[8][NMAT];
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int mi = 0; mi < NMAT; ++mi) acc[u][mi] = row_dot<QT, CPL>(wc[u][mi], xd);
+        reduce_scatter<LPR, U, NMAT>(acc, lane);
+        if (writer && r < rows) {
+            float sv[NMAT];
+#pragma unroll
+            for (int mi = 0; mi < NMAT; ++mi) sv[mi] = acc[0][mi] * xscale * sc[mi];
+            gemv_epilogue(p, epi, r, sv, rs, in_place, best_v, best_r);
+        }
+    };
+    // Every group but a wave's last requests its successor's weights and
+    // epilogue operands before it is computed (software pipeline of depth
+    // one); the last one is peeled off, so no wave requests rows it does not
+    // use and every path keeps static wait counts.
+    for (; g + gstride < ngroups; g += gstride) {
         Chunk wn[U][NMAT][CPL];
         float scln[NMAT], residn;
         {
-            const int gn = min(g + gstride, ngroups - 1);
+            const int gn = g + gstride;
             const SegSel seln = seg_select<NMAT>(p, gn * RG);
             load_group<QT, LPR, CPL, U, NMAT>(seln, row_bytes, rows, gn, sub, l, wn);
             const int rn = min((gn * U + my_u) * RPW + sub, rows - 1);
@@ -789,19 +807,7 @@ __global__ void __launch_bounds__(kThreads) k_gemv(GemvParams p, int pro, int ep
             for (int mi = 0; mi < NMAT; ++mi) scln[mi] = (mi == 0 ? seln.scale0 : seln.scale1)[rn - seln.start];
             residn = need_resid ? p.residual[rn] : 0.0f;
         }
-        const int r = (g * U + my_u) * RPW + sub;
-        float acc[8][NMAT];
-#pragma unroll
-        for (int u = 0; u < U; ++u)
-#pragma unroll
-            for (int mi = 0; mi < NMAT; ++mi) acc[u][mi] = row_dot<QT, CPL>(w[u][mi], xd);
-        reduce_scatter<LPR, U, NMAT>(acc, lane);
-        if (writer && r < rows) {
-            float s[NMAT];
-#pragma unroll
-            for (int mi = 0; mi < NMAT; ++mi) s[mi] = acc[0][mi] * xscale * scl[mi];
-            gemv_epilogue(p, epi, r, s, resid, in_place, best_v, best_r);
-        }
+        compute(g, w, scl, resid);
 #pragma unroll
         for (int u = 0; u < U; ++u)
 #pragma unroll
@@ -812,6 +818,7 @@ __global__ void __launch_bounds__(kThreads) k_gemv(GemvParams p, int pro, int ep
         for (int mi = 0; mi < NMAT; ++mi) scl[mi] = scln[mi];
         resid = residn;
     }
+    if (g < ngroups) compute(g, w, scl, resid);
     if (epi == EPI_ARGMAX) argmax_finish(p, best_v, best_r, red);
 }
 
@@ -1265,50 +1272,74 @@ static __global__ void __launch_bounds__(kThreads) k_attn_decode(AttnParams p) {
     }
 }
 
-// Merge of the per-split records, one workgroup per q head, thread d owns
-// output dim d: M = max m_s, out = Σ e_s·acc_s / Σ e_s·l_s with
-// e_s = FastExp(m_s − M).  A separate launch: the kernel boundary orders the
-// record writes before these reads on every XCD.  The first batch of records
-// is requested before the step state is read; splits at or past the step's
-// length hold stale records and are skipped.
+// Merge of the per-split records, one workgroup per q head (two waves),
+// thread d owns output dim d: M = max m_s, out = Σ e_s·acc_s / Σ e_s·l_s with
+// e_s = FastExp(m_s − M).  Wave 0 computes the split weights lane-parallel
+// (lane = split) and hands them over in LDS.  A separate launch: the kernel
+// boundary orders the record writes before these reads on every XCD.  The
+// first batch of records is requested before the step state is read; splits
+// at or past the step's length hold stale records and are skipped.
+constexpr int kMaxSplits = 1024;  // cache capacity ≤ 65536 rows
+
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, xchg<XQ1>(v));
+    v = fmaxf(v, xchg<XQ2>(v));
+    v = fmaxf(v, xchg<XM8>(v));
+    v = fmaxf(v, xchg<XM16>(v));
+    v = fmaxf(v, xchg<XS16>(v));
+    v = fmaxf(v, xchg<XS32>(v));
+    return v;
+}
+
 static __global__ void __launch_bounds__(kHD) k_attn_merge(AttnParams p) {
+    __shared__ float e_lds[kMaxSplits];
+    __shared__ float l_lds;
     const int hq = blockIdx.x;  // q head
     const int group = p.heads / p.kvh;
     const int g = hq / group, h = hq % group;
-    const int d = threadIdx.x;
+    const int d = threadIdx.x, lane = d & 63;
+    const bool wave0 = d < 64;
     const int chunk = attn_chunk(p.rows_cap, p.nsplit);
     const float *base = p.part + ((size_t)g * p.nsplit * kMaxGroup + h) * kRec;
-    constexpr int B = 32;
     auto rec = [&](int sidx) { return base + (size_t)sidx * kMaxGroup * kRec; };
-    float ms[B], ls[B], av[B];
+    constexpr int B = 32;  // acc values requested up front
+    float av[B];
 #pragma unroll
-    for (int b = 0; b < B; ++b) {
-        const float *r = rec(min(b, p.nsplit - 1));
-        ms[b] = r[0];
-        ls[b] = r[1];
-        av[b] = r[2 + d];
+    for (int b = 0; b < B; ++b) av[b] = rec(min(b, p.nsplit - 1))[2 + d];
+    float m0 = 0.0f, l0 = 0.0f;
+    if (wave0) {
+        const float *r = rec(min(lane, p.nsplit - 1));
+        m0 = r[0];
+        l0 = r[1];
     }
     if (p.st && p.st->err) return;
     const int L = p.st ? p.st->len : p.len;
     const int used = min(p.nsplit, (L + chunk - 1) / chunk);  // ≥ 1 for L ≥ 1
-    float M = -INFINITY;
-#pragma unroll
-    for (int b = 0; b < B; ++b) M = b < used ? fmaxf(M, ms[b]) : M;
-    for (int s = B; s < used; ++s) M = fmaxf(M, rec(s)[0]);
-    float lsum = 0.0f, o = 0.0f;
-#pragma unroll
-    for (int b = 0; b < B; ++b) {
-        const float e = b < used ? fast_exp_ref(ms[b] - M) : 0.0f;
-        lsum = fmaf(e, ls[b], lsum);
-        o = fmaf(e, av[b], o);
+    if (wave0) {  // split weights, lane s + 64k ↔ split
+        float M = lane < used ? m0 : -INFINITY;
+        for (int s = 64 + lane; s - lane < used; s += 64) M = fmaxf(M, s < used ? rec(s)[0] : -INFINITY);
+        M = wave_max(M);
+        float ls = 0.0f;
+        for (int s = lane; s - lane < used; s += 64) {
+            float e = 0.0f, lv = 0.0f;
+            if (s < used) {
+                const float ms = s < 64 ? m0 : rec(s)[0];
+                lv = s < 64 ? l0 : rec(s)[1];
+                e = fast_exp_ref(ms - M);
+                e_lds[s] = e;
+            }
+            ls = fmaf(e, lv, ls);
+        }
+        ls = wave_sum(ls);
+        if (lane == 0) l_lds = ls;
     }
-    for (int s = B; s < used; ++s) {
-        const float *r = rec(s);
-        const float e = fast_exp_ref(r[0] - M);
-        lsum = fmaf(e, r[1], lsum);
-        o = fmaf(e, r[2 + d], o);
-    }
-    p.head_out[(size_t)hq * kHD + d] = o * (1.0f / lsum);
+    __syncthreads();
+    float o = 0.0f;
+#pragma unroll
+    for (int b = 0; b < B; ++b)
+        if (b < used) o = fmaf(e_lds[b], av[b], o);
+    for (int s = B; s < used; ++s) o = fmaf(e_lds[s], rec(s)[2 + d], o);
+    p.head_out[(size_t)hq * kHD + d] = o * (1.0f / l_lds);
 }
 
 // Attention for head dims other than 128 (small test shapes): one workgroup

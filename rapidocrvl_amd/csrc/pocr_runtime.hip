@@ -555,6 +555,7 @@ extern "C" int pocr_text_attention(pocr_ctx *ctx, const float *q, const float *k
     const int group = heads / kv_heads;
     if (head_dim == kHD && group <= kMaxGroup) {
         const int nsplit = attn_nsplit(cache_len);
+        if (nsplit > kMaxSplits) return fail(POCR_ERR_UNSUPPORTED, "text_attention: cache above %d rows", kMaxSplits * kMaxChunk);
         RC(ctx->part.ensure((size_t)kv_heads * nsplit * kMaxGroup * kRec * 4));
         AttnParams p{};
         p.q = ctx->x.as<float>();
@@ -752,6 +753,12 @@ extern "C" int pocr_seq_create(pocr_model *m, int capacity, pocr_seq **out) {
     s->m = m;
     s->cap = capacity;
     s->nsplit = attn_nsplit(capacity);
+    if (s->nsplit > kMaxSplits) {
+        delete s;
+        m->refs.fetch_sub(1);
+        return fail(POCR_ERR_UNSUPPORTED, "pocr_seq_create: capacity %d above %d rows", capacity,
+                    kMaxSplits * kMaxChunk);
+    }
     s->max_tokens = capacity + 1;
     const size_t kvd = (size_t)c.kv_heads * c.head_dim;
     const size_t q_rows = (size_t)c.heads * c.head_dim;
