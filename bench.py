@@ -106,6 +106,73 @@ def gemv_sweep(ctx, rng):
     return out
 
 
+def lm_head_q4(cfg, seed=0):
+    """The Q4 LM head of the synthetic 0.3B weights (same draw as make_weights)."""
+    from rapidocrvl_amd import lib, synth
+
+    lm = synth.normal((cfg.vocab, cfg.hidden), [seed, 1000, 0])
+    s, p = lib.quantize_rows(lib.Q4, lm)
+    return lib.QMatrix(lib.Q4, cfg.vocab, cfg.hidden, s, p)
+
+
+def lm_head_roofline(ctx, lmq):
+    us, wbytes = gemv_rotation(ctx, lmq)
+    alg = wbytes + 4 * (lmq.rows + lmq.cols)
+    return us, alg, alg / us / 1e3
+
+
+def measured_traffic():
+    """HBM bytes per launch of the roofline kernel, from the committed
+    rocprofv3 FETCH_SIZE/WRITE_SIZE passes (scaled by the copy-kernel factor)."""
+    path = os.path.join(ROOT, "profiles", "lm_head_q4_traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get("traffic_bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def copy_calibration(nbytes=512 << 20, reps=3):
+    """A plain device copy of known size (read nbytes, write nbytes): the
+    reference point that scales the FETCH_SIZE/WRITE_SIZE counters.  HIP's own
+    device-to-device copy (the runtime's blit kernel) is used through ctypes."""
+    import ctypes
+
+    hip = ctypes.CDLL("libamdhip64.so")
+    src, dst = ctypes.c_void_p(), ctypes.c_void_p()
+    for ptr in (src, dst):
+        if hip.hipMalloc(ctypes.byref(ptr), ctypes.c_size_t(nbytes)) != 0:
+            raise RuntimeError("hipMalloc failed")
+    try:
+        if hip.hipMemset(src, 1, ctypes.c_size_t(nbytes)) != 0:
+            raise RuntimeError("hipMemset failed")
+        for _ in range(reps):
+            if hip.hipMemcpy(dst, src, ctypes.c_size_t(nbytes), 3) != 0:  # hipMemcpyDeviceToDevice
+                raise RuntimeError("hipMemcpy failed")
+        hip.hipDeviceSynchronize()
+    finally:
+        hip.hipFree(src)
+        hip.hipFree(dst)
+    log(f"[bench] copy calibration: {reps} device copies of {nbytes} bytes")
+
+
+def roofline_only(args):
+    """Only the roofline kernel: the Q4 LM-head GEMV rotation (the command the
+    committed rocprofv3 summaries profile)."""
+    from rapidocrvl_amd import lib
+    from rapidocrvl_amd.config import ERNIE_0P3B as cfg
+
+    ctx = lib.Context(0)
+    lmq = lm_head_q4(cfg)
+    us, alg, achieved = lm_head_roofline(ctx, lmq)
+    log(f"[bench] q4 lm_head gemv {us:.2f} us → {achieved:.0f} GB/s")
+    if args.calibrate_copy:
+        copy_calibration()
+    print(json.dumps({"kernel": "q4 lm_head gemv 103424x1024 m=1", "us_per_launch": round(us, 3),
+                      "algorithmic_bytes": int(alg), "achieved_GB_s": round(achieved, 1),
+                      "frac": round(achieved / HBM_PEAK_GBS, 4)}), flush=True)
+
+
 def cpu_baseline(cfg, weights, gpu_seq, first_tok, first_pos, gpu_tokens, n_prefix, budget_s=12.0):
     import oracle
 
@@ -144,11 +211,16 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-q8", action="store_true")
+    ap.add_argument("--roofline-only", action="store_true", help="time only the Q4 LM-head GEMV rotation")
+    ap.add_argument("--calibrate-copy", action="store_true", help="with --roofline-only: add a 512 MiB copy")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the decoder step runs on a single MI355X "
               "(multi-GPU sharding is a design note, not built)", file=sys.stderr)
         sys.exit(2)
+    if args.roofline_only:
+        roofline_only(args)
+        return
 
     from rapidocrvl_amd import lib, synth
     from rapidocrvl_amd.config import ERNIE_0P3B as cfg
@@ -171,9 +243,7 @@ def main():
     # roofline: Q4 LM-head GEMV, rotating copies > Infinity Cache
     lm_qt, lm_sc, lm_data, lm_cols = weights["lm_head"]
     lmq = lib.QMatrix(lm_qt, lm_sc.size, lm_cols, lm_sc, lm_data)
-    us, wbytes = gemv_rotation(ctx, lmq)
-    alg = wbytes + 4 * (lmq.rows + lmq.cols)
-    achieved = alg / us / 1e3
+    us, alg, achieved = lm_head_roofline(ctx, lmq)
     log(f"[bench] q4 lm_head gemv {us:.2f} us → {achieved:.0f} GB/s")
 
     cpu = None
@@ -217,7 +287,7 @@ def main():
                    "layers": cfg.layers, "hidden": cfg.hidden, "heads": f"{cfg.heads}q/{cfg.kv_heads}kv",
                    "context": f"{n_prefix}->{n_prefix + args.decode_tokens}", "parallelism": "single-gpu"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                      "kernel": "q4 lm_head gemv 103424x1024 m=1", "us_per_launch": round(us, 3),
                      "algorithmic_bytes": int(alg)},
         "decode_effective_GB_s": round(per_token_bytes * tok_s / 1e9, 1),

@@ -32,6 +32,9 @@ struct DevMat {
 
 // Per-sequence step state kept in HBM so one captured graph can be replayed
 // token after token.
+constexpr int kArgSlots = 64;
+constexpr int kSlotPitch = 16;  // u64 per slot: 128 bytes
+
 struct StepState {
     int32_t len;       // cache rows after this step's append
     int32_t clen;      // cache rows before the append (= token index)
@@ -43,9 +46,13 @@ struct StepState {
     int32_t has_rope;
     int32_t half;
     int32_t pad;
-    unsigned long long argmax_key;
     alignas(16) float cos_t[kMaxHalf];
     float sin_t[kMaxHalf];
+    // greedy argmax: workgroup b of the LM head folds its best (score, row)
+    // key into slot b % kArgSlots with atomicMax; slots sit one 128-byte line
+    // apart so the atomics spread over memory channels.  The consumer takes
+    // the max over the slots (0 = no candidate).
+    alignas(128) unsigned long long argmax_slot[kArgSlots * kSlotPitch];
 };
 
 // ---------------------------------------------------------------------------
@@ -652,7 +659,7 @@ __device__ __forceinline__ void argmax_finish(const GemvParams &p, float best_v,
     if (threadIdx.x == 0) {
         unsigned long long m = kred[0];
         for (int w = 1; w < kWaves; ++w) m = kred[w] > m ? kred[w] : m;
-        if (m) atomicMax(&p.st->argmax_key, m);
+        if (m) atomicMax(&p.st->argmax_slot[(blockIdx.x % kArgSlots) * kSlotPitch], m);
     }
 }
 
@@ -926,12 +933,23 @@ static __global__ void __launch_bounds__(kThreads) k_step_begin(StepState *st, c
                                                            int vocab, const double *freq, const uint8_t *axis,
                                                            int mode, int32_t *tokens, int max_tokens) {
     __shared__ int s_tok, s_err, s_pos[3];
+    __shared__ unsigned long long s_key;
+    if (threadIdx.x < 64) {  // wave 0: max over the argmax slots
+        unsigned long long k = st->argmax_slot[threadIdx.x * kSlotPitch];
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+            const unsigned long long o = __shfl_xor(k, off, 64);
+            k = o > k ? o : k;
+        }
+        if (threadIdx.x == 0) s_key = k;
+    }
+    __syncthreads();
     if (threadIdx.x == 0) {
         int err = st->err;
         int tok = -1;
         if (!err && st->len >= st->cap) err = 1;
         if (!err && mode == 1) {
-            const unsigned long long key = st->argmax_key;
+            const unsigned long long key = s_key;
             if (key == 0ull) err = 2;
             tok = (int)(0xFFFFFFFFu - (uint32_t)(key & 0xFFFFFFFFull));
             if (tok < 0 || tok >= vocab) err = 3;
@@ -948,7 +966,6 @@ static __global__ void __launch_bounds__(kThreads) k_step_begin(StepState *st, c
             st->clen = st->len;
             st->len = st->len + 1;
             st->has_rope = (st->pos[0] != 0 || st->pos[1] != 0 || st->pos[2] != 0) ? 1 : 0;
-            st->argmax_key = 0ull;
         }
         st->err = err;
         s_err = err;
@@ -958,6 +975,7 @@ static __global__ void __launch_bounds__(kThreads) k_step_begin(StepState *st, c
         s_pos[2] = st->pos[2];
     }
     __syncthreads();
+    if (!s_err && threadIdx.x < kArgSlots) st->argmax_slot[threadIdx.x * kSlotPitch] = 0ull;
     if (s_err) return;
     const int half = st->half;
     for (int i = threadIdx.x; i < half; i += kThreads) {

@@ -338,6 +338,13 @@ extern "C" int pocr_matvec(pocr_ctx *ctx, const pocr_weight *w, const float *x, 
     return sync(s);
 }
 
+// greedy argmax key of a step state: the max over the LM head's slots
+static unsigned long long argmax_of(const StepState &s) {
+    unsigned long long k = 0;
+    for (int i = 0; i < kArgSlots; ++i) k = std::max(k, s.argmax_slot[i * kSlotPitch]);
+    return k;
+}
+
 static float key_value(unsigned long long key) {
     uint32_t ord = (uint32_t)(key >> 32);
     uint32_t b = (ord & 0x80000000u) ? (ord & 0x7FFFFFFFu) : ~ord;
@@ -364,9 +371,10 @@ extern "C" int pocr_matvec_argmax(pocr_ctx *ctx, const pocr_weight *w, const flo
     RC(d2h(s, &hst, ctx->state.p, sizeof(StepState)));
     RC(sync(s));
     if (hst.err) return fail(POCR_ERR_DEVICE, "matvec_argmax: device error %d", hst.err);
-    if (hst.argmax_key == 0ull) return fail(POCR_ERR_DEVICE, "matvec_argmax: no finite score");
-    *index = (int32_t)(0xFFFFFFFFu - (uint32_t)(hst.argmax_key & 0xFFFFFFFFull));
-    if (score) *score = key_value(hst.argmax_key);
+    const unsigned long long key = argmax_of(hst);
+    if (key == 0ull) return fail(POCR_ERR_DEVICE, "matvec_argmax: no finite score");
+    *index = (int32_t)(0xFFFFFFFFu - (uint32_t)(key & 0xFFFFFFFFull));
+    if (score) *score = key_value(key);
     return POCR_OK;
 }
 
@@ -1039,8 +1047,9 @@ int pocr::step_locked(pocr_seq *s, const float *emb, const int32_t pos3[3], int 
     s->len = hs.len;
     if (need_logits) {
         if (token) {
-            if (hs.argmax_key == 0ull) return fail(POCR_ERR_DEVICE, "step: no finite logit");
-            *token = (int32_t)(0xFFFFFFFFu - (uint32_t)(hs.argmax_key & 0xFFFFFFFFull));
+            const unsigned long long key = argmax_of(hs);
+            if (key == 0ull) return fail(POCR_ERR_DEVICE, "step: no finite logit");
+            *token = (int32_t)(0xFFFFFFFFu - (uint32_t)(key & 0xFFFFFFFFull));
         }
         if (logits) {
             HIP_TRY(hipMemcpy(logits, s->logits, (size_t)m->cfg.vocab * 4, hipMemcpyDeviceToHost));
@@ -1109,7 +1118,8 @@ static int decode_locked(pocr_seq *s, int32_t first_token, int32_t first_pos, in
     hs.err = 0;
     hs.n_out = 0;
     hs.next_pos = first_pos;
-    hs.argmax_key = (1ull << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)first_token);
+    for (int i = 0; i < kArgSlots; ++i) hs.argmax_slot[i * kSlotPitch] = 0ull;
+    hs.argmax_slot[0] = (1ull << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)first_token);
     HIP_TRY(hipMemcpyAsync(s->st, &hs, sizeof(hs), hipMemcpyHostToDevice, st));
     HIP_TRY(hipStreamSynchronize(st));  // hs is reused as a read-back target below
     int produced = 0;  // tokens known on the host
@@ -1136,7 +1146,7 @@ static int decode_locked(pocr_seq *s, int32_t first_token, int32_t first_pos, in
         }
     }
     // the token chosen by the last step
-    out_tokens[produced] = (int32_t)(0xFFFFFFFFu - (uint32_t)(hs.argmax_key & 0xFFFFFFFFull));
+    out_tokens[produced] = (int32_t)(0xFFFFFFFFu - (uint32_t)(argmax_of(hs) & 0xFFFFFFFFull));
     ++produced;
     s->len = hs.len;
     return produced;
