@@ -187,9 +187,10 @@ int pocr_seq_write_kv(pocr_seq *s, int layer, const float *k, const float *v, in
  * are optional outputs. */
 int pocr_step(pocr_seq *s, const float *emb, const int32_t pos3[3], int need_logits, float *logits,
               int32_t *token);
-/* batched prompt prefill of n embeddings at positions pos3[n][3] on MFMA;
- * same results as n sequential pocr_step calls (token-by-token prefill,
- * internal/model/model.go:1514-1536).  logits/token of the last row. */
+/* prompt prefill of n embeddings at positions pos3[n][3]: the same results
+ * as n sequential pocr_step calls (token-by-token prefill,
+ * internal/model/model.go:1514-1536), run on the device without host round
+ * trips between tokens.  logits/token of the last row. */
 int pocr_prefill(pocr_seq *s, int n, const float *emb, const int32_t *pos3, float *logits,
                  int32_t *token);
 /* greedy decode loop kept on the device (decode loop, model.go:1538-1568):
@@ -201,7 +202,7 @@ int pocr_decode_greedy(pocr_seq *s, int32_t first_token, int32_t first_pos, int 
 /* whole greedy generation: GenerateWithOptions / generateWithImageEmbeds
  * (internal/model/model.go:1492-1572, 1618-1711) incl. multimodal positions
  * (1717-1783).  image rows replace ids equal to image_token_id in order.
- * use_prefill=1 runs the MFMA batched prefill, 0 the token-by-token steps. */
+ * use_prefill=1 runs pocr_prefill, 0 one pocr_step per prompt token. */
 int pocr_generate(pocr_seq *s, const int32_t *ids, int n_ids, const float *image_embeds, int n_image,
                   int32_t image_token_id, const int32_t grid[3], int32_t merge, int max_new,
                   const int32_t *eos, int n_eos, int use_prefill, int32_t *out_tokens);
