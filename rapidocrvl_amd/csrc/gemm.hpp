@@ -1,0 +1,513 @@
+// gemm.hpp — batched (M > 1) decoder kernels on the matrix cores: prompt
+// prefill and the batched GEMV.
+//
+// Prefill runs the same step as the decode kernels (forwardEmbeddingForSampling,
+// internal/model/model.go:3475-3643) for N prompt tokens at once, with the
+// per-token semantics of the token-by-token loop (model.go:1514-1536): token n
+// sees cache rows [0, clen0+n], the Q4/Q6 residual behaviour depends on its own
+// cache length, and its K/V rows land at clen0+n.
+//
+// Quantized products use int8 MFMA (v_mfma_i32_16x16x64_i8).  Activations are
+// written per token as three int8 digit planes with one power-of-two scale S_n:
+//   x = S_n·(d0 + d1/2^7 + d2/2^14) + e,  |e| ≤ S_n/2^15,
+// so a whole row of K products accumulates exactly in int32 (|Σ| < 2^26) and
+// the f32 result differs from the reference's f32 accumulation by rounding
+// only.  Weight codes enter the MFMA as stored: Q8 bytes, Q4 nibbles u ∈ [0,15]
+// (code = u − 8), Q6 fields u ∈ [0,63] (code = u − 32); the offset is removed
+// exactly as IBIAS·Σ_k d_k per token and plane.
+#pragma once
+
+#include "kernels.hpp"
+
+namespace pocr {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+constexpr int kGemmK = 64;       // K per MFMA step
+constexpr int kGemmWaveRows = 64;  // rows per wave (4 blocks of 16)
+constexpr int kGemmRows = kGemmWaveRows * kWaves;  // rows per workgroup
+
+// Within each 16-column group the K order is a permutation shared by the
+// weights and the activation digits: Q4 puts the group's even columns first
+// (the low nibbles of its 8 packed bytes), then the odd ones; Q8/Q6 keep the
+// natural order.
+template <int QT>
+__host__ __device__ constexpr int digit_pos16(int c) {
+    return QT == QT_Q4 ? ((c & 1) ? 8 + (c >> 1) : (c >> 1)) : c;
+}
+
+// ---------------------------------------------------------------------------
+// Activation digitizer: one workgroup per token row.  y = x (or x·w with the
+// RMSNorm factor fastRsqrt(Σx²/K + eps) carried in the row scale, ops.go:
+// 1015-1037), S = 2^e ≥ max|y|/127, planes [3][npad][K] int8 in the K order
+// above, row scale S·factor, bias sums Σd per plane.
+// ---------------------------------------------------------------------------
+struct DigitizeParams {
+    const float *x;        // [n][x_stride]
+    int x_stride;
+    const float *norm_w;   // null → no RMSNorm
+    float eps;
+    int K;                 // multiple of 16, ≤ 4096
+    int8_t *xd;            // planes [3][npad][K]
+    size_t plane_stride;   // npad·K
+    float *xs;             // [n] row scale
+    int *xb;               // [n][4] Σd per plane (4th unused)
+};
+
+template <int QT>
+static __global__ void __launch_bounds__(kThreads) k_digitize(DigitizeParams p) {
+    __shared__ float red[kWaves];
+    __shared__ int redi[3][kWaves];
+    const int n = blockIdx.x;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int c0 = 16 * t;  // this thread's 16-column group
+    const bool valid = c0 < p.K;
+    const int cl = valid ? c0 : p.K - 16;  // clamped, never written
+    const float *xr = p.x + (size_t)n * p.x_stride + cl;
+    float y[16], w[16];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float4 v = reinterpret_cast<const float4 *>(xr)[i];
+        y[4 * i] = v.x;
+        y[4 * i + 1] = v.y;
+        y[4 * i + 2] = v.z;
+        y[4 * i + 3] = v.w;
+    }
+    float factor = 1.0f;
+    if (p.norm_w) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float4 v = reinterpret_cast<const float4 *>(p.norm_w + cl)[i];
+            w[4 * i] = v.x;
+            w[4 * i + 1] = v.y;
+            w[4 * i + 2] = v.z;
+            w[4 * i + 3] = v.w;
+        }
+        float ss = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) ss = fmaf(y[i], y[i], ss);
+        ss = wave_sum(valid ? ss : 0.0f);
+        if (lane == 0) red[wave] = ss;
+        __syncthreads();
+        float tot = red[0];
+#pragma unroll
+        for (int k = 1; k < kWaves; ++k) tot += red[k];
+        factor = fast_rsqrt_ref(tot / (float)p.K + p.eps);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) y[i] = y[i] * w[i];  // a lone product: nothing to contract
+        __syncthreads();  // red is reused below
+    }
+    float m = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) m = fmaxf(m, fabsf(y[i]));
+    m = wave_max(valid ? m : 0.0f);
+    if (lane == 0) red[wave] = m;
+    __syncthreads();
+    m = red[0];
+#pragma unroll
+    for (int k = 1; k < kWaves; ++k) m = fmaxf(m, red[k]);
+    int ex = 0;
+    (void)frexpf(m * (1.0f / 127.0f), &ex);  // m/127 < 2^ex
+    const float inv = m > 0.0f ? ldexpf(1.0f, -ex) : 1.0f;
+    const float S = m > 0.0f ? ldexpf(1.0f, ex) : 1.0f;
+    int d[3][16];  // digit of K position pos (the group's shared order)
+    int sd[3] = {0, 0, 0};
+#pragma unroll
+    for (int c = 0; c < 16; ++c) {
+        const float tt = y[c] * inv;  // exact: inv is a power of two
+        const float a = rintf(tt);
+        const float t1 = (tt - a) * 128.0f;
+        const float b = rintf(t1);
+        const int d2 = (int)rintf((t1 - b) * 128.0f);
+        const int pos = digit_pos16<QT>(c);
+        d[0][pos] = (int)a;
+        d[1][pos] = (int)b;
+        d[2][pos] = d2;
+        sd[0] += (int)a;
+        sd[1] += (int)b;
+        sd[2] += d2;
+    }
+    if (valid) {
+#pragma unroll
+        for (int pl = 0; pl < 3; ++pl)
+            *reinterpret_cast<int4 *>(p.xd + pl * p.plane_stride + (size_t)n * p.K + c0) =
+                make_int4(pack4(d[pl][0], d[pl][1], d[pl][2], d[pl][3]), pack4(d[pl][4], d[pl][5], d[pl][6], d[pl][7]),
+                          pack4(d[pl][8], d[pl][9], d[pl][10], d[pl][11]),
+                          pack4(d[pl][12], d[pl][13], d[pl][14], d[pl][15]));
+    }
+    __syncthreads();
+#pragma unroll
+    for (int pl = 0; pl < 3; ++pl) {
+        const int s = (int)wave_sum((float)(valid ? sd[pl] : 0));  // |Σ| ≤ 4096·127: exact in f32
+        if (lane == 0) redi[pl][wave] = s;
+    }
+    __syncthreads();
+    if (t < 3) {
+        int s = 0;
+#pragma unroll
+        for (int k = 0; k < kWaves; ++k) s += redi[t][k];
+        p.xb[n * 4 + t] = s;
+    }
+    if (t == 0) p.xs[n] = S * factor;
+}
+
+// ---------------------------------------------------------------------------
+// MFMA GEMM: Y[n][r] = epilogue(scale[r]·xs[n]·(D0 + D1/2^7 + D2/2^14)),
+// D_p = Σ_k u[r][k]·d_p[n][k] − IBIAS·Σ_k d_p[n][k].  Workgroup: 256 rows ×
+// 16·TN tokens; wave w owns rows r0+64w.. (4 blocks of 16) for all its tokens.
+// Rows come from up to three matrices (segments, as the fused QKV GEMV) or,
+// with NMAT = 2, from two matrices side by side (gate and up).
+// ---------------------------------------------------------------------------
+enum : int { G_PLAIN = 0, G_SWIGLU = 1, G_OPROJ = 2, G_DOWN = 3 };
+
+struct GemmParams {
+    DevMat m[3];
+    int seg_end[3];
+    int rows;              // multiple of 64
+    int K;                 // multiple of 64
+    const int8_t *xd;      // planes [3][npad][K]
+    size_t plane_stride;
+    const float *xs;       // [n]
+    const int *xb;         // [n][4]
+    int ntok;
+    float *out;            // PLAIN / SWIGLU: [n][out_stride]
+    int out_stride;
+    float *h;              // OPROJ / DOWN residual rows [n][rows]
+    float *vbuf;           // [n][rows]
+    int quirk;             // OPROJ: Q4/Q6 residual behaviour
+    int clen0;             // cache rows before token 0
+    int last;              // DOWN: last layer → vbuf = h + y (h untouched)
+};
+
+// 16 weight codes of row `row` at columns k..k+15 (k multiple of 16) as the
+// MFMA A operand, in the shared K order
+template <int QT>
+__device__ __forceinline__ v4i load_codes16(const uint8_t *rowp, int k) {
+    v4i a;
+    if constexpr (QT == QT_Q8) {
+        const uint4 v = *reinterpret_cast<const uint4 *>(rowp + k);
+        a = v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
+    } else if constexpr (QT == QT_Q4) {
+        const uint2 v = *reinterpret_cast<const uint2 *>(rowp + k / 2);
+        a = v4i{(int)(v.x & 0x0F0F0F0Fu), (int)(v.y & 0x0F0F0F0Fu), (int)((v.x >> 4) & 0x0F0F0F0Fu),
+                (int)((v.y >> 4) & 0x0F0F0F0Fu)};
+    } else {
+        const uint8_t *q = rowp + (k / 16) * 12;
+        const uint32_t d0 = *reinterpret_cast<const uint32_t *>(q);
+        const uint32_t d1 = *reinterpret_cast<const uint32_t *>(q + 4);
+        const uint32_t d2 = *reinterpret_cast<const uint32_t *>(q + 8);
+        a = v4i{spread6(d0), spread6(__builtin_amdgcn_alignbit(d1, d0, 24)),
+                spread6(__builtin_amdgcn_alignbit(d2, d1, 16)), spread6(d2 >> 8)};
+    }
+    return a;
+}
+
+__device__ __forceinline__ bool prefill_in_place(const GemmParams &p, int n) {
+    // model.go:3895-3902, 4051-4057: Q4/Q6 take the OutOnly variant at cache
+    // length 0 and ≥ 6
+    const int clen = p.clen0 + n;
+    return !(p.quirk && (clen == 0 || clen >= 6));
+}
+
+template <int QT, int NMAT, int TN>
+static __global__ void __launch_bounds__(kThreads) k_gemm(GemmParams p, int epi) {
+    constexpr int IB = DigitTraits<QT>::IBIAS;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r0 = blockIdx.x * kGemmRows + wave * kGemmWaveRows;
+    if (r0 >= p.rows) return;  // rows are a multiple of 64: whole waves only
+    const int n0 = blockIdx.y * 16 * TN;
+    const int lr = lane & 15, lg = lane >> 4;
+
+    // the wave's 64 rows lie in one segment (segment ends are multiples of 64)
+    const uint8_t *base0;
+    const uint8_t *base1 = nullptr;
+    const float *scale0;
+    const float *scale1 = nullptr;
+    int start = 0;
+    if (NMAT == 2) {
+        base0 = p.m[0].data;
+        base1 = p.m[1].data;
+        scale0 = p.m[0].scale;
+        scale1 = p.m[1].scale;
+    } else if (r0 >= p.seg_end[1]) {
+        base0 = p.m[2].data;
+        scale0 = p.m[2].scale;
+        start = p.seg_end[1];
+    } else if (r0 >= p.seg_end[0]) {
+        base0 = p.m[1].data;
+        scale0 = p.m[1].scale;
+        start = p.seg_end[0];
+    } else {
+        base0 = p.m[0].data;
+        scale0 = p.m[0].scale;
+    }
+    const int row_bytes = p.m[0].row_bytes;
+    const uint8_t *arow[NMAT][4];
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) {
+        const size_t off = (size_t)(r0 + 16 * rb + lr - start) * row_bytes;
+        arow[0][rb] = base0 + off;
+        if (NMAT == 2) arow[NMAT - 1][rb] = base1 + off;
+    }
+    const int8_t *brow[TN];
+#pragma unroll
+    for (int tb = 0; tb < TN; ++tb) brow[tb] = p.xd + (size_t)(n0 + 16 * tb + lr) * p.K + 16 * lg;
+
+    v4i acc[NMAT][4][TN][3];
+#pragma unroll
+    for (int mi = 0; mi < NMAT; ++mi)
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+            for (int tb = 0; tb < TN; ++tb)
+#pragma unroll
+                for (int pl = 0; pl < 3; ++pl) acc[mi][rb][tb][pl] = v4i{0, 0, 0, 0};
+
+    v4i a[NMAT][4], b[TN][3];
+    auto load = [&](int k0, v4i (&aa)[NMAT][4], v4i (&bb)[TN][3]) {
+        const int k = k0 + 16 * lg;
+#pragma unroll
+        for (int mi = 0; mi < NMAT; ++mi)
+#pragma unroll
+            for (int rb = 0; rb < 4; ++rb) aa[mi][rb] = load_codes16<QT>(arow[mi][rb], k);
+#pragma unroll
+        for (int tb = 0; tb < TN; ++tb)
+#pragma unroll
+            for (int pl = 0; pl < 3; ++pl)
+                bb[tb][pl] = *reinterpret_cast<const v4i *>(brow[tb] + pl * p.plane_stride + k0);
+    };
+    load(0, a, b);
+    for (int k0 = 0; k0 < p.K; k0 += kGemmK) {
+        v4i an[NMAT][4], bn[TN][3];
+        const bool more = k0 + kGemmK < p.K;  // uniform
+        if (more) load(k0 + kGemmK, an, bn);
+#pragma unroll
+        for (int mi = 0; mi < NMAT; ++mi)
+#pragma unroll
+            for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+                for (int tb = 0; tb < TN; ++tb)
+#pragma unroll
+                    for (int pl = 0; pl < 3; ++pl)
+                        acc[mi][rb][tb][pl] =
+                            __builtin_amdgcn_mfma_i32_16x16x64_i8(a[mi][rb], b[tb][pl], acc[mi][rb][tb][pl], 0, 0, 0);
+        if (more) {
+#pragma unroll
+            for (int mi = 0; mi < NMAT; ++mi)
+#pragma unroll
+                for (int rb = 0; rb < 4; ++rb) a[mi][rb] = an[mi][rb];
+#pragma unroll
+            for (int tb = 0; tb < TN; ++tb)
+#pragma unroll
+                for (int pl = 0; pl < 3; ++pl) b[tb][pl] = bn[tb][pl];
+        }
+    }
+
+    // epilogue: lane holds token n0+16tb+lr, rows r0+16rb+4lg+i (i < 4)
+#pragma unroll
+    for (int tb = 0; tb < TN; ++tb) {
+        const int n = n0 + 16 * tb + lr;
+        if (n >= p.ntok) continue;
+        const float sx = p.xs[n];
+        const int4 bs = *reinterpret_cast<const int4 *>(p.xb + 4 * n);
+        const bool inpl = epi == G_OPROJ ? prefill_in_place(p, n) : false;
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) {
+            const int rr = r0 + 16 * rb + 4 * lg;  // 4 consecutive rows
+            float y[NMAT][4];
+#pragma unroll
+            for (int mi = 0; mi < NMAT; ++mi) {
+                const float *sc = (mi == 0 ? scale0 : scale1) + (rr - start);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float f0 = (float)(acc[mi][rb][tb][0][i] - IB * bs.x);
+                    const float f1 = (float)(acc[mi][rb][tb][1][i] - IB * bs.y);
+                    const float f2 = (float)(acc[mi][rb][tb][2][i] - IB * bs.z);
+                    y[mi][i] = fmaf(f2, 1.0f / 16384.0f, fmaf(f1, 1.0f / 128.0f, f0)) * sx * sc[i];
+                }
+            }
+            if (epi == G_PLAIN) {
+                *reinterpret_cast<float4 *>(p.out + (size_t)n * p.out_stride + rr) =
+                    make_float4(y[0][0], y[0][1], y[0][2], y[0][3]);
+            } else if (epi == G_SWIGLU) {
+                float o[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+#pragma clang fp contract(off)
+                    o[i] = silu_ref(y[0][i]) * y[NMAT - 1][i];
+                }
+                *reinterpret_cast<float4 *>(p.out + (size_t)n * p.out_stride + rr) = make_float4(o[0], o[1], o[2], o[3]);
+            } else {
+                float4 *hp = reinterpret_cast<float4 *>(p.h + (size_t)n * p.rows + rr);
+                const float4 hv = *hp;
+                float4 v;
+                {
+#pragma clang fp contract(off)
+                    v = make_float4(hv.x + y[0][0], hv.y + y[0][1], hv.z + y[0][2], hv.w + y[0][3]);
+                }
+                float4 *vp = reinterpret_cast<float4 *>(p.vbuf + (size_t)n * p.rows + rr);
+                if (epi == G_OPROJ) {
+                    *vp = v;
+                    if (inpl) *hp = v;
+                } else if (p.last) {
+                    *vp = v;
+                } else {
+                    *hp = v;
+                }
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Per-token RoPE of q and k (table from the token's (T,H,W) position in f64,
+// buildMRoPETable, model.go:7318-7357) and the K/V append of token n at cache
+// row clen0+n (kvCache.append, model.go:5593-5612).  qkv rows are
+// [q heads | k heads | v heads] of head_dim floats; q is rotated in place.
+// ---------------------------------------------------------------------------
+static __global__ void __launch_bounds__(kThreads) k_rope_append(float *qkv, int stride, const int32_t *pos3,
+                                                            const double *freq, const uint8_t *axis, int heads,
+                                                            int kvh, int head_dim, float *kc, float *vc,
+                                                            int clen0) {
+    __shared__ float cs[kMaxHalf], sn[kMaxHalf];
+    const int n = blockIdx.x;
+    const int half = head_dim / 2;
+    for (int i = threadIdx.x; i < half; i += kThreads) {
+        const int a = axis[i];
+        const double ang = (double)pos3[3 * n + a] * freq[i];
+        cs[i] = (float)cos(ang);
+        sn[i] = (float)sin(ang);
+    }
+    __syncthreads();
+    float *row = qkv + (size_t)n * stride;
+    const int kvd = kvh * head_dim;
+    const int t = clen0 + n;
+    for (int i = threadIdx.x; i < (heads + kvh) * half; i += kThreads) {
+        const int h = i / half, j = i % half;
+        float *x = row + (size_t)h * head_dim;  // k heads follow the q heads
+        float a = x[j], b = x[j + half];
+        rope_pair(a, b, cs[j], sn[j]);
+        if (h < heads) {
+            x[j] = a;
+            x[j + half] = b;
+        } else {
+            float *kd = kc + (size_t)t * kvd + (h - heads) * head_dim;
+            kd[j] = a;
+            kd[j + half] = b;
+        }
+    }
+    const float *v = row + (size_t)(heads + kvh) * head_dim;
+    for (int i = threadIdx.x; i < kvd; i += kThreads) vc[(size_t)t * kvd + i] = v[i];
+}
+
+// ---------------------------------------------------------------------------
+// Causal GQA prefill attention, head_dim 128.  Workgroup (g, qb): kv head g,
+// query tokens [8qb, 8qb+8) for all GROUP (≤ 8) q heads of g: 64 query rows,
+// four threads per row (row = t/4, dims 32·(t%4)..+31).  Keys stream through
+// LDS in blocks of 32 rows; each row keeps an online softmax (max, Σexp) and
+// its output slice.  Token n attends cache rows [0, clen0+n].  Scores:
+// dot·f32(1/√128) (model.go:4623-4795, 7391); softmax with FastExp.
+// ---------------------------------------------------------------------------
+constexpr int kPfTok = 8;     // query tokens per workgroup
+constexpr int kPfKeys = 32;   // key rows per LDS block
+
+static __global__ void __launch_bounds__(kThreads) k_attn_prefill(const float *qkv, int stride, const float *kc,
+                                                             const float *vc, int heads, int kvh, int ntok,
+                                                             int clen0, float scale, float *out, int out_stride) {
+    __shared__ float4 ks[kPfKeys][kHD / 4];
+    __shared__ float4 vs[kPfKeys][kHD / 4];
+    __shared__ float sc[kPfTok * kMaxGroup][kPfKeys + 1];
+    const int g = blockIdx.x;
+    const int group = heads / kvh;
+    const int t = threadIdx.x;
+    const int row = t >> 2, qd = t & 3;            // query row, dim quarter
+    const int tok = blockIdx.y * kPfTok + row % kPfTok;
+    const int hq = g * group + row / kPfTok;       // q head
+    const bool active = row / kPfTok < group && tok < ntok;
+    const int kvd = kvh * kHD;
+    float q[32];
+    {
+        const int tq = min(tok, ntok - 1);
+        const int hh = min(hq, heads - 1);
+        const float4 *src = reinterpret_cast<const float4 *>(qkv + (size_t)tq * stride + (size_t)hh * kHD + 32 * qd);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float4 v = src[i];
+            q[4 * i] = v.x;
+            q[4 * i + 1] = v.y;
+            q[4 * i + 2] = v.z;
+            q[4 * i + 3] = v.w;
+        }
+    }
+    float o[32];
+#pragma unroll
+    for (int i = 0; i < 32; ++i) o[i] = 0.0f;
+    float m = -INFINITY, l = 0.0f;
+    const int last_key = clen0 + min((int)blockIdx.y * kPfTok + kPfTok, ntok) - 1;  // block's last visible row
+    const int my_last = clen0 + min(tok, ntok - 1);
+    for (int k0 = 0; k0 <= last_key; k0 += kPfKeys) {
+        __syncthreads();
+        for (int i = t; i < kPfKeys * (kHD / 4); i += kThreads) {
+            const int r = i / (kHD / 4), c = i % (kHD / 4);
+            const int key = min(k0 + r, last_key);
+            ks[r][c] = reinterpret_cast<const float4 *>(kc + (size_t)key * kvd + g * kHD)[c];
+            vs[r][c] = reinterpret_cast<const float4 *>(vc + (size_t)key * kvd + g * kHD)[c];
+        }
+        __syncthreads();
+        // scores of this row against the block's keys (the row's 4 threads are
+        // adjacent lanes of one wave: two DPP adds give every one the sum)
+        float mb = m;
+#pragma unroll 2
+        for (int r = 0; r < kPfKeys; ++r) {
+            float a = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float4 kv = ks[r][8 * qd + i];
+                a = fmaf(q[4 * i], kv.x, a);
+                a = fmaf(q[4 * i + 1], kv.y, a);
+                a = fmaf(q[4 * i + 2], kv.z, a);
+                a = fmaf(q[4 * i + 3], kv.w, a);
+            }
+            a += xchg<XQ1>(a);
+            a += xchg<XQ2>(a);
+            const float sv = k0 + r <= my_last ? a * scale : -INFINITY;
+            if (qd == 0) sc[row][r] = sv;
+            mb = fmaxf(mb, sv);
+        }
+        // the row's scores were written by lane 4·row of this wave: LDS keeps
+        // a wave's accesses in order, the fence keeps the compiler from
+        // reordering them
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        if (mb != -INFINITY) {  // rows with no visible key in this block skip it
+            const float f = m == -INFINITY ? 0.0f : fast_exp_ref(m - mb);
+            l *= f;
+#pragma unroll
+            for (int i = 0; i < 32; ++i) o[i] *= f;
+#pragma unroll 2
+            for (int r = 0; r < kPfKeys; ++r) {
+                const float sv = sc[row][r];
+                const float e = sv == -INFINITY ? 0.0f : fast_exp_ref(sv - mb);
+                l += e;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const float4 vv = vs[r][8 * qd + i];
+                    o[4 * i] = fmaf(e, vv.x, o[4 * i]);
+                    o[4 * i + 1] = fmaf(e, vv.y, o[4 * i + 1]);
+                    o[4 * i + 2] = fmaf(e, vv.z, o[4 * i + 2]);
+                    o[4 * i + 3] = fmaf(e, vv.w, o[4 * i + 3]);
+                }
+            }
+            m = mb;
+        }
+    }
+    if (active) {
+        const float inv = 1.0f / l;
+        float4 *dst = reinterpret_cast<float4 *>(out + (size_t)tok * out_stride + (size_t)hq * kHD + 32 * qd);
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            dst[i] = make_float4(o[4 * i] * inv, o[4 * i + 1] * inv, o[4 * i + 2] * inv, o[4 * i + 3] * inv);
+    }
+}
+
+}  // namespace pocr

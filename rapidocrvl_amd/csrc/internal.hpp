@@ -66,6 +66,7 @@ struct pocr_ctx {
     std::mutex mu;
     // op-level staging
     DevBuf x, out, out2, out3, res, vbuf, kc, vc, part, tabs, state;
+    DevBuf gxd, gxs, gxb;  // batched GEMV activation digits
 };
 
 struct pocr_weight {
@@ -101,13 +102,16 @@ struct pocr_model {
 
 // prefill / batched GEMV (prefill.hip)
 struct PrefillBufs {
-    float *x = nullptr;      // [n][max(hidden, q_rows, inter)] activations
-    float *y = nullptr;      // [n][max rows] GEMM outputs
-    float *h = nullptr;      // [n][hidden] residual rows
-    float *v = nullptr;      // [n][hidden] residual + attention rows
-    int32_t *pos = nullptr;  // [n][3]
-    float *tabs = nullptr;   // [n][2][half] RoPE tables
-    int cap_rows = 0;
+    float *h = nullptr;      // [rows][hidden] residual rows
+    float *v = nullptr;      // [rows][hidden] residual + attention rows
+    float *qkv = nullptr;    // [rows][q_rows + 2·kv_rows]
+    float *ho = nullptr;     // [rows][q_rows] attention output
+    float *g = nullptr;      // [rows][inter] SwiGLU output
+    int8_t *xd = nullptr;    // activation digit planes [3][rows][max K]
+    float *xs = nullptr;     // [rows] digit row scales
+    int *xb = nullptr;       // [rows][4] digit sums
+    int32_t *pos = nullptr;  // [rows][3]
+    int cap_rows = 0;        // rows allocated (a multiple of 32)
 };
 void prefill_free(PrefillBufs &b);
 
@@ -139,7 +143,9 @@ GemvParams gemv_params_1(const pocr_weight *w);
 int step_locked(pocr_seq *s, const float *emb, const int32_t pos3[3], int need_logits, float *logits,
                 int32_t *token);
 int prefill_locked(pocr_seq *s, int n, const float *emb, const int32_t *pos3, float *logits, int32_t *token);
-int batched_gemv(hipStream_t s, const DevMat &w, const float *x, int m, float *out);
+int batched_gemv(pocr_ctx *ctx, const DevMat &w, const float *x, int m, float *out);
+int read_state(pocr_seq *s, StepState *out);
+unsigned long long argmax_of(const StepState &s);
 float *layer_k(const pocr_seq *s, int layer);
 float *layer_v(const pocr_seq *s, int layer);
 int seq_set_state(pocr_seq *s, int len);

@@ -327,7 +327,7 @@ extern "C" int pocr_matvec(pocr_ctx *ctx, const pocr_weight *w, const float *x, 
     RC(ctx->out.ensure((size_t)m * w->rows * 4));
     RC(h2d(s, ctx->x.p, x, (size_t)m * w->cols * 4));
     if (m > 1) {
-        RC(batched_gemv(s, dev_mat(w), ctx->x.as<float>(), m, ctx->out.as<float>()));
+        RC(batched_gemv(ctx, dev_mat(w), ctx->x.as<float>(), m, ctx->out.as<float>()));
     } else {
         GemvParams p = gemv_params_1(w);
         p.x = ctx->x.as<float>();
@@ -339,7 +339,7 @@ extern "C" int pocr_matvec(pocr_ctx *ctx, const pocr_weight *w, const float *x, 
 }
 
 // greedy argmax key of a step state: the max over the LM head's slots
-static unsigned long long argmax_of(const StepState &s) {
+unsigned long long pocr::argmax_of(const StepState &s) {
     unsigned long long k = 0;
     for (int i = 0; i < kArgSlots; ++i) k = std::max(k, s.argmax_slot[i * kSlotPitch]);
     return k;
@@ -1027,7 +1027,7 @@ static int enqueue_step(pocr_seq *s, int mode, bool need_logits, bool want_logit
     return POCR_OK;
 }
 
-static int read_state(pocr_seq *s, StepState *out) {
+int pocr::read_state(pocr_seq *s, StepState *out) {
     HIP_TRY(hipMemcpyAsync(out, s->st, sizeof(StepState), hipMemcpyDeviceToHost, s->m->ctx->stream));
     HIP_TRY(hipStreamSynchronize(s->m->ctx->stream));
     return POCR_OK;

@@ -1,37 +1,292 @@
-// prefill.hip — prompt prefill and batched (M>1) GEMV.
+// prefill.hip — prompt prefill and batched (M>1) GEMV on the matrix cores.
+#include "gemm.hpp"
 #include "internal.hpp"
 
+using namespace pocr;
+
 void prefill_free(PrefillBufs &b) {
-    for (void *p : {(void *)b.x, (void *)b.y, (void *)b.h, (void *)b.v, (void *)b.pos, (void *)b.tabs})
+    for (void *p : {(void *)b.h, (void *)b.v, (void *)b.qkv, (void *)b.ho, (void *)b.g, (void *)b.xd, (void *)b.xs,
+                    (void *)b.xb, (void *)b.pos})
         if (p) (void)hipFree(p);
     b = PrefillBufs{};
 }
 
-namespace pocr {
+namespace {
 
-// M rows of activations against one weight stream
-int batched_gemv(hipStream_t s, const DevMat &w, const float *x, int m, float *out) {
-    for (int i = 0; i < m; ++i) {
-        GemvParams p{};
-        p.m[0] = p.m[1] = p.m[2] = w;
-        p.seg_end[0] = p.seg_end[1] = p.seg_end[2] = w.rows;
-        p.rows = w.rows;
-        p.cols = w.cols;
-        p.x = x + (size_t)i * w.cols;
-        p.out = out + (size_t)i * w.rows;
-        RC(gemv_launch(s, p, 1, PRO_COPY, EPI_PLAIN, kBigGrid));
+int round_up(int x, int m) { return (x + m - 1) / m * m; }
+
+// the MFMA GEMM takes rows in whole 64-row wave tiles and K in 64-column steps
+bool gemm_shape_ok(int rows, int K) { return rows % kGemmWaveRows == 0 && K % kGemmK == 0 && K <= kMaxCols; }
+
+int launch_digitize(hipStream_t s, int qtype, const DigitizeParams &p, int n) {
+    switch (qtype) {
+    case QT_Q8: hipLaunchKernelGGL(k_digitize<QT_Q8>, dim3(n), dim3(kThreads), 0, s, p); break;
+    case QT_Q4: hipLaunchKernelGGL(k_digitize<QT_Q4>, dim3(n), dim3(kThreads), 0, s, p); break;
+    case QT_Q6: hipLaunchKernelGGL(k_digitize<QT_Q6>, dim3(n), dim3(kThreads), 0, s, p); break;
+    default: return fail(POCR_ERR_UNSUPPORTED, "digitize: qtype %d", qtype);
     }
+    HIP_TRY(hipGetLastError());
     return POCR_OK;
 }
 
-// token-by-token prefill (model.go:1514-1536): same semantics as n steps
-int prefill_locked(pocr_seq *s, int n, const float *emb, const int32_t *pos3, float *logits, int32_t *token) {
+template <int NMAT, int TN>
+int launch_gemm_t(hipStream_t s, int qtype, const GemmParams &p, int epi, int npad) {
+    const dim3 grid((p.rows + kGemmRows - 1) / kGemmRows, npad / (16 * TN));
+    switch (qtype) {
+    case QT_Q8: hipLaunchKernelGGL((k_gemm<QT_Q8, NMAT, TN>), grid, dim3(kThreads), 0, s, p, epi); break;
+    case QT_Q4: hipLaunchKernelGGL((k_gemm<QT_Q4, NMAT, TN>), grid, dim3(kThreads), 0, s, p, epi); break;
+    case QT_Q6: hipLaunchKernelGGL((k_gemm<QT_Q6, NMAT, TN>), grid, dim3(kThreads), 0, s, p, epi); break;
+    default: return fail(POCR_ERR_UNSUPPORTED, "gemm: qtype %d", qtype);
+    }
+    HIP_TRY(hipGetLastError());
+    return POCR_OK;
+}
+
+// npad: token rows of the digit planes, a multiple of 32
+int launch_gemm(hipStream_t s, int qtype, int nmat, const GemmParams &p, int epi, int npad) {
+    if (nmat == 2) return launch_gemm_t<2, 1>(s, qtype, p, epi, npad);
+    return launch_gemm_t<1, 2>(s, qtype, p, epi, npad);
+}
+
+GemmParams gemm_params_1(const pocr_weight *w) {
+    GemmParams p{};
+    p.m[0] = p.m[1] = p.m[2] = dev_mat(w);
+    p.seg_end[0] = p.seg_end[1] = p.seg_end[2] = w->rows;
+    p.rows = w->rows;
+    p.K = w->cols;
+    return p;
+}
+
+template <class T>
+int grow(T *&p, size_t count) {
+    if (p) (void)hipFree(p);
+    p = nullptr;
+    HIP_TRY(hipMalloc(&p, std::max<size_t>(count, 64) * sizeof(T)));
+    return POCR_OK;
+}
+
+int ensure_bufs(pocr_seq *s, int rows) {
+    PrefillBufs &b = s->pf;
+    if (rows <= b.cap_rows) return POCR_OK;
+    const pocr_config &c = s->m->cfg;
+    const size_t H = c.hidden, Q = (size_t)c.heads * c.head_dim, KV = (size_t)c.kv_heads * c.head_dim;
+    const size_t kmax = std::max({H, Q, (size_t)c.intermediate});
+    prefill_free(b);
+    RC(grow(b.h, rows * H));
+    RC(grow(b.v, rows * H));
+    RC(grow(b.qkv, rows * (Q + 2 * KV)));
+    RC(grow(b.ho, rows * Q));
+    RC(grow(b.g, rows * (size_t)c.intermediate));
+    RC(grow(b.xd, 3 * rows * kmax));
+    RC(grow(b.xs, (size_t)rows));
+    RC(grow(b.xb, (size_t)rows * 4));
+    RC(grow(b.pos, (size_t)rows * 3));
+    b.cap_rows = rows;
+    return POCR_OK;
+}
+
+// every shape the batched layer needs, else the token-by-token path runs
+bool prefill_supported(const pocr_model *m) {
+    const pocr_config &c = m->cfg;
+    const int Q = c.heads * c.head_dim, KV = c.kv_heads * c.head_dim;
+    if (c.head_dim != kHD || c.heads % c.kv_heads || c.heads / c.kv_heads > kMaxGroup) return false;
+    if (c.hidden % 16 || Q % 16 || c.intermediate % 16) return false;
+    for (int li = 0; li < c.layers; ++li) {
+        const LayerW &L = m->layers[li];
+        const int qt = L.w[POCR_W_Q]->qtype;
+        for (int r = 0; r < 7; ++r)
+            if (L.w[r]->qtype != qt) return false;
+        if (L.w[POCR_W_GATE]->qtype != L.w[POCR_W_UP]->qtype) return false;
+        if (Q % kGemmWaveRows || KV % kGemmWaveRows) return false;
+        if (!gemm_shape_ok(Q + 2 * KV, c.hidden) || !gemm_shape_ok(c.hidden, Q) ||
+            !gemm_shape_ok(c.intermediate, c.hidden) || !gemm_shape_ok(c.hidden, c.intermediate))
+            return false;
+    }
+    return true;
+}
+
+// token-by-token prefill (model.go:1514-1536): n sequential steps
+int prefill_tokenwise(pocr_seq *s, int n, const float *emb, const int32_t *pos3, float *logits, int32_t *token) {
     const int H = s->m->cfg.hidden;
     for (int i = 0; i < n; ++i) {
         const bool last = i == n - 1;
         RC(step_locked(s, emb + (size_t)i * H, pos3 + 3 * i, last ? 1 : 0, last ? logits : nullptr,
                        last ? token : nullptr));
     }
+    return POCR_OK;
+}
+
+}  // namespace
+
+namespace pocr {
+
+// M rows of activations against one weight stream: digit planes per row, then
+// the MFMA GEMM; shapes it does not take run M launches of the GEMV
+int batched_gemv(pocr_ctx *ctx, const DevMat &w, const float *x, int m, float *out) {
+    hipStream_t s = ctx->stream;
+    if (!gemm_shape_ok(w.rows, w.cols)) {
+        for (int i = 0; i < m; ++i) {
+            GemvParams p{};
+            p.m[0] = p.m[1] = p.m[2] = w;
+            p.seg_end[0] = p.seg_end[1] = p.seg_end[2] = w.rows;
+            p.rows = w.rows;
+            p.cols = w.cols;
+            p.x = x + (size_t)i * w.cols;
+            p.out = out + (size_t)i * w.rows;
+            RC(gemv_launch(s, p, 1, PRO_COPY, EPI_PLAIN, kBigGrid));
+        }
+        return POCR_OK;
+    }
+    const int npad = round_up(m, 32);
+    RC(ctx->gxd.ensure((size_t)3 * npad * w.cols));
+    RC(ctx->gxs.ensure((size_t)npad * 4));
+    RC(ctx->gxb.ensure((size_t)npad * 16));
+    DigitizeParams d{};
+    d.x = x;
+    d.x_stride = w.cols;
+    d.K = w.cols;
+    d.xd = ctx->gxd.as<int8_t>();
+    d.plane_stride = (size_t)npad * w.cols;
+    d.xs = ctx->gxs.as<float>();
+    d.xb = ctx->gxb.as<int>();
+    RC(launch_digitize(s, w.qtype, d, m));
+    GemmParams p{};
+    p.m[0] = p.m[1] = p.m[2] = w;
+    p.seg_end[0] = p.seg_end[1] = p.seg_end[2] = w.rows;
+    p.rows = w.rows;
+    p.K = w.cols;
+    p.xd = d.xd;
+    p.plane_stride = d.plane_stride;
+    p.xs = d.xs;
+    p.xb = d.xb;
+    p.ntok = m;
+    p.out = out;
+    p.out_stride = w.rows;
+    return launch_gemm(s, w.qtype, 1, p, G_PLAIN, npad);
+}
+
+// Batched prefill: every layer runs once over the n prompt tokens (digit
+// planes → MFMA GEMMs with the step's epilogues, per-token RoPE + K/V append,
+// causal attention), then the LM head on the last token.  Per-token semantics
+// match n sequential steps (model.go:1514-1536, 3475-3643).
+int prefill_locked(pocr_seq *s, int n, const float *emb, const int32_t *pos3, float *logits, int32_t *token) {
+    pocr_model *m = s->m;
+    const char *env = getenv("POCR_BATCHED_PREFILL");
+    if ((env && env[0] == '0') || !prefill_supported(m)) return prefill_tokenwise(s, n, emb, pos3, logits, token);
+    const pocr_config &c = m->cfg;
+    hipStream_t st = m->ctx->stream;
+    const int H = c.hidden, Q = c.heads * c.head_dim, KV = c.kv_heads * c.head_dim, F = c.intermediate;
+    const int QKV = Q + 2 * KV;
+    const int clen0 = s->len;
+    if (clen0 + n > s->cap) return fail(POCR_ERR_ARG, "prefill: %d rows exceed capacity", n);
+    const int npad = round_up(n, 32);
+    RC(ensure_bufs(s, npad));
+    PrefillBufs &b = s->pf;
+    HIP_TRY(hipMemcpyAsync(b.h, emb, (size_t)n * H * 4, hipMemcpyHostToDevice, st));
+    HIP_TRY(hipMemcpyAsync(b.pos, pos3, (size_t)n * 12, hipMemcpyHostToDevice, st));
+    const float eps = c.rms_norm_eps;
+    const float scale = (float)(1.0 / std::sqrt((double)c.head_dim));
+    const int qt = m->layers[0].w[POCR_W_Q]->qtype;
+
+    auto digitize = [&](const float *x, int stride, const float *norm_w, int K) {
+        DigitizeParams d{};
+        d.x = x;
+        d.x_stride = stride;
+        d.norm_w = norm_w;
+        d.eps = eps;
+        d.K = K;
+        d.xd = b.xd;
+        d.plane_stride = (size_t)npad * K;
+        d.xs = b.xs;
+        d.xb = b.xb;
+        return launch_digitize(st, qt, d, n);
+    };
+    auto gemm_in = [&](GemmParams &p) {
+        p.xd = b.xd;
+        p.plane_stride = (size_t)npad * p.K;
+        p.xs = b.xs;
+        p.xb = b.xb;
+        p.ntok = n;
+        p.clen0 = clen0;
+    };
+
+    for (int li = 0; li < c.layers; ++li) {
+        const LayerW &L = m->layers[li];
+        const bool last = li + 1 == c.layers;
+        // 1. RMSNorm(h)·ln1 → q|k|v
+        RC(digitize(b.h, H, L.ln1, H));
+        GemmParams g{};
+        g.m[0] = dev_mat(L.w[POCR_W_Q]);
+        g.m[1] = dev_mat(L.w[POCR_W_K]);
+        g.m[2] = dev_mat(L.w[POCR_W_V]);
+        g.seg_end[0] = Q;
+        g.seg_end[1] = Q + KV;
+        g.seg_end[2] = QKV;
+        g.rows = QKV;
+        g.K = H;
+        gemm_in(g);
+        g.out = b.qkv;
+        g.out_stride = QKV;
+        RC(launch_gemm(st, qt, 1, g, G_PLAIN, npad));
+        // 2. per-token RoPE, K/V append at rows clen0.., causal attention
+        hipLaunchKernelGGL(k_rope_append, dim3(n), dim3(kThreads), 0, st, b.qkv, QKV, b.pos, m->freq, m->axis,
+                           c.heads, c.kv_heads, c.head_dim, layer_k(s, li), layer_v(s, li), clen0);
+        hipLaunchKernelGGL(k_attn_prefill, dim3(c.kv_heads, (n + kPfTok - 1) / kPfTok), dim3(kThreads), 0, st,
+                           b.qkv, QKV, layer_k(s, li), layer_v(s, li), c.heads, c.kv_heads, n, clen0, scale, b.ho, Q);
+        HIP_TRY(hipGetLastError());
+        // 3. o_proj + residual (+ the Q4/Q6 behaviour per token) → v; h if in place
+        RC(digitize(b.ho, Q, nullptr, Q));
+        GemmParams o = gemm_params_1(L.w[POCR_W_O]);
+        gemm_in(o);
+        o.h = b.h;
+        o.vbuf = b.v;
+        o.quirk = (m->quirk && (qt == POCR_Q4 || qt == POCR_Q6)) ? 1 : 0;
+        RC(launch_gemm(st, qt, 1, o, G_OPROJ, npad));
+        // 4. RMSNorm(v)·ln2 → SiLU(gate)·up
+        RC(digitize(b.v, H, L.ln2, H));
+        GemmParams gu = gemm_params_1(L.w[POCR_W_GATE]);
+        gu.m[1] = dev_mat(L.w[POCR_W_UP]);
+        gemm_in(gu);
+        gu.out = b.g;
+        gu.out_stride = F;
+        RC(launch_gemm(st, qt, 2, gu, G_SWIGLU, npad));
+        // 5. down + residual; last layer: v = h + down
+        RC(digitize(b.g, F, nullptr, F));
+        GemmParams d = gemm_params_1(L.w[POCR_W_DOWN]);
+        gemm_in(d);
+        d.h = b.h;
+        d.vbuf = b.v;
+        d.last = last ? 1 : 0;
+        RC(launch_gemm(st, qt, 1, d, G_DOWN, npad));
+    }
+
+    // step state after the last prompt token, then the LM head on its row
+    StepState hs{};
+    hs.len = clen0 + n;
+    hs.clen = clen0 + n - 1;
+    hs.cap = s->cap;
+    hs.half = c.head_dim / 2;
+    hs.pos[0] = pos3[3 * (n - 1)];
+    hs.pos[1] = pos3[3 * (n - 1) + 1];
+    hs.pos[2] = pos3[3 * (n - 1) + 2];
+    HIP_TRY(hipMemcpyAsync(s->st, &hs, sizeof(hs), hipMemcpyHostToDevice, st));
+    HIP_TRY(hipStreamSynchronize(st));  // hs is a stack object
+    GemvParams p = gemv_params_1(m->lm);
+    p.x = b.v + (size_t)(n - 1) * H;
+    p.norm_w = m->final_norm;
+    p.eps = eps;
+    p.out = logits ? s->logits : nullptr;
+    p.st = s->st;
+    RC(gemv_launch(st, p, 1, PRO_RMSNORM, EPI_ARGMAX, kBigGrid));
+    StepState out;
+    RC(read_state(s, &out));
+    s->len = clen0 + n;
+    if (token) {
+        const unsigned long long key = argmax_of(out);
+        if (key == 0ull) return fail(POCR_ERR_DEVICE, "prefill: no finite logit");
+        *token = (int32_t)(0xFFFFFFFFu - (uint32_t)(key & 0xFFFFFFFFull));
+    }
+    if (logits) HIP_TRY(hipMemcpy(logits, s->logits, (size_t)c.vocab * 4, hipMemcpyDeviceToHost));
     return POCR_OK;
 }
 

@@ -208,7 +208,7 @@ def test_gpu_weighted_value_sum(ctx):
     assert np.max(np.abs(out[4:] - np.array(k["out_head1"]))) < 2e-5
 
 
-def _gpu_stream(ctx, rec):
+def _gpu_stream(ctx, rec, use_prefill=False):
     cfg = _cfg(rec)
     w = synth.make_weights(cfg, rec["qtype"], seed=rec["weight_seed"])
     m = lib.Model(ctx, cfg)
@@ -216,14 +216,15 @@ def _gpu_stream(ctx, rec):
     m.set_residual_quirk(rec["quirk"])
     ids, kw = _stream_inputs(rec)
     s = m.seq(len(ids) + rec["max_new"] + 4)
-    got = s.generate(ids, rec["max_new"], eos=(), **kw)
+    got = s.generate(ids, rec["max_new"], eos=(), use_prefill=use_prefill, **kw)
     s.close()
     m.close()
     return got
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("use_prefill", [False, True], ids=["steps", "prefill"])
 @pytest.mark.parametrize("name", TINY_CASES + ERNIE_CASES)
-def test_gpu_matches_golden_streams(ctx, name):
+def test_gpu_matches_golden_streams(ctx, name, use_prefill):
     rec = STREAMS[name]
-    assert list(_gpu_stream(ctx, rec)) == rec["tokens"], name
+    assert list(_gpu_stream(ctx, rec, use_prefill)) == rec["tokens"], name
