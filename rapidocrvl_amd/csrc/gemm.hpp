@@ -402,111 +402,155 @@ static __global__ void __launch_bounds__(kThreads) k_rope_append(float *qkv, int
 }
 
 // ---------------------------------------------------------------------------
-// Causal GQA prefill attention, head_dim 128.  Workgroup (g, qb): kv head g,
-// query tokens [8qb, 8qb+8) for all GROUP (≤ 8) q heads of g: 64 query rows,
-// four threads per row (row = t/4, dims 32·(t%4)..+31).  Keys stream through
-// LDS in blocks of 32 rows; each row keeps an online softmax (max, Σexp) and
-// its output slice.  Token n attends cache rows [0, clen0+n].  Scores:
-// dot·f32(1/√128) (model.go:4623-4795, 7391); softmax with FastExp.
+// Causal GQA prefill attention, head_dim 128, on fp32 MFMA
+// (v_mfma_f32_16x16x4f32; lane l of an operand holds row/column l%16 and K
+// index l/16, the result lane l holds rows 4·(l/16)+i of column l%16).
+//
+// Workgroup (g, qb): kv head g, query tokens [16qb, 16qb+16).  Wave w owns
+// q heads 2w, 2w+1 of the group, one 16×16 tile (token × ·) each.  Per key
+// block of 32 rows (K and V staged in LDS) it forms Sᵀ = K·Qᵀ — the scores of
+// its 16 tokens, keys down the rows — so the probabilities are already laid
+// out as the B operand of Oᵀ += Vᵀ·Pᵀ: no transpose.  The K index of the
+// Sᵀ products is dim 32·(l/16)+s at step s (any order sums the same), which
+// makes every lane's q and k reads contiguous.  Online softmax per token
+// (max, Σexp) with FastExp; token n attends cache rows [0, clen0+n].
+// Scores: dot·f32(1/√128) (model.go:4623-4795, 7391).
 // ---------------------------------------------------------------------------
-constexpr int kPfTok = 8;     // query tokens per workgroup
+typedef float v4f __attribute__((ext_vector_type(4)));
+constexpr int kPfTok = 16;    // query tokens per workgroup
 constexpr int kPfKeys = 32;   // key rows per LDS block
+constexpr int kPfPad = 4;     // LDS row padding (floats)
 
 static __global__ void __launch_bounds__(kThreads) k_attn_prefill(const float *qkv, int stride, const float *kc,
                                                              const float *vc, int heads, int kvh, int ntok,
                                                              int clen0, float scale, float *out, int out_stride) {
-    __shared__ float4 ks[kPfKeys][kHD / 4];
-    __shared__ float4 vs[kPfKeys][kHD / 4];
-    __shared__ float sc[kPfTok * kMaxGroup][kPfKeys + 1];
+    __shared__ float ks[kPfKeys][kHD + kPfPad];
+    __shared__ float vs[kPfKeys][kHD + kPfPad];
     const int g = blockIdx.x;
     const int group = heads / kvh;
-    const int t = threadIdx.x;
-    const int row = t >> 2, qd = t & 3;            // query row, dim quarter
-    const int tok = blockIdx.y * kPfTok + row % kPfTok;
-    const int hq = g * group + row / kPfTok;       // q head
-    const bool active = row / kPfTok < group && tok < ntok;
+    const int t = threadIdx.x, l = t & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int lr = l & 15, lg = l >> 4;
+    const int q0 = blockIdx.y * kPfTok;
+    const int tok = q0 + lr;  // this lane's token (column of every tile)
     const int kvd = kvh * kHD;
-    float q[32];
-    {
-        const int tq = min(tok, ntok - 1);
-        const int hh = min(hq, heads - 1);
-        const float4 *src = reinterpret_cast<const float4 *>(qkv + (size_t)tq * stride + (size_t)hh * kHD + 32 * qd);
+    const bool wave_on = 2 * wave < group;  // uniform
+
+    // Qᵀ operands: tile qt = head 2·wave+qt, lane: token lr, dims 32·lg + s
+    float qv[2][32];
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+        const int hh = g * group + min(2 * wave + qt, group - 1);
+        const float4 *src =
+            reinterpret_cast<const float4 *>(qkv + (size_t)min(tok, ntok - 1) * stride + (size_t)hh * kHD + 32 * lg);
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const float4 v = src[i];
-            q[4 * i] = v.x;
-            q[4 * i + 1] = v.y;
-            q[4 * i + 2] = v.z;
-            q[4 * i + 3] = v.w;
+            qv[qt][4 * i] = v.x;
+            qv[qt][4 * i + 1] = v.y;
+            qv[qt][4 * i + 2] = v.z;
+            qv[qt][4 * i + 3] = v.w;
         }
     }
-    float o[32];
+    v4f o[2][8];
 #pragma unroll
-    for (int i = 0; i < 32; ++i) o[i] = 0.0f;
-    float m = -INFINITY, l = 0.0f;
-    const int last_key = clen0 + min((int)blockIdx.y * kPfTok + kPfTok, ntok) - 1;  // block's last visible row
+    for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) o[qt][dt] = v4f{0.f, 0.f, 0.f, 0.f};
+    float m[2] = {-INFINITY, -INFINITY}, lsum[2] = {0.f, 0.f};
+    const int last_key = clen0 + min(q0 + kPfTok, ntok) - 1;  // the block's last visible row
     const int my_last = clen0 + min(tok, ntok - 1);
+
     for (int k0 = 0; k0 <= last_key; k0 += kPfKeys) {
         __syncthreads();
         for (int i = t; i < kPfKeys * (kHD / 4); i += kThreads) {
-            const int r = i / (kHD / 4), c = i % (kHD / 4);
+            const int r = i / (kHD / 4), c = 4 * (i % (kHD / 4));
             const int key = min(k0 + r, last_key);
-            ks[r][c] = reinterpret_cast<const float4 *>(kc + (size_t)key * kvd + g * kHD)[c];
-            vs[r][c] = reinterpret_cast<const float4 *>(vc + (size_t)key * kvd + g * kHD)[c];
+            const float4 kv = *reinterpret_cast<const float4 *>(kc + (size_t)key * kvd + g * kHD + c);
+            const float4 vv = *reinterpret_cast<const float4 *>(vc + (size_t)key * kvd + g * kHD + c);
+            *reinterpret_cast<float4 *>(&ks[r][c]) = kv;
+            *reinterpret_cast<float4 *>(&vs[r][c]) = vv;
         }
         __syncthreads();
-        // scores of this row against the block's keys (the row's 4 threads are
-        // adjacent lanes of one wave: two DPP adds give every one the sum)
-        float mb = m;
-#pragma unroll 2
-        for (int r = 0; r < kPfKeys; ++r) {
-            float a = 0.0f;
+        if (!wave_on) continue;
+        // Sᵀ[kt][qt]: keys k0+16kt+4lg+i (rows) × tokens (columns)
+        v4f sT[2][2];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const float4 kv = ks[r][8 * qd + i];
-                a = fmaf(q[4 * i], kv.x, a);
-                a = fmaf(q[4 * i + 1], kv.y, a);
-                a = fmaf(q[4 * i + 2], kv.z, a);
-                a = fmaf(q[4 * i + 3], kv.w, a);
+        for (int kt = 0; kt < 2; ++kt) {
+            sT[kt][0] = sT[kt][1] = v4f{0.f, 0.f, 0.f, 0.f};
+            const float *krow = &ks[16 * kt + lr][32 * lg];
+#pragma unroll
+            for (int s4 = 0; s4 < 8; ++s4) {
+                const float4 ka = *reinterpret_cast<const float4 *>(krow + 4 * s4);
+                const float kk[4] = {ka.x, ka.y, ka.z, ka.w};
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+#pragma unroll
+                    for (int qt = 0; qt < 2; ++qt)
+                        sT[kt][qt] = __builtin_amdgcn_mfma_f32_16x16x4f32(kk[j], qv[qt][4 * s4 + j], sT[kt][qt], 0, 0, 0);
             }
-            a += xchg<XQ1>(a);
-            a += xchg<XQ2>(a);
-            const float sv = k0 + r <= my_last ? a * scale : -INFINITY;
-            if (qd == 0) sc[row][r] = sv;
-            mb = fmaxf(mb, sv);
         }
-        // the row's scores were written by lane 4·row of this wave: LDS keeps
-        // a wave's accesses in order, the fence keeps the compiler from
-        // reordering them
-        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-        if (mb != -INFINITY) {  // rows with no visible key in this block skip it
-            const float f = m == -INFINITY ? 0.0f : fast_exp_ref(m - mb);
-            l *= f;
+        // online softmax per token (column): keys of a column sit in 4 lane groups
 #pragma unroll
-            for (int i = 0; i < 32; ++i) o[i] *= f;
-#pragma unroll 2
-            for (int r = 0; r < kPfKeys; ++r) {
-                const float sv = sc[row][r];
-                const float e = sv == -INFINITY ? 0.0f : fast_exp_ref(sv - mb);
-                l += e;
+        for (int qt = 0; qt < 2; ++qt) {
+            float sv[2][4];
+            float mb = m[qt];
 #pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    const float4 vv = vs[r][8 * qd + i];
-                    o[4 * i] = fmaf(e, vv.x, o[4 * i]);
-                    o[4 * i + 1] = fmaf(e, vv.y, o[4 * i + 1]);
-                    o[4 * i + 2] = fmaf(e, vv.z, o[4 * i + 2]);
-                    o[4 * i + 3] = fmaf(e, vv.w, o[4 * i + 3]);
+            for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int key = k0 + 16 * kt + 4 * lg + i;
+                    sv[kt][i] = key <= my_last ? sT[kt][qt][i] * scale : -INFINITY;
+                    mb = fmaxf(mb, sv[kt][i]);
+                }
+            mb = fmaxf(mb, xchg<XS16>(mb));
+            mb = fmaxf(mb, xchg<XS32>(mb));
+            float ps = 0.0f;
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float e = sv[kt][i] == -INFINITY ? 0.0f : fast_exp_ref(sv[kt][i] - mb);
+                    sT[kt][qt][i] = e;  // Pᵀ, in place
+                    ps += e;
+                }
+            ps += xchg<XS16>(ps);
+            ps += xchg<XS32>(ps);
+            // mb is finite: key 0 is visible to every token, so from the first
+            // block on every column has a finite maximum
+            const float f = m[qt] == -INFINITY ? 0.0f : fast_exp_ref(m[qt] - mb);
+            lsum[qt] = lsum[qt] * f + ps;
+            m[qt] = mb;
+#pragma unroll
+            for (int dt = 0; dt < 8; ++dt) o[qt][dt] *= f;
+        }
+        // Oᵀ[dt][qt] += Vᵀ (dims × keys) · Pᵀ (keys × tokens); MFMA step (kt, i)
+        // takes keys 16kt + 4·lg' + i of lane group lg'
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float *vrow = &vs[16 * kt + 4 * lg + i][lr];
+#pragma unroll
+                for (int dt = 0; dt < 8; ++dt) {
+                    const float va = vrow[16 * dt];
+#pragma unroll
+                    for (int qt = 0; qt < 2; ++qt)
+                        o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(va, sT[kt][qt][i], o[qt][dt], 0, 0, 0);
                 }
             }
-            m = mb;
-        }
     }
-    if (active) {
-        const float inv = 1.0f / l;
-        float4 *dst = reinterpret_cast<float4 *>(out + (size_t)tok * out_stride + (size_t)hq * kHD + 32 * qd);
+    if (!wave_on || tok >= ntok) return;
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
-            dst[i] = make_float4(o[4 * i] * inv, o[4 * i + 1] * inv, o[4 * i + 2] * inv, o[4 * i + 3] * inv);
+    for (int qt = 0; qt < 2; ++qt) {
+        if (2 * wave + qt >= group) break;
+        const int hq = g * group + 2 * wave + qt;
+        const float inv = 1.0f / lsum[qt];
+        float *dst = out + (size_t)tok * out_stride + (size_t)hq * kHD + 4 * lg;
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt)
+            *reinterpret_cast<float4 *>(dst + 16 * dt) =
+                make_float4(o[qt][dt][0] * inv, o[qt][dt][1] * inv, o[qt][dt][2] * inv, o[qt][dt][3] * inv);
     }
 }
 
