@@ -742,6 +742,13 @@ __global__ void __launch_bounds__(kThreads) k_gemv(GemvParams p, int pro, int ep
     __shared__ float red[2 * kWaves];
     constexpr int RPW = 64 / LPR;
     constexpr int RG = RPW * U;
+    // Every kernel argument is made live here, so their scalar loads issue as
+    // one batch: one kernel-argument round trip instead of one per branch.
+    asm volatile("" ::"s"(p.m[0].data), "s"(p.m[0].scale), "s"(p.m[1].data), "s"(p.m[1].scale), "s"(p.m[2].data),
+                 "s"(p.m[2].scale));
+    asm volatile("" ::"s"(p.x), "s"(p.norm_w), "s"(p.out), "s"(p.residual), "s"(p.vbuf), "s"(p.st));
+    asm volatile("" ::"s"(p.seg_end[0]), "s"(p.seg_end[1]), "s"(p.rows), "s"(p.cols), "s"(p.m[0].row_bytes),
+                 "s"(p.eps), "s"(p.flag), "s"(p.quirk), "s"(pro), "s"(epi));
 
     const int rows = p.rows;
     const int row_bytes = p.m[0].row_bytes;
@@ -1072,7 +1079,19 @@ __device__ __forceinline__ void f4_to(float (&d)[8], const float4 &a, const floa
     d[4] = b.x; d[5] = b.y; d[6] = b.z; d[7] = b.w;
 }
 
-static __global__ void __launch_bounds__(kThreads) k_attn_decode(AttnParams p) {
+// Kernel arguments pinned in SGPRs: one batch of scalar loads at entry (the
+// in/out asm operands stop the compiler from reloading a field from the
+// argument segment at its first use, a round trip each).
+__device__ __forceinline__ void pin_args(AttnParams &p) {
+    asm volatile("" : "+s"(p.q), "+s"(p.k_new), "+s"(p.v_new), "+s"(p.kc), "+s"(p.vc), "+s"(p.st), "+s"(p.part),
+                 "+s"(p.head_out));
+    asm volatile("" : "+s"(p.cos_t), "+s"(p.sin_t), "+s"(p.heads), "+s"(p.kvh), "+s"(p.nsplit), "+s"(p.rows_cap));
+    asm volatile("" ::"s"(p.len), "s"(p.has_rope));
+}
+
+static __global__ void __launch_bounds__(kThreads) k_attn_decode(AttnParams args) {
+    AttnParams p = args;
+    pin_args(p);
     StepState *st = p.st;
     __shared__ float4 e_lds[kWaves][kMaxGroup][4];      // wave-private probabilities [head][16 rows]
     __shared__ float w_m[kWaves][kMaxGroup], w_l[kWaves][kMaxGroup];
@@ -1309,7 +1328,9 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
-static __global__ void __launch_bounds__(kHD) k_attn_merge(AttnParams p) {
+static __global__ void __launch_bounds__(kHD) k_attn_merge(AttnParams args) {
+    AttnParams p = args;
+    pin_args(p);
     __shared__ float e_lds[kMaxSplits];
     __shared__ float l_lds;
     const int hq = blockIdx.x;  // q head
