@@ -93,22 +93,22 @@ def time_decode(seq, n_prefix, first_tok, first_pos, n_tokens, warmup, steps):
     return dt, toks
 
 
-def gemv_rotation(ctx, q, target_bytes=600 << 20, iters=None):
-    """Average µs of one M=1 GEMV launch rotating over copies of q."""
-    from rapidocrvl_amd import lib
-
+def gemv_rotation(ctx, q, target_bytes=600 << 20, iters=None, m=1):
+    """Average µs of one GEMV launch (M rows of x) rotating over copies of q."""
     wbytes = q.packed.nbytes + q.scales.nbytes
     n = max(2, int(np.ceil(target_bytes / wbytes)))
     copies = [ctx.upload(q) for _ in range(n)]
-    x = np.random.default_rng(0).standard_normal(q.cols).astype(np.float32)
+    x = np.random.default_rng(0).standard_normal((m, q.cols)).astype(np.float32)
     iters = iters or max(4 * n, 200)
-    us = ctx.time_matvec(copies, x, iters)
+    us = ctx.time_matvec(copies, x[0], iters) if m == 1 else ctx.time_matvec_batched(copies, x, iters)
     for c in copies:
         c.close()
     return us, wbytes
 
 
 def gemv_sweep(ctx, rng):
+    """The four decoder GEMV shapes × Q8/Q6/Q4 × M ∈ {1, 4, 16} (M > 1: digit
+    planes + MFMA GEMM); GB/s of algorithmic bytes (weights + scales + M·(x + y))."""
     from rapidocrvl_amd import lib
 
     shapes = {"gate_up": (3072, 1024), "down": (1024, 3072), "qkv": (2560, 1024), "lm_head": (103424, 1024)}
@@ -117,9 +117,22 @@ def gemv_sweep(ctx, rng):
         for sname, (rows, cols) in shapes.items():
             w = (rng.standard_normal((rows, cols), dtype=np.float32) * np.float32(0.02))
             q = lib.QMatrix.quantize(w, qtype)
-            us, wbytes = gemv_rotation(ctx, q)
-            alg = wbytes + 4 * (rows + cols)
-            out[f"{qname}_{sname}_m1"] = {"us": round(us, 3), "GB/s": round(alg / us / 1e3, 1)}
+            for m in (1, 4, 16):
+                us, wbytes = gemv_rotation(ctx, q, m=m)
+                alg = wbytes + 4 * m * (rows + cols)
+                out[f"{qname}_{sname}_m{m}"] = {"us": round(us, 3), "GB/s": round(alg / us / 1e3, 1),
+                                                "TOP/s": round(2 * m * rows * cols / us / 1e6, 2)}
+    return out
+
+
+def attention_sweep(ctx, cfg):
+    """Decode attention (RoPE, K/V append, GQA over L fp32 rows) at
+    L ∈ {1024, 4096, 8192}, rotating over the model's 18 layer caches."""
+    out = {}
+    for L in (1024, 4096, 8192):
+        us = ctx.time_attention(cfg.heads, cfg.kv_heads, cfg.head_dim, L, cfg.layers, 400)
+        alg = 2 * L * cfg.kv_heads * cfg.head_dim * 4 + 4 * (cfg.heads + 2 * cfg.kv_heads) * cfg.head_dim
+        out[f"L{L}"] = {"us": round(us, 3), "GB/s": round(alg / us / 1e3, 1)}
     return out
 
 
@@ -285,6 +298,7 @@ def main():
     extra["prefill_TFLOP_s"] = round(prefill_flops(cfg, n_prefix) / t_prefill / 1e12, 2)
     if not args.no_sweep:
         extra["gemv_sweep"] = gemv_sweep(ctx, np.random.default_rng(0))
+        extra["attention_sweep"] = attention_sweep(ctx, cfg)
 
     per_token_bytes = 181_542_912 + 36_864 * (n_prefix + args.decode_tokens // 2)
     result = {

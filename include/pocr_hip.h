@@ -156,6 +156,20 @@ int pocr_text_attention(pocr_ctx *ctx, const float *q, const float *k_cache, con
 int pocr_time_matvec(pocr_ctx *ctx, const pocr_weight *const *weights, int n_weights, const float *x, int iters,
                      float *avg_us);
 
+/* The same for the batched GEMV: m rows of x (m*cols floats) per launch pair
+ * (digit planes + MFMA GEMM).  Measurement counterpart of the reference's
+ * M-row benchmarks (internal/tensor/model_dims_bench_test.go). */
+int pocr_time_matvec_batched(pocr_ctx *ctx, const pocr_weight *const *weights, int n_weights, const float *x, int m,
+                             int iters, float *avg_us);
+
+/* Average device time (microseconds) of one decode-attention call — RoPE,
+ * K/V append and GQA attention of one token over cache_len fp32 rows, the
+ * work of cacheAttentionScores + weightedCacheValueSum
+ * (internal/model/model.go:4623-4795, 5201-5590) — rotating over n_layers
+ * separate caches so the working set can exceed the Infinity Cache. */
+int pocr_time_attention(pocr_ctx *ctx, int heads, int kv_heads, int head_dim, int cache_len, int n_layers, int iters,
+                        float *avg_us);
+
 /* ---------------- model / step level (device-resident) ---------------- */
 int pocr_model_create(pocr_ctx *ctx, const pocr_config *cfg, pocr_model **out);
 void pocr_model_destroy(pocr_model *m);

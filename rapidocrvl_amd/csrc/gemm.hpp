@@ -209,9 +209,91 @@ __device__ __forceinline__ bool prefill_in_place(const GemmParams &p, int n) {
     return !(p.quirk && (clen == 0 || clen >= 6));
 }
 
+// Epilogue of rows rr..rr+3 for token n, given the int32 accumulators of the
+// three digit planes: y = scale[r]·xs[n]·(D0 + D1/2^7 + D2/2^14).
+template <int QT, int NMAT>
+__device__ __forceinline__ void gemm_store(const GemmParams &p, int epi, int n, int rr, const float *const (&scl)[2],
+                                           const v4i (&a)[NMAT][3]) {
+    constexpr int IB = DigitTraits<QT>::IBIAS;
+    const float sx = p.xs[n];
+    const int4 bs = *reinterpret_cast<const int4 *>(p.xb + 4 * n);
+    float y[NMAT][4];
+#pragma unroll
+    for (int mi = 0; mi < NMAT; ++mi) {
+        const float *sc = scl[mi];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float f0 = (float)(a[mi][0][i] - IB * bs.x);
+            const float f1 = (float)(a[mi][1][i] - IB * bs.y);
+            const float f2 = (float)(a[mi][2][i] - IB * bs.z);
+            y[mi][i] = fmaf(f2, 1.0f / 16384.0f, fmaf(f1, 1.0f / 128.0f, f0)) * sx * sc[i];
+        }
+    }
+    if (epi == G_PLAIN) {
+        *reinterpret_cast<float4 *>(p.out + (size_t)n * p.out_stride + rr) = make_float4(y[0][0], y[0][1], y[0][2], y[0][3]);
+    } else if (epi == G_SWIGLU) {
+        float o[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+#pragma clang fp contract(off)
+            o[i] = silu_ref(y[0][i]) * y[NMAT - 1][i];
+        }
+        *reinterpret_cast<float4 *>(p.out + (size_t)n * p.out_stride + rr) = make_float4(o[0], o[1], o[2], o[3]);
+    } else {
+        float4 *hp = reinterpret_cast<float4 *>(p.h + (size_t)n * p.rows + rr);
+        const float4 hv = *hp;
+        float4 v;
+        {
+#pragma clang fp contract(off)
+            v = make_float4(hv.x + y[0][0], hv.y + y[0][1], hv.z + y[0][2], hv.w + y[0][3]);
+        }
+        float4 *vp = reinterpret_cast<float4 *>(p.vbuf + (size_t)n * p.rows + rr);
+        if (epi == G_OPROJ) {
+            *vp = v;
+            if (prefill_in_place(p, n)) *hp = v;
+        } else if (p.last) {
+            *vp = v;
+        } else {
+            *hp = v;
+        }
+    }
+}
+
+// the wave's rows lie in one segment (segment ends are multiples of 16 rows
+// for the small kernel, of 64 for the prefill one)
+struct GemmSeg {
+    const uint8_t *base[2];
+    const float *scale[2];
+    int start;
+};
+template <int NMAT>
+__device__ __forceinline__ GemmSeg gemm_seg(const GemmParams &p, int r0) {
+    GemmSeg g;
+    g.base[1] = nullptr;
+    g.scale[1] = nullptr;
+    g.start = 0;
+    if (NMAT == 2) {
+        g.base[0] = p.m[0].data;
+        g.base[1] = p.m[1].data;
+        g.scale[0] = p.m[0].scale;
+        g.scale[1] = p.m[1].scale;
+    } else if (r0 >= p.seg_end[1]) {
+        g.base[0] = p.m[2].data;
+        g.scale[0] = p.m[2].scale;
+        g.start = p.seg_end[1];
+    } else if (r0 >= p.seg_end[0]) {
+        g.base[0] = p.m[1].data;
+        g.scale[0] = p.m[1].scale;
+        g.start = p.seg_end[0];
+    } else {
+        g.base[0] = p.m[0].data;
+        g.scale[0] = p.m[0].scale;
+    }
+    return g;
+}
+
 template <int QT, int NMAT, int TN>
 static __global__ void __launch_bounds__(kThreads) k_gemm(GemmParams p, int epi) {
-    constexpr int IB = DigitTraits<QT>::IBIAS;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r0 = blockIdx.x * kGemmRows + wave * kGemmWaveRows;
@@ -309,55 +391,106 @@ static __global__ void __launch_bounds__(kThreads) k_gemm(GemmParams p, int epi)
     for (int tb = 0; tb < TN; ++tb) {
         const int n = n0 + 16 * tb + lr;
         if (n >= p.ntok) continue;
-        const float sx = p.xs[n];
-        const int4 bs = *reinterpret_cast<const int4 *>(p.xb + 4 * n);
-        const bool inpl = epi == G_OPROJ ? prefill_in_place(p, n) : false;
 #pragma unroll
         for (int rb = 0; rb < 4; ++rb) {
             const int rr = r0 + 16 * rb + 4 * lg;  // 4 consecutive rows
-            float y[NMAT][4];
+            const float *const scl[2] = {scale0 + (rr - start), NMAT == 2 ? scale1 + (rr - start) : nullptr};
+            v4i a3[NMAT][3];
 #pragma unroll
-            for (int mi = 0; mi < NMAT; ++mi) {
-                const float *sc = (mi == 0 ? scale0 : scale1) + (rr - start);
+            for (int mi = 0; mi < NMAT; ++mi)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const float f0 = (float)(acc[mi][rb][tb][0][i] - IB * bs.x);
-                    const float f1 = (float)(acc[mi][rb][tb][1][i] - IB * bs.y);
-                    const float f2 = (float)(acc[mi][rb][tb][2][i] - IB * bs.z);
-                    y[mi][i] = fmaf(f2, 1.0f / 16384.0f, fmaf(f1, 1.0f / 128.0f, f0)) * sx * sc[i];
-                }
-            }
-            if (epi == G_PLAIN) {
-                *reinterpret_cast<float4 *>(p.out + (size_t)n * p.out_stride + rr) =
-                    make_float4(y[0][0], y[0][1], y[0][2], y[0][3]);
-            } else if (epi == G_SWIGLU) {
-                float o[4];
+                for (int pl = 0; pl < 3; ++pl) a3[mi][pl] = acc[mi][rb][tb][pl];
+            gemm_store<QT, NMAT>(p, epi, n, rr, scl, a3);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Small-M MFMA GEMM (M ≤ 16 tokens, the batched GEMV): a workgroup owns 16
+// rows (of each matrix with NMAT = 2) and all tokens; its 4 waves split K in
+// quarters, request their K-steps in double-buffered batches of four (a wave
+// waits on memory once or twice, not once per step), and their exact int32
+// partials are summed through LDS before wave 0 applies the epilogue.
+// ---------------------------------------------------------------------------
+constexpr int kSmallBatch = 4;  // K-steps per request batch
+
+template <int QT, int NMAT>
+static __global__ void __launch_bounds__(kThreads) k_gemm_small(GemmParams p, int epi) {
+    __shared__ v4i part[kWaves - 1][NMAT][3][64];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r0 = blockIdx.x * 16;
+    const int lr = lane & 15, lg = lane >> 4;
+    const GemmSeg sg = gemm_seg<NMAT>(p, r0);
+    const int row_bytes = p.m[0].row_bytes;
+    const uint8_t *arow[NMAT];
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-#pragma clang fp contract(off)
-                    o[i] = silu_ref(y[0][i]) * y[NMAT - 1][i];
-                }
-                *reinterpret_cast<float4 *>(p.out + (size_t)n * p.out_stride + rr) = make_float4(o[0], o[1], o[2], o[3]);
-            } else {
-                float4 *hp = reinterpret_cast<float4 *>(p.h + (size_t)n * p.rows + rr);
-                const float4 hv = *hp;
-                float4 v;
-                {
-#pragma clang fp contract(off)
-                    v = make_float4(hv.x + y[0][0], hv.y + y[0][1], hv.z + y[0][2], hv.w + y[0][3]);
-                }
-                float4 *vp = reinterpret_cast<float4 *>(p.vbuf + (size_t)n * p.rows + rr);
-                if (epi == G_OPROJ) {
-                    *vp = v;
-                    if (inpl) *hp = v;
-                } else if (p.last) {
-                    *vp = v;
-                } else {
-                    *hp = v;
-                }
+    for (int mi = 0; mi < NMAT; ++mi) arow[mi] = sg.base[mi] + (size_t)(r0 + lr - sg.start) * row_bytes;
+    const int8_t *brow = p.xd + (size_t)lr * p.K + 16 * lg;
+    const int kq = p.K / kWaves;  // this wave's K range [wave·kq, (wave+1)·kq), a multiple of 64
+    const int kbeg = wave * kq;
+    const int nsteps = kq / kGemmK;
+
+    v4i acc[NMAT][3];
+#pragma unroll
+    for (int mi = 0; mi < NMAT; ++mi)
+#pragma unroll
+        for (int pl = 0; pl < 3; ++pl) acc[mi][pl] = v4i{0, 0, 0, 0};
+    v4i a[kSmallBatch][NMAT], b[kSmallBatch][3];
+    auto load = [&](int s0, v4i (&aa)[kSmallBatch][NMAT], v4i (&bb)[kSmallBatch][3]) {
+#pragma unroll
+        for (int j = 0; j < kSmallBatch; ++j) {
+            const int k0 = kbeg + kGemmK * min(s0 + j, nsteps - 1);  // clamped: loaded, not used
+            const int k = k0 + 16 * lg;
+#pragma unroll
+            for (int mi = 0; mi < NMAT; ++mi) aa[j][mi] = load_codes16<QT>(arow[mi], k);
+#pragma unroll
+            for (int pl = 0; pl < 3; ++pl) bb[j][pl] = *reinterpret_cast<const v4i *>(brow + pl * p.plane_stride + k0);
+        }
+    };
+    load(0, a, b);
+    for (int s0 = 0; s0 < nsteps; s0 += kSmallBatch) {
+        v4i an[kSmallBatch][NMAT], bn[kSmallBatch][3];
+        const bool more = s0 + kSmallBatch < nsteps;  // uniform
+        if (more) load(s0 + kSmallBatch, an, bn);
+#pragma unroll
+        for (int j = 0; j < kSmallBatch; ++j) {
+            if (s0 + j >= nsteps) break;  // uniform
+#pragma unroll
+            for (int mi = 0; mi < NMAT; ++mi)
+#pragma unroll
+                for (int pl = 0; pl < 3; ++pl)
+                    acc[mi][pl] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[j][mi], b[j][pl], acc[mi][pl], 0, 0, 0);
+        }
+        if (more) {
+#pragma unroll
+            for (int j = 0; j < kSmallBatch; ++j) {
+#pragma unroll
+                for (int mi = 0; mi < NMAT; ++mi) a[j][mi] = an[j][mi];
+#pragma unroll
+                for (int pl = 0; pl < 3; ++pl) b[j][pl] = bn[j][pl];
             }
         }
     }
+    if (wave > 0) {
+#pragma unroll
+        for (int mi = 0; mi < NMAT; ++mi)
+#pragma unroll
+            for (int pl = 0; pl < 3; ++pl) part[wave - 1][mi][pl][lane] = acc[mi][pl];
+    }
+    __syncthreads();
+    if (wave > 0) return;
+#pragma unroll
+    for (int w = 0; w < kWaves - 1; ++w)
+#pragma unroll
+        for (int mi = 0; mi < NMAT; ++mi)
+#pragma unroll
+            for (int pl = 0; pl < 3; ++pl) acc[mi][pl] += part[w][mi][pl][lane];
+    const int n = lr;  // token (column)
+    if (n >= p.ntok) return;
+    const int rr = r0 + 4 * lg;
+    const float *const scl[2] = {sg.scale[0] + (rr - sg.start), NMAT == 2 ? sg.scale[1] + (rr - sg.start) : nullptr};
+    gemm_store<QT, NMAT>(p, epi, n, rr, scl, acc);
 }
 
 // ---------------------------------------------------------------------------

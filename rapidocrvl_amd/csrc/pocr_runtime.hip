@@ -917,6 +917,110 @@ extern "C" int pocr_time_matvec(pocr_ctx *ctx, const pocr_weight *const *weights
     return POCR_OK;
 }
 
+extern "C" int pocr_time_matvec_batched(pocr_ctx *ctx, const pocr_weight *const *weights, int n_weights,
+                                        const float *x, int m, int iters, float *avg_us) {
+    if (!ctx || !weights || n_weights <= 0 || !x || m <= 0 || iters <= 0 || !avg_us)
+        return fail(POCR_ERR_ARG, "pocr_time_matvec_batched: bad arguments");
+    for (int i = 0; i < n_weights; ++i)
+        if (!weights[i] || weights[i]->rows != weights[0]->rows || weights[i]->cols != weights[0]->cols ||
+            weights[i]->qtype != weights[0]->qtype || weights[i]->ctx != ctx)
+            return fail(POCR_ERR_ARG, "pocr_time_matvec_batched: weights differ in shape/type/context");
+    CHECK_INJECT("time_matvec_batched");
+    CTX_GUARD(ctx);
+    hipStream_t s = ctx->stream;
+    const pocr_weight *w0 = weights[0];
+    RC(ctx->x.ensure((size_t)m * w0->cols * 4));
+    RC(ctx->out.ensure((size_t)m * w0->rows * 4));
+    RC(h2d(s, ctx->x.p, x, (size_t)m * w0->cols * 4));
+    for (int i = 0; i < n_weights; ++i)  // warm-up pass (allocates the digit buffers)
+        RC(batched_gemv(ctx, dev_mat(weights[i]), ctx->x.as<float>(), m, ctx->out.as<float>()));
+    hipEvent_t e0, e1;
+    HIP_TRY(hipEventCreate(&e0));
+    HIP_TRY(hipEventCreate(&e1));
+    HIP_TRY(hipEventRecord(e0, s));
+    for (int it = 0; it < iters; ++it)
+        RC(batched_gemv(ctx, dev_mat(weights[it % n_weights]), ctx->x.as<float>(), m, ctx->out.as<float>()));
+    HIP_TRY(hipEventRecord(e1, s));
+    HIP_TRY(hipEventSynchronize(e1));
+    float ms = 0.0f;
+    HIP_TRY(hipEventElapsedTime(&ms, e0, e1));
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    *avg_us = ms * 1000.0f / (float)iters;
+    return POCR_OK;
+}
+
+extern "C" int pocr_time_attention(pocr_ctx *ctx, int heads, int kv_heads, int head_dim, int cache_len, int n_layers,
+                                   int iters, float *avg_us) {
+    if (!ctx || heads <= 0 || kv_heads <= 0 || heads % kv_heads || cache_len <= 0 || n_layers <= 0 || iters <= 0 ||
+        !avg_us)
+        return fail(POCR_ERR_ARG, "pocr_time_attention: bad arguments");
+    if (head_dim != kHD || heads / kv_heads > kMaxGroup)
+        return fail(POCR_ERR_UNSUPPORTED, "pocr_time_attention: head_dim 128 and GQA group <= 8 only");
+    const int nsplit = attn_nsplit(cache_len);
+    if (nsplit > kMaxSplits) return fail(POCR_ERR_UNSUPPORTED, "pocr_time_attention: cache above %d rows",
+                                         kMaxSplits * kMaxChunk);
+    CHECK_INJECT("time_attention");
+    CTX_GUARD(ctx);
+    hipStream_t s = ctx->stream;
+    const size_t kvd = (size_t)kv_heads * kHD;
+    const size_t layer_floats = 2 * (size_t)cache_len * kvd;
+    RC(ctx->kc.ensure(layer_floats * n_layers * 4));
+    RC(ctx->x.ensure((size_t)(heads + 2 * kv_heads) * kHD * 4));
+    RC(ctx->out.ensure((size_t)heads * kHD * 4));
+    RC(ctx->part.ensure((size_t)kv_heads * nsplit * kMaxGroup * kRec * 4));
+    RC(ctx->state.ensure(sizeof(StepState)));
+    // cache rows and q/k/v hold 1/128 (the values do not change the work)
+    HIP_TRY(hipMemsetD32Async((hipDeviceptr_t)ctx->kc.p, 0x3C000000, layer_floats * n_layers, s));
+    HIP_TRY(hipMemsetD32Async((hipDeviceptr_t)ctx->x.p, 0x3C000000, (size_t)(heads + 2 * kv_heads) * kHD, s));
+    StepState hs{};
+    hs.len = cache_len;
+    hs.clen = cache_len - 1;  // each launch re-appends the last row
+    hs.cap = cache_len;
+    hs.half = kHD / 2;
+    hs.has_rope = 1;
+    for (int i = 0; i < kHD / 2; ++i) {
+        hs.cos_t[i] = 1.0f;
+        hs.sin_t[i] = 0.0f;
+    }
+    HIP_TRY(hipMemcpyAsync(ctx->state.p, &hs, sizeof(hs), hipMemcpyHostToDevice, s));
+    HIP_TRY(hipStreamSynchronize(s));  // hs is a stack object
+    AttnParams a{};
+    a.q = ctx->x.as<float>();
+    a.k_new = a.q + (size_t)heads * kHD;
+    a.v_new = a.k_new + kvd;
+    a.st = ctx->state.as<StepState>();
+    a.part = ctx->part.as<float>();
+    a.head_out = ctx->out.as<float>();
+    a.heads = heads;
+    a.kvh = kv_heads;
+    a.nsplit = nsplit;
+    a.rows_cap = cache_len;
+    a.scale = (float)(1.0 / std::sqrt((double)kHD));
+    auto launch = [&](int layer) {
+        a.kc = ctx->kc.as<float>() + layer * layer_floats;
+        a.vc = a.kc + (size_t)cache_len * kvd;
+        hipLaunchKernelGGL(k_attn_decode, dim3(kv_heads, nsplit), dim3(kThreads), 0, s, a);
+        hipLaunchKernelGGL(k_attn_merge, dim3(heads), dim3(kHD), 0, s, a);
+    };
+    for (int l = 0; l < n_layers; ++l) launch(l);
+    HIP_TRY(hipGetLastError());
+    hipEvent_t e0, e1;
+    HIP_TRY(hipEventCreate(&e0));
+    HIP_TRY(hipEventCreate(&e1));
+    HIP_TRY(hipEventRecord(e0, s));
+    for (int it = 0; it < iters; ++it) launch(it % n_layers);
+    HIP_TRY(hipEventRecord(e1, s));
+    HIP_TRY(hipEventSynchronize(e1));
+    HIP_TRY(hipGetLastError());
+    float ms = 0.0f;
+    HIP_TRY(hipEventElapsedTime(&ms, e0, e1));
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    *avg_us = ms * 1000.0f / (float)iters;
+    return POCR_OK;
+}
+
 // ---------------------------------------------------------------------------
 // the decoder step on the device
 // ---------------------------------------------------------------------------

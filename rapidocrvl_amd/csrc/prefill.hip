@@ -42,6 +42,22 @@ int launch_gemm_t(hipStream_t s, int qtype, const GemmParams &p, int epi, int np
     return POCR_OK;
 }
 
+// small M (≤ 16 tokens): 16-row workgroups whose waves split K
+template <int NMAT>
+int launch_gemm_small_t(hipStream_t s, int qtype, const GemmParams &p, int epi) {
+    const dim3 grid(p.rows / 16);
+    switch (qtype) {
+    case QT_Q8: hipLaunchKernelGGL((k_gemm_small<QT_Q8, NMAT>), grid, dim3(kThreads), 0, s, p, epi); break;
+    case QT_Q4: hipLaunchKernelGGL((k_gemm_small<QT_Q4, NMAT>), grid, dim3(kThreads), 0, s, p, epi); break;
+    case QT_Q6: hipLaunchKernelGGL((k_gemm_small<QT_Q6, NMAT>), grid, dim3(kThreads), 0, s, p, epi); break;
+    default: return fail(POCR_ERR_UNSUPPORTED, "gemm: qtype %d", qtype);
+    }
+    HIP_TRY(hipGetLastError());
+    return POCR_OK;
+}
+
+bool small_shape_ok(int rows, int K) { return rows % 16 == 0 && K % (kGemmK * kWaves) == 0 && K <= kMaxCols; }
+
 // npad: token rows of the digit planes, a multiple of 32
 int launch_gemm(hipStream_t s, int qtype, int nmat, const GemmParams &p, int epi, int npad) {
     if (nmat == 2) return launch_gemm_t<2, 1>(s, qtype, p, epi, npad);
@@ -137,7 +153,8 @@ int batched_gemv(pocr_ctx *ctx, const DevMat &w, const float *x, int m, float *o
         }
         return POCR_OK;
     }
-    const int npad = round_up(m, 32);
+    const bool small = m <= 16 && small_shape_ok(w.rows, w.cols);
+    const int npad = small ? 16 : round_up(m, 32);
     RC(ctx->gxd.ensure((size_t)3 * npad * w.cols));
     RC(ctx->gxs.ensure((size_t)npad * 4));
     RC(ctx->gxb.ensure((size_t)npad * 16));
@@ -162,6 +179,7 @@ int batched_gemv(pocr_ctx *ctx, const DevMat &w, const float *x, int m, float *o
     p.ntok = m;
     p.out = out;
     p.out_stride = w.rows;
+    if (small) return launch_gemm_small_t<1>(s, w.qtype, p, G_PLAIN);
     return launch_gemm(s, w.qtype, 1, p, G_PLAIN, npad);
 }
 

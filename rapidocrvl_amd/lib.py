@@ -81,6 +81,8 @@ _SIGS = {
     "pocr_seq_read_kv": (_i, [_vp, _i, _vp, _vp]),
     "pocr_seq_truncate": (_i, [_vp, _i]),
     "pocr_time_matvec": (_i, [_vp, _vp, _i, _vp, _i, _vp]),
+    "pocr_time_matvec_batched": (_i, [_vp, _vp, _i, _vp, _i, _i, _vp]),
+    "pocr_time_attention": (_i, [_vp, _i, _i, _i, _i, _i, _i, _vp]),
     "pocr_seq_write_kv": (_i, [_vp, _i, _vp, _vp, _i]),
     "pocr_step": (_i, [_vp, _vp, _vp, _i, _vp, _vp]),
     "pocr_prefill": (_i, [_vp, _i, _vp, _vp, _vp, _vp]),
@@ -283,6 +285,20 @@ class Context:
         arr = (_vp * len(weights))(*[w.h for w in weights])
         us = np.zeros(1, np.float32)
         check(load().pocr_time_matvec(self.h, arr, len(weights), _ptr(x), iters, _ptr(us)))
+        return float(us[0])
+
+    def time_matvec_batched(self, weights, x, iters):
+        """Average µs per batched GEMV (x: [m][cols]) rotating over `weights`."""
+        x = _f32(x)
+        arr = (_vp * len(weights))(*[w.h for w in weights])
+        us = np.zeros(1, np.float32)
+        check(load().pocr_time_matvec_batched(self.h, arr, len(weights), _ptr(x), x.shape[0], iters, _ptr(us)))
+        return float(us[0])
+
+    def time_attention(self, heads, kv_heads, head_dim, cache_len, n_layers, iters):
+        """Average µs of one decode-attention call over cache_len rows."""
+        us = np.zeros(1, np.float32)
+        check(load().pocr_time_attention(self.h, heads, kv_heads, head_dim, cache_len, n_layers, iters, _ptr(us)))
         return float(us[0])
 
     def text_attention(self, q, k_cache, v_cache, cache_len, heads, kv_heads, head_dim):
