@@ -21,20 +21,9 @@
 
 namespace pocr {
 
-typedef int v4i __attribute__((ext_vector_type(4)));
-
 constexpr int kGemmK = 64;       // K per MFMA step
 constexpr int kGemmWaveRows = 64;  // rows per wave (4 blocks of 16)
 constexpr int kGemmRows = kGemmWaveRows * kWaves;  // rows per workgroup
-
-// Within each 16-column group the K order is a permutation shared by the
-// weights and the activation digits: Q4 puts the group's even columns first
-// (the low nibbles of its 8 packed bytes), then the odd ones; Q8/Q6 keep the
-// natural order.
-template <int QT>
-__host__ __device__ constexpr int digit_pos16(int c) {
-    return QT == QT_Q4 ? ((c & 1) ? 8 + (c >> 1) : (c >> 1)) : c;
-}
 
 // ---------------------------------------------------------------------------
 // Activation digitizer: one workgroup per token row.  y = x (or x·w with the

@@ -114,6 +114,17 @@ struct Chunk {
     uint32_t d[4];
 };
 
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+// Within each 16-column group the K order of an int8 MFMA is a permutation
+// shared by the weights and the activation digits: Q4 puts the group's even
+// columns first (the low nibbles of its 8 packed bytes), then the odd ones;
+// Q8/Q6 keep the natural order.
+template <int QT>
+__host__ __device__ constexpr int digit_pos16(int c) {
+    return QT == QT_Q4 ? ((c & 1) ? 8 + (c >> 1) : (c >> 1)) : c;
+}
+
 template <int QT>
 __device__ __forceinline__ Chunk load_chunk(const uint8_t *p) {
     Chunk c;
@@ -319,8 +330,8 @@ __device__ __forceinline__ float xchg(float v) {
 // One reduce-scatter step over N entries of NM floats: lanes whose step bit
 // is set keep the upper half (and receive it from the partner); with one
 // entry left the step is a butterfly add.
-template <int N, int NM, int S, int BIT>
-__device__ __forceinline__ void rs_step(float (&v)[8][NM], int lane) {
+template <int N, int NM, int S, int BIT, int CAP>
+__device__ __forceinline__ void rs_step(float (&v)[CAP][NM], int lane) {
     if constexpr (N > 1) {
         const bool hi = (lane & BIT) != 0;
 #pragma unroll
@@ -339,8 +350,9 @@ __device__ __forceinline__ void rs_step(float (&v)[8][NM], int lane) {
 
 // Sums U entries (of NM floats) over the LPR lanes of a row group.  Lane
 // u·(LPR/U) ends up with the full sum of entry u in v[0].
-template <int LPR, int U, int NM>
-__device__ __forceinline__ void reduce_scatter(float (&v)[8][NM], int lane) {
+template <int LPR, int U, int NM, int CAP>
+__device__ __forceinline__ void reduce_scatter(float (&v)[CAP][NM], int lane) {
+    static_assert(U <= CAP && U <= LPR, "entries exceed the array or the lanes");
     constexpr int N1 = U, N2 = N1 > 1 ? N1 / 2 : 1, N3 = N2 > 1 ? N2 / 2 : 1, N4 = N3 > 1 ? N3 / 2 : 1;
     if constexpr (LPR == 64) {
         constexpr int N5 = N4 > 1 ? N4 / 2 : 1, N6 = N5 > 1 ? N5 / 2 : 1;
@@ -371,6 +383,18 @@ __device__ __forceinline__ float wave_sum(float v) {
     v += xchg<XS32>(v);
     return v;
 }
+
+// Maximum over the 64 lanes of a wave, the same value in every lane.
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, xchg<XQ1>(v));
+    v = fmaxf(v, xchg<XQ2>(v));
+    v = fmaxf(v, xchg<XM8>(v));
+    v = fmaxf(v, xchg<XM16>(v));
+    v = fmaxf(v, xchg<XS16>(v));
+    v = fmaxf(v, xchg<XS32>(v));
+    return v;
+}
+
 
 // ---------------------------------------------------------------------------
 // Activation prologue.  Thread t owns 8 consecutive columns per pass (2048
@@ -732,7 +756,9 @@ __device__ __forceinline__ void load_group(const SegSel &sel, int row_bytes, int
 // U·CPL·NMAT 16-byte loads in flight.  The U row sums are reduced together
 // with one reduce-scatter, leaving row u's sum in lane u·(LPR/U).
 // TAG only separates instances for profiling (TAG=1: the timing entry point).
-template <int QT, int LPR, int CPL, int U, int NMAT, int TAG = 0>
+// ONE: the grid gives every wave at most one group (no row loop, no prefetch
+// registers), for the large single-matrix launch.
+template <int QT, int LPR, int CPL, int U, int NMAT, int TAG = 0, bool ONE = false>
 __global__ void __launch_bounds__(kThreads) k_gemv(GemvParams p, int pro, int epi) {
     // No step-state check up front: a GEMV writes only step scratch (the
     // residual stream, q/k/v, gate) and never indexes by the step state, so a
@@ -792,7 +818,7 @@ __global__ void __launch_bounds__(kThreads) k_gemv(GemvParams p, int pro, int ep
     // one group: row sums, reduce-scatter, epilogue by the writer lanes
     auto compute = [&](int gg, const Chunk (&wc)[U][NMAT][CPL], const float (&sc)[NMAT], float rs) {
         const int r = (gg * U + my_u) * RPW + sub;
-        float acc[8][NMAT];
+        float acc[U > 8 ? U : 8][NMAT];
 #pragma unroll
         for (int u = 0; u < U; ++u)
 #pragma unroll
@@ -809,7 +835,7 @@ __global__ void __launch_bounds__(kThreads) k_gemv(GemvParams p, int pro, int ep
     // epilogue operands before it is computed (software pipeline of depth
     // one); the last one is peeled off, so no wave requests rows it does not
     // use and every path keeps static wait counts.
-    for (; g + gstride < ngroups; g += gstride) {
+    if constexpr (!ONE) for (; g + gstride < ngroups; g += gstride) {
         Chunk wn[U][NMAT][CPL];
         float scln[NMAT], residn;
         {
@@ -1317,16 +1343,6 @@ static __global__ void __launch_bounds__(kThreads) k_attn_decode(AttnParams args
 // first batch of records is requested before the step state is read; splits
 // at or past the step's length hold stale records and are skipped.
 constexpr int kMaxSplits = 1024;  // cache capacity ≤ 65536 rows
-
-__device__ __forceinline__ float wave_max(float v) {
-    v = fmaxf(v, xchg<XQ1>(v));
-    v = fmaxf(v, xchg<XQ2>(v));
-    v = fmaxf(v, xchg<XM8>(v));
-    v = fmaxf(v, xchg<XM16>(v));
-    v = fmaxf(v, xchg<XS16>(v));
-    v = fmaxf(v, xchg<XS32>(v));
-    return v;
-}
 
 static __global__ void __launch_bounds__(kHD) k_attn_merge(AttnParams args) {
     AttnParams p = args;

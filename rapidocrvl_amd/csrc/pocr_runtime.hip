@@ -185,14 +185,14 @@ DevMat pocr::dev_mat(const pocr_weight *w) {
 // ---------------------------------------------------------------------------
 // GEMV dispatch
 // ---------------------------------------------------------------------------
-template <int QT, int NMAT, int U, int TAG = 0>
+template <int QT, int NMAT, int U, int TAG = 0, bool ONE = false>
 static bool gemv_fast_kernel(int lpr, int cpl, const void **fn) {
-#define POCR_K(L, C)                                                           \
-    if (lpr == L && cpl == C) {                                                \
-        *fn = reinterpret_cast<const void *>(&k_gemv<QT, L, C, U, NMAT, TAG>); \
-        return true;                                                           \
+#define POCR_K(L, C)                                                                \
+    if (lpr == L && cpl == C) {                                                     \
+        *fn = reinterpret_cast<const void *>(&k_gemv<QT, L, C, U, NMAT, TAG, ONE>); \
+        return true;                                                                \
     }
-    if constexpr (U == 8) {
+    if constexpr (U > 2) {  // the large single-matrix shape: one chunk per lane
         POCR_K(64, 1)
         POCR_K(32, 1)
     } else {
@@ -208,11 +208,26 @@ static bool gemv_fast_kernel(int lpr, int cpl, const void **fn) {
     return false;
 }
 
+// Launch shape of the large single-matrix GEMV (the LM head): rows per lane
+// group and step, and the workgroup cap (rows loop inside the kernel).
+#ifndef POCR_BIG_U
+#define POCR_BIG_U 8
+#endif
+#ifndef POCR_BIG_GRID
+#define POCR_BIG_GRID 4096  // enough for one group per wave up to 262144 rows
+#endif
+constexpr int kBigU = POCR_BIG_U;
+
+// one: every wave gets at most one row group (the big launch covers them all)
 template <int QT>
-static bool pick_fast(int nmat, int u, int tag, int lpr, int cpl, const void **fn) {
+static bool pick_fast(int nmat, int u, int tag, int lpr, int cpl, bool one, const void **fn) {
     if (nmat == 2) return gemv_fast_kernel<QT, 2, 2>(lpr, cpl, fn);
-    if (tag == 1) return u == 8 ? gemv_fast_kernel<QT, 1, 8, 1>(lpr, cpl, fn) : gemv_fast_kernel<QT, 1, 2, 1>(lpr, cpl, fn);
-    return u == 8 ? gemv_fast_kernel<QT, 1, 8>(lpr, cpl, fn) : gemv_fast_kernel<QT, 1, 2>(lpr, cpl, fn);
+    if (u == kBigU && one)
+        return tag == 1 ? gemv_fast_kernel<QT, 1, kBigU, 1, true>(lpr, cpl, fn)
+                        : gemv_fast_kernel<QT, 1, kBigU, 0, true>(lpr, cpl, fn);
+    if (tag == 1)
+        return u == kBigU ? gemv_fast_kernel<QT, 1, kBigU, 1>(lpr, cpl, fn) : gemv_fast_kernel<QT, 1, 2, 1>(lpr, cpl, fn);
+    return u == kBigU ? gemv_fast_kernel<QT, 1, kBigU>(lpr, cpl, fn) : gemv_fast_kernel<QT, 1, 2>(lpr, cpl, fn);
 }
 
 struct GemvPlan {
@@ -248,24 +263,31 @@ static int plan_gemv(int qtype, int nmat, int rows, int cols, const DevMat *mats
     }
     bool ok = false;
     // big row counts: 8 rows per lane group and step (more bytes in flight)
-    const int u = (fast && nmat == 1 && cpl == 1 && rows >= 8192) ? 8 : 2;
+    const bool big = fast && nmat == 1 && cpl == 1 && rows >= 8192;
+    const int u = big ? kBigU : 2;
+    if (big) max_grid = std::max(max_grid, POCR_BIG_GRID);
     // row groups must not straddle segments
     if (fast && nmat == 1 && seg_end) {
         const int rg = (64 / lpr) * u;
         for (int i = 0; i < 2; ++i)
             if (seg_end[i] % rg != 0) fast = false;
     }
+    int grid = 1;
+    bool one = false;
     if (fast) {
-        if (qtype == POCR_Q4) ok = pick_fast<QT_Q4>(nmat, u, tag, lpr, cpl, &plan->fn);
-        if (qtype == POCR_Q8) ok = pick_fast<QT_Q8>(nmat, u, tag, lpr, cpl, &plan->fn);
-        if (qtype == POCR_Q6) ok = pick_fast<QT_Q6>(nmat, u, tag, lpr, cpl, &plan->fn);
+        const int rows_per_group = (64 / lpr) * u;
+        const int groups = (rows + rows_per_group - 1) / rows_per_group;
+        const int want = (groups + kWaves - 1) / kWaves;
+        grid = std::max(1, std::min(want, max_grid));
+        one = big && grid == want;
+        if (qtype == POCR_Q4) ok = pick_fast<QT_Q4>(nmat, u, tag, lpr, cpl, one, &plan->fn);
+        if (qtype == POCR_Q8) ok = pick_fast<QT_Q8>(nmat, u, tag, lpr, cpl, one, &plan->fn);
+        if (qtype == POCR_Q6) ok = pick_fast<QT_Q6>(nmat, u, tag, lpr, cpl, one, &plan->fn);
     }
     if (ok) {
         plan->lds = qtype == POCR_Q4 ? gemv_lds_bytes<QT_Q4>(cols)
                                      : (qtype == POCR_Q8 ? gemv_lds_bytes<QT_Q8>(cols) : gemv_lds_bytes<QT_Q6>(cols));
-        const int rows_per_group = (64 / lpr) * u;
-        const int groups = (rows + rows_per_group - 1) / rows_per_group;
-        plan->grid = std::max(1, std::min((groups + kWaves - 1) / kWaves, max_grid));
+        plan->grid = grid;
     } else {
         plan->fn = nmat == 1 ? reinterpret_cast<const void *>(&k_gemv_any<1>)
                              : reinterpret_cast<const void *>(&k_gemv_any<2>);
