@@ -156,6 +156,11 @@ int pocr_text_attention(pocr_ctx *ctx, const float *q, const float *k_cache, con
 int pocr_time_matvec(pocr_ctx *ctx, const pocr_weight *const *weights, int n_weights, const float *x, int iters,
                      float *avg_us);
 
+/* The same for the greedy LM-head launch (MatVecArgmaxQ*, argmax_quant.go:
+ * 11-433): the argmax kernel the device decode loop runs, no logits written. */
+int pocr_time_matvec_argmax(pocr_ctx *ctx, const pocr_weight *const *weights, int n_weights, const float *x,
+                            int iters, float *avg_us);
+
 /* The same for the batched GEMV: m rows of x (m*cols floats) per launch pair
  * (digit planes + MFMA GEMM).  Measurement counterpart of the reference's
  * M-row benchmarks (internal/tensor/model_dims_bench_test.go). */

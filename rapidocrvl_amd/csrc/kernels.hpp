@@ -237,6 +237,10 @@ struct XDigits {
     int d[CPL][DigitTraits<QT>::NDW][3];
     int bias[CPL][3];
     float scale[CPL];
+    // Q4: the planes' int32 sums are combined in integer before one convert
+    // (bias and scale of the combination below)
+    int bias_comb[CPL];
+    float scale_comb[CPL];
 };
 
 // column (within a chunk) of byte m of digit dword k: Q4 dword 2k' holds the
@@ -265,10 +269,12 @@ __host__ __device__ constexpr size_t gemv_lds_bytes(int cols) {
     return (size_t)(cols / QTraits<QT>::W) * DigitRec<QT>::RS * 4;
 }
 
-__device__ __forceinline__ void dot3(int code4, const int (&x)[3], int (&a)[3]) {
-    a[0] = __builtin_amdgcn_sdot4(code4, x[0], a[0], false);
-    a[1] = __builtin_amdgcn_sdot4(code4, x[1], a[1], false);
-    a[2] = __builtin_amdgcn_sdot4(code4, x[2], a[2], false);
+// code4 · digits of the first NPL planes (NPL = 3: x to 2^-15 of the chunk
+// scale; NPL = 2: to 2^-8)
+template <int NPL>
+__device__ __forceinline__ void dotp(int code4, const int (&x)[3], int (&a)[3]) {
+#pragma unroll
+    for (int pl = 0; pl < NPL; ++pl) a[pl] = __builtin_amdgcn_sdot4(code4, x[pl], a[pl], false);
 }
 
 // six-bit fields of one 24-bit group spread into the four bytes of a dword
@@ -280,7 +286,7 @@ __device__ __forceinline__ int spread6(uint32_t g) {
     return (int)r;
 }
 
-template <int QT, int CPL>
+template <int QT, int CPL, int NPL = 3>
 __device__ __forceinline__ float row_dot(const Chunk (&w)[CPL], const XDigits<QT, CPL> &xd) {
     float r = 0.0f;
 #pragma unroll
@@ -288,24 +294,31 @@ __device__ __forceinline__ float row_dot(const Chunk (&w)[CPL], const XDigits<QT
         int a[3] = {0, 0, 0};
         if constexpr (QT == QT_Q8) {
 #pragma unroll
-            for (int k = 0; k < 4; ++k) dot3((int)w[j].d[k], xd.d[j][k], a);
+            for (int k = 0; k < 4; ++k) dotp<NPL>((int)w[j].d[k], xd.d[j][k], a);
         } else if constexpr (QT == QT_Q4) {
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
-                dot3((int)(w[j].d[k] & 0x0F0F0F0Fu), xd.d[j][2 * k], a);
-                dot3((int)((w[j].d[k] >> 4) & 0x0F0F0F0Fu), xd.d[j][2 * k + 1], a);
+                dotp<NPL>((int)(w[j].d[k] & 0x0F0F0F0Fu), xd.d[j][2 * k], a);
+                dotp<NPL>((int)((w[j].d[k] >> 4) & 0x0F0F0F0Fu), xd.d[j][2 * k + 1], a);
             }
         } else {
             const uint32_t d0 = w[j].d[0], d1 = w[j].d[1], d2 = w[j].d[2];
-            dot3(spread6(d0), xd.d[j][0], a);
-            dot3(spread6(__builtin_amdgcn_alignbit(d1, d0, 24)), xd.d[j][1], a);
-            dot3(spread6(__builtin_amdgcn_alignbit(d2, d1, 16)), xd.d[j][2], a);
-            dot3(spread6(d2 >> 8), xd.d[j][3], a);
+            dotp<NPL>(spread6(d0), xd.d[j][0], a);
+            dotp<NPL>(spread6(__builtin_amdgcn_alignbit(d1, d0, 24)), xd.d[j][1], a);
+            dotp<NPL>(spread6(__builtin_amdgcn_alignbit(d2, d1, 16)), xd.d[j][2], a);
+            dotp<NPL>(spread6(d2 >> 8), xd.d[j][3], a);
         }
-        const float f0 = (float)(a[0] - xd.bias[j][0]);
-        const float f1 = (float)(a[1] - xd.bias[j][1]);
-        const float f2 = (float)(a[2] - xd.bias[j][2]);
-        r = fmaf(xd.scale[j], fmaf(f2, 1.0f / 16384.0f, fmaf(f1, 1.0f / 128.0f, f0)), r);
+        if constexpr (QT == QT_Q4) {
+            // |a0| ≤ 32·15·127 < 2^16: a0·2^14 + a1·2^7 + a2 stays inside int32
+            const int comb = NPL == 3 ? a[0] * 16384 + a[1] * 128 + a[2] : a[0] * 128 + a[1];
+            r = fmaf(xd.scale_comb[j], (float)(comb - xd.bias_comb[j]), r);
+        } else {
+            const float f0 = (float)(a[0] - xd.bias[j][0]);
+            const float f1 = (float)(a[1] - xd.bias[j][1]);
+            const float f = NPL == 3 ? fmaf((float)(a[2] - xd.bias[j][2]), 1.0f / 16384.0f, fmaf(f1, 1.0f / 128.0f, f0))
+                                     : fmaf(f1, 1.0f / 128.0f, f0);
+            r = fmaf(xd.scale[j], f, r);
+        }
     }
     return r;
 }
@@ -528,7 +541,7 @@ __device__ __forceinline__ float x_digits(const XRegs &r, bool norm, int cols, f
 }
 
 // The lane's CPL chunk records (chunks l + j·LPR) → registers.
-template <int QT, int LPR, int CPL>
+template <int QT, int LPR, int CPL, int NPL = 3>
 __device__ __forceinline__ void load_digits(const int *lds, int l, XDigits<QT, CPL> &xd) {
     constexpr int NDW = DigitRec<QT>::NDW, RS = DigitRec<QT>::RS;
 #pragma unroll
@@ -551,6 +564,13 @@ __device__ __forceinline__ void load_digits(const int *lds, int l, XDigits<QT, C
         xd.bias[j][1] = v[NDW * 3 + 1];
         xd.bias[j][2] = v[NDW * 3 + 2];
         xd.scale[j] = __int_as_float(v[NDW * 3 + 3]);
+        if constexpr (NPL == 3) {
+            xd.bias_comb[j] = xd.bias[j][0] * 16384 + xd.bias[j][1] * 128 + xd.bias[j][2];
+            xd.scale_comb[j] = xd.scale[j] * (1.0f / 16384.0f);  // exact: powers of two
+        } else {
+            xd.bias_comb[j] = xd.bias[j][0] * 128 + xd.bias[j][1];
+            xd.scale_comb[j] = xd.scale[j] * (1.0f / 128.0f);
+        }
     }
 }
 
@@ -668,17 +688,45 @@ __device__ __forceinline__ bool oproj_in_place(const GemvParams &p) {
     return !(p.quirk && (clen == 0 || clen >= 6));
 }
 
+__device__ __forceinline__ uint32_t ordered_bits(float v) {
+    const uint32_t b = __float_as_uint(v);
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+// unsigned max / signed min over the 64 lanes of a wave (DPP and swizzle
+// exchanges of the bit pattern), the same value in every lane
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    v = max(v, __float_as_uint(xchg<XQ1>(__uint_as_float(v))));
+    v = max(v, __float_as_uint(xchg<XQ2>(__uint_as_float(v))));
+    v = max(v, __float_as_uint(xchg<XM8>(__uint_as_float(v))));
+    v = max(v, __float_as_uint(xchg<XM16>(__uint_as_float(v))));
+    v = max(v, __float_as_uint(xchg<XS16>(__uint_as_float(v))));
+    v = max(v, __float_as_uint(xchg<XS32>(__uint_as_float(v))));
+    return v;
+}
+__device__ __forceinline__ int wave_min_i32(int v) {
+    v = min(v, __float_as_int(xchg<XQ1>(__int_as_float(v))));
+    v = min(v, __float_as_int(xchg<XQ2>(__int_as_float(v))));
+    v = min(v, __float_as_int(xchg<XM8>(__int_as_float(v))));
+    v = min(v, __float_as_int(xchg<XM16>(__int_as_float(v))));
+    v = min(v, __float_as_int(xchg<XS16>(__int_as_float(v))));
+    v = min(v, __float_as_int(xchg<XS32>(__int_as_float(v))));
+    return v;
+}
+
+// Greedy argmax of the workgroup's rows into its slot: the largest score
+// (compared as order-preserving bits, like the 64-bit key), then the lowest
+// row holding it (argmax_quant.go:255-262: ties keep the first index).
 __device__ __forceinline__ void argmax_finish(const GemvParams &p, float best_v, int best_r, float *red) {
-    unsigned long long k = best_r == 0x7FFFFFFF ? 0ull : argmax_key(best_v, best_r);
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        const unsigned long long o = __shfl_xor(k, off, 64);
-        k = o > k ? o : k;
-    }
+    const bool has = best_r != 0x7FFFFFFF;
+    const uint32_t ob = wave_max_u32(has ? ordered_bits(best_v) : 0u);
+    const int rmin = wave_min_i32(has && ordered_bits(best_v) == ob ? best_r : 0x7FFFFFFF);
     unsigned long long *kred = reinterpret_cast<unsigned long long *>(red);
     const int wave = threadIdx.x >> 6;
-    __syncthreads();
-    if ((threadIdx.x & 63) == 0) kred[wave] = k;
+    __syncthreads();  // red may still be read by the prologue's reductions
+    if ((threadIdx.x & 63) == 0)
+        kred[wave] = rmin == 0x7FFFFFFF ? 0ull
+                                        : (((unsigned long long)ob << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)rmin));
     __syncthreads();
     if (threadIdx.x == 0) {
         unsigned long long m = kred[0];
@@ -758,8 +806,10 @@ __device__ __forceinline__ void load_group(const SegSel &sel, int row_bytes, int
 // TAG only separates instances for profiling (TAG=1: the timing entry point).
 // ONE: the grid gives every wave at most one group (no row loop, no prefetch
 // registers), for the large single-matrix launch.
-template <int QT, int LPR, int CPL, int U, int NMAT, int TAG = 0, bool ONE = false>
-__global__ void __launch_bounds__(kThreads) k_gemv(GemvParams p, int pro, int epi) {
+// NPL: digit planes of the activation (3, or 2 for the LM head, whose result
+// feeds only the argmax: x to 2^-15 of each 32-column chunk's maximum)
+template <int QT, int LPR, int CPL, int U, int NMAT, int TAG, bool ONE, int NPL>
+__device__ __forceinline__ void gemv_body(GemvParams p, int pro, int epi) {
     // No step-state check up front: a GEMV writes only step scratch (the
     // residual stream, q/k/v, gate) and never indexes by the step state, so a
     // failed step needs no guard here and the first loads wait for nothing.
@@ -810,7 +860,7 @@ __global__ void __launch_bounds__(kThreads) k_gemv(GemvParams p, int pro, int ep
     }
     const float xscale = x_digits<QT>(xr, norm, cols, p.eps, lds, red);
     XDigits<QT, CPL> xd;
-    load_digits<QT, LPR, CPL>(lds, l, xd);
+    load_digits<QT, LPR, CPL, NPL>(lds, l, xd);
     const bool in_place = epi == EPI_OPROJ ? oproj_in_place(p) : false;
     float best_v = -INFINITY;
     int best_r = 0x7FFFFFFF;
@@ -822,7 +872,7 @@ __global__ void __launch_bounds__(kThreads) k_gemv(GemvParams p, int pro, int ep
 #pragma unroll
         for (int u = 0; u < U; ++u)
 #pragma unroll
-            for (int mi = 0; mi < NMAT; ++mi) acc[u][mi] = row_dot<QT, CPL>(wc[u][mi], xd);
+            for (int mi = 0; mi < NMAT; ++mi) acc[u][mi] = row_dot<QT, CPL, NPL>(wc[u][mi], xd);
         reduce_scatter<LPR, U, NMAT>(acc, lane);
         if (writer && r < rows) {
             float sv[NMAT];
@@ -860,6 +910,17 @@ __global__ void __launch_bounds__(kThreads) k_gemv(GemvParams p, int pro, int ep
     }
     if (g < ngroups) compute(g, w, scl, resid);
     if (epi == EPI_ARGMAX) argmax_finish(p, best_v, best_r, red);
+}
+
+template <int QT, int LPR, int CPL, int U, int NMAT, int TAG = 0, int NPL = 3>
+__global__ void __launch_bounds__(kThreads) k_gemv(GemvParams p, int pro, int epi) {
+    gemv_body<QT, LPR, CPL, U, NMAT, TAG, false, NPL>(p, pro, epi);
+}
+
+// One row group per wave (no row loop, no prefetch registers).
+template <int QT, int LPR, int CPL, int U, int NMAT, int TAG = 0, int NPL = 3>
+__global__ void __launch_bounds__(kThreads) k_gemv_one(GemvParams p, int pro, int epi) {
+    gemv_body<QT, LPR, CPL, U, NMAT, TAG, true, NPL>(p, pro, epi);
 }
 
 // Any shape (tiny test matrices, odd column counts): one wavefront per row,

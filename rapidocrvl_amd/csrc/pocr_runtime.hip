@@ -185,12 +185,18 @@ DevMat pocr::dev_mat(const pocr_weight *w) {
 // ---------------------------------------------------------------------------
 // GEMV dispatch
 // ---------------------------------------------------------------------------
-template <int QT, int NMAT, int U, int TAG = 0, bool ONE = false>
+template <int QT, int L, int C, int U, int NMAT, int TAG, bool ONE, int NPL>
+static const void *gemv_fn() {
+    if constexpr (ONE) return reinterpret_cast<const void *>(&k_gemv_one<QT, L, C, U, NMAT, TAG, NPL>);
+    else return reinterpret_cast<const void *>(&k_gemv<QT, L, C, U, NMAT, TAG, NPL>);
+}
+
+template <int QT, int NMAT, int U, int TAG = 0, bool ONE = false, int NPL = 3>
 static bool gemv_fast_kernel(int lpr, int cpl, const void **fn) {
-#define POCR_K(L, C)                                                                \
-    if (lpr == L && cpl == C) {                                                     \
-        *fn = reinterpret_cast<const void *>(&k_gemv<QT, L, C, U, NMAT, TAG, ONE>); \
-        return true;                                                                \
+#define POCR_K(L, C)                                            \
+    if (lpr == L && cpl == C) {                                 \
+        *fn = gemv_fn<QT, L, C, U, NMAT, TAG, ONE, NPL>();      \
+        return true;                                            \
     }
     if constexpr (U > 2) {  // the large single-matrix shape: one chunk per lane
         POCR_K(64, 1)
@@ -217,17 +223,28 @@ static bool gemv_fast_kernel(int lpr, int cpl, const void **fn) {
 #define POCR_BIG_GRID 4096  // enough for one group per wave up to 262144 rows
 #endif
 constexpr int kBigU = POCR_BIG_U;
+#ifndef POCR_BIG_PLANES
+#define POCR_BIG_PLANES 2
+#endif
+constexpr int kBigPlanes = POCR_BIG_PLANES;
 
-// one: every wave gets at most one row group (the big launch covers them all)
+// one: every wave gets at most one row group (the big launch covers them all);
+// argmax: the greedy LM head, whose scores only feed the argmax, takes
+// kBigPlanes digit planes, every other launch three
+template <int QT, int NPL>
+static bool pick_big(int tag, bool one, int lpr, int cpl, const void **fn) {
+    if (one)
+        return tag == 1 ? gemv_fast_kernel<QT, 1, kBigU, 1, true, NPL>(lpr, cpl, fn)
+                        : gemv_fast_kernel<QT, 1, kBigU, 0, true, NPL>(lpr, cpl, fn);
+    return tag == 1 ? gemv_fast_kernel<QT, 1, kBigU, 1, false, NPL>(lpr, cpl, fn)
+                    : gemv_fast_kernel<QT, 1, kBigU, 0, false, NPL>(lpr, cpl, fn);
+}
+
 template <int QT>
-static bool pick_fast(int nmat, int u, int tag, int lpr, int cpl, bool one, const void **fn) {
+static bool pick_fast(int nmat, int u, int tag, int lpr, int cpl, bool one, bool argmax, const void **fn) {
     if (nmat == 2) return gemv_fast_kernel<QT, 2, 2>(lpr, cpl, fn);
-    if (u == kBigU && one)
-        return tag == 1 ? gemv_fast_kernel<QT, 1, kBigU, 1, true>(lpr, cpl, fn)
-                        : gemv_fast_kernel<QT, 1, kBigU, 0, true>(lpr, cpl, fn);
-    if (tag == 1)
-        return u == kBigU ? gemv_fast_kernel<QT, 1, kBigU, 1>(lpr, cpl, fn) : gemv_fast_kernel<QT, 1, 2, 1>(lpr, cpl, fn);
-    return u == kBigU ? gemv_fast_kernel<QT, 1, kBigU>(lpr, cpl, fn) : gemv_fast_kernel<QT, 1, 2>(lpr, cpl, fn);
+    if (u == kBigU) return argmax ? pick_big<QT, kBigPlanes>(tag, one, lpr, cpl, fn) : pick_big<QT, 3>(tag, one, lpr, cpl, fn);
+    return tag == 1 ? gemv_fast_kernel<QT, 1, 2, 1>(lpr, cpl, fn) : gemv_fast_kernel<QT, 1, 2>(lpr, cpl, fn);
 }
 
 struct GemvPlan {
@@ -239,7 +256,7 @@ struct GemvPlan {
 // Choose the kernel for `rows` outputs of matrices with `cols` columns.
 // max_grid caps the workgroup count (rows loop inside the kernel).
 static int plan_gemv(int qtype, int nmat, int rows, int cols, const DevMat *mats, int nm, int max_grid,
-                     GemvPlan *plan, int tag = 0, const int *seg_end = nullptr) {
+                     GemvPlan *plan, int tag, const int *seg_end, int epi) {
     if (cols > 16384) return fail(POCR_ERR_UNSUPPORTED, "gemv: cols %d > 16384", cols);
     plan->lds = (size_t)cols * 4;
     int W = qtype == POCR_Q4 ? 32 : 16;
@@ -280,9 +297,9 @@ static int plan_gemv(int qtype, int nmat, int rows, int cols, const DevMat *mats
         const int want = (groups + kWaves - 1) / kWaves;
         grid = std::max(1, std::min(want, max_grid));
         one = big && grid == want;
-        if (qtype == POCR_Q4) ok = pick_fast<QT_Q4>(nmat, u, tag, lpr, cpl, one, &plan->fn);
-        if (qtype == POCR_Q8) ok = pick_fast<QT_Q8>(nmat, u, tag, lpr, cpl, one, &plan->fn);
-        if (qtype == POCR_Q6) ok = pick_fast<QT_Q6>(nmat, u, tag, lpr, cpl, one, &plan->fn);
+        if (qtype == POCR_Q4) ok = pick_fast<QT_Q4>(nmat, u, tag, lpr, cpl, one, epi == EPI_ARGMAX, &plan->fn);
+        if (qtype == POCR_Q8) ok = pick_fast<QT_Q8>(nmat, u, tag, lpr, cpl, one, epi == EPI_ARGMAX, &plan->fn);
+        if (qtype == POCR_Q6) ok = pick_fast<QT_Q6>(nmat, u, tag, lpr, cpl, one, epi == EPI_ARGMAX, &plan->fn);
     }
     if (ok) {
         plan->lds = qtype == POCR_Q4 ? gemv_lds_bytes<QT_Q4>(cols)
@@ -314,7 +331,7 @@ GemvParams pocr::gemv_params_1(const pocr_weight *w) {
 int pocr::gemv_launch(hipStream_t s, GemvParams p, int nmat, int pro, int epi, int max_grid) {
     GemvPlan plan;
     const int nm = nmat == 2 ? 2 : (p.seg_end[0] == p.rows ? 1 : (p.seg_end[1] == p.rows ? 2 : 3));
-    int rc = plan_gemv(p.m[0].qtype, nmat, p.rows, p.cols, p.m, nm, max_grid, &plan, 0, p.seg_end);
+    int rc = plan_gemv(p.m[0].qtype, nmat, p.rows, p.cols, p.m, nm, max_grid, &plan, 0, p.seg_end, epi);
     if (rc) return rc;
     return launch_gemv(s, plan, p, pro, epi);
 }
@@ -894,41 +911,40 @@ extern "C" int pocr_seq_truncate(pocr_seq *s, int len) {
     return seq_set_state(s, len);
 }
 
-extern "C" int pocr_time_matvec(pocr_ctx *ctx, const pocr_weight *const *weights, int n_weights, const float *x,
-                                int iters, float *avg_us) {
+static int time_matvec_impl(pocr_ctx *ctx, const pocr_weight *const *weights, int n_weights, const float *x,
+                            int iters, float *avg_us, bool argmax, const char *name) {
     if (!ctx || !weights || n_weights <= 0 || !x || iters <= 0 || !avg_us)
-        return fail(POCR_ERR_ARG, "pocr_time_matvec: bad arguments");
+        return fail(POCR_ERR_ARG, "%s: bad arguments", name);
     for (int i = 0; i < n_weights; ++i)
         if (!weights[i] || weights[i]->rows != weights[0]->rows || weights[i]->cols != weights[0]->cols ||
             weights[i]->qtype != weights[0]->qtype || weights[i]->ctx != ctx)
-            return fail(POCR_ERR_ARG, "pocr_time_matvec: weights differ in shape/type/context");
-    CHECK_INJECT("time_matvec");
+            return fail(POCR_ERR_ARG, "%s: weights differ in shape/type/context", name);
+    CHECK_INJECT(name + 5);  // the op name without "pocr_"
     CTX_GUARD(ctx);
     hipStream_t s = ctx->stream;
     const pocr_weight *w0 = weights[0];
+    const int epi = argmax ? EPI_ARGMAX : EPI_PLAIN;
     RC(ctx->x.ensure((size_t)w0->cols * 4));
     RC(ctx->out.ensure((size_t)w0->rows * 4));
+    RC(ctx->state.ensure(sizeof(StepState)));
     RC(h2d(s, ctx->x.p, x, (size_t)w0->cols * 4));
+    HIP_TRY(hipMemsetAsync(ctx->state.p, 0, sizeof(StepState), s));
     GemvPlan plan;
     DevMat dm = dev_mat(w0);
-    RC(plan_gemv(w0->qtype, 1, w0->rows, w0->cols, &dm, 1, kBigGrid, &plan, 1));
+    RC(plan_gemv(w0->qtype, 1, w0->rows, w0->cols, &dm, 1, kBigGrid, &plan, 1, nullptr, epi));
+    auto params = [&](int i) {
+        GemvParams p = gemv_params_1(weights[i]);
+        p.x = ctx->x.as<float>();
+        p.out = argmax ? nullptr : ctx->out.as<float>();
+        p.st = ctx->state.as<StepState>();  // argmax slots (the key only grows: no reset needed)
+        return p;
+    };
     hipEvent_t e0, e1;
     HIP_TRY(hipEventCreate(&e0));
     HIP_TRY(hipEventCreate(&e1));
-    // warm-up pass over every copy
-    for (int i = 0; i < n_weights; ++i) {
-        GemvParams p = gemv_params_1(weights[i]);
-        p.x = ctx->x.as<float>();
-        p.out = ctx->out.as<float>();
-        RC(launch_gemv(s, plan, p, PRO_COPY, EPI_PLAIN));
-    }
+    for (int i = 0; i < n_weights; ++i) RC(launch_gemv(s, plan, params(i), PRO_COPY, epi));  // warm-up pass
     HIP_TRY(hipEventRecord(e0, s));
-    for (int it = 0; it < iters; ++it) {
-        GemvParams p = gemv_params_1(weights[it % n_weights]);
-        p.x = ctx->x.as<float>();
-        p.out = ctx->out.as<float>();
-        RC(launch_gemv(s, plan, p, PRO_COPY, EPI_PLAIN));
-    }
+    for (int it = 0; it < iters; ++it) RC(launch_gemv(s, plan, params(it % n_weights), PRO_COPY, epi));
     HIP_TRY(hipEventRecord(e1, s));
     HIP_TRY(hipEventSynchronize(e1));
     float ms = 0.0f;
@@ -937,6 +953,16 @@ extern "C" int pocr_time_matvec(pocr_ctx *ctx, const pocr_weight *const *weights
     (void)hipEventDestroy(e1);
     *avg_us = ms * 1000.0f / (float)iters;
     return POCR_OK;
+}
+
+extern "C" int pocr_time_matvec(pocr_ctx *ctx, const pocr_weight *const *weights, int n_weights, const float *x,
+                                int iters, float *avg_us) {
+    return time_matvec_impl(ctx, weights, n_weights, x, iters, avg_us, false, "pocr_time_matvec");
+}
+
+extern "C" int pocr_time_matvec_argmax(pocr_ctx *ctx, const pocr_weight *const *weights, int n_weights,
+                                       const float *x, int iters, float *avg_us) {
+    return time_matvec_impl(ctx, weights, n_weights, x, iters, avg_us, true, "pocr_time_matvec_argmax");
 }
 
 extern "C" int pocr_time_matvec_batched(pocr_ctx *ctx, const pocr_weight *const *weights, int n_weights,

@@ -81,6 +81,7 @@ _SIGS = {
     "pocr_seq_read_kv": (_i, [_vp, _i, _vp, _vp]),
     "pocr_seq_truncate": (_i, [_vp, _i]),
     "pocr_time_matvec": (_i, [_vp, _vp, _i, _vp, _i, _vp]),
+    "pocr_time_matvec_argmax": (_i, [_vp, _vp, _i, _vp, _i, _vp]),
     "pocr_time_matvec_batched": (_i, [_vp, _vp, _i, _vp, _i, _i, _vp]),
     "pocr_time_attention": (_i, [_vp, _i, _i, _i, _i, _i, _i, _vp]),
     "pocr_seq_write_kv": (_i, [_vp, _i, _vp, _vp, _i]),
@@ -285,6 +286,14 @@ class Context:
         arr = (_vp * len(weights))(*[w.h for w in weights])
         us = np.zeros(1, np.float32)
         check(load().pocr_time_matvec(self.h, arr, len(weights), _ptr(x), iters, _ptr(us)))
+        return float(us[0])
+
+    def time_matvec_argmax(self, weights, x, iters):
+        """Average µs per greedy LM-head launch (argmax only) rotating over `weights`."""
+        x = _f32(x)
+        arr = (_vp * len(weights))(*[w.h for w in weights])
+        us = np.zeros(1, np.float32)
+        check(load().pocr_time_matvec_argmax(self.h, arr, len(weights), _ptr(x), iters, _ptr(us)))
         return float(us[0])
 
     def time_matvec_batched(self, weights, x, iters):

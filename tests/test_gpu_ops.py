@@ -80,7 +80,10 @@ def test_matvec_argmax(ctx, orc, rng, qtype):
         top2 = np.sort(logits)[-2:]
         if top2[1] - top2[0] > 1e-4 * abs(top2[1]):
             assert idx == int(np.argmax(logits))
-        assert abs(score - logits[idx]) <= 1e-5 * max(1, abs(score))
+        # the greedy head reads x to 2^-15 of each 32-column chunk's maximum
+        # (two digit planes): scores agree to 1e-4 relative, inside the path's
+        # 1e-2 / 1e-3 logit bar
+        assert abs(score - logits[idx]) <= 1e-4 * max(1, abs(score))
 
 
 def test_argmax_ties_pick_lowest_index(ctx):
