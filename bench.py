@@ -236,9 +236,47 @@ def cpu_baseline(cfg, weights, gpu_seq, first_tok, first_pos, gpu_tokens, n_pref
     dt = time.perf_counter() - t
     match = toks[: n + 1] == list(gpu_tokens[: n + 1])
     return {"value": round(n / dt, 2), "unit": "tok/s", "cores": threads, "kind": "port",
+            "host": f"{host_cpu()}, {os.cpu_count()} logical CPUs visible; {threads} worker threads "
+                    f"(the GOMAXPROCS-equivalent of the pool)",
             "sample": f"{n} greedy Q4 decode steps of the 18-layer decoder from the same 1345-token KV state "
                       f"(oracle, C restatement of the pure-Go CPU path, {threads} threads)",
             "tokens_match_gpu": bool(match)}
+
+
+def host_cpu():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_config1(cfg, weights_q8, gpu_model):
+    """The reference's own CPU workload: Q8, 64 ids from [0,100000) seed 0,
+    greedy 16 tokens — timed on the oracle in plain and VNNI-emulation mode,
+    tokens compared with the GPU's."""
+    import oracle
+    from rapidocrvl_amd import synth
+
+    threads = min(16, os.cpu_count() or 1)
+    oracle.set_threads(threads)
+    ids = synth.prompt_ids(64, seed=0)
+    gpu = list(gpu_model.seq(96).generate(ids, 16, eos=(), use_prefill=True))
+    out = {"workload": "q8, 64 prompt ids (seed 0), 16 greedy tokens, 18 layers", "threads": threads}
+    for mode in ("plain", "vnni"):
+        om = oracle.Model(cfg)
+        om.load_weights(weights_q8)
+        om.set_vnni(mode == "vnni")
+        t = time.perf_counter()
+        toks = list(om.generate(ids, 16, eos=()))
+        dt = time.perf_counter() - t
+        out[mode] = {"s": round(dt, 3), "tok_s_end_to_end": round(16 / dt, 2),
+                     "tokens_match_gpu": toks == gpu}
+        om.close()
+    return out
 
 
 def main():
@@ -252,6 +290,7 @@ def main():
     ap.add_argument("--no-q8", action="store_true")
     ap.add_argument("--roofline-only", action="store_true", help="time only the Q4 LM-head GEMV rotation")
     ap.add_argument("--calibrate-copy", action="store_true", help="with --roofline-only: add a 512 MiB copy")
+    ap.add_argument("--prefill-only", action="store_true", help="time only the 1345-token Q4 image prefill")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the decoder step runs on a single MI355X "
@@ -275,6 +314,12 @@ def main():
     seq = model.seq(n_prefix + args.decode_tokens + 8)
     first_tok, t_prefill = prefill(seq, ids, img, reps=3)
     log(f"[bench] prefill {n_prefix} tokens in {t_prefill * 1e3:.1f} ms, first token {first_tok}")
+    if args.prefill_only:
+        print(json.dumps({"workload": f"q4 image prefill, {n_prefix} tokens", "prefill_ms": round(t_prefill * 1e3, 3),
+                          "prefill_tok_s": round(n_prefix / t_prefill, 1),
+                          "prefill_TFLOP_s": round(prefill_flops(cfg, n_prefix) / t_prefill / 1e12, 2),
+                          "first_token": first_tok}), flush=True)
+        return
     dt, toks = time_decode(seq, n_prefix, first_tok, first_pos, args.decode_tokens, args.warmup, args.steps)
     tok_s = args.decode_tokens * args.steps / dt
     log(f"[bench] q4 decode {tok_s:.1f} tok/s ({dt / args.steps * 1e3:.1f} ms per {args.decode_tokens} tokens)")
@@ -300,6 +345,9 @@ def main():
         dt8, _ = time_decode(s8, n_prefix, t8, first_pos, args.decode_tokens, 1, max(1, args.steps // 2))
         extra["q8_decode_tok_s"] = round(args.decode_tokens * max(1, args.steps // 2) / dt8, 1)
         s8.close()
+        if not args.no_cpu:
+            extra["cpu_config1"] = cpu_config1(cfg, w8, m8)
+            log(f"[bench] cpu config 1 {extra['cpu_config1']}")
         m8.close()
         del w8
     extra["prefill_ms"] = round(t_prefill * 1e3, 2)

@@ -198,26 +198,10 @@ __device__ __forceinline__ bool prefill_in_place(const GemmParams &p, int n) {
     return !(p.quirk && (clen == 0 || clen >= 6));
 }
 
-// Epilogue of rows rr..rr+3 for token n, given the int32 accumulators of the
-// three digit planes: y = scale[r]·xs[n]·(D0 + D1/2^7 + D2/2^14).
-template <int QT, int NMAT>
-__device__ __forceinline__ void gemm_store(const GemmParams &p, int epi, int n, int rr, const float *const (&scl)[2],
-                                           const v4i (&a)[NMAT][3]) {
-    constexpr int IB = DigitTraits<QT>::IBIAS;
-    const float sx = p.xs[n];
-    const int4 bs = *reinterpret_cast<const int4 *>(p.xb + 4 * n);
-    float y[NMAT][4];
-#pragma unroll
-    for (int mi = 0; mi < NMAT; ++mi) {
-        const float *sc = scl[mi];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float f0 = (float)(a[mi][0][i] - IB * bs.x);
-            const float f1 = (float)(a[mi][1][i] - IB * bs.y);
-            const float f2 = (float)(a[mi][2][i] - IB * bs.z);
-            y[mi][i] = fmaf(f2, 1.0f / 16384.0f, fmaf(f1, 1.0f / 128.0f, f0)) * sx * sc[i];
-        }
-    }
+// Store of rows rr..rr+3 for token n, given their f32 values y (one set per
+// matrix; SwiGLU pairs gate and up).
+template <int NMAT>
+__device__ __forceinline__ void gemm_store_y(const GemmParams &p, int epi, int n, int rr, const float (&y)[NMAT][4]) {
     if (epi == G_PLAIN) {
         *reinterpret_cast<float4 *>(p.out + (size_t)n * p.out_stride + rr) = make_float4(y[0][0], y[0][1], y[0][2], y[0][3]);
     } else if (epi == G_SWIGLU) {
@@ -246,6 +230,29 @@ __device__ __forceinline__ void gemm_store(const GemmParams &p, int epi, int n, 
             *hp = v;
         }
     }
+}
+
+// Epilogue of rows rr..rr+3 for token n, given the int32 accumulators of the
+// three digit planes: y = scale[r]·xs[n]·(D0 + D1/2^7 + D2/2^14).
+template <int QT, int NMAT>
+__device__ __forceinline__ void gemm_store(const GemmParams &p, int epi, int n, int rr, const float *const (&scl)[2],
+                                           const v4i (&a)[NMAT][3]) {
+    constexpr int IB = DigitTraits<QT>::IBIAS;
+    const float sx = p.xs[n];
+    const int4 bs = *reinterpret_cast<const int4 *>(p.xb + 4 * n);
+    float y[NMAT][4];
+#pragma unroll
+    for (int mi = 0; mi < NMAT; ++mi) {
+        const float *sc = scl[mi];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float f0 = (float)(a[mi][0][i] - IB * bs.x);
+            const float f1 = (float)(a[mi][1][i] - IB * bs.y);
+            const float f2 = (float)(a[mi][2][i] - IB * bs.z);
+            y[mi][i] = fmaf(f2, 1.0f / 16384.0f, fmaf(f1, 1.0f / 128.0f, f0)) * sx * sc[i];
+        }
+    }
+    gemm_store_y<NMAT>(p, epi, n, rr, y);
 }
 
 // the wave's rows lie in one segment (segment ends are multiples of 16 rows
@@ -384,6 +391,258 @@ static __global__ void __launch_bounds__(kThreads) k_gemm(GemmParams p, int epi)
         for (int rb = 0; rb < 4; ++rb) {
             const int rr = r0 + 16 * rb + 4 * lg;  // 4 consecutive rows
             const float *const scl[2] = {scale0 + (rr - start), NMAT == 2 ? scale1 + (rr - start) : nullptr};
+            v4i a3[NMAT][3];
+#pragma unroll
+            for (int mi = 0; mi < NMAT; ++mi)
+#pragma unroll
+                for (int pl = 0; pl < 3; ++pl) a3[mi][pl] = acc[mi][rb][tb][pl];
+            gemm_store<QT, NMAT>(p, epi, n, rr, scl, a3);
+        }
+    }
+}
+
+// raw code bytes of 16 columns (Q8 16 B, Q4 8 B, Q6 12 B)
+template <int QT>
+struct RawCodes {
+    uint32_t d[QT == QT_Q8 ? 4 : (QT == QT_Q4 ? 2 : 3)];
+};
+
+// the MFMA A operand of 16 raw columns, unpacked as load_codes16 does
+template <int QT>
+__device__ __forceinline__ v4i unpack_codes16(const RawCodes<QT> &r) {
+    if constexpr (QT == QT_Q8) {
+        return v4i{(int)r.d[0], (int)r.d[1], (int)r.d[2], (int)r.d[3]};
+    } else if constexpr (QT == QT_Q4) {
+        return v4i{(int)(r.d[0] & 0x0F0F0F0Fu), (int)(r.d[1] & 0x0F0F0F0Fu), (int)((r.d[0] >> 4) & 0x0F0F0F0Fu),
+                   (int)((r.d[1] >> 4) & 0x0F0F0F0Fu)};
+    } else {
+        return v4i{spread6(r.d[0]), spread6(__builtin_amdgcn_alignbit(r.d[1], r.d[0], 24)),
+                   spread6(__builtin_amdgcn_alignbit(r.d[2], r.d[1], 16)), spread6(r.d[2] >> 8)};
+    }
+}
+
+// XCD-aware tile order: workgroups are dispatched round-robin over the 8 XCDs
+// (XCD = linear id mod 8), so XCD j is given the j-th contiguous run of tiles
+// in token-major order: its L2 keeps a few token tiles' digit planes and the
+// weight rows they meet, instead of every XCD streaming every tile.
+__device__ __forceinline__ int2 xcd_tile() {
+    const int gx = gridDim.x;
+    const int L = blockIdx.x + gx * blockIdx.y;
+    const int W = gx * gridDim.y, q = W >> 3, r = W & 7, j = L & 7;
+    const int logical = j * q + min(j, r) + (L >> 3);
+    return make_int2(logical % gx, logical / gx);
+}
+
+// ---------------------------------------------------------------------------
+// Prefill GEMM with both operands streamed into LDS by direct loads
+// (global_load_lds: HBM → LDS with no staging registers) through a ring of
+// NST stages of 128 columns.  Workgroup: 4 waves along the rows (256 rows, or
+// 128 gate + 128 up rows) × 32 tokens; wave tile 64 rows × 32 tokens, 24
+// MFMAs (4 row blocks × 2 token blocks × 3 digit planes) per 64 columns.
+//
+// K order of the MFMA operands: in stage u, MFMA step s, lane group lg takes
+// columns 128u + 32lg + 16s .. +15 (A and B alike; inside a 16-column group
+// the digit planes follow the weight codes' own order).  So a lane's weight
+// bytes for a stage are contiguous (Q4 16 B, Q8 32 B, Q6 24 B of its row):
+// each lane loads exactly the A operand it will use, and the LDS ring only
+// decouples the loads from the MFMAs (no register cost for the prefetch).
+// The digit planes are shared by the 4 waves.
+//
+// Per stage and wave: B 3 loads (1 KB each: 12 per workgroup), A 4 (Q4) or
+// 8 (Q8, Q6) loads.  One barrier per stage: at its top every wave has waited
+// for its own loads of this stage, and every wave has finished the previous
+// stage, whose slot is then refilled NST−1 stages ahead.
+// ---------------------------------------------------------------------------
+constexpr int kStageCols = 128;
+
+template <int QT>
+struct ALds {
+    static constexpr int chunks = QT == QT_Q4 ? 1 : 2;       // loads per (matrix, row block) and stage
+    static constexpr int bytes = QT == QT_Q6 ? 12 : 16;      // bytes per lane and load
+    static constexpr int lane_words = QT == QT_Q4 ? 4 : (QT == QT_Q8 ? 8 : 6);
+};
+// the direct load places lane i's bytes at 16·i for 12- and 16-byte loads alike
+constexpr int kLdsLaneStride = 16;
+
+template <int QT, int NMAT, int NST>
+struct GemmLdsLayout {
+    static constexpr int RB = 4 / NMAT;
+    static constexpr int b_bytes = 2 * 3 * 2 * 64 * 16;                                       // [s][pl][tb][lane]
+    static constexpr int a_wave = NMAT * RB * ALds<QT>::chunks * 64 * kLdsLaneStride;        // [mi][rb][c][lane]
+    static constexpr int stage = b_bytes + kWaves * a_wave;
+    static constexpr int total = NST * stage;
+};
+
+// HBM → LDS load of BYTES (16 or 12) per lane: lane i's bytes land at
+// lds + 16·i.  Written as inline asm so the compiler's wait-count pass does
+// not see an LDS write it cannot place (it would wait for every load in flight
+// before each LDS read); the kernel orders these loads itself with wait_vm and
+// lds_barrier.
+template <int BYTES>
+__device__ __forceinline__ void lds_load(const void *g, void *lds) {
+    const uint32_t base = __builtin_amdgcn_readfirstlane(
+        (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)lds);
+    if constexpr (BYTES == 16)
+        asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(base)
+                     : "m0");
+    else
+        asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx3 %0, off" ::"v"(g), "s"(base)
+                     : "m0");
+}
+
+// s_waitcnt vmcnt(N): at most N of this wave's vector-memory loads in flight
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// workgroup barrier that keeps LDS reads and loads on their side of it
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_barrier" ::: "memory");
+}
+
+template <int QT, int NMAT, int NST>
+static __global__ void __launch_bounds__(kThreads) k_gemm_lds(GemmParams p, int epi) {
+    static_assert(NST == 3, "the main loop is unrolled over three slots");
+    using Lay = GemmLdsLayout<QT, NMAT, NST>;
+    constexpr int RB = Lay::RB;
+    constexpr int WR = 16 * RB;                 // rows per matrix and wave
+    constexpr int TB = 2;
+    constexpr int CH = ALds<QT>::chunks, AB = ALds<QT>::bytes;
+    constexpr int LPS = 3 + NMAT * RB * CH;     // loads per stage and wave
+    __shared__ __attribute__((aligned(16))) uint8_t slot0[Lay::stage];
+    __shared__ __attribute__((aligned(16))) uint8_t slot1[Lay::stage];
+    __shared__ __attribute__((aligned(16))) uint8_t slot2[Lay::stage];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lr = lane & 15, lg = lane >> 4;
+    const int2 tile = xcd_tile();
+    const int n0 = tile.y * 16 * TB;
+    const int r0 = tile.x * (WR * kWaves) + wave * WR;
+    const bool on = r0 < p.rows;              // uniform; rows are a multiple of WR
+    const int rc = on ? r0 : p.rows - WR;     // loads stay in bounds for idle waves
+    const int nst = p.K / kStageCols;
+
+    const GemmSeg sg = gemm_seg<NMAT>(p, rc);
+    const int row_bytes = p.m[0].row_bytes;
+    constexpr int stage_row = QT == QT_Q4 ? 64 : (QT == QT_Q8 ? 128 : 96);  // row bytes per stage
+    // this lane's A source: row rc+16rb+lr, bytes lg·(stage_row/4) + c·AB of the stage slice
+    const uint8_t *asrc[NMAT][RB];
+#pragma unroll
+    for (int mi = 0; mi < NMAT; ++mi)
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+            asrc[mi][rb] = sg.base[mi] + (size_t)(rc + 16 * rb + lr - sg.start) * row_bytes + lg * (stage_row / 4);
+    // this wave's 3 B loads: chunk j = 3·wave + i → (s, pl, tb); lane: token 16tb+lr, columns 32lg + 16s
+    const int8_t *bsrc[3];
+    int boff[3];
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        const int j = 3 * wave + i;
+        const int tb = j % 2, pl = (j / 2) % 3, s = j / 6;
+        bsrc[i] = p.xd + pl * p.plane_stride + (size_t)(n0 + 16 * tb + lr) * p.K + 32 * lg + 16 * s;
+        boff[i] = j * 1024;
+    }
+    const int aoff = Lay::b_bytes + wave * Lay::a_wave;
+
+    auto issue = [&](int u, uint8_t *st) {
+#pragma unroll
+        for (int i = 0; i < 3; ++i) lds_load<16>(bsrc[i] + kStageCols * u, st + boff[i]);
+#pragma unroll
+        for (int mi = 0; mi < NMAT; ++mi)
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+                for (int c = 0; c < CH; ++c)
+                    lds_load<AB>(asrc[mi][rb] + stage_row * u + c * AB,
+                                 st + aoff + ((mi * RB + rb) * CH + c) * 64 * kLdsLaneStride);
+    };
+
+    v4i acc[NMAT][RB][TB][3];
+#pragma unroll
+    for (int mi = 0; mi < NMAT; ++mi)
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+            for (int tb = 0; tb < TB; ++tb)
+#pragma unroll
+                for (int pl = 0; pl < 3; ++pl) acc[mi][rb][tb][pl] = v4i{0, 0, 0, 0};
+
+    auto compute = [&](const uint8_t *st) {
+        const v4i *bl = reinterpret_cast<const v4i *>(st);
+        uint32_t raw[NMAT][RB][ALds<QT>::lane_words];  // the stage's weight bytes of this lane
+#pragma unroll
+        for (int mi = 0; mi < NMAT; ++mi)
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+                for (int c = 0; c < CH; ++c) {
+                    const uint8_t *q = st + aoff + (((mi * RB + rb) * CH + c) * 64 + lane) * kLdsLaneStride;
+                    if constexpr (AB == 16) {
+                        const uint4 v = *reinterpret_cast<const uint4 *>(q);
+                        raw[mi][rb][4 * c] = v.x; raw[mi][rb][4 * c + 1] = v.y;
+                        raw[mi][rb][4 * c + 2] = v.z; raw[mi][rb][4 * c + 3] = v.w;
+                    } else {
+                        const uint32_t *w = reinterpret_cast<const uint32_t *>(q);
+                        raw[mi][rb][3 * c] = w[0]; raw[mi][rb][3 * c + 1] = w[1]; raw[mi][rb][3 * c + 2] = w[2];
+                    }
+                }
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            v4i b[TB][3];
+#pragma unroll
+            for (int tb = 0; tb < TB; ++tb)
+#pragma unroll
+                for (int pl = 0; pl < 3; ++pl) b[tb][pl] = bl[((s * 3 + pl) * TB + tb) * 64 + lane];
+#pragma unroll
+            for (int mi = 0; mi < NMAT; ++mi)
+#pragma unroll
+                for (int rb = 0; rb < RB; ++rb) {
+                    RawCodes<QT> rcd;
+                    constexpr int W = QT == QT_Q8 ? 4 : (QT == QT_Q4 ? 2 : 3);
+#pragma unroll
+                    for (int w = 0; w < W; ++w) rcd.d[w] = raw[mi][rb][W * s + w];
+                    const v4i av = unpack_codes16<QT>(rcd);
+#pragma unroll
+                    for (int tb = 0; tb < TB; ++tb)
+#pragma unroll
+                        for (int pl = 0; pl < 3; ++pl)
+                            acc[mi][rb][tb][pl] =
+                                __builtin_amdgcn_mfma_i32_16x16x64_i8(av, b[tb][pl], acc[mi][rb][tb][pl], 0, 0, 0);
+                }
+        }
+    };
+    // stage u: wait for this wave's loads of u (stage u+1 may stay in flight),
+    // barrier (every wave's loads of u have landed; every wave is done with
+    // u−1, whose slot takes stage u+2), then the MFMAs of u
+    auto body = [&](int u, const uint8_t *cur, uint8_t *refill) {
+        if (u + 1 < nst) wait_vm<LPS>();
+        else wait_vm<0>();
+        lds_barrier();
+        if (u + 2 < nst) issue(u + 2, refill);
+        if (on) compute(cur);
+    };
+
+    issue(0, slot0);
+    if (nst > 1) issue(1, slot1);
+    for (int u = 0; u < nst; u += 3) {
+        body(u, slot0, slot2);
+        if (u + 1 < nst) body(u + 1, slot1, slot0);
+        if (u + 2 < nst) body(u + 2, slot2, slot1);
+    }
+    if (!on) return;
+
+    // epilogue: lane holds token n0+16tb+lr, rows r0+16rb+4lg+i (i < 4)
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb) {
+        const int n = n0 + 16 * tb + lr;
+        if (n >= p.ntok) continue;
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+            const int rr = r0 + 16 * rb + 4 * lg;
+            const float *const scl[2] = {sg.scale[0] + (rr - sg.start),
+                                         NMAT == 2 ? sg.scale[1] + (rr - sg.start) : nullptr};
             v4i a3[NMAT][3];
 #pragma unroll
             for (int mi = 0; mi < NMAT; ++mi)

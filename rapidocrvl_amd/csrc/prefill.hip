@@ -58,8 +58,31 @@ int launch_gemm_small_t(hipStream_t s, int qtype, const GemmParams &p, int epi) 
 
 bool small_shape_ok(int rows, int K) { return rows % 16 == 0 && K % (kGemmK * kWaves) == 0 && K <= kMaxCols; }
 
+template <int NMAT>
+int launch_gemm_lds_t(hipStream_t s, int qtype, const GemmParams &p, int epi, int npad) {
+    const dim3 grid((p.rows + kGemmRows / NMAT - 1) / (kGemmRows / NMAT), npad / 32);
+    switch (qtype) {
+    case QT_Q8: hipLaunchKernelGGL((k_gemm_lds<QT_Q8, NMAT, 3>), grid, dim3(kThreads), 0, s, p, epi); break;
+    case QT_Q4: hipLaunchKernelGGL((k_gemm_lds<QT_Q4, NMAT, 3>), grid, dim3(kThreads), 0, s, p, epi); break;
+    case QT_Q6: hipLaunchKernelGGL((k_gemm_lds<QT_Q6, NMAT, 3>), grid, dim3(kThreads), 0, s, p, epi); break;
+    default: return fail(POCR_ERR_UNSUPPORTED, "gemm: qtype %d", qtype);
+    }
+    HIP_TRY(hipGetLastError());
+    return POCR_OK;
+}
+
+// the LDS-ring kernel takes K in whole 128-column stages
+bool lds_gemm_ok(int K) {
+    const char *env = getenv("POCR_PREFILL_GEMM");
+    return K % kStageCols == 0 && !(env && env[0] == 'd');
+}
+
 // npad: token rows of the digit planes, a multiple of 32
 int launch_gemm(hipStream_t s, int qtype, int nmat, const GemmParams &p, int epi, int npad) {
+    if (lds_gemm_ok(p.K)) {
+        if (nmat == 2) return launch_gemm_lds_t<2>(s, qtype, p, epi, npad);
+        return launch_gemm_lds_t<1>(s, qtype, p, epi, npad);
+    }
     if (nmat == 2) return launch_gemm_t<2, 1>(s, qtype, p, epi, npad);
     return launch_gemm_t<1, 2>(s, qtype, p, epi, npad);
 }
