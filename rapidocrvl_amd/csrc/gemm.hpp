@@ -783,155 +783,216 @@ static __global__ void __launch_bounds__(kThreads) k_rope_append(float *qkv, int
 }
 
 // ---------------------------------------------------------------------------
-// Causal GQA prefill attention, head_dim 128, on fp32 MFMA
-// (v_mfma_f32_16x16x4f32; lane l of an operand holds row/column l%16 and K
-// index l/16, the result lane l holds rows 4·(l/16)+i of column l%16).
+// Causal prefill attention on bf16 MFMA (v_mfma_f32_16x16x32_bf16) with split
+// operands: every fp32 operand x is carried as hi = bf16(x), lo = bf16(x − hi)
+// (x = hi + lo to 2^-17 relative) and a product as hi·hi + hi·lo + lo·hi,
+// accumulated in fp32 (the dropped lo·lo term is below 2^-16 relative).
 //
-// Workgroup (g, qb): kv head g, query tokens [16qb, 16qb+16).  Wave w owns
-// q heads 2w, 2w+1 of the group, one 16×16 tile (token × ·) each.  Per key
-// block of 32 rows (K and V staged in LDS) it forms Sᵀ = K·Qᵀ — the scores of
-// its 16 tokens, keys down the rows — so the probabilities are already laid
-// out as the B operand of Oᵀ += Vᵀ·Pᵀ: no transpose.  The K index of the
-// Sᵀ products is dim 32·(l/16)+s at step s (any order sums the same), which
-// makes every lane's q and k reads contiguous.  Online softmax per token
-// (max, Σexp) with FastExp; token n attends cache rows [0, clen0+n].
-// Scores: dot·f32(1/√128) (model.go:4623-4795, 7391).
+// Workgroup: one KV head, 4 query heads of its group (one per wave) and two
+// 16-token tiles, i and NT−1−i, so every workgroup meets the same number of
+// key blocks under the causal mask.  Per 32-key block the 256 threads stage
+// K as [plane][key][dim] and V transposed as [plane][dim][key] (bf16 hi/lo)
+// in LDS, double-buffered; each wave then runs
+//   Sᵀ (keys × tokens) = K · Qᵀ     2 key tiles × 4 dim chunks × 3 MFMAs
+//   online softmax per token column (the column's keys sit in 4 lane groups)
+//   Oᵀ (dims × tokens) += Vᵀ · Pᵀ   8 dim tiles × 3 MFMAs, K index = keys
+// Pᵀ feeds the second product straight from the first one's accumulators: MFMA
+// step element e of lane group lg is key 4lg+e (e < 4) or 16+4lg+(e−4), the
+// rows that lane already holds, and Vᵀ is read in the same key order.
+// Online softmax per token (max, Σexp) with FastExp; token n attends cache
+// rows [0, clen0+n]; scores dot·f32(1/√128) (model.go:4623-4795, 7391).
 // ---------------------------------------------------------------------------
 typedef float v4f __attribute__((ext_vector_type(4)));
-constexpr int kPfTok = 16;    // query tokens per workgroup
-constexpr int kPfKeys = 32;   // key rows per LDS block
-constexpr int kPfPad = 4;     // LDS row padding (floats)
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef __bf16 v4bf __attribute__((ext_vector_type(4)));
+constexpr int kPfTok = 16;    // query tokens per tile
+constexpr int kPfKeys = 32;   // keys per LDS block
+constexpr int kPfKRow = kHD + 8;       // K row pitch (bf16): 272 B, rows land 4 banks apart
+constexpr int kPfVRow = kPfKeys + 8;   // Vᵀ row pitch (bf16): 80 B
+
+struct PfSlot {
+    __bf16 k[2][kPfKeys][kPfKRow];   // [hi/lo][key][dim]
+    __bf16 vt[2][kHD][kPfVRow];      // [hi/lo][dim][key]
+};
+
+__device__ __forceinline__ void split_bf16(float x, __bf16 &hi, __bf16 &lo) {
+    hi = (__bf16)x;
+    lo = (__bf16)(x - (float)hi);
+}
 
 static __global__ void __launch_bounds__(kThreads) k_attn_prefill(const float *qkv, int stride, const float *kc,
                                                              const float *vc, int heads, int kvh, int ntok,
                                                              int clen0, float scale, float *out, int out_stride) {
-    __shared__ float ks[kPfKeys][kHD + kPfPad];
-    __shared__ float vs[kPfKeys][kHD + kPfPad];
-    const int g = blockIdx.x;
+    __shared__ PfSlot sl[2];
     const int group = heads / kvh;
+    const int quads = (group + 3) / 4;
+    const int g = blockIdx.x / quads, quad = blockIdx.x % quads;
     const int t = threadIdx.x, l = t & 63;
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
     const int lr = l & 15, lg = l >> 4;
-    const int q0 = blockIdx.y * kPfTok;
-    const int tok = q0 + lr;  // this lane's token (column of every tile)
+    const int hl = 4 * quad + wave;               // head within the group
+    const bool wave_on = hl < group;              // uniform
+    const int hh = g * group + min(hl, group - 1);
     const int kvd = kvh * kHD;
-    const bool wave_on = 2 * wave < group;  // uniform
+    const int nt = (ntok + kPfTok - 1) / kPfTok;
+    // staging roles: K row kk, dims 16·kd..; V keys 4·vq.., dims 4·vd..
+    const int kk = t >> 3, kd = t & 7;
+    const int vq = t >> 5, vd = t & 31;
 
-    // Qᵀ operands: tile qt = head 2·wave+qt, lane: token lr, dims 32·lg + s
-    float qv[2][32];
-#pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
-        const int hh = g * group + min(2 * wave + qt, group - 1);
-        const float4 *src =
-            reinterpret_cast<const float4 *>(qkv + (size_t)min(tok, ntok - 1) * stride + (size_t)hh * kHD + 32 * lg);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const float4 v = src[i];
-            qv[qt][4 * i] = v.x;
-            qv[qt][4 * i + 1] = v.y;
-            qv[qt][4 * i + 2] = v.z;
-            qv[qt][4 * i + 3] = v.w;
-        }
-    }
-    v4f o[2][8];
-#pragma unroll
-    for (int qt = 0; qt < 2; ++qt)
-#pragma unroll
-        for (int dt = 0; dt < 8; ++dt) o[qt][dt] = v4f{0.f, 0.f, 0.f, 0.f};
-    float m[2] = {-INFINITY, -INFINITY}, lsum[2] = {0.f, 0.f};
-    const int last_key = clen0 + min(q0 + kPfTok, ntok) - 1;  // the block's last visible row
-    const int my_last = clen0 + min(tok, ntok - 1);
+    for (int pass = 0; pass < 2; ++pass) {
+        const int tile = pass == 0 ? (int)blockIdx.y : nt - 1 - (int)blockIdx.y;
+        if (pass == 1 && tile <= (int)blockIdx.y) break;  // uniform
+        const int q0 = tile * kPfTok;
+        const int tq = min(q0 + lr, ntok - 1);    // this lane's token (clamped; stored only if < ntok)
+        const int last_key = clen0 + min(q0 + kPfTok, ntok) - 1;
+        const int my_last = clen0 + tq;
+        const int nblk = last_key / kPfKeys + 1;
 
-    for (int k0 = 0; k0 <= last_key; k0 += kPfKeys) {
-        __syncthreads();
-        for (int i = t; i < kPfKeys * (kHD / 4); i += kThreads) {
-            const int r = i / (kHD / 4), c = 4 * (i % (kHD / 4));
-            const int key = min(k0 + r, last_key);
-            const float4 kv = *reinterpret_cast<const float4 *>(kc + (size_t)key * kvd + g * kHD + c);
-            const float4 vv = *reinterpret_cast<const float4 *>(vc + (size_t)key * kvd + g * kHD + c);
-            *reinterpret_cast<float4 *>(&ks[r][c]) = kv;
-            *reinterpret_cast<float4 *>(&vs[r][c]) = vv;
-        }
-        __syncthreads();
-        if (!wave_on) continue;
-        // Sᵀ[kt][qt]: keys k0+16kt+4lg+i (rows) × tokens (columns)
-        v4f sT[2][2];
+        // Qᵀ operand of the first product: token lr, dims 32c + 8lg + e
+        v8bf qh[4], ql[4];
+        {
+            const float *qs = qkv + (size_t)tq * stride + (size_t)hh * kHD + 8 * lg;
 #pragma unroll
-        for (int kt = 0; kt < 2; ++kt) {
-            sT[kt][0] = sT[kt][1] = v4f{0.f, 0.f, 0.f, 0.f};
-            const float *krow = &ks[16 * kt + lr][32 * lg];
+            for (int c = 0; c < 4; ++c) {
+                const float4 a = *reinterpret_cast<const float4 *>(qs + 32 * c);
+                const float4 b = *reinterpret_cast<const float4 *>(qs + 32 * c + 4);
+                const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
-            for (int s4 = 0; s4 < 8; ++s4) {
-                const float4 ka = *reinterpret_cast<const float4 *>(krow + 4 * s4);
-                const float kk[4] = {ka.x, ka.y, ka.z, ka.w};
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-#pragma unroll
-                    for (int qt = 0; qt < 2; ++qt)
-                        sT[kt][qt] = __builtin_amdgcn_mfma_f32_16x16x4f32(kk[j], qv[qt][4 * s4 + j], sT[kt][qt], 0, 0, 0);
+                for (int e = 0; e < 8; ++e) {
+                    __bf16 h, lo;
+                    split_bf16(x[e], h, lo);
+                    qh[c][e] = h;
+                    ql[c][e] = lo;
+                }
             }
         }
-        // online softmax per token (column): keys of a column sit in 4 lane groups
+        v4f o[8];
 #pragma unroll
-        for (int qt = 0; qt < 2; ++qt) {
-            float sv[2][4];
-            float mb = m[qt];
+        for (int dt = 0; dt < 8; ++dt) o[dt] = v4f{0.f, 0.f, 0.f, 0.f};
+        float m = -INFINITY, lsum = 0.0f;
+
+        float4 kr[4], vr[4];
+        auto load_block = [&](int b) {
+            const int k0 = b * kPfKeys;
+            const float *ks = kc + (size_t)min(k0 + kk, last_key) * kvd + g * kHD + 16 * kd;
 #pragma unroll
-            for (int kt = 0; kt < 2; ++kt)
+            for (int i = 0; i < 4; ++i) kr[i] = reinterpret_cast<const float4 *>(ks)[i];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                vr[i] = *reinterpret_cast<const float4 *>(vc + (size_t)min(k0 + 4 * vq + i, last_key) * kvd + g * kHD +
+                                                          4 * vd);
+        };
+        auto store_block = [&](PfSlot &s) {
+#pragma unroll
+            for (int half = 0; half < 2; ++half) {
+                v8bf h, lo;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float4 v = kr[2 * half + e / 4];
+                    const float x = e % 4 == 0 ? v.x : (e % 4 == 1 ? v.y : (e % 4 == 2 ? v.z : v.w));
+                    __bf16 a, b;
+                    split_bf16(x, a, b);
+                    h[e] = a;
+                    lo[e] = b;
+                }
+                *reinterpret_cast<v8bf *>(&s.k[0][kk][16 * kd + 8 * half]) = h;
+                *reinterpret_cast<v8bf *>(&s.k[1][kk][16 * kd + 8 * half]) = lo;
+            }
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+                v4bf h, lo;
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const int key = k0 + 16 * kt + 4 * lg + i;
-                    sv[kt][i] = key <= my_last ? sT[kt][qt][i] * scale : -INFINITY;
-                    mb = fmaxf(mb, sv[kt][i]);
+                    const float4 v = vr[i];
+                    const float x = d == 0 ? v.x : (d == 1 ? v.y : (d == 2 ? v.z : v.w));
+                    __bf16 a, b;
+                    split_bf16(x, a, b);
+                    h[i] = a;
+                    lo[i] = b;
                 }
-            mb = fmaxf(mb, xchg<XS16>(mb));
-            mb = fmaxf(mb, xchg<XS32>(mb));
-            float ps = 0.0f;
+                *reinterpret_cast<v4bf *>(&s.vt[0][4 * vd + d][4 * vq]) = h;
+                *reinterpret_cast<v4bf *>(&s.vt[1][4 * vd + d][4 * vq]) = lo;
+            }
+        };
+
+        load_block(0);
+        __syncthreads();  // the previous tile's last block is read
+        store_block(sl[0]);
+        __syncthreads();
+        for (int b = 0; b < nblk; ++b) {
+            const bool more = b + 1 < nblk;  // uniform
+            if (more) load_block(b + 1);
+            if (wave_on) {
+                const PfSlot &s = sl[b & 1];
+                const int k0 = b * kPfKeys;
+                v4f sT[2];
 #pragma unroll
-            for (int kt = 0; kt < 2; ++kt)
+                for (int kt = 0; kt < 2; ++kt) {
+                    sT[kt] = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const float e = sv[kt][i] == -INFINITY ? 0.0f : fast_exp_ref(sv[kt][i] - mb);
-                    sT[kt][qt][i] = e;  // Pᵀ, in place
-                    ps += e;
+                    for (int c = 0; c < 4; ++c) {
+                        const v8bf kh = *reinterpret_cast<const v8bf *>(&s.k[0][16 * kt + lr][32 * c + 8 * lg]);
+                        const v8bf kl = *reinterpret_cast<const v8bf *>(&s.k[1][16 * kt + lr][32 * c + 8 * lg]);
+                        sT[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, qh[c], sT[kt], 0, 0, 0);
+                        sT[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, ql[c], sT[kt], 0, 0, 0);
+                        sT[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kl, qh[c], sT[kt], 0, 0, 0);
+                    }
                 }
-            ps += xchg<XS16>(ps);
-            ps += xchg<XS32>(ps);
-            // mb is finite: key 0 is visible to every token, so from the first
-            // block on every column has a finite maximum
-            const float f = m[qt] == -INFINITY ? 0.0f : fast_exp_ref(m[qt] - mb);
-            lsum[qt] = lsum[qt] * f + ps;
-            m[qt] = mb;
+                // online softmax of token column lr
+                float sv[8];
+                float mb = m;
 #pragma unroll
-            for (int dt = 0; dt < 8; ++dt) o[qt][dt] *= f;
-        }
-        // Oᵀ[dt][qt] += Vᵀ (dims × keys) · Pᵀ (keys × tokens); MFMA step (kt, i)
-        // takes keys 16kt + 4·lg' + i of lane group lg'
+                for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-        for (int kt = 0; kt < 2; ++kt)
+                    for (int i = 0; i < 4; ++i) {
+                        const int key = k0 + 16 * kt + 4 * lg + i;
+                        sv[4 * kt + i] = key <= my_last ? sT[kt][i] * scale : -INFINITY;
+                        mb = fmaxf(mb, sv[4 * kt + i]);
+                    }
+                mb = fmaxf(mb, xchg<XS16>(mb));
+                mb = fmaxf(mb, xchg<XS32>(mb));
+                // mb is finite: key 0 is visible to every token
+                float ps = 0.0f;
+                v8bf ph, pl;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float *vrow = &vs[16 * kt + 4 * lg + i][lr];
+                for (int e = 0; e < 8; ++e) {
+                    const float p = sv[e] == -INFINITY ? 0.0f : fast_exp_ref(sv[e] - mb);
+                    ps += p;
+                    __bf16 a, c;
+                    split_bf16(p, a, c);
+                    ph[e] = a;
+                    pl[e] = c;
+                }
+                ps += xchg<XS16>(ps);
+                ps += xchg<XS32>(ps);
+                const float f = m == -INFINITY ? 0.0f : fast_exp_ref(m - mb);
+                lsum = lsum * f + ps;
+                m = mb;
 #pragma unroll
                 for (int dt = 0; dt < 8; ++dt) {
-                    const float va = vrow[16 * dt];
-#pragma unroll
-                    for (int qt = 0; qt < 2; ++qt)
-                        o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(va, sT[kt][qt][i], o[qt][dt], 0, 0, 0);
+                    o[dt] *= f;
+                    const v4bf ah0 = *reinterpret_cast<const v4bf *>(&s.vt[0][16 * dt + lr][4 * lg]);
+                    const v4bf ah1 = *reinterpret_cast<const v4bf *>(&s.vt[0][16 * dt + lr][16 + 4 * lg]);
+                    const v4bf al0 = *reinterpret_cast<const v4bf *>(&s.vt[1][16 * dt + lr][4 * lg]);
+                    const v4bf al1 = *reinterpret_cast<const v4bf *>(&s.vt[1][16 * dt + lr][16 + 4 * lg]);
+                    const v8bf vh = __builtin_shufflevector(ah0, ah1, 0, 1, 2, 3, 4, 5, 6, 7);
+                    const v8bf vl = __builtin_shufflevector(al0, al1, 0, 1, 2, 3, 4, 5, 6, 7);
+                    o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vh, ph, o[dt], 0, 0, 0);
+                    o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vh, pl, o[dt], 0, 0, 0);
+                    o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vl, ph, o[dt], 0, 0, 0);
                 }
             }
-    }
-    if (!wave_on || tok >= ntok) return;
+            if (more) store_block(sl[(b + 1) & 1]);
+            __syncthreads();
+        }
+        if (wave_on && q0 + lr < ntok) {
+            const float inv = 1.0f / lsum;
+            float *dst = out + (size_t)(q0 + lr) * out_stride + (size_t)hh * kHD + 4 * lg;
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
-        if (2 * wave + qt >= group) break;
-        const int hq = g * group + 2 * wave + qt;
-        const float inv = 1.0f / lsum[qt];
-        float *dst = out + (size_t)tok * out_stride + (size_t)hq * kHD + 4 * lg;
-#pragma unroll
-        for (int dt = 0; dt < 8; ++dt)
-            *reinterpret_cast<float4 *>(dst + 16 * dt) =
-                make_float4(o[qt][dt][0] * inv, o[qt][dt][1] * inv, o[qt][dt][2] * inv, o[qt][dt][3] * inv);
+            for (int dt = 0; dt < 8; ++dt)
+                *reinterpret_cast<float4 *>(dst + 16 * dt) =
+                    make_float4(o[dt][0] * inv, o[dt][1] * inv, o[dt][2] * inv, o[dt][3] * inv);
+        }
     }
 }
 

@@ -272,7 +272,8 @@ int prefill_locked(pocr_seq *s, int n, const float *emb, const int32_t *pos3, fl
         // 2. per-token RoPE, K/V append at rows clen0.., causal attention
         hipLaunchKernelGGL(k_rope_append, dim3(n), dim3(kThreads), 0, st, b.qkv, QKV, b.pos, m->freq, m->axis,
                            c.heads, c.kv_heads, c.head_dim, layer_k(s, li), layer_v(s, li), clen0);
-        hipLaunchKernelGGL(k_attn_prefill, dim3(c.kv_heads, (n + kPfTok - 1) / kPfTok), dim3(kThreads), 0, st,
+        const int ntiles = (n + kPfTok - 1) / kPfTok, quads = (c.heads / c.kv_heads + 3) / 4;
+        hipLaunchKernelGGL(k_attn_prefill, dim3(c.kv_heads * quads, (ntiles + 1) / 2), dim3(kThreads), 0, st,
                            b.qkv, QKV, layer_k(s, li), layer_v(s, li), c.heads, c.kv_heads, n, clen0, scale, b.ho, Q);
         HIP_TRY(hipGetLastError());
         // 3. o_proj + residual (+ the Q4/Q6 behaviour per token) → v; h if in place
