@@ -788,11 +788,16 @@ static __global__ void __launch_bounds__(kThreads) k_rope_append(float *qkv, int
 // (x = hi + lo to 2^-17 relative) and a product as hi·hi + hi·lo + lo·hi,
 // accumulated in fp32 (the dropped lo·lo term is below 2^-16 relative).
 //
-// Workgroup: one KV head, 4 query heads of its group (one per wave) and two
-// 16-token tiles, i and NT−1−i, so every workgroup meets the same number of
-// key blocks under the causal mask.  Per 32-key block the 256 threads stage
-// K as [plane][key][dim] and V transposed as [plane][dim][key] (bf16 hi/lo)
-// in LDS, double-buffered; each wave then runs
+// k_kv_blocks first writes, per KV head and 32-key block, the block's LDS
+// image (32 KB): K as [hi/lo][key][16 chunks of 8 dims] with chunk j of key r
+// at position j ^ (r & 15), and V transposed as [hi/lo][dim][8 quads of 4 keys]
+// with quad q of dim d at position q ^ ((d >> 1) & 7).  The XOR swizzles make
+// the attention kernel's operand reads bank-conflict free with unpadded rows.
+//
+// k_attn_prefill — workgroup: one KV head, 4 query heads of its group (one per
+// wave) and two 16-token tiles, i and NT−1−i, so every workgroup meets the
+// same number of key blocks under the causal mask.  Block images stream
+// HBM → LDS by direct loads through a ring of 3 slots; per block each wave runs
 //   Sᵀ (keys × tokens) = K · Qᵀ     2 key tiles × 4 dim chunks × 3 MFMAs
 //   online softmax per token column (the column's keys sit in 4 lane groups)
 //   Oᵀ (dims × tokens) += Vᵀ · Pᵀ   8 dim tiles × 3 MFMAs, K index = keys
@@ -805,39 +810,119 @@ static __global__ void __launch_bounds__(kThreads) k_rope_append(float *qkv, int
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 typedef __bf16 v4bf __attribute__((ext_vector_type(4)));
-constexpr int kPfTok = 16;    // query tokens per tile
-constexpr int kPfKeys = 32;   // keys per LDS block
-constexpr int kPfKRow = kHD + 8;       // K row pitch (bf16): 272 B, rows land 4 banks apart
-constexpr int kPfVRow = kPfKeys + 8;   // Vᵀ row pitch (bf16): 80 B
-
-struct PfSlot {
-    __bf16 k[2][kPfKeys][kPfKRow];   // [hi/lo][key][dim]
-    __bf16 vt[2][kHD][kPfVRow];      // [hi/lo][dim][key]
-};
+constexpr int kPfTok = 16;                  // query tokens per tile
+constexpr int kPfKeys = 32;                 // keys per block
+constexpr int kPfKPlane = kPfKeys * kHD;    // bf16 per K plane of a block image
+constexpr int kPfImage = 4 * kPfKPlane * 2; // bytes per block image (K and Vᵀ, hi and lo): 32 KB
 
 __device__ __forceinline__ void split_bf16(float x, __bf16 &hi, __bf16 &lo) {
     hi = (__bf16)x;
     lo = (__bf16)(x - (float)hi);
 }
 
-static __global__ void __launch_bounds__(kThreads) k_attn_prefill(const float *qkv, int stride, const float *kc,
-                                                             const float *vc, int heads, int kvh, int ntok,
-                                                             int clen0, float scale, float *out, int out_stride) {
-    __shared__ PfSlot sl[2];
+// image offsets (bf16 elements) of K chunk (plane, key r, chunk j) and Vᵀ quad
+// (plane, dim d, quad q)
+__device__ __forceinline__ int pf_k_at(int plane, int r, int j) {
+    return plane * kPfKPlane + r * kHD + 8 * (j ^ (r & 15));
+}
+__device__ __forceinline__ int pf_v_at(int plane, int d, int q) {
+    return 2 * kPfKPlane + plane * kPfKPlane + d * kPfKeys + 4 * (q ^ ((d >> 1) & 7));
+}
+
+// grid (blocks, kvh): block images of cache rows [0, rows) (rows past the end
+// repeat the last one; the attention masks them)
+static __global__ void __launch_bounds__(kThreads) k_kv_blocks(const float *kc, const float *vc, int kvh, int rows,
+                                                          int nblk, uint8_t *img) {
+    const int b = blockIdx.x, g = blockIdx.y, t = threadIdx.x;
+    const int kvd = kvh * kHD;
+    __bf16 *im = reinterpret_cast<__bf16 *>(img + ((size_t)g * nblk + b) * kPfImage);
+    {   // K: key r = t/8, chunks 2·(t%8), 2·(t%8)+1
+        const int r = t >> 3, j0 = 2 * (t & 7);
+        const float4 *src = reinterpret_cast<const float4 *>(kc + (size_t)min(b * kPfKeys + r, rows - 1) * kvd +
+                                                             g * kHD + 8 * j0);
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            const float4 x0 = src[2 * c], x1 = src[2 * c + 1];
+            const float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+            v8bf h, l;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                __bf16 a, bb;
+                split_bf16(x[e], a, bb);
+                h[e] = a;
+                l[e] = bb;
+            }
+            *reinterpret_cast<v8bf *>(im + pf_k_at(0, r, j0 + c)) = h;
+            *reinterpret_cast<v8bf *>(im + pf_k_at(1, r, j0 + c)) = l;
+        }
+    }
+    {   // Vᵀ: dim d = t/2, quads 4·(t%2) .. +3
+        const int d = t >> 1, qb = 4 * (t & 1);
+#pragma unroll
+        for (int q = qb; q < qb + 4; ++q) {
+            v4bf h, l;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float x = vc[(size_t)min(b * kPfKeys + 4 * q + i, rows - 1) * kvd + g * kHD + d];
+                __bf16 a, bb;
+                split_bf16(x, a, bb);
+                h[i] = a;
+                l[i] = bb;
+            }
+            *reinterpret_cast<v4bf *>(im + pf_v_at(0, d, q)) = h;
+            *reinterpret_cast<v4bf *>(im + pf_v_at(1, d, q)) = l;
+        }
+    }
+}
+
+// max / sum over the lanes l, l^16, l^32, l^48 (the 4 lane groups of an MFMA
+// column) with VALU lane swaps: swap(x, x) leaves {x[l], x[l^16]} (resp.
+// l^32) in the two results of every lane
+__device__ __forceinline__ float groups4_max(float v) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float groups4_sum(float v) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+constexpr int kPfThreads = 512;   // 8 waves: 4 query heads × 2 key-block parities
+
+static __global__ void __launch_bounds__(kPfThreads) k_attn_prefill(const float *qkv, int stride, const uint8_t *img,
+                                                               int nblk_img, int heads, int kvh, int ntok,
+                                                               int clen0, float scale, float *out, int out_stride) {
+    // two stages of two block images (blocks 2s, 2s+1): 128 KB
+    __shared__ __attribute__((aligned(16))) uint8_t stage0[2 * kPfImage];
+    __shared__ __attribute__((aligned(16))) uint8_t stage1[2 * kPfImage];
+    constexpr int kW = kPfThreads / 64;
+    constexpr int LPS = 2 * kPfImage / 1024 / kW;  // direct loads per stage and wave (8)
     const int group = heads / kvh;
     const int quads = (group + 3) / 4;
     const int g = blockIdx.x / quads, quad = blockIdx.x % quads;
     const int t = threadIdx.x, l = t & 63;
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int par = wave >> 2;                    // key-block parity of this wave
     const int lr = l & 15, lg = l >> 4;
-    const int hl = 4 * quad + wave;               // head within the group
+    const int hl = 4 * quad + (wave & 3);         // head within the group
     const bool wave_on = hl < group;              // uniform
     const int hh = g * group + min(hl, group - 1);
-    const int kvd = kvh * kHD;
     const int nt = (ntok + kPfTok - 1) / kPfTok;
-    // staging roles: K row kk, dims 16·kd..; V keys 4·vq.., dims 4·vd..
-    const int kk = t >> 3, kd = t & 7;
-    const int vq = t >> 5, vd = t & 31;
+    const uint8_t *gimg = img + (size_t)g * nblk_img * kPfImage + (size_t)wave * LPS * 1024 + 16 * l;
+    auto issue = [&](int s, int nblk, uint8_t *st) {
+        // blocks 2s, 2s+1 are contiguous in the image; a missing 2s+1 is not loaded
+        const uint8_t *src = gimg + (size_t)(2 * s) * kPfImage;
+        const bool two = 2 * s + 1 < nblk;
+#pragma unroll
+        for (int i = 0; i < LPS; ++i) {
+            const int chunk = wave * LPS + i;  // 1 KB chunk of the stage
+            if (two || chunk < kPfImage / 1024) lds_load<16>(src + 1024 * i, st + chunk * 1024);
+        }
+    };
 
     for (int pass = 0; pass < 2; ++pass) {
         const int tile = pass == 0 ? (int)blockIdx.y : nt - 1 - (int)blockIdx.y;
@@ -847,6 +932,7 @@ static __global__ void __launch_bounds__(kThreads) k_attn_prefill(const float *q
         const int last_key = clen0 + min(q0 + kPfTok, ntok) - 1;
         const int my_last = clen0 + tq;
         const int nblk = last_key / kPfKeys + 1;
+        const int nstage = (nblk + 1) / 2;
 
         // Qᵀ operand of the first product: token lr, dims 32c + 8lg + e
         v8bf qh[4], ql[4];
@@ -871,127 +957,121 @@ static __global__ void __launch_bounds__(kThreads) k_attn_prefill(const float *q
         for (int dt = 0; dt < 8; ++dt) o[dt] = v4f{0.f, 0.f, 0.f, 0.f};
         float m = -INFINITY, lsum = 0.0f;
 
-        float4 kr[4], vr[4];
-        auto load_block = [&](int b) {
+        auto compute = [&](int b, const uint8_t *slot) {
+            const __bf16 *im = reinterpret_cast<const __bf16 *>(slot);
             const int k0 = b * kPfKeys;
-            const float *ks = kc + (size_t)min(k0 + kk, last_key) * kvd + g * kHD + 16 * kd;
+            v4f sT[2];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) kr[i] = reinterpret_cast<const float4 *>(ks)[i];
+            for (int kt = 0; kt < 2; ++kt) {
+                sT[kt] = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                vr[i] = *reinterpret_cast<const float4 *>(vc + (size_t)min(k0 + 4 * vq + i, last_key) * kvd + g * kHD +
-                                                          4 * vd);
-        };
-        auto store_block = [&](PfSlot &s) {
-#pragma unroll
-            for (int half = 0; half < 2; ++half) {
-                v8bf h, lo;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const float4 v = kr[2 * half + e / 4];
-                    const float x = e % 4 == 0 ? v.x : (e % 4 == 1 ? v.y : (e % 4 == 2 ? v.z : v.w));
-                    __bf16 a, b;
-                    split_bf16(x, a, b);
-                    h[e] = a;
-                    lo[e] = b;
+                for (int c = 0; c < 4; ++c) {
+                    const v8bf kh = *reinterpret_cast<const v8bf *>(im + pf_k_at(0, 16 * kt + lr, 4 * c + lg));
+                    const v8bf kl = *reinterpret_cast<const v8bf *>(im + pf_k_at(1, 16 * kt + lr, 4 * c + lg));
+                    sT[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, qh[c], sT[kt], 0, 0, 0);
+                    sT[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, ql[c], sT[kt], 0, 0, 0);
+                    sT[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kl, qh[c], sT[kt], 0, 0, 0);
                 }
-                *reinterpret_cast<v8bf *>(&s.k[0][kk][16 * kd + 8 * half]) = h;
-                *reinterpret_cast<v8bf *>(&s.k[1][kk][16 * kd + 8 * half]) = lo;
             }
+            // online softmax of token column lr (branch-free: masked keys get
+            // p = 0 by selection after an exp of a clamped argument)
+            float sv[8];
+            bool vis[8];
+            float mb = m;
 #pragma unroll
-            for (int d = 0; d < 4; ++d) {
-                v4bf h, lo;
+            for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const float4 v = vr[i];
-                    const float x = d == 0 ? v.x : (d == 1 ? v.y : (d == 2 ? v.z : v.w));
-                    __bf16 a, b;
-                    split_bf16(x, a, b);
-                    h[i] = a;
-                    lo[i] = b;
+                    vis[4 * kt + i] = k0 + 16 * kt + 4 * lg + i <= my_last;
+                    sv[4 * kt + i] = vis[4 * kt + i] ? sT[kt][i] * scale : -INFINITY;
+                    mb = fmaxf(mb, sv[4 * kt + i]);
                 }
-                *reinterpret_cast<v4bf *>(&s.vt[0][4 * vd + d][4 * vq]) = h;
-                *reinterpret_cast<v4bf *>(&s.vt[1][4 * vd + d][4 * vq]) = lo;
+            mb = groups4_max(mb);
+            // a column may have seen no visible key yet on this parity (mb = −∞):
+            // its p are all 0 and its running sums stay 0
+            const float mx = mb == -INFINITY ? 0.0f : mb;
+            float ps = 0.0f;
+            v8bf ph, pl;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float ex = fast_exp_ref(sv[e] - mx);
+                const float p = vis[e] ? ex : 0.0f;
+                ps += p;
+                __bf16 a, c;
+                split_bf16(p, a, c);
+                ph[e] = a;
+                pl[e] = c;
+            }
+            ps = groups4_sum(ps);
+            // rescale only when a column's maximum moved (FastExp(0) is exactly
+            // 1, so skipping is exact)
+            if (__builtin_amdgcn_ballot_w64(mb != m)) {
+                const float fe = fast_exp_ref(m - mx);
+                const float f = m == -INFINITY ? 0.0f : fe;
+                lsum *= f;
+#pragma unroll
+                for (int dt = 0; dt < 8; ++dt) o[dt] *= f;
+            }
+            lsum += ps;
+            m = mb;
+#pragma unroll
+            for (int dt = 0; dt < 8; ++dt) {
+                const int d = 16 * dt + lr;
+                const v4bf ah0 = *reinterpret_cast<const v4bf *>(im + pf_v_at(0, d, lg));
+                const v4bf ah1 = *reinterpret_cast<const v4bf *>(im + pf_v_at(0, d, 4 + lg));
+                const v4bf al0 = *reinterpret_cast<const v4bf *>(im + pf_v_at(1, d, lg));
+                const v4bf al1 = *reinterpret_cast<const v4bf *>(im + pf_v_at(1, d, 4 + lg));
+                const v8bf vh = __builtin_shufflevector(ah0, ah1, 0, 1, 2, 3, 4, 5, 6, 7);
+                const v8bf vl = __builtin_shufflevector(al0, al1, 0, 1, 2, 3, 4, 5, 6, 7);
+                o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vh, ph, o[dt], 0, 0, 0);
+                o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vh, pl, o[dt], 0, 0, 0);
+                o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vl, ph, o[dt], 0, 0, 0);
             }
         };
-
-        load_block(0);
-        __syncthreads();  // the previous tile's last block is read
-        store_block(sl[0]);
-        __syncthreads();
-        for (int b = 0; b < nblk; ++b) {
-            const bool more = b + 1 < nblk;  // uniform
-            if (more) load_block(b + 1);
-            if (wave_on) {
-                const PfSlot &s = sl[b & 1];
-                const int k0 = b * kPfKeys;
-                v4f sT[2];
-#pragma unroll
-                for (int kt = 0; kt < 2; ++kt) {
-                    sT[kt] = v4f{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                    for (int c = 0; c < 4; ++c) {
-                        const v8bf kh = *reinterpret_cast<const v8bf *>(&s.k[0][16 * kt + lr][32 * c + 8 * lg]);
-                        const v8bf kl = *reinterpret_cast<const v8bf *>(&s.k[1][16 * kt + lr][32 * c + 8 * lg]);
-                        sT[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, qh[c], sT[kt], 0, 0, 0);
-                        sT[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, ql[c], sT[kt], 0, 0, 0);
-                        sT[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kl, qh[c], sT[kt], 0, 0, 0);
-                    }
-                }
-                // online softmax of token column lr
-                float sv[8];
-                float mb = m;
-#pragma unroll
-                for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const int key = k0 + 16 * kt + 4 * lg + i;
-                        sv[4 * kt + i] = key <= my_last ? sT[kt][i] * scale : -INFINITY;
-                        mb = fmaxf(mb, sv[4 * kt + i]);
-                    }
-                mb = fmaxf(mb, xchg<XS16>(mb));
-                mb = fmaxf(mb, xchg<XS32>(mb));
-                // mb is finite: key 0 is visible to every token
-                float ps = 0.0f;
-                v8bf ph, pl;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const float p = sv[e] == -INFINITY ? 0.0f : fast_exp_ref(sv[e] - mb);
-                    ps += p;
-                    __bf16 a, c;
-                    split_bf16(p, a, c);
-                    ph[e] = a;
-                    pl[e] = c;
-                }
-                ps += xchg<XS16>(ps);
-                ps += xchg<XS32>(ps);
-                const float f = m == -INFINITY ? 0.0f : fast_exp_ref(m - mb);
-                lsum = lsum * f + ps;
-                m = mb;
-#pragma unroll
-                for (int dt = 0; dt < 8; ++dt) {
-                    o[dt] *= f;
-                    const v4bf ah0 = *reinterpret_cast<const v4bf *>(&s.vt[0][16 * dt + lr][4 * lg]);
-                    const v4bf ah1 = *reinterpret_cast<const v4bf *>(&s.vt[0][16 * dt + lr][16 + 4 * lg]);
-                    const v4bf al0 = *reinterpret_cast<const v4bf *>(&s.vt[1][16 * dt + lr][4 * lg]);
-                    const v4bf al1 = *reinterpret_cast<const v4bf *>(&s.vt[1][16 * dt + lr][16 + 4 * lg]);
-                    const v8bf vh = __builtin_shufflevector(ah0, ah1, 0, 1, 2, 3, 4, 5, 6, 7);
-                    const v8bf vl = __builtin_shufflevector(al0, al1, 0, 1, 2, 3, 4, 5, 6, 7);
-                    o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vh, ph, o[dt], 0, 0, 0);
-                    o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vh, pl, o[dt], 0, 0, 0);
-                    o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vl, ph, o[dt], 0, 0, 0);
-                }
-            }
-            if (more) store_block(sl[(b + 1) & 1]);
-            __syncthreads();
+        // stage s: wait for this wave's loads of s, barrier (every wave's loads
+        // of s have landed; every wave is done with s−1, whose buffer takes
+        // s+1), then this wave's block 2s + parity
+        auto body = [&](int s, const uint8_t *cur, uint8_t *next) {
+            wait_vm<0>();
+            lds_barrier();
+            if (s + 1 < nstage) issue(s + 1, nblk, next);
+            const int b = 2 * s + par;
+            if (wave_on && b < nblk) compute(b, cur + par * kPfImage);
+        };
+        lds_barrier();  // the previous tile's stages are read
+        issue(0, nblk, stage0);
+        for (int s = 0; s < nstage; s += 2) {
+            body(s, stage0, stage1);
+            if (s + 1 < nstage) body(s + 1, stage1, stage0);
         }
-        if (wave_on && q0 + lr < ntok) {
-            const float inv = 1.0f / lsum;
-            float *dst = out + (size_t)(q0 + lr) * out_stride + (size_t)hh * kHD + 4 * lg;
+
+        // merge the two parities of each head through LDS (stage0 is free
+        // after the barrier: no loads are in flight)
+        lds_barrier();
+        float *mrg = reinterpret_cast<float *>(stage0) + (size_t)((wave & 3) * 64 + l) * 34;
+        if (par == 1) {
+            mrg[0] = m;
+            mrg[1] = lsum;
 #pragma unroll
             for (int dt = 0; dt < 8; ++dt)
-                *reinterpret_cast<float4 *>(dst + 16 * dt) =
-                    make_float4(o[dt][0] * inv, o[dt][1] * inv, o[dt][2] * inv, o[dt][3] * inv);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) mrg[2 + 4 * dt + i] = o[dt][i];
+        }
+        lds_barrier();
+        if (par == 0 && wave_on && q0 + lr < ntok) {
+            const float m1 = mrg[0], l1 = mrg[1];
+            const float M = fmaxf(m, m1);  // finite: key 0 is in block 0
+            const float f0 = m == -INFINITY ? 0.0f : fast_exp_ref(m - M);
+            const float f1 = m1 == -INFINITY ? 0.0f : fast_exp_ref(m1 - M);
+            const float inv = 1.0f / (lsum * f0 + l1 * f1);
+            float *dst = out + (size_t)(q0 + lr) * out_stride + (size_t)hh * kHD + 4 * lg;
+#pragma unroll
+            for (int dt = 0; dt < 8; ++dt) {
+                float r[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) r[i] = (o[dt][i] * f0 + mrg[2 + 4 * dt + i] * f1) * inv;
+                *reinterpret_cast<float4 *>(dst + 16 * dt) = make_float4(r[0], r[1], r[2], r[3]);
+            }
         }
     }
 }

@@ -111,7 +111,9 @@ struct PrefillBufs {
     float *xs = nullptr;     // [rows] digit row scales
     int *xb = nullptr;       // [rows][4] digit sums
     int32_t *pos = nullptr;  // [rows][3]
+    uint8_t *kvimg = nullptr;  // one layer's attention block images [kv head][block][32 KB]
     int cap_rows = 0;        // rows allocated (a multiple of 32)
+    int img_blocks = 0;      // key blocks per kv head in kvimg
 };
 void prefill_free(PrefillBufs &b);
 

@@ -6,7 +6,7 @@ using namespace pocr;
 
 void prefill_free(PrefillBufs &b) {
     for (void *p : {(void *)b.h, (void *)b.v, (void *)b.qkv, (void *)b.ho, (void *)b.g, (void *)b.xd, (void *)b.xs,
-                    (void *)b.xb, (void *)b.pos})
+                    (void *)b.xb, (void *)b.pos, (void *)b.kvimg})
         if (p) (void)hipFree(p);
     b = PrefillBufs{};
 }
@@ -106,7 +106,9 @@ int grow(T *&p, size_t count) {
 
 int ensure_bufs(pocr_seq *s, int rows) {
     PrefillBufs &b = s->pf;
-    if (rows <= b.cap_rows) return POCR_OK;
+    const int img_blocks = (s->cap + kPfKeys - 1) / kPfKeys;
+    if (rows <= b.cap_rows && img_blocks <= b.img_blocks) return POCR_OK;
+    rows = std::max(rows, b.cap_rows);
     const pocr_config &c = s->m->cfg;
     const size_t H = c.hidden, Q = (size_t)c.heads * c.head_dim, KV = (size_t)c.kv_heads * c.head_dim;
     const size_t kmax = std::max({H, Q, (size_t)c.intermediate});
@@ -120,7 +122,9 @@ int ensure_bufs(pocr_seq *s, int rows) {
     RC(grow(b.xs, (size_t)rows));
     RC(grow(b.xb, (size_t)rows * 4));
     RC(grow(b.pos, (size_t)rows * 3));
+    RC(grow(b.kvimg, (size_t)c.kv_heads * img_blocks * kPfImage));
     b.cap_rows = rows;
+    b.img_blocks = img_blocks;
     return POCR_OK;
 }
 
@@ -273,8 +277,11 @@ int prefill_locked(pocr_seq *s, int n, const float *emb, const int32_t *pos3, fl
         hipLaunchKernelGGL(k_rope_append, dim3(n), dim3(kThreads), 0, st, b.qkv, QKV, b.pos, m->freq, m->axis,
                            c.heads, c.kv_heads, c.head_dim, layer_k(s, li), layer_v(s, li), clen0);
         const int ntiles = (n + kPfTok - 1) / kPfTok, quads = (c.heads / c.kv_heads + 3) / 4;
-        hipLaunchKernelGGL(k_attn_prefill, dim3(c.kv_heads * quads, (ntiles + 1) / 2), dim3(kThreads), 0, st,
-                           b.qkv, QKV, layer_k(s, li), layer_v(s, li), c.heads, c.kv_heads, n, clen0, scale, b.ho, Q);
+        const int nblk = (clen0 + n + kPfKeys - 1) / kPfKeys;
+        hipLaunchKernelGGL(k_kv_blocks, dim3(nblk, c.kv_heads), dim3(kThreads), 0, st, layer_k(s, li), layer_v(s, li),
+                           c.kv_heads, clen0 + n, nblk, b.kvimg);
+        hipLaunchKernelGGL(k_attn_prefill, dim3(c.kv_heads * quads, (ntiles + 1) / 2), dim3(kPfThreads), 0, st, b.qkv,
+                           QKV, b.kvimg, nblk, c.heads, c.kv_heads, n, clen0, scale, b.ho, Q);
         HIP_TRY(hipGetLastError());
         // 3. o_proj + residual (+ the Q4/Q6 behaviour per token) → v; h if in place
         RC(digitize(b.ho, Q, nullptr, Q));
