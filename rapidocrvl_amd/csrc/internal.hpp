@@ -67,6 +67,11 @@ struct pocr_ctx {
     // op-level staging
     DevBuf x, out, out2, out3, res, vbuf, kc, vc, part, tabs, state;
     DevBuf gxd, gxs, gxb;  // batched GEMV activation digits
+    // pinned host staging for large host→device uploads: two halves, each
+    // reused once the copy recorded on its event has finished
+    uint8_t *pin = nullptr;
+    size_t pin_half = 0;
+    hipEvent_t pin_ev[2] = {nullptr, nullptr};
 };
 
 struct pocr_weight {
@@ -145,6 +150,13 @@ GemvParams gemv_params_1(const pocr_weight *w);
 int step_locked(pocr_seq *s, const float *emb, const int32_t pos3[3], int need_logits, float *logits,
                 int32_t *token);
 int prefill_locked(pocr_seq *s, int n, const float *emb, const int32_t *pos3, float *logits, int32_t *token);
+// prefill from token ids: image rows uploaded straight into the device rows,
+// text rows gathered from the device embedding table; POCR_ERR_UNSUPPORTED
+// (no error recorded) when the model's shapes need the token-by-token path
+int prefill_ids_locked(pocr_seq *s, const int32_t *ids, int n, const float *image, int32_t image_token,
+                       const int32_t *pos3, float *logits, int32_t *token);
+// host → device copy through the context's pinned staging (stream-ordered)
+int upload_staged(pocr_ctx *ctx, void *dst, const void *src, size_t bytes);
 int batched_gemv(pocr_ctx *ctx, const DevMat &w, const float *x, int m, float *out);
 int read_state(pocr_seq *s, StepState *out);
 unsigned long long argmax_of(const StepState &s);

@@ -106,7 +106,33 @@ void pocr::ctx_release(pocr_ctx *ctx) {
         (void)hipStreamSynchronize(ctx->stream);
         (void)hipStreamDestroy(ctx->stream);
     }
+    for (hipEvent_t &e : ctx->pin_ev)
+        if (e) (void)hipEventDestroy(e);
+    if (ctx->pin) (void)hipHostFree(ctx->pin);
     delete ctx;
+}
+
+// Chunks of at most pin_half bytes alternate between the two pinned halves:
+// the host copy into a half waits only for that half's previous transfer, so
+// the memcpy of one chunk overlaps the DMA of the one before.
+int pocr::upload_staged(pocr_ctx *ctx, void *dst, const void *src, size_t bytes) {
+    constexpr size_t kHalf = 2u << 20;
+    if (!ctx->pin) {
+        HIP_TRY(hipHostMalloc((void **)&ctx->pin, 2 * kHalf, hipHostMallocDefault));
+        ctx->pin_half = kHalf;
+        for (hipEvent_t &e : ctx->pin_ev) HIP_TRY(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+    }
+    const uint8_t *s8 = static_cast<const uint8_t *>(src);
+    uint8_t *d8 = static_cast<uint8_t *>(dst);
+    for (size_t off = 0, c = 0; off < bytes; off += ctx->pin_half, ++c) {
+        const size_t len = std::min(ctx->pin_half, bytes - off);
+        uint8_t *half = ctx->pin + (c & 1) * ctx->pin_half;
+        HIP_TRY(hipEventSynchronize(ctx->pin_ev[c & 1]));
+        std::memcpy(half, s8 + off, len);
+        HIP_TRY(hipMemcpyAsync(d8 + off, half, len, hipMemcpyHostToDevice, ctx->stream));
+        HIP_TRY(hipEventRecord(ctx->pin_ev[c & 1], ctx->stream));
+    }
+    return POCR_OK;
 }
 
 extern "C" void pocr_ctx_destroy(pocr_ctx *ctx) { ctx_release(ctx); }
@@ -1345,12 +1371,28 @@ extern "C" int pocr_generate(pocr_seq *s, const int32_t *ids, int n_ids, const f
     } else {
         for (int i = 0; i < n_ids; ++i) pos[3 * i] = pos[3 * i + 1] = pos[3 * i + 2] = i;
     }
-    std::vector<float> emb((size_t)n_ids * H);
-    std::vector<float> row(H);
+    int n_placeholders = 0;
+    for (int i = 0; i < n_ids; ++i) {
+        if (n_image > 0 && ids[i] == image_token_id) ++n_placeholders;
+        else if (ids[i] < 0 || ids[i] >= m->cfg.vocab) return fail(POCR_ERR_ARG, "token id %d outside vocab", ids[i]);
+    }
+    if (n_placeholders != n_image)
+        return fail(POCR_ERR_ARG, "image placeholder tokens: got %d need %d", n_placeholders, n_image);
+    std::vector<float> emb;
     int img = 0;
     {
         std::lock_guard<std::mutex> lk(m->ctx->mu);
         HIP_TRY(hipSetDevice(m->ctx->device));
+        RC(seq_set_state(s, 0));
+        if (n_ids + max_new - 1 > s->cap) return fail(POCR_ERR_ARG, "pocr_generate: capacity %d too small", s->cap);
+        int32_t next = -1;
+        if (use_prefill) {
+            const int rc = prefill_ids_locked(s, ids, n_ids, n_image > 0 ? image_embeds : nullptr,
+                                              n_image > 0 ? image_token_id : -1, pos.data(), nullptr, &next);
+            if (rc == POCR_OK) return decode_locked(s, next, n_ids + rope_delta, max_new, eos, n_eos, out_tokens);
+            if (rc != POCR_ERR_UNSUPPORTED) return rc;
+        }
+        emb.resize((size_t)n_ids * H);
         for (int i = 0; i < n_ids; ++i) {
             if (n_image > 0 && ids[i] == image_token_id) {
                 if (img >= n_image) return fail(POCR_ERR_ARG, "too many image placeholder tokens");
@@ -1362,10 +1404,6 @@ extern "C" int pocr_generate(pocr_seq *s, const int32_t *ids, int n_ids, const f
                                   hipMemcpyDeviceToHost));
             }
         }
-        if (img != n_image) return fail(POCR_ERR_ARG, "not enough image placeholder tokens: got %d need %d", img, n_image);
-        RC(seq_set_state(s, 0));
-        if (n_ids + max_new - 1 > s->cap) return fail(POCR_ERR_ARG, "pocr_generate: capacity %d too small", s->cap);
-        int32_t next = -1;
         if (use_prefill) {
             RC(prefill_locked(s, n_ids, emb.data(), pos.data(), nullptr, &next));
         } else {

@@ -121,7 +121,7 @@ int ensure_bufs(pocr_seq *s, int rows) {
     RC(grow(b.xd, 3 * rows * kmax));
     RC(grow(b.xs, (size_t)rows));
     RC(grow(b.xb, (size_t)rows * 4));
-    RC(grow(b.pos, (size_t)rows * 3));
+    RC(grow(b.pos, (size_t)rows * 4));  // positions [rows][3], then the prompt ids
     RC(grow(b.kvimg, (size_t)c.kv_heads * img_blocks * kPfImage));
     b.cap_rows = rows;
     b.img_blocks = img_blocks;
@@ -214,20 +214,77 @@ int batched_gemv(pocr_ctx *ctx, const DevMat &w, const float *x, int m, float *o
 // planes → MFMA GEMMs with the step's epilogues, per-token RoPE + K/V append,
 // causal attention), then the LM head on the last token.  Per-token semantics
 // match n sequential steps (model.go:1514-1536, 3475-3643).
-int prefill_locked(pocr_seq *s, int n, const float *emb, const int32_t *pos3, float *logits, int32_t *token) {
-    pocr_model *m = s->m;
+namespace {
+
+bool batched_prefill_on(const pocr_model *m) {
     const char *env = getenv("POCR_BATCHED_PREFILL");
-    if ((env && env[0] == '0') || !prefill_supported(m)) return prefill_tokenwise(s, n, emb, pos3, logits, token);
+    return !(env && env[0] == '0') && prefill_supported(m);
+}
+
+// text rows of the prompt from the device embedding table; image rows
+// (id == image_token) are left as uploaded
+__global__ void k_embed_rows(const int32_t *ids, int n, int32_t image_token, const float *embed, int H, float *h) {
+    const int i = blockIdx.x;
+    if (i >= n || ids[i] == image_token) return;
+    const float4 *src = reinterpret_cast<const float4 *>(embed + (size_t)ids[i] * H);
+    float4 *dst = reinterpret_cast<float4 *>(h + (size_t)i * H);
+    for (int c = threadIdx.x; c < H / 4; c += blockDim.x) dst[c] = src[c];
+}
+
+// the layers over b.h (the n embedding rows) and the LM head on the last row
+int prefill_run(pocr_seq *s, int n, const int32_t *pos3, float *logits, int32_t *token);
+
+}  // namespace
+
+int prefill_locked(pocr_seq *s, int n, const float *emb, const int32_t *pos3, float *logits, int32_t *token) {
+    if (!batched_prefill_on(s->m)) return prefill_tokenwise(s, n, emb, pos3, logits, token);
+    if (s->len + n > s->cap) return fail(POCR_ERR_ARG, "prefill: %d rows exceed capacity", n);
+    RC(ensure_bufs(s, round_up(n, 32)));
+    RC(upload_staged(s->m->ctx, s->pf.h, emb, (size_t)n * s->m->cfg.hidden * 4));
+    return prefill_run(s, n, pos3, logits, token);
+}
+
+int prefill_ids_locked(pocr_seq *s, const int32_t *ids, int n, const float *image, int32_t image_token,
+                       const int32_t *pos3, float *logits, int32_t *token) {
+    pocr_model *m = s->m;
+    if (!batched_prefill_on(m) || m->cfg.hidden % 4) return POCR_ERR_UNSUPPORTED;
+    if (s->len + n > s->cap) return fail(POCR_ERR_ARG, "prefill: %d rows exceed capacity", n);
+    const int H = m->cfg.hidden;
+    RC(ensure_bufs(s, round_up(n, 32)));
+    PrefillBufs &b = s->pf;
+    // runs of image placeholders: their rows straight from the caller's buffer
+    int img = 0;
+    for (int i = 0; i < n;) {
+        if (!image || ids[i] != image_token) {
+            ++i;
+            continue;
+        }
+        int j = i;
+        while (j < n && ids[j] == image_token) ++j;
+        RC(upload_staged(m->ctx, b.h + (size_t)i * H, image + (size_t)img * H, (size_t)(j - i) * H * 4));
+        img += j - i;
+        i = j;
+    }
+    // ids ride in the position buffer's tail (rows·3 int32 + n)
+    HIP_TRY(hipMemcpyAsync(b.pos + (size_t)3 * b.cap_rows, ids, (size_t)n * 4, hipMemcpyHostToDevice,
+                           m->ctx->stream));
+    hipLaunchKernelGGL(k_embed_rows, dim3(n), dim3(kThreads), 0, m->ctx->stream, b.pos + (size_t)3 * b.cap_rows, n,
+                       image ? image_token : -1, m->embed, H, b.h);
+    HIP_TRY(hipGetLastError());
+    return prefill_run(s, n, pos3, logits, token);
+}
+
+namespace {
+
+int prefill_run(pocr_seq *s, int n, const int32_t *pos3, float *logits, int32_t *token) {
+    pocr_model *m = s->m;
     const pocr_config &c = m->cfg;
     hipStream_t st = m->ctx->stream;
     const int H = c.hidden, Q = c.heads * c.head_dim, KV = c.kv_heads * c.head_dim, F = c.intermediate;
     const int QKV = Q + 2 * KV;
     const int clen0 = s->len;
-    if (clen0 + n > s->cap) return fail(POCR_ERR_ARG, "prefill: %d rows exceed capacity", n);
     const int npad = round_up(n, 32);
-    RC(ensure_bufs(s, npad));
     PrefillBufs &b = s->pf;
-    HIP_TRY(hipMemcpyAsync(b.h, emb, (size_t)n * H * 4, hipMemcpyHostToDevice, st));
     HIP_TRY(hipMemcpyAsync(b.pos, pos3, (size_t)n * 12, hipMemcpyHostToDevice, st));
     const float eps = c.rms_norm_eps;
     const float scale = (float)(1.0 / std::sqrt((double)c.head_dim));
@@ -338,5 +395,7 @@ int prefill_locked(pocr_seq *s, int n, const float *emb, const int32_t *pos3, fl
     if (logits) HIP_TRY(hipMemcpy(logits, s->logits, (size_t)c.vocab * 4, hipMemcpyDeviceToHost));
     return POCR_OK;
 }
+
+}  // namespace
 
 }  // namespace pocr
