@@ -125,24 +125,23 @@ __host__ __device__ constexpr int digit_pos16(int c) {
     return QT == QT_Q4 ? ((c & 1) ? 8 + (c >> 1) : (c >> 1)) : c;
 }
 
+// Weights stream once per launch: non-temporal loads (global_load … nt).
 template <int QT>
 __device__ __forceinline__ Chunk load_chunk(const uint8_t *p) {
     Chunk c;
     if constexpr (QT == QT_Q6) {
-        struct __attribute__((aligned(4))) U3 {
-            uint32_t a, b, c;
-        };
-        U3 v = *reinterpret_cast<const U3 *>(p);
-        c.d[0] = v.a;
-        c.d[1] = v.b;
-        c.d[2] = v.c;
+        const uint32_t *q = reinterpret_cast<const uint32_t *>(p);  // 4-byte aligned 12-byte chunk
+        c.d[0] = __builtin_nontemporal_load(q);
+        c.d[1] = __builtin_nontemporal_load(q + 1);
+        c.d[2] = __builtin_nontemporal_load(q + 2);
         c.d[3] = 0;
     } else {
-        uint4 v = *reinterpret_cast<const uint4 *>(p);
-        c.d[0] = v.x;
-        c.d[1] = v.y;
-        c.d[2] = v.z;
-        c.d[3] = v.w;
+        typedef unsigned u4v __attribute__((ext_vector_type(4)));
+        const u4v v = __builtin_nontemporal_load(reinterpret_cast<const u4v *>(p));
+        c.d[0] = v[0];
+        c.d[1] = v[1];
+        c.d[2] = v[2];
+        c.d[3] = v[3];
     }
     return c;
 }
