@@ -10,6 +10,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <type_traits>
 #include <stdint.h>
 
 namespace pocr {
@@ -242,6 +243,23 @@ struct XDigits {
     float scale_comb[CPL];
 };
 
+// Q4 nibble planes (NPL = kNibPlanes, the greedy LM head): the activation of
+// a 32-column chunk as four balanced base-15 digit planes
+//   x = S·(e0 + e1/15 + e2/15² + e3/15³) + e,   e_k ∈ [−7, 7],
+// S a power of two > max|x|/7 over the chunk, |e| ≤ S/(2·15³) (≈2^-14.5 of
+// the chunk maximum).  A plane packs 8 columns per dword as signed nibbles in
+// column order — the order of the Q4 codes in a weight dword — and a code
+// nibble u = code + 8 becomes the signed nibble code by u ^ 8, so a row dot
+// is one XOR and four v_dot8_i32_i4 per weight dword, combined in integer.
+constexpr int kNibPlanes = 4;
+template <int CPL>
+struct XNib {
+    int n[CPL][4][4];       // [chunk][dword k: columns 8k..8k+7][plane]
+    float scale_comb[CPL];  // S / 15³
+};
+template <int QT, int CPL, int NPL>
+using XDig = typename std::conditional<NPL == kNibPlanes, XNib<CPL>, XDigits<QT, CPL>>::type;
+
 // column (within a chunk) of byte m of digit dword k: Q4 dword 2k' holds the
 // low nibbles of chunk dword k' (cols 8k'+0,2,4,6), dword 2k'+1 the high ones
 // (cols 8k'+1,3,5,7); Q8/Q6 dword k holds cols 4k..4k+3.
@@ -285,8 +303,27 @@ __device__ __forceinline__ int spread6(uint32_t g) {
     return (int)r;
 }
 
+template <int CPL>
+__device__ __forceinline__ float row_dot_nib(const Chunk (&w)[CPL], const XNib<CPL> &xd) {
+    float r = 0.0f;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+        int a[4] = {0, 0, 0, 0};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int sw = (int)(w[j].d[k] ^ 0x88888888u);  // signed codes, column order
+#pragma unroll
+            for (int pl = 0; pl < 4; ++pl) a[pl] = __builtin_amdgcn_sdot8(sw, xd.n[j][k][pl], a[pl], false);
+        }
+        // |a| ≤ 32·8·7: the base-15 combination stays far inside int32
+        const int comb = ((a[0] * 15 + a[1]) * 15 + a[2]) * 15 + a[3];
+        r = fmaf(xd.scale_comb[j], (float)comb, r);
+    }
+    return r;
+}
+
 template <int QT, int CPL, int NPL = 3>
-__device__ __forceinline__ float row_dot(const Chunk (&w)[CPL], const XDigits<QT, CPL> &xd) {
+__device__ __forceinline__ float row_dot_bytes(const Chunk (&w)[CPL], const XDigits<QT, CPL> &xd) {
     float r = 0.0f;
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
@@ -320,6 +357,16 @@ __device__ __forceinline__ float row_dot(const Chunk (&w)[CPL], const XDigits<QT
         }
     }
     return r;
+}
+
+template <int QT, int CPL, int NPL = 3>
+__device__ __forceinline__ float row_dot(const Chunk (&w)[CPL], const XDig<QT, CPL, NPL> &xd) {
+    if constexpr (NPL == kNibPlanes) {
+        static_assert(QT == QT_Q4, "nibble planes pair with Q4 codes");
+        return row_dot_nib<CPL>(w, xd);
+    } else {
+        return row_dot_bytes<QT, CPL, NPL>(w, xd);
+    }
 }
 
 // Cross-lane exchanges used by the reduce-scatter.  Each pairs every lane with
@@ -539,10 +586,107 @@ __device__ __forceinline__ float x_digits(const XRegs &r, bool norm, int cols, f
     return fast_rsqrt_ref(tot / (float)cols + eps);
 }
 
+// Nibble-plane prologue (Q4 greedy head): thread t owns 4 consecutive
+// columns per pass (1024 columns a pass), so all 256 threads share the digit
+// work; the 8 threads of a 32-column chunk are adjacent lanes, and lanes 2m,
+// 2m+1 each build half of the chunk's nibble dword m of every plane.
+constexpr int kNibPass = 4 * kThreads;
+__device__ __forceinline__ void x_load_nib(const float *x, const float *nw, bool norm, int cols, XRegs &r) {
+#pragma unroll
+    for (int pp = 0; pp < kMaxCols / kNibPass; ++pp) {
+        if (pp * kNibPass >= cols) break;  // uniform
+        const int cb = min((pp * kThreads + (int)threadIdx.x) * 4, cols - 4);
+        r.x[pp >> 1][pp & 1] = *reinterpret_cast<const float4 *>(x + cb);
+        if (norm) r.w[pp >> 1][pp & 1] = *reinterpret_cast<const float4 *>(nw + cb);
+    }
+}
+
+__device__ __forceinline__ int xchg_i(int v) { return __float_as_int(xchg<XQ1>(__int_as_float(v))); }
+
+__device__ __forceinline__ float x_digits_nib(const XRegs &r, bool norm, int cols, float eps, int *lds, float *red) {
+    constexpr int NDW = DigitRec<QT_Q4>::NDW, RS = DigitRec<QT_Q4>::RS;
+    const int lane = threadIdx.x & 63;
+    float ss = 0.0f;
+#pragma unroll
+    for (int pp = 0; pp < kMaxCols / kNibPass; ++pp) {
+        if (pp * kNibPass >= cols) break;  // uniform
+        const int G = pp * kThreads + (int)threadIdx.x;  // 4-column group
+        const bool valid = G * 4 < cols;
+        const float4 xv = r.x[pp >> 1][pp & 1];
+        float y[4] = {xv.x, xv.y, xv.z, xv.w};
+        if (norm) {
+            const float4 wv = r.w[pp >> 1][pp & 1];
+            const float w[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                ss = valid ? fmaf(y[i], y[i], ss) : ss;
+                y[i] = y[i] * w[i];  // a lone product: nothing to contract
+            }
+        }
+        float m = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) m = fmaxf(m, fabsf(y[i]));
+        m = fmaxf(m, xchg<XQ1>(m));
+        m = fmaxf(m, xchg<XQ2>(m));
+        m = fmaxf(m, xchg<XM8>(m));  // the chunk's 8 lanes
+        int ex = 0;
+        (void)frexpf(m * (1.0f / 7.0f), &ex);  // |x|·2^-ex < 7 (+ rounding)
+        const float inv = m > 0.0f ? ldexpf(1.0f, -ex) : 1.0f;
+        const int sh = 16 * (G & 1);  // this lane's half of the dword
+        int pk[4] = {0, 0, 0, 0};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float t = y[i] * inv;  // exact: inv is a power of two
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                // |t| ≤ 7.5 → e ∈ [−7, 7] and |t − e| ≤ 1/2
+                const float e = __builtin_amdgcn_fmed3f(rintf(t), -7.0f, 7.0f);
+                pk[k] |= ((int)e & 15) << (4 * i + sh);
+                t = fmaf(t, 15.0f, -15.0f * e);  // (t − e)·15, one rounding
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) pk[k] |= xchg_i(pk[k]);
+        if (valid && (G & 1) == 0) {
+            const int c = G / 8, q = (G & 7) >> 1;
+            int *rec = lds + c * RS;
+            *reinterpret_cast<int4 *>(rec + 4 * q) = make_int4(pk[0], pk[1], pk[2], pk[3]);
+            if (q == 0) rec[NDW * 3 + 3] = __float_as_int(m > 0.0f ? ldexpf(1.0f, ex) : 1.0f);
+        }
+    }
+    if (norm) {
+        ss = wave_sum(ss);
+        if (lane == 0) red[threadIdx.x >> 6] = ss;
+    }
+    __syncthreads();
+    if (!norm) return 1.0f;
+    float tot = red[0];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) tot += red[w];
+    // RMSNorm (ops.go:1015-1037): x·fastRsqrt(Σx²/n + eps)·w
+    return fast_rsqrt_ref(tot / (float)cols + eps);
+}
+
 // The lane's CPL chunk records (chunks l + j·LPR) → registers.
 template <int QT, int LPR, int CPL, int NPL = 3>
-__device__ __forceinline__ void load_digits(const int *lds, int l, XDigits<QT, CPL> &xd) {
+__device__ __forceinline__ void load_digits(const int *lds, int l, XDig<QT, CPL, NPL> &xd) {
     constexpr int NDW = DigitRec<QT>::NDW, RS = DigitRec<QT>::RS;
+    if constexpr (NPL == kNibPlanes) {
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            const int4 *rec = reinterpret_cast<const int4 *>(lds + (l + j * LPR) * RS);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int4 t = rec[k];
+                xd.n[j][k][0] = t.x;
+                xd.n[j][k][1] = t.y;
+                xd.n[j][k][2] = t.z;
+                xd.n[j][k][3] = t.w;
+            }
+            xd.scale_comb[j] = __int_as_float(lds[(l + j * LPR) * RS + NDW * 3 + 3]) * (1.0f / 3375.0f);
+        }
+        return;
+    } else {
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
         const int4 *rec = reinterpret_cast<const int4 *>(lds + (l + j * LPR) * RS);
@@ -570,6 +714,7 @@ __device__ __forceinline__ void load_digits(const int *lds, int l, XDigits<QT, C
             xd.bias_comb[j] = xd.bias[j][0] * 128 + xd.bias[j][1];
             xd.scale_comb[j] = xd.scale[j] * (1.0f / 128.0f);
         }
+    }
     }
 }
 
@@ -843,7 +988,8 @@ __device__ __forceinline__ void gemv_body(GemvParams p, int pro, int epi) {
     const int cols = p.cols;
     const bool norm = pro == PRO_RMSNORM;
     XRegs xr;
-    x_load(p.x, p.norm_w, norm, cols, xr);
+    if constexpr (NPL == kNibPlanes) x_load_nib(p.x, p.norm_w, norm, cols, xr);
+    else x_load(p.x, p.norm_w, norm, cols, xr);
     // first group: weights, then the writer lane's epilogue operands (row
     // scale, residual), all requested before the prologue's first wait
     Chunk w[U][NMAT][CPL];
@@ -857,8 +1003,10 @@ __device__ __forceinline__ void gemv_body(GemvParams p, int pro, int epi) {
         for (int mi = 0; mi < NMAT; ++mi) scl[mi] = (mi == 0 ? sel.scale0 : sel.scale1)[rc - sel.start];
         resid = need_resid ? p.residual[rc] : 0.0f;
     }
-    const float xscale = x_digits<QT>(xr, norm, cols, p.eps, lds, red);
-    XDigits<QT, CPL> xd;
+    float xscale;
+    if constexpr (NPL == kNibPlanes) xscale = x_digits_nib(xr, norm, cols, p.eps, lds, red);
+    else xscale = x_digits<QT>(xr, norm, cols, p.eps, lds, red);
+    XDig<QT, CPL, NPL> xd;
     load_digits<QT, LPR, CPL, NPL>(lds, l, xd);
     const bool in_place = epi == EPI_OPROJ ? oproj_in_place(p) : false;
     float best_v = -INFINITY;

@@ -249,14 +249,14 @@ static bool gemv_fast_kernel(int lpr, int cpl, const void **fn) {
 #define POCR_BIG_GRID 4096  // enough for one group per wave up to 262144 rows
 #endif
 constexpr int kBigU = POCR_BIG_U;
-#ifndef POCR_BIG_PLANES
-#define POCR_BIG_PLANES 2
-#endif
-constexpr int kBigPlanes = POCR_BIG_PLANES;
+// digit planes of the greedy LM head: Q4 → the nibble planes (v_dot8),
+// Q8 / Q6 → two byte planes
+template <int QT>
+constexpr int big_planes() { return QT == QT_Q4 ? kNibPlanes : 2; }
 
 // one: every wave gets at most one row group (the big launch covers them all);
 // argmax: the greedy LM head, whose scores only feed the argmax, takes
-// kBigPlanes digit planes, every other launch three
+// big_planes<QT>() digit planes, every other launch three byte planes
 template <int QT, int NPL>
 static bool pick_big(int tag, bool one, int lpr, int cpl, const void **fn) {
     if (one)
@@ -269,7 +269,8 @@ static bool pick_big(int tag, bool one, int lpr, int cpl, const void **fn) {
 template <int QT>
 static bool pick_fast(int nmat, int u, int tag, int lpr, int cpl, bool one, bool argmax, const void **fn) {
     if (nmat == 2) return gemv_fast_kernel<QT, 2, 2>(lpr, cpl, fn);
-    if (u == kBigU) return argmax ? pick_big<QT, kBigPlanes>(tag, one, lpr, cpl, fn) : pick_big<QT, 3>(tag, one, lpr, cpl, fn);
+    if (u == kBigU)
+        return argmax ? pick_big<QT, big_planes<QT>()>(tag, one, lpr, cpl, fn) : pick_big<QT, 3>(tag, one, lpr, cpl, fn);
     return tag == 1 ? gemv_fast_kernel<QT, 1, 2, 1>(lpr, cpl, fn) : gemv_fast_kernel<QT, 1, 2>(lpr, cpl, fn);
 }
 
