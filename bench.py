@@ -45,6 +45,39 @@ def workload_ids():
     return np.concatenate([head, np.full(1332, IMAGE_TOKEN, np.int32), tail]).astype(np.int32)
 
 
+def batch_decode(model, cfg, n_seq=4, n_new=1024, reps=2):
+    """Server-style generation: n_seq independent sequences (5 ids + 1332 visual
+    rows + 11 ids, seeds 0..n_seq-1), each prefilled, then greedy-decoded
+    together for n_new tokens (one device step per token for all of them: the
+    layer GEMVs run at M = n_seq).  Returns aggregate tok/s of the last rep."""
+    from rapidocrvl_amd import lib, synth
+
+    grid = (1, 72, 74)
+    seqs, firsts, poss, n_pre = [], [], [], []
+    for i in range(n_seq):
+        ids = np.concatenate([synth.prompt_ids(5, seed=100 + i), np.full(1332, IMAGE_TOKEN, np.int32),
+                              synth.prompt_ids(11, seed=200 + i)]).astype(np.int32)
+        img = synth.image_embeds(1332, cfg.hidden, seed=i)
+        s = model.seq(ids.size + n_new + 8)
+        first = s.generate(ids, 1, eos=(), image_embeds=img, image_token_id=IMAGE_TOKEN, grid=grid,
+                           use_prefill=True)
+        _, delta = lib.mm_positions(ids, IMAGE_TOKEN, grid)
+        seqs.append(s)
+        firsts.append(int(first[0]))
+        poss.append(ids.size + delta)
+        n_pre.append(ids.size)
+    dt = None
+    for _ in range(reps):
+        for s, n in zip(seqs, n_pre):
+            s.truncate(n)
+        t = time.perf_counter()
+        out = lib.decode_batch(seqs, firsts, poss, n_new, eos=())
+        dt = time.perf_counter() - t
+        assert all(len(o) == n_new for o in out)
+    return {"sequences": n_seq, "tokens_each": n_new, "context": f"{n_pre[0]}->{n_pre[0] + n_new}",
+            "tok_s": round(n_seq * n_new / dt, 1), "ms_per_step": round(dt / (n_new - 1) * 1e3, 4)}
+
+
 def build_model(ctx, cfg, qtype, seed=0):
     from rapidocrvl_amd import lib, synth
 
@@ -292,6 +325,7 @@ def main():
     ap.add_argument("--roofline-only", action="store_true", help="time only the Q4 LM-head GEMV rotation")
     ap.add_argument("--calibrate-copy", action="store_true", help="with --roofline-only: add a 512 MiB copy")
     ap.add_argument("--prefill-only", action="store_true", help="time only the 1345-token Q4 image prefill")
+    ap.add_argument("--no-batch", action="store_true", help="skip the 4-sequence batched decode")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the decoder step runs on a single MI355X "
@@ -354,6 +388,14 @@ def main():
     extra["prefill_ms"] = round(t_prefill * 1e3, 2)
     extra["prefill_tok_s"] = round(n_prefix / t_prefill, 1)
     extra["prefill_TFLOP_s"] = round(prefill_flops(cfg, n_prefix) / t_prefill / 1e12, 2)
+    if not args.no_batch:
+        extra["batch4_decode"] = {"q4": batch_decode(model, cfg)}
+        log(f"[bench] 4-sequence batched decode q4 {extra['batch4_decode']['q4']}")
+        _, m6 = build_model(ctx, cfg, lib.Q6)
+        extra["batch4_decode"]["q6"] = batch_decode(m6, cfg)
+        log(f"[bench] 4-sequence batched decode q6 {extra['batch4_decode']['q6']}")
+        del m6
+
     if not args.no_sweep:
         extra["gemv_sweep"] = gemv_sweep(ctx, np.random.default_rng(0))
         extra["attention_sweep"] = attention_sweep(ctx, cfg)

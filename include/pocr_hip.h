@@ -218,6 +218,17 @@ int pocr_prefill(pocr_seq *s, int n, const float *emb, const int32_t *pos3, floa
  * number of tokens written (>=0) or an error status (<0). */
 int pocr_decode_greedy(pocr_seq *s, int32_t first_token, int32_t first_pos, int max_new,
                        const int32_t *eos, int n_eos, int32_t *out_tokens);
+/* greedy decode of n_seq (1..4) sequences of one model together: the
+ * server's concurrent requests (cmd/paddleocrvl-server/main.go:1106, one
+ * decode loop each, model.go:1538-1568) batched into one device step — each
+ * layer's weights stream once for all of them (M = n_seq batched GEMV), each
+ * sequence keeps its own KV cache.  Sequence i starts from first_tokens[i] at
+ * first_positions[i]; its tokens go to out_tokens[i*max_new ...] (first token
+ * first), out_counts[i] of them, stopping after an EOS id.  Per-sequence
+ * results equal pocr_decode_greedy's up to f32 summation order. */
+int pocr_decode_batch(pocr_seq *const *seqs, int n_seq, const int32_t *first_tokens,
+                      const int32_t *first_positions, int max_new, const int32_t *eos, int n_eos,
+                      int32_t *out_tokens, int32_t *out_counts);
 /* whole greedy generation: GenerateWithOptions / generateWithImageEmbeds
  * (internal/model/model.go:1492-1572, 1618-1711) incl. multimodal positions
  * (1717-1783).  image rows replace ids equal to image_token_id in order.

@@ -145,7 +145,8 @@ void weight_retain(const pocr_weight *w);
 void weight_release(const pocr_weight *w);
 void model_release(pocr_model *m);
 DevMat dev_mat(const pocr_weight *w);
-int gemv_launch(hipStream_t s, GemvParams p, int nmat, int pro, int epi, int max_grid);
+int gemv_launch(hipStream_t s, GemvParams p, int nmat, int pro, int epi, int max_grid, int nv = 1,
+                const GemvNV *q = nullptr);
 GemvParams gemv_params_1(const pocr_weight *w);
 int step_locked(pocr_seq *s, const float *emb, const int32_t pos3[3], int need_logits, float *logits,
                 int32_t *token);

@@ -487,12 +487,12 @@ __device__ __forceinline__ void x_load(const float *x, const float *nw, bool nor
     }
 }
 
-// Digit planes of the thread's columns → LDS records; returns the RMSNorm
-// factor fastRsqrt(Σx²/n + eps) (1 without norm).  With the norm on, the
-// digits encode x·w and the row sums are scaled by the factor afterwards.
-// Ends with the workgroup's only barrier.
+// Digit planes of the thread's columns → LDS records, and the wave's Σx²
+// into red[wave] (with the norm on, the digits encode x·w and the row sums
+// are scaled by fastRsqrt(Σx²/n + eps) afterwards: x_norm_factor after the
+// workgroup barrier).
 template <int QT>
-__device__ __forceinline__ float x_digits(const XRegs &r, bool norm, int cols, float eps, int *lds, float *red) {
+__device__ __forceinline__ void x_digits(const XRegs &r, const XRegs &rw, bool norm, int cols, int *lds, float *red) {
     constexpr int NDW = DigitRec<QT>::NDW, RS = DigitRec<QT>::RS, TPC = DigitRec<QT>::TPC;
     const int lane = threadIdx.x & 63;
     float ss = 0.0f;
@@ -504,8 +504,8 @@ __device__ __forceinline__ float x_digits(const XRegs &r, bool norm, int cols, f
         float y[8] = {r.x[pp][0].x, r.x[pp][0].y, r.x[pp][0].z, r.x[pp][0].w,
                       r.x[pp][1].x, r.x[pp][1].y, r.x[pp][1].z, r.x[pp][1].w};
         if (norm) {
-            const float wv[8] = {r.w[pp][0].x, r.w[pp][0].y, r.w[pp][0].z, r.w[pp][0].w,
-                                 r.w[pp][1].x, r.w[pp][1].y, r.w[pp][1].z, r.w[pp][1].w};
+            const float wv[8] = {rw.w[pp][0].x, rw.w[pp][0].y, rw.w[pp][0].z, rw.w[pp][0].w,
+                                 rw.w[pp][1].x, rw.w[pp][1].y, rw.w[pp][1].z, rw.w[pp][1].w};
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 ss = valid ? fmaf(y[i], y[i], ss) : ss;
@@ -577,13 +577,6 @@ __device__ __forceinline__ float x_digits(const XRegs &r, bool norm, int cols, f
         ss = wave_sum(ss);
         if (lane == 0) red[threadIdx.x >> 6] = ss;
     }
-    __syncthreads();
-    if (!norm) return 1.0f;
-    float tot = red[0];
-#pragma unroll
-    for (int w = 1; w < kWaves; ++w) tot += red[w];
-    // RMSNorm (ops.go:1015-1037): x·fastRsqrt(Σx²/n + eps)·w
-    return fast_rsqrt_ref(tot / (float)cols + eps);
 }
 
 // Nibble-plane prologue (Q4 greedy head): thread t owns 4 consecutive
@@ -603,7 +596,8 @@ __device__ __forceinline__ void x_load_nib(const float *x, const float *nw, bool
 
 __device__ __forceinline__ int xchg_i(int v) { return __float_as_int(xchg<XQ1>(__int_as_float(v))); }
 
-__device__ __forceinline__ float x_digits_nib(const XRegs &r, bool norm, int cols, float eps, int *lds, float *red) {
+__device__ __forceinline__ void x_digits_nib(const XRegs &r, const XRegs &rw, bool norm, int cols, int *lds,
+                                             float *red) {
     constexpr int NDW = DigitRec<QT_Q4>::NDW, RS = DigitRec<QT_Q4>::RS;
     const int lane = threadIdx.x & 63;
     float ss = 0.0f;
@@ -615,7 +609,7 @@ __device__ __forceinline__ float x_digits_nib(const XRegs &r, bool norm, int col
         const float4 xv = r.x[pp >> 1][pp & 1];
         float y[4] = {xv.x, xv.y, xv.z, xv.w};
         if (norm) {
-            const float4 wv = r.w[pp >> 1][pp & 1];
+            const float4 wv = rw.w[pp >> 1][pp & 1];
             const float w[4] = {wv.x, wv.y, wv.z, wv.w};
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
@@ -658,12 +652,15 @@ __device__ __forceinline__ float x_digits_nib(const XRegs &r, bool norm, int col
         ss = wave_sum(ss);
         if (lane == 0) red[threadIdx.x >> 6] = ss;
     }
-    __syncthreads();
+}
+
+// RMSNorm (ops.go:1015-1037): x·fastRsqrt(Σx²/n + eps)·w — the factor from
+// the waves' Σx² (after the barrier that follows x_digits)
+__device__ __forceinline__ float x_norm_factor(bool norm, int cols, float eps, const float *red) {
     if (!norm) return 1.0f;
     float tot = red[0];
 #pragma unroll
     for (int w = 1; w < kWaves; ++w) tot += red[w];
-    // RMSNorm (ops.go:1015-1037): x·fastRsqrt(Σx²/n + eps)·w
     return fast_rsqrt_ref(tot / (float)cols + eps);
 }
 
@@ -746,6 +743,15 @@ struct GemvParams {
     int flag;       // EPI_OPROJ: in-place when st==null; EPI_DOWN: last layer
     int quirk;      // EPI_OPROJ: Q4/Q6 residual behaviour on
 };
+// NV > 1 activation vectors (a separate kernel argument, so single-vector
+// launches keep their argument block): vector v reads x + v·x_stride and
+// writes out/residual/vbuf + v·o_stride; its step state is stv[v−1] (v ≥ 1)
+struct GemvNV {
+    int x_stride;
+    int o_stride;
+    StepState *stv[3];
+};
+constexpr int kMaxNV = 4;
 
 __device__ __forceinline__ unsigned long long argmax_key(float v, int row) {
     uint32_t b = __float_as_uint(v);
@@ -792,27 +798,28 @@ __device__ __forceinline__ void stage_x(float *xs, const float *x, const float *
 }
 
 // resid = residual[r], read by the caller ahead of time (EPI_OPROJ/DOWN/ADDV)
-__device__ __forceinline__ void gemv_epilogue(const GemvParams &p, int epi, int r, const float *s, float resid,
+// row r of activation vector v (memory index o = v·o_stride + r)
+__device__ __forceinline__ void gemv_epilogue(const GemvParams &p, int epi, int r, int o, const float *s, float resid,
                                               bool in_place, float &best_v, int &best_r) {
 #pragma clang fp contract(off)
     switch (epi) {
-    case EPI_PLAIN: p.out[r] = s[0]; break;
-    case EPI_SWIGLU: p.out[r] = silu_ref(s[0]) * s[1]; break;
+    case EPI_PLAIN: p.out[o] = s[0]; break;
+    case EPI_SWIGLU: p.out[o] = silu_ref(s[0]) * s[1]; break;
     case EPI_OPROJ: {
         const float v = resid + s[0];
-        p.vbuf[r] = v;
-        if (in_place) p.residual[r] = v;
+        p.vbuf[o] = v;
+        if (in_place) p.residual[o] = v;
         break;
     }
     case EPI_DOWN: {
         const float v = resid + s[0];
-        if (p.flag) p.vbuf[r] = v;
-        else p.residual[r] = v;
+        if (p.flag) p.vbuf[o] = v;
+        else p.residual[o] = v;
         break;
     }
-    case EPI_ADDV: p.vbuf[r] = resid + s[0]; break;
+    case EPI_ADDV: p.vbuf[o] = resid + s[0]; break;
     default:  // EPI_ARGMAX
-        if (p.out) p.out[r] = s[0];
+        if (p.out) p.out[o] = s[0];
         if (s[0] > best_v || (s[0] == best_v && r < best_r)) {
             best_v = s[0];
             best_r = r;
@@ -824,11 +831,15 @@ __device__ __forceinline__ bool epi_reads_residual(int epi) {
     return epi == EPI_OPROJ || epi == EPI_DOWN || epi == EPI_ADDV;
 }
 
-__device__ __forceinline__ bool oproj_in_place(const GemvParams &p) {
-    if (!p.st) return p.flag != 0;
+__device__ __forceinline__ StepState *st_of(const GemvParams &p, const GemvNV &q, int v) {
+    return v == 0 ? p.st : (v == 1 ? q.stv[0] : (v == 2 ? q.stv[1] : q.stv[2]));
+}
+
+__device__ __forceinline__ bool oproj_in_place(const GemvParams &p, const StepState *st) {
+    if (!st) return p.flag != 0;
     // model.go:3895-3902 (first token) and 4051-4057 (len > 6): Q4/Q6 use the
     // OutOnly variant; positions 1..5 go through matVecOutAddRMSNormCPU (in place).
-    const int clen = p.st->clen;
+    const int clen = st->clen;
     return !(p.quirk && (clen == 0 || clen >= 6));
 }
 
@@ -861,7 +872,7 @@ __device__ __forceinline__ int wave_min_i32(int v) {
 // Greedy argmax of the workgroup's rows into its slot: the largest score
 // (compared as order-preserving bits, like the 64-bit key), then the lowest
 // row holding it (argmax_quant.go:255-262: ties keep the first index).
-__device__ __forceinline__ void argmax_finish(const GemvParams &p, float best_v, int best_r, float *red) {
+__device__ __forceinline__ void argmax_finish(StepState *st, float best_v, int best_r, float *red) {
     const bool has = best_r != 0x7FFFFFFF;
     const uint32_t ob = wave_max_u32(has ? ordered_bits(best_v) : 0u);
     const int rmin = wave_min_i32(has && ordered_bits(best_v) == ob ? best_r : 0x7FFFFFFF);
@@ -875,7 +886,7 @@ __device__ __forceinline__ void argmax_finish(const GemvParams &p, float best_v,
     if (threadIdx.x == 0) {
         unsigned long long m = kred[0];
         for (int w = 1; w < kWaves; ++w) m = kred[w] > m ? kred[w] : m;
-        if (m) atomicMax(&p.st->argmax_slot[(blockIdx.x % kArgSlots) * kSlotPitch], m);
+        if (m) atomicMax(&st->argmax_slot[(blockIdx.x % kArgSlots) * kSlotPitch], m);
     }
 }
 
@@ -950,18 +961,23 @@ __device__ __forceinline__ void load_group(const SegSel &sel, int row_bytes, int
 // TAG only separates instances for profiling (TAG=1: the timing entry point).
 // ONE: the grid gives every wave at most one group (no row loop, no prefetch
 // registers), for the large single-matrix launch.
-// NPL: digit planes of the activation (3, or 2 for the LM head, whose result
-// feeds only the argmax: x to 2^-15 of each 32-column chunk's maximum)
-template <int QT, int LPR, int CPL, int U, int NMAT, int TAG, bool ONE, int NPL>
-__device__ __forceinline__ void gemv_body(GemvParams p, int pro, int epi) {
+// NPL: digit planes of the activation (3 byte planes, 2 for the Q8/Q6 greedy
+// head, kNibPlanes for the Q4 greedy head).
+// NV: activation vectors sharing each weight pass (batched decode, M = NV):
+// every chunk is dotted against each vector's digits (read from LDS per
+// group), and the reduce-scatter runs over U·NV entries e = u·NV + v.
+template <int QT, int LPR, int CPL, int U, int NMAT, int TAG, bool ONE, int NPL, int NV>
+__device__ __forceinline__ void gemv_body(GemvParams p, int pro, int epi, const GemvNV &q) {
     // No step-state check up front: a GEMV writes only step scratch (the
     // residual stream, q/k/v, gate) and never indexes by the step state, so a
     // failed step needs no guard here and the first loads wait for nothing.
     extern __shared__ int4 lds4[];
     int *lds = reinterpret_cast<int *>(lds4);
-    __shared__ float red[2 * kWaves];
+    __shared__ float red[2 * kWaves * NV];
     constexpr int RPW = 64 / LPR;
     constexpr int RG = RPW * U;
+    constexpr int E = U * NV;  // reduce-scatter entries
+    static_assert(E <= LPR && (E & (E - 1)) == 0, "entries: a power of two within the row's lanes");
     // Every kernel argument is made live here, so their scalar loads issue as
     // one batch: one kernel-argument round trip instead of one per branch.
     asm volatile("" ::"s"(p.m[0].data), "s"(p.m[0].scale), "s"(p.m[1].data), "s"(p.m[1].scale), "s"(p.m[2].data),
@@ -969,6 +985,7 @@ __device__ __forceinline__ void gemv_body(GemvParams p, int pro, int epi) {
     asm volatile("" ::"s"(p.x), "s"(p.norm_w), "s"(p.out), "s"(p.residual), "s"(p.vbuf), "s"(p.st));
     asm volatile("" ::"s"(p.seg_end[0]), "s"(p.seg_end[1]), "s"(p.rows), "s"(p.cols), "s"(p.m[0].row_bytes),
                  "s"(p.eps), "s"(p.flag), "s"(p.quirk), "s"(pro), "s"(epi));
+    if constexpr (NV > 1) asm volatile("" ::"s"(q.x_stride), "s"(q.o_stride), "s"(q.stv[0]), "s"(q.stv[1]), "s"(q.stv[2]));
 
     const int rows = p.rows;
     const int row_bytes = p.m[0].row_bytes;
@@ -979,17 +996,23 @@ __device__ __forceinline__ void gemv_body(GemvParams p, int pro, int epi) {
     const int ngroups = (rows + RG - 1) / RG;
     const int gstride = gridDim.x * kWaves;
     int g = blockIdx.x * kWaves + wave;
-    constexpr int SPAN = LPR / U;  // lanes per entry after the reduce-scatter
-    const int my_u = l / SPAN;
+    constexpr int SPAN = LPR / E;  // lanes per entry after the reduce-scatter
+    const int my_e = l / SPAN;
+    const int my_u = my_e / NV, my_v = my_e % NV;
     const bool writer = (l % SPAN) == 0;
     const bool need_resid = epi_reads_residual(epi);
+    const int my_o = NV > 1 ? my_v * q.o_stride : 0;  // the writer's vector in out/residual/vbuf
 
     // activations first, so that waiting for them does not wait for weights
     const int cols = p.cols;
     const bool norm = pro == PRO_RMSNORM;
-    XRegs xr;
-    if constexpr (NPL == kNibPlanes) x_load_nib(p.x, p.norm_w, norm, cols, xr);
-    else x_load(p.x, p.norm_w, norm, cols, xr);
+    XRegs xr[NV];
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+        const float *xv = p.x + (NV > 1 ? v * q.x_stride : 0);
+        if constexpr (NPL == kNibPlanes) x_load_nib(xv, p.norm_w, norm && v == 0, cols, xr[v]);
+        else x_load(xv, p.norm_w, norm && v == 0, cols, xr[v]);
+    }
     // first group: weights, then the writer lane's epilogue operands (row
     // scale, residual), all requested before the prologue's first wait
     Chunk w[U][NMAT][CPL];
@@ -1001,31 +1024,57 @@ __device__ __forceinline__ void gemv_body(GemvParams p, int pro, int epi) {
         const int rc = min((gc * U + my_u) * RPW + sub, rows - 1);
 #pragma unroll
         for (int mi = 0; mi < NMAT; ++mi) scl[mi] = (mi == 0 ? sel.scale0 : sel.scale1)[rc - sel.start];
-        resid = need_resid ? p.residual[rc] : 0.0f;
+        resid = need_resid ? p.residual[my_o + rc] : 0.0f;
     }
-    float xscale;
-    if constexpr (NPL == kNibPlanes) xscale = x_digits_nib(xr, norm, cols, p.eps, lds, red);
-    else xscale = x_digits<QT>(xr, norm, cols, p.eps, lds, red);
-    XDig<QT, CPL, NPL> xd;
-    load_digits<QT, LPR, CPL, NPL>(lds, l, xd);
-    const bool in_place = epi == EPI_OPROJ ? oproj_in_place(p) : false;
+    const int recs = QT == QT_Q4 ? (cols / 32) * DigitRec<QT>::RS : (cols / 16) * DigitRec<QT>::RS;
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+        // the norm weight was loaded once, with vector 0
+        if constexpr (NPL == kNibPlanes) x_digits_nib(xr[v], xr[0], norm, cols, lds + v * recs, red + v * kWaves);
+        else x_digits<QT>(xr[v], xr[0], norm, cols, lds + v * recs, red + v * kWaves);
+    }
+    __syncthreads();
+    float xscale = x_norm_factor(norm, cols, p.eps, red);
+#pragma unroll
+    for (int v = 1; v < NV; ++v) {
+        const float f = x_norm_factor(norm, cols, p.eps, red + v * kWaves);
+        xscale = my_v == v ? f : xscale;
+    }
+    XDig<QT, CPL, NPL> xd;  // NV = 1: the vector's digits stay in registers across groups
+    if constexpr (NV == 1) load_digits<QT, LPR, CPL, NPL>(lds, l, xd);
+    const bool in_place = epi == EPI_OPROJ ? oproj_in_place(p, st_of(p, q, my_v)) : false;
     float best_v = -INFINITY;
     int best_r = 0x7FFFFFFF;
 
     // one group: row sums, reduce-scatter, epilogue by the writer lanes
     auto compute = [&](int gg, const Chunk (&wc)[U][NMAT][CPL], const float (&sc)[NMAT], float rs) {
         const int r = (gg * U + my_u) * RPW + sub;
-        float acc[U > 8 ? U : 8][NMAT];
+        float acc[E > 8 ? E : 8][NMAT];
+        if constexpr (NV == 1) {
 #pragma unroll
-        for (int u = 0; u < U; ++u)
+            for (int u = 0; u < U; ++u)
 #pragma unroll
-            for (int mi = 0; mi < NMAT; ++mi) acc[u][mi] = row_dot<QT, CPL, NPL>(wc[u][mi], xd);
-        reduce_scatter<LPR, U, NMAT>(acc, lane);
+                for (int mi = 0; mi < NMAT; ++mi) acc[u][mi] = row_dot<QT, CPL, NPL>(wc[u][mi], xd);
+        } else {
+#pragma unroll
+            for (int v = 0; v < NV; ++v) {
+                XDig<QT, CPL, NPL> xv;
+                load_digits<QT, LPR, CPL, NPL>(lds + v * recs, l, xv);
+#pragma unroll
+                for (int u = 0; u < U; ++u)
+#pragma unroll
+                    for (int mi = 0; mi < NMAT; ++mi) acc[u * NV + v][mi] = row_dot<QT, CPL, NPL>(wc[u][mi], xv);
+                // one vector's digits live at a time: keep the next vector's
+                // LDS reads below this point
+                asm volatile("" ::: "memory");
+            }
+        }
+        reduce_scatter<LPR, E, NMAT>(acc, lane);
         if (writer && r < rows) {
             float sv[NMAT];
 #pragma unroll
             for (int mi = 0; mi < NMAT; ++mi) sv[mi] = acc[0][mi] * xscale * sc[mi];
-            gemv_epilogue(p, epi, r, sv, rs, in_place, best_v, best_r);
+            gemv_epilogue(p, epi, r, my_o + r, sv, rs, in_place, best_v, best_r);
         }
     };
     // Every group but a wave's last requests its successor's weights and
@@ -1042,7 +1091,7 @@ __device__ __forceinline__ void gemv_body(GemvParams p, int pro, int epi) {
             const int rn = min((gn * U + my_u) * RPW + sub, rows - 1);
 #pragma unroll
             for (int mi = 0; mi < NMAT; ++mi) scln[mi] = (mi == 0 ? seln.scale0 : seln.scale1)[rn - seln.start];
-            residn = need_resid ? p.residual[rn] : 0.0f;
+            residn = need_resid ? p.residual[my_o + rn] : 0.0f;
         }
         compute(g, w, scl, resid);
 #pragma unroll
@@ -1056,18 +1105,28 @@ __device__ __forceinline__ void gemv_body(GemvParams p, int pro, int epi) {
         resid = residn;
     }
     if (g < ngroups) compute(g, w, scl, resid);
-    if (epi == EPI_ARGMAX) argmax_finish(p, best_v, best_r, red);
+    if (epi == EPI_ARGMAX) {
+#pragma unroll
+        for (int v = 0; v < NV; ++v)
+            argmax_finish(st_of(p, q, v), my_v == v ? best_v : -INFINITY, my_v == v ? best_r : 0x7FFFFFFF, red);
+    }
 }
 
 template <int QT, int LPR, int CPL, int U, int NMAT, int TAG = 0, int NPL = 3>
 __global__ void __launch_bounds__(kThreads) k_gemv(GemvParams p, int pro, int epi) {
-    gemv_body<QT, LPR, CPL, U, NMAT, TAG, false, NPL>(p, pro, epi);
+    gemv_body<QT, LPR, CPL, U, NMAT, TAG, false, NPL, 1>(p, pro, epi, GemvNV{});
 }
 
 // One row group per wave (no row loop, no prefetch registers).
 template <int QT, int LPR, int CPL, int U, int NMAT, int TAG = 0, int NPL = 3>
 __global__ void __launch_bounds__(kThreads) k_gemv_one(GemvParams p, int pro, int epi) {
-    gemv_body<QT, LPR, CPL, U, NMAT, TAG, true, NPL>(p, pro, epi);
+    gemv_body<QT, LPR, CPL, U, NMAT, TAG, true, NPL, 1>(p, pro, epi, GemvNV{});
+}
+
+// NV activation vectors per weight pass (batched decode, M = NV)
+template <int QT, int LPR, int CPL, int U, int NMAT, int NPL, int NV, bool ONE>
+__global__ void __launch_bounds__(kThreads) k_gemv_nv(GemvParams p, int pro, int epi, GemvNV q) {
+    gemv_body<QT, LPR, CPL, U, NMAT, 0, ONE, NPL, NV>(p, pro, epi, q);
 }
 
 // Any shape (tiny test matrices, odd column counts): one wavefront per row,
@@ -1093,7 +1152,7 @@ __global__ void __launch_bounds__(kThreads) k_gemv_any(GemvParams p, int pro, in
     else stage_x<PRO_COPY>(xs, p.x, p.norm_w, p.cols, p.eps, red);
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const bool in_place = epi == EPI_OPROJ ? oproj_in_place(p) : false;
+    const bool in_place = epi == EPI_OPROJ ? oproj_in_place(p, p.st) : false;
     float best_v = -INFINITY;
     int best_r = 0x7FFFFFFF;
     const int nw = gridDim.x * kWaves;
@@ -1122,9 +1181,9 @@ __global__ void __launch_bounds__(kThreads) k_gemv_any(GemvParams p, int pro, in
             }
         }
         if (lane == 0 && valid)
-            gemv_epilogue(p, epi, r, s, epi_reads_residual(epi) ? p.residual[r] : 0.0f, in_place, best_v, best_r);
+            gemv_epilogue(p, epi, r, r, s, epi_reads_residual(epi) ? p.residual[r] : 0.0f, in_place, best_v, best_r);
     }
-    if (epi == EPI_ARGMAX) argmax_finish(p, best_v, best_r, red);
+    if (epi == EPI_ARGMAX) argmax_finish(p.st, best_v, best_r, red);
 }
 
 // ---------------------------------------------------------------------------
@@ -1170,9 +1229,9 @@ static __global__ void __launch_bounds__(kThreads) k_rope(float *q, float *k, co
 // mode 0: h and pos were written by the host.  mode 1: greedy decode — the
 // token is the previous step's argmax, its embedding row is copied into h and
 // the position is next_pos (decode position len(out)-1+ropeDelta, model.go:1695).
-static __global__ void __launch_bounds__(kThreads) k_step_begin(StepState *st, const float *embed, float *h, int hidden,
-                                                           int vocab, const double *freq, const uint8_t *axis,
-                                                           int mode, int32_t *tokens, int max_tokens) {
+__device__ __forceinline__ void step_begin_body(StepState *st, const float *embed, float *h, int hidden, int vocab,
+                                                const double *freq, const uint8_t *axis, int mode, int32_t *tokens,
+                                                int max_tokens) {
     __shared__ int s_tok, s_err, s_pos[3];
     __shared__ unsigned long long s_key;
     if (threadIdx.x < 64) {  // wave 0: max over the argmax slots
@@ -1230,6 +1289,29 @@ static __global__ void __launch_bounds__(kThreads) k_step_begin(StepState *st, c
         const float *src = embed + (size_t)s_tok * hidden;
         for (int i = threadIdx.x; i < hidden; i += kThreads) h[i] = src[i];
     }
+}
+
+static __global__ void __launch_bounds__(kThreads) k_step_begin(StepState *st, const float *embed, float *h, int hidden,
+                                                           int vocab, const double *freq, const uint8_t *axis,
+                                                           int mode, int32_t *tokens, int max_tokens) {
+    step_begin_body(st, embed, h, hidden, vocab, freq, axis, mode, tokens, max_tokens);
+}
+
+// Greedy decode of several sequences in one step: workgroup b runs sequence
+// b's prologue (mode 1) and writes its embedding row to h + b·hidden.
+struct StepBatch {
+    StepState *st[kMaxNV];
+    int32_t *tokens[kMaxNV];
+    int max_tokens[kMaxNV];
+};
+static __global__ void __launch_bounds__(kThreads) k_step_begin_multi(StepBatch b, const float *embed, float *h,
+                                                                 int hidden, int vocab, const double *freq,
+                                                                 const uint8_t *axis) {
+    const int i = blockIdx.x;
+    StepState *st = i == 0 ? b.st[0] : (i == 1 ? b.st[1] : (i == 2 ? b.st[2] : b.st[3]));
+    int32_t *tok = i == 0 ? b.tokens[0] : (i == 1 ? b.tokens[1] : (i == 2 ? b.tokens[2] : b.tokens[3]));
+    const int mt = i == 0 ? b.max_tokens[0] : (i == 1 ? b.max_tokens[1] : (i == 2 ? b.max_tokens[2] : b.max_tokens[3]));
+    step_begin_body(st, embed, h + (size_t)i * hidden, hidden, vocab, freq, axis, 1, tok, mt);
 }
 
 // ---------------------------------------------------------------------------
@@ -1323,9 +1405,7 @@ __device__ __forceinline__ void pin_args(AttnParams &p) {
     asm volatile("" ::"s"(p.len), "s"(p.has_rope));
 }
 
-static __global__ void __launch_bounds__(kThreads) k_attn_decode(AttnParams args) {
-    AttnParams p = args;
-    pin_args(p);
+__device__ __forceinline__ void attn_decode_body(AttnParams p) {
     StepState *st = p.st;
     __shared__ float4 e_lds[kWaves][kMaxGroup][4];      // wave-private probabilities [head][16 rows]
     __shared__ float w_m[kWaves][kMaxGroup], w_l[kWaves][kMaxGroup];
@@ -1552,9 +1632,7 @@ static __global__ void __launch_bounds__(kThreads) k_attn_decode(AttnParams args
 // at or past the step's length hold stale records and are skipped.
 constexpr int kMaxSplits = 1024;  // cache capacity ≤ 65536 rows
 
-static __global__ void __launch_bounds__(kHD) k_attn_merge(AttnParams args) {
-    AttnParams p = args;
-    pin_args(p);
+__device__ __forceinline__ void attn_merge_body(AttnParams p) {
     __shared__ float e_lds[kMaxSplits];
     __shared__ float l_lds;
     const int hq = blockIdx.x;  // q head
@@ -1604,6 +1682,34 @@ static __global__ void __launch_bounds__(kHD) k_attn_merge(AttnParams args) {
     for (int s = B; s < used; ++s) o = fmaf(e_lds[s], rec(s)[2 + d], o);
     p.head_out[(size_t)hq * kHD + d] = o * (1.0f / l_lds);
 }
+
+static __global__ void __launch_bounds__(kThreads) k_attn_decode(AttnParams args) {
+    AttnParams p = args;
+    pin_args(p);
+    attn_decode_body(p);
+}
+static __global__ void __launch_bounds__(kHD) k_attn_merge(AttnParams args) {
+    AttnParams p = args;
+    pin_args(p);
+    attn_merge_body(p);
+}
+
+// Several sequences in one launch (batched decode): blockIdx.z picks the
+// sequence's parameters (its cache, step state, partials, q and output rows);
+// splits past a sequence's own count exit at once.
+struct AttnMulti {
+    AttnParams a[kMaxNV];
+};
+__device__ __forceinline__ AttnParams attn_pick(const AttnMulti &b) {
+    const int i = blockIdx.z;
+    return i == 0 ? b.a[0] : (i == 1 ? b.a[1] : (i == 2 ? b.a[2] : b.a[3]));
+}
+static __global__ void __launch_bounds__(kThreads) k_attn_decode_multi(AttnMulti b) {
+    const AttnParams p = attn_pick(b);
+    if ((int)blockIdx.y >= p.nsplit) return;  // uniform
+    attn_decode_body(p);
+}
+static __global__ void __launch_bounds__(kHD) k_attn_merge_multi(AttnMulti b) { attn_merge_body(attn_pick(b)); }
 
 // Attention for head dims other than 128 (small test shapes): one workgroup
 // per q head, serial over rows, same math.

@@ -211,17 +211,18 @@ DevMat pocr::dev_mat(const pocr_weight *w) {
 // ---------------------------------------------------------------------------
 // GEMV dispatch
 // ---------------------------------------------------------------------------
-template <int QT, int L, int C, int U, int NMAT, int TAG, bool ONE, int NPL>
+template <int QT, int L, int C, int U, int NMAT, int TAG, bool ONE, int NPL, int NV>
 static const void *gemv_fn() {
-    if constexpr (ONE) return reinterpret_cast<const void *>(&k_gemv_one<QT, L, C, U, NMAT, TAG, NPL>);
+    if constexpr (NV > 1) return reinterpret_cast<const void *>(&k_gemv_nv<QT, L, C, U, NMAT, NPL, NV, ONE>);
+    else if constexpr (ONE) return reinterpret_cast<const void *>(&k_gemv_one<QT, L, C, U, NMAT, TAG, NPL>);
     else return reinterpret_cast<const void *>(&k_gemv<QT, L, C, U, NMAT, TAG, NPL>);
 }
 
-template <int QT, int NMAT, int U, int TAG = 0, bool ONE = false, int NPL = 3>
+template <int QT, int NMAT, int U, int TAG = 0, bool ONE = false, int NPL = 3, int NV = 1>
 static bool gemv_fast_kernel(int lpr, int cpl, const void **fn) {
 #define POCR_K(L, C)                                            \
     if (lpr == L && cpl == C) {                                 \
-        *fn = gemv_fn<QT, L, C, U, NMAT, TAG, ONE, NPL>();      \
+        *fn = gemv_fn<QT, L, C, U, NMAT, TAG, ONE, NPL, NV>();  \
         return true;                                            \
     }
     if constexpr (U > 2) {  // the large single-matrix shape: one chunk per lane
@@ -266,8 +267,21 @@ static bool pick_big(int tag, bool one, int lpr, int cpl, const void **fn) {
                     : gemv_fast_kernel<QT, 1, kBigU, 0, false, NPL>(lpr, cpl, fn);
 }
 
+// NV activation vectors per weight pass (batched decode): the big launch keeps
+// U·NV = kBigU entries and always gives every wave one group
+template <int QT, int NV>
+static bool pick_nv(int nmat, bool big, int lpr, int cpl, bool argmax, const void **fn) {
+    if (nmat == 2) return gemv_fast_kernel<QT, 2, 2, 0, false, 3, NV>(lpr, cpl, fn);
+    if (big)
+        return argmax ? gemv_fast_kernel<QT, 1, kBigU / NV, 0, true, big_planes<QT>(), NV>(lpr, cpl, fn)
+                      : gemv_fast_kernel<QT, 1, kBigU / NV, 0, true, 3, NV>(lpr, cpl, fn);
+    return gemv_fast_kernel<QT, 1, 2, 0, false, 3, NV>(lpr, cpl, fn);
+}
+
 template <int QT>
-static bool pick_fast(int nmat, int u, int tag, int lpr, int cpl, bool one, bool argmax, const void **fn) {
+static bool pick_fast(int nmat, int u, int tag, int lpr, int cpl, bool one, bool argmax, int nv, const void **fn) {
+    if (nv == 2) return pick_nv<QT, 2>(nmat, u != 2, lpr, cpl, argmax, fn);
+    if (nv == 4) return pick_nv<QT, 4>(nmat, u != 2, lpr, cpl, argmax, fn);
     if (nmat == 2) return gemv_fast_kernel<QT, 2, 2>(lpr, cpl, fn);
     if (u == kBigU)
         return argmax ? pick_big<QT, big_planes<QT>()>(tag, one, lpr, cpl, fn) : pick_big<QT, 3>(tag, one, lpr, cpl, fn);
@@ -278,12 +292,14 @@ struct GemvPlan {
     const void *fn = nullptr;
     int grid = 1;
     size_t lds = 0;
+    int nv = 1;  // > 1: the kernel takes a GemvNV argument
 };
 
 // Choose the kernel for `rows` outputs of matrices with `cols` columns.
 // max_grid caps the workgroup count (rows loop inside the kernel).
 static int plan_gemv(int qtype, int nmat, int rows, int cols, const DevMat *mats, int nm, int max_grid,
-                     GemvPlan *plan, int tag, const int *seg_end, int epi) {
+                     GemvPlan *plan, int tag, const int *seg_end, int epi, int nv = 1) {
+    if (nv != 1 && nv != 2 && nv != 4) return fail(POCR_ERR_UNSUPPORTED, "gemv: %d vectors per pass", nv);
     if (cols > 16384) return fail(POCR_ERR_UNSUPPORTED, "gemv: cols %d > 16384", cols);
     plan->lds = (size_t)cols * 4;
     int W = qtype == POCR_Q4 ? 32 : 16;
@@ -308,8 +324,8 @@ static int plan_gemv(int qtype, int nmat, int rows, int cols, const DevMat *mats
     bool ok = false;
     // big row counts: 8 rows per lane group and step (more bytes in flight)
     const bool big = fast && nmat == 1 && cpl == 1 && rows >= 8192;
-    const int u = big ? kBigU : 2;
-    if (big) max_grid = std::max(max_grid, POCR_BIG_GRID);
+    const int u = big ? kBigU / nv : 2;
+    if (big) max_grid = nv > 1 ? 1 << 30 : std::max(max_grid, POCR_BIG_GRID);
     // row groups must not straddle segments
     if (fast && nmat == 1 && seg_end) {
         const int rg = (64 / lpr) * u;
@@ -324,14 +340,19 @@ static int plan_gemv(int qtype, int nmat, int rows, int cols, const DevMat *mats
         const int want = (groups + kWaves - 1) / kWaves;
         grid = std::max(1, std::min(want, max_grid));
         one = big && grid == want;
-        if (qtype == POCR_Q4) ok = pick_fast<QT_Q4>(nmat, u, tag, lpr, cpl, one, epi == EPI_ARGMAX, &plan->fn);
-        if (qtype == POCR_Q8) ok = pick_fast<QT_Q8>(nmat, u, tag, lpr, cpl, one, epi == EPI_ARGMAX, &plan->fn);
-        if (qtype == POCR_Q6) ok = pick_fast<QT_Q6>(nmat, u, tag, lpr, cpl, one, epi == EPI_ARGMAX, &plan->fn);
+        const bool am = epi == EPI_ARGMAX;
+        if (qtype == POCR_Q4) ok = pick_fast<QT_Q4>(nmat, big ? kBigU : 2, tag, lpr, cpl, one, am, nv, &plan->fn);
+        if (qtype == POCR_Q8) ok = pick_fast<QT_Q8>(nmat, big ? kBigU : 2, tag, lpr, cpl, one, am, nv, &plan->fn);
+        if (qtype == POCR_Q6) ok = pick_fast<QT_Q6>(nmat, big ? kBigU : 2, tag, lpr, cpl, one, am, nv, &plan->fn);
     }
     if (ok) {
-        plan->lds = qtype == POCR_Q4 ? gemv_lds_bytes<QT_Q4>(cols)
-                                     : (qtype == POCR_Q8 ? gemv_lds_bytes<QT_Q8>(cols) : gemv_lds_bytes<QT_Q6>(cols));
+        plan->lds = (size_t)nv * (qtype == POCR_Q4 ? gemv_lds_bytes<QT_Q4>(cols)
+                                                   : (qtype == POCR_Q8 ? gemv_lds_bytes<QT_Q8>(cols)
+                                                                       : gemv_lds_bytes<QT_Q6>(cols)));
         plan->grid = grid;
+        plan->nv = nv;
+    } else if (nv > 1) {
+        return fail(POCR_ERR_UNSUPPORTED, "gemv: %d vectors need the fast kernel shapes", nv);
     } else {
         plan->fn = nmat == 1 ? reinterpret_cast<const void *>(&k_gemv_any<1>)
                              : reinterpret_cast<const void *>(&k_gemv_any<2>);
@@ -340,8 +361,9 @@ static int plan_gemv(int qtype, int nmat, int rows, int cols, const DevMat *mats
     return POCR_OK;
 }
 
-static int launch_gemv(hipStream_t s, const GemvPlan &plan, GemvParams p, int pro, int epi) {
-    void *args[] = {&p, &pro, &epi};
+static int launch_gemv(hipStream_t s, const GemvPlan &plan, GemvParams p, int pro, int epi, GemvNV q = {}) {
+    void *args[] = {&p, &pro, &epi, &q};
+    if (plan.nv == 1) args[3] = nullptr;
     HIP_TRY(hipLaunchKernel(plan.fn, dim3(plan.grid), dim3(kThreads), args, plan.lds, s));
     return POCR_OK;
 }
@@ -355,12 +377,14 @@ GemvParams pocr::gemv_params_1(const pocr_weight *w) {
     return p;
 }
 
-int pocr::gemv_launch(hipStream_t s, GemvParams p, int nmat, int pro, int epi, int max_grid) {
+int pocr::gemv_launch(hipStream_t s, GemvParams p, int nmat, int pro, int epi, int max_grid, int nv,
+                      const GemvNV *q) {
     GemvPlan plan;
     const int nm = nmat == 2 ? 2 : (p.seg_end[0] == p.rows ? 1 : (p.seg_end[1] == p.rows ? 2 : 3));
-    int rc = plan_gemv(p.m[0].qtype, nmat, p.rows, p.cols, p.m, nm, max_grid, &plan, 0, p.seg_end, epi);
+    int rc = plan_gemv(p.m[0].qtype, nmat, p.rows, p.cols, p.m, nm, max_grid, &plan, 0, p.seg_end, epi, nv);
     if (rc) return rc;
-    return launch_gemv(s, plan, p, pro, epi);
+    if (nv > 1 && !q) return fail(POCR_ERR_ARG, "gemv: %d vectors need their strides", nv);
+    return launch_gemv(s, plan, p, pro, epi, nv > 1 ? *q : GemvNV{});
 }
 
 
@@ -383,6 +407,30 @@ static int sync(hipStream_t s) {
     HIP_TRY(hipStreamSynchronize(s));
     return POCR_OK;
 }
+// M rows of activations (device, row-major) against one weight: M ≤ 4 share
+// each weight pass in the GEMV (2 or 4 vectors per launch), larger M take the
+// digit-plane MFMA GEMM; shapes the vector kernel does not take fall back too.
+static int matvec_rows(pocr_ctx *ctx, const pocr_weight *w, const float *x, int m, float *out) {
+    hipStream_t s = ctx->stream;
+    if (m <= 4) {
+        for (int r0 = 0; r0 < m;) {
+            const int nv = m - r0 >= 4 ? 4 : (m - r0 >= 2 ? 2 : 1);
+            GemvParams p = gemv_params_1(w);
+            p.x = x + (size_t)r0 * w->cols;
+            p.out = out + (size_t)r0 * w->rows;
+            GemvNV q{};
+            q.x_stride = w->cols;
+            q.o_stride = w->rows;
+            const int rc = gemv_launch(s, p, 1, PRO_COPY, EPI_PLAIN, kBigGrid, nv, &q);
+            if (rc == POCR_ERR_UNSUPPORTED && nv > 1) return batched_gemv(ctx, dev_mat(w), x, m, out);
+            RC(rc);
+            r0 += nv;
+        }
+        return POCR_OK;
+    }
+    return batched_gemv(ctx, dev_mat(w), x, m, out);
+}
+
 extern "C" int pocr_matvec(pocr_ctx *ctx, const pocr_weight *w, const float *x, int m, float *out) {
     if (!ctx || !w || !x || !out || m <= 0) return fail(POCR_ERR_ARG, "pocr_matvec: bad arguments");
     if (w->ctx != ctx) return fail(POCR_ERR_ARG, "pocr_matvec: weight from another context");
@@ -392,14 +440,7 @@ extern "C" int pocr_matvec(pocr_ctx *ctx, const pocr_weight *w, const float *x, 
     RC(ctx->x.ensure((size_t)m * w->cols * 4));
     RC(ctx->out.ensure((size_t)m * w->rows * 4));
     RC(h2d(s, ctx->x.p, x, (size_t)m * w->cols * 4));
-    if (m > 1) {
-        RC(batched_gemv(ctx, dev_mat(w), ctx->x.as<float>(), m, ctx->out.as<float>()));
-    } else {
-        GemvParams p = gemv_params_1(w);
-        p.x = ctx->x.as<float>();
-        p.out = ctx->out.as<float>();
-        RC(gemv_launch(s, p, 1, PRO_COPY, EPI_PLAIN, kBigGrid));
-    }
+    RC(matvec_rows(ctx, w, ctx->x.as<float>(), m, ctx->out.as<float>()));
     RC(d2h(s, out, ctx->out.p, (size_t)m * w->rows * 4));
     return sync(s);
 }
@@ -1339,6 +1380,252 @@ extern "C" int pocr_decode_greedy(pocr_seq *s, int32_t first_token, int32_t firs
     std::lock_guard<std::mutex> lk(s->m->ctx->mu);
     HIP_TRY(hipSetDevice(s->m->ctx->device));
     return decode_locked(s, first_token, first_pos, max_new, eos, n_eos, out_tokens);
+}
+
+// ---------------------------------------------------------------------------
+// Batched greedy decode: up to kMaxNV sequences of one model advance together.
+// Every layer GEMV streams its weights once for all of them (NV activation
+// vectors per pass, padded to 2 or 4), attention and its merge run in one
+// launch each with the sequence in blockIdx.z, and each sequence keeps its own
+// KV cache, step state and token buffer.  One step is captured into a HIP
+// graph and replayed; the host reads the states back every 16 steps.
+// ---------------------------------------------------------------------------
+namespace {
+
+struct DecodeBatch {
+    pocr_model *m = nullptr;
+    int n = 0;    // sequences
+    int nv = 1;   // vectors per GEMV pass (n padded to 1, 2 or 4)
+    pocr_seq *seq[kMaxNV] = {};
+    float *h = nullptr, *v = nullptr, *qkv = nullptr, *ho = nullptr, *g = nullptr;
+    StepState *pad = nullptr;  // step state of the padding vectors
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    ~DecodeBatch() {
+        if (exec) (void)hipGraphExecDestroy(exec);
+        if (graph) (void)hipGraphDestroy(graph);
+        for (void *p : {(void *)h, (void *)v, (void *)qkv, (void *)ho, (void *)g, (void *)pad})
+            if (p) (void)hipFree(p);
+    }
+    StepState *st(int i) const { return i < n ? seq[i]->st : pad; }
+};
+
+GemvNV batch_nv(const DecodeBatch &b, int x_stride, int o_stride) {
+    GemvNV q{};
+    q.x_stride = x_stride;
+    q.o_stride = o_stride;
+    for (int i = 1; i < kMaxNV; ++i) q.stv[i - 1] = b.st(i);
+    return q;
+}
+
+int enqueue_batch_step(DecodeBatch &b) {
+    pocr_model *m = b.m;
+    const pocr_config &c = m->cfg;
+    hipStream_t st = m->ctx->stream;
+    const int H = c.hidden, Q = c.heads * c.head_dim, KV = c.kv_heads * c.head_dim, F = c.intermediate;
+    const int QKV = Q + 2 * KV;
+    const float eps = c.rms_norm_eps;
+    StepBatch sb{};
+    for (int i = 0; i < b.n; ++i) {
+        sb.st[i] = b.seq[i]->st;
+        sb.tokens[i] = b.seq[i]->tokens;
+        sb.max_tokens[i] = b.seq[i]->max_tokens;
+    }
+    hipLaunchKernelGGL(k_step_begin_multi, dim3(b.n), dim3(kThreads), 0, st, sb, m->embed, b.h, H, c.vocab, m->freq,
+                       m->axis);
+    HIP_TRY(hipGetLastError());
+    int max_split = 1;
+    for (int i = 0; i < b.n; ++i) max_split = std::max(max_split, b.seq[i]->nsplit);
+    for (int li = 0; li < c.layers; ++li) {
+        const LayerW &L = m->layers[li];
+        const bool last = li + 1 == c.layers;
+        // 1. RMSNorm(h)·ln1 → q|k|v for every sequence
+        GemvParams p{};
+        p.m[0] = dev_mat(L.w[POCR_W_Q]);
+        p.m[1] = dev_mat(L.w[POCR_W_K]);
+        p.m[2] = dev_mat(L.w[POCR_W_V]);
+        p.seg_end[0] = Q;
+        p.seg_end[1] = Q + KV;
+        p.seg_end[2] = QKV;
+        p.rows = QKV;
+        p.cols = H;
+        p.x = b.h;
+        p.norm_w = L.ln1;
+        p.eps = eps;
+        p.out = b.qkv;
+        p.st = b.st(0);
+        GemvNV q = batch_nv(b, H, QKV);
+        RC(gemv_launch(st, p, 1, PRO_RMSNORM, EPI_PLAIN, kBigGrid, b.nv, &q));
+        // 2. per sequence: RoPE + KV append + split attention, then the merge
+        AttnMulti am{};
+        for (int i = 0; i < b.n; ++i) {
+            pocr_seq *s = b.seq[i];
+            AttnParams &a = am.a[i];
+            a.q = b.qkv + (size_t)i * QKV;
+            a.k_new = a.q + Q;
+            a.v_new = a.q + Q + KV;
+            a.kc = layer_k(s, li);
+            a.vc = layer_v(s, li);
+            a.st = s->st;
+            a.part = s->part;
+            a.head_out = b.ho + (size_t)i * Q;
+            a.heads = c.heads;
+            a.kvh = c.kv_heads;
+            a.nsplit = s->nsplit;
+            a.rows_cap = s->cap;
+            a.scale = (float)(1.0 / std::sqrt((double)c.head_dim));
+        }
+        hipLaunchKernelGGL(k_attn_decode_multi, dim3(c.kv_heads, max_split, b.n), dim3(kThreads), 0, st, am);
+        hipLaunchKernelGGL(k_attn_merge_multi, dim3(c.heads, 1, b.n), dim3(kHD), 0, st, am);
+        HIP_TRY(hipGetLastError());
+        // 3. o_proj + residual (+ the Q4/Q6 behaviour per sequence)
+        const pocr_weight *wo = L.w[POCR_W_O];
+        GemvParams o = gemv_params_1(wo);
+        o.x = b.ho;
+        o.residual = b.h;
+        o.vbuf = b.v;
+        o.st = b.st(0);
+        o.quirk = (m->quirk && (wo->qtype == POCR_Q4 || wo->qtype == POCR_Q6)) ? 1 : 0;
+        q = batch_nv(b, Q, H);
+        RC(gemv_launch(st, o, 1, PRO_COPY, EPI_OPROJ, kBigGrid, b.nv, &q));
+        // 4. RMSNorm(v)·ln2 → gate/up → SiLU(g)·u
+        GemvParams gu = gemv_params_1(L.w[POCR_W_GATE]);
+        gu.m[1] = dev_mat(L.w[POCR_W_UP]);
+        gu.x = b.v;
+        gu.norm_w = L.ln2;
+        gu.eps = eps;
+        gu.out = b.g;
+        gu.st = b.st(0);
+        q = batch_nv(b, H, F);
+        RC(gemv_launch(st, gu, 2, PRO_RMSNORM, EPI_SWIGLU, kBigGrid, b.nv, &q));
+        // 5. down + residual; last layer: v = h + down
+        GemvParams d = gemv_params_1(L.w[POCR_W_DOWN]);
+        d.x = b.g;
+        d.residual = b.h;
+        d.vbuf = b.v;
+        d.st = b.st(0);
+        d.flag = last ? 1 : 0;
+        q = batch_nv(b, F, H);
+        RC(gemv_launch(st, d, 1, PRO_COPY, EPI_DOWN, kBigGrid, b.nv, &q));
+    }
+    // LM head on RMSNorm(v)·final_norm, argmax into each sequence's state
+    GemvParams lm = gemv_params_1(m->lm);
+    lm.x = b.v;
+    lm.norm_w = m->final_norm;
+    lm.eps = eps;
+    lm.st = b.st(0);
+    GemvNV q = batch_nv(b, H, 0);
+    return gemv_launch(st, lm, 1, PRO_RMSNORM, EPI_ARGMAX, kBigGrid, b.nv, &q);
+}
+
+int batch_alloc(DecodeBatch &b) {
+    const pocr_config &c = b.m->cfg;
+    const size_t H = c.hidden, Q = (size_t)c.heads * c.head_dim, KV = (size_t)c.kv_heads * c.head_dim;
+    const size_t nv = b.nv;
+    for (auto pr : {std::make_pair(&b.h, H), std::make_pair(&b.v, H), std::make_pair(&b.qkv, Q + 2 * KV),
+                    std::make_pair(&b.ho, Q), std::make_pair(&b.g, (size_t)c.intermediate)}) {
+        HIP_TRY(hipMalloc(pr.first, nv * pr.second * 4));
+        // padding rows stay finite zeros (their results are never read)
+        HIP_TRY(hipMemsetAsync(*pr.first, 0, nv * pr.second * 4, b.m->ctx->stream));
+    }
+    HIP_TRY(hipMalloc(&b.pad, sizeof(StepState)));
+    HIP_TRY(hipMemsetAsync(b.pad, 0, sizeof(StepState), b.m->ctx->stream));
+    return POCR_OK;
+}
+
+}  // namespace
+
+extern "C" int pocr_decode_batch(pocr_seq *const *seqs, int n_seq, const int32_t *first_tokens,
+                                 const int32_t *first_positions, int max_new, const int32_t *eos, int n_eos,
+                                 int32_t *out_tokens, int32_t *out_counts) {
+    if (!seqs || n_seq <= 0 || n_seq > kMaxNV || !first_tokens || !first_positions || !out_tokens || !out_counts ||
+        (n_eos > 0 && !eos))
+        return fail(POCR_ERR_ARG, "pocr_decode_batch: bad arguments (1..%d sequences)", kMaxNV);
+    pocr_model *m = seqs[0] ? seqs[0]->m : nullptr;
+    for (int i = 0; i < n_seq; ++i) {
+        if (!seqs[i] || seqs[i]->m != m) return fail(POCR_ERR_ARG, "pocr_decode_batch: sequences of one model");
+        for (int j = 0; j < i; ++j)
+            if (seqs[j] == seqs[i]) return fail(POCR_ERR_ARG, "pocr_decode_batch: sequence %d repeated", i);
+        if (first_tokens[i] < 0 || first_tokens[i] >= m->cfg.vocab)
+            return fail(POCR_ERR_ARG, "pocr_decode_batch: token out of vocab");
+    }
+    for (int i = 0; i < n_seq; ++i) out_counts[i] = 0;
+    if (max_new <= 0) return POCR_OK;
+    RC(model_ready(m));
+    CHECK_INJECT("decode_batch");
+    std::lock_guard<std::mutex> lk(m->ctx->mu);
+    HIP_TRY(hipSetDevice(m->ctx->device));
+    hipStream_t st = m->ctx->stream;
+    const int steps_needed = max_new - 1;
+    for (int i = 0; i < n_seq; ++i)
+        if (seqs[i]->len + steps_needed > seqs[i]->cap || max_new > seqs[i]->max_tokens)
+            return fail(POCR_ERR_ARG, "pocr_decode_batch: sequence %d: %d steps exceed capacity", i, steps_needed);
+    DecodeBatch b;
+    b.m = m;
+    b.n = n_seq;
+    b.nv = n_seq == 1 ? 1 : (n_seq == 2 ? 2 : 4);
+    for (int i = 0; i < n_seq; ++i) b.seq[i] = seqs[i];
+    RC(batch_alloc(b));
+    // per-sequence state: the first token sits in the argmax slots as if the
+    // previous step had chosen it (the step prologue reads it from there)
+    std::vector<StepState> hs(n_seq);
+    for (int i = 0; i < n_seq; ++i) {
+        RC(read_state(seqs[i], &hs[i]));
+        hs[i].err = 0;
+        hs[i].n_out = 0;
+        hs[i].next_pos = first_positions[i];
+        for (int k = 0; k < kArgSlots; ++k) hs[i].argmax_slot[k * kSlotPitch] = 0ull;
+        hs[i].argmax_slot[0] = (1ull << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)first_tokens[i]);
+        HIP_TRY(hipMemcpyAsync(seqs[i]->st, &hs[i], sizeof(StepState), hipMemcpyHostToDevice, st));
+    }
+    HIP_TRY(hipStreamSynchronize(st));
+    const char *g_env = getenv("POCR_HIP_GRAPH");
+    const bool use_graph = !(g_env && g_env[0] == '0');
+    if (use_graph) {
+        HIP_TRY(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+        const int rc = enqueue_batch_step(b);
+        const hipError_t e = hipStreamEndCapture(st, &b.graph);
+        if (rc != POCR_OK) return rc;
+        if (e != hipSuccess) return fail(POCR_ERR_DEVICE, "graph capture: %s", hipGetErrorString(e));
+        HIP_TRY(hipGraphInstantiate(&b.exec, b.graph, nullptr, nullptr, 0));
+    }
+    std::vector<int> produced(n_seq, 0);
+    std::vector<char> done(n_seq, 0);
+    std::vector<int32_t> tok;
+    int launched = 0;
+    const int batch = 16;
+    while (launched < steps_needed) {
+        const int k = std::min(batch, steps_needed - launched);
+        for (int i = 0; i < k; ++i) {
+            if (use_graph) HIP_TRY(hipGraphLaunch(b.exec, st));
+            else RC(enqueue_batch_step(b));
+        }
+        launched += k;
+        bool all_done = true;
+        for (int i = 0; i < n_seq; ++i) {
+            RC(read_state(seqs[i], &hs[i]));
+            if (done[i]) continue;
+            if (hs[i].err) return fail(POCR_ERR_DEVICE, "decode_batch: sequence %d: device state error %d", i, hs[i].err);
+            tok.resize(hs[i].n_out);
+            HIP_TRY(hipMemcpy(tok.data(), seqs[i]->tokens, (size_t)hs[i].n_out * 4, hipMemcpyDeviceToHost));
+            for (; produced[i] < hs[i].n_out && !done[i]; ++produced[i]) {
+                out_tokens[(size_t)i * max_new + produced[i]] = tok[produced[i]];
+                if (is_eos(tok[produced[i]], eos, n_eos)) done[i] = 1;
+            }
+            all_done = all_done && done[i];
+        }
+        if (all_done) break;
+    }
+    for (int i = 0; i < n_seq; ++i) {
+        if (!done[i]) {  // the token chosen by the last step
+            out_tokens[(size_t)i * max_new + produced[i]] =
+                (int32_t)(0xFFFFFFFFu - (uint32_t)(argmax_of(hs[i]) & 0xFFFFFFFFull));
+            ++produced[i];
+        }
+        out_counts[i] = produced[i];
+        seqs[i]->len = hs[i].len;
+    }
+    return POCR_OK;
 }
 
 extern "C" int pocr_prefill(pocr_seq *s, int n, const float *emb, const int32_t *pos3, float *logits,

@@ -88,6 +88,7 @@ _SIGS = {
     "pocr_step": (_i, [_vp, _vp, _vp, _i, _vp, _vp]),
     "pocr_prefill": (_i, [_vp, _i, _vp, _vp, _vp, _vp]),
     "pocr_decode_greedy": (_i, [_vp, C.c_int32, C.c_int32, _i, _vp, _i, _vp]),
+    "pocr_decode_batch": (_i, [_vp, _i, _vp, _vp, _i, _vp, _i, _vp, _vp]),
     "pocr_generate": (_i, [_vp, _vp, _i, _vp, _i, C.c_int32, _vp, C.c_int32, _i, _vp, _i, _i, _vp]),
     "pocr_mm_positions": (_i, [_vp, _i, C.c_int32, _vp, C.c_int32, _vp, _vp]),
 }
@@ -158,6 +159,21 @@ def mm_positions(ids, image_token_id: int, grid, merge: int = 2):
     g = np.ascontiguousarray(grid, dtype=np.int32)
     n = check(load().pocr_mm_positions(_ptr(ids), ids.size, image_token_id, _ptr(g), merge, _ptr(pos), _ptr(delta)))
     return pos[:n], int(delta[0])
+
+
+def decode_batch(seqs, first_tokens, first_positions, max_new: int, eos=(2,)):
+    """Greedy decode of 1..4 sequences of one model together (pocr_decode_batch):
+    returns one token array per sequence, first token first."""
+    n = len(seqs)
+    handles = (C.c_void_p * n)(*[s.h for s in seqs])
+    ft = np.ascontiguousarray(first_tokens, dtype=np.int32)
+    fp = np.ascontiguousarray(first_positions, dtype=np.int32)
+    eos = np.ascontiguousarray(list(eos) if eos else [-(1 << 30)], dtype=np.int32)
+    out = np.zeros((n, max(max_new, 1)), np.int32)
+    counts = np.zeros(n, np.int32)
+    check(load().pocr_decode_batch(C.cast(handles, C.c_void_p), n, _ptr(ft), _ptr(fp), max_new, _ptr(eos),
+                                   eos.size, _ptr(out), _ptr(counts)))
+    return [out[i, :counts[i]] for i in range(n)]
 
 
 def device_count() -> int:

@@ -60,13 +60,26 @@ def test_matvec_closed_form_known_answers(ctx, orc, qtype):
 
 
 @pytest.mark.parametrize("qtype", [Q8, Q4, Q6], ids=["q8", "q4", "q6"])
-@pytest.mark.parametrize("m", [2, 4, 16])
+@pytest.mark.parametrize("m", [2, 3, 4, 16])
 def test_batched_matvec(ctx, orc, rng, qtype, m):
     q = _qmat(rng, 3072, 1024, qtype)
     x = rng.standard_normal((m, 1024)).astype(np.float32)
     got = ctx.matvec(ctx.upload(q), x)
     for i in range(m):
         _close(got[i], orc.matvec(qtype, q.scales, q.packed, x[i]), rel=5e-5)
+
+
+@pytest.mark.parametrize("qtype", [Q8, Q4, Q6], ids=["q8", "q4", "q6"])
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: f"{s[0]}x{s[1]}")
+def test_matvec_vectors_per_pass(ctx, orc, rng, qtype, shape):
+    # M = 2 and 4 share each weight pass of the GEMV (the LM head included)
+    q = _qmat(rng, *shape, qtype)
+    w = ctx.upload(q)
+    for m in (2, 4):
+        x = rng.standard_normal((m, shape[1])).astype(np.float32)
+        got = ctx.matvec(w, x)
+        for i in range(m):
+            _close(got[i], orc.matvec(qtype, q.scales, q.packed, x[i]))
 
 
 @pytest.mark.parametrize("qtype", [Q8, Q4, Q6], ids=["q8", "q4", "q6"])
