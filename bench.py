@@ -326,6 +326,8 @@ def main():
     ap.add_argument("--calibrate-copy", action="store_true", help="with --roofline-only: add a 512 MiB copy")
     ap.add_argument("--prefill-only", action="store_true", help="time only the 1345-token Q4 image prefill")
     ap.add_argument("--no-batch", action="store_true", help="skip the 4-sequence batched decode")
+    ap.add_argument("--batch-only", action="store_true", help="time only the 4-sequence Q4 batched decode")
+    ap.add_argument("--batch-tokens", type=int, default=1024, help="tokens per sequence of the batched decode")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the decoder step runs on a single MI355X "
@@ -339,6 +341,11 @@ def main():
     from rapidocrvl_amd.config import ERNIE_0P3B as cfg
 
     ctx = lib.Context(0)
+    if args.batch_only:
+        _, model = build_model(ctx, cfg, lib.Q4)
+        print(json.dumps({"workload": "4-sequence q4 batched greedy decode",
+                          **batch_decode(model, cfg, n_new=args.batch_tokens, reps=1)}), flush=True)
+        return
     ids = workload_ids()
     img = synth.image_embeds(1332, cfg.hidden, seed=0)
     pos, delta = lib.mm_positions(ids, IMAGE_TOKEN, (1, 72, 74))
@@ -389,10 +396,10 @@ def main():
     extra["prefill_tok_s"] = round(n_prefix / t_prefill, 1)
     extra["prefill_TFLOP_s"] = round(prefill_flops(cfg, n_prefix) / t_prefill / 1e12, 2)
     if not args.no_batch:
-        extra["batch4_decode"] = {"q4": batch_decode(model, cfg)}
+        extra["batch4_decode"] = {"q4": batch_decode(model, cfg, n_new=args.batch_tokens)}
         log(f"[bench] 4-sequence batched decode q4 {extra['batch4_decode']['q4']}")
         _, m6 = build_model(ctx, cfg, lib.Q6)
-        extra["batch4_decode"]["q6"] = batch_decode(m6, cfg)
+        extra["batch4_decode"]["q6"] = batch_decode(m6, cfg, n_new=args.batch_tokens)
         log(f"[bench] 4-sequence batched decode q6 {extra['batch4_decode']['q6']}")
         del m6
 

@@ -958,6 +958,8 @@ static __global__ void __launch_bounds__(kPfThreads) k_attn_prefill(const float 
         float m = -INFINITY, lsum = 0.0f;
 
         auto compute = [&](int b, const uint8_t *slot) {
+            // scores are rounded (s·scale) before the max is subtracted
+#pragma clang fp contract(off)
             const __bf16 *im = reinterpret_cast<const __bf16 *>(slot);
             const int k0 = b * kPfKeys;
             v4f sT[2];

@@ -132,7 +132,8 @@ struct pocr_seq {
     pocr::StepState *st = nullptr;
     int32_t *tokens = nullptr;
     int max_tokens = 0;
-    int nsplit = 32;
+    int nsplit = 32;  // attention splits for rpw rows per wave
+    int rpw = 16;
     hipGraphExec_t decode_exec = nullptr;
     hipGraph_t decode_graph = nullptr;
     PrefillBufs pf;

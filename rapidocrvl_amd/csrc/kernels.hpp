@@ -1318,8 +1318,10 @@ static __global__ void __launch_bounds__(kThreads) k_step_begin_multi(StepBatch 
 // GQA decode attention, head_dim 128, split over cache rows.
 //
 // Workgroup (g, s) owns kv head g and cache rows [s·chunk, (s+1)·chunk),
-// chunk ≤ 64; wave w of it owns the 16 rows from s·chunk + 16w and is a
-// softmax split of its own.  Every request (the wave's K and V rows, the q
+// chunk ≤ 4·RPW; wave w of it owns the RPW rows from s·chunk + RPW·w and is
+// a softmax split of its own.  RPW (8 or 16 rows per wave) trades workgroups
+// in flight against split records to merge: the host picks it from the cache
+// capacity.  Every request (the wave's K and V rows, the q
 // heads of the group, the RoPE table entries, the new K/V row) is issued
 // before the step state is read, in one memory round trip.  q (and the new k)
 // are rotated in registers: the pair (d, d+64) of RoPE sits in lanes l and
@@ -1335,8 +1337,8 @@ static __global__ void __launch_bounds__(kThreads) k_step_begin_multi(StepBatch 
 // ---------------------------------------------------------------------------
 constexpr int kHD = 128;
 constexpr int kMaxGroup = 8;
-constexpr int kMaxChunk = 64;  // cache rows per workgroup (16 per wave)
-constexpr int kRec = kHD + 2;  // partial record per head: m, l, acc[128]
+constexpr int kMaxChunk = 64;  // cache rows per workgroup (RPW 16)
+constexpr int kRec = kHD + 4;  // partial record per head: m, l, 2 pad, acc[128] (16-byte aligned)
 
 struct AttnParams {
     const float *q;        // [heads*128] (unrotated if rope)
@@ -1354,12 +1356,14 @@ struct AttnParams {
     int heads, kvh, nsplit;
     int rows_cap;          // rows the splits are cut from (cache capacity)
     float scale;
+    int chunk;             // rows per split, attn_chunk(rows_cap, nsplit, 4·RPW)
 };
 
-__host__ __device__ constexpr int attn_chunk(int rows_cap, int nsplit) {
-    return ((rows_cap + nsplit - 1) / nsplit + 15) / 16 * 16 < kMaxChunk
+// rows per split: the capacity's share rounded up to 16, at most max_chunk
+__host__ __device__ constexpr int attn_chunk(int rows_cap, int nsplit, int max_chunk) {
+    return ((rows_cap + nsplit - 1) / nsplit + 15) / 16 * 16 < max_chunk
                ? ((rows_cap + nsplit - 1) / nsplit + 15) / 16 * 16
-               : kMaxChunk;
+               : max_chunk;
 }
 
 // reduce-scatter of 8 per-head partial dots over the 16 lanes of a row:
@@ -1402,12 +1406,18 @@ __device__ __forceinline__ void pin_args(AttnParams &p) {
     asm volatile("" : "+s"(p.q), "+s"(p.k_new), "+s"(p.v_new), "+s"(p.kc), "+s"(p.vc), "+s"(p.st), "+s"(p.part),
                  "+s"(p.head_out));
     asm volatile("" : "+s"(p.cos_t), "+s"(p.sin_t), "+s"(p.heads), "+s"(p.kvh), "+s"(p.nsplit), "+s"(p.rows_cap));
-    asm volatile("" ::"s"(p.len), "s"(p.has_rope));
+    asm volatile("" ::"s"(p.len), "s"(p.has_rope), "s"(p.chunk));
 }
 
+template <int RPW>
 __device__ __forceinline__ void attn_decode_body(AttnParams p) {
+    // products round before any later add (scores: s·scale, then s − max, as
+    // the reference does); the fused steps are written as fmaf
+#pragma clang fp contract(off)
+    static_assert(RPW == 8 || RPW == 16, "rows per wave");
+    constexpr int NJ = RPW / 4;  // score passes of 4 rows
     StepState *st = p.st;
-    __shared__ float4 e_lds[kWaves][kMaxGroup][4];      // wave-private probabilities [head][16 rows]
+    __shared__ float4 e_lds[kWaves][kMaxGroup][NJ];     // wave-private probabilities [head][RPW rows]
     __shared__ float w_m[kWaves][kMaxGroup], w_l[kWaves][kMaxGroup];
     __shared__ float2 w_acc[kWaves][kMaxGroup][kHD / 2];
 
@@ -1424,24 +1434,24 @@ __device__ __forceinline__ void attn_decode_body(AttnParams p) {
 
     // Splits are cut from the row capacity (a launch constant), so every
     // request below is issued before the step state has arrived.
-    const int chunk = attn_chunk(p.rows_cap, p.nsplit);
+    const int chunk = p.chunk;
     const int t0 = split * chunk;
-    const int wr0 = t0 + 16 * wave;  // first row of this wave
+    const int wr0 = t0 + RPW * wave;  // first row of this wave
     const int tmax = p.rows_cap - 1;
 
     // ---- 1. requests.  Rows past the capacity are clamped to the last row
     // (loaded, masked below); every lane issues the same loads.
-    float4 ka[4][2];  // K, score layout: pass j → row wr0 + 4j + rg, dims 8·l16..
+    float4 ka[NJ][2];  // K, score layout: pass j → row wr0 + 4j + rg, dims 8·l16..
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < NJ; ++j) {
         const int t = min(wr0 + 4 * j + rg, tmax);
         const float4 *src = reinterpret_cast<const float4 *>(p.kc + (size_t)t * kvd + g * kHD + 8 * l16);
         ka[j][0] = src[0];
         ka[j][1] = src[1];
     }
-    float2 va[16];  // V, P·V layout: row wr0 + i, dims 2·lane, 2·lane+1
+    float2 va[RPW];  // V, P·V layout: row wr0 + i, dims 2·lane, 2·lane+1
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
+    for (int i = 0; i < RPW; ++i) {
         const int t = min(wr0 + i, tmax);
         va[i] = *reinterpret_cast<const float2 *>(p.vc + (size_t)t * kvd + g * kHD + 2 * lane);
     }
@@ -1495,21 +1505,21 @@ __device__ __forceinline__ void attn_decode_body(AttnParams p) {
         f4_to(q[h], qr[h][0], qr[h][1]);
         if (rope && h < group) rope8(q[h], cs, sn, upper);
     }
-    if (newest >= wr0 && newest < wr0 + 16 && newest < t1) {  // uniform per wave
+    if (newest >= wr0 && newest < wr0 + RPW && newest < t1) {  // uniform per wave
         float k8[8];
         f4_to(k8, kn[0], kn[1]);
         if (rope) rope8(k8, cs, sn, upper);
         const int i = newest - wr0;
         if (rg == (i & 3)) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
+            for (int j = 0; j < NJ; ++j)
                 if (j == (i >> 2)) {
                     ka[j][0] = make_float4(k8[0], k8[1], k8[2], k8[3]);
                     ka[j][1] = make_float4(k8[4], k8[5], k8[6], k8[7]);
                 }
         }
 #pragma unroll
-        for (int ii = 0; ii < 16; ++ii)
+        for (int ii = 0; ii < RPW; ++ii)
             if (ii == i) va[ii] = vn;
         if (rg == 0) {
             float4 *kd = reinterpret_cast<float4 *>(p.kc + (size_t)newest * kvd + g * kHD + 8 * l16);
@@ -1521,10 +1531,10 @@ __device__ __forceinline__ void attn_decode_body(AttnParams p) {
 
     // ---- 4. scores; lanes 2h, 2h+1 of each 16-lane row hold head h's score
     const int hs = l16 >> 1;  // this lane's head after the reduce-scatter
-    float sj[4];
-    bool ok[4];
+    float sj[NJ];
+    bool ok[NJ];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < NJ; ++j) {
         float kv[8];
         f4_to(kv, ka[j][0], ka[j][1]);
         float part[8][1];
@@ -1540,15 +1550,15 @@ __device__ __forceinline__ void attn_decode_body(AttnParams p) {
         sj[j] = sdot * p.scale;
     }
 
-    // ---- 5. the wave's softmax per head (rows of head hs: 4 passes × 4 lane rows)
+    // ---- 5. the wave's softmax per head (rows of head hs: NJ passes × 4 lane rows)
     float m = -INFINITY;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) m = ok[j] ? fmaxf(m, sj[j]) : m;
+    for (int j = 0; j < NJ; ++j) m = ok[j] ? fmaxf(m, sj[j]) : m;
     m = fmaxf(m, xchg<XS16>(m));
     m = fmaxf(m, xchg<XS32>(m));
-    float ej[4], lsum = 0.0f;
+    float ej[NJ], lsum = 0.0f;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < NJ; ++j) {
         ej[j] = ok[j] ? fast_exp_ref(sj[j] - m) : 0.0f;
         lsum += ej[j];
     }
@@ -1557,7 +1567,7 @@ __device__ __forceinline__ void attn_decode_body(AttnParams p) {
     float *erow = reinterpret_cast<float *>(&e_lds[wave][0][0]);
     if ((l16 & 1) == 0 && hs < group) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) erow[hs * 16 + 4 * j + rg] = ej[j];
+        for (int j = 0; j < NJ; ++j) erow[hs * RPW + 4 * j + rg] = ej[j];
         if (rg == 0) {
             w_m[wave][hs] = m;
             w_l[wave][hs] = lsum;
@@ -1567,13 +1577,13 @@ __device__ __forceinline__ void attn_decode_body(AttnParams p) {
     // accesses in order, the fence keeps the compiler from reordering them
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
 
-    // ---- 6. Σ e·V for every head over the wave's 16 rows (2 dims per lane)
+    // ---- 6. Σ e·V for every head over the wave's RPW rows (2 dims per lane)
 #pragma unroll
     for (int h = 0; h < kMaxGroup; ++h) {
         if (h >= group) break;
-        float ev[16];
+        float ev[RPW];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
+        for (int k = 0; k < NJ; ++k) {
             const float4 t = e_lds[wave][h][k];
             ev[4 * k] = t.x;
             ev[4 * k + 1] = t.y;
@@ -1582,7 +1592,7 @@ __device__ __forceinline__ void attn_decode_body(AttnParams p) {
         }
         float a0 = 0.0f, a1 = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
+        for (int i = 0; i < RPW; ++i) {
             a0 = fmaf(ev[i], va[i].x, a0);
             a1 = fmaf(ev[i], va[i].y, a1);
         }
@@ -1612,60 +1622,60 @@ __device__ __forceinline__ void attn_decode_body(AttnParams p) {
             o.w = fmaf(f, b.y, o.w);
         }
         float *rh = p.part + ((size_t)(g * p.nsplit + split) * kMaxGroup + h) * kRec;
-        if (d4 == 0) {
-            rh[0] = M;
-            rh[1] = lt;
-        }
-        rh[2 + d4] = o.x;
-        rh[3 + d4] = o.y;
-        rh[4 + d4] = o.z;
-        rh[5 + d4] = o.w;
+        if (d4 == 0) *reinterpret_cast<float2 *>(rh) = make_float2(M, lt);
+        *reinterpret_cast<float4 *>(rh + 4 + d4) = o;
     }
 }
 
-// Merge of the per-split records, one workgroup per q head (two waves),
-// thread d owns output dim d: M = max m_s, out = Σ e_s·acc_s / Σ e_s·l_s with
-// e_s = FastExp(m_s − M).  Wave 0 computes the split weights lane-parallel
-// (lane = split) and hands them over in LDS.  A separate launch: the kernel
-// boundary orders the record writes before these reads on every XCD.  The
-// first batch of records is requested before the step state is read; splits
-// at or past the step's length hold stale records and are skipped.
+// Merge of the per-split records, one workgroup per q head (four waves):
+// M = max m_s, out = Σ e_s·acc_s / Σ e_s·l_s with e_s = FastExp(m_s − M).
+// Wave 0 computes the split weights lane-parallel (lane = split) and hands
+// them over in LDS; the 256 threads are 8 split groups × 32 lanes of 4 dims,
+// group k summing splits k, k+8, … with 16-byte loads, and the groups' sums
+// are added in group order.  A separate launch: the kernel boundary orders
+// the record writes before these reads on every XCD.  The first records are
+// requested before the step state is read; splits at or past the step's
+// length hold stale records and are skipped.
 constexpr int kMaxSplits = 1024;  // cache capacity ≤ 65536 rows
+constexpr int kMergeThreads = 256;
+constexpr int kMergeGroups = kMergeThreads / 32;
 
 __device__ __forceinline__ void attn_merge_body(AttnParams p) {
     __shared__ float e_lds[kMaxSplits];
+    __shared__ float4 o_lds[kMergeGroups][32];
     __shared__ float l_lds;
     const int hq = blockIdx.x;  // q head
     const int group = p.heads / p.kvh;
     const int g = hq / group, h = hq % group;
-    const int d = threadIdx.x, lane = d & 63;
-    const bool wave0 = d < 64;
-    const int chunk = attn_chunk(p.rows_cap, p.nsplit);
+    const int t = threadIdx.x, lane = t & 63;
+    const int sg = t >> 5, j = t & 31;  // split group, dims 4j..4j+3
+    const bool wave0 = t < 64;
     const float *base = p.part + ((size_t)g * p.nsplit * kMaxGroup + h) * kRec;
-    auto rec = [&](int sidx) { return base + (size_t)sidx * kMaxGroup * kRec; };
-    constexpr int B = 32;  // acc values requested up front
-    float av[B];
+    constexpr size_t RS = (size_t)kMaxGroup * kRec;  // split stride
+    auto acc = [&](int sidx) { return *reinterpret_cast<const float4 *>(base + sidx * RS + 4 + 4 * j); };
+    constexpr int B = 8;  // acc vectors requested up front (splits sg + 8b)
+    float4 av[B];
 #pragma unroll
-    for (int b = 0; b < B; ++b) av[b] = rec(min(b, p.nsplit - 1))[2 + d];
+    for (int b = 0; b < B; ++b) av[b] = acc(min(sg + kMergeGroups * b, p.nsplit - 1));
     float m0 = 0.0f, l0 = 0.0f;
     if (wave0) {
-        const float *r = rec(min(lane, p.nsplit - 1));
-        m0 = r[0];
-        l0 = r[1];
+        const float2 ml = *reinterpret_cast<const float2 *>(base + min(lane, p.nsplit - 1) * RS);
+        m0 = ml.x;
+        l0 = ml.y;
     }
     if (p.st && p.st->err) return;
     const int L = p.st ? p.st->len : p.len;
-    const int used = min(p.nsplit, (L + chunk - 1) / chunk);  // ≥ 1 for L ≥ 1
+    const int used = min(p.nsplit, (L + p.chunk - 1) / p.chunk);  // ≥ 1 for L ≥ 1
     if (wave0) {  // split weights, lane s + 64k ↔ split
         float M = lane < used ? m0 : -INFINITY;
-        for (int s = 64 + lane; s - lane < used; s += 64) M = fmaxf(M, s < used ? rec(s)[0] : -INFINITY);
+        for (int s = 64 + lane; s - lane < used; s += 64) M = fmaxf(M, s < used ? base[s * RS] : -INFINITY);
         M = wave_max(M);
         float ls = 0.0f;
         for (int s = lane; s - lane < used; s += 64) {
             float e = 0.0f, lv = 0.0f;
             if (s < used) {
-                const float ms = s < 64 ? m0 : rec(s)[0];
-                lv = s < 64 ? l0 : rec(s)[1];
+                const float ms = s < 64 ? m0 : base[s * RS];
+                lv = s < 64 ? l0 : base[s * RS + 1];
                 e = fast_exp_ref(ms - M);
                 e_lds[s] = e;
             }
@@ -1675,20 +1685,44 @@ __device__ __forceinline__ void attn_merge_body(AttnParams p) {
         if (lane == 0) l_lds = ls;
     }
     __syncthreads();
-    float o = 0.0f;
+    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+    auto add = [&](int s, const float4 &a) {
+        const float e = e_lds[s];
+        o.x = fmaf(e, a.x, o.x);
+        o.y = fmaf(e, a.y, o.y);
+        o.z = fmaf(e, a.z, o.z);
+        o.w = fmaf(e, a.w, o.w);
+    };
 #pragma unroll
     for (int b = 0; b < B; ++b)
-        if (b < used) o = fmaf(e_lds[b], av[b], o);
-    for (int s = B; s < used; ++s) o = fmaf(e_lds[s], rec(s)[2 + d], o);
-    p.head_out[(size_t)hq * kHD + d] = o * (1.0f / l_lds);
+        if (sg + kMergeGroups * b < used) add(sg + kMergeGroups * b, av[b]);
+#pragma unroll 4
+    for (int s = sg + kMergeGroups * B; s < used; s += kMergeGroups) add(s, acc(s));
+    o_lds[sg][j] = o;
+    __syncthreads();
+    if (t < 32) {
+        float4 r = o_lds[0][t];
+#pragma unroll
+        for (int k = 1; k < kMergeGroups; ++k) {
+            const float4 a = o_lds[k][t];
+            r.x += a.x;
+            r.y += a.y;
+            r.z += a.z;
+            r.w += a.w;
+        }
+        const float inv = 1.0f / l_lds;
+        *reinterpret_cast<float4 *>(p.head_out + (size_t)hq * kHD + 4 * t) =
+            make_float4(r.x * inv, r.y * inv, r.z * inv, r.w * inv);
+    }
 }
 
-static __global__ void __launch_bounds__(kThreads) k_attn_decode(AttnParams args) {
+template <int RPW>
+__global__ void __launch_bounds__(kThreads) k_attn_decode(AttnParams args) {
     AttnParams p = args;
     pin_args(p);
-    attn_decode_body(p);
+    attn_decode_body<RPW>(p);
 }
-static __global__ void __launch_bounds__(kHD) k_attn_merge(AttnParams args) {
+static __global__ void __launch_bounds__(kMergeThreads) k_attn_merge(AttnParams args) {
     AttnParams p = args;
     pin_args(p);
     attn_merge_body(p);
@@ -1700,16 +1734,25 @@ static __global__ void __launch_bounds__(kHD) k_attn_merge(AttnParams args) {
 struct AttnMulti {
     AttnParams a[kMaxNV];
 };
-__device__ __forceinline__ AttnParams attn_pick(const AttnMulti &b) {
-    const int i = blockIdx.z;
-    return i == 0 ? b.a[0] : (i == 1 ? b.a[1] : (i == 2 ? b.a[2] : b.a[3]));
-}
-static __global__ void __launch_bounds__(kThreads) k_attn_decode_multi(AttnMulti b) {
-    const AttnParams p = attn_pick(b);
+// b is the kernel's only argument (offset 0 of the argument segment): entry
+// blockIdx.z is read in place with scalar loads (a select over the array
+// would copy it to scratch).  The argument segment exists in the device pass.
+typedef __attribute__((address_space(4))) const AttnParams KernargAttn;
+template <int RPW>
+__global__ void __launch_bounds__(kThreads) k_attn_decode_multi(AttnMulti b) {
+    (void)b;
+#if defined(__HIP_DEVICE_COMPILE__)
+    const AttnParams p = ((KernargAttn *)__builtin_amdgcn_kernarg_segment_ptr())[blockIdx.z];
     if ((int)blockIdx.y >= p.nsplit) return;  // uniform
-    attn_decode_body(p);
+    attn_decode_body<RPW>(p);
+#endif
 }
-static __global__ void __launch_bounds__(kHD) k_attn_merge_multi(AttnMulti b) { attn_merge_body(attn_pick(b)); }
+static __global__ void __launch_bounds__(kMergeThreads) k_attn_merge_multi(AttnMulti b) {
+    (void)b;
+#if defined(__HIP_DEVICE_COMPILE__)
+    attn_merge_body(((KernargAttn *)__builtin_amdgcn_kernarg_segment_ptr())[blockIdx.z]);
+#endif
+}
 
 // Attention for head dims other than 128 (small test shapes): one workgroup
 // per q head, serial over rows, same math.

@@ -268,13 +268,15 @@ static bool pick_big(int tag, bool one, int lpr, int cpl, const void **fn) {
 }
 
 // NV activation vectors per weight pass (batched decode): the big launch keeps
-// U·NV = kBigU entries and always gives every wave one group
+// kBigU rows per lane group (U·NV ≤ 32 reduce-scatter entries, the workgroup
+// count and its activation prologues as for one vector) and gives every wave
+// one group
 template <int QT, int NV>
 static bool pick_nv(int nmat, bool big, int lpr, int cpl, bool argmax, const void **fn) {
     if (nmat == 2) return gemv_fast_kernel<QT, 2, 2, 0, false, 3, NV>(lpr, cpl, fn);
     if (big)
-        return argmax ? gemv_fast_kernel<QT, 1, kBigU / NV, 0, true, big_planes<QT>(), NV>(lpr, cpl, fn)
-                      : gemv_fast_kernel<QT, 1, kBigU / NV, 0, true, 3, NV>(lpr, cpl, fn);
+        return argmax ? gemv_fast_kernel<QT, 1, kBigU, 0, true, big_planes<QT>(), NV>(lpr, cpl, fn)
+                      : gemv_fast_kernel<QT, 1, kBigU, 0, true, 3, NV>(lpr, cpl, fn);
     return gemv_fast_kernel<QT, 1, 2, 0, false, 3, NV>(lpr, cpl, fn);
 }
 
@@ -324,7 +326,7 @@ static int plan_gemv(int qtype, int nmat, int rows, int cols, const DevMat *mats
     bool ok = false;
     // big row counts: 8 rows per lane group and step (more bytes in flight)
     const bool big = fast && nmat == 1 && cpl == 1 && rows >= 8192;
-    const int u = big ? kBigU / nv : 2;
+    const int u = big ? kBigU : 2;
     if (big) max_grid = nv > 1 ? 1 << 30 : std::max(max_grid, POCR_BIG_GRID);
     // row groups must not straddle segments
     if (fast && nmat == 1 && seg_end) {
@@ -646,8 +648,27 @@ extern "C" int pocr_mrope_pair(pocr_ctx *ctx, float *q, float *k, const float *c
     return sync(s);
 }
 
-// one split per kMaxChunk rows of capacity
-static int attn_nsplit(int cap) { return std::max(1, (cap + kMaxChunk - 1) / kMaxChunk); }
+// Rows per wave of the decode attention for a cache capacity: short caches
+// take 32-row splits (more workgroups in flight), longer ones 64-row splits
+// (half the records to merge); the split count stays ≤ kMaxSplits.  On
+// MI355X (18 layers, 16 q / 2 kv heads) 8 rows per wave lead up to ~2k rows
+// of capacity, 16 beyond (4 rows per wave trail everywhere: the merge of
+// four times the records costs more than the workgroups gain).
+static int attn_rpw(int cap) { return cap <= 2048 ? 8 : 16; }
+// one split per 4·rpw rows of capacity
+static int attn_nsplit(int cap, int rpw) { return std::max(1, (cap + 4 * rpw - 1) / (4 * rpw)); }
+
+// the launch shape of one decode attention: rows per wave, splits, rows per split
+static void attn_shape(AttnParams &a, int cap, int rpw) {
+    a.rows_cap = cap;
+    a.nsplit = attn_nsplit(cap, rpw);
+    a.chunk = attn_chunk(cap, a.nsplit, 4 * rpw);
+}
+
+static void launch_attn_decode(hipStream_t s, int rpw, dim3 grid, const AttnParams &a) {
+    if (rpw == 8) hipLaunchKernelGGL(k_attn_decode<8>, grid, dim3(kThreads), 0, s, a);
+    else hipLaunchKernelGGL(k_attn_decode<16>, grid, dim3(kThreads), 0, s, a);
+}
 
 extern "C" int pocr_text_attention(pocr_ctx *ctx, const float *q, const float *k_cache, const float *v_cache,
                                    int cache_len, int heads, int kv_heads, int head_dim, float *out) {
@@ -669,7 +690,8 @@ extern "C" int pocr_text_attention(pocr_ctx *ctx, const float *q, const float *k
     const float scale = (float)(1.0 / std::sqrt((double)head_dim));  // invSqrt, model.go:7391
     const int group = heads / kv_heads;
     if (head_dim == kHD && group <= kMaxGroup) {
-        const int nsplit = attn_nsplit(cache_len);
+        const int rpw = attn_rpw(cache_len);
+        const int nsplit = attn_nsplit(cache_len, rpw);
         if (nsplit > kMaxSplits) return fail(POCR_ERR_UNSUPPORTED, "text_attention: cache above %d rows", kMaxSplits * kMaxChunk);
         RC(ctx->part.ensure((size_t)kv_heads * nsplit * kMaxGroup * kRec * 4));
         AttnParams p{};
@@ -683,11 +705,10 @@ extern "C" int pocr_text_attention(pocr_ctx *ctx, const float *q, const float *k
         p.head_out = ctx->out.as<float>();
         p.heads = heads;
         p.kvh = kv_heads;
-        p.nsplit = nsplit;
-        p.rows_cap = cache_len;
+        attn_shape(p, cache_len, rpw);
         p.scale = scale;
-        hipLaunchKernelGGL(k_attn_decode, dim3(kv_heads, nsplit), dim3(kThreads), 0, s, p);
-        hipLaunchKernelGGL(k_attn_merge, dim3(heads), dim3(kHD), 0, s, p);
+        launch_attn_decode(s, rpw, dim3(kv_heads, nsplit), p);
+        hipLaunchKernelGGL(k_attn_merge, dim3(heads), dim3(kMergeThreads), 0, s, p);
     } else {
         if ((size_t)cache_len * 4 > 60 * 1024) return fail(POCR_ERR_UNSUPPORTED, "text_attention: cache too long");
         hipLaunchKernelGGL(k_attn_small, dim3(heads), dim3(kThreads), (size_t)cache_len * 4, s, ctx->x.as<float>(),
@@ -867,7 +888,8 @@ extern "C" int pocr_seq_create(pocr_model *m, int capacity, pocr_seq **out) {
     m->refs.fetch_add(1);
     s->m = m;
     s->cap = capacity;
-    s->nsplit = attn_nsplit(capacity);
+    s->rpw = attn_rpw(capacity);
+    s->nsplit = attn_nsplit(capacity, s->rpw);
     if (s->nsplit > kMaxSplits) {
         delete s;
         m->refs.fetch_sub(1);
@@ -1073,7 +1095,8 @@ extern "C" int pocr_time_attention(pocr_ctx *ctx, int heads, int kv_heads, int h
         return fail(POCR_ERR_ARG, "pocr_time_attention: bad arguments");
     if (head_dim != kHD || heads / kv_heads > kMaxGroup)
         return fail(POCR_ERR_UNSUPPORTED, "pocr_time_attention: head_dim 128 and GQA group <= 8 only");
-    const int nsplit = attn_nsplit(cache_len);
+    const int rpw = attn_rpw(cache_len);
+    const int nsplit = attn_nsplit(cache_len, rpw);
     if (nsplit > kMaxSplits) return fail(POCR_ERR_UNSUPPORTED, "pocr_time_attention: cache above %d rows",
                                          kMaxSplits * kMaxChunk);
     CHECK_INJECT("time_attention");
@@ -1110,14 +1133,13 @@ extern "C" int pocr_time_attention(pocr_ctx *ctx, int heads, int kv_heads, int h
     a.head_out = ctx->out.as<float>();
     a.heads = heads;
     a.kvh = kv_heads;
-    a.nsplit = nsplit;
-    a.rows_cap = cache_len;
+    attn_shape(a, cache_len, rpw);
     a.scale = (float)(1.0 / std::sqrt((double)kHD));
     auto launch = [&](int layer) {
         a.kc = ctx->kc.as<float>() + layer * layer_floats;
         a.vc = a.kc + (size_t)cache_len * kvd;
-        hipLaunchKernelGGL(k_attn_decode, dim3(kv_heads, nsplit), dim3(kThreads), 0, s, a);
-        hipLaunchKernelGGL(k_attn_merge, dim3(heads), dim3(kHD), 0, s, a);
+        launch_attn_decode(s, rpw, dim3(kv_heads, nsplit), a);
+        hipLaunchKernelGGL(k_attn_merge, dim3(heads), dim3(kMergeThreads), 0, s, a);
     };
     for (int l = 0; l < n_layers; ++l) launch(l);
     HIP_TRY(hipGetLastError());
@@ -1181,11 +1203,10 @@ static int enqueue_layer(pocr_seq *s, int li, bool last, bool kv_only) {
     a.head_out = s->head_out;
     a.heads = c.heads;
     a.kvh = c.kv_heads;
-    a.nsplit = s->nsplit;
-    a.rows_cap = s->cap;
+    attn_shape(a, s->cap, s->rpw);
     a.scale = (float)(1.0 / std::sqrt((double)c.head_dim));
-    hipLaunchKernelGGL(k_attn_decode, dim3(c.kv_heads, s->nsplit), dim3(kThreads), 0, st, a);
-    hipLaunchKernelGGL(k_attn_merge, dim3(c.heads), dim3(kHD), 0, st, a);
+    launch_attn_decode(st, s->rpw, dim3(c.kv_heads, s->nsplit), a);
+    hipLaunchKernelGGL(k_attn_merge, dim3(c.heads), dim3(kMergeThreads), 0, st, a);
     HIP_TRY(hipGetLastError());
     if (kv_only) return POCR_OK;
 
@@ -1434,8 +1455,11 @@ int enqueue_batch_step(DecodeBatch &b) {
     hipLaunchKernelGGL(k_step_begin_multi, dim3(b.n), dim3(kThreads), 0, st, sb, m->embed, b.h, H, c.vocab, m->freq,
                        m->axis);
     HIP_TRY(hipGetLastError());
-    int max_split = 1;
-    for (int i = 0; i < b.n; ++i) max_split = std::max(max_split, b.seq[i]->nsplit);
+    // one rows-per-wave for all: the largest the sequences' capacities pick
+    // (no more splits than any sequence's records were sized for)
+    int rpw = 8, max_split = 1;
+    for (int i = 0; i < b.n; ++i) rpw = std::max(rpw, b.seq[i]->rpw);
+    for (int i = 0; i < b.n; ++i) max_split = std::max(max_split, attn_nsplit(b.seq[i]->cap, rpw));
     for (int li = 0; li < c.layers; ++li) {
         const LayerW &L = m->layers[li];
         const bool last = li + 1 == c.layers;
@@ -1471,12 +1495,13 @@ int enqueue_batch_step(DecodeBatch &b) {
             a.head_out = b.ho + (size_t)i * Q;
             a.heads = c.heads;
             a.kvh = c.kv_heads;
-            a.nsplit = s->nsplit;
-            a.rows_cap = s->cap;
+            attn_shape(a, s->cap, rpw);
             a.scale = (float)(1.0 / std::sqrt((double)c.head_dim));
         }
-        hipLaunchKernelGGL(k_attn_decode_multi, dim3(c.kv_heads, max_split, b.n), dim3(kThreads), 0, st, am);
-        hipLaunchKernelGGL(k_attn_merge_multi, dim3(c.heads, 1, b.n), dim3(kHD), 0, st, am);
+        const dim3 ag(c.kv_heads, max_split, b.n);
+        if (rpw == 8) hipLaunchKernelGGL(k_attn_decode_multi<8>, ag, dim3(kThreads), 0, st, am);
+        else hipLaunchKernelGGL(k_attn_decode_multi<16>, ag, dim3(kThreads), 0, st, am);
+        hipLaunchKernelGGL(k_attn_merge_multi, dim3(c.heads, 1, b.n), dim3(kMergeThreads), 0, st, am);
         HIP_TRY(hipGetLastError());
         // 3. o_proj + residual (+ the Q4/Q6 behaviour per sequence)
         const pocr_weight *wo = L.w[POCR_W_O];

@@ -163,7 +163,8 @@ def test_rmsnorm_and_rope_known_answers(ctx, orc):
     assert list(k) == [-3, -1, 1, 3] and list(q) == [-3, -1, 1, 3]
 
 
-@pytest.mark.parametrize("L", [1, 2, 6, 7, 33, 300, 1024, 4096])
+# lengths cover both rows-per-wave kernels (≤ 2048 rows: 8, above: 16)
+@pytest.mark.parametrize("L", [1, 2, 6, 7, 33, 300, 1024, 2049, 4096, 8193])
 def test_text_attention_head128(ctx, orc, rng, L):
     q = rng.standard_normal(16 * 128).astype(np.float32)
     kc = rng.standard_normal(L * 256).astype(np.float32)
