@@ -365,6 +365,12 @@ def main():
     dt, toks = time_decode(seq, n_prefix, first_tok, first_pos, args.decode_tokens, args.warmup, args.steps)
     tok_s = args.decode_tokens * args.steps / dt
     log(f"[bench] q4 decode {tok_s:.1f} tok/s ({dt / args.steps * 1e3:.1f} ms per {args.decode_tokens} tokens)")
+    # the same decode drawing every token from the top 40 candidates (T = 0.8)
+    seq.set_sampling(0.8, 40, 1)
+    dts, _ = time_decode(seq, n_prefix, first_tok, first_pos, args.decode_tokens, 1, max(1, args.steps // 2))
+    seq.set_sampling(0.0, 0, 0)
+    sampled_tok_s = args.decode_tokens * max(1, args.steps // 2) / dts
+    log(f"[bench] q4 sampled decode (top-40, T 0.8) {sampled_tok_s:.1f} tok/s")
 
     # roofline: Q4 LM-head GEMV, rotating copies > Infinity Cache
     lm_qt, lm_sc, lm_data, lm_cols = weights["lm_head"]
@@ -392,6 +398,7 @@ def main():
             log(f"[bench] cpu config 1 {extra['cpu_config1']}")
         m8.close()
         del w8
+    extra["sampled_decode_tok_s"] = {"top_k": 40, "temperature": 0.8, "tok_s": round(sampled_tok_s, 1)}
     extra["prefill_ms"] = round(t_prefill * 1e3, 2)
     extra["prefill_tok_s"] = round(n_prefix / t_prefill, 1)
     extra["prefill_TFLOP_s"] = round(prefill_flops(cfg, n_prefix) / t_prefill / 1e12, 2)

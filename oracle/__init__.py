@@ -84,6 +84,14 @@ def lib():
         L.orc_step.argtypes = [C.c_void_p, C.c_void_p, _f32p, _i32p, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p]
         L.orc_generate.argtypes = [C.c_void_p, _i32p, C.c_int, C.c_void_p, C.c_int, C.c_int, _i32p, C.c_int,
                                    C.c_int, _i32p, C.c_int, _i32p]
+        L.orc_generate_sampled.argtypes = [C.c_void_p, _i32p, C.c_int, C.c_void_p, C.c_int, C.c_int, _i32p,
+                                           C.c_int, C.c_int, _i32p, C.c_int, C.c_double, C.c_int, C.c_uint64,
+                                           _i32p]
+        L.orc_rng_float64.restype = C.c_double
+        L.orc_rng_float64.argtypes = [C.POINTER(C.c_uint64)]
+        L.orc_topk.argtypes = [_f32p, C.c_int, C.c_int, _i32p, _f32p]
+        L.orc_sample_candidates.restype = C.c_int32
+        L.orc_sample_candidates.argtypes = [_i32p, _f32p, C.c_int, C.c_double, C.POINTER(C.c_uint64)]
         L.orc_set_threads.argtypes = [C.c_int]
         L.orc_get_threads.restype = C.c_int
         _lib = L
@@ -92,6 +100,32 @@ def lib():
 
 def _f32(a):
     return np.ascontiguousarray(a, dtype=np.float32)
+
+
+class Rng:
+    """fastRNG (model.go:1829-1840): SplitMix64 state, Float64 draws."""
+
+    def __init__(self, seed: int):
+        self.state = C.c_uint64(seed & ((1 << 64) - 1))
+
+    def float64(self) -> float:
+        return float(lib().orc_rng_float64(C.byref(self.state)))
+
+
+def topk(scores, k):
+    """topKSelectWithWork (topk.go:322-345): ids and scores of the min(k, n)
+    best, score descending, equal scores by lower index."""
+    scores = _f32(scores)
+    ids = np.zeros(max(k, 1), np.int32)
+    sc = np.zeros(max(k, 1), np.float32)
+    n = lib().orc_topk(scores, scores.size, k, ids, sc)
+    return ids[:n], sc[:n]
+
+
+def sample_candidates(ids, scores, temperature, rng: Rng) -> int:
+    """sampleCandidateScoresScratch (model.go:1950-1990) on sorted candidates."""
+    ids = np.ascontiguousarray(ids, np.int32)
+    return int(lib().orc_sample_candidates(ids, _f32(scores), ids.size, temperature, C.byref(rng.state)))
 
 
 def row_bytes(qtype: int, cols: int) -> int:
@@ -313,7 +347,8 @@ class Model:
     def seq(self, capacity):
         return Seq(self, capacity)
 
-    def generate(self, ids, max_new, eos=(2,), image_embeds=None, image_token_id=-1, grid=(1, 1, 1), merge=2):
+    def generate(self, ids, max_new, eos=(2,), image_embeds=None, image_token_id=-1, grid=(1, 1, 1), merge=2,
+                 temperature=0.0, top_k=0, seed=0):
         ids = np.ascontiguousarray(ids, dtype=np.int32)
         out = np.zeros(max_new, np.int32)
         eos = np.ascontiguousarray(list(eos) if eos else [-(1 << 30)], dtype=np.int32)
@@ -323,8 +358,9 @@ class Model:
             ptr = img.ctypes.data
         else:
             img, n_img, ptr = None, 0, None
-        n = lib().orc_generate(self.h, ids, ids.size, ptr, n_img, image_token_id,
-                               np.asarray(grid, np.int32), merge, max_new, eos, eos.size, out)
+        n = lib().orc_generate_sampled(self.h, ids, ids.size, ptr, n_img, image_token_id,
+                                       np.asarray(grid, np.int32), merge, max_new, eos, eos.size,
+                                       float(temperature), int(top_k), seed & ((1 << 64) - 1), out)
         if n < 0:
             raise RuntimeError(f"orc_generate failed: {n}")
         return out[:n]

@@ -991,10 +991,193 @@ static int is_eos(int id, const int32_t *eos, int n) {
     return 0;
 }
 
+/* ---- sampling LM head ---- */
+
+double orc_rng_float64(uint64_t *state) {
+    /* model.go:1833-1840 */
+    *state += 0x9e3779b97f4a7c15ull;
+    uint64_t z = *state;
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    z ^= z >> 31;
+    return (double)(z >> 11) * (1.0 / 9007199254740992.0);
+}
+
+int orc_topk(const float *scores, int n, int k, int32_t *ids, float *out_scores) {
+    /* topk.go:322-345: partial selection sort; score desc, ties lower id */
+    if (k <= 0 || n <= 0) return 0;
+    if (k > n) k = n;
+    int32_t *idx = (int32_t *)malloc(sizeof(int32_t) * (size_t)n);
+    for (int i = 0; i < n; i++) idx[i] = i;
+    for (int i = 0; i < k; i++) {
+        int best = i;
+        for (int j = i + 1; j < n; j++) {
+            const float sj = scores[idx[j]], sb = scores[idx[best]];
+            if (sj > sb || (sj == sb && idx[j] < idx[best])) best = j;
+        }
+        const int32_t t = idx[i];
+        idx[i] = idx[best];
+        idx[best] = t;
+    }
+    for (int i = 0; i < k; i++) {
+        ids[i] = idx[i];
+        out_scores[i] = scores[idx[i]];
+    }
+    free(idx);
+    return k;
+}
+
+/* pickWeightedRawFloat32, model.go:2418-2456 (f32 running sum) */
+static int pick_raw_f32(const float *w, int n, float pick) {
+    float acc = 0.0f;
+    for (int i = 0; i < n; i++) {
+        acc += w[i];
+        if (pick <= acc) return i;
+    }
+    return -1;
+}
+
+/* pickWeightedFloat32, model.go:2342-2416 (f64 running sum of f32 weights) */
+static int pick_f64(const float *w, int n, double pick) {
+    double acc = 0.0;
+    for (int i = 0; i < n; i++) {
+        acc += (double)w[i];
+        if (pick <= acc) return i;
+    }
+    return -1;
+}
+
+int32_t orc_sample_candidates(const int32_t *ids, const float *sc, int n, double temperature, uint64_t *state) {
+    if (n <= 0) return 0;
+    if (n == 1) return ids[0];
+    float w[64];
+    float wv[4];
+    if (n > 64) return -1;
+    if (temperature == 1.0) {
+        /* model.go:1954-1963 */
+        float mx = sc[0];
+        for (int i = 1; i < n; i++) mx = sc[i] > mx ? sc[i] : mx;
+        if (n == 2) { /* model.go:2145-2158 */
+            const float s0 = sc[0], s1 = sc[1];
+            if (s0 >= s1) {
+                const double w1 = (double)orc_fast_exp(s1 - s0);
+                return orc_rng_float64(state) * (1 + w1) <= 1 ? ids[0] : ids[1];
+            }
+            const double w0 = (double)orc_fast_exp(s0 - s1);
+            return orc_rng_float64(state) * (w0 + 1) <= w0 ? ids[0] : ids[1];
+        }
+        if (n <= 4) { /* model.go:2159-2199 */
+            for (int i = 0; i < n; i++) wv[i] = orc_fast_exp(sc[i] - mx);
+            if (n == 3) {
+                const float pick = (float)orc_rng_float64(state) * ((wv[0] + wv[1]) + wv[2]);
+                if (pick <= wv[0]) return ids[0];
+                if (pick <= wv[0] + wv[1]) return ids[1];
+                return ids[2];
+            }
+            const float pick = (float)orc_rng_float64(state) * ((wv[0] + wv[1]) + (wv[2] + wv[3]));
+            float acc = wv[0];
+            if (pick <= acc) return ids[0];
+            acc += wv[1];
+            if (pick <= acc) return ids[1];
+            acc += wv[2];
+            if (pick <= acc) return ids[2];
+            return ids[3];
+        }
+        /* sampleCandidateScoresTemp1Scratch, model.go:2040-2063 */
+        float sum = 0.0f;
+        for (int i = 0; i < n; i++) {
+            w[i] = orc_fast_exp(sc[i] - mx);
+            sum += w[i];
+        }
+        const float pick = (float)orc_rng_float64(state) * sum;
+        const int idx = pick_raw_f32(w, n, pick);
+        return idx >= 0 ? ids[idx] : ids[n - 1];
+    }
+    /* model.go:1965-1990 */
+    const float inv = (float)(1.0 / temperature);
+    float mxr = sc[0];
+    for (int i = 1; i < n; i++) mxr = sc[i] > mxr ? sc[i] : mxr;
+    const float mx = mxr * inv;
+    if (n == 2) { /* sampleCandidateScoresSmall, model.go:1997-2011 */
+        const float s0 = sc[0] * inv, s1 = sc[1] * inv;
+        if (s0 >= s1) {
+            const double w1 = (double)orc_fast_exp(s1 - s0);
+            return orc_rng_float64(state) * (1 + w1) <= 1 ? ids[0] : ids[1];
+        }
+        const double w0 = (double)orc_fast_exp(s0 - s1);
+        return orc_rng_float64(state) * (w0 + 1) <= w0 ? ids[0] : ids[1];
+    }
+    if (n <= 4) { /* model.go:2012-2037 */
+        double d[4];
+        for (int i = 0; i < n; i++) d[i] = (double)orc_fast_exp(sc[i] * inv - mx);
+        if (n == 3) {
+            const double pick = orc_rng_float64(state) * ((d[0] + d[1]) + d[2]);
+            double acc = d[0];
+            if (pick <= acc) return ids[0];
+            acc += d[1];
+            if (pick <= acc) return ids[1];
+            return ids[2];
+        }
+        const double pick = orc_rng_float64(state) * ((d[0] + d[1]) + (d[2] + d[3]));
+        double acc = d[0];
+        if (pick <= acc) return ids[0];
+        acc += d[1];
+        if (pick <= acc) return ids[1];
+        acc += d[2];
+        if (pick <= acc) return ids[2];
+        return ids[3];
+    }
+    double sum = 0.0;
+    for (int i = 0; i < n; i++) {
+        const double wi = (double)orc_fast_exp(sc[i] * inv - mx);
+        w[i] = (float)wi;
+        sum += wi;
+    }
+    const double pick = orc_rng_float64(state) * sum;
+    const int idx = pick_f64(w, n, pick);
+    return idx >= 0 ? ids[idx] : ids[n - 1];
+}
+
+static int generate_impl(orc_model *m, const int32_t *ids, int n_ids, const float *image_embeds, int n_image,
+                         int image_token_id, const int32_t grid[3], int merge, int max_new, const int32_t *eos,
+                         int n_eos, double temperature, int top_k, uint64_t seed, int32_t *out_tokens);
+
 int orc_generate(orc_model *m, const int32_t *ids, int n_ids, const float *image_embeds, int n_image,
                  int image_token_id, const int32_t grid[3], int merge, int max_new, const int32_t *eos,
                  int n_eos, int32_t *out_tokens) {
+    return generate_impl(m, ids, n_ids, image_embeds, n_image, image_token_id, grid, merge, max_new, eos, n_eos,
+                         0.0, 0, 0, out_tokens);
+}
+
+int orc_generate_sampled(orc_model *m, const int32_t *ids, int n_ids, const float *image_embeds, int n_image,
+                         int image_token_id, const int32_t grid[3], int merge, int max_new, const int32_t *eos,
+                         int n_eos, double temperature, int top_k, uint64_t seed, int32_t *out_tokens) {
+    return generate_impl(m, ids, n_ids, image_embeds, n_image, image_token_id, grid, merge, max_new, eos, n_eos,
+                         temperature, top_k, seed, out_tokens);
+}
+
+/* one token from the step's logits: the candidates path of
+ * forwardEmbeddingForSampling (model.go:3632-3638, matVecTopKMaybeCPU
+ * 7202-7235) and sampleCandidateScoresScratch; greedy when not sampling */
+static int32_t pick_token(const float *logits, int vocab, int sampling, int top_k, double temperature,
+                          uint64_t *state, int32_t greedy) {
+    if (!sampling) return greedy;
+    int32_t cid[64];
+    float csc[64];
+    const int n = orc_topk(logits, vocab, top_k, cid, csc);
+    return orc_sample_candidates(cid, csc, n, temperature, state);
+}
+
+static int generate_impl(orc_model *m, const int32_t *ids, int n_ids, const float *image_embeds, int n_image,
+                         int image_token_id, const int32_t grid[3], int merge, int max_new, const int32_t *eos,
+                         int n_eos, double temperature, int top_k, uint64_t seed, int32_t *out_tokens) {
     if (n_ids <= 0 || max_new <= 0) return 0;
+    /* generationCanReturnCandidatesOnly (model.go:1866-1868) with the
+     * candidate width this oracle supports (1 < top_k <= 64, top_k < vocab) */
+    const int sampling = temperature > 0 && top_k > 1;
+    if (sampling && (top_k > 64 || top_k >= m->vocab)) return -5;
+    uint64_t state = seed; /* samplingRNGInto, model.go:1846-1852 */
+    float *logits = sampling ? (float *)malloc(sizeof(float) * (size_t)m->vocab) : NULL;
     int32_t *pos = (int32_t *)malloc(sizeof(int32_t) * 3 * (size_t)n_ids);
     int rope_delta = 0;
     if (n_image > 0) {
@@ -1020,9 +1203,10 @@ int orc_generate(orc_model *m, const int32_t *ids, int n_ids, const float *image
             if (ids[p] < 0 || ids[p] >= m->vocab) { rc = -4; goto done; }
             emb = m->embed + (size_t)ids[p] * m->hidden;
         }
-        orc_step(m, s, emb, pos + 3 * p, p == n_ids - 1, NULL, &next, NULL);
+        orc_step(m, s, emb, pos + 3 * p, p == n_ids - 1, p == n_ids - 1 ? logits : NULL, &next, NULL);
     }
     if (img != n_image) { rc = -3; goto done; }
+    next = pick_token(logits, m->vocab, sampling, top_k, temperature, &state, next);
     int n_out = 0;
     for (int i = 0; i < max_new; i++) {
         out_tokens[n_out++] = next;
@@ -1030,11 +1214,13 @@ int orc_generate(orc_model *m, const int32_t *ids, int n_ids, const float *image
         if (i + 1 >= max_new) break;
         int32_t p = n_ids + n_out - 1 + rope_delta; /* len(out)-1+ropeDelta (model.go:1695) */
         int32_t p3[3] = {p, p, p};
-        orc_step(m, s, m->embed + (size_t)next * m->hidden, p3, 1, NULL, &next, NULL);
+        orc_step(m, s, m->embed + (size_t)next * m->hidden, p3, 1, logits, &next, NULL);
+        next = pick_token(logits, m->vocab, sampling, top_k, temperature, &state, next);
     }
     rc = n_out;
 done:
     orc_seq_free(s);
     free(pos);
+    free(logits);
     return rc;
 }

@@ -119,6 +119,30 @@ int orc_generate(orc_model *m, const int32_t *ids, int n_ids, const float *image
                  int n_image, int image_token_id, const int32_t grid[3], int merge,
                  int max_new, const int32_t *eos, int n_eos, int32_t *out_tokens);
 
+/* ---- sampling LM head (SURVEY (f) 2) ---- */
+/* fastRNG.Float64 (model.go:1829-1840): one SplitMix64 step of *state, the
+ * top 53 bits of the mixed word as a double in [0, 1) */
+double orc_rng_float64(uint64_t *state);
+/* topKSelectWithWork (topk.go:322-345): the min(k, n) best of scores[0..n),
+ * score descending, equal scores by lower index.  Returns the count. */
+int orc_topk(const float *scores, int n, int k, int32_t *ids, float *out_scores);
+/* sampleCandidateScoresScratch (model.go:1950-1990) over candidates sorted
+ * as orc_topk returns them, with the branches it takes: temperature 1 →
+ * sampleCandidateScoresTemp1Small (n <= 4, model.go:2139-2200) or
+ * sampleCandidateScoresTemp1Scratch (model.go:2040-2063, f32 weights and
+ * sums, pickWeightedRawFloat32 2418-2456); otherwise
+ * sampleCandidateScoresSmall (n <= 4, model.go:1992-2038) or f64 sums with
+ * f32-stored weights (pickWeightedFloat32 2342-2416).  Draws one value from
+ * *state unless n <= 1.  Returns the chosen id. */
+int32_t orc_sample_candidates(const int32_t *ids, const float *scores, int n, double temperature, uint64_t *state);
+/* orc_generate with GenerateOptions sampling (model.go:1538-1568, 1846-1868,
+ * 3632-3638): temperature > 0 with 1 < top_k < vocab samples every token
+ * from the top_k candidates of the LM-head scores with a generator seeded
+ * by seed; otherwise greedy.  Returns as orc_generate. */
+int orc_generate_sampled(orc_model *m, const int32_t *ids, int n_ids, const float *image_embeds, int n_image,
+                         int image_token_id, const int32_t grid[3], int merge, int max_new, const int32_t *eos,
+                         int n_eos, double temperature, int top_k, uint64_t seed, int32_t *out_tokens);
+
 /* thread pool for the CPU baseline (parallelForMax, ops.go:570-614) */
 void orc_set_threads(int n);
 int orc_get_threads(void);

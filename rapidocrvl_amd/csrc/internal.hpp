@@ -15,6 +15,7 @@
 
 #include "../../include/pocr_hip.h"
 #include "kernels.hpp"
+#include "sample.hpp"
 
 namespace pocr {
 int fail(int code, const char *fmt, ...);
@@ -67,6 +68,7 @@ struct pocr_ctx {
     // op-level staging
     DevBuf x, out, out2, out3, res, vbuf, kc, vc, part, tabs, state;
     DevBuf gxd, gxs, gxb;  // batched GEMV activation digits
+    DevBuf topk_part, samp;  // top-k partial keys, sampler state
     // pinned host staging for large host→device uploads: two halves, each
     // reused once the copy recorded on its event has finished
     uint8_t *pin = nullptr;
@@ -134,6 +136,13 @@ struct pocr_seq {
     int max_tokens = 0;
     int nsplit = 32;  // attention splits for rpw rows per wave
     int rpw = 16;
+    // sampling head (temperature > 0, 1 < top_k ≤ 64); greedy otherwise
+    bool sampling = false;
+    double temperature = 0.0;
+    int top_k = 0;
+    uint64_t seed = 0;
+    pocr::SampleState *samp = nullptr;
+    unsigned long long *topk_part = nullptr;  // [kTopKMaxParts][kTopKMax] keys
     hipGraphExec_t decode_exec = nullptr;
     hipGraph_t decode_graph = nullptr;
     PrefillBufs pf;
@@ -165,5 +174,9 @@ unsigned long long argmax_of(const StepState &s);
 float *layer_k(const pocr_seq *s, int layer);
 float *layer_v(const pocr_seq *s, int layer);
 int seq_set_state(pocr_seq *s, int len);
+// LM head on RMSNorm(x)·final_norm: greedy argmax into the step state, or the
+// sampling head (logits, top-k, one draw into argmax slot 0) when the
+// sequence samples
+int enqueue_lm_head(pocr_seq *s, const float *x, bool want_logits);
 constexpr int kBigGrid = 1024;
 }  // namespace pocr

@@ -71,6 +71,8 @@ pocr_seq::~pocr_seq() {
     free_dev(part);
     free_dev(st);
     free_dev(tokens);
+    free_dev(samp);
+    free_dev(topk_part);
     prefill_free(pf);
 }
 
@@ -484,6 +486,80 @@ extern "C" int pocr_matvec_argmax(pocr_ctx *ctx, const pocr_weight *w, const flo
     if (key == 0ull) return fail(POCR_ERR_DEVICE, "matvec_argmax: no finite score");
     *index = (int32_t)(0xFFFFFFFFu - (uint32_t)(key & 0xFFFFFFFFull));
     if (score) *score = key_value(key);
+    return POCR_OK;
+}
+
+// top-k of `rows` scores into ss (and, with sample, one draw into ss and
+// argmax slot 0 of st)
+static int enqueue_topk(hipStream_t s, const float *scores, int rows, int k, unsigned long long *part,
+                        SampleState *ss, StepState *st, int sample) {
+    const int nparts = (rows + kTopKSlice - 1) / kTopKSlice;
+    if (k < 1 || k > kTopKMax || k > rows || nparts > kTopKMaxParts)
+        return fail(POCR_ERR_UNSUPPORTED, "top-k: k=%d over %d rows (k <= 64, rows <= %d)", k, rows,
+                    kTopKMaxParts * kTopKSlice);
+    hipLaunchKernelGGL(k_topk_partial, dim3(nparts), dim3(kTopKThreads), 0, s, scores, rows, k, part);
+    hipLaunchKernelGGL(k_topk_final, dim3(1), dim3(kTopKThreads), 0, s, part, nparts, k, ss, st, sample);
+    HIP_TRY(hipGetLastError());
+    return POCR_OK;
+}
+
+// top-k of `rows` device scores in ctx->out through ctx's sampler state;
+// returns the state read back
+static int ctx_topk(pocr_ctx *ctx, int rows, int k, int sample, const SampleState &in, SampleState *out) {
+    hipStream_t s = ctx->stream;
+    RC(ctx->topk_part.ensure((size_t)kTopKMaxParts * kTopKMax * 8));
+    RC(ctx->samp.ensure(sizeof(SampleState)));
+    RC(h2d(s, ctx->samp.p, &in, sizeof(SampleState)));
+    RC(enqueue_topk(s, ctx->out.as<float>(), rows, k, ctx->topk_part.as<unsigned long long>(),
+                    ctx->samp.as<SampleState>(), nullptr, sample));
+    RC(d2h(s, out, ctx->samp.p, sizeof(SampleState)));
+    return sync(s);
+}
+
+extern "C" int pocr_matvec_topk(pocr_ctx *ctx, const pocr_weight *w, const float *x, int k, int32_t *ids,
+                                float *scores) {
+    if (!ctx || !w || !x || !ids || k < 1) return fail(POCR_ERR_ARG, "pocr_matvec_topk: bad arguments");
+    if (k > kTopKMax || k > w->rows) return fail(POCR_ERR_UNSUPPORTED, "pocr_matvec_topk: k %d (<= 64, <= rows)", k);
+    CHECK_INJECT("matvec_topk");
+    CTX_GUARD(ctx);
+    hipStream_t s = ctx->stream;
+    RC(ctx->x.ensure((size_t)w->cols * 4));
+    RC(ctx->out.ensure((size_t)w->rows * 4));
+    RC(h2d(s, ctx->x.p, x, (size_t)w->cols * 4));
+    GemvParams p = gemv_params_1(w);
+    p.x = ctx->x.as<float>();
+    p.out = ctx->out.as<float>();
+    RC(gemv_launch(s, p, 1, PRO_COPY, EPI_PLAIN, kBigGrid));
+    SampleState in{}, out;
+    RC(ctx_topk(ctx, w->rows, k, 0, in, &out));
+    for (int i = 0; i < out.n; ++i) {
+        ids[i] = out.ids[i];
+        if (scores) scores[i] = out.scores[i];
+    }
+    return out.n;
+}
+
+extern "C" int pocr_sample_topk(pocr_ctx *ctx, const float *logits, int n, int k, double temperature,
+                                uint64_t *rng_state, int32_t *token, int32_t *ids, float *scores) {
+    if (!ctx || !logits || !rng_state || !token || n <= 0) return fail(POCR_ERR_ARG, "pocr_sample_topk: bad arguments");
+    if (!(temperature > 0.0) || std::isinf(temperature) || k < 2 || k >= n)
+        return fail(POCR_ERR_ARG, "pocr_sample_topk: needs temperature > 0 and 1 < k < n");
+    if (k > kTopKMax) return fail(POCR_ERR_UNSUPPORTED, "pocr_sample_topk: k %d > 64", k);
+    CHECK_INJECT("sample_topk");
+    CTX_GUARD(ctx);
+    RC(ctx->out.ensure((size_t)n * 4));
+    RC(h2d(ctx->stream, ctx->out.p, logits, (size_t)n * 4));
+    SampleState in{}, out;
+    in.rng = *rng_state;
+    in.temperature = temperature;
+    in.top_k = k;
+    RC(ctx_topk(ctx, n, k, 1, in, &out));
+    *rng_state = out.rng;
+    *token = out.token;
+    for (int i = 0; i < out.n; ++i) {
+        if (ids) ids[i] = out.ids[i];
+        if (scores) scores[i] = out.scores[i];
+    }
     return POCR_OK;
 }
 
@@ -910,6 +986,9 @@ extern "C" int pocr_seq_create(pocr_model *m, int capacity, pocr_seq **out) {
     if (e == hipSuccess) e = hipMalloc(&s->part, (size_t)c.kv_heads * s->nsplit * kMaxGroup * kRec * 4);
     if (e == hipSuccess) e = hipMalloc(&s->st, sizeof(StepState));
     if (e == hipSuccess) e = hipMalloc(&s->tokens, (size_t)s->max_tokens * 4);
+    if (e == hipSuccess) e = hipMalloc(&s->samp, sizeof(SampleState));
+    if (e == hipSuccess) e = hipMalloc(&s->topk_part, (size_t)kTopKMaxParts * kTopKMax * 8);
+    if (e == hipSuccess) e = hipMemset(s->samp, 0, sizeof(SampleState));
     if (e == hipSuccess) e = hipMemset(s->kv, 0, (size_t)c.layers * 2 * capacity * kvd * 4);
     if (e != hipSuccess) {
         delete s;
@@ -969,6 +1048,46 @@ extern "C" int pocr_seq_reset(pocr_seq *s) {
 }
 
 extern "C" int pocr_seq_len(const pocr_seq *s) { return s ? s->len : POCR_ERR_ARG; }
+
+// the generator at its seed (samplingRNGInto, model.go:1846-1852)
+static int seed_sampler(pocr_seq *s) {
+    hipStream_t st = s->m->ctx->stream;
+    HIP_TRY(hipMemcpyAsync(&s->samp->rng, &s->seed, 8, hipMemcpyHostToDevice, st));
+    HIP_TRY(hipStreamSynchronize(st));  // s->seed may change once the lock is released
+    return POCR_OK;
+}
+
+extern "C" int pocr_seq_set_sampling(pocr_seq *s, double temperature, int top_k, uint64_t seed) {
+    if (!s) return fail(POCR_ERR_ARG, "pocr_seq_set_sampling: null");
+    // ValidateGenerateOptions (model.go:450-470)
+    if (!(temperature >= 0.0) || std::isinf(temperature)) return fail(POCR_ERR_ARG, "temperature must be finite and >= 0");
+    if (top_k < 0) return fail(POCR_ERR_ARG, "top_k must be >= 0");
+    // generationUsesArgmaxSampling (model.go:1858-1860) → greedy; otherwise
+    // the candidates path (1866-1868, topK < vocab) with at most 64 of them
+    const bool greedy = temperature <= 0.0 || top_k == 1;
+    if (!greedy && (top_k == 0 || top_k > kTopKMax || top_k >= s->m->cfg.vocab))
+        return fail(POCR_ERR_UNSUPPORTED, "sampling: top_k %d (device sampling takes 1 < top_k <= 64 < vocab)", top_k);
+    std::lock_guard<std::mutex> lk(s->m->ctx->mu);
+    HIP_TRY(hipSetDevice(s->m->ctx->device));
+    HIP_TRY(hipStreamSynchronize(s->m->ctx->stream));
+    if (s->sampling != !greedy || (!greedy && s->top_k != top_k)) {
+        // the captured step ends in the other LM head: capture again
+        if (s->decode_exec) (void)hipGraphExecDestroy(s->decode_exec);
+        if (s->decode_graph) (void)hipGraphDestroy(s->decode_graph);
+        s->decode_exec = nullptr;
+        s->decode_graph = nullptr;
+    }
+    s->sampling = !greedy;
+    s->temperature = temperature;
+    s->top_k = greedy ? 0 : top_k;
+    s->seed = seed;
+    SampleState h{};
+    h.rng = seed;
+    h.temperature = temperature;
+    h.top_k = s->top_k;
+    HIP_TRY(hipMemcpy(s->samp, &h, sizeof(h), hipMemcpyHostToDevice));
+    return POCR_OK;
+}
 
 extern "C" int pocr_seq_read_kv(pocr_seq *s, int layer, float *k, float *v) {
     if (!s || !k || !v || layer < 0 || layer >= s->m->cfg.layers) return fail(POCR_ERR_ARG, "pocr_seq_read_kv");
@@ -1241,16 +1360,23 @@ static int enqueue_layer(pocr_seq *s, int li, bool last, bool kv_only) {
     return POCR_OK;
 }
 
-// LM head on RMSNorm(vbuf)·final_norm, argmax into the step state
-static int enqueue_head(pocr_seq *s, bool want_logits) {
+int pocr::enqueue_lm_head(pocr_seq *s, const float *x, bool want_logits) {
     pocr_model *m = s->m;
+    hipStream_t st = m->ctx->stream;
     GemvParams p = gemv_params_1(m->lm);
-    p.x = s->vbuf;
+    p.x = x;
     p.norm_w = m->final_norm;
     p.eps = m->cfg.rms_norm_eps;
-    p.out = want_logits ? s->logits : nullptr;
     p.st = s->st;
-    return gemv_launch(m->ctx->stream, p, 1, PRO_RMSNORM, EPI_ARGMAX, kBigGrid);
+    if (!s->sampling) {
+        p.out = want_logits ? s->logits : nullptr;
+        return gemv_launch(st, p, 1, PRO_RMSNORM, EPI_ARGMAX, kBigGrid);
+    }
+    // matVecTopKMaybeCPU (model.go:7202-7235): every score, then the top-k
+    // and the draw (sampleCandidateScoresScratch, 1950-1990)
+    p.out = s->logits;
+    RC(gemv_launch(st, p, 1, PRO_RMSNORM, EPI_PLAIN, kBigGrid));
+    return enqueue_topk(st, s->logits, m->cfg.vocab, s->top_k, s->topk_part, s->samp, s->st, 1);
 }
 
 static int enqueue_step(pocr_seq *s, int mode, bool need_logits, bool want_logits) {
@@ -1264,7 +1390,7 @@ static int enqueue_step(pocr_seq *s, int mode, bool need_logits, bool want_logit
         const bool last = li + 1 == c.layers;
         RC(enqueue_layer(s, li, last, last && !need_logits));
     }
-    if (need_logits) RC(enqueue_head(s, want_logits));
+    if (need_logits) RC(enqueue_lm_head(s, s->vbuf, want_logits));
     return POCR_OK;
 }
 
@@ -1573,6 +1699,8 @@ extern "C" int pocr_decode_batch(pocr_seq *const *seqs, int n_seq, const int32_t
             if (seqs[j] == seqs[i]) return fail(POCR_ERR_ARG, "pocr_decode_batch: sequence %d repeated", i);
         if (first_tokens[i] < 0 || first_tokens[i] >= m->cfg.vocab)
             return fail(POCR_ERR_ARG, "pocr_decode_batch: token out of vocab");
+        if (seqs[i]->sampling)
+            return fail(POCR_ERR_UNSUPPORTED, "pocr_decode_batch: sequence %d samples (the batch is greedy)", i);
     }
     for (int i = 0; i < n_seq; ++i) out_counts[i] = 0;
     if (max_new <= 0) return POCR_OK;
@@ -1698,6 +1826,7 @@ extern "C" int pocr_generate(pocr_seq *s, const int32_t *ids, int n_ids, const f
         HIP_TRY(hipSetDevice(m->ctx->device));
         RC(seq_set_state(s, 0));
         if (n_ids + max_new - 1 > s->cap) return fail(POCR_ERR_ARG, "pocr_generate: capacity %d too small", s->cap);
+        if (s->sampling) RC(seed_sampler(s));  // one generator per generation call
         int32_t next = -1;
         if (use_prefill) {
             const int rc = prefill_ids_locked(s, ids, n_ids, n_image > 0 ? image_embeds : nullptr,

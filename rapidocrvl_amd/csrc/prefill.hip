@@ -377,13 +377,7 @@ int prefill_run(pocr_seq *s, int n, const int32_t *pos3, float *logits, int32_t 
     hs.pos[2] = pos3[3 * (n - 1) + 2];
     HIP_TRY(hipMemcpyAsync(s->st, &hs, sizeof(hs), hipMemcpyHostToDevice, st));
     HIP_TRY(hipStreamSynchronize(st));  // hs is a stack object
-    GemvParams p = gemv_params_1(m->lm);
-    p.x = b.v + (size_t)(n - 1) * H;
-    p.norm_w = m->final_norm;
-    p.eps = eps;
-    p.out = logits ? s->logits : nullptr;
-    p.st = s->st;
-    RC(gemv_launch(st, p, 1, PRO_RMSNORM, EPI_ARGMAX, kBigGrid));
+    RC(enqueue_lm_head(s, b.v + (size_t)(n - 1) * H, logits != nullptr));
     StepState out;
     RC(read_state(s, &out));
     s->len = clen0 + n;

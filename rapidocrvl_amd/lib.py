@@ -61,6 +61,8 @@ _SIGS = {
     "pocr_weight_free": (None, [_vp]),
     "pocr_matvec": (_i, [_vp, _vp, _vp, _i, _vp]),
     "pocr_matvec_argmax": (_i, [_vp, _vp, _vp, _vp, _vp]),
+    "pocr_matvec_topk": (_i, [_vp, _vp, _vp, _i, _vp, _vp]),
+    "pocr_sample_topk": (_i, [_vp, _vp, _i, _i, C.c_double, C.POINTER(C.c_uint64), _vp, _vp, _vp]),
     "pocr_fused_matvec3": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "pocr_fused_matvec3_mrope": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp, _vp, _vp]),
     "pocr_swiglu_gate_up": (_i, [_vp, _vp, _vp, _vp, _vp]),
@@ -77,6 +79,7 @@ _SIGS = {
     "pocr_seq_create": (_i, [_vp, _i, C.POINTER(_vp)]),
     "pocr_seq_destroy": (None, [_vp]),
     "pocr_seq_reset": (_i, [_vp]),
+    "pocr_seq_set_sampling": (_i, [_vp, C.c_double, _i, C.c_uint64]),
     "pocr_seq_len": (_i, [_vp]),
     "pocr_seq_read_kv": (_i, [_vp, _i, _vp, _vp]),
     "pocr_seq_truncate": (_i, [_vp, _i]),
@@ -256,6 +259,26 @@ class Context:
         check(load().pocr_matvec_argmax(self.h, w.h, _ptr(x), _ptr(idx), _ptr(sc)))
         return int(idx[0]), float(sc[0])
 
+    def matvec_topk(self, w: Weight, x, k: int):
+        """The k best rows of W·x (score descending, equal scores by lower row)."""
+        x = _f32(x)
+        ids = np.zeros(max(k, 1), np.int32)
+        sc = np.zeros(max(k, 1), np.float32)
+        n = check(load().pocr_matvec_topk(self.h, w.h, _ptr(x), k, _ptr(ids), _ptr(sc)))
+        return ids[:n], sc[:n]
+
+    def sample_topk(self, logits, k: int, temperature: float, rng_state: int):
+        """One draw from the top k of logits with the fastRNG state rng_state;
+        returns (token, advanced state, candidate ids, candidate scores)."""
+        logits = _f32(logits)
+        st = C.c_uint64(rng_state & ((1 << 64) - 1))
+        tok = np.zeros(1, np.int32)
+        ids = np.zeros(k, np.int32)
+        sc = np.zeros(k, np.float32)
+        check(load().pocr_sample_topk(self.h, _ptr(logits), logits.size, k, float(temperature), C.byref(st),
+                                      _ptr(tok), _ptr(ids), _ptr(sc)))
+        return int(tok[0]), int(st.value), ids, sc
+
     def fused_matvec3(self, a: Weight, b: Weight, c: Weight, x):
         x = _f32(x)
         oa, ob, oc = (np.zeros(w.rows, np.float32) for w in (a, b, c))
@@ -417,6 +440,11 @@ class Sequence:
 
     def reset(self):
         check(load().pocr_seq_reset(self.h))
+
+    def set_sampling(self, temperature: float, top_k: int, seed: int = 0):
+        """Token choice of generate/decode: greedy (temperature <= 0 or
+        top_k == 1) or draws from the top_k candidates (1 < top_k <= 64)."""
+        check(load().pocr_seq_set_sampling(self.h, float(temperature), int(top_k), seed & ((1 << 64) - 1)))
 
     def read_kv(self, layer: int):
         cfg = self.model.cfg

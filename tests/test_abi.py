@@ -28,6 +28,9 @@ def test_null_arguments_are_arg_errors():
     assert L.pocr_step(None, None, None, 1, None, None) == lib.POCR_ERR_ARG
     assert L.pocr_quantize_rows(7, 0, None, 1, 1, None, None) == lib.POCR_ERR_ARG
     assert b"pocr_step" in L.pocr_last_error()
+    assert L.pocr_matvec_topk(None, None, None, 4, None, None) == lib.POCR_ERR_ARG
+    assert L.pocr_sample_topk(None, None, 8, 4, 1.0, None, None, None, None) == lib.POCR_ERR_ARG
+    assert L.pocr_seq_set_sampling(None, 1.0, 4, 0) == lib.POCR_ERR_ARG
 
 
 def test_fault_injection_is_reported_before_device_work(monkeypatch):

@@ -1,0 +1,188 @@
+"""Sampling LM head on the device: top-k candidates and the draw among them
+against the oracle (topKSelectWithWork + sampleCandidateScoresScratch with
+fastRNG), at op level and inside generation."""
+import json
+import os
+
+import numpy as np
+import pytest
+
+from rapidocrvl_amd import lib, synth
+from rapidocrvl_amd.config import ERNIE_0P3B, DecoderConfig
+
+pytestmark = pytest.mark.gpu
+
+Q8, Q4, Q6 = 1000, 1001, 1002
+KAT = json.load(open(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "reference_kats.json")))
+MID = DecoderConfig(hidden=1024, inter=3072, layers=3, heads=16, kv_heads=2, head_dim=128, vocab=5000, eps=1e-5,
+                    rope_theta=500000.0)
+
+
+def _exact_q8(rng, rows, cols):
+    """Q8 rows whose scale is a power of two and codes integers, with integer
+    x: every score is exact in f32 on both sides, so ids must match exactly,
+    ties included."""
+    codes = rng.integers(-20, 21, (rows, cols)).astype(np.float32)
+    codes[:, 0] = 127  # max |w| = 127·2^e → scale 2^e exactly
+    e = rng.integers(-3, 2, rows).astype(np.float32)
+    return codes * (2.0 ** e)[:, None]
+
+
+@pytest.mark.parametrize("k", [1, 2, 7, 50, 64])
+def test_matvec_topk_exact_scores_with_ties(ctx, orc, k):
+    rng = np.random.default_rng(k)
+    w = _exact_q8(rng, 9000, 256)
+    w[[100, 4000, 8999]] = w[50]  # identical rows: exact ties, lower row first
+    x = rng.integers(-3, 4, 256).astype(np.float32)
+    x[0] = 0.0
+    q = lib.QMatrix.quantize(w, Q8)
+    logits = orc.matvec(Q8, q.scales, q.packed, x)
+    want_ids, want_sc = orc.topk(logits, k)
+    ids, sc = ctx.matvec_topk(ctx.upload(q), x, k)
+    assert list(ids) == list(want_ids)
+    assert np.array_equal(sc, want_sc)
+
+
+@pytest.mark.parametrize("qtype", [Q8, Q4, Q6], ids=["q8", "q4", "q6"])
+def test_matvec_topk_planted_rows(ctx, orc, qtype):
+    # the reference's own top-k test shape (270 rows × 5 columns, k = 50)
+    k = KAT["topk_planted"]
+    rows, cols = k["rows"], k["cols"]
+    r = np.arange(rows)[:, None]
+    c = np.arange(cols)[None, :]
+    w = (((r % 17) - 8) * 0.125 + ((r + c) % 7 - 3) * 0.25).astype(np.float32)
+    for row, vals in k["planted"].items():
+        w[int(row)] = vals
+    x = np.asarray(k["x"], np.float32)
+    q = lib.QMatrix.quantize(w, qtype)
+    logits = orc.matvec(qtype, q.scales, q.packed, x)
+    ids, sc = ctx.matvec_topk(ctx.upload(q), x, k["k"])
+    assert len(ids) == k["k"]
+    # scores to 1e-4 (the reference's bar); order by score, then lower row
+    assert np.max(np.abs(sc - logits[ids])) <= 1e-4
+    key = [(-float(s), int(i)) for s, i in zip(sc, ids)]
+    assert key == sorted(key)
+    # the set is the oracle's top-k up to scores within 1e-4 of the k-th
+    kth = np.sort(logits)[::-1][k["k"] - 1]
+    want, _ = orc.topk(logits, k["k"])
+    sure = {int(i) for i in want if logits[i] > kth + 1e-4}
+    assert sure <= set(int(i) for i in ids)
+    assert ids[0] == 269
+
+
+def test_matvec_topk_lm_head(ctx, orc):
+    rng = np.random.default_rng(5)
+    w = (rng.standard_normal((103424, 1024)) * 0.02).astype(np.float32)
+    q = lib.QMatrix.quantize(w, Q4)
+    wd = ctx.upload(q)
+    for seed in range(3):
+        x = np.random.default_rng(seed).standard_normal(1024).astype(np.float32)
+        logits = orc.matvec(Q4, q.scales, q.packed, x)
+        ids, sc = ctx.matvec_topk(wd, x, 64)
+        want, wsc = orc.topk(logits, 64)
+        assert np.max(np.abs(sc - logits[ids])) <= 1e-4 * max(1.0, float(np.max(np.abs(wsc))))
+        gaps = np.diff(np.sort(logits)[::-1][:65])
+        if np.min(np.abs(gaps)) > 1e-5:  # no near-ties: the same ids in the same order
+            assert list(ids) == list(want)
+
+
+@pytest.mark.parametrize("k", [2, 3, 4, 5, 8, 9, 20, 64])
+@pytest.mark.parametrize("temp", [1.0, 0.7, 2.5, 0.04])
+def test_sample_topk_matches_oracle(ctx, orc, k, temp):
+    # same logits on both sides: candidates, draw and generator state are
+    # bit-identical (temperature 0.04 reaches FastExp's wrap below −88.7)
+    rng = np.random.default_rng(k * 100 + int(temp * 100))
+    logits = (rng.standard_normal(50000) * 3).astype(np.float32)
+    logits[rng.integers(0, 50000, 8)] = logits.max()  # ties at the top
+    state = 0x1234_5678_9ABC_DEF0 + k
+    r = orc.Rng(state)
+    for _ in range(12):
+        want_ids, want_sc = orc.topk(logits, k)
+        want_tok = orc.sample_candidates(want_ids, want_sc, temp, r)
+        tok, state, ids, sc = ctx.sample_topk(logits, k, temp, state)
+        assert list(ids) == list(want_ids) and np.array_equal(sc, want_sc)
+        assert tok == want_tok
+        assert state == r.state.value
+        logits = np.roll(logits, 977)
+
+
+def test_sample_topk_rejects_bad_arguments(ctx):
+    logits = np.zeros(100, np.float32)
+    for k, temp in ((1, 1.0), (100, 1.0), (4, 0.0), (4, -1.0), (4, float("nan"))):
+        with pytest.raises(lib.PocrError):
+            ctx.sample_topk(logits, k, temp, 1)
+    with pytest.raises(lib.PocrError):
+        ctx.sample_topk(np.zeros(200, np.float32), 65, 1.0, 1)
+
+
+def _models(orc, ctx, cfg, qtype, seed):
+    w = synth.make_weights(cfg, qtype, seed=seed)
+    om = orc.Model(cfg)
+    om.load_weights(w)
+    gm = lib.Model(ctx, cfg)
+    gm.load_weights(w)
+    return om, gm
+
+
+@pytest.mark.parametrize("qtype", [Q4, Q8], ids=["q4", "q8"])
+@pytest.mark.parametrize("temp,top_k", [(0.8, 20), (1.0, 3), (1.0, 64), (1.7, 9)])
+def test_generate_sampled_matches_oracle(orc, ctx, qtype, temp, top_k):
+    om, gm = _models(orc, ctx, MID, qtype, seed=9)
+    ids = synth.prompt_ids(23, seed=4, high=MID.vocab)
+    for seed in (1, 2024):
+        want = list(om.generate(ids, 24, eos=(), temperature=temp, top_k=top_k, seed=seed))
+        s = gm.seq(ids.size + 24)
+        s.set_sampling(temp, top_k, seed)
+        assert list(s.generate(ids, 24, eos=(), use_prefill=True)) == want
+        # the generator restarts at the seed for every generation
+        assert list(s.generate(ids, 24, eos=(), use_prefill=True)) == want
+        s.close()
+
+
+def test_generate_sampled_ernie_image(orc, ctx):
+    cfg = ERNIE_0P3B
+    om, gm = _models(orc, ctx, cfg, Q4, seed=0)
+    orc.set_threads(16)
+    img_tok = 100295
+    ids = np.concatenate([synth.prompt_ids(5, seed=10), np.full(24, img_tok, np.int32),
+                          synth.prompt_ids(8, seed=20)]).astype(np.int32)
+    img = synth.image_embeds(24, cfg.hidden, seed=1)
+    kw = dict(image_embeds=img, image_token_id=img_tok, grid=(1, 8, 12))
+    want = list(om.generate(ids, 12, eos=(), temperature=0.9, top_k=40, seed=77, **kw))
+    s = gm.seq(ids.size + 12)
+    s.set_sampling(0.9, 40, 77)
+    assert list(s.generate(ids, 12, eos=(), use_prefill=True, **kw)) == want
+
+
+def test_greedy_settings_stay_greedy(orc, ctx):
+    om, gm = _models(orc, ctx, MID, Q4, seed=3)
+    ids = synth.prompt_ids(17, seed=8, high=MID.vocab)
+    want = list(om.generate(ids, 12, eos=()))
+    s = gm.seq(ids.size + 12)
+    for temp, top_k in ((0.0, 40), (1.3, 1)):
+        s.set_sampling(temp, top_k, 5)
+        assert list(s.generate(ids, 12, eos=(), use_prefill=True)) == want
+    # back from sampling to greedy: the captured step is rebuilt
+    s.set_sampling(0.8, 10, 5)
+    s.generate(ids, 12, eos=(), use_prefill=True)
+    s.set_sampling(0.0, 0, 0)
+    assert list(s.generate(ids, 12, eos=(), use_prefill=True)) == want
+
+
+def test_sampling_settings_errors(ctx):
+    gm = lib.Model(ctx, MID)
+    gm.load_weights(synth.make_weights(MID, Q4, seed=1))
+    s = gm.seq(16)
+    for temp, top_k in ((float("nan"), 4), (float("inf"), 4), (-0.5, 4), (1.0, -2)):
+        with pytest.raises(lib.PocrError) as e:
+            s.set_sampling(temp, top_k, 0)
+        assert e.value.code == lib.POCR_ERR_ARG
+    for top_k in (0, 65, MID.vocab):
+        with pytest.raises(lib.PocrError) as e:
+            s.set_sampling(0.7, top_k, 0)
+        assert e.value.code == lib.POCR_ERR_UNSUPPORTED
+    # the batch decodes greedily only
+    s.set_sampling(0.7, 8, 0)
+    with pytest.raises(lib.PocrError) as e:
+        lib.decode_batch([s], [1], [0], 2)
+    assert e.value.code == lib.POCR_ERR_UNSUPPORTED
