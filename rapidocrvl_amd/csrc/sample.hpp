@@ -58,11 +58,23 @@ __device__ __forceinline__ unsigned long long cand_key(float s, int row) {
 }
 
 // The threshold T such that this workgroup's nonzero keys ≥ T are its `want`
-// largest (all of them when fewer; 0 is "no key").  hist: 256 LDS counters,
-// pick: 3 LDS ints.
+// largest (all of them when fewer: T = 1; 0 is "no key").  hist: 256 LDS
+// counters, pick: 3 LDS ints.
 template <int E>
 __device__ unsigned long long radix_select(const unsigned long long (&key)[E], int want, unsigned *hist, int *pick) {
     const int tid = threadIdx.x, lane = tid & 63;
+    // nonzero keys in the workgroup
+    int mine = 0;
+#pragma unroll
+    for (int e = 0; e < E; ++e) mine += key[e] != 0ull;
+    for (int off = 32; off > 0; off >>= 1) mine += __shfl_xor(mine, off, 64);
+    if (tid == 0) pick[0] = 0;
+    __syncthreads();
+    if (lane == 0) atomicAdd(&pick[0], mine);
+    __syncthreads();
+    const int valid = pick[0];
+    __syncthreads();
+    if (valid <= want) return 1ull;
     unsigned long long prefix = 0ull, pmask = 0ull;
     int need = want;
     for (int shift = 56; shift >= 0; shift -= 8) {
@@ -70,7 +82,7 @@ __device__ unsigned long long radix_select(const unsigned long long (&key)[E], i
         __syncthreads();
 #pragma unroll
         for (int e = 0; e < E; ++e)
-            if ((key[e] & pmask) == prefix) atomicAdd(&hist[(uint32_t)(key[e] >> shift) & 255u], 1u);
+            if (key[e] != 0ull && (key[e] & pmask) == prefix) atomicAdd(&hist[(uint32_t)(key[e] >> shift) & 255u], 1u);
         __syncthreads();
         if (tid < 64) {
             // lane l holds digits 4l..4l+3; the digit whose bin contains the
@@ -159,8 +171,10 @@ __device__ __forceinline__ double rng_float64(unsigned long long &s) {
 }
 
 // sampleCandidateScoresScratch (model.go:1950-1990) over n ≥ 2 candidates
-// sorted as above; returns the candidate index.  One thread.
-static __device__ int draw_candidate(const float *sc, int n, double temp, unsigned long long &rng) {
+// sorted as above; returns the candidate index.  One thread; for n > 4, w
+// holds the weights FastExp(s − max) (temperature 1) or FastExp(s·(1/T) −
+// max·(1/T)) (otherwise), computed lane-parallel by the caller.
+static __device__ int draw_candidate(const float *sc, const float *w, int n, double temp, unsigned long long &rng) {
 #pragma clang fp contract(off)
     if (temp == 1.0) {
         float mx = sc[0];
@@ -195,11 +209,11 @@ static __device__ int draw_candidate(const float *sc, int n, double temp, unsign
         // sampleCandidateScoresTemp1Scratch (model.go:2040-2063): f32 weights
         // and sum, pickWeightedRawFloat32 (2418-2456)
         float sum = 0.0f;
-        for (int i = 0; i < n; ++i) sum += fast_exp_wrap(sc[i] - mx);
+        for (int i = 0; i < n; ++i) sum += w[i];
         const float pick = (float)rng_float64(rng) * sum;
         float acc = 0.0f;
         for (int i = 0; i < n; ++i) {
-            acc += fast_exp_wrap(sc[i] - mx);
+            acc += w[i];
             if (pick <= acc) return i;
         }
         return n - 1;
@@ -241,11 +255,11 @@ static __device__ int draw_candidate(const float *sc, int n, double temp, unsign
     // model.go:1971-1989: f64 sum of the weights, the f32-stored weights
     // summed again in f64 by pickWeightedFloat32 (2342-2416)
     double sum = 0.0;
-    for (int i = 0; i < n; ++i) sum += (double)fast_exp_wrap(sc[i] * inv - mx);
+    for (int i = 0; i < n; ++i) sum += (double)w[i];
     const double pick = rng_float64(rng) * sum;
     double acc = 0.0;
     for (int i = 0; i < n; ++i) {
-        acc += (double)fast_exp_wrap(sc[i] * inv - mx);
+        acc += (double)w[i];
         if (pick <= acc) return i;
     }
     return n - 1;
@@ -267,6 +281,7 @@ static __global__ void __launch_bounds__(kTopKThreads) k_topk_final(const unsign
     __shared__ int count;
     __shared__ unsigned long long sel[kTopKMax];
     __shared__ float csc[kTopKMax];
+    __shared__ float cw[kTopKMax];
     __shared__ int cid[kTopKMax];
     const int tid = threadIdx.x, lane = tid & 63;
     if (st && st->err) return;  // a failed step draws nothing (uniform)
@@ -303,10 +318,24 @@ static __global__ void __launch_bounds__(kTopKThreads) k_topk_final(const unsign
     }
     if (lane == 0) ss->n = n;
     if (!sample) return;
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");  // csc, cid written by the wave's lanes
+    {
+        // the draw's weights, one per lane (the maximum is lane 0's score)
+#pragma clang fp contract(off)
+        const double temp = ss->temperature;
+        const float mx0 = __shfl(score, 0, 64);
+        float wgt;
+        if (temp == 1.0) {
+            wgt = fast_exp_wrap(score - mx0);
+        } else {
+            const float inv = (float)(1.0 / temp);
+            wgt = fast_exp_wrap(score * inv - mx0 * inv);
+        }
+        if (lane < n) cw[lane] = wgt;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");  // csc, cw, cid written by the wave's lanes
     if (lane == 0) {
         unsigned long long rng = ss->rng;
-        const int c = n >= 2 ? draw_candidate(csc, n, ss->temperature, rng) : 0;
+        const int c = n >= 2 ? draw_candidate(csc, cw, n, ss->temperature, rng) : 0;
         const int tok = cid[c];
         ss->rng = rng;
         ss->token = tok;
