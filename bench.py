@@ -92,6 +92,44 @@ def build_model(ctx, cfg, qtype, seed=0):
 PREFILL_FLOPS_PER_TOKEN_LAYER = 2 * 14_155_776  # q,k,v,o,gate,up,down weights of one layer
 
 
+def projector_bench(ctx, with_cpu=True):
+    """The vision projector (mlp_AR) at PaddleOCR-VL's widths (vision 1152 →
+    4608 → 1024) on the bench image grid (1, 72, 74) → 1332 rows: device time
+    per image, useful TFLOP/s (2·rows·(4608² + 1024·4608)), and the oracle's
+    single-thread rows/s on a 6-row sample."""
+    from rapidocrvl_amd import lib
+
+    import oracle
+
+    vd, td, grid = 1152, 1024, (1, 72, 74)
+    K = 4 * vd
+    rng = np.random.default_rng(11)
+    w1 = (rng.standard_normal((K, K)) * (1.5 / np.sqrt(K))).astype(np.float32)
+    w2 = (rng.standard_normal((td, K)) * (1.0 / np.sqrt(K))).astype(np.float32)
+    nw = (1 + 0.1 * rng.standard_normal(vd)).astype(np.float32)
+    nb = (0.1 * rng.standard_normal(vd)).astype(np.float32)
+    b1 = (0.1 * rng.standard_normal(K)).astype(np.float32)
+    b2 = (0.1 * rng.standard_normal(td)).astype(np.float32)
+    proj = lib.Projector(ctx, nw, nb, w1, b1, w2, b2)
+    us = proj.time_project(grid, iters=20)
+    rows = grid[0] * (grid[1] // 2) * (grid[2] // 2)
+    flops = 2.0 * rows * (K * K + td * K)
+    res = {"workload": "vision projector, 1332 rows (grid 1x72x74), 1152->4608->1024, Q8",
+           "ms": round(us / 1e3, 3), "TFLOP_s": round(flops / (us * 1e-6) / 1e12, 1)}
+    if with_cpu:
+        sample = (1, 2, 12)  # 6 rows
+        x = rng.standard_normal((12 * 2, vd)).astype(np.float32)
+        q1 = lib.quantize_rows(lib.Q8, w1)
+        q2 = lib.quantize_rows(lib.Q8, w2)
+        t = time.perf_counter()
+        oracle.project_image(x, sample, nw, nb, q1, b1, q2, b2)
+        dt = time.perf_counter() - t
+        res["cpu_oracle_rows_s"] = round(6 / dt, 1)
+        res["cpu_oracle_threads"] = 1
+    proj.close()
+    return res
+
+
 def prefill_flops(cfg, n):
     """Linear layers 2·N·weights, causal attention 2·(QKᵀ + PV) = 4·dim·N(N+1)/2
     per head and layer, LM head on the last token."""
@@ -327,6 +365,7 @@ def main():
     ap.add_argument("--prefill-only", action="store_true", help="time only the 1345-token Q4 image prefill")
     ap.add_argument("--no-batch", action="store_true", help="skip the 4-sequence batched decode")
     ap.add_argument("--batch-only", action="store_true", help="time only the 4-sequence Q4 batched decode")
+    ap.add_argument("--projector-only", action="store_true", help="time only the vision projector")
     ap.add_argument("--batch-tokens", type=int, default=1024, help="tokens per sequence of the batched decode")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -341,6 +380,9 @@ def main():
     from rapidocrvl_amd.config import ERNIE_0P3B as cfg
 
     ctx = lib.Context(0)
+    if args.projector_only:
+        print(json.dumps(projector_bench(ctx, with_cpu=not args.no_cpu)), flush=True)
+        return
     if args.batch_only:
         _, model = build_model(ctx, cfg, lib.Q4)
         print(json.dumps({"workload": "4-sequence q4 batched greedy decode",
@@ -410,6 +452,8 @@ def main():
         log(f"[bench] 4-sequence batched decode q6 {extra['batch4_decode']['q6']}")
         del m6
 
+    extra["projector"] = projector_bench(ctx, with_cpu=not args.no_cpu)
+    log(f"[bench] projector {extra['projector']}")
     if not args.no_sweep:
         extra["gemv_sweep"] = gemv_sweep(ctx, np.random.default_rng(0))
         extra["attention_sweep"] = attention_sweep(ctx, cfg)

@@ -69,6 +69,7 @@ typedef struct pocr_ctx pocr_ctx;
 typedef struct pocr_weight pocr_weight;
 typedef struct pocr_model pocr_model;
 typedef struct pocr_seq pocr_seq;
+typedef struct pocr_projector pocr_projector;
 
 /* decoder hyper-parameters (internal/config/config.go:31-49).  Unlike the
  * reference loader (internal/model/model.go:647-653) heads*head_dim may
@@ -261,6 +262,37 @@ int pocr_decode_batch(pocr_seq *const *seqs, int n_seq, const int32_t *first_tok
 int pocr_generate(pocr_seq *s, const int32_t *ids, int n_ids, const float *image_embeds, int n_image,
                   int32_t image_token_id, const int32_t grid[3], int32_t merge, int max_new,
                   const int32_t *eos, int n_eos, int use_prefill, int32_t *out_tokens);
+
+/* ---------------- vision projector ---------------- */
+/* mlp_AR of the vision tower (internal/model/vision.go:224-302): pre_norm
+ * LayerNorm over vision_dim, linear_1 w1 [4·vd][4·vd] + b1, GELU(tanh),
+ * linear_2 w2 [text_dim][4·vd] + b2, f32 row-major.  Both matrices are
+ * quantized to Q8 rows here, as cacheVisionWeights does (vision.go:286-302).
+ * 4·vision_dim a multiple of 128 and <= 8192, text_dim a multiple of 64;
+ * POCR_ERR_UNSUPPORTED otherwise. */
+int pocr_projector_create(pocr_ctx *ctx, int vision_dim, int text_dim, const float *norm_w, const float *norm_b,
+                          const float *w1, const float *b1, const float *w2, const float *b2, float eps,
+                          pocr_projector **out);
+void pocr_projector_destroy(pocr_projector *p);
+/* projectImage (vision.go:1029-1108; the op behind VulkanProjectImageF32,
+ * internal/backend/vulkan_exec_stub.go:122, with the runtime's Q8 weights):
+ * vision-encoder rows [T·H·W][vision_dim] (frame-major, then row, column) →
+ * one row [text_dim] per 2×2 block, T·(H/2)·(W/2) of them, frame-major.
+ * Returns the row count. */
+int pocr_project_image(pocr_projector *p, const float *vision_rows, int grid_t, int grid_h, int grid_w,
+                       float *out);
+/* image generation from vision-encoder rows (EncodeImageWithGrid's
+ * projection, vision.go:146, feeding generateWithImageEmbeds, model.go:
+ * 1618-1711): the rows are projected on the device straight into the
+ * prompt's image rows (placeholders = T·(H/2)·(W/2), merge 2), then as
+ * pocr_generate with use_prefill=1.  grid = (T, H, W) of vision patches;
+ * the projector belongs to the sequence's context. */
+int pocr_generate_vision(pocr_seq *s, pocr_projector *proj, const int32_t *ids, int n_ids,
+                         const float *vision_rows, int32_t image_token_id, const int32_t grid[3], int max_new,
+                         const int32_t *eos, int n_eos, int32_t *out_tokens);
+/* device time of one projection of a T·H·W grid (rows resident, HIP events
+ * over `iters` back-to-back runs): the bench's measurement hook */
+int pocr_time_project(pocr_projector *p, int grid_t, int grid_h, int grid_w, int iters, float *avg_us);
 
 /* multimodal RoPE positions (internal/model/model.go:1717-1783), host only.
  * Returns the number of positions written, rope_delta via pointer. */

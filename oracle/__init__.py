@@ -87,6 +87,11 @@ def lib():
         L.orc_generate_sampled.argtypes = [C.c_void_p, _i32p, C.c_int, C.c_void_p, C.c_int, C.c_int, _i32p,
                                            C.c_int, C.c_int, _i32p, C.c_int, C.c_double, C.c_int, C.c_uint64,
                                            _i32p]
+        L.orc_layernorm.argtypes = [_f32p, _f32p, _f32p, _f32p, C.c_int, C.c_float]
+        L.orc_gelu_tanh.restype = C.c_float
+        L.orc_gelu_tanh.argtypes = [C.c_float]
+        L.orc_project_image.argtypes = [_f32p, C.c_int, C.c_int, C.c_int, C.c_int, _f32p, _f32p, C.c_void_p, _f32p,
+                                        C.c_void_p, _f32p, C.c_float, _f32p]
         L.orc_rng_float64.restype = C.c_double
         L.orc_rng_float64.argtypes = [C.POINTER(C.c_uint64)]
         L.orc_topk.argtypes = [_f32p, C.c_int, C.c_int, _i32p, _f32p]
@@ -100,6 +105,36 @@ def lib():
 
 def _f32(a):
     return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def layernorm(x, w, b, eps=1e-5):
+    """LayerNorm (ops.go:1060-1097), scalar-path order."""
+    x = _f32(x)
+    out = np.zeros_like(x)
+    lib().orc_layernorm(out, x, _f32(w), _f32(b), x.size, eps)
+    return out
+
+
+def gelu_tanh(x):
+    """GELUTanh (ops.go:1140-1164) elementwise."""
+    return np.array([lib().orc_gelu_tanh(float(v)) for v in np.ravel(_f32(x))], np.float32).reshape(np.shape(x))
+
+
+def project_image(x, grid, norm_w, norm_b, q1, b1, q2, b2, eps=1e-5):
+    """projectImageRows (vision.go:1066-1108) with Q8 matrices q = (scales, packed)."""
+    x = _f32(x)
+    t, h, w = grid
+    vd = _f32(norm_w).size
+    K = 4 * vd
+    s1, d1 = _f32(q1[0]), np.ascontiguousarray(q1[1], np.uint8)
+    s2, d2 = _f32(q2[0]), np.ascontiguousarray(q2[1], np.uint8)
+    m1 = _QMat(Q8, s1.size, K, s1.ctypes.data, d1.ctypes.data)
+    m2 = _QMat(Q8, s2.size, K, s2.ctypes.data, d2.ctypes.data)
+    rows = t * (h // 2) * (w // 2)
+    out = np.zeros((max(rows, 1), s2.size), np.float32)
+    n = lib().orc_project_image(x, t, h, w, vd, _f32(norm_w), _f32(norm_b), C.byref(m1), _f32(b1), C.byref(m2),
+                                _f32(b2), eps, out)
+    return out[:n]
 
 
 class Rng:

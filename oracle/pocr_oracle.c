@@ -991,6 +991,87 @@ static int is_eos(int id, const int32_t *eos, int n) {
     return 0;
 }
 
+/* ---- vision projector ---- */
+
+/* sumF32Scalar (ops.go:1448-1466) */
+static float sum8(const float *x, int n) {
+    float s[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    int i = 0;
+    for (; i + 7 < n; i += 8)
+        for (int k = 0; k < 8; k++) s[k] += x[i + k];
+    float sum = (s[0] + s[1]) + (s[2] + s[3]) + (s[4] + s[5]) + (s[6] + s[7]);
+    for (; i < n; i++) sum += x[i];
+    return sum;
+}
+
+/* sumSquaresCenteredScalar (ops.go:1468-1490) */
+static float sum_sq_centered8(const float *x, int n, float mean) {
+    float s[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    int i = 0;
+    for (; i + 7 < n; i += 8)
+        for (int k = 0; k < 8; k++) {
+            const float d = x[i + k] - mean;
+            s[k] += d * d;
+        }
+    float v = (s[0] + s[1]) + (s[2] + s[3]) + (s[4] + s[5]) + (s[6] + s[7]);
+    for (; i < n; i++) {
+        const float d = x[i] - mean;
+        v += d * d;
+    }
+    return v;
+}
+
+void orc_layernorm(float *out, const float *x, const float *w, const float *b, int n, float eps) {
+    const float mean = sum8(x, n) / (float)n;
+    const float var = sum_sq_centered8(x, n, mean);
+    const float scale = orc_fast_rsqrt(var / (float)n + eps);
+    for (int i = 0; i < n; i++) out[i] = (x[i] - mean) * scale * w[i] + b[i];
+}
+
+/* fastExpF32T (ops.go:1152-1164) */
+static float fast_exp2_t(float x) {
+    const float magic = 12582912.0f;
+    int32_t n = (int32_t)((x + magic) - magic);
+    float f = x - (float)n;
+    float f2 = f * f;
+    float poly = (1.0f + 0.6931471824645996f * f) +
+                 f2 * (0.24022650718688965f + 0.05550410971045494f * f +
+                       f2 * (0.009618128649890423f + 0.0013352063251659274f * f));
+    return bits_to_f32(f32_to_bits(poly) + ((uint32_t)n << 23));
+}
+
+float orc_gelu_tanh(float x) {
+    /* ops.go:1140-1150; the constants are the exact products rounded once */
+    const float c1 = 0x1.26aec2p+1f;
+    const float c3 = 0x1.a5a7dp-4f;
+    const float x3 = x * (x * x);
+    const float e = fast_exp2_t(c1 * x + c3 * x3);
+    const float th = (e - 1.0f) / (e + 1.0f);
+    return 0.5f * x * (1.0f + th);
+}
+
+int orc_project_image(const float *x, int grid_t, int grid_h, int grid_w, int vd, const float *norm_w,
+                      const float *norm_b, const orc_qmat *q1, const float *b1, const orc_qmat *q2, const float *b2,
+                      float eps, float *out) {
+    const int bw = grid_w / 2, bh = grid_h / 2, rows = grid_t * bh * bw, K = 4 * vd, td = q2->rows;
+    float *merged = (float *)malloc(sizeof(float) * (size_t)K);
+    float *hid = (float *)malloc(sizeof(float) * (size_t)K);
+    for (int row = 0; row < rows; row++) {
+        const int t = row / (bh * bw), local = row - t * bh * bw, by = local / bw, bx = local - by * bw;
+        const int base = t * grid_h * grid_w + by * 2 * grid_w + bx * 2;
+        const int src[4] = {base, base + 1, base + grid_w, base + grid_w + 1};
+        for (int q = 0; q < 4; q++) orc_layernorm(merged + q * vd, x + (size_t)src[q] * vd, norm_w, norm_b, vd, eps);
+        orc_matvec(q1, merged, hid); /* dotQ8·scale */
+        for (int i = 0; i < K; i++) hid[i] = orc_gelu_tanh(hid[i] + b1[i]);
+        float *o = out + (size_t)row * td;
+        orc_matvec(q2, hid, o);
+        for (int i = 0; i < td; i++) o[i] = o[i] + b2[i];
+    }
+    free(merged);
+    free(hid);
+    return rows;
+}
+
 /* ---- sampling LM head ---- */
 
 double orc_rng_float64(uint64_t *state) {

@@ -36,46 +36,49 @@ struct DigitizeParams {
     int x_stride;
     const float *norm_w;   // null → no RMSNorm
     float eps;
-    int K;                 // multiple of 16, ≤ 4096
+    int K;                 // multiple of 16, ≤ 8192
     int8_t *xd;            // planes [3][npad][K]
     size_t plane_stride;   // npad·K
     float *xs;             // [n] row scale
     int *xb;               // [n][4] Σd per plane (4th unused)
 };
 
-template <int QT>
+template <int QT, int G>
 static __global__ void __launch_bounds__(kThreads) k_digitize(DigitizeParams p) {
+    // G 16-column groups per thread: K ≤ 4096·G
     __shared__ float red[kWaves];
     __shared__ int redi[3][kWaves];
     const int n = blockIdx.x;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    const int c0 = 16 * t;  // this thread's 16-column group
-    const bool valid = c0 < p.K;
-    const int cl = valid ? c0 : p.K - 16;  // clamped, never written
-    const float *xr = p.x + (size_t)n * p.x_stride + cl;
-    float y[16], w[16];
+    float y[G][16];
+    bool valid[G];
+    int c0[G];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const float4 v = reinterpret_cast<const float4 *>(xr)[i];
-        y[4 * i] = v.x;
-        y[4 * i + 1] = v.y;
-        y[4 * i + 2] = v.z;
-        y[4 * i + 3] = v.w;
+    for (int g = 0; g < G; ++g) {
+        c0[g] = 16 * (t + g * kThreads);  // this thread's 16-column groups
+        valid[g] = c0[g] < p.K;
+        const int cl = valid[g] ? c0[g] : p.K - 16;  // clamped, never written
+        const float *xr = p.x + (size_t)n * p.x_stride + cl;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float4 v = reinterpret_cast<const float4 *>(xr)[i];
+            y[g][4 * i] = v.x;
+            y[g][4 * i + 1] = v.y;
+            y[g][4 * i + 2] = v.z;
+            y[g][4 * i + 3] = v.w;
+        }
     }
     float factor = 1.0f;
     if (p.norm_w) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float4 v = reinterpret_cast<const float4 *>(p.norm_w + cl)[i];
-            w[4 * i] = v.x;
-            w[4 * i + 1] = v.y;
-            w[4 * i + 2] = v.z;
-            w[4 * i + 3] = v.w;
-        }
         float ss = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) ss = fmaf(y[i], y[i], ss);
-        ss = wave_sum(valid ? ss : 0.0f);
+        for (int g = 0; g < G; ++g) {
+            float sg = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) sg = fmaf(y[g][i], y[g][i], sg);
+            ss += valid[g] ? sg : 0.0f;
+        }
+        ss = wave_sum(ss);
         if (lane == 0) red[wave] = ss;
         __syncthreads();
         float tot = red[0];
@@ -83,13 +86,28 @@ static __global__ void __launch_bounds__(kThreads) k_digitize(DigitizeParams p) 
         for (int k = 1; k < kWaves; ++k) tot += red[k];
         factor = fast_rsqrt_ref(tot / (float)p.K + p.eps);
 #pragma unroll
-        for (int i = 0; i < 16; ++i) y[i] = y[i] * w[i];  // a lone product: nothing to contract
+        for (int g = 0; g < G; ++g) {
+            const int cl = valid[g] ? c0[g] : p.K - 16;
+            float w[16];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float4 v = reinterpret_cast<const float4 *>(p.norm_w + cl)[i];
+                w[4 * i] = v.x;
+                w[4 * i + 1] = v.y;
+                w[4 * i + 2] = v.z;
+                w[4 * i + 3] = v.w;
+            }
+#pragma unroll
+            for (int i = 0; i < 16; ++i) y[g][i] = y[g][i] * w[i];  // a lone product: nothing to contract
+        }
         __syncthreads();  // red is reused below
     }
     float m = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) m = fmaxf(m, fabsf(y[i]));
-    m = wave_max(valid ? m : 0.0f);
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) m = valid[g] ? fmaxf(m, fabsf(y[g][i])) : m;
+    m = wave_max(m);
     if (lane == 0) red[wave] = m;
     __syncthreads();
     m = red[0];
@@ -99,35 +117,42 @@ static __global__ void __launch_bounds__(kThreads) k_digitize(DigitizeParams p) 
     (void)frexpf(m * (1.0f / 127.0f), &ex);  // m/127 < 2^ex
     const float inv = m > 0.0f ? ldexpf(1.0f, -ex) : 1.0f;
     const float S = m > 0.0f ? ldexpf(1.0f, ex) : 1.0f;
-    int d[3][16];  // digit of K position pos (the group's shared order)
     int sd[3] = {0, 0, 0};
 #pragma unroll
-    for (int c = 0; c < 16; ++c) {
-        const float tt = y[c] * inv;  // exact: inv is a power of two
-        const float a = rintf(tt);
-        const float t1 = (tt - a) * 128.0f;
-        const float b = rintf(t1);
-        const int d2 = (int)rintf((t1 - b) * 128.0f);
-        const int pos = digit_pos16<QT>(c);
-        d[0][pos] = (int)a;
-        d[1][pos] = (int)b;
-        d[2][pos] = d2;
-        sd[0] += (int)a;
-        sd[1] += (int)b;
-        sd[2] += d2;
-    }
-    if (valid) {
+    for (int g = 0; g < G; ++g) {
+        int d[3][16];  // digit of K position pos (the group's shared order)
+        int sg[3] = {0, 0, 0};
 #pragma unroll
-        for (int pl = 0; pl < 3; ++pl)
-            *reinterpret_cast<int4 *>(p.xd + pl * p.plane_stride + (size_t)n * p.K + c0) =
-                make_int4(pack4(d[pl][0], d[pl][1], d[pl][2], d[pl][3]), pack4(d[pl][4], d[pl][5], d[pl][6], d[pl][7]),
-                          pack4(d[pl][8], d[pl][9], d[pl][10], d[pl][11]),
-                          pack4(d[pl][12], d[pl][13], d[pl][14], d[pl][15]));
+        for (int c = 0; c < 16; ++c) {
+            const float tt = y[g][c] * inv;  // exact: inv is a power of two
+            const float a = rintf(tt);
+            const float t1 = (tt - a) * 128.0f;
+            const float b = rintf(t1);
+            const int d2 = (int)rintf((t1 - b) * 128.0f);
+            const int pos = digit_pos16<QT>(c);
+            d[0][pos] = (int)a;
+            d[1][pos] = (int)b;
+            d[2][pos] = d2;
+            sg[0] += (int)a;
+            sg[1] += (int)b;
+            sg[2] += d2;
+        }
+        if (valid[g]) {
+#pragma unroll
+            for (int pl = 0; pl < 3; ++pl) {
+                *reinterpret_cast<int4 *>(p.xd + pl * p.plane_stride + (size_t)n * p.K + c0[g]) =
+                    make_int4(pack4(d[pl][0], d[pl][1], d[pl][2], d[pl][3]),
+                              pack4(d[pl][4], d[pl][5], d[pl][6], d[pl][7]),
+                              pack4(d[pl][8], d[pl][9], d[pl][10], d[pl][11]),
+                              pack4(d[pl][12], d[pl][13], d[pl][14], d[pl][15]));
+                sd[pl] += sg[pl];
+            }
+        }
     }
     __syncthreads();
 #pragma unroll
     for (int pl = 0; pl < 3; ++pl) {
-        const int s = (int)wave_sum((float)(valid ? sd[pl] : 0));  // |Σ| ≤ 4096·127: exact in f32
+        const int s = (int)wave_sum((float)sd[pl]);  // |Σ| ≤ 8192·127: exact in f32
         if (lane == 0) redi[pl][wave] = s;
     }
     __syncthreads();
@@ -147,7 +172,7 @@ static __global__ void __launch_bounds__(kThreads) k_digitize(DigitizeParams p) 
 // Rows come from up to three matrices (segments, as the fused QKV GEMV) or,
 // with NMAT = 2, from two matrices side by side (gate and up).
 // ---------------------------------------------------------------------------
-enum : int { G_PLAIN = 0, G_SWIGLU = 1, G_OPROJ = 2, G_DOWN = 3 };
+enum : int { G_PLAIN = 0, G_SWIGLU = 1, G_OPROJ = 2, G_DOWN = 3, G_BIAS = 4, G_BIAS_GELU = 5 };
 
 struct GemmParams {
     DevMat m[3];
@@ -166,6 +191,7 @@ struct GemmParams {
     int quirk;             // OPROJ: Q4/Q6 residual behaviour
     int clen0;             // cache rows before token 0
     int last;              // DOWN: last layer → vbuf = h + y (h untouched)
+    const float *bias;     // BIAS / BIAS_GELU: [rows]
 };
 
 // 16 weight codes of row `row` at columns k..k+15 (k multiple of 16) as the
@@ -204,6 +230,24 @@ template <int NMAT>
 __device__ __forceinline__ void gemm_store_y(const GemmParams &p, int epi, int n, int rr, const float (&y)[NMAT][4]) {
     if (epi == G_PLAIN) {
         *reinterpret_cast<float4 *>(p.out + (size_t)n * p.out_stride + rr) = make_float4(y[0][0], y[0][1], y[0][2], y[0][3]);
+    } else if (epi == G_BIAS || epi == G_BIAS_GELU) {
+        // matVecQ8BiasSerial (quant.go:1469-1472): y·scale + bias, then
+        // GELUTanhInPlace over the row (ops.go:1166-1177) for the first
+        // projector matrix
+        const float4 bv = *reinterpret_cast<const float4 *>(p.bias + rr);
+        float o[4];
+        {
+#pragma clang fp contract(off)
+            o[0] = y[0][0] + bv.x;
+            o[1] = y[0][1] + bv.y;
+            o[2] = y[0][2] + bv.z;
+            o[3] = y[0][3] + bv.w;
+        }
+        if (epi == G_BIAS_GELU) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) o[i] = gelu_tanh_ref(o[i]);
+        }
+        *reinterpret_cast<float4 *>(p.out + (size_t)n * p.out_stride + rr) = make_float4(o[0], o[1], o[2], o[3]);
     } else if (epi == G_SWIGLU) {
         float o[4];
 #pragma unroll

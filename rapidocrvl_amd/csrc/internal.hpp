@@ -165,7 +165,7 @@ int prefill_locked(pocr_seq *s, int n, const float *emb, const int32_t *pos3, fl
 // text rows gathered from the device embedding table; POCR_ERR_UNSUPPORTED
 // (no error recorded) when the model's shapes need the token-by-token path
 int prefill_ids_locked(pocr_seq *s, const int32_t *ids, int n, const float *image, int32_t image_token,
-                       const int32_t *pos3, float *logits, int32_t *token);
+                       const int32_t *pos3, float *logits, int32_t *token, bool image_on_device = false);
 // host → device copy through the context's pinned staging (stream-ordered)
 int upload_staged(pocr_ctx *ctx, void *dst, const void *src, size_t bytes);
 int batched_gemv(pocr_ctx *ctx, const DevMat &w, const float *x, int m, float *out);
@@ -178,5 +178,21 @@ int seq_set_state(pocr_seq *s, int len);
 // sampling head (logits, top-k, one draw into argmax slot 0) when the
 // sequence samples
 int enqueue_lm_head(pocr_seq *s, const float *x, bool want_logits);
+// batched building blocks (prefill.hip): digit planes of n rows, and the
+// MFMA GEMM over them (npad = n rounded up to 32 tokens)
+struct DigitizeParams;
+struct GemmParams;
+int digitize_rows(hipStream_t s, int qtype, const DigitizeParams &p, int n);
+int gemm_rows(hipStream_t s, int qtype, int nmat, const GemmParams &p, int epi, int npad);
+// vision projector (projector.hip); callers hold the context lock
+int project_locked(pocr_projector *p, int grid_t, int grid_h, int grid_w, int *rows);
+int project_upload_locked(pocr_projector *p, const float *vision_rows, int grid_t, int grid_h, int grid_w,
+                          const float **out_dev, int *rows);
+int projector_text_dim(const pocr_projector *p);
+pocr_ctx *projector_ctx(const pocr_projector *p);
+// pocr_generate under the context lock, image rows from the host or (image_dev) the device
+int generate_locked(pocr_seq *s, const int32_t *ids, int n_ids, const float *image, bool image_dev, int n_image,
+                    int32_t image_token_id, const int32_t grid[3], int32_t merge, int max_new, const int32_t *eos,
+                    int n_eos, int use_prefill, int32_t *out_tokens);
 constexpr int kBigGrid = 1024;
 }  // namespace pocr

@@ -93,6 +93,33 @@ __device__ __forceinline__ float silu_ref(float x) {
     return x / (1.0f + fast_exp_ref(-x));
 }
 
+// fastExpF32T (ops.go:1152-1164): 2^x for x already scaled by log2(e); the
+// exponent add wraps outside about ±127 exactly as in the reference
+__device__ __forceinline__ float fast_exp2_wrap(float x) {
+#pragma clang fp contract(off)
+    const float magic = 12582912.0f;
+    const int32_t n = (int32_t)((x + magic) - magic);
+    const float f = x - (float)n;
+    const float f2 = f * f;
+    const float poly = (1.0f + 0.6931471824645996f * f) +
+                       f2 * (0.24022650718688965f + 0.05550410971045494f * f +
+                             f2 * (0.009618128649890423f + 0.0013352063251659274f * f));
+    return __uint_as_float(__float_as_uint(poly) + ((uint32_t)n << 23));
+}
+
+// GELUTanh (ops.go:1140-1150): 0.5·x·(1 + tanh(√(2/π)(x + 0.044715x³))) with
+// tanh = (e−1)/(e+1), e = 2^(x·2c·log2e + x³·2ck·log2e); the two constants
+// are the reference's exact products rounded once to f32
+__device__ __forceinline__ float gelu_tanh_ref(float x) {
+#pragma clang fp contract(off)
+    const float c1 = 0x1.26aec2p+1f;  // 2·0.7978845608028654·1.4426950408889634
+    const float c3 = 0x1.a5a7dp-4f;   // 2·0.7978845608028654·0.044715·1.4426950408889634
+    const float x3 = x * (x * x);
+    const float e = fast_exp2_wrap(c1 * x + c3 * x3);
+    const float th = (e - 1.0f) / (e + 1.0f);
+    return 0.5f * x * (1.0f + th);
+}
+
 // ---------------------------------------------------------------------------
 // code decode: chunk of packed bytes → Σ u·x with unsigned codes u; the signed
 // value is u − BIAS, folded as −BIAS·Σx once per lane.

@@ -1800,6 +1800,15 @@ extern "C" int pocr_generate(pocr_seq *s, const int32_t *ids, int n_ids, const f
     if (max_new <= 0) return 0;
     RC(model_ready(s->m));
     CHECK_INJECT("generate");
+    std::lock_guard<std::mutex> lk(s->m->ctx->mu);
+    HIP_TRY(hipSetDevice(s->m->ctx->device));
+    return generate_locked(s, ids, n_ids, image_embeds, false, n_image, image_token_id, grid, merge, max_new, eos,
+                           n_eos, use_prefill, out_tokens);
+}
+
+int pocr::generate_locked(pocr_seq *s, const int32_t *ids, int n_ids, const float *image_embeds, bool image_dev,
+                          int n_image, int32_t image_token_id, const int32_t grid[3], int32_t merge, int max_new,
+                          const int32_t *eos, int n_eos, int use_prefill, int32_t *out_tokens) {
     pocr_model *m = s->m;
     const int H = m->cfg.hidden;
     // positions (model.go:1717-1783) and embeddings (tokenEmbeddingInto 3251 /
@@ -1819,41 +1828,66 @@ extern "C" int pocr_generate(pocr_seq *s, const int32_t *ids, int n_ids, const f
     }
     if (n_placeholders != n_image)
         return fail(POCR_ERR_ARG, "image placeholder tokens: got %d need %d", n_placeholders, n_image);
-    std::vector<float> emb;
-    int img = 0;
-    {
-        std::lock_guard<std::mutex> lk(m->ctx->mu);
-        HIP_TRY(hipSetDevice(m->ctx->device));
-        RC(seq_set_state(s, 0));
-        if (n_ids + max_new - 1 > s->cap) return fail(POCR_ERR_ARG, "pocr_generate: capacity %d too small", s->cap);
-        if (s->sampling) RC(seed_sampler(s));  // one generator per generation call
-        int32_t next = -1;
-        if (use_prefill) {
-            const int rc = prefill_ids_locked(s, ids, n_ids, n_image > 0 ? image_embeds : nullptr,
-                                              n_image > 0 ? image_token_id : -1, pos.data(), nullptr, &next);
-            if (rc == POCR_OK) return decode_locked(s, next, n_ids + rope_delta, max_new, eos, n_eos, out_tokens);
-            if (rc != POCR_ERR_UNSUPPORTED) return rc;
-        }
-        emb.resize((size_t)n_ids * H);
-        for (int i = 0; i < n_ids; ++i) {
-            if (n_image > 0 && ids[i] == image_token_id) {
-                if (img >= n_image) return fail(POCR_ERR_ARG, "too many image placeholder tokens");
-                std::memcpy(&emb[(size_t)i * H], image_embeds + (size_t)img * H, (size_t)H * 4);
-                ++img;
-            } else {
-                if (ids[i] < 0 || ids[i] >= m->cfg.vocab) return fail(POCR_ERR_ARG, "token id %d outside vocab", ids[i]);
-                HIP_TRY(hipMemcpy(&emb[(size_t)i * H], m->embed + (size_t)ids[i] * H, (size_t)H * 4,
-                                  hipMemcpyDeviceToHost));
-            }
-        }
-        if (use_prefill) {
-            RC(prefill_locked(s, n_ids, emb.data(), pos.data(), nullptr, &next));
-        } else {
-            for (int i = 0; i < n_ids; ++i)
-                RC(step_locked(s, &emb[(size_t)i * H], &pos[3 * i], i == n_ids - 1, nullptr,
-                               i == n_ids - 1 ? &next : nullptr));
-        }
-        // first decode token sits at position len(out)-1+ropeDelta = n_ids+rope_delta
-        return decode_locked(s, next, n_ids + rope_delta, max_new, eos, n_eos, out_tokens);
+    RC(seq_set_state(s, 0));
+    if (n_ids + max_new - 1 > s->cap) return fail(POCR_ERR_ARG, "pocr_generate: capacity %d too small", s->cap);
+    if (s->sampling) RC(seed_sampler(s));  // one generator per generation call
+    int32_t next = -1;
+    if (use_prefill) {
+        const int rc = prefill_ids_locked(s, ids, n_ids, n_image > 0 ? image_embeds : nullptr,
+                                          n_image > 0 ? image_token_id : -1, pos.data(), nullptr, &next, image_dev);
+        if (rc == POCR_OK) return decode_locked(s, next, n_ids + rope_delta, max_new, eos, n_eos, out_tokens);
+        if (rc != POCR_ERR_UNSUPPORTED) return rc;
     }
+    // token-by-token or host-assembled prompt: image rows on the host
+    std::vector<float> host_img;
+    if (image_dev && n_image > 0) {
+        host_img.resize((size_t)n_image * H);
+        HIP_TRY(hipMemcpyAsync(host_img.data(), image_embeds, host_img.size() * 4, hipMemcpyDeviceToHost,
+                               m->ctx->stream));
+        HIP_TRY(hipStreamSynchronize(m->ctx->stream));
+        image_embeds = host_img.data();
+    }
+    std::vector<float> emb((size_t)n_ids * H);
+    int img = 0;
+    for (int i = 0; i < n_ids; ++i) {
+        if (n_image > 0 && ids[i] == image_token_id) {
+            if (img >= n_image) return fail(POCR_ERR_ARG, "too many image placeholder tokens");
+            std::memcpy(&emb[(size_t)i * H], image_embeds + (size_t)img * H, (size_t)H * 4);
+            ++img;
+        } else {
+            HIP_TRY(hipMemcpy(&emb[(size_t)i * H], m->embed + (size_t)ids[i] * H, (size_t)H * 4,
+                              hipMemcpyDeviceToHost));
+        }
+    }
+    if (use_prefill) {
+        RC(prefill_locked(s, n_ids, emb.data(), pos.data(), nullptr, &next));
+    } else {
+        for (int i = 0; i < n_ids; ++i)
+            RC(step_locked(s, &emb[(size_t)i * H], &pos[3 * i], i == n_ids - 1, nullptr,
+                           i == n_ids - 1 ? &next : nullptr));
+    }
+    // first decode token sits at position len(out)-1+ropeDelta = n_ids+rope_delta
+    return decode_locked(s, next, n_ids + rope_delta, max_new, eos, n_eos, out_tokens);
+}
+
+extern "C" int pocr_generate_vision(pocr_seq *s, pocr_projector *proj, const int32_t *ids, int n_ids,
+                                    const float *vision_rows, int32_t image_token_id, const int32_t grid[3],
+                                    int max_new, const int32_t *eos, int n_eos, int32_t *out_tokens) {
+    if (!s || !proj || !ids || n_ids <= 0 || !out_tokens || !vision_rows || !grid || grid[0] <= 0 || grid[1] <= 0 ||
+        grid[2] <= 0)
+        return fail(POCR_ERR_ARG, "pocr_generate_vision: bad arguments");
+    if (projector_ctx(proj) != s->m->ctx) return fail(POCR_ERR_ARG, "pocr_generate_vision: projector of another context");
+    if (projector_text_dim(proj) != s->m->cfg.hidden)
+        return fail(POCR_ERR_ARG, "pocr_generate_vision: projector width %d, model hidden %d",
+                    projector_text_dim(proj), s->m->cfg.hidden);
+    if (max_new <= 0) return 0;
+    RC(model_ready(s->m));
+    CHECK_INJECT("generate");
+    std::lock_guard<std::mutex> lk(s->m->ctx->mu);
+    HIP_TRY(hipSetDevice(s->m->ctx->device));
+    const float *rows_dev = nullptr;
+    int n_image = 0;
+    RC(project_upload_locked(proj, vision_rows, grid[0], grid[1], grid[2], &rows_dev, &n_image));
+    return generate_locked(s, ids, n_ids, rows_dev, true, n_image, image_token_id, grid, 2, max_new, eos, n_eos, 1,
+                           out_tokens);
 }

@@ -18,15 +18,21 @@ int round_up(int x, int m) { return (x + m - 1) / m * m; }
 // the MFMA GEMM takes rows in whole 64-row wave tiles and K in 64-column steps
 bool gemm_shape_ok(int rows, int K) { return rows % kGemmWaveRows == 0 && K % kGemmK == 0 && K <= kMaxCols; }
 
-int launch_digitize(hipStream_t s, int qtype, const DigitizeParams &p, int n) {
+template <int G>
+int launch_digitize_g(hipStream_t s, int qtype, const DigitizeParams &p, int n) {
     switch (qtype) {
-    case QT_Q8: hipLaunchKernelGGL(k_digitize<QT_Q8>, dim3(n), dim3(kThreads), 0, s, p); break;
-    case QT_Q4: hipLaunchKernelGGL(k_digitize<QT_Q4>, dim3(n), dim3(kThreads), 0, s, p); break;
-    case QT_Q6: hipLaunchKernelGGL(k_digitize<QT_Q6>, dim3(n), dim3(kThreads), 0, s, p); break;
+    case QT_Q8: hipLaunchKernelGGL((k_digitize<QT_Q8, G>), dim3(n), dim3(kThreads), 0, s, p); break;
+    case QT_Q4: hipLaunchKernelGGL((k_digitize<QT_Q4, G>), dim3(n), dim3(kThreads), 0, s, p); break;
+    case QT_Q6: hipLaunchKernelGGL((k_digitize<QT_Q6, G>), dim3(n), dim3(kThreads), 0, s, p); break;
     default: return fail(POCR_ERR_UNSUPPORTED, "digitize: qtype %d", qtype);
     }
     HIP_TRY(hipGetLastError());
     return POCR_OK;
+}
+
+int launch_digitize(hipStream_t s, int qtype, const DigitizeParams &p, int n) {
+    if (p.K % 16 || p.K > 2 * 16 * kThreads) return fail(POCR_ERR_UNSUPPORTED, "digitize: K %d", p.K);
+    return p.K > 16 * kThreads ? launch_digitize_g<2>(s, qtype, p, n) : launch_digitize_g<1>(s, qtype, p, n);
 }
 
 template <int NMAT, int TN>
@@ -245,7 +251,7 @@ int prefill_locked(pocr_seq *s, int n, const float *emb, const int32_t *pos3, fl
 }
 
 int prefill_ids_locked(pocr_seq *s, const int32_t *ids, int n, const float *image, int32_t image_token,
-                       const int32_t *pos3, float *logits, int32_t *token) {
+                       const int32_t *pos3, float *logits, int32_t *token, bool image_on_device) {
     pocr_model *m = s->m;
     if (!batched_prefill_on(m) || m->cfg.hidden % 4) return POCR_ERR_UNSUPPORTED;
     if (s->len + n > s->cap) return fail(POCR_ERR_ARG, "prefill: %d rows exceed capacity", n);
@@ -261,7 +267,11 @@ int prefill_ids_locked(pocr_seq *s, const int32_t *ids, int n, const float *imag
         }
         int j = i;
         while (j < n && ids[j] == image_token) ++j;
-        RC(upload_staged(m->ctx, b.h + (size_t)i * H, image + (size_t)img * H, (size_t)(j - i) * H * 4));
+        if (image_on_device)
+            HIP_TRY(hipMemcpyAsync(b.h + (size_t)i * H, image + (size_t)img * H, (size_t)(j - i) * H * 4,
+                                   hipMemcpyDeviceToDevice, m->ctx->stream));
+        else
+            RC(upload_staged(m->ctx, b.h + (size_t)i * H, image + (size_t)img * H, (size_t)(j - i) * H * 4));
         img += j - i;
         i = j;
     }
@@ -391,5 +401,10 @@ int prefill_run(pocr_seq *s, int n, const int32_t *pos3, float *logits, int32_t 
 }
 
 }  // namespace
+
+int digitize_rows(hipStream_t s, int qtype, const DigitizeParams &p, int n) { return launch_digitize(s, qtype, p, n); }
+int gemm_rows(hipStream_t s, int qtype, int nmat, const GemmParams &p, int epi, int npad) {
+    return launch_gemm(s, qtype, nmat, p, epi, npad);
+}
 
 }  // namespace pocr

@@ -80,6 +80,11 @@ _SIGS = {
     "pocr_seq_destroy": (None, [_vp]),
     "pocr_seq_reset": (_i, [_vp]),
     "pocr_seq_set_sampling": (_i, [_vp, C.c_double, _i, C.c_uint64]),
+    "pocr_projector_create": (_i, [_vp, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, C.c_float, C.POINTER(_vp)]),
+    "pocr_projector_destroy": (None, [_vp]),
+    "pocr_project_image": (_i, [_vp, _vp, _i, _i, _i, _vp]),
+    "pocr_generate_vision": (_i, [_vp, _vp, _vp, _i, _vp, _i, _vp, _i, _vp, _i, _vp]),
+    "pocr_time_project": (_i, [_vp, _i, _i, _i, _i, _vp]),
     "pocr_seq_len": (_i, [_vp]),
     "pocr_seq_read_kv": (_i, [_vp, _i, _vp, _vp]),
     "pocr_seq_truncate": (_i, [_vp, _i]),
@@ -418,6 +423,43 @@ class Model:
         return Sequence(self, capacity)
 
 
+class Projector:
+    """The vision projector (mlp_AR, vision.go:224-302) with Q8 matrices on the device."""
+
+    def __init__(self, ctx: "Context", norm_w, norm_b, w1, b1, w2, b2, eps: float = 1e-5):
+        norm_w, norm_b, w1, b1, w2, b2 = (_f32(a) for a in (norm_w, norm_b, w1, b1, w2, b2))
+        self.vd = norm_w.size
+        self.td = w2.shape[0]
+        h = _vp()
+        check(load().pocr_projector_create(ctx.h, self.vd, self.td, _ptr(norm_w), _ptr(norm_b), _ptr(w1), _ptr(b1),
+                                           _ptr(w2), _ptr(b2), float(eps), C.byref(h)))
+        self.h = h
+
+    def close(self):
+        if getattr(self, "h", None):
+            load().pocr_projector_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def time_project(self, grid, iters=20):
+        """Average µs of one device projection of a T·H·W grid."""
+        us = np.zeros(1, np.float32)
+        check(load().pocr_time_project(self.h, grid[0], grid[1], grid[2], iters, _ptr(us)))
+        return float(us[0])
+
+    def project(self, vision_rows, grid):
+        """vision rows [T·H·W][vd] → [T·(H/2)·(W/2)][td]."""
+        x = _f32(vision_rows)
+        t, h, w = grid
+        if x.ndim != 2 or x.shape[0] < t * h * w or x.shape[1] != self.vd:
+            raise ValueError(f"vision rows {x.shape}: need [{t * h * w}][{self.vd}]")
+        out = np.zeros((t * (h // 2) * (w // 2), self.td), np.float32)
+        n = check(load().pocr_project_image(self.h, _ptr(x), t, h, w, _ptr(out)))
+        return out[:n]
+
+
 class Sequence:
     def __init__(self, model: Model, capacity: int):
         self.model = model
@@ -479,6 +521,18 @@ class Sequence:
         tok = np.zeros(1, np.int32)
         check(load().pocr_prefill(self.h, emb.shape[0], _ptr(emb), _ptr(pos), _ptr(logits), _ptr(tok)))
         return int(tok[0]), logits
+
+    def generate_vision(self, proj: Projector, ids, vision_rows, image_token_id: int, grid, max_new, eos=(2,)):
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        eos = np.ascontiguousarray(list(eos) if eos else [-(1 << 30)], dtype=np.int32)
+        out = np.zeros(max(max_new, 1), np.int32)
+        x = _f32(vision_rows)
+        g = np.ascontiguousarray(grid, dtype=np.int32)
+        if x.ndim != 2 or x.shape[0] < int(np.prod(g)) or x.shape[1] != proj.vd:
+            raise ValueError(f"vision rows {x.shape}: need [{int(np.prod(g))}][{proj.vd}]")
+        n = check(load().pocr_generate_vision(self.h, proj.h, _ptr(ids), ids.size, _ptr(x), image_token_id, _ptr(g),
+                                              max_new, _ptr(eos), eos.size, _ptr(out)))
+        return out[:n]
 
     def decode_greedy(self, first_token: int, first_pos: int, max_new: int, eos=(2,)):
         eos = np.ascontiguousarray(list(eos) if eos else [-(1 << 30)], dtype=np.int32)
