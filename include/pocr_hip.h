@@ -70,6 +70,7 @@ typedef struct pocr_weight pocr_weight;
 typedef struct pocr_model pocr_model;
 typedef struct pocr_seq pocr_seq;
 typedef struct pocr_projector pocr_projector;
+typedef struct pocr_gguf pocr_gguf;
 
 /* decoder hyper-parameters (internal/config/config.go:31-49).  Unlike the
  * reference loader (internal/model/model.go:647-653) heads*head_dim may
@@ -262,6 +263,33 @@ int pocr_decode_batch(pocr_seq *const *seqs, int n_seq, const int32_t *first_tok
 int pocr_generate(pocr_seq *s, const int32_t *ids, int n_ids, const float *image_embeds, int n_image,
                   int32_t image_token_id, const int32_t grid[3], int32_t merge, int max_new,
                   const int32_t *eos, int n_eos, int use_prefill, int32_t *out_tokens);
+
+/* ---------------- checkpoints ---------------- */
+/* gguf.Open (internal/gguf/gguf.go:111-251) with its validation (counts,
+ * string sizes, keys and names, shapes, types, offsets within the file:
+ * 253-296, 586-667).  Tensor types F32 (0), Q8_ROW/Q4_ROW/Q6_ROW
+ * (1000/1001/1002, = POCR_Q8/Q4/Q6); metadata u32 (4), u64 (10), string (8).
+ * Host only; no device needed. */
+int pocr_gguf_open(const char *path, pocr_gguf **out);
+void pocr_gguf_close(pocr_gguf *g);
+int pocr_gguf_tensor_count(const pocr_gguf *g);
+/* index of a tensor by name (File.Tensors), or POCR_ERR_ARG when missing */
+int pocr_gguf_find(const pocr_gguf *g, const char *name);
+/* name, type, dims (up to 8) and payload bytes (TensorBytes) of tensor i */
+int pocr_gguf_tensor_info(const pocr_gguf *g, int i, const char **name, uint32_t *type, int *ndim, int64_t *dims,
+                          int64_t *bytes);
+/* the payload of tensor i (F32 values; Q*_ROW: f32 scales[rows] then the
+ * packed rows), exactly `bytes` of it */
+int pocr_gguf_read(const pocr_gguf *g, int i, void *dst, int64_t bytes);
+int pocr_gguf_meta_count(const pocr_gguf *g);
+/* metadata entry i: key, type, numeric value (u32/u64) or string */
+int pocr_gguf_meta(const pocr_gguf *g, int i, const char **key, uint32_t *type, uint64_t *value, const char **str);
+/* a decoder model from a checkpoint: the tensors preloadTextWeights reads
+ * (internal/model/model.go:2861-2885) — model.embed_tokens / model.norm /
+ * lm_head and model.layers.N.{input_layernorm, post_attention_layernorm,
+ * self_attn.{q,k,v,o}_proj, mlp.{gate,up,down}_proj}.weight — with cfg from
+ * config.json (internal/config/config.go:51).  Matrices Q*_ROW, the rest F32. */
+int pocr_model_load_gguf(pocr_ctx *ctx, const pocr_config *cfg, const char *path, pocr_model **out);
 
 /* ---------------- vision projector ---------------- */
 /* mlp_AR of the vision tower (internal/model/vision.go:224-302): pre_norm

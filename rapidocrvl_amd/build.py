@@ -27,7 +27,7 @@ HIP_FLAGS = [
 HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-ffp-contract=off"]
 
 HIP_SOURCES = ["pocr_runtime.hip", "prefill.hip", "projector.hip"]
-HOST_SOURCES = ["quant_host.cpp"]
+HOST_SOURCES = ["quant_host.cpp", "gguf.cpp"]
 
 
 def _run(cmd):

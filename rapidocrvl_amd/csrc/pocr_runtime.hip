@@ -929,6 +929,79 @@ extern "C" int pocr_model_set_embed(pocr_model *m, const float *embed) {
     return upload_floats(m->ctx, &m->embed, embed, (size_t)m->cfg.vocab * m->cfg.hidden);
 }
 
+// A decoder model straight from a checkpoint: the tensors preloadTextWeights
+// reads by name (model.go:2861-2885) out of a GGUF file (gguf.Open,
+// internal/gguf/gguf.go:110-243); the config comes from config.json as in the
+// reference (internal/config/config.go:51).  Matrices must be Q*_ROW, norms
+// and embeddings F32.
+extern "C" int pocr_model_load_gguf(pocr_ctx *ctx, const pocr_config *cfg, const char *path, pocr_model **out) {
+    if (!ctx || !cfg || !path || !out) return fail(POCR_ERR_ARG, "pocr_model_load_gguf: null argument");
+    *out = nullptr;
+    CHECK_INJECT("model_load_gguf");
+    pocr_gguf *g = nullptr;
+    RC(pocr_gguf_open(path, &g));
+    pocr_model *m = nullptr;
+    int rc = pocr_model_create(ctx, cfg, &m);
+    std::vector<uint8_t> buf;
+    auto matrix = [&](const std::string &name, int layer, int role) -> int {
+        const int i = pocr_gguf_find(g, name.c_str());
+        if (i < 0) return i;
+        uint32_t type = 0;
+        int nd = 0;
+        int64_t dims[8], bytes = 0;
+        RC(pocr_gguf_tensor_info(g, i, nullptr, &type, &nd, dims, &bytes));
+        if (type != POCR_Q8 && type != POCR_Q4 && type != POCR_Q6)
+            return fail(POCR_ERR_UNSUPPORTED, "gguf: %s has type %u (Q8_ROW/Q4_ROW/Q6_ROW only)", name.c_str(), type);
+        if (nd != 2 || dims[0] > INT32_MAX || dims[1] > INT32_MAX)
+            return fail(POCR_ERR_ARG, "gguf: %s is not a 2-D matrix", name.c_str());
+        const int rows = (int)dims[0], cols = (int)dims[1];
+        buf.resize((size_t)bytes);
+        RC(pocr_gguf_read(g, i, buf.data(), bytes));
+        pocr_weight *w = nullptr;
+        RC(pocr_weight_upload(ctx, (int)type, rows, cols, reinterpret_cast<const float *>(buf.data()),
+                              buf.data() + (size_t)rows * 4, &w));
+        const int r = pocr_model_set_weight(m, layer, role, w);  // checks the shape, retains w
+        pocr_weight_free(w);
+        return r;
+    };
+    auto floats = [&](const std::string &name, int64_t n) -> int {
+        const int i = pocr_gguf_find(g, name.c_str());
+        if (i < 0) return i;
+        uint32_t type = 0;
+        int64_t bytes = 0;
+        RC(pocr_gguf_tensor_info(g, i, nullptr, &type, nullptr, nullptr, &bytes));
+        if (type != 0 || bytes != n * 4)
+            return fail(POCR_ERR_ARG, "gguf: %s must be F32 with %lld values", name.c_str(), (long long)n);
+        buf.resize((size_t)bytes);
+        return pocr_gguf_read(g, i, buf.data(), bytes);
+    };
+    const float *fbuf = nullptr;
+    if (rc == POCR_OK) rc = floats("model.embed_tokens.weight", (int64_t)cfg->vocab * cfg->hidden);
+    fbuf = reinterpret_cast<const float *>(buf.data());
+    if (rc == POCR_OK) rc = pocr_model_set_embed(m, fbuf);
+    if (rc == POCR_OK) rc = floats("model.norm.weight", cfg->hidden);
+    if (rc == POCR_OK) rc = pocr_model_set_norm(m, -1, POCR_N_FINAL, reinterpret_cast<const float *>(buf.data()));
+    if (rc == POCR_OK) rc = matrix("lm_head.weight", -1, POCR_W_LM_HEAD);
+    static const char *roles[] = {"self_attn.q_proj.weight", "self_attn.k_proj.weight", "self_attn.v_proj.weight",
+                                  "self_attn.o_proj.weight", "mlp.gate_proj.weight",    "mlp.up_proj.weight",
+                                  "mlp.down_proj.weight"};
+    for (int li = 0; li < cfg->layers && rc == POCR_OK; ++li) {
+        const std::string pre = "model.layers." + std::to_string(li) + ".";
+        rc = floats(pre + "input_layernorm.weight", cfg->hidden);
+        if (rc == POCR_OK) rc = pocr_model_set_norm(m, li, POCR_N_LN1, reinterpret_cast<const float *>(buf.data()));
+        if (rc == POCR_OK) rc = floats(pre + "post_attention_layernorm.weight", cfg->hidden);
+        if (rc == POCR_OK) rc = pocr_model_set_norm(m, li, POCR_N_LN2, reinterpret_cast<const float *>(buf.data()));
+        for (int role = 0; role <= POCR_W_DOWN && rc == POCR_OK; ++role) rc = matrix(pre + roles[role], li, role);
+    }
+    pocr_gguf_close(g);
+    if (rc != POCR_OK) {
+        if (m) pocr_model_destroy(m);
+        return rc;
+    }
+    *out = m;
+    return POCR_OK;
+}
+
 extern "C" int pocr_model_set_residual_quirk(pocr_model *m, int on) {
     if (!m) return fail(POCR_ERR_ARG, "pocr_model_set_residual_quirk: null model");
     m->quirk = on ? 1 : 0;

@@ -99,6 +99,17 @@ _SIGS = {
     "pocr_decode_batch": (_i, [_vp, _i, _vp, _vp, _i, _vp, _i, _vp, _vp]),
     "pocr_generate": (_i, [_vp, _vp, _i, _vp, _i, C.c_int32, _vp, C.c_int32, _i, _vp, _i, _i, _vp]),
     "pocr_mm_positions": (_i, [_vp, _i, C.c_int32, _vp, C.c_int32, _vp, _vp]),
+    "pocr_gguf_open": (_i, [C.c_char_p, C.POINTER(_vp)]),
+    "pocr_gguf_close": (None, [_vp]),
+    "pocr_gguf_tensor_count": (_i, [_vp]),
+    "pocr_gguf_find": (_i, [_vp, C.c_char_p]),
+    "pocr_gguf_tensor_info": (_i, [_vp, _i, C.POINTER(C.c_char_p), C.POINTER(C.c_uint32), C.POINTER(_i), _vp,
+                                   C.POINTER(C.c_int64)]),
+    "pocr_gguf_read": (_i, [_vp, _i, _vp, C.c_int64]),
+    "pocr_gguf_meta_count": (_i, [_vp]),
+    "pocr_gguf_meta": (_i, [_vp, _i, C.POINTER(C.c_char_p), C.POINTER(C.c_uint32), C.POINTER(C.c_uint64),
+                            C.POINTER(C.c_char_p)]),
+    "pocr_model_load_gguf": (_i, [_vp, C.POINTER(PocrConfig), C.c_char_p, C.POINTER(_vp)]),
 }
 
 _lib = None
@@ -365,13 +376,16 @@ class Context:
 class Model:
     """Device-resident decoder (weights borrowed, norms/embedding copied)."""
 
-    def __init__(self, ctx: Context, cfg):
+    def __init__(self, ctx: Context, cfg, gguf_path: str | None = None):
         self.ctx, self.cfg = ctx, cfg
         c = PocrConfig(cfg.hidden, cfg.inter, cfg.layers, cfg.heads, cfg.kv_heads, cfg.head_dim, cfg.vocab,
                        cfg.eps, cfg.rope_theta, (C.c_int32 * 3)(*cfg.mrope_section))
         self._seqs = weakref.WeakSet()
         h = _vp()
-        check(load().pocr_model_create(ctx.h, C.byref(c), C.byref(h)))
+        if gguf_path is None:
+            check(load().pocr_model_create(ctx.h, C.byref(c), C.byref(h)))
+        else:
+            check(load().pocr_model_load_gguf(ctx.h, C.byref(c), os.fsencode(gguf_path), C.byref(h)))
         self.h = h
         self._weights = []
         ctx._children.add(self)
@@ -419,8 +433,74 @@ class Model:
         self.set_norm(-1, N_FINAL, weights["final_norm"])
         self.set_embed(weights["embed"])
 
+    @classmethod
+    def from_gguf(cls, ctx: Context, cfg, path: str) -> "Model":
+        """All decoder tensors from a GGUF checkpoint (pocr_model_load_gguf)."""
+        return cls(ctx, cfg, gguf_path=path)
+
     def seq(self, capacity: int) -> "Sequence":
         return Sequence(self, capacity)
+
+
+class GgufFile:
+    """A GGUF checkpoint opened by the native reader (gguf.Open,
+    internal/gguf/gguf.go:111-251): ``tensors`` maps name → (type, shape,
+    payload bytes), ``metadata`` key → int or str."""
+
+    def __init__(self, path: str):
+        h = _vp()
+        check(load().pocr_gguf_open(os.fsencode(path), C.byref(h)))
+        self.h = h
+        L = load()
+        self.tensors = {}
+        dims = (C.c_int64 * 8)()
+        for i in range(check(L.pocr_gguf_tensor_count(h))):
+            name, typ, nd, nb = C.c_char_p(), C.c_uint32(), C.c_int(), C.c_int64()
+            check(L.pocr_gguf_tensor_info(h, i, C.byref(name), C.byref(typ), C.byref(nd), dims, C.byref(nb)))
+            self.tensors[name.value.decode()] = (typ.value, tuple(dims[j] for j in range(nd.value)), nb.value)
+        self.metadata = {}
+        for i in range(check(L.pocr_gguf_meta_count(h))):
+            key, typ, val, sval = C.c_char_p(), C.c_uint32(), C.c_uint64(), C.c_char_p()
+            check(L.pocr_gguf_meta(h, i, C.byref(key), C.byref(typ), C.byref(val), C.byref(sval)))
+            self.metadata[key.value.decode()] = sval.value.decode() if typ.value == 8 else val.value
+
+    def close(self):
+        if getattr(self, "h", None):
+            load().pocr_gguf_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def raw(self, name: str) -> np.ndarray:
+        typ, shape, nb = self.tensors[name]
+        out = np.empty(nb, np.uint8)
+        i = check(load().pocr_gguf_find(self.h, name.encode()))
+        check(load().pocr_gguf_read(self.h, i, _ptr(out), nb))
+        return out
+
+    def float32(self, name: str) -> np.ndarray:
+        """File.Float32 (gguf.go:313-327): an F32 tensor in its shape."""
+        typ, shape, _ = self.tensors[name]
+        if typ != F32:
+            raise ValueError(f"{name} has type {typ}, not F32")
+        return self.raw(name).view(np.float32).reshape(shape)
+
+    def qrows(self, name: str) -> "QMatrix":
+        """File.Q8Row / Q4Row / Q6Row (gguf.go:435-569): scales and packed rows."""
+        typ, shape, _ = self.tensors[name]
+        if typ not in (Q8, Q4, Q6):
+            raise ValueError(f"{name} has type {typ}, not a Q*_ROW")
+        rows, cols = shape
+        raw = self.raw(name)
+        return QMatrix(typ, rows, cols, raw[:rows * 4].view(np.float32).copy(),
+                       raw[rows * 4:].reshape(rows, row_bytes(typ, cols)).copy())
 
 
 class Projector:

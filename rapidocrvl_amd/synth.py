@@ -66,6 +66,35 @@ def make_weights(cfg: DecoderConfig, qtype: int, seed: int = 0, tie: int = lib.T
     return out
 
 
+_CKPT_ROLE = {"q": "self_attn.q_proj", "k": "self_attn.k_proj", "v": "self_attn.v_proj", "o": "self_attn.o_proj",
+              "gate": "mlp.gate_proj", "up": "mlp.up_proj", "down": "mlp.down_proj"}
+
+
+def make_checkpoint(cfg: DecoderConfig, seed: int = 0) -> dict:
+    """The f32 (bf16-exact) tensors ``make_weights`` quantizes, under the
+    checkpoint's names (preloadTextWeights, internal/model/model.go:2861-2885);
+    converting them reproduces ``make_weights(cfg, q, seed, TIE_AMD64)``."""
+    out = {}
+    for li in range(cfg.layers):
+        pre = f"model.layers.{li}."
+        for role in ROLES:
+            out[pre + _CKPT_ROLE[role] + ".weight"] = normal(shape_of(cfg, role), [seed, li, _ROLE_ID[role]])
+        out[pre + "input_layernorm.weight"] = bf16_round(1.0 + normal(cfg.hidden, [seed, li, 100]))
+        out[pre + "post_attention_layernorm.weight"] = bf16_round(1.0 + normal(cfg.hidden, [seed, li, 101]))
+    out["lm_head.weight"] = normal((cfg.vocab, cfg.hidden), [seed, 1000, 0])
+    out["model.norm.weight"] = bf16_round(1.0 + normal(cfg.hidden, [seed, 1000, 1]))
+    out["model.embed_tokens.weight"] = normal((cfg.vocab, cfg.hidden), [seed, 1000, 2])
+    return out
+
+
+def config_json(cfg: DecoderConfig) -> dict:
+    """config.json fields of a decoder configuration (internal/config/config.go:31-49)."""
+    return {"vocab_size": cfg.vocab, "hidden_size": cfg.hidden, "intermediate_size": cfg.inter,
+            "num_hidden_layers": cfg.layers, "num_attention_heads": cfg.heads, "num_key_value_heads": cfg.kv_heads,
+            "head_dim": cfg.head_dim, "rms_norm_eps": cfg.eps, "rope_theta": cfg.rope_theta,
+            "rope_scaling": {"mrope_section": list(cfg.mrope_section)}, "vision_config": {"num_hidden_layers": 0}}
+
+
 def prompt_ids(n: int, seed: int = 0, high: int = 100000):
     """Token ids drawn uniformly from [0, high) with the given seed."""
     return np.random.default_rng(seed).integers(0, high, size=n, dtype=np.int64).astype(np.int32)

@@ -31,6 +31,14 @@ def test_null_arguments_are_arg_errors():
     assert L.pocr_matvec_topk(None, None, None, 4, None, None) == lib.POCR_ERR_ARG
     assert L.pocr_sample_topk(None, None, 8, 4, 1.0, None, None, None, None) == lib.POCR_ERR_ARG
     assert L.pocr_seq_set_sampling(None, 1.0, 4, 0) == lib.POCR_ERR_ARG
+    assert L.pocr_gguf_open(None, None) == lib.POCR_ERR_ARG
+    assert L.pocr_gguf_tensor_count(None) == lib.POCR_ERR_ARG
+    assert L.pocr_gguf_find(None, b"x") == lib.POCR_ERR_ARG
+    assert L.pocr_gguf_tensor_info(None, 0, None, None, None, None, None) == lib.POCR_ERR_ARG
+    assert L.pocr_gguf_read(None, 0, None, 4) == lib.POCR_ERR_ARG
+    assert L.pocr_gguf_meta(None, 0, None, None, None, None) == lib.POCR_ERR_ARG
+    assert L.pocr_model_load_gguf(None, None, b"x", None) == lib.POCR_ERR_ARG
+    L.pocr_gguf_close(None)
 
 
 def test_fault_injection_is_reported_before_device_work(monkeypatch):
