@@ -78,6 +78,65 @@ def batch_decode(model, cfg, n_seq=4, n_new=1024, reps=2):
             "tok_s": round(n_seq * n_new / dt, 1), "ms_per_step": round(dt / (n_new - 1) * 1e3, 4)}
 
 
+SERVE_BUDGETS = (512, 128, 384, 256, 640, 192, 448, 320)
+
+
+def serve(model, cfg, budgets=SERVE_BUDGETS, slots=4, chunk=16):
+    """Server-style serving of len(budgets) image requests (5 ids + 1332 visual
+    rows + 11 ids, seeds 300+i; request i generates budgets[i] greedy tokens):
+    one request at a time (prefill, then its own decode loop: the reference
+    server with one run slot) against continuous batching (requests prefilled
+    as slots free up, joining and leaving a 4-member decode batch between
+    token steps).  Wall time covers prefills and decodes; tokens/s counts
+    generated tokens.  Each request's tokens must be the same both ways."""
+    from rapidocrvl_amd import lib, synth
+
+    grid = (1, 72, 74)
+    reqs = []
+    for i, n in enumerate(budgets):
+        ids = np.concatenate([synth.prompt_ids(5, seed=300 + i), np.full(1332, IMAGE_TOKEN, np.int32),
+                              synth.prompt_ids(11, seed=400 + i)]).astype(np.int32)
+        _, delta = lib.mm_positions(ids, IMAGE_TOKEN, grid)
+        reqs.append((ids, synth.image_embeds(1332, cfg.hidden, seed=300 + i), ids.size + delta, n))
+    seqs = [model.seq(ids.size + n + 8) for ids, _, _, n in reqs]
+
+    def first_token(s, ids, img):
+        s.reset()
+        return int(s.generate(ids, 1, eos=(), image_embeds=img, image_token_id=IMAGE_TOKEN, grid=grid,
+                              use_prefill=True)[0])
+
+    t = time.perf_counter()
+    one = []
+    for s, (ids, img, pos, n) in zip(seqs, reqs):
+        one.append(list(s.decode_greedy(first_token(s, ids, img), pos, n, eos=())))
+    t_one = time.perf_counter() - t
+
+    t = time.perf_counter()
+    b = lib.Batch(model)
+    queue, members, got = list(range(len(reqs))), [], {}
+    while queue or members:
+        while queue and len(members) < slots:
+            i = queue.pop(0)
+            ids, img, pos, n = reqs[i]
+            b.join(seqs[i], first_token(seqs[i], ids, img), pos, n, eos=())
+            members.append(i)
+        b.step(chunk)
+        for i in list(members):
+            if b.poll(seqs[i])[1]:
+                got[i] = list(b.leave(seqs[i]))
+                members.remove(i)
+    t_cb = time.perf_counter() - t
+    b.close()
+    for s in seqs:
+        s.close()
+    total = sum(budgets)
+    return {"requests": len(budgets), "tokens": total, "slots": slots,
+            "one_at_a_time": {"s": round(t_one, 3), "tok_s": round(total / t_one, 1)},
+            "continuous_batch": {"s": round(t_cb, 3), "tok_s": round(total / t_cb, 1)},
+            "speedup": round(t_one / t_cb, 2),
+            "tokens_match": all(got[i] == one[i] for i in range(len(reqs)))}
+
+
 def build_model(ctx, cfg, qtype, seed=0):
     from rapidocrvl_amd import lib, synth
 
@@ -366,6 +425,7 @@ def main():
     ap.add_argument("--no-batch", action="store_true", help="skip the 4-sequence batched decode")
     ap.add_argument("--batch-only", action="store_true", help="time only the 4-sequence Q4 batched decode")
     ap.add_argument("--projector-only", action="store_true", help="time only the vision projector")
+    ap.add_argument("--serve-only", action="store_true", help="time only the 8-request serving comparison")
     ap.add_argument("--batch-tokens", type=int, default=1024, help="tokens per sequence of the batched decode")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -387,6 +447,10 @@ def main():
         _, model = build_model(ctx, cfg, lib.Q4)
         print(json.dumps({"workload": "4-sequence q4 batched greedy decode",
                           **batch_decode(model, cfg, n_new=args.batch_tokens, reps=1)}), flush=True)
+        return
+    if args.serve_only:
+        _, model = build_model(ctx, cfg, lib.Q4)
+        print(json.dumps({"workload": "q4 serving of 8 image requests", **serve(model, cfg)}), flush=True)
         return
     ids = workload_ids()
     img = synth.image_embeds(1332, cfg.hidden, seed=0)
@@ -426,6 +490,16 @@ def main():
         log(f"[bench] cpu baseline {cpu}")
 
     extra = {}
+    if not args.no_batch:
+        extra["batch4_decode"] = {"q4": batch_decode(model, cfg, n_new=args.batch_tokens)}
+        log(f"[bench] 4-sequence batched decode q4 {extra['batch4_decode']['q4']}")
+        extra["serving_q4"] = serve(model, cfg)
+        log(f"[bench] serving q4 {extra['serving_q4']}")
+        _, m6 = build_model(ctx, cfg, lib.Q6)
+        extra["batch4_decode"]["q6"] = batch_decode(m6, cfg, n_new=args.batch_tokens)
+        log(f"[bench] 4-sequence batched decode q6 {extra['batch4_decode']['q6']}")
+        m6.close()
+        del m6
     if not args.no_q8:
         model.close()
         seq.close()
@@ -444,13 +518,6 @@ def main():
     extra["prefill_ms"] = round(t_prefill * 1e3, 2)
     extra["prefill_tok_s"] = round(n_prefix / t_prefill, 1)
     extra["prefill_TFLOP_s"] = round(prefill_flops(cfg, n_prefix) / t_prefill / 1e12, 2)
-    if not args.no_batch:
-        extra["batch4_decode"] = {"q4": batch_decode(model, cfg, n_new=args.batch_tokens)}
-        log(f"[bench] 4-sequence batched decode q4 {extra['batch4_decode']['q4']}")
-        _, m6 = build_model(ctx, cfg, lib.Q6)
-        extra["batch4_decode"]["q6"] = batch_decode(m6, cfg, n_new=args.batch_tokens)
-        log(f"[bench] 4-sequence batched decode q6 {extra['batch4_decode']['q6']}")
-        del m6
 
     extra["projector"] = projector_bench(ctx, with_cpu=not args.no_cpu)
     log(f"[bench] projector {extra['projector']}")

@@ -71,6 +71,7 @@ typedef struct pocr_model pocr_model;
 typedef struct pocr_seq pocr_seq;
 typedef struct pocr_projector pocr_projector;
 typedef struct pocr_gguf pocr_gguf;
+typedef struct pocr_batch pocr_batch;
 
 /* decoder hyper-parameters (internal/config/config.go:31-49).  Unlike the
  * reference loader (internal/model/model.go:647-653) heads*head_dim may
@@ -256,6 +257,31 @@ int pocr_decode_greedy(pocr_seq *s, int32_t first_token, int32_t first_pos, int 
 int pocr_decode_batch(pocr_seq *const *seqs, int n_seq, const int32_t *first_tokens,
                       const int32_t *first_positions, int max_new, const int32_t *eos, int n_eos,
                       int32_t *out_tokens, int32_t *out_counts);
+/* continuous batching: a decode batch that requests join and leave between
+ * token steps, in place of the server's per-request slots, each running its
+ * own decode loop (cmd/paddleocrvl-server/main.go:1106-1124, acquire/release;
+ * model.go:1538-1568).  Up to 4 members decode at once, one batched device
+ * step per token as in pocr_decode_batch; each member's tokens equal its
+ * pocr_decode_greedy stream.  A batch is driven by one thread; a member
+ * sequence accepts no other generation or cache call until it leaves
+ * (POCR_ERR_ARG), and destroying it removes it from the batch. */
+int pocr_batch_create(pocr_model *m, pocr_batch **out);
+void pocr_batch_destroy(pocr_batch *b);
+/* a prefilled sequence joins with the token its prefill chose, at position
+ * first_pos, for at most max_new tokens (first_token counted) and the EOS
+ * ids given; greedy sequences only (POCR_ERR_UNSUPPORTED otherwise).
+ * POCR_ERR_ARG if 4 members are still decoding or the capacity is short. */
+int pocr_batch_join(pocr_batch *b, pocr_seq *s, int32_t first_token, int32_t first_pos, int max_new,
+                    const int32_t *eos, int n_eos);
+/* up to max_steps token steps for every decoding member (fewer when a
+ * member's budget ends first); members reaching an EOS id or max_new tokens
+ * finish.  Returns the number of members still decoding. */
+int pocr_batch_step(pocr_batch *b, int max_steps);
+/* tokens a member has produced so far (>= 0), *finished set when it is done */
+int pocr_batch_poll(pocr_batch *b, const pocr_seq *s, int *finished);
+/* the member leaves, finished or not: copies up to cap of its tokens (first
+ * token first) and returns how many it produced */
+int pocr_batch_leave(pocr_batch *b, pocr_seq *s, int32_t *out_tokens, int cap);
 /* whole greedy generation: GenerateWithOptions / generateWithImageEmbeds
  * (internal/model/model.go:1492-1572, 1618-1711) incl. multimodal positions
  * (1717-1783).  image rows replace ids equal to image_token_id in order.

@@ -9,6 +9,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <memory>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -136,6 +137,7 @@ struct pocr_seq {
     int max_tokens = 0;
     int nsplit = 32;  // attention splits for rpw rows per wave
     int rpw = 16;
+    pocr_batch *batch = nullptr;  // the continuous batch this sequence decodes in (ctx lock)
     // sampling head (temperature > 0, 1 < top_k ≤ 64); greedy otherwise
     bool sampling = false;
     double temperature = 0.0;
@@ -174,6 +176,8 @@ unsigned long long argmax_of(const StepState &s);
 float *layer_k(const pocr_seq *s, int layer);
 float *layer_v(const pocr_seq *s, int layer);
 int seq_set_state(pocr_seq *s, int len);
+// POCR_ERR_ARG while the sequence is a member of a continuous batch (ctx lock held)
+int seq_idle(const pocr_seq *s, const char *op);
 // LM head on RMSNorm(x)·final_norm: greedy argmax into the step state, or the
 // sampling head (logits, top-k, one draw into argmax slot 0) when the
 // sequence samples

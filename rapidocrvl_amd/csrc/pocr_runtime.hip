@@ -1081,6 +1081,8 @@ extern "C" int pocr_seq_create(pocr_model *m, int capacity, pocr_seq **out) {
     return POCR_OK;
 }
 
+static void batch_forget(pocr_batch *b, const pocr_seq *s);
+
 extern "C" void pocr_seq_destroy(pocr_seq *s) {
     if (!s) return;
     pocr_model *m = s->m;
@@ -1088,9 +1090,14 @@ extern "C" void pocr_seq_destroy(pocr_seq *s) {
         std::lock_guard<std::mutex> lk(m->ctx->mu);
         (void)hipSetDevice(m->ctx->device);
         (void)hipStreamSynchronize(m->ctx->stream);
+        if (s->batch) batch_forget(s->batch, s);
         delete s;
     }
     model_release(m);
+}
+
+int pocr::seq_idle(const pocr_seq *s, const char *op) {
+    return s->batch ? fail(POCR_ERR_ARG, "%s: the sequence is in a decode batch", op) : POCR_OK;
 }
 
 float *pocr::layer_k(const pocr_seq *s, int layer) {
@@ -1116,6 +1123,7 @@ int pocr::seq_set_state(pocr_seq *s, int len) {
 extern "C" int pocr_seq_reset(pocr_seq *s) {
     if (!s) return fail(POCR_ERR_ARG, "pocr_seq_reset: null");
     std::lock_guard<std::mutex> lk(s->m->ctx->mu);
+    RC(seq_idle(s, "pocr_seq_reset"));
     HIP_TRY(hipSetDevice(s->m->ctx->device));
     return seq_set_state(s, 0);
 }
@@ -1141,6 +1149,7 @@ extern "C" int pocr_seq_set_sampling(pocr_seq *s, double temperature, int top_k,
     if (!greedy && (top_k == 0 || top_k > kTopKMax || top_k >= s->m->cfg.vocab))
         return fail(POCR_ERR_UNSUPPORTED, "sampling: top_k %d (device sampling takes 1 < top_k <= 64 < vocab)", top_k);
     std::lock_guard<std::mutex> lk(s->m->ctx->mu);
+    RC(seq_idle(s, "pocr_seq_set_sampling"));
     HIP_TRY(hipSetDevice(s->m->ctx->device));
     HIP_TRY(hipStreamSynchronize(s->m->ctx->stream));
     if (s->sampling != !greedy || (!greedy && s->top_k != top_k)) {
@@ -1177,6 +1186,7 @@ extern "C" int pocr_seq_write_kv(pocr_seq *s, int layer, const float *k, const f
     if (!s || !k || !v || layer < 0 || layer >= s->m->cfg.layers || len < 0 || len > s->cap)
         return fail(POCR_ERR_ARG, "pocr_seq_write_kv: bad arguments");
     std::lock_guard<std::mutex> lk(s->m->ctx->mu);
+    RC(seq_idle(s, "pocr_seq_write_kv"));
     HIP_TRY(hipSetDevice(s->m->ctx->device));
     const size_t n = (size_t)len * s->m->cfg.kv_heads * s->m->cfg.head_dim * 4;
     if (n) {
@@ -1189,6 +1199,7 @@ extern "C" int pocr_seq_write_kv(pocr_seq *s, int layer, const float *k, const f
 extern "C" int pocr_seq_truncate(pocr_seq *s, int len) {
     if (!s || len < 0 || len > s->len) return fail(POCR_ERR_ARG, "pocr_seq_truncate: bad length");
     std::lock_guard<std::mutex> lk(s->m->ctx->mu);
+    RC(seq_idle(s, "pocr_seq_truncate"));
     HIP_TRY(hipSetDevice(s->m->ctx->device));
     return seq_set_state(s, len);
 }
@@ -1504,6 +1515,7 @@ extern "C" int pocr_step(pocr_seq *s, const float *emb, const int32_t pos3[3], i
     RC(model_ready(s->m));
     CHECK_INJECT("step");
     std::lock_guard<std::mutex> lk(s->m->ctx->mu);
+    RC(seq_idle(s, "pocr_step"));
     HIP_TRY(hipSetDevice(s->m->ctx->device));
     return step_locked(s, emb, pos3, need_logits, logits, token);
 }
@@ -1598,6 +1610,7 @@ extern "C" int pocr_decode_greedy(pocr_seq *s, int32_t first_token, int32_t firs
     RC(model_ready(s->m));
     CHECK_INJECT("decode");
     std::lock_guard<std::mutex> lk(s->m->ctx->mu);
+    RC(seq_idle(s, "pocr_decode_greedy"));
     HIP_TRY(hipSetDevice(s->m->ctx->device));
     return decode_locked(s, first_token, first_pos, max_new, eos, n_eos, out_tokens);
 }
@@ -1621,11 +1634,13 @@ struct DecodeBatch {
     StepState *pad = nullptr;  // step state of the padding vectors
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
+    bool owns = true;  // false: the vector buffers belong to a continuous batch
     ~DecodeBatch() {
         if (exec) (void)hipGraphExecDestroy(exec);
         if (graph) (void)hipGraphDestroy(graph);
-        for (void *p : {(void *)h, (void *)v, (void *)qkv, (void *)ho, (void *)g, (void *)pad})
-            if (p) (void)hipFree(p);
+        if (owns)
+            for (void *p : {(void *)h, (void *)v, (void *)qkv, (void *)ho, (void *)g, (void *)pad})
+                if (p) (void)hipFree(p);
     }
     StepState *st(int i) const { return i < n ? seq[i]->st : pad; }
 };
@@ -1742,6 +1757,24 @@ int enqueue_batch_step(DecodeBatch &b) {
     return gemv_launch(st, lm, 1, PRO_RMSNORM, EPI_ARGMAX, kBigGrid, b.nv, &q);
 }
 
+// the first token of a batched decode sits in the argmax slots as if the
+// previous step had chosen it (the step prologue reads it from there)
+int seed_first_token(pocr_seq *s, int32_t first_token, int32_t first_pos, StepState &hs) {
+    RC(read_state(s, &hs));
+    hs.err = 0;
+    hs.n_out = 0;
+    hs.next_pos = first_pos;
+    for (int k = 0; k < kArgSlots; ++k) hs.argmax_slot[k * kSlotPitch] = 0ull;
+    hs.argmax_slot[0] = (1ull << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)first_token);
+    HIP_TRY(hipMemcpyAsync(s->st, &hs, sizeof(StepState), hipMemcpyHostToDevice, s->m->ctx->stream));
+    HIP_TRY(hipStreamSynchronize(s->m->ctx->stream));
+    return POCR_OK;
+}
+
+int32_t pending_token(const StepState &hs) {
+    return (int32_t)(0xFFFFFFFFu - (uint32_t)(argmax_of(hs) & 0xFFFFFFFFull));
+}
+
 int batch_alloc(DecodeBatch &b) {
     const pocr_config &c = b.m->cfg;
     const size_t H = c.hidden, Q = (size_t)c.heads * c.head_dim, KV = (size_t)c.kv_heads * c.head_dim;
@@ -1780,6 +1813,7 @@ extern "C" int pocr_decode_batch(pocr_seq *const *seqs, int n_seq, const int32_t
     RC(model_ready(m));
     CHECK_INJECT("decode_batch");
     std::lock_guard<std::mutex> lk(m->ctx->mu);
+    for (int i = 0; i < n_seq; ++i) RC(seq_idle(seqs[i], "pocr_decode_batch"));
     HIP_TRY(hipSetDevice(m->ctx->device));
     hipStream_t st = m->ctx->stream;
     const int steps_needed = max_new - 1;
@@ -1795,16 +1829,7 @@ extern "C" int pocr_decode_batch(pocr_seq *const *seqs, int n_seq, const int32_t
     // per-sequence state: the first token sits in the argmax slots as if the
     // previous step had chosen it (the step prologue reads it from there)
     std::vector<StepState> hs(n_seq);
-    for (int i = 0; i < n_seq; ++i) {
-        RC(read_state(seqs[i], &hs[i]));
-        hs[i].err = 0;
-        hs[i].n_out = 0;
-        hs[i].next_pos = first_positions[i];
-        for (int k = 0; k < kArgSlots; ++k) hs[i].argmax_slot[k * kSlotPitch] = 0ull;
-        hs[i].argmax_slot[0] = (1ull << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)first_tokens[i]);
-        HIP_TRY(hipMemcpyAsync(seqs[i]->st, &hs[i], sizeof(StepState), hipMemcpyHostToDevice, st));
-    }
-    HIP_TRY(hipStreamSynchronize(st));
+    for (int i = 0; i < n_seq; ++i) RC(seed_first_token(seqs[i], first_tokens[i], first_positions[i], hs[i]));
     const char *g_env = getenv("POCR_HIP_GRAPH");
     const bool use_graph = !(g_env && g_env[0] == '0');
     if (use_graph) {
@@ -1844,8 +1869,7 @@ extern "C" int pocr_decode_batch(pocr_seq *const *seqs, int n_seq, const int32_t
     }
     for (int i = 0; i < n_seq; ++i) {
         if (!done[i]) {  // the token chosen by the last step
-            out_tokens[(size_t)i * max_new + produced[i]] =
-                (int32_t)(0xFFFFFFFFu - (uint32_t)(argmax_of(hs[i]) & 0xFFFFFFFFull));
+            out_tokens[(size_t)i * max_new + produced[i]] = pending_token(hs[i]);
             ++produced[i];
         }
         out_counts[i] = produced[i];
@@ -1854,12 +1878,222 @@ extern "C" int pocr_decode_batch(pocr_seq *const *seqs, int n_seq, const int32_t
     return POCR_OK;
 }
 
+// ---------------------------------------------------------------------------
+// Continuous batching: members join and leave between token steps.  The
+// device set (members still decoding) is captured into one batched step graph,
+// captured again whenever the set changes; the vector buffers are allocated
+// once for kMaxNV vectors.  A member decodes from its seeded first token until
+// an EOS id or its token budget; steps are issued in chunks no longer than any
+// member's remaining budget, so no cache grows past what its join checked.
+// ---------------------------------------------------------------------------
+struct pocr_batch {
+    struct Member {
+        pocr_seq *s = nullptr;
+        int max_new = 0;
+        int steps = 0;                // device steps run
+        std::vector<int32_t> eos;
+        std::vector<int32_t> out;     // tokens produced, first token first
+        bool finished = false;
+    };
+    pocr_model *m = nullptr;
+    std::vector<Member> members;      // join order
+    DecodeBatch bufs;                 // owns the kMaxNV vector buffers
+    std::unique_ptr<DecodeBatch> cur; // the captured device set, null when stale
+    bool use_graph = true;
+};
+
+static void batch_forget(pocr_batch *b, const pocr_seq *s) {
+    for (size_t i = 0; i < b->members.size(); ++i)
+        if (b->members[i].s == s) {
+            if (!b->members[i].finished) b->cur.reset();
+            b->members.erase(b->members.begin() + (long)i);
+            break;
+        }
+    const_cast<pocr_seq *>(s)->batch = nullptr;
+}
+
+extern "C" int pocr_batch_create(pocr_model *m, pocr_batch **out) {
+    if (!m || !out) return fail(POCR_ERR_ARG, "pocr_batch_create: null argument");
+    *out = nullptr;
+    CHECK_INJECT("batch");
+    std::lock_guard<std::mutex> lk(m->ctx->mu);
+    HIP_TRY(hipSetDevice(m->ctx->device));
+    pocr_batch *b = new pocr_batch();
+    b->m = m;
+    b->bufs.m = m;
+    b->bufs.nv = kMaxNV;
+    const int rc = batch_alloc(b->bufs);
+    if (rc == POCR_OK) {
+        const hipError_t e = hipStreamSynchronize(m->ctx->stream);
+        if (e != hipSuccess) {
+            delete b;
+            return fail(POCR_ERR_DEVICE, "pocr_batch_create: %s", hipGetErrorString(e));
+        }
+    }
+    if (rc != POCR_OK) {
+        delete b;
+        return rc;
+    }
+    const char *g_env = getenv("POCR_HIP_GRAPH");
+    b->use_graph = !(g_env && g_env[0] == '0');
+    m->refs.fetch_add(1);
+    *out = b;
+    return POCR_OK;
+}
+
+extern "C" void pocr_batch_destroy(pocr_batch *b) {
+    if (!b) return;
+    pocr_model *m = b->m;
+    {
+        std::lock_guard<std::mutex> lk(m->ctx->mu);
+        (void)hipSetDevice(m->ctx->device);
+        (void)hipStreamSynchronize(m->ctx->stream);
+        for (auto &mb : b->members) mb.s->batch = nullptr;
+        delete b;
+    }
+    model_release(m);
+}
+
+extern "C" int pocr_batch_join(pocr_batch *b, pocr_seq *s, int32_t first_token, int32_t first_pos, int max_new,
+                               const int32_t *eos, int n_eos) {
+    if (!b || !s || max_new <= 0 || n_eos < 0 || (n_eos > 0 && !eos))
+        return fail(POCR_ERR_ARG, "pocr_batch_join: bad arguments");
+    if (s->m != b->m) return fail(POCR_ERR_ARG, "pocr_batch_join: the sequence belongs to another model");
+    if (first_token < 0 || first_token >= b->m->cfg.vocab) return fail(POCR_ERR_ARG, "pocr_batch_join: token out of vocab");
+    RC(model_ready(b->m));
+    CHECK_INJECT("batch_join");
+    std::lock_guard<std::mutex> lk(b->m->ctx->mu);
+    HIP_TRY(hipSetDevice(b->m->ctx->device));
+    if (s->batch) return fail(POCR_ERR_ARG, "pocr_batch_join: the sequence is already in a decode batch");
+    if (s->sampling) return fail(POCR_ERR_UNSUPPORTED, "pocr_batch_join: the sequence samples (the batch is greedy)");
+    int decoding = 0;
+    for (const auto &mb : b->members) decoding += mb.finished ? 0 : 1;
+    if (decoding >= kMaxNV) return fail(POCR_ERR_ARG, "pocr_batch_join: %d members are decoding", kMaxNV);
+    if (s->len + max_new - 1 > s->cap || max_new > s->max_tokens)
+        return fail(POCR_ERR_ARG, "pocr_batch_join: %d tokens exceed the capacity", max_new);
+    pocr_batch::Member mb;
+    mb.s = s;
+    mb.max_new = max_new;
+    mb.eos.assign(eos, eos + n_eos);
+    if (max_new == 1 || is_eos(first_token, eos, n_eos)) {
+        mb.out.push_back(first_token);  // done before any device step
+        mb.finished = true;
+    } else {
+        StepState hs;
+        RC(seed_first_token(s, first_token, first_pos, hs));
+        b->cur.reset();
+    }
+    s->batch = b;
+    b->members.push_back(std::move(mb));
+    return POCR_OK;
+}
+
+static int batch_capture(pocr_batch *b) {
+    auto d = std::make_unique<DecodeBatch>();
+    d->m = b->m;
+    d->owns = false;
+    for (auto &mb : b->members)
+        if (!mb.finished) d->seq[d->n++] = mb.s;
+    d->nv = d->n == 1 ? 1 : (d->n == 2 ? 2 : 4);
+    d->h = b->bufs.h;
+    d->v = b->bufs.v;
+    d->qkv = b->bufs.qkv;
+    d->ho = b->bufs.ho;
+    d->g = b->bufs.g;
+    d->pad = b->bufs.pad;
+    if (b->use_graph) {
+        hipStream_t st = b->m->ctx->stream;
+        HIP_TRY(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+        const int rc = enqueue_batch_step(*d);
+        const hipError_t e = hipStreamEndCapture(st, &d->graph);
+        if (rc != POCR_OK) return rc;
+        if (e != hipSuccess) return fail(POCR_ERR_DEVICE, "graph capture: %s", hipGetErrorString(e));
+        HIP_TRY(hipGraphInstantiate(&d->exec, d->graph, nullptr, nullptr, 0));
+    }
+    b->cur = std::move(d);
+    return POCR_OK;
+}
+
+extern "C" int pocr_batch_step(pocr_batch *b, int max_steps) {
+    if (!b || max_steps <= 0) return fail(POCR_ERR_ARG, "pocr_batch_step: bad arguments");
+    CHECK_INJECT("batch_step");
+    std::lock_guard<std::mutex> lk(b->m->ctx->mu);
+    HIP_TRY(hipSetDevice(b->m->ctx->device));
+    int k = max_steps, decoding = 0;
+    for (const auto &mb : b->members)
+        if (!mb.finished) {
+            k = std::min(k, mb.max_new - 1 - mb.steps);  // >= 1: a member at its budget has finished
+            ++decoding;
+        }
+    if (decoding == 0) return 0;
+    if (!b->cur) RC(batch_capture(b));
+    hipStream_t st = b->m->ctx->stream;
+    for (int i = 0; i < k; ++i) {
+        if (b->use_graph) HIP_TRY(hipGraphLaunch(b->cur->exec, st));
+        else RC(enqueue_batch_step(*b->cur));
+    }
+    StepState hs;
+    std::vector<int32_t> tok;
+    decoding = 0;
+    for (auto &mb : b->members) {
+        if (mb.finished) continue;
+        RC(read_state(mb.s, &hs));
+        if (hs.err) return fail(POCR_ERR_DEVICE, "pocr_batch_step: device state error %d", hs.err);
+        mb.s->len = hs.len;
+        mb.steps += k;
+        // tokens the steps appended (the first one is the seeded first token)
+        tok.resize(hs.n_out);
+        if (hs.n_out > (int)mb.out.size())
+            HIP_TRY(hipMemcpy(tok.data(), mb.s->tokens, (size_t)hs.n_out * 4, hipMemcpyDeviceToHost));
+        for (int t = (int)mb.out.size(); t < hs.n_out && !mb.finished; ++t) {
+            mb.out.push_back(tok[t]);
+            mb.finished = is_eos(tok[t], mb.eos.data(), (int)mb.eos.size());
+        }
+        // the token the last step chose ends the member at its budget or an EOS
+        if (!mb.finished) {
+            const int32_t next = pending_token(hs);
+            if (mb.steps == mb.max_new - 1 || is_eos(next, mb.eos.data(), (int)mb.eos.size())) {
+                mb.out.push_back(next);
+                mb.finished = true;
+            }
+        }
+        if (mb.finished) b->cur.reset();
+        else ++decoding;
+    }
+    return decoding;
+}
+
+extern "C" int pocr_batch_poll(pocr_batch *b, const pocr_seq *s, int *finished) {
+    if (!b || !s) return fail(POCR_ERR_ARG, "pocr_batch_poll: null argument");
+    std::lock_guard<std::mutex> lk(b->m->ctx->mu);
+    for (const auto &mb : b->members)
+        if (mb.s == s) {
+            if (finished) *finished = mb.finished ? 1 : 0;
+            return (int)mb.out.size();
+        }
+    return fail(POCR_ERR_ARG, "pocr_batch_poll: the sequence is not in this batch");
+}
+
+extern "C" int pocr_batch_leave(pocr_batch *b, pocr_seq *s, int32_t *out_tokens, int cap) {
+    if (!b || !s || cap < 0 || (cap > 0 && !out_tokens)) return fail(POCR_ERR_ARG, "pocr_batch_leave: bad arguments");
+    std::lock_guard<std::mutex> lk(b->m->ctx->mu);
+    for (const auto &mb : b->members)
+        if (mb.s == s) {
+            const int n = (int)mb.out.size();
+            std::copy(mb.out.begin(), mb.out.begin() + std::min(n, cap), out_tokens);
+            batch_forget(b, s);
+            return n;
+        }
+    return fail(POCR_ERR_ARG, "pocr_batch_leave: the sequence is not in this batch");
+}
+
 extern "C" int pocr_prefill(pocr_seq *s, int n, const float *emb, const int32_t *pos3, float *logits,
                             int32_t *token) {
     if (!s || !emb || !pos3 || n <= 0) return fail(POCR_ERR_ARG, "pocr_prefill: bad arguments");
     RC(model_ready(s->m));
     CHECK_INJECT("prefill");
     std::lock_guard<std::mutex> lk(s->m->ctx->mu);
+    RC(seq_idle(s, "pocr_prefill"));
     HIP_TRY(hipSetDevice(s->m->ctx->device));
     if (s->len + n > s->cap) return fail(POCR_ERR_ARG, "pocr_prefill: %d rows exceed capacity", n);
     return prefill_locked(s, n, emb, pos3, logits, token);
@@ -1874,6 +2108,7 @@ extern "C" int pocr_generate(pocr_seq *s, const int32_t *ids, int n_ids, const f
     RC(model_ready(s->m));
     CHECK_INJECT("generate");
     std::lock_guard<std::mutex> lk(s->m->ctx->mu);
+    RC(seq_idle(s, "pocr_generate"));
     HIP_TRY(hipSetDevice(s->m->ctx->device));
     return generate_locked(s, ids, n_ids, image_embeds, false, n_image, image_token_id, grid, merge, max_new, eos,
                            n_eos, use_prefill, out_tokens);
@@ -1957,6 +2192,7 @@ extern "C" int pocr_generate_vision(pocr_seq *s, pocr_projector *proj, const int
     RC(model_ready(s->m));
     CHECK_INJECT("generate");
     std::lock_guard<std::mutex> lk(s->m->ctx->mu);
+    RC(seq_idle(s, "pocr_generate_vision"));
     HIP_TRY(hipSetDevice(s->m->ctx->device));
     const float *rows_dev = nullptr;
     int n_image = 0;

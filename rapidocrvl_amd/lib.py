@@ -110,6 +110,12 @@ _SIGS = {
     "pocr_gguf_meta": (_i, [_vp, _i, C.POINTER(C.c_char_p), C.POINTER(C.c_uint32), C.POINTER(C.c_uint64),
                             C.POINTER(C.c_char_p)]),
     "pocr_model_load_gguf": (_i, [_vp, C.POINTER(PocrConfig), C.c_char_p, C.POINTER(_vp)]),
+    "pocr_batch_create": (_i, [_vp, C.POINTER(_vp)]),
+    "pocr_batch_destroy": (None, [_vp]),
+    "pocr_batch_join": (_i, [_vp, _vp, C.c_int32, C.c_int32, _i, _vp, _i]),
+    "pocr_batch_step": (_i, [_vp, _i]),
+    "pocr_batch_poll": (_i, [_vp, _vp, C.POINTER(_i)]),
+    "pocr_batch_leave": (_i, [_vp, _vp, _vp, _i]),
 }
 
 _lib = None
@@ -193,6 +199,46 @@ def decode_batch(seqs, first_tokens, first_positions, max_new: int, eos=(2,)):
     check(load().pocr_decode_batch(C.cast(handles, C.c_void_p), n, _ptr(ft), _ptr(fp), max_new, _ptr(eos),
                                    eos.size, _ptr(out), _ptr(counts)))
     return [out[i, :counts[i]] for i in range(n)]
+
+
+class Batch:
+    """Continuous batching (pocr_batch_*): prefilled sequences of one model
+    join and leave between token steps; up to four decode together."""
+
+    def __init__(self, model: "Model"):
+        h = _vp()
+        check(load().pocr_batch_create(model.h, C.byref(h)))
+        self.h, self.model = h, model
+        self._budget = {}
+
+    def close(self):
+        if getattr(self, "h", None):
+            load().pocr_batch_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def join(self, seq: "Sequence", first_token: int, first_pos: int, max_new: int, eos=(2,)):
+        e = np.ascontiguousarray(list(eos), dtype=np.int32)
+        check(load().pocr_batch_join(self.h, seq.h, first_token, first_pos, max_new, _ptr(e) if e.size else None,
+                                     e.size))
+        self._budget[seq.h.value] = max_new
+
+    def step(self, max_steps: int = 16) -> int:
+        """Runs up to max_steps token steps; returns the members still decoding."""
+        return check(load().pocr_batch_step(self.h, max_steps))
+
+    def poll(self, seq: "Sequence"):
+        done = C.c_int()
+        n = check(load().pocr_batch_poll(self.h, seq.h, C.byref(done)))
+        return n, bool(done.value)
+
+    def leave(self, seq: "Sequence") -> np.ndarray:
+        cap = self._budget.pop(seq.h.value, 0)
+        out = np.zeros(max(cap, 1), np.int32)
+        n = check(load().pocr_batch_leave(self.h, seq.h, _ptr(out), cap))
+        return out[:min(n, cap)]
 
 
 def device_count() -> int:

@@ -39,6 +39,12 @@ def test_null_arguments_are_arg_errors():
     assert L.pocr_gguf_meta(None, 0, None, None, None, None) == lib.POCR_ERR_ARG
     assert L.pocr_model_load_gguf(None, None, b"x", None) == lib.POCR_ERR_ARG
     L.pocr_gguf_close(None)
+    assert L.pocr_batch_create(None, None) == lib.POCR_ERR_ARG
+    assert L.pocr_batch_join(None, None, 0, 0, 1, None, 0) == lib.POCR_ERR_ARG
+    assert L.pocr_batch_step(None, 1) == lib.POCR_ERR_ARG
+    assert L.pocr_batch_poll(None, None, None) == lib.POCR_ERR_ARG
+    assert L.pocr_batch_leave(None, None, None, 0) == lib.POCR_ERR_ARG
+    L.pocr_batch_destroy(None)
 
 
 def test_fault_injection_is_reported_before_device_work(monkeypatch):

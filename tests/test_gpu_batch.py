@@ -93,3 +93,121 @@ def test_decode_batch_ernie_images(orc, ctx):
     got = lib.decode_batch(seqs, firsts, poss, n_new, eos=())
     for i in range(4):
         assert list(got[i]) == want[i], i
+
+
+# ---- continuous batching (pocr_batch_*) --------------------------------------
+
+def _oracle_streams(om, prompts, n_new, eos=()):
+    return [list(om.generate(ids, n_new, eos=eos)) for ids in prompts]
+
+
+def test_continuous_batch_staggered_joins(orc, ctx):
+    # members join at different token steps and with different budgets; each
+    # stream equals its single-sequence greedy stream
+    om, gm = _models(orc, ctx, MID, Q4, seed=7)
+    lens, budgets = [11, 26, 7, 33, 19], [14, 9, 20, 6, 12]
+    prompts = [synth.prompt_ids(n, seed=60 + i, high=MID.vocab) for i, n in enumerate(lens)]
+    want = [list(om.generate(ids, b, eos=())) for ids, b in zip(prompts, budgets)]
+    b = lib.Batch(gm)
+    seqs = []
+    for i in range(5):
+        s, f = _prefilled(gm, prompts[i], budgets[i])
+        seqs.append((s, f))
+    got = {}
+    b.join(seqs[0][0], seqs[0][1], lens[0], budgets[0], eos=())
+    assert b.step(3) == 1
+    b.join(seqs[1][0], seqs[1][1], lens[1], budgets[1], eos=())
+    b.join(seqs[2][0], seqs[2][1], lens[2], budgets[2], eos=())
+    assert b.step(2) == 3
+    b.join(seqs[3][0], seqs[3][1], lens[3], budgets[3], eos=())
+    with pytest.raises(lib.PocrError):  # four members are decoding
+        b.join(seqs[4][0], seqs[4][1], lens[4], budgets[4], eos=())
+    pending = [0, 1, 2, 3]
+    joined_last = False
+    for _ in range(100):
+        left = b.step(4)
+        for i in list(pending):
+            n, done = b.poll(seqs[i][0])
+            assert n <= budgets[i]
+            if done:
+                got[i] = list(b.leave(seqs[i][0]))
+                pending.remove(i)
+        if not joined_last and len(pending) < 4:
+            b.join(seqs[4][0], seqs[4][1], lens[4], budgets[4], eos=())
+            pending.append(4)
+            joined_last = True
+        if not pending:
+            break
+        assert left >= 0
+    assert sorted(got) == [0, 1, 2, 3, 4]
+    for i in range(5):
+        assert got[i] == want[i], i
+        assert len(seqs[i][0]) == lens[i] + budgets[i] - 1
+    b.close()
+
+
+def test_continuous_batch_eos_and_leave_early(orc, ctx):
+    om, gm = _models(orc, ctx, MID, Q6, seed=8)
+    prompts = [synth.prompt_ids(n, seed=80 + n, high=MID.vocab) for n in (15, 22, 9)]
+    full = _oracle_streams(om, prompts, 18)
+    stop = full[0][4]
+    b = lib.Batch(gm)
+    seqs = [_prefilled(gm, ids, 18) for ids in prompts]
+    for (s, f), ids in zip(seqs, prompts):
+        b.join(s, f, ids.size, 18, eos=(stop,))
+    b.step(2)
+    # sequence 2 is cancelled after two steps: it has its first tokens only
+    early = list(b.leave(seqs[2][0]))
+    assert 1 <= len(early) <= 3 and early == full[2][:len(early)]
+    while b.step(16):
+        pass
+    for i in (0, 1):
+        exp = full[i][: full[i].index(stop) + 1] if stop in full[i] else full[i]
+        n, done = b.poll(seqs[i][0])
+        assert done and n == len(exp)
+        assert list(b.leave(seqs[i][0])) == exp
+    # a left sequence takes ordinary calls again
+    seqs[2][0].reset()
+    assert b.step(4) == 0
+    b.close()
+
+
+def test_continuous_batch_rules(ctx):
+    gm = lib.Model(ctx, MID)
+    gm.load_weights(synth.make_weights(MID, Q4, seed=2))
+    b = lib.Batch(gm)
+    s = gm.seq(16)
+    ids = synth.prompt_ids(4, seed=1, high=MID.vocab)
+    first = int(s.generate(ids, 1, eos=(), use_prefill=True)[0])
+    with pytest.raises(lib.PocrError):  # more tokens than the capacity
+        b.join(s, first, 4, 20, eos=())
+    b.join(s, first, 4, 6, eos=())
+    with pytest.raises(lib.PocrError):  # already a member
+        b.join(s, first, 4, 6, eos=())
+    with pytest.raises(lib.PocrError):  # members take no other generation call
+        s.generate(ids, 2, eos=())
+    with pytest.raises(lib.PocrError):
+        s.reset()
+    # one token is done at the join, with no device step
+    t = gm.seq(16)
+    first_t = int(t.generate(ids, 1, eos=(), use_prefill=True)[0])
+    b.join(t, first_t, 4, 1, eos=())
+    assert b.poll(t) == (1, True)
+    assert list(b.leave(t)) == [first_t]
+    # a sampling sequence cannot join
+    u = gm.seq(16)
+    u.set_sampling(0.8, 8, 3)
+    with pytest.raises(lib.PocrError) as e:
+        b.join(u, first, 4, 4, eos=())
+    assert e.value.code == lib.POCR_ERR_UNSUPPORTED
+    # destroying a member removes it; the batch carries on
+    b.step(1)
+    s.close()
+    assert b.step(4) == 0
+    other = lib.Model(ctx, MID)
+    other.load_weights(synth.make_weights(MID, Q4, seed=2))
+    w = other.seq(16)
+    with pytest.raises(lib.PocrError):  # a sequence of another model
+        b.join(w, first, 4, 4, eos=())
+    b.close()
+    other.close()
