@@ -85,8 +85,9 @@ def test_prefill_after_cached_rows(orc, ctx, qtype):
     _check_kv(gs, os_, MID, 42)
 
 
-@pytest.mark.parametrize("n", [1, 2, 33, 130])
+@pytest.mark.parametrize("n", [1, 2, 33, 130, 270, 300])
 def test_prefill_lengths(orc, ctx, n):
+    # 270 and 300 tokens: several 32-token tiles, the last one partly padding
     w, om, gm = _pair(orc, ctx, MID, Q4)
     ids = synth.prompt_ids(n, seed=n, high=MID.vocab)
     pos = np.array([[p, p, p] for p in range(n)], np.int32)
@@ -114,7 +115,7 @@ def test_prefill_image_generation_ernie(orc, ctx):
 
 
 @pytest.mark.parametrize("qtype", [Q8, Q4, Q6], ids=["q8", "q4", "q6"])
-@pytest.mark.parametrize("m", [4, 16, 33, 100])
+@pytest.mark.parametrize("m", [4, 16, 33, 100, 256, 270, 513])
 def test_batched_matvec_mfma_shapes(ctx, orc, rng, qtype, m):
     # the MFMA batched GEMV at the decoder's shapes; 1088 rows leave idle waves
     # in the last workgroup, 320 columns are not whole 256-column LDS stages
