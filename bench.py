@@ -291,6 +291,16 @@ def lm_head_roofline(ctx, lmq, target_bytes=600 << 20):
     return us, alg, alg / us / 1e3
 
 
+def stream_read_ceiling(ctx, nbytes, target_bytes=600 << 20):
+    """A plain 16-byte streaming read of nbytes (rounded up to 16) timed the
+    same way as the GEMV (rotating buffers past the Infinity Cache, median of
+    5 batches): the ceiling a single launch of that size reaches on this chip."""
+    nbytes = (nbytes + 15) // 16 * 16
+    n = max(2, int(np.ceil(target_bytes / nbytes)))
+    trials = sorted(ctx.time_stream_read(nbytes, n, max(4 * n, 200)) for _ in range(5))
+    return trials[len(trials) // 2]
+
+
 def measured_traffic():
     """HBM bytes per launch of the roofline kernel, from the committed
     rocprofv3 FETCH_SIZE/WRITE_SIZE passes (scaled by the copy-kernel factor)."""
@@ -336,11 +346,13 @@ def roofline_only(args):
     lmq = lm_head_q4(cfg)
     us, alg, achieved = lm_head_roofline(ctx, lmq)
     log(f"[bench] q4 lm_head gemv {us:.2f} us → {achieved:.0f} GB/s")
+    stream_us = stream_read_ceiling(ctx, int(alg))
     if args.calibrate_copy:
         copy_calibration()
     print(json.dumps({"kernel": "q4 lm_head greedy gemv (argmax) 103424x1024 m=1", "us_per_launch": round(us, 3),
                       "algorithmic_bytes": int(alg), "achieved_GB_s": round(achieved, 1),
-                      "frac": round(achieved / HBM_PEAK_GBS, 4)}), flush=True)
+                      "frac": round(achieved / HBM_PEAK_GBS, 4), "stream_read_us": round(stream_us, 3),
+                      "frac_of_stream_read": round(stream_us / us, 4)}), flush=True)
 
 
 def cpu_baseline(cfg, weights, gpu_seq, first_tok, first_pos, gpu_tokens, n_prefix, budget_s=12.0):
@@ -483,6 +495,8 @@ def main():
     lmq = lib.QMatrix(lm_qt, lm_sc.size, lm_cols, lm_sc, lm_data)
     us, alg, achieved = lm_head_roofline(ctx, lmq)
     log(f"[bench] q4 lm_head gemv {us:.2f} us → {achieved:.0f} GB/s")
+    stream_us = stream_read_ceiling(ctx, int(alg))
+    log(f"[bench] plain streaming read of the same {alg} bytes: {stream_us:.2f} us")
 
     cpu = None
     if not args.no_cpu:
@@ -546,7 +560,9 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                      "kernel": "q4 lm_head greedy gemv (argmax) 103424x1024 m=1", "us_per_launch": round(us, 3),
-                     "algorithmic_bytes": int(alg)},
+                     "algorithmic_bytes": int(alg),
+                     # a bare 16-byte streaming read of the same bytes, timed the same way
+                     "stream_read_us": round(stream_us, 3), "frac_of_stream_read": round(stream_us / us, 4)},
         "decode_effective_GB_s": round(per_token_bytes * tok_s / 1e9, 1),
         "cpu_baseline": cpu,
     }

@@ -192,6 +192,13 @@ int pocr_time_matvec_batched(pocr_ctx *ctx, const pocr_weight *const *weights, i
 int pocr_time_attention(pocr_ctx *ctx, int heads, int kv_heads, int head_dim, int cache_len, int n_layers, int iters,
                         float *avg_us);
 
+/* Average device time (microseconds) of a plain streaming read of `bytes`
+ * (a multiple of 16) from one of n_buffers device buffers, rotating so the
+ * working set can exceed the Infinity Cache: the read ceiling a
+ * weight-streaming kernel of the same size is compared with.  No counterpart
+ * in the reference (a measurement aid); allocates and frees its buffers. */
+int pocr_time_stream_read(pocr_ctx *ctx, int64_t bytes, int n_buffers, int iters, float *avg_us);
+
 /* ---------------- model / step level (device-resident) ---------------- */
 int pocr_model_create(pocr_ctx *ctx, const pocr_config *cfg, pocr_model **out);
 void pocr_model_destroy(pocr_model *m);

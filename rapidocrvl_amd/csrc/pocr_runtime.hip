@@ -1362,6 +1362,84 @@ extern "C" int pocr_time_attention(pocr_ctx *ctx, int heads, int kv_heads, int h
     return POCR_OK;
 }
 
+// The read ceiling a weight-streaming kernel is measured against: every
+// workgroup reads 16-byte nontemporal chunks of one buffer in a grid-stride
+// loop (4 in flight per lane) and folds them into one xor per workgroup.
+static __global__ void __launch_bounds__(kThreads) k_stream_read(const uint4 *p, size_t n16, unsigned *out) {
+    constexpr int U = 4;
+    typedef unsigned u4v __attribute__((ext_vector_type(4)));
+    const u4v *q = reinterpret_cast<const u4v *>(p);
+    const size_t stride = (size_t)gridDim.x * kThreads * U;
+    size_t i = (size_t)blockIdx.x * kThreads * U + threadIdx.x;
+    unsigned acc = 0;
+    for (; i + (U - 1) * kThreads < n16; i += stride) {
+        u4v v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) v[u] = __builtin_nontemporal_load(q + i + u * kThreads);
+#pragma unroll
+        for (int u = 0; u < U; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    }
+    for (; i < n16; i += kThreads) acc ^= q[i].x ^ q[i].y ^ q[i].z ^ q[i].w;
+    __shared__ unsigned sh[kThreads];
+    sh[threadIdx.x] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        unsigned a = 0;
+        for (int t = 0; t < kThreads; ++t) a ^= sh[t];
+        out[blockIdx.x] = a;
+    }
+}
+
+extern "C" int pocr_time_stream_read(pocr_ctx *ctx, int64_t bytes, int n_buffers, int iters, float *avg_us) {
+    if (!ctx || bytes < 16 || bytes % 16 || n_buffers <= 0 || n_buffers > 64 || iters <= 0 || !avg_us)
+        return fail(POCR_ERR_ARG, "pocr_time_stream_read: bad arguments");
+    CHECK_INJECT("time_stream_read");
+    CTX_GUARD(ctx);
+    hipStream_t s = ctx->stream;
+    constexpr int kGrid = 2048;
+    std::vector<void *> bufs(n_buffers, nullptr);
+    unsigned *out = nullptr;
+    auto release = [&] {
+        (void)hipStreamSynchronize(s);
+        for (void *b : bufs)
+            if (b) (void)hipFree(b);
+        if (out) (void)hipFree(out);
+    };
+    hipError_t e = hipMalloc(&out, kGrid * sizeof(unsigned));
+    for (int i = 0; i < n_buffers && e == hipSuccess; ++i) {
+        e = hipMalloc(&bufs[i], (size_t)bytes);
+        if (e == hipSuccess) e = hipMemsetAsync(bufs[i], 1, (size_t)bytes, s);
+    }
+    if (e != hipSuccess) {
+        release();
+        return fail(POCR_ERR_NOMEM, "pocr_time_stream_read: %s", hipGetErrorString(e));
+    }
+    const size_t n16 = (size_t)bytes / 16;
+    auto launch = [&](int i) {
+        hipLaunchKernelGGL(k_stream_read, dim3(kGrid), dim3(kThreads), 0, s,
+                           static_cast<const uint4 *>(bufs[i % n_buffers]), n16, out);
+    };
+    for (int i = 0; i < n_buffers; ++i) launch(i);
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    float ms = 0.0f;
+    e = hipEventCreate(&e0);
+    if (e == hipSuccess) e = hipEventCreate(&e1);
+    if (e == hipSuccess) e = hipEventRecord(e0, s);
+    if (e == hipSuccess) {
+        for (int it = 0; it < iters; ++it) launch(it);
+        e = hipEventRecord(e1, s);
+    }
+    if (e == hipSuccess) e = hipEventSynchronize(e1);
+    if (e == hipSuccess) e = hipGetLastError();
+    if (e == hipSuccess) e = hipEventElapsedTime(&ms, e0, e1);
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    release();
+    if (e != hipSuccess) return fail(POCR_ERR_DEVICE, "pocr_time_stream_read: %s", hipGetErrorString(e));
+    *avg_us = ms * 1000.0f / (float)iters;
+    return POCR_OK;
+}
+
 // ---------------------------------------------------------------------------
 // the decoder step on the device
 // ---------------------------------------------------------------------------

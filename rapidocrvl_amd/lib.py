@@ -92,6 +92,7 @@ _SIGS = {
     "pocr_time_matvec_argmax": (_i, [_vp, _vp, _i, _vp, _i, _vp]),
     "pocr_time_matvec_batched": (_i, [_vp, _vp, _i, _vp, _i, _i, _vp]),
     "pocr_time_attention": (_i, [_vp, _i, _i, _i, _i, _i, _i, _vp]),
+    "pocr_time_stream_read": (_i, [_vp, C.c_int64, _i, _i, _vp]),
     "pocr_seq_write_kv": (_i, [_vp, _i, _vp, _vp, _i]),
     "pocr_step": (_i, [_vp, _vp, _vp, _i, _vp, _vp]),
     "pocr_prefill": (_i, [_vp, _i, _vp, _vp, _vp, _vp]),
@@ -409,6 +410,12 @@ class Context:
         """Average µs of one decode-attention call over cache_len rows."""
         us = np.zeros(1, np.float32)
         check(load().pocr_time_attention(self.h, heads, kv_heads, head_dim, cache_len, n_layers, iters, _ptr(us)))
+        return float(us[0])
+
+    def time_stream_read(self, nbytes, n_buffers, iters):
+        """Average µs of a plain streaming read of nbytes, rotating over n_buffers buffers."""
+        us = np.zeros(1, np.float32)
+        check(load().pocr_time_stream_read(self.h, nbytes, n_buffers, iters, _ptr(us)))
         return float(us[0])
 
     def text_attention(self, q, k_cache, v_cache, cache_len, heads, kv_heads, head_dim):
