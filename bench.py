@@ -81,7 +81,21 @@ def batch_decode(model, cfg, n_seq=4, n_new=1024, reps=2):
 SERVE_BUDGETS = (512, 128, 384, 256, 640, 192, 448, 320)
 
 
-def serve(model, cfg, budgets=SERVE_BUDGETS, slots=4, chunk=16):
+_EMBED = {}
+
+
+def model_embed(model, tok):
+    """Embedding row of a token of the bench's synthetic Q4 model (seed 0)."""
+    from rapidocrvl_amd import synth
+
+    key = id(model)
+    if key not in _EMBED:
+        _EMBED.clear()
+        _EMBED[key] = synth.normal((model.cfg.vocab, model.cfg.hidden), [0, 1000, 2])
+    return _EMBED[key][tok]
+
+
+def serve(model, cfg, budgets=SERVE_BUDGETS, slots=4, chunk=16, seed0=300):
     """Server-style serving of len(budgets) image requests (5 ids + 1332 visual
     rows + 11 ids, seeds 300+i; request i generates budgets[i] greedy tokens):
     one request at a time (prefill, then its own decode loop: the reference
@@ -94,10 +108,10 @@ def serve(model, cfg, budgets=SERVE_BUDGETS, slots=4, chunk=16):
     grid = (1, 72, 74)
     reqs = []
     for i, n in enumerate(budgets):
-        ids = np.concatenate([synth.prompt_ids(5, seed=300 + i), np.full(1332, IMAGE_TOKEN, np.int32),
-                              synth.prompt_ids(11, seed=400 + i)]).astype(np.int32)
+        ids = np.concatenate([synth.prompt_ids(5, seed=seed0 + i), np.full(1332, IMAGE_TOKEN, np.int32),
+                              synth.prompt_ids(11, seed=seed0 + 100 + i)]).astype(np.int32)
         _, delta = lib.mm_positions(ids, IMAGE_TOKEN, grid)
-        reqs.append((ids, synth.image_embeds(1332, cfg.hidden, seed=300 + i), ids.size + delta, n))
+        reqs.append((ids, synth.image_embeds(1332, cfg.hidden, seed=seed0 + i), ids.size + delta, n))
     seqs = [model.seq(ids.size + n + 8) for ids, _, _, n in reqs]
 
     def first_token(s, ids, img):
@@ -127,6 +141,23 @@ def serve(model, cfg, budgets=SERVE_BUDGETS, slots=4, chunk=16):
                 members.remove(i)
     t_cb = time.perf_counter() - t
     b.close()
+    # a request whose two streams differ: the single-sequence logits at the
+    # first differing token, top-2 gap (greedy choice between near-equal logits)
+    differ = []
+    for i in range(len(reqs)):
+        if got[i] == one[i]:
+            continue
+        k = next(j for j in range(len(one[i])) if j >= len(got[i]) or got[i][j] != one[i][j])
+        ids, img, pos, n = reqs[i]
+        s = seqs[i]
+        toks = list(s.decode_greedy(first_token(s, ids, img), pos, k, eos=())) if k > 0 else []
+        gap = None
+        if k > 0:
+            _, lg = s.step(model_embed(model, toks[k - 1]), (pos + k - 1,) * 3)
+            t2 = np.sort(lg)[-2:]
+            gap = float(t2[1] - t2[0])
+        differ.append({"request": i, "token": k, "of": n, "single_top2_gap": gap,
+                       "single_top2_rel_gap": None if gap is None else gap / max(abs(float(t2[1])), 1e-30)})
     for s in seqs:
         s.close()
     total = sum(budgets)
@@ -134,7 +165,7 @@ def serve(model, cfg, budgets=SERVE_BUDGETS, slots=4, chunk=16):
             "one_at_a_time": {"s": round(t_one, 3), "tok_s": round(total / t_one, 1)},
             "continuous_batch": {"s": round(t_cb, 3), "tok_s": round(total / t_cb, 1)},
             "speedup": round(t_one / t_cb, 2),
-            "tokens_match": all(got[i] == one[i] for i in range(len(reqs)))}
+            "tokens_match": not differ, "differ": differ}
 
 
 def build_model(ctx, cfg, qtype, seed=0):
@@ -439,6 +470,7 @@ def main():
     ap.add_argument("--projector-only", action="store_true", help="time only the vision projector")
     ap.add_argument("--serve-only", action="store_true", help="time only the 8-request serving comparison")
     ap.add_argument("--batch-tokens", type=int, default=1024, help="tokens per sequence of the batched decode")
+    ap.add_argument("--batch-seqs", default="4,8,16", help="with --batch-only: batch sizes to time")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the decoder step runs on a single MI355X "
@@ -457,12 +489,15 @@ def main():
         return
     if args.batch_only:
         _, model = build_model(ctx, cfg, lib.Q4)
-        print(json.dumps({"workload": "4-sequence q4 batched greedy decode",
-                          **batch_decode(model, cfg, n_new=args.batch_tokens, reps=1)}), flush=True)
+        for n in (int(v) for v in args.batch_seqs.split(",")):
+            print(json.dumps({"workload": f"{n}-sequence q4 batched greedy decode",
+                              **batch_decode(model, cfg, n_seq=n, n_new=args.batch_tokens, reps=1)}), flush=True)
         return
     if args.serve_only:
         _, model = build_model(ctx, cfg, lib.Q4)
         print(json.dumps({"workload": "q4 serving of 8 image requests", **serve(model, cfg)}), flush=True)
+        print(json.dumps({"workload": "q4 serving of 24 image requests, 16 slots",
+                          **serve(model, cfg, budgets=SERVE_BUDGETS * 3, slots=16)}), flush=True)
         return
     ids = workload_ids()
     img = synth.image_embeds(1332, cfg.hidden, seed=0)
@@ -507,8 +542,12 @@ def main():
     if not args.no_batch:
         extra["batch4_decode"] = {"q4": batch_decode(model, cfg, n_new=args.batch_tokens)}
         log(f"[bench] 4-sequence batched decode q4 {extra['batch4_decode']['q4']}")
+        extra["batch_wide_decode"] = {str(n): batch_decode(model, cfg, n_seq=n, n_new=512) for n in (8, 16)}
+        log(f"[bench] 8/16-sequence batched decode q4 {extra['batch_wide_decode']}")
         extra["serving_q4"] = serve(model, cfg)
         log(f"[bench] serving q4 {extra['serving_q4']}")
+        extra["serving_q4_16slots"] = serve(model, cfg, budgets=SERVE_BUDGETS * 3, slots=16)
+        log(f"[bench] serving q4, 16 slots {extra['serving_q4_16slots']}")
         _, m6 = build_model(ctx, cfg, lib.Q6)
         extra["batch4_decode"]["q6"] = batch_decode(m6, cfg, n_new=args.batch_tokens)
         log(f"[bench] 4-sequence batched decode q6 {extra['batch4_decode']['q6']}")

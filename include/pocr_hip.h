@@ -253,22 +253,26 @@ int pocr_prefill(pocr_seq *s, int n, const float *emb, const int32_t *pos3, floa
  * number of tokens written (>=0) or an error status (<0). */
 int pocr_decode_greedy(pocr_seq *s, int32_t first_token, int32_t first_pos, int max_new,
                        const int32_t *eos, int n_eos, int32_t *out_tokens);
-/* greedy decode of n_seq (1..4) sequences of one model together: the
+/* greedy decode of n_seq (1..16) sequences of one model together: the
  * server's concurrent requests (cmd/paddleocrvl-server/main.go:1106, one
  * decode loop each, model.go:1538-1568) batched into one device step — each
  * layer's weights stream once for all of them (M = n_seq batched GEMV), each
  * sequence keeps its own KV cache.  Sequence i starts from first_tokens[i] at
  * first_positions[i]; its tokens go to out_tokens[i*max_new ...] (first token
  * first), out_counts[i] of them, stopping after an EOS id.  Per-sequence
- * results equal pocr_decode_greedy's up to f32 summation order. */
+ * results equal pocr_decode_greedy's up to f32 summation order.  Up to 4
+ * sequences share GEMV passes; 5..16 need layer matrices with rows a
+ * multiple of 16 and inputs a multiple of 256 (POCR_ERR_UNSUPPORTED
+ * otherwise). */
 int pocr_decode_batch(pocr_seq *const *seqs, int n_seq, const int32_t *first_tokens,
                       const int32_t *first_positions, int max_new, const int32_t *eos, int n_eos,
                       int32_t *out_tokens, int32_t *out_counts);
 /* continuous batching: a decode batch that requests join and leave between
  * token steps, in place of the server's per-request slots, each running its
  * own decode loop (cmd/paddleocrvl-server/main.go:1106-1124, acquire/release;
- * model.go:1538-1568).  Up to 4 members decode at once, one batched device
- * step per token as in pocr_decode_batch; each member's tokens equal its
+ * model.go:1538-1568).  As many members decode at once as pocr_decode_batch
+ * takes sequences (16, or 4 for models outside the wide step's shapes), one
+ * batched device step per token; each member's tokens equal its
  * pocr_decode_greedy stream.  A batch is driven by one thread; a member
  * sequence accepts no other generation or cache call until it leaves
  * (POCR_ERR_ARG), and destroying it removes it from the batch. */
@@ -277,7 +281,8 @@ void pocr_batch_destroy(pocr_batch *b);
 /* a prefilled sequence joins with the token its prefill chose, at position
  * first_pos, for at most max_new tokens (first_token counted) and the EOS
  * ids given; greedy sequences only (POCR_ERR_UNSUPPORTED otherwise).
- * POCR_ERR_ARG if 4 members are still decoding or the capacity is short. */
+ * POCR_ERR_ARG if the batch's limit of members is decoding or the capacity
+ * is short. */
 int pocr_batch_join(pocr_batch *b, pocr_seq *s, int32_t first_token, int32_t first_pos, int max_new,
                     const int32_t *eos, int n_eos);
 /* up to max_steps token steps for every decoding member (fewer when a

@@ -189,7 +189,8 @@ struct GemmParams {
     float *h;              // OPROJ / DOWN residual rows [n][rows]
     float *vbuf;           // [n][rows]
     int quirk;             // OPROJ: Q4/Q6 residual behaviour
-    int clen0;             // cache rows before token 0
+    int clen0;             // cache rows before token 0 (one sequence's rows)
+    StepState *const *rst; // [n] step state of row n (batched decode: rows are sequences), or null
     int last;              // DOWN: last layer → vbuf = h + y (h untouched)
     const float *bias;     // BIAS / BIAS_GELU: [rows]
 };
@@ -219,8 +220,9 @@ __device__ __forceinline__ v4i load_codes16(const uint8_t *rowp, int k) {
 
 __device__ __forceinline__ bool prefill_in_place(const GemmParams &p, int n) {
     // model.go:3895-3902, 4051-4057: Q4/Q6 take the OutOnly variant at cache
-    // length 0 and ≥ 6
-    const int clen = p.clen0 + n;
+    // length 0 and ≥ 6; row n is token clen0 + n of one sequence, or the
+    // current token of sequence n in a batched decode step
+    const int clen = p.rst ? p.rst[n]->clen : p.clen0 + n;
     return !(p.quirk && (clen == 0 || clen >= 6));
 }
 

@@ -188,6 +188,9 @@ struct DigitizeParams;
 struct GemmParams;
 int digitize_rows(hipStream_t s, int qtype, const DigitizeParams &p, int n);
 int gemm_rows(hipStream_t s, int qtype, int nmat, const GemmParams &p, int epi, int npad);
+// the small MFMA GEMM over at most 16 rows (digit planes of 16 rows)
+bool gemm_small_ok(int rows, int K);
+int gemm_small_rows(hipStream_t s, int qtype, int nmat, const GemmParams &p, int epi);
 // vision projector (projector.hip); callers hold the context lock
 int project_locked(pocr_projector *p, int grid_t, int grid_h, int grid_w, int *rows);
 int project_upload_locked(pocr_projector *p, const float *vision_rows, int grid_t, int grid_h, int grid_w,

@@ -779,6 +779,7 @@ struct GemvNV {
     StepState *stv[3];
 };
 constexpr int kMaxNV = 4;
+constexpr int kMaxBatch = 16;  // sequences of one batched decode step
 
 __device__ __forceinline__ unsigned long long argmax_key(float v, int row) {
     uint32_t b = __float_as_uint(v);
@@ -1327,18 +1328,24 @@ static __global__ void __launch_bounds__(kThreads) k_step_begin(StepState *st, c
 // Greedy decode of several sequences in one step: workgroup b runs sequence
 // b's prologue (mode 1) and writes its embedding row to h + b·hidden.
 struct StepBatch {
-    StepState *st[kMaxNV];
-    int32_t *tokens[kMaxNV];
-    int max_tokens[kMaxNV];
+    StepState *st[kMaxBatch];
+    int32_t *tokens[kMaxBatch];
+    int max_tokens[kMaxBatch];
 };
+// b is the kernel's first argument (offset 0 of the argument segment): entry
+// blockIdx.x is read in place with scalar loads.  The argument segment exists
+// in the device pass only.
+typedef __attribute__((address_space(4))) const StepBatch KernargStepBatch;
 static __global__ void __launch_bounds__(kThreads) k_step_begin_multi(StepBatch b, const float *embed, float *h,
                                                                  int hidden, int vocab, const double *freq,
                                                                  const uint8_t *axis) {
+    (void)b;
+#if defined(__HIP_DEVICE_COMPILE__)
+    const KernargStepBatch *kb = (KernargStepBatch *)__builtin_amdgcn_kernarg_segment_ptr();
     const int i = blockIdx.x;
-    StepState *st = i == 0 ? b.st[0] : (i == 1 ? b.st[1] : (i == 2 ? b.st[2] : b.st[3]));
-    int32_t *tok = i == 0 ? b.tokens[0] : (i == 1 ? b.tokens[1] : (i == 2 ? b.tokens[2] : b.tokens[3]));
-    const int mt = i == 0 ? b.max_tokens[0] : (i == 1 ? b.max_tokens[1] : (i == 2 ? b.max_tokens[2] : b.max_tokens[3]));
-    step_begin_body(st, embed, h + (size_t)i * hidden, hidden, vocab, freq, axis, 1, tok, mt);
+    step_begin_body(kb->st[i], embed, h + (size_t)i * hidden, hidden, vocab, freq, axis, 1, kb->tokens[i],
+                    kb->max_tokens[i]);
+#endif
 }
 
 // ---------------------------------------------------------------------------
@@ -1759,8 +1766,9 @@ static __global__ void __launch_bounds__(kMergeThreads) k_attn_merge(AttnParams 
 // sequence's parameters (its cache, step state, partials, q and output rows);
 // splits past a sequence's own count exit at once.
 struct AttnMulti {
-    AttnParams a[kMaxNV];
+    AttnParams a[kMaxBatch];
 };
+static_assert(sizeof(AttnMulti) <= 4096, "kernel arguments of the batched attention");
 // b is the kernel's only argument (offset 0 of the argument segment): entry
 // blockIdx.z is read in place with scalar loads (a select over the array
 // would copy it to scratch).  The argument segment exists in the device pass.

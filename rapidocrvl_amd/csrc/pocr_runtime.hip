@@ -7,6 +7,7 @@
 // after token without host round trips.
 #include <cmath>
 
+#include "gemm.hpp"
 #include "internal.hpp"
 
 namespace pocr {
@@ -1694,7 +1695,7 @@ extern "C" int pocr_decode_greedy(pocr_seq *s, int32_t first_token, int32_t firs
 }
 
 // ---------------------------------------------------------------------------
-// Batched greedy decode: up to kMaxNV sequences of one model advance together.
+// Batched greedy decode: up to kMaxBatch sequences of one model advance together.
 // Every layer GEMV streams its weights once for all of them (NV activation
 // vectors per pass, padded to 2 or 4), attention and its merge run in one
 // launch each with the sequence in blockIdx.z, and each sequence keeps its own
@@ -1706,10 +1707,17 @@ namespace {
 struct DecodeBatch {
     pocr_model *m = nullptr;
     int n = 0;    // sequences
-    int nv = 1;   // vectors per GEMV pass (n padded to 1, 2 or 4)
-    pocr_seq *seq[kMaxNV] = {};
+    int nv = 1;   // vectors per GEMV pass (n ≤ 4: n padded to 1, 2 or 4)
+    int cap = 0;  // vector rows the buffers hold (≥ nv; kMaxBatch for the wide step)
+    pocr_seq *seq[kMaxBatch] = {};
     float *h = nullptr, *v = nullptr, *qkv = nullptr, *ho = nullptr, *g = nullptr;
     StepState *pad = nullptr;  // step state of the padding vectors
+    // wide step (n > 4): digit planes of 16 rows, row scales and sums, and the
+    // rows' step states (the o_proj epilogue reads each sequence's clen)
+    int8_t *xd = nullptr;
+    float *xs = nullptr;
+    int *xb = nullptr;
+    StepState **rst = nullptr;
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
     bool owns = true;  // false: the vector buffers belong to a continuous batch
@@ -1717,18 +1725,133 @@ struct DecodeBatch {
         if (exec) (void)hipGraphExecDestroy(exec);
         if (graph) (void)hipGraphDestroy(graph);
         if (owns)
-            for (void *p : {(void *)h, (void *)v, (void *)qkv, (void *)ho, (void *)g, (void *)pad})
+            for (void *p : {(void *)h, (void *)v, (void *)qkv, (void *)ho, (void *)g, (void *)pad, (void *)xd,
+                            (void *)xs, (void *)xb, (void *)rst})
                 if (p) (void)hipFree(p);
     }
     StepState *st(int i) const { return i < n ? seq[i]->st : pad; }
 };
 
-GemvNV batch_nv(const DecodeBatch &b, int x_stride, int o_stride) {
+// states of the vectors base .. base+3 of a GEMV pass (padding: the dummy state)
+GemvNV batch_nv(const DecodeBatch &b, int x_stride, int o_stride, int base = 0) {
     GemvNV q{};
     q.x_stride = x_stride;
     q.o_stride = o_stride;
-    for (int i = 1; i < kMaxNV; ++i) q.stv[i - 1] = b.st(i);
+    for (int i = 1; i < kMaxNV; ++i) q.stv[i - 1] = b.st(base + i);
     return q;
+}
+
+// Sequences a batch step can take: up to 4 on the GEMV passes, up to 16 when
+// every layer matrix fits the small MFMA GEMM (rows a multiple of 16, K a
+// multiple of 256).
+int batch_limit(const pocr_model *m) {
+    const pocr_config &c = m->cfg;
+    const int Q = c.heads * c.head_dim, KV = c.kv_heads * c.head_dim;
+    const bool wide = gemm_small_ok(Q + 2 * KV, c.hidden) && Q % 16 == 0 && KV % 16 == 0 &&
+                      gemm_small_ok(c.hidden, Q) && gemm_small_ok(c.intermediate, c.hidden) &&
+                      gemm_small_ok(c.hidden, c.intermediate);
+    return wide ? kMaxBatch : kMaxNV;
+}
+
+// digit planes of the batch's n rows of x (RMSNorm·norm_w first if norm_w)
+int batch_digitize(const DecodeBatch &b, int qtype, const float *x, int K, const float *norm_w) {
+    DigitizeParams d{};
+    d.x = x;
+    d.x_stride = K;
+    d.norm_w = norm_w;
+    d.eps = b.m->cfg.rms_norm_eps;
+    d.K = K;
+    d.xd = b.xd;
+    d.plane_stride = (size_t)16 * K;
+    d.xs = b.xs;
+    d.xb = b.xb;
+    return digitize_rows(b.m->ctx->stream, qtype, d, b.n);
+}
+
+GemmParams batch_gemm(const DecodeBatch &b, const pocr_weight *w, int K) {
+    GemmParams p{};
+    p.m[0] = p.m[1] = p.m[2] = dev_mat(w);
+    p.seg_end[0] = p.seg_end[1] = p.seg_end[2] = w->rows;
+    p.rows = w->rows;
+    p.K = K;
+    p.xd = b.xd;
+    p.plane_stride = (size_t)16 * K;
+    p.xs = b.xs;
+    p.xb = b.xb;
+    p.ntok = b.n;
+    p.rst = b.rst;
+    return p;
+}
+
+// One layer of the wide step (5..16 sequences): digit planes of the rows,
+// then the small MFMA GEMM with the prefill epilogues (each row a sequence);
+// attention and its merge as in the narrow step.
+int batch_layer_wide(DecodeBatch &b, const LayerW &L, int li, bool last, int rpw, int max_split) {
+    pocr_model *m = b.m;
+    const pocr_config &c = m->cfg;
+    hipStream_t st = m->ctx->stream;
+    const int H = c.hidden, Q = c.heads * c.head_dim, KV = c.kv_heads * c.head_dim, F = c.intermediate;
+    const int QKV = Q + 2 * KV;
+    const int qt = L.w[POCR_W_Q]->qtype;
+    // 1. RMSNorm(h)·ln1 → q|k|v
+    RC(batch_digitize(b, qt, b.h, H, L.ln1));
+    GemmParams g = batch_gemm(b, L.w[POCR_W_Q], H);
+    g.m[1] = dev_mat(L.w[POCR_W_K]);
+    g.m[2] = dev_mat(L.w[POCR_W_V]);
+    g.seg_end[0] = Q;
+    g.seg_end[1] = Q + KV;
+    g.seg_end[2] = QKV;
+    g.rows = QKV;
+    g.out = b.qkv;
+    g.out_stride = QKV;
+    RC(gemm_small_rows(st, qt, 1, g, G_PLAIN));
+    // 2. RoPE + KV append + split attention, then the merge
+    AttnMulti am{};
+    for (int i = 0; i < b.n; ++i) {
+        pocr_seq *s = b.seq[i];
+        AttnParams &a = am.a[i];
+        a.q = b.qkv + (size_t)i * QKV;
+        a.k_new = a.q + Q;
+        a.v_new = a.q + Q + KV;
+        a.kc = layer_k(s, li);
+        a.vc = layer_v(s, li);
+        a.st = s->st;
+        a.part = s->part;
+        a.head_out = b.ho + (size_t)i * Q;
+        a.heads = c.heads;
+        a.kvh = c.kv_heads;
+        attn_shape(a, s->cap, rpw);
+        a.scale = (float)(1.0 / std::sqrt((double)c.head_dim));
+    }
+    const dim3 ag(c.kv_heads, max_split, b.n);
+    if (rpw == 8) hipLaunchKernelGGL(k_attn_decode_multi<8>, ag, dim3(kThreads), 0, st, am);
+    else hipLaunchKernelGGL(k_attn_decode_multi<16>, ag, dim3(kThreads), 0, st, am);
+    hipLaunchKernelGGL(k_attn_merge_multi, dim3(c.heads, 1, b.n), dim3(kMergeThreads), 0, st, am);
+    HIP_TRY(hipGetLastError());
+    // 3. o_proj + residual (+ the Q4/Q6 behaviour by each sequence's clen)
+    const pocr_weight *wo = L.w[POCR_W_O];
+    RC(batch_digitize(b, wo->qtype, b.ho, Q, nullptr));
+    GemmParams o = batch_gemm(b, wo, Q);
+    o.h = b.h;
+    o.vbuf = b.v;
+    o.quirk = (m->quirk && (wo->qtype == POCR_Q4 || wo->qtype == POCR_Q6)) ? 1 : 0;
+    RC(gemm_small_rows(st, wo->qtype, 1, o, G_OPROJ));
+    // 4. RMSNorm(v)·ln2 → gate/up → SiLU(g)·u
+    const pocr_weight *wg = L.w[POCR_W_GATE];
+    RC(batch_digitize(b, wg->qtype, b.v, H, L.ln2));
+    GemmParams gu = batch_gemm(b, wg, H);
+    gu.m[1] = dev_mat(L.w[POCR_W_UP]);
+    gu.out = b.g;
+    gu.out_stride = F;
+    RC(gemm_small_rows(st, wg->qtype, 2, gu, G_SWIGLU));
+    // 5. down + residual; last layer: v = h + down
+    const pocr_weight *wd = L.w[POCR_W_DOWN];
+    RC(batch_digitize(b, wd->qtype, b.g, F, nullptr));
+    GemmParams d = batch_gemm(b, wd, F);
+    d.h = b.h;
+    d.vbuf = b.v;
+    d.last = last ? 1 : 0;
+    return gemm_small_rows(st, wd->qtype, 1, d, G_DOWN);
 }
 
 int enqueue_batch_step(DecodeBatch &b) {
@@ -1752,9 +1875,14 @@ int enqueue_batch_step(DecodeBatch &b) {
     int rpw = 8, max_split = 1;
     for (int i = 0; i < b.n; ++i) rpw = std::max(rpw, b.seq[i]->rpw);
     for (int i = 0; i < b.n; ++i) max_split = std::max(max_split, attn_nsplit(b.seq[i]->cap, rpw));
+    const bool wide = b.n > kMaxNV;
     for (int li = 0; li < c.layers; ++li) {
         const LayerW &L = m->layers[li];
         const bool last = li + 1 == c.layers;
+        if (wide) {
+            RC(batch_layer_wide(b, L, li, last, rpw, max_split));
+            continue;
+        }
         // 1. RMSNorm(h)·ln1 → q|k|v for every sequence
         GemvParams p{};
         p.m[0] = dev_mat(L.w[POCR_W_Q]);
@@ -1825,14 +1953,20 @@ int enqueue_batch_step(DecodeBatch &b) {
         q = batch_nv(b, F, H);
         RC(gemv_launch(st, d, 1, PRO_COPY, EPI_DOWN, kBigGrid, b.nv, &q));
     }
-    // LM head on RMSNorm(v)·final_norm, argmax into each sequence's state
-    GemvParams lm = gemv_params_1(m->lm);
-    lm.x = b.v;
-    lm.norm_w = m->final_norm;
-    lm.eps = eps;
-    lm.st = b.st(0);
-    GemvNV q = batch_nv(b, H, 0);
-    return gemv_launch(st, lm, 1, PRO_RMSNORM, EPI_ARGMAX, kBigGrid, b.nv, &q);
+    // LM head on RMSNorm(v)·final_norm, argmax into each sequence's state: one
+    // GEMV pass per 4 sequences (the last pass padded to 1, 2 or 4 vectors)
+    for (int base = 0; base < b.n; base += kMaxNV) {
+        const int left = b.n - base;
+        const int nv = wide ? (left == 1 ? 1 : (left == 2 ? 2 : 4)) : b.nv;
+        GemvParams lm = gemv_params_1(m->lm);
+        lm.x = b.v + (size_t)base * H;
+        lm.norm_w = m->final_norm;
+        lm.eps = eps;
+        lm.st = b.st(base);
+        GemvNV q = batch_nv(b, H, 0, base);
+        RC(gemv_launch(st, lm, 1, PRO_RMSNORM, EPI_ARGMAX, kBigGrid, nv, &q));
+    }
+    return POCR_OK;
 }
 
 // the first token of a batched decode sits in the argmax slots as if the
@@ -1853,18 +1987,38 @@ int32_t pending_token(const StepState &hs) {
     return (int32_t)(0xFFFFFFFFu - (uint32_t)(argmax_of(hs) & 0xFFFFFFFFull));
 }
 
+// vector buffers for b.cap rows; with cap > 4 also the wide step's digit
+// planes (16 rows of the widest input) and row-state table
 int batch_alloc(DecodeBatch &b) {
     const pocr_config &c = b.m->cfg;
     const size_t H = c.hidden, Q = (size_t)c.heads * c.head_dim, KV = (size_t)c.kv_heads * c.head_dim;
-    const size_t nv = b.nv;
+    const size_t rows = std::max(b.cap, b.nv);
+    hipStream_t s = b.m->ctx->stream;
     for (auto pr : {std::make_pair(&b.h, H), std::make_pair(&b.v, H), std::make_pair(&b.qkv, Q + 2 * KV),
                     std::make_pair(&b.ho, Q), std::make_pair(&b.g, (size_t)c.intermediate)}) {
-        HIP_TRY(hipMalloc(pr.first, nv * pr.second * 4));
+        HIP_TRY(hipMalloc(pr.first, rows * pr.second * 4));
         // padding rows stay finite zeros (their results are never read)
-        HIP_TRY(hipMemsetAsync(*pr.first, 0, nv * pr.second * 4, b.m->ctx->stream));
+        HIP_TRY(hipMemsetAsync(*pr.first, 0, rows * pr.second * 4, s));
     }
     HIP_TRY(hipMalloc(&b.pad, sizeof(StepState)));
-    HIP_TRY(hipMemsetAsync(b.pad, 0, sizeof(StepState), b.m->ctx->stream));
+    HIP_TRY(hipMemsetAsync(b.pad, 0, sizeof(StepState), s));
+    if (rows > (size_t)kMaxNV) {
+        const size_t kmax = std::max(std::max(H, Q), (size_t)c.intermediate);
+        HIP_TRY(hipMalloc(&b.xd, 3 * 16 * kmax));
+        HIP_TRY(hipMemsetAsync(b.xd, 0, 3 * 16 * kmax, s));
+        HIP_TRY(hipMalloc(&b.xs, 16 * sizeof(float)));
+        HIP_TRY(hipMalloc(&b.xb, 16 * 4 * sizeof(int)));
+        HIP_TRY(hipMalloc(&b.rst, kMaxBatch * sizeof(StepState *)));
+    }
+    return POCR_OK;
+}
+
+// the row-state table of a wide step (rows = sequences), before its capture
+int batch_set_rows(DecodeBatch &b) {
+    if (b.n <= kMaxNV) return POCR_OK;
+    StepState *h[kMaxBatch] = {};
+    for (int i = 0; i < b.n; ++i) h[i] = b.seq[i]->st;
+    HIP_TRY(hipMemcpy(b.rst, h, sizeof(h), hipMemcpyHostToDevice));
     return POCR_OK;
 }
 
@@ -1873,9 +2027,9 @@ int batch_alloc(DecodeBatch &b) {
 extern "C" int pocr_decode_batch(pocr_seq *const *seqs, int n_seq, const int32_t *first_tokens,
                                  const int32_t *first_positions, int max_new, const int32_t *eos, int n_eos,
                                  int32_t *out_tokens, int32_t *out_counts) {
-    if (!seqs || n_seq <= 0 || n_seq > kMaxNV || !first_tokens || !first_positions || !out_tokens || !out_counts ||
+    if (!seqs || n_seq <= 0 || n_seq > kMaxBatch || !first_tokens || !first_positions || !out_tokens || !out_counts ||
         (n_eos > 0 && !eos))
-        return fail(POCR_ERR_ARG, "pocr_decode_batch: bad arguments (1..%d sequences)", kMaxNV);
+        return fail(POCR_ERR_ARG, "pocr_decode_batch: bad arguments (1..%d sequences)", kMaxBatch);
     pocr_model *m = seqs[0] ? seqs[0]->m : nullptr;
     for (int i = 0; i < n_seq; ++i) {
         if (!seqs[i] || seqs[i]->m != m) return fail(POCR_ERR_ARG, "pocr_decode_batch: sequences of one model");
@@ -1901,9 +2055,13 @@ extern "C" int pocr_decode_batch(pocr_seq *const *seqs, int n_seq, const int32_t
     DecodeBatch b;
     b.m = m;
     b.n = n_seq;
+    if (n_seq > batch_limit(m))
+        return fail(POCR_ERR_UNSUPPORTED, "pocr_decode_batch: %d sequences need layer shapes the small GEMM takes", n_seq);
     b.nv = n_seq == 1 ? 1 : (n_seq == 2 ? 2 : 4);
+    b.cap = n_seq;
     for (int i = 0; i < n_seq; ++i) b.seq[i] = seqs[i];
     RC(batch_alloc(b));
+    RC(batch_set_rows(b));
     // per-sequence state: the first token sits in the argmax slots as if the
     // previous step had chosen it (the step prologue reads it from there)
     std::vector<StepState> hs(n_seq);
@@ -1960,7 +2118,7 @@ extern "C" int pocr_decode_batch(pocr_seq *const *seqs, int n_seq, const int32_t
 // Continuous batching: members join and leave between token steps.  The
 // device set (members still decoding) is captured into one batched step graph,
 // captured again whenever the set changes; the vector buffers are allocated
-// once for kMaxNV vectors.  A member decodes from its seeded first token until
+// once for the batch's limit of vectors.  A member decodes from its seeded first token until
 // an EOS id or its token budget; steps are issued in chunks no longer than any
 // member's remaining budget, so no cache grows past what its join checked.
 // ---------------------------------------------------------------------------
@@ -1975,7 +2133,8 @@ struct pocr_batch {
     };
     pocr_model *m = nullptr;
     std::vector<Member> members;      // join order
-    DecodeBatch bufs;                 // owns the kMaxNV vector buffers
+    DecodeBatch bufs;                 // owns the vector buffers (limit rows)
+    int limit = kMaxNV;               // members decoding at once
     std::unique_ptr<DecodeBatch> cur; // the captured device set, null when stale
     bool use_graph = true;
 };
@@ -1999,7 +2158,9 @@ extern "C" int pocr_batch_create(pocr_model *m, pocr_batch **out) {
     pocr_batch *b = new pocr_batch();
     b->m = m;
     b->bufs.m = m;
+    b->limit = batch_limit(m);
     b->bufs.nv = kMaxNV;
+    b->bufs.cap = b->limit;
     const int rc = batch_alloc(b->bufs);
     if (rc == POCR_OK) {
         const hipError_t e = hipStreamSynchronize(m->ctx->stream);
@@ -2046,7 +2207,7 @@ extern "C" int pocr_batch_join(pocr_batch *b, pocr_seq *s, int32_t first_token, 
     if (s->sampling) return fail(POCR_ERR_UNSUPPORTED, "pocr_batch_join: the sequence samples (the batch is greedy)");
     int decoding = 0;
     for (const auto &mb : b->members) decoding += mb.finished ? 0 : 1;
-    if (decoding >= kMaxNV) return fail(POCR_ERR_ARG, "pocr_batch_join: %d members are decoding", kMaxNV);
+    if (decoding >= b->limit) return fail(POCR_ERR_ARG, "pocr_batch_join: %d members are decoding", b->limit);
     if (s->len + max_new - 1 > s->cap || max_new > s->max_tokens)
         return fail(POCR_ERR_ARG, "pocr_batch_join: %d tokens exceed the capacity", max_new);
     pocr_batch::Member mb;
@@ -2073,12 +2234,18 @@ static int batch_capture(pocr_batch *b) {
     for (auto &mb : b->members)
         if (!mb.finished) d->seq[d->n++] = mb.s;
     d->nv = d->n == 1 ? 1 : (d->n == 2 ? 2 : 4);
+    d->cap = b->bufs.cap;
     d->h = b->bufs.h;
     d->v = b->bufs.v;
     d->qkv = b->bufs.qkv;
     d->ho = b->bufs.ho;
     d->g = b->bufs.g;
     d->pad = b->bufs.pad;
+    d->xd = b->bufs.xd;
+    d->xs = b->bufs.xs;
+    d->xb = b->bufs.xb;
+    d->rst = b->bufs.rst;
+    RC(batch_set_rows(*d));
     if (b->use_graph) {
         hipStream_t st = b->m->ctx->stream;
         HIP_TRY(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));

@@ -406,5 +406,11 @@ int digitize_rows(hipStream_t s, int qtype, const DigitizeParams &p, int n) { re
 int gemm_rows(hipStream_t s, int qtype, int nmat, const GemmParams &p, int epi, int npad) {
     return launch_gemm(s, qtype, nmat, p, epi, npad);
 }
+bool gemm_small_ok(int rows, int K) { return small_shape_ok(rows, K); }
+int gemm_small_rows(hipStream_t s, int qtype, int nmat, const GemmParams &p, int epi) {
+    if (p.ntok > 16 || !small_shape_ok(p.rows, p.K) || p.plane_stride != (size_t)16 * p.K)
+        return fail(POCR_ERR_UNSUPPORTED, "gemm: %d tokens of %dx%d outside the small kernel", p.ntok, p.rows, p.K);
+    return nmat == 2 ? launch_gemm_small_t<2>(s, qtype, p, epi) : launch_gemm_small_t<1>(s, qtype, p, epi);
+}
 
 }  // namespace pocr

@@ -120,10 +120,11 @@ def test_continuous_batch_staggered_joins(orc, ctx):
     b.join(seqs[2][0], seqs[2][1], lens[2], budgets[2], eos=())
     assert b.step(2) == 3
     b.join(seqs[3][0], seqs[3][1], lens[3], budgets[3], eos=())
-    with pytest.raises(lib.PocrError):  # four members are decoding
-        b.join(seqs[4][0], seqs[4][1], lens[4], budgets[4], eos=())
-    pending = [0, 1, 2, 3]
-    joined_last = False
+    assert b.step(1) == 4
+    # the fifth member moves the batch from the 4-vector GEMV passes to the
+    # wide (MFMA) step, and back once members finish
+    b.join(seqs[4][0], seqs[4][1], lens[4], budgets[4], eos=())
+    pending = [0, 1, 2, 3, 4]
     for _ in range(100):
         left = b.step(4)
         for i in list(pending):
@@ -132,10 +133,6 @@ def test_continuous_batch_staggered_joins(orc, ctx):
             if done:
                 got[i] = list(b.leave(seqs[i][0]))
                 pending.remove(i)
-        if not joined_last and len(pending) < 4:
-            b.join(seqs[4][0], seqs[4][1], lens[4], budgets[4], eos=())
-            pending.append(4)
-            joined_last = True
         if not pending:
             break
         assert left >= 0
@@ -211,3 +208,84 @@ def test_continuous_batch_rules(ctx):
         b.join(w, first, 4, 4, eos=())
     b.close()
     other.close()
+
+
+# ---- wide batches: 5..16 sequences on the small MFMA GEMM ---------------------
+
+@pytest.mark.parametrize("qtype,nseq", [(Q4, 5), (Q4, 8), (Q4, 16), (Q6, 16), (Q8, 11)],
+                         ids=["q4-5", "q4-8", "q4-16", "q6-16", "q8-11"])
+def test_decode_batch_wide_matches_oracle(orc, ctx, qtype, nseq):
+    om, gm = _models(orc, ctx, MID, qtype, seed=9)
+    lens = [5 + (7 * i) % 23 for i in range(nseq)]  # 5 (the Q4/Q6 in-place rows) .. 27
+    prompts = [synth.prompt_ids(n, seed=100 + i, high=MID.vocab) for i, n in enumerate(lens)]
+    n_new = 12
+    want = [list(om.generate(ids, n_new, eos=())) for ids in prompts]
+    seqs, firsts = zip(*[_prefilled(gm, ids, n_new) for ids in prompts])
+    got = lib.decode_batch(list(seqs), list(firsts), lens, n_new, eos=())
+    for i in range(nseq):
+        assert list(got[i]) == want[i], i
+        assert len(seqs[i]) == lens[i] + n_new - 1
+
+
+def test_decode_batch_wide_short_prompts(orc, ctx):
+    # cache lengths 1..5 keep the Q4 o_proj residual in place (model.go:3895-3902,
+    # 4051-4057): each row of the wide step follows its own sequence's length
+    om, gm = _models(orc, ctx, MID, Q4, seed=10)
+    lens = [1, 2, 3, 4, 5, 6, 1, 3]
+    prompts = [synth.prompt_ids(n, seed=200 + i, high=MID.vocab) for i, n in enumerate(lens)]
+    want = [list(om.generate(ids, 10, eos=())) for ids in prompts]
+    seqs, firsts = zip(*[_prefilled(gm, ids, 10) for ids in prompts])
+    got = lib.decode_batch(list(seqs), list(firsts), lens, 10, eos=())
+    for i in range(len(lens)):
+        assert list(got[i]) == want[i], i
+
+
+def test_continuous_batch_sixteen_members(orc, ctx):
+    om, gm = _models(orc, ctx, MID, Q4, seed=11)
+    n_req = 20
+    lens = [6 + (5 * i) % 19 for i in range(n_req)]
+    budgets = [4 + (3 * i) % 11 for i in range(n_req)]
+    prompts = [synth.prompt_ids(n, seed=300 + i, high=MID.vocab) for i, n in enumerate(lens)]
+    want = [list(om.generate(ids, bud, eos=())) for ids, bud in zip(prompts, budgets)]
+    b = lib.Batch(gm)
+    queue, members, got = list(range(n_req)), [], {}
+    seqs = {}
+    most = 0
+    while queue or members:
+        while queue and len(members) < 16:
+            i = queue.pop(0)
+            s, f = _prefilled(gm, prompts[i], budgets[i])
+            seqs[i] = s
+            b.join(s, f, lens[i], budgets[i], eos=())
+            members.append(i)
+        most = max(most, len(members))
+        b.step(3)
+        for i in list(members):
+            if b.poll(seqs[i])[1]:
+                got[i] = list(b.leave(seqs[i]))
+                members.remove(i)
+                seqs[i].close()
+    assert most == 16
+    for i in range(n_req):
+        assert got[i] == want[i], i
+    b.close()
+
+
+def test_continuous_batch_limit(ctx):
+    gm = lib.Model(ctx, MID)
+    gm.load_weights(synth.make_weights(MID, Q4, seed=2))
+    b = lib.Batch(gm)
+    ids = synth.prompt_ids(4, seed=1, high=MID.vocab)
+    seqs = []
+    for i in range(17):
+        s = gm.seq(16)
+        first = int(s.generate(ids, 1, eos=(), use_prefill=True)[0])
+        if i < 16:
+            b.join(s, first, 4, 6, eos=())
+        else:
+            with pytest.raises(lib.PocrError):  # 16 members are decoding
+                b.join(s, first, 4, 6, eos=())
+        seqs.append(s)
+    with pytest.raises(lib.PocrError):
+        lib.decode_batch(seqs, [1] * 17, [4] * 17, 4)  # 17 sequences
+    b.close()
