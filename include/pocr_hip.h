@@ -225,9 +225,9 @@ int pocr_seq_len(const pocr_seq *s);
  * the prefill's first included, from the top_k LM-head candidates on the
  * device (model.go:3632-3638, 1950-1990).  The generator restarts at `seed`
  * here and at every pocr_generate (samplingRNGInto, 1846-1852);
- * pocr_decode_greedy continues it.  Other sampling settings (top_k 0 or
- * > 64: full-vocabulary or wide draws) return POCR_ERR_UNSUPPORTED, and
- * pocr_decode_batch rejects sampling sequences. */
+ * pocr_decode_greedy, pocr_decode_batch and pocr_batch_step continue it.
+ * Other sampling settings (top_k 0 or > 64: full-vocabulary or wide draws)
+ * return POCR_ERR_UNSUPPORTED. */
 int pocr_seq_set_sampling(pocr_seq *s, double temperature, int top_k, uint64_t seed);
 /* copy layer's first len rows of K/V (len*kv_heads*head_dim floats each) */
 int pocr_seq_read_kv(pocr_seq *s, int layer, float *k, float *v);
@@ -253,14 +253,16 @@ int pocr_prefill(pocr_seq *s, int n, const float *emb, const int32_t *pos3, floa
  * number of tokens written (>=0) or an error status (<0). */
 int pocr_decode_greedy(pocr_seq *s, int32_t first_token, int32_t first_pos, int max_new,
                        const int32_t *eos, int n_eos, int32_t *out_tokens);
-/* greedy decode of n_seq (1..16) sequences of one model together: the
+/* decode of n_seq (1..16) sequences of one model together: the
  * server's concurrent requests (cmd/paddleocrvl-server/main.go:1106, one
  * decode loop each, model.go:1538-1568) batched into one device step — each
  * layer's weights stream once for all of them (M = n_seq batched GEMV), each
  * sequence keeps its own KV cache.  Sequence i starts from first_tokens[i] at
  * first_positions[i]; its tokens go to out_tokens[i*max_new ...] (first token
- * first), out_counts[i] of them, stopping after an EOS id.  Per-sequence
- * results equal pocr_decode_greedy's up to f32 summation order.  Up to 4
+ * first), out_counts[i] of them, stopping after an EOS id.  Greedy sequences
+ * take the argmax, sampling ones (pocr_seq_set_sampling) draw from their own
+ * generator.  Per-sequence results equal pocr_decode_greedy's up to f32
+ * summation order.  Up to 4
  * sequences share GEMV passes; 5..16 need layer matrices with rows a
  * multiple of 16 and inputs a multiple of 256 (POCR_ERR_UNSUPPORTED
  * otherwise). */
@@ -280,7 +282,7 @@ int pocr_batch_create(pocr_model *m, pocr_batch **out);
 void pocr_batch_destroy(pocr_batch *b);
 /* a prefilled sequence joins with the token its prefill chose, at position
  * first_pos, for at most max_new tokens (first_token counted) and the EOS
- * ids given; greedy sequences only (POCR_ERR_UNSUPPORTED otherwise).
+ * ids given; a sampling sequence keeps drawing from its generator.
  * POCR_ERR_ARG if the batch's limit of members is decoding or the capacity
  * is short. */
 int pocr_batch_join(pocr_batch *b, pocr_seq *s, int32_t first_token, int32_t first_pos, int max_new,

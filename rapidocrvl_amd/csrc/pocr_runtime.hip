@@ -1706,7 +1706,8 @@ namespace {
 
 struct DecodeBatch {
     pocr_model *m = nullptr;
-    int n = 0;    // sequences
+    int n = 0;    // sequences: the ng greedy ones first, then the sampling ones
+    int ng = 0;
     int nv = 1;   // vectors per GEMV pass (n ≤ 4: n padded to 1, 2 or 4)
     int cap = 0;  // vector rows the buffers hold (≥ nv; kMaxBatch for the wide step)
     pocr_seq *seq[kMaxBatch] = {};
@@ -1732,13 +1733,25 @@ struct DecodeBatch {
     StepState *st(int i) const { return i < n ? seq[i]->st : pad; }
 };
 
-// states of the vectors base .. base+3 of a GEMV pass (padding: the dummy state)
-GemvNV batch_nv(const DecodeBatch &b, int x_stride, int o_stride, int base = 0) {
+// states of the vectors base .. base+3 of a GEMV pass; vectors at or past lim
+// (padding, or rows outside the pass) take the dummy state
+GemvNV batch_nv(const DecodeBatch &b, int x_stride, int o_stride, int base = 0, int lim = kMaxBatch) {
     GemvNV q{};
     q.x_stride = x_stride;
     q.o_stride = o_stride;
-    for (int i = 1; i < kMaxNV; ++i) q.stv[i - 1] = b.st(base + i);
+    for (int i = 1; i < kMaxNV; ++i) q.stv[i - 1] = base + i < lim ? b.st(base + i) : b.pad;
     return q;
+}
+
+// the batch's sequences in step order: greedy ones first (their LM head runs
+// as 4-vector argmax passes over consecutive rows), then the sampling ones
+void batch_order(DecodeBatch &b, pocr_seq *const *seqs, int n) {
+    b.n = b.ng = 0;
+    for (int i = 0; i < n; ++i)
+        if (!seqs[i]->sampling) b.seq[b.n++] = seqs[i];
+    b.ng = b.n;
+    for (int i = 0; i < n; ++i)
+        if (seqs[i]->sampling) b.seq[b.n++] = seqs[i];
 }
 
 // Sequences a batch step can take: up to 4 on the GEMV passes, up to 16 when
@@ -1953,19 +1966,22 @@ int enqueue_batch_step(DecodeBatch &b) {
         q = batch_nv(b, F, H);
         RC(gemv_launch(st, d, 1, PRO_COPY, EPI_DOWN, kBigGrid, b.nv, &q));
     }
-    // LM head on RMSNorm(v)·final_norm, argmax into each sequence's state: one
-    // GEMV pass per 4 sequences (the last pass padded to 1, 2 or 4 vectors)
-    for (int base = 0; base < b.n; base += kMaxNV) {
-        const int left = b.n - base;
-        const int nv = wide ? (left == 1 ? 1 : (left == 2 ? 2 : 4)) : b.nv;
+    // LM head on RMSNorm(v)·final_norm.  Greedy sequences: argmax into each
+    // one's state, one GEMV pass per 4 of them (the last pass padded to 1, 2
+    // or 4 vectors).  Sampling sequences: each its own logits, top-k and draw
+    // (the draw lands in argmax slot 0, where the next step reads it).
+    for (int base = 0; base < b.ng; base += kMaxNV) {
+        const int left = b.ng - base;
+        const int nv = left == 1 ? 1 : (left == 2 ? 2 : 4);
         GemvParams lm = gemv_params_1(m->lm);
         lm.x = b.v + (size_t)base * H;
         lm.norm_w = m->final_norm;
         lm.eps = eps;
         lm.st = b.st(base);
-        GemvNV q = batch_nv(b, H, 0, base);
+        GemvNV q = batch_nv(b, H, 0, base, b.ng);
         RC(gemv_launch(st, lm, 1, PRO_RMSNORM, EPI_ARGMAX, kBigGrid, nv, &q));
     }
+    for (int i = b.ng; i < b.n; ++i) RC(enqueue_lm_head(b.seq[i], b.v + (size_t)i * H, false));
     return POCR_OK;
 }
 
@@ -2037,8 +2053,6 @@ extern "C" int pocr_decode_batch(pocr_seq *const *seqs, int n_seq, const int32_t
             if (seqs[j] == seqs[i]) return fail(POCR_ERR_ARG, "pocr_decode_batch: sequence %d repeated", i);
         if (first_tokens[i] < 0 || first_tokens[i] >= m->cfg.vocab)
             return fail(POCR_ERR_ARG, "pocr_decode_batch: token out of vocab");
-        if (seqs[i]->sampling)
-            return fail(POCR_ERR_UNSUPPORTED, "pocr_decode_batch: sequence %d samples (the batch is greedy)", i);
     }
     for (int i = 0; i < n_seq; ++i) out_counts[i] = 0;
     if (max_new <= 0) return POCR_OK;
@@ -2059,7 +2073,7 @@ extern "C" int pocr_decode_batch(pocr_seq *const *seqs, int n_seq, const int32_t
         return fail(POCR_ERR_UNSUPPORTED, "pocr_decode_batch: %d sequences need layer shapes the small GEMM takes", n_seq);
     b.nv = n_seq == 1 ? 1 : (n_seq == 2 ? 2 : 4);
     b.cap = n_seq;
-    for (int i = 0; i < n_seq; ++i) b.seq[i] = seqs[i];
+    batch_order(b, seqs, n_seq);
     RC(batch_alloc(b));
     RC(batch_set_rows(b));
     // per-sequence state: the first token sits in the argmax slots as if the
@@ -2204,7 +2218,6 @@ extern "C" int pocr_batch_join(pocr_batch *b, pocr_seq *s, int32_t first_token, 
     std::lock_guard<std::mutex> lk(b->m->ctx->mu);
     HIP_TRY(hipSetDevice(b->m->ctx->device));
     if (s->batch) return fail(POCR_ERR_ARG, "pocr_batch_join: the sequence is already in a decode batch");
-    if (s->sampling) return fail(POCR_ERR_UNSUPPORTED, "pocr_batch_join: the sequence samples (the batch is greedy)");
     int decoding = 0;
     for (const auto &mb : b->members) decoding += mb.finished ? 0 : 1;
     if (decoding >= b->limit) return fail(POCR_ERR_ARG, "pocr_batch_join: %d members are decoding", b->limit);
@@ -2231,8 +2244,11 @@ static int batch_capture(pocr_batch *b) {
     auto d = std::make_unique<DecodeBatch>();
     d->m = b->m;
     d->owns = false;
+    pocr_seq *dec[kMaxBatch];
+    int nd = 0;
     for (auto &mb : b->members)
-        if (!mb.finished) d->seq[d->n++] = mb.s;
+        if (!mb.finished) dec[nd++] = mb.s;
+    batch_order(*d, dec, nd);
     d->nv = d->n == 1 ? 1 : (d->n == 2 ? 2 : 4);
     d->cap = b->bufs.cap;
     d->h = b->bufs.h;

@@ -191,12 +191,6 @@ def test_continuous_batch_rules(ctx):
     b.join(t, first_t, 4, 1, eos=())
     assert b.poll(t) == (1, True)
     assert list(b.leave(t)) == [first_t]
-    # a sampling sequence cannot join
-    u = gm.seq(16)
-    u.set_sampling(0.8, 8, 3)
-    with pytest.raises(lib.PocrError) as e:
-        b.join(u, first, 4, 4, eos=())
-    assert e.value.code == lib.POCR_ERR_UNSUPPORTED
     # destroying a member removes it; the batch carries on
     b.step(1)
     s.close()
@@ -288,4 +282,80 @@ def test_continuous_batch_limit(ctx):
         seqs.append(s)
     with pytest.raises(lib.PocrError):
         lib.decode_batch(seqs, [1] * 17, [4] * 17, 4)  # 17 sequences
+    b.close()
+
+
+# ---- sampling members ----------------------------------------------------------
+
+def _sampled_prefill(gm, ids, n_new, temp, top_k, seed):
+    s = gm.seq(len(ids) + n_new + 4)
+    s.set_sampling(temp, top_k, seed)
+    first = s.generate(ids, 1, eos=(), use_prefill=True)  # seeds the generator, draws the first token
+    return s, int(first[0])
+
+
+def _single_streams(om, gm, prompts, budgets, opts):
+    """What each request generates on its own: the oracle's stream for greedy
+    ones; for sampling ones the device's single-sequence stream after the same
+    batched prefill (a draw can fall within the prefill's last-bit K/V
+    differences of a cumulative-weight boundary; the single sampled path is
+    checked against the oracle in test_gpu_sampling.py)."""
+    out = []
+    for ids, bud, (t, k, sd) in zip(prompts, budgets, opts):
+        if t > 0:
+            s = gm.seq(len(ids) + bud + 4)
+            s.set_sampling(t, k, sd)
+            out.append(list(s.generate(ids, bud, eos=(), use_prefill=True)))
+            s.close()
+        else:
+            out.append(list(om.generate(ids, bud, eos=())))
+    return out
+
+
+@pytest.mark.parametrize("nseq", [3, 8], ids=["narrow", "wide"])
+def test_decode_batch_mixes_greedy_and_sampling(orc, ctx, nseq):
+    # every other sequence draws from its top-k (its own generator, continued
+    # from its prefill's draw); each stream equals its single-sequence stream
+    om, gm = _models(orc, ctx, MID, Q4, seed=12)
+    lens = [7 + 3 * i for i in range(nseq)]
+    prompts = [synth.prompt_ids(n, seed=400 + i, high=MID.vocab) for i, n in enumerate(lens)]
+    opts = [(0.0, 0, 0) if i % 2 == 0 else (0.7 + 0.1 * i, 8 + 4 * i, 1000 + i) for i in range(nseq)]
+    n_new = 14
+    want = _single_streams(om, gm, prompts, [n_new] * nseq, opts)
+    seqs, firsts = [], []
+    for ids, (t, k, sd) in zip(prompts, opts):
+        s, f = _sampled_prefill(gm, ids, n_new, t, k, sd) if t > 0 else _prefilled(gm, ids, n_new)
+        seqs.append(s)
+        firsts.append(f)
+    got = lib.decode_batch(seqs, firsts, lens, n_new, eos=())
+    for i in range(nseq):
+        assert list(got[i]) == want[i], (i, opts[i])
+
+
+def test_continuous_batch_sampling_members(orc, ctx):
+    om, gm = _models(orc, ctx, MID, Q6, seed=13)
+    n_req = 7
+    lens = [9 + 2 * i for i in range(n_req)]
+    budgets = [6 + 2 * i for i in range(n_req)]
+    prompts = [synth.prompt_ids(n, seed=500 + i, high=MID.vocab) for i, n in enumerate(lens)]
+    opts = [(0.9, 16, 77 + i) if i % 3 else (0.0, 0, 0) for i in range(n_req)]
+    want = _single_streams(om, gm, prompts, budgets, opts)
+    b = lib.Batch(gm)
+    queue, members, got, seqs = list(range(n_req)), [], {}, {}
+    while queue or members:
+        while queue and len(members) < 5:
+            i = queue.pop(0)
+            t, k, sd = opts[i]
+            s, f = (_sampled_prefill(gm, prompts[i], budgets[i], t, k, sd) if t > 0
+                    else _prefilled(gm, prompts[i], budgets[i]))
+            seqs[i] = s
+            b.join(s, f, lens[i], budgets[i], eos=())
+            members.append(i)
+        b.step(4)
+        for i in list(members):
+            if b.poll(seqs[i])[1]:
+                got[i] = list(b.leave(seqs[i]))
+                members.remove(i)
+    for i in range(n_req):
+        assert got[i] == want[i], (i, opts[i])
     b.close()

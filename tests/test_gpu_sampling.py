@@ -181,8 +181,6 @@ def test_sampling_settings_errors(ctx):
         with pytest.raises(lib.PocrError) as e:
             s.set_sampling(0.7, top_k, 0)
         assert e.value.code == lib.POCR_ERR_UNSUPPORTED
-    # the batch decodes greedily only
+    # a sampling sequence decodes in a batch too (its own generator)
     s.set_sampling(0.7, 8, 0)
-    with pytest.raises(lib.PocrError) as e:
-        lib.decode_batch([s], [1], [0], 2)
-    assert e.value.code == lib.POCR_ERR_UNSUPPORTED
+    assert len(lib.decode_batch([s], [1], [0], 2, eos=())[0]) == 2
