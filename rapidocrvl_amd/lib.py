@@ -568,6 +568,15 @@ class Projector:
                                            _ptr(w2), _ptr(b2), float(eps), C.byref(h)))
         self.h = h
 
+    @classmethod
+    def from_gguf(cls, ctx: "Context", gguf: "GgufFile", eps: float = 1e-5) -> "Projector":
+        """The mlp_AR tensors of a checkpoint (cacheVisionWeights, vision.go:224-302):
+        pre_norm weight/bias, linear_1 and linear_2 weights and biases, all F32."""
+        t = {n: gguf.float32("mlp_AR." + n) for n in ("pre_norm.weight", "pre_norm.bias", "linear_1.weight",
+                                                       "linear_1.bias", "linear_2.weight", "linear_2.bias")}
+        return cls(ctx, t["pre_norm.weight"], t["pre_norm.bias"], t["linear_1.weight"], t["linear_1.bias"],
+                   t["linear_2.weight"], t["linear_2.bias"], eps=eps)
+
     def close(self):
         if getattr(self, "h", None):
             load().pocr_projector_destroy(self.h)

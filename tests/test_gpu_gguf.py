@@ -78,3 +78,25 @@ def test_gguf_model_rejections(ctx, ckpt, tmp_path):
     # the model still loads afterwards
     m = lib.Model.from_gguf(ctx, cfg, q4)
     m.close()
+
+
+def test_projector_from_gguf(ctx, tmp_path):
+    # the mlp_AR tensors stay F32 in a converted file; the projector built from
+    # them equals the one built from the same arrays
+    rng = np.random.default_rng(4)
+    vd, td = 64, 1024
+    K = 4 * vd
+    t = {"mlp_AR.pre_norm.weight": 1 + 0.1 * rng.standard_normal(vd), "mlp_AR.pre_norm.bias": 0.1 * rng.standard_normal(vd),
+         "mlp_AR.linear_1.weight": rng.standard_normal((K, K)) / np.sqrt(K), "mlp_AR.linear_1.bias": 0.1 * rng.standard_normal(K),
+         "mlp_AR.linear_2.weight": rng.standard_normal((td, K)) / np.sqrt(K), "mlp_AR.linear_2.bias": 0.1 * rng.standard_normal(td)}
+    t = {k: np.ascontiguousarray(v, np.float32) for k, v in t.items()}
+    path = str(tmp_path / "vision.gguf")
+    convert.write_gguf(path, [], [(k, convert.F32, v.shape, v.tobytes()) for k, v in sorted(t.items())])
+    with lib.GgufFile(path) as g:
+        pg = lib.Projector.from_gguf(ctx, g)
+    pd = lib.Projector(ctx, t["mlp_AR.pre_norm.weight"], t["mlp_AR.pre_norm.bias"], t["mlp_AR.linear_1.weight"],
+                       t["mlp_AR.linear_1.bias"], t["mlp_AR.linear_2.weight"], t["mlp_AR.linear_2.bias"])
+    x = rng.standard_normal((2 * 4 * 6, vd)).astype(np.float32)
+    np.testing.assert_array_equal(pg.project(x, (2, 4, 6)), pd.project(x, (2, 4, 6)))
+    pg.close()
+    pd.close()
