@@ -64,3 +64,20 @@ def test_no_device_is_a_device_error():
 def test_positions_reject_grid_larger_than_placeholders():
     with pytest.raises(lib.PocrError):
         lib.mm_positions([1, 7, 7, 2], 7, (1, 4, 4))
+
+
+def test_every_entry_point_rejects_null_arguments():
+    # null handles and pointers, zero sizes: every status-returning entry point
+    # answers POCR_ERR_ARG before touching a device; destroy/free calls accept null
+    L = lib.load()
+    plain = {"pocr_abi_version", "pocr_last_error", "pocr_device_count", "pocr_row_bytes"}
+    for name, (res, args) in sorted(lib._SIGS.items()):
+        if name in plain:
+            continue
+        vals = [0 if a in (C.c_int, C.c_int32, C.c_int64, C.c_uint64, C.c_uint32, C.c_size_t)
+                else 0.0 if a in (C.c_float, C.c_double) else None for a in args]
+        r = getattr(L, name)(*vals)
+        if res is None:
+            assert r is None, name
+        else:
+            assert r == lib.POCR_ERR_ARG, (name, r)
