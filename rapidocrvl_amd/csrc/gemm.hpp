@@ -1124,4 +1124,40 @@ static __global__ void __launch_bounds__(kPfThreads) k_attn_prefill(const float 
     }
 }
 
+
+// Greedy choice over rows of logits (the batched LM head): workgroup (x, i)
+// scans its slice of row i and folds the best (score, index) key into argmax
+// slot x of sequence i's state, as the GEMV argmax epilogue does: key =
+// ordered score bits · 2^32 + (2^32 − 1 − index), so the maximum key is the
+// highest score and, among equal scores, the lowest index; NaN and −inf are
+// never chosen.
+static __global__ void __launch_bounds__(kThreads) k_argmax_rows(const float *logits, int ld, int cols, int slice,
+                                                               StepState *const *rst) {
+    const int i = blockIdx.y;
+    const int c0 = blockIdx.x * slice, c1 = min(cols, c0 + slice);
+    const float *row = logits + (size_t)i * ld;
+    unsigned long long best = 0ull;
+    for (int c = c0 + (int)threadIdx.x; c < c1; c += kThreads) {
+        const float v = row[c];
+        if (v > -INFINITY) {
+            const unsigned long long k =
+                ((unsigned long long)ordered_bits(v) << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)c);
+            best = k > best ? k : best;
+        }
+    }
+#pragma unroll
+    for (int m = 32; m > 0; m >>= 1) {
+        const unsigned long long o = ((unsigned long long)__shfl_xor((unsigned)(best >> 32), m, 64) << 32) |
+                                     (unsigned)__shfl_xor((unsigned)best, m, 64);
+        best = o > best ? o : best;
+    }
+    __shared__ unsigned long long wb[kWaves];
+    if ((threadIdx.x & 63) == 0) wb[threadIdx.x >> 6] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        unsigned long long m = wb[0];
+        for (int w = 1; w < kWaves; ++w) m = wb[w] > m ? wb[w] : m;
+        if (m) atomicMax(&rst[i]->argmax_slot[(blockIdx.x % kArgSlots) * kSlotPitch], m);
+    }
+}
 }  // namespace pocr

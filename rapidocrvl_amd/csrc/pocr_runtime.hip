@@ -1719,6 +1719,7 @@ struct DecodeBatch {
     float *xs = nullptr;
     int *xb = nullptr;
     StepState **rst = nullptr;
+    float *logits = nullptr;  // [16][vocab] greedy rows of the MFMA LM head (vocab a multiple of 16)
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
     bool owns = true;  // false: the vector buffers belong to a continuous batch
@@ -1727,7 +1728,7 @@ struct DecodeBatch {
         if (graph) (void)hipGraphDestroy(graph);
         if (owns)
             for (void *p : {(void *)h, (void *)v, (void *)qkv, (void *)ho, (void *)g, (void *)pad, (void *)xd,
-                            (void *)xs, (void *)xb, (void *)rst})
+                            (void *)xs, (void *)xb, (void *)rst, (void *)logits})
                 if (p) (void)hipFree(p);
     }
     StepState *st(int i) const { return i < n ? seq[i]->st : pad; }
@@ -1967,10 +1968,25 @@ int enqueue_batch_step(DecodeBatch &b) {
         RC(gemv_launch(st, d, 1, PRO_COPY, EPI_DOWN, kBigGrid, b.nv, &q));
     }
     // LM head on RMSNorm(v)·final_norm.  Greedy sequences: argmax into each
-    // one's state, one GEMV pass per 4 of them (the last pass padded to 1, 2
-    // or 4 vectors).  Sampling sequences: each its own logits, top-k and draw
-    // (the draw lands in argmax slot 0, where the next step reads it).
-    for (int base = 0; base < b.ng; base += kMaxNV) {
+    // one's state — more than 4 of them (and a vocabulary in 16-row blocks):
+    // digit planes, the small MFMA GEMM into logits rows and a per-row argmax;
+    // otherwise one GEMV pass per 4 of them (the last pass padded to 1, 2 or 4
+    // vectors).  Sampling sequences: each its own logits, top-k and draw (the
+    // draw lands in argmax slot 0, where the next step reads it).
+    if (wide && b.ng > kMaxNV && b.logits) {
+        const int V = c.vocab;
+        RC(batch_digitize(b, m->lm->qtype, b.v, H, m->final_norm));
+        GemmParams lp = batch_gemm(b, m->lm, H);
+        lp.ntok = b.ng;
+        lp.out = b.logits;
+        lp.out_stride = V;
+        RC(gemm_small_rows(st, m->lm->qtype, 1, lp, G_PLAIN));
+        constexpr int kSlice = 2048;
+        hipLaunchKernelGGL(k_argmax_rows, dim3((V + kSlice - 1) / kSlice, b.ng), dim3(kThreads), 0, st, b.logits, V, V,
+                           kSlice, b.rst);
+        HIP_TRY(hipGetLastError());
+    }
+    for (int base = 0; base < b.ng && !(wide && b.ng > kMaxNV && b.logits); base += kMaxNV) {
         const int left = b.ng - base;
         const int nv = left == 1 ? 1 : (left == 2 ? 2 : 4);
         GemvParams lm = gemv_params_1(m->lm);
@@ -2025,6 +2041,7 @@ int batch_alloc(DecodeBatch &b) {
         HIP_TRY(hipMalloc(&b.xs, 16 * sizeof(float)));
         HIP_TRY(hipMalloc(&b.xb, 16 * 4 * sizeof(int)));
         HIP_TRY(hipMalloc(&b.rst, kMaxBatch * sizeof(StepState *)));
+        if (gemm_small_ok(c.vocab, c.hidden)) HIP_TRY(hipMalloc(&b.logits, (size_t)16 * c.vocab * 4));
     }
     return POCR_OK;
 }
@@ -2261,6 +2278,7 @@ static int batch_capture(pocr_batch *b) {
     d->xs = b->bufs.xs;
     d->xb = b->bufs.xb;
     d->rst = b->bufs.rst;
+    d->logits = b->bufs.logits;
     RC(batch_set_rows(*d));
     if (b->use_graph) {
         hipStream_t st = b->m->ctx->stream;

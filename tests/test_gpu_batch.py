@@ -359,3 +359,39 @@ def test_continuous_batch_sampling_members(orc, ctx):
     for i in range(n_req):
         assert got[i] == want[i], (i, opts[i])
     b.close()
+
+
+# a vocabulary in 16-row blocks: more than 4 greedy rows take the MFMA LM head
+# (logits rows + per-row argmax) instead of the 4-vector GEMV passes
+MID16 = DecoderConfig(hidden=1024, inter=3072, layers=3, heads=16, kv_heads=2, head_dim=128, vocab=5008, eps=1e-5,
+                      rope_theta=500000.0)
+
+
+@pytest.mark.parametrize("qtype,nseq", [(Q4, 6), (Q4, 16), (Q8, 9)], ids=["q4-6", "q4-16", "q8-9"])
+def test_decode_batch_mfma_lm_head(orc, ctx, qtype, nseq):
+    om, gm = _models(orc, ctx, MID16, qtype, seed=14)
+    lens = [3 + (11 * i) % 29 for i in range(nseq)]
+    prompts = [synth.prompt_ids(n, seed=600 + i, high=MID16.vocab) for i, n in enumerate(lens)]
+    want = [list(om.generate(ids, 12, eos=())) for ids in prompts]
+    seqs, firsts = zip(*[_prefilled(gm, ids, 12) for ids in prompts])
+    got = lib.decode_batch(list(seqs), list(firsts), lens, 12, eos=())
+    for i in range(nseq):
+        assert list(got[i]) == want[i], i
+
+
+def test_decode_batch_mfma_lm_head_with_sampling(orc, ctx):
+    # 12 sequences, 8 greedy (MFMA head) and 4 sampling (their own heads)
+    om, gm = _models(orc, ctx, MID16, Q4, seed=15)
+    nseq = 12
+    lens = [5 + 2 * i for i in range(nseq)]
+    prompts = [synth.prompt_ids(n, seed=700 + i, high=MID16.vocab) for i, n in enumerate(lens)]
+    opts = [(0.85, 10, 50 + i) if i % 3 == 1 else (0.0, 0, 0) for i in range(nseq)]
+    want = _single_streams(om, gm, prompts, [10] * nseq, opts)
+    seqs, firsts = [], []
+    for ids, (t, k, sd) in zip(prompts, opts):
+        s, f = _sampled_prefill(gm, ids, 10, t, k, sd) if t > 0 else _prefilled(gm, ids, 10)
+        seqs.append(s)
+        firsts.append(f)
+    got = lib.decode_batch(seqs, firsts, lens, 10, eos=())
+    for i in range(nseq):
+        assert list(got[i]) == want[i], (i, opts[i])
