@@ -188,7 +188,7 @@ def mm_positions(ids, image_token_id: int, grid, merge: int = 2):
 
 
 def decode_batch(seqs, first_tokens, first_positions, max_new: int, eos=(2,)):
-    """Greedy decode of 1..4 sequences of one model together (pocr_decode_batch):
+    """Decode of 1..16 sequences of one model together (pocr_decode_batch):
     returns one token array per sequence, first token first."""
     n = len(seqs)
     handles = (C.c_void_p * n)(*[s.h for s in seqs])
@@ -204,7 +204,7 @@ def decode_batch(seqs, first_tokens, first_positions, max_new: int, eos=(2,)):
 
 class Batch:
     """Continuous batching (pocr_batch_*): prefilled sequences of one model
-    join and leave between token steps; up to four decode together."""
+    join and leave between token steps; up to 16 decode together."""
 
     def __init__(self, model: "Model"):
         h = _vp()
