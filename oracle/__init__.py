@@ -1,8 +1,8 @@
 """ctypes view of the CPU oracle (oracle/pocr_oracle.c).
 
 Test infrastructure only: tests/, ``__graft_entry__.smoke()`` and the
-``cpu_baseline`` leg of bench.py use it as the checker.  The HIP product path
-never imports it.
+``cpu_baseline`` leg of bench.py use it, to check results and to time the CPU
+baseline.  The HIP product path never imports it.
 """
 from __future__ import annotations
 

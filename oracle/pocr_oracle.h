@@ -119,7 +119,7 @@ int orc_generate(orc_model *m, const int32_t *ids, int n_ids, const float *image
                  int n_image, int image_token_id, const int32_t grid[3], int merge,
                  int max_new, const int32_t *eos, int n_eos, int32_t *out_tokens);
 
-/* ---- vision projector (SURVEY (f) 1) ---- */
+/* ---- vision projector ---- */
 /* LayerNorm (ops.go:1060-1097), the scalar path: 8-lane partial sums
  * (sumF32Scalar 1448-1466, sumSquaresCenteredScalar 1468-1490), scale =
  * fastRsqrt(var/n + eps), out = (x − mean)·scale·w + b */
@@ -133,7 +133,7 @@ int orc_project_image(const float *x, int grid_t, int grid_h, int grid_w, int vd
                       const float *norm_b, const orc_qmat *q1, const float *b1, const orc_qmat *q2, const float *b2,
                       float eps, float *out);
 
-/* ---- sampling LM head (SURVEY (f) 2) ---- */
+/* ---- sampling LM head ---- */
 /* fastRNG.Float64 (model.go:1829-1840): one SplitMix64 step of *state, the
  * top 53 bits of the mixed word as a double in [0, 1) */
 double orc_rng_float64(uint64_t *state);
