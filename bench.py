@@ -95,7 +95,7 @@ def model_embed(model, tok):
     return _EMBED[key][tok]
 
 
-def serve(model, cfg, budgets=SERVE_BUDGETS, slots=4, chunk=16, seed0=300):
+def serve(model, cfg, budgets=SERVE_BUDGETS, slots=4, chunk=16, seed0=300, sample_every=0):
     """Server-style serving of len(budgets) image requests (5 ids + 1332 visual
     rows + 11 ids, seeds 300+i; request i generates budgets[i] greedy tokens):
     one request at a time (prefill, then its own decode loop: the reference
@@ -113,16 +113,19 @@ def serve(model, cfg, budgets=SERVE_BUDGETS, slots=4, chunk=16, seed0=300):
         _, delta = lib.mm_positions(ids, IMAGE_TOKEN, grid)
         reqs.append((ids, synth.image_embeds(1332, cfg.hidden, seed=seed0 + i), ids.size + delta, n))
     seqs = [model.seq(ids.size + n + 8) for ids, _, _, n in reqs]
+    # with sample_every = k, request i with i % k == 1 draws from its top 40 at T 0.8
+    samples = [bool(sample_every) and i % sample_every == 1 for i in range(len(reqs))]
 
-    def first_token(s, ids, img):
+    def first_token(s, ids, img, i):
         s.reset()
+        s.set_sampling(*((0.8, 40, 1000 + i) if samples[i] else (0.0, 0, 0)))
         return int(s.generate(ids, 1, eos=(), image_embeds=img, image_token_id=IMAGE_TOKEN, grid=grid,
                               use_prefill=True)[0])
 
     t = time.perf_counter()
     one = []
-    for s, (ids, img, pos, n) in zip(seqs, reqs):
-        one.append(list(s.decode_greedy(first_token(s, ids, img), pos, n, eos=())))
+    for i, (s, (ids, img, pos, n)) in enumerate(zip(seqs, reqs)):
+        one.append(list(s.decode_greedy(first_token(s, ids, img, i), pos, n, eos=())))
     t_one = time.perf_counter() - t
 
     t = time.perf_counter()
@@ -132,7 +135,7 @@ def serve(model, cfg, budgets=SERVE_BUDGETS, slots=4, chunk=16, seed0=300):
         while queue and len(members) < slots:
             i = queue.pop(0)
             ids, img, pos, n = reqs[i]
-            b.join(seqs[i], first_token(seqs[i], ids, img), pos, n, eos=())
+            b.join(seqs[i], first_token(seqs[i], ids, img, i), pos, n, eos=())
             members.append(i)
         b.step(chunk)
         for i in list(members):
@@ -149,8 +152,11 @@ def serve(model, cfg, budgets=SERVE_BUDGETS, slots=4, chunk=16, seed0=300):
             continue
         k = next(j for j in range(len(one[i])) if j >= len(got[i]) or got[i][j] != one[i][j])
         ids, img, pos, n = reqs[i]
+        if samples[i]:  # a draw: the logit gap says nothing about where u fell
+            differ.append({"request": i, "token": k, "of": n, "sampled": True})
+            continue
         s = seqs[i]
-        toks = list(s.decode_greedy(first_token(s, ids, img), pos, k, eos=())) if k > 0 else []
+        toks = list(s.decode_greedy(first_token(s, ids, img, i), pos, k, eos=())) if k > 0 else []
         gap = None
         if k > 0:
             _, lg = s.step(model_embed(model, toks[k - 1]), (pos + k - 1,) * 3)
@@ -161,11 +167,12 @@ def serve(model, cfg, budgets=SERVE_BUDGETS, slots=4, chunk=16, seed0=300):
     for s in seqs:
         s.close()
     total = sum(budgets)
-    return {"requests": len(budgets), "tokens": total, "slots": slots,
+    return {"requests": len(budgets), "tokens": total, "slots": slots, "sampling_requests": sum(samples),
             "one_at_a_time": {"s": round(t_one, 3), "tok_s": round(total / t_one, 1)},
             "continuous_batch": {"s": round(t_cb, 3), "tok_s": round(total / t_cb, 1)},
             "speedup": round(t_one / t_cb, 2),
-            "tokens_match": not differ, "differ": differ}
+            "tokens_match": not differ,
+            "greedy_tokens_match": not any(not d.get("sampled") for d in differ), "differ": differ}
 
 
 def build_model(ctx, cfg, qtype, seed=0):
@@ -498,6 +505,8 @@ def main():
         print(json.dumps({"workload": "q4 serving of 8 image requests", **serve(model, cfg)}), flush=True)
         print(json.dumps({"workload": "q4 serving of 24 image requests, 16 slots",
                           **serve(model, cfg, budgets=SERVE_BUDGETS * 3, slots=16)}), flush=True)
+        print(json.dumps({"workload": "q4 serving of 24 image requests, 16 slots, every third sampling",
+                          **serve(model, cfg, budgets=SERVE_BUDGETS * 3, slots=16, sample_every=3)}), flush=True)
         return
     ids = workload_ids()
     img = synth.image_embeds(1332, cfg.hidden, seed=0)
@@ -548,6 +557,8 @@ def main():
         log(f"[bench] serving q4 {extra['serving_q4']}")
         extra["serving_q4_16slots"] = serve(model, cfg, budgets=SERVE_BUDGETS * 3, slots=16)
         log(f"[bench] serving q4, 16 slots {extra['serving_q4_16slots']}")
+        extra["serving_q4_16slots_sampling"] = serve(model, cfg, budgets=SERVE_BUDGETS * 3, slots=16, sample_every=3)
+        log(f"[bench] serving q4, 16 slots, every third request sampling {extra['serving_q4_16slots_sampling']}")
         _, m6 = build_model(ctx, cfg, lib.Q6)
         extra["batch4_decode"]["q6"] = batch_decode(m6, cfg, n_new=args.batch_tokens)
         log(f"[bench] 4-sequence batched decode q6 {extra['batch4_decode']['q6']}")
