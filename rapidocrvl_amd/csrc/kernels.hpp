@@ -35,6 +35,10 @@ struct DevMat {
 // token after token.
 constexpr int kArgSlots = 64;
 constexpr int kSlotPitch = 16;  // u64 per slot: 128 bytes
+constexpr int kMaxEos = 16;     // EOS ids the device decode loop stops on
+// err value of a decode loop that took an EOS token: not a failure, but like
+// one every later kernel of the sequence returns at once (nothing appended)
+constexpr int kErrStopped = -1;
 
 struct StepState {
     int32_t len;       // cache rows after this step's append
@@ -46,7 +50,8 @@ struct StepState {
     int32_t n_out;     // tokens emitted by the device decode loop
     int32_t has_rope;
     int32_t half;
-    int32_t pad;
+    int32_t n_eos;     // decode loop: a taken token equal to eos[i < n_eos] stops it
+    int32_t eos[kMaxEos];
     alignas(16) float cos_t[kMaxHalf];
     float sin_t[kMaxHalf];
     // greedy argmax: workgroup b of the LM head folds its best (score, row)
@@ -271,21 +276,25 @@ struct XDigits {
 };
 
 // Q4 nibble planes (NPL = kNibPlanes, the greedy LM head): the activation of
-// a 32-column chunk as four balanced base-15 digit planes
-//   x = S·(e0 + e1/15 + e2/15² + e3/15³) + e,   e_k ∈ [−7, 7],
-// S a power of two > max|x|/7 over the chunk, |e| ≤ S/(2·15³) (≈2^-14.5 of
-// the chunk maximum).  A plane packs 8 columns per dword as signed nibbles in
-// column order — the order of the Q4 codes in a weight dword — and a code
-// nibble u = code + 8 becomes the signed nibble code by u ^ 8, so a row dot
-// is one XOR and four v_dot8_i32_i4 per weight dword, combined in integer.
-constexpr int kNibPlanes = 4;
+// a 32-column chunk as six balanced base-15 digit planes
+//   x = S·(e0 + e1/15 + … + e5/15⁵) + e,   e_k ∈ [−7, 7],
+// S a power of two > max|x|/7 over the chunk, |e| ≤ S/(2·15⁵) (≤ 2^-22.3 of
+// the chunk maximum, as fine as the three byte planes of the layer GEMVs).
+// A plane packs 8 columns per dword as signed nibbles in column order — the
+// order of the Q4 codes in a weight dword — and a code nibble u = code + 8
+// becomes the signed nibble code by u ^ 8, so a row dot is one XOR and six
+// v_dot8_i32_i4 per weight dword, combined in integer.
+constexpr int kNibPlanes = 6;
+constexpr float kNibComb = 759375.0f;  // 15⁵
+template <int NPL>
+constexpr bool is_nib() { return NPL >= 4; }
 template <int CPL>
 struct XNib {
-    int n[CPL][4][4];       // [chunk][dword k: columns 8k..8k+7][plane]
-    float scale_comb[CPL];  // S / 15³
+    int n[CPL][4][kNibPlanes];  // [chunk][dword k: columns 8k..8k+7][plane]
+    float scale_comb[CPL];      // S / 15⁵
 };
 template <int QT, int CPL, int NPL>
-using XDig = typename std::conditional<NPL == kNibPlanes, XNib<CPL>, XDigits<QT, CPL>>::type;
+using XDig = typename std::conditional<is_nib<NPL>(), XNib<CPL>, XDigits<QT, CPL>>::type;
 
 // column (within a chunk) of byte m of digit dword k: Q4 dword 2k' holds the
 // low nibbles of chunk dword k' (cols 8k'+0,2,4,6), dword 2k'+1 the high ones
@@ -335,15 +344,18 @@ __device__ __forceinline__ float row_dot_nib(const Chunk (&w)[CPL], const XNib<C
     float r = 0.0f;
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
-        int a[4] = {0, 0, 0, 0};
+        int a[kNibPlanes] = {};
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             const int sw = (int)(w[j].d[k] ^ 0x88888888u);  // signed codes, column order
 #pragma unroll
-            for (int pl = 0; pl < 4; ++pl) a[pl] = __builtin_amdgcn_sdot8(sw, xd.n[j][k][pl], a[pl], false);
+            for (int pl = 0; pl < kNibPlanes; ++pl) a[pl] = __builtin_amdgcn_sdot8(sw, xd.n[j][k][pl], a[pl], false);
         }
-        // |a| ≤ 32·8·7: the base-15 combination stays far inside int32
-        const int comb = ((a[0] * 15 + a[1]) * 15 + a[2]) * 15 + a[3];
+        // |a_k| ≤ 32·8·7 = 1792 and Σ 15^k (k < 6) = 813616: the base-15
+        // combination stays inside int32 (|comb| < 1.46e9)
+        int comb = a[0];
+#pragma unroll
+        for (int pl = 1; pl < kNibPlanes; ++pl) comb = comb * 15 + a[pl];
         r = fmaf(xd.scale_comb[j], (float)comb, r);
     }
     return r;
@@ -388,7 +400,7 @@ __device__ __forceinline__ float row_dot_bytes(const Chunk (&w)[CPL], const XDig
 
 template <int QT, int CPL, int NPL = 3>
 __device__ __forceinline__ float row_dot(const Chunk (&w)[CPL], const XDig<QT, CPL, NPL> &xd) {
-    if constexpr (NPL == kNibPlanes) {
+    if constexpr (is_nib<NPL>()) {
         static_assert(QT == QT_Q4, "nibble planes pair with Q4 codes");
         return row_dot_nib<CPL>(w, xd);
     } else {
@@ -654,12 +666,12 @@ __device__ __forceinline__ void x_digits_nib(const XRegs &r, const XRegs &rw, bo
         (void)frexpf(m * (1.0f / 7.0f), &ex);  // |x|·2^-ex < 7 (+ rounding)
         const float inv = m > 0.0f ? ldexpf(1.0f, -ex) : 1.0f;
         const int sh = 16 * (G & 1);  // this lane's half of the dword
-        int pk[4] = {0, 0, 0, 0};
+        int pk[kNibPlanes] = {};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             float t = y[i] * inv;  // exact: inv is a power of two
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
+            for (int k = 0; k < kNibPlanes; ++k) {
                 // |t| ≤ 7.5 → e ∈ [−7, 7] and |t − e| ≤ 1/2
                 const float e = __builtin_amdgcn_fmed3f(rintf(t), -7.0f, 7.0f);
                 pk[k] |= ((int)e & 15) << (4 * i + sh);
@@ -667,12 +679,15 @@ __device__ __forceinline__ void x_digits_nib(const XRegs &r, const XRegs &rw, bo
             }
         }
 #pragma unroll
-        for (int k = 0; k < 4; ++k) pk[k] |= xchg_i(pk[k]);
+        for (int k = 0; k < kNibPlanes; ++k) pk[k] |= xchg_i(pk[k]);
         if (valid && (G & 1) == 0) {
+            // dword q of the chunk: its six planes at record ints 6q..6q+5
             const int c = G / 8, q = (G & 7) >> 1;
-            int *rec = lds + c * RS;
-            *reinterpret_cast<int4 *>(rec + 4 * q) = make_int4(pk[0], pk[1], pk[2], pk[3]);
-            if (q == 0) rec[NDW * 3 + 3] = __float_as_int(m > 0.0f ? ldexpf(1.0f, ex) : 1.0f);
+            int2 *rec = reinterpret_cast<int2 *>(lds + c * RS + kNibPlanes * q);
+            rec[0] = make_int2(pk[0], pk[1]);
+            rec[1] = make_int2(pk[2], pk[3]);
+            rec[2] = make_int2(pk[4], pk[5]);
+            if (q == 0) lds[c * RS + NDW * 3 + 3] = __float_as_int(m > 0.0f ? ldexpf(1.0f, ex) : 1.0f);
         }
     }
     if (norm) {
@@ -695,19 +710,25 @@ __device__ __forceinline__ float x_norm_factor(bool norm, int cols, float eps, c
 template <int QT, int LPR, int CPL, int NPL = 3>
 __device__ __forceinline__ void load_digits(const int *lds, int l, XDig<QT, CPL, NPL> &xd) {
     constexpr int NDW = DigitRec<QT>::NDW, RS = DigitRec<QT>::RS;
-    if constexpr (NPL == kNibPlanes) {
+    if constexpr (is_nib<NPL>()) {
+        static_assert(4 * kNibPlanes <= NDW * 3 + 3, "nibble planes overlap the chunk scale");
 #pragma unroll
         for (int j = 0; j < CPL; ++j) {
             const int4 *rec = reinterpret_cast<const int4 *>(lds + (l + j * LPR) * RS);
+            int v[4 * kNibPlanes];
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const int4 t = rec[k];
-                xd.n[j][k][0] = t.x;
-                xd.n[j][k][1] = t.y;
-                xd.n[j][k][2] = t.z;
-                xd.n[j][k][3] = t.w;
+            for (int i = 0; i < kNibPlanes; ++i) {
+                const int4 t = rec[i];
+                v[4 * i] = t.x;
+                v[4 * i + 1] = t.y;
+                v[4 * i + 2] = t.z;
+                v[4 * i + 3] = t.w;
             }
-            xd.scale_comb[j] = __int_as_float(lds[(l + j * LPR) * RS + NDW * 3 + 3]) * (1.0f / 3375.0f);
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+#pragma unroll
+                for (int pl = 0; pl < kNibPlanes; ++pl) xd.n[j][k][pl] = v[kNibPlanes * k + pl];
+            xd.scale_comb[j] = __int_as_float(lds[(l + j * LPR) * RS + NDW * 3 + 3]) * (1.0f / kNibComb);
         }
         return;
     } else {
@@ -989,8 +1010,10 @@ __device__ __forceinline__ void load_group(const SegSel &sel, int row_bytes, int
 // TAG only separates instances for profiling (TAG=1: the timing entry point).
 // ONE: the grid gives every wave at most one group (no row loop, no prefetch
 // registers), for the large single-matrix launch.
-// NPL: digit planes of the activation (3 byte planes, 2 for the Q8/Q6 greedy
-// head, kNibPlanes for the Q4 greedy head).
+// NPL: digit planes of the activation (3 byte planes; kNibPlanes nibble
+// planes for the Q4 greedy head).  Both read x to about 2^-22 of each chunk's
+// maximum, so a greedy choice departs from the exact one only where the top
+// two scores lie within that resolution.
 // NV: activation vectors sharing each weight pass (batched decode, M = NV):
 // every chunk is dotted against each vector's digits (read from LDS per
 // group), and the reduce-scatter runs over U·NV entries e = u·NV + v.
@@ -1038,7 +1061,7 @@ __device__ __forceinline__ void gemv_body(GemvParams p, int pro, int epi, const 
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
         const float *xv = p.x + (NV > 1 ? v * q.x_stride : 0);
-        if constexpr (NPL == kNibPlanes) x_load_nib(xv, p.norm_w, norm && v == 0, cols, xr[v]);
+        if constexpr (is_nib<NPL>()) x_load_nib(xv, p.norm_w, norm && v == 0, cols, xr[v]);
         else x_load(xv, p.norm_w, norm && v == 0, cols, xr[v]);
     }
     // first group: weights, then the writer lane's epilogue operands (row
@@ -1058,7 +1081,7 @@ __device__ __forceinline__ void gemv_body(GemvParams p, int pro, int epi, const 
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
         // the norm weight was loaded once, with vector 0
-        if constexpr (NPL == kNibPlanes) x_digits_nib(xr[v], xr[0], norm, cols, lds + v * recs, red + v * kWaves);
+        if constexpr (is_nib<NPL>()) x_digits_nib(xr[v], xr[0], norm, cols, lds + v * recs, red + v * kWaves);
         else x_digits<QT>(xr[v], xr[0], norm, cols, lds + v * recs, red + v * kWaves);
     }
     __syncthreads();
@@ -1288,6 +1311,11 @@ __device__ __forceinline__ void step_begin_body(StepState *st, const float *embe
                 const int p = st->next_pos;
                 st->next_pos = p + 1;
                 st->pos[0] = st->pos[1] = st->pos[2] = p;
+                // the generation loop stops at an EOS token once it is in the
+                // output, before any step for it (model.go:1545-1548)
+                const int ne = min(st->n_eos, kMaxEos);
+                for (int i = 0; i < ne; ++i)
+                    if (st->eos[i] == tok) err = kErrStopped;
             }
         }
         if (!err) {

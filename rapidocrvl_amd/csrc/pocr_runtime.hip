@@ -254,9 +254,9 @@ static bool gemv_fast_kernel(int lpr, int cpl, const void **fn) {
 #endif
 constexpr int kBigU = POCR_BIG_U;
 // digit planes of the greedy LM head: Q4 → the nibble planes (v_dot8),
-// Q8 / Q6 → two byte planes
+// Q8 / Q6 → three byte planes, like every other launch
 template <int QT>
-constexpr int big_planes() { return QT == QT_Q4 ? kNibPlanes : 2; }
+constexpr int big_planes() { return QT == QT_Q4 ? kNibPlanes : 3; }
 
 // one: every wave gets at most one row group (the big launch covers them all);
 // argmax: the greedy LM head, whose scores only feed the argmax, takes
@@ -1626,9 +1626,25 @@ static bool is_eos(int32_t t, const int32_t *eos, int n) {
     return false;
 }
 
+// the decode loop's EOS ids in the step state; a list longer than the state
+// holds leaves the device loop running and the host cuts the cache at the EOS
+static void set_state_eos(StepState &hs, const int32_t *eos, int n_eos) {
+    hs.n_eos = n_eos <= kMaxEos ? n_eos : 0;
+    for (int i = 0; i < kMaxEos; ++i) hs.eos[i] = i < hs.n_eos ? eos[i] : 0;
+}
+
+static bool state_failed(const StepState &hs) { return hs.err != 0 && hs.err != kErrStopped; }
+
+// The generation loop ended at an EOS token, output index `index` (the first
+// token is index 0): the reference ran no step for it, so the cache holds the
+// rows of tokens 0..index-1 (model.go:1538-1548).  Rows later steps of the
+// chunk appended are dropped and the state is cleared (a stopped state would
+// turn the sequence's next step into a no-op).
+static int end_at_eos(pocr_seq *s, int start_len, int index) { return seq_set_state(s, start_len + index); }
+
 // Greedy decode loop (model.go:1538-1568) with the step graph replayed on the
-// device.  Tokens are checked for EOS every `batch` steps; steps run past an
-// EOS only append rows nobody reads.
+// device.  The step prologue stops the loop at an EOS token (later replays of
+// the chunk do nothing); the host reads the tokens every `batch` steps.
 static int decode_locked(pocr_seq *s, int32_t first_token, int32_t first_pos, int max_new, const int32_t *eos,
                          int n_eos, int32_t *out_tokens) {
     pocr_model *m = s->m;
@@ -1646,9 +1662,11 @@ static int decode_locked(pocr_seq *s, int32_t first_token, int32_t first_pos, in
     if (use_graph) RC(build_decode_graph(s));
     StepState hs;
     RC(read_state(s, &hs));
+    const int start_len = hs.len;
     hs.err = 0;
     hs.n_out = 0;
     hs.next_pos = first_pos;
+    set_state_eos(hs, eos, n_eos);
     for (int i = 0; i < kArgSlots; ++i) hs.argmax_slot[i * kSlotPitch] = 0ull;
     hs.argmax_slot[0] = (1ull << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)first_token);
     HIP_TRY(hipMemcpyAsync(s->st, &hs, sizeof(hs), hipMemcpyHostToDevice, st));
@@ -1665,13 +1683,13 @@ static int decode_locked(pocr_seq *s, int32_t first_token, int32_t first_pos, in
         }
         launched += n;
         RC(read_state(s, &hs));
-        if (hs.err) return fail(POCR_ERR_DEVICE, "decode: device state error %d", hs.err);
+        if (state_failed(hs)) return fail(POCR_ERR_DEVICE, "decode: device state error %d", hs.err);
         tok.resize(hs.n_out);
         HIP_TRY(hipMemcpy(tok.data(), s->tokens, (size_t)hs.n_out * 4, hipMemcpyDeviceToHost));
         for (; produced < hs.n_out; ++produced) {
             out_tokens[produced] = tok[produced];
             if (is_eos(tok[produced], eos, n_eos)) {
-                s->len = hs.len;
+                RC(end_at_eos(s, start_len, produced));
                 return produced + 1;
             }
         }
@@ -2003,11 +2021,13 @@ int enqueue_batch_step(DecodeBatch &b) {
 
 // the first token of a batched decode sits in the argmax slots as if the
 // previous step had chosen it (the step prologue reads it from there)
-int seed_first_token(pocr_seq *s, int32_t first_token, int32_t first_pos, StepState &hs) {
+int seed_first_token(pocr_seq *s, int32_t first_token, int32_t first_pos, const int32_t *eos, int n_eos,
+                     StepState &hs) {
     RC(read_state(s, &hs));
     hs.err = 0;
     hs.n_out = 0;
     hs.next_pos = first_pos;
+    set_state_eos(hs, eos, n_eos);
     for (int k = 0; k < kArgSlots; ++k) hs.argmax_slot[k * kSlotPitch] = 0ull;
     hs.argmax_slot[0] = (1ull << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)first_token);
     HIP_TRY(hipMemcpyAsync(s->st, &hs, sizeof(StepState), hipMemcpyHostToDevice, s->m->ctx->stream));
@@ -2096,7 +2116,11 @@ extern "C" int pocr_decode_batch(pocr_seq *const *seqs, int n_seq, const int32_t
     // per-sequence state: the first token sits in the argmax slots as if the
     // previous step had chosen it (the step prologue reads it from there)
     std::vector<StepState> hs(n_seq);
-    for (int i = 0; i < n_seq; ++i) RC(seed_first_token(seqs[i], first_tokens[i], first_positions[i], hs[i]));
+    std::vector<int> start_len(n_seq);
+    for (int i = 0; i < n_seq; ++i) {
+        start_len[i] = seqs[i]->len;
+        RC(seed_first_token(seqs[i], first_tokens[i], first_positions[i], eos, n_eos, hs[i]));
+    }
     const char *g_env = getenv("POCR_HIP_GRAPH");
     const bool use_graph = !(g_env && g_env[0] == '0');
     if (use_graph) {
@@ -2123,7 +2147,8 @@ extern "C" int pocr_decode_batch(pocr_seq *const *seqs, int n_seq, const int32_t
         for (int i = 0; i < n_seq; ++i) {
             RC(read_state(seqs[i], &hs[i]));
             if (done[i]) continue;
-            if (hs[i].err) return fail(POCR_ERR_DEVICE, "decode_batch: sequence %d: device state error %d", i, hs[i].err);
+            if (state_failed(hs[i]))
+                return fail(POCR_ERR_DEVICE, "decode_batch: sequence %d: device state error %d", i, hs[i].err);
             tok.resize(hs[i].n_out);
             HIP_TRY(hipMemcpy(tok.data(), seqs[i]->tokens, (size_t)hs[i].n_out * 4, hipMemcpyDeviceToHost));
             for (; produced[i] < hs[i].n_out && !done[i]; ++produced[i]) {
@@ -2138,9 +2163,11 @@ extern "C" int pocr_decode_batch(pocr_seq *const *seqs, int n_seq, const int32_t
         if (!done[i]) {  // the token chosen by the last step
             out_tokens[(size_t)i * max_new + produced[i]] = pending_token(hs[i]);
             ++produced[i];
+            seqs[i]->len = hs[i].len;
+        } else {
+            RC(end_at_eos(seqs[i], start_len[i], produced[i] - 1));
         }
         out_counts[i] = produced[i];
-        seqs[i]->len = hs[i].len;
     }
     return POCR_OK;
 }
@@ -2160,6 +2187,7 @@ struct pocr_batch {
         int steps = 0;                // device steps run
         std::vector<int32_t> eos;
         std::vector<int32_t> out;     // tokens produced, first token first
+        int start_len = 0;            // cache rows at the join
         bool finished = false;
     };
     pocr_model *m = nullptr;
@@ -2244,12 +2272,13 @@ extern "C" int pocr_batch_join(pocr_batch *b, pocr_seq *s, int32_t first_token, 
     mb.s = s;
     mb.max_new = max_new;
     mb.eos.assign(eos, eos + n_eos);
+    mb.start_len = s->len;
     if (max_new == 1 || is_eos(first_token, eos, n_eos)) {
         mb.out.push_back(first_token);  // done before any device step
         mb.finished = true;
     } else {
         StepState hs;
-        RC(seed_first_token(s, first_token, first_pos, hs));
+        RC(seed_first_token(s, first_token, first_pos, eos, n_eos, hs));
         b->cur.reset();
     }
     s->batch = b;
@@ -2317,7 +2346,7 @@ extern "C" int pocr_batch_step(pocr_batch *b, int max_steps) {
     for (auto &mb : b->members) {
         if (mb.finished) continue;
         RC(read_state(mb.s, &hs));
-        if (hs.err) return fail(POCR_ERR_DEVICE, "pocr_batch_step: device state error %d", hs.err);
+        if (state_failed(hs)) return fail(POCR_ERR_DEVICE, "pocr_batch_step: device state error %d", hs.err);
         mb.s->len = hs.len;
         mb.steps += k;
         // tokens the steps appended (the first one is the seeded first token)
@@ -2327,6 +2356,7 @@ extern "C" int pocr_batch_step(pocr_batch *b, int max_steps) {
         for (int t = (int)mb.out.size(); t < hs.n_out && !mb.finished; ++t) {
             mb.out.push_back(tok[t]);
             mb.finished = is_eos(tok[t], mb.eos.data(), (int)mb.eos.size());
+            if (mb.finished) RC(end_at_eos(mb.s, mb.start_len, t));
         }
         // the token the last step chose ends the member at its budget or an EOS
         if (!mb.finished) {

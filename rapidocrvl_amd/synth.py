@@ -20,9 +20,15 @@ _ROLE_ID = {r: i for i, r in enumerate(ROLES)}
 
 
 def bf16_round(x: np.ndarray) -> np.ndarray:
-    b = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
-    b = (b + 0x7FFF + ((b >> 16) & 1)) & 0xFFFF0000
-    return b.astype(np.uint32).view(np.float32)
+    """Round f32 to bf16 (nearest, ties to even) and back.  In place on a
+    copy in uint32: for every finite f32 the bits plus 0x8000 stay below 2^32."""
+    a = np.array(x, dtype=np.float32, copy=True, order="C")
+    b = a.view(np.uint32)
+    r = (b >> 16) & 1
+    r += 0x7FFF
+    b += r
+    b &= 0xFFFF0000
+    return a
 
 
 def normal(shape, seed, std=0.02):

@@ -58,6 +58,9 @@ def test_decode_batch_eos_stops_one_sequence(orc, ctx):
     got = lib.decode_batch(list(seqs), list(firsts), [12, 25], 16, eos=(stop,))
     assert list(got[0]) == expect0
     assert list(got[1]) == expect1
+    # cache rows: the prompt's and one per token before the EOS (or the last token)
+    assert len(seqs[0]) == 12 + len(expect0) - 1
+    assert len(seqs[1]) == 25 + len(expect1) - 1
 
 
 def test_decode_batch_rejects_bad_arguments(ctx):
@@ -163,6 +166,7 @@ def test_continuous_batch_eos_and_leave_early(orc, ctx):
         n, done = b.poll(seqs[i][0])
         assert done and n == len(exp)
         assert list(b.leave(seqs[i][0])) == exp
+        assert len(seqs[i][0]) == prompts[i].size + len(exp) - 1
     # a left sequence takes ordinary calls again
     seqs[2][0].reset()
     assert b.step(4) == 0

@@ -6,6 +6,8 @@ import pytest
 
 from rapidocrvl_amd import lib
 
+import digit_model as dm
+
 pytestmark = pytest.mark.gpu
 
 Q8, Q4, Q6 = 1000, 1001, 1002
@@ -82,21 +84,63 @@ def test_matvec_vectors_per_pass(ctx, orc, rng, qtype, shape):
             _close(got[i], orc.matvec(qtype, q.scales, q.packed, x[i]))
 
 
+F32_STEPS = 10 * 2.0 ** -24  # convert, chunk fma, ≤ 6 lane-reduction adds, row scale (+1 spare)
+
+
 @pytest.mark.parametrize("qtype", [Q8, Q4, Q6], ids=["q8", "q4", "q6"])
 def test_matvec_argmax(ctx, orc, rng, qtype):
+    """The greedy head computes codes · digitize(x) (nibble planes for Q4,
+    byte planes for Q8/Q6, restated in tests/digit_model.py) up to its f32
+    steps; its choice is the exact argmax unless the exact top scores lie
+    within the digitization's actual deviation plus those f32 steps."""
     q = _qmat(rng, 103424, 1024, qtype)
     w = ctx.upload(q)
+    codes = lib.unpack_rows(qtype, q.packed, q.cols)
+    nib = qtype == Q4
     for seed in range(3):
         x = np.random.default_rng(seed).standard_normal(1024).astype(np.float32)
-        logits = orc.matvec(qtype, q.scales, q.packed, x)
+        exact, _ = dm.scores(qtype, codes, q.scales, x)
+        dig, mag = dm.scores(qtype, codes, q.scales, dm.digitize(qtype, x, nib))
+        f32b = F32_STEPS * mag
+        dev = np.abs(dig - exact)  # the digit planes' own deviation, per row
+        # about 2^-22 of each chunk's maximum: 1e-6 of the largest score
+        assert dev.max() <= 1e-6 * np.abs(exact).max()
         idx, score = ctx.matvec_argmax(w, x)
-        top2 = np.sort(logits)[-2:]
-        if top2[1] - top2[0] > 1e-4 * abs(top2[1]):
-            assert idx == int(np.argmax(logits))
-        # the greedy head reads x to 2^-15 of each 32-column chunk's maximum
-        # (two digit planes): scores agree to 1e-4 relative, inside the path's
-        # 1e-2 / 1e-3 logit bar
-        assert abs(score - logits[idx]) <= 1e-4 * max(1, abs(score))
+        assert abs(score - dig[idx]) <= f32b[idx]
+        best = int(np.argmax(exact))
+        assert exact[best] - exact[idx] <= dev[best] + dev[idx] + f32b[best] + f32b[idx]
+        logits = orc.matvec(qtype, q.scales, q.packed, x)
+        assert idx == int(np.argmax(logits)) or exact[best] - exact[idx] <= dev[best] + dev[idx] + f32b[best] + f32b[idx]
+
+
+@pytest.mark.parametrize("qtype", [Q8, Q4, Q6], ids=["q8", "q4", "q6"])
+def test_matvec_argmax_planted_near_tie(ctx, orc, qtype):
+    """Rows 100 and 200 differ in one code, at a column whose activation is
+    2.2e-5 of its chunk's maximum: row 200 wins by ~3e-6, below what a head
+    reading x to 2^-14.5 (four nibble planes) or 2^-14 (two byte planes)
+    resolves (it would see a tie and take row 100) and far above the head's
+    2^-22 resolution and the f32 rounding of these small scores."""
+    rows, cols, j, i0 = 4096, 1024, 64, 65
+    rng = np.random.default_rng(7)
+    wf = (rng.standard_normal((rows, cols)) * 1e-4).astype(np.float32)
+    wf[100] = 0.0
+    wf[100, i0] = 0.875
+    wf[200] = wf[100]
+    wf[200, j] = 0.125
+    q = lib.QMatrix.quantize(wf, qtype)
+    codes = lib.unpack_rows(qtype, q.packed, cols)
+    assert q.scales[100] == q.scales[200] and codes[200, j] > 0 and codes[100, j] == 0
+    x = rng.standard_normal(cols).astype(np.float32)
+    x[64:96] = rng.uniform(-0.9, 0.9, 32).astype(np.float32)
+    x[i0] = 1.0
+    x[j] = 2.2e-5
+    exact, _ = dm.scores(qtype, codes, q.scales, x)
+    assert int(np.argmax(exact)) == 200 and exact[200] - exact[100] > 1e-6
+    assert int(np.argmax(orc.matvec(qtype, q.scales, q.packed, x))) == 200
+    idx, score = ctx.matvec_argmax(ctx.upload(q), x)
+    assert idx == 200
+    dig, mag = dm.scores(qtype, codes[[200]], q.scales[[200]], dm.digitize(qtype, x, qtype == Q4))
+    assert abs(score - dig[0]) <= F32_STEPS * mag[0]
 
 
 def test_argmax_ties_pick_lowest_index(ctx):

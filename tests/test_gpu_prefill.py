@@ -16,6 +16,14 @@ MID = DecoderConfig(hidden=1024, inter=3072, layers=3, heads=16, kv_heads=2, hea
                     rope_theta=500000.0)
 
 
+def assert_same_choice(gt, ot, gl, ol):
+    """Greedy tokens agree, unless the oracle's scores of the two picks are
+    closer than twice the measured logit error (each pick's logit then moved
+    by at most that error: the flip is the logit bar's, not a new one)."""
+    err = float(np.max(np.abs(np.asarray(gl, np.float64) - ol)))
+    assert gt == ot or float(ol[ot]) - float(ol[gt]) <= 2 * err, (gt, ot, err)
+
+
 def _pair(orc, ctx, cfg, qtype, seed=3, quirk=True):
     w = synth.make_weights(cfg, qtype, seed=seed)
     om = orc.Model(cfg)
@@ -64,7 +72,7 @@ def test_prefill_matches_token_steps(orc, ctx, cfg, qtype, quirk):
     gt, gl = gs.prefill(w["embed"][ids], pos, want_logits=True)
     _check_logits(gl, ol)
     assert gt == int(np.argmax(gl))
-    assert gt == ot or np.sort(ol)[-1] - np.sort(ol)[-2] < 1e-4
+    assert_same_choice(gt, ot, gl, ol)
     assert len(gs) == n
     _check_kv(gs, os_, cfg, n)
 
@@ -81,7 +89,7 @@ def test_prefill_after_cached_rows(orc, ctx, qtype):
         gs.step(w["embed"][ids[i]], tuple(pos[i]), need_logits=False)
     gt, gl = gs.prefill(w["embed"][ids[5:]], pos[5:], want_logits=True)
     _check_logits(gl, ol)
-    assert gt == ot or np.sort(ol)[-1] - np.sort(ol)[-2] < 1e-4
+    assert_same_choice(gt, ot, gl, ol)
     _check_kv(gs, os_, MID, 42)
 
 

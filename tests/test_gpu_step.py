@@ -14,6 +14,14 @@ MID = DecoderConfig(hidden=1024, inter=3072, layers=3, heads=16, kv_heads=2, hea
                     rope_theta=500000.0)
 
 
+def assert_same_choice(gt, ot, gl, ol):
+    """Greedy tokens agree, unless the oracle's scores of the two picks are
+    closer than twice the measured logit error (each pick's logit then moved
+    by at most that error: the flip is the logit bar's, not a new one)."""
+    err = float(np.max(np.abs(np.asarray(gl, np.float64) - ol)))
+    assert gt == ot or float(ol[ot]) - float(ol[gt]) <= 2 * err, (gt, ot, err)
+
+
 def _pair(orc, ctx, cfg, qtype, seed=3, quirk=True):
     w = synth.make_weights(cfg, qtype, seed=seed)
     om = orc.Model(cfg)
@@ -46,7 +54,7 @@ def test_step_logits_and_kv(orc, ctx, cfg, qtype, quirk):
         assert np.sqrt(np.mean((gl - ol) ** 2)) <= 1e-3 * np.sqrt(np.mean(ol ** 2))
         _close(gl, ol, 2e-4)
         assert gt == int(np.argmax(gl))
-        assert gt == ot or np.sort(ol)[-1] - np.sort(ol)[-2] < 1e-4
+        assert_same_choice(gt, ot, gl, ol)
     assert len(gs) == len(os_) == 10
     for li in range(cfg.layers):
         gk, gv = gs.read_kv(li)
@@ -92,9 +100,25 @@ def test_generate_eos(orc, ctx):
     full = om.generate(ids, 24, eos=())
     eos = int(full[5])
     want = om.generate(ids, 24, eos=(eos,))
-    got = gm.seq(64).generate(ids, 24, eos=(eos,))
+    s = gm.seq(64)
+    got = s.generate(ids, 24, eos=(eos,))
     assert list(got) == list(want)
     assert got[-1] == eos
+    # the loop stops at the EOS before any step for it (model.go:1545-1548):
+    # one cache row per prompt token and per token before the EOS, although
+    # the device ran its chunk of 16 steps
+    assert len(s) == ids.size + len(got) - 1
+    ref = gm.seq(64)
+    ref.generate(ids, 24, eos=())
+    for li in (0, MID.layers - 1):
+        k, v = s.read_kv(li)
+        rk, rv = ref.read_kv(li)
+        n = k.size
+        assert n == len(s) * MID.kv_rows
+        assert np.array_equal(k, rk[:n]) and np.array_equal(v, rv[:n])
+    # the sequence steps on from there: its next row is row len(s)
+    tok, _ = s.step(w["embed"][eos], (len(s),) * 3)
+    assert len(s) == ids.size + len(got)
 
 
 @pytest.mark.parametrize("qtype", [Q4, Q6], ids=["q4", "q6"])
