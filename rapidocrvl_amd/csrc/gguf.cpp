@@ -214,10 +214,11 @@ int parse(pocr_gguf *g) {
         if (!elem_count(t.dims, n)) return fail(POCR_ERR_ARG, "gguf: tensor %s has invalid shape", t.name.c_str());
         const int64_t size = tensor_bytes(t);
         if (size <= 0) return fail(POCR_ERR_ARG, "gguf: tensor %s has invalid type or shape", t.name.c_str());
-        if (t.offset > (uint64_t)INT64_MAX) return fail(POCR_ERR_ARG, "gguf: tensor %s offset too large", t.name.c_str());
-        const int64_t start = (int64_t)g->data_start + (int64_t)t.offset;
-        if (start < (int64_t)g->data_start || start > g->file_size)
+        // compared in unsigned before any addition (data_start ≤ file_size
+        // above), so no sum can overflow
+        if (t.offset > (uint64_t)g->file_size - g->data_start)
             return fail(POCR_ERR_ARG, "gguf: tensor %s offset exceeds file size", t.name.c_str());
+        const int64_t start = (int64_t)(g->data_start + t.offset);
         if (size > g->file_size - start) return fail(POCR_ERR_ARG, "gguf: tensor %s exceeds file size", t.name.c_str());
     }
     return POCR_OK;

@@ -92,9 +92,12 @@ def test_open_rejects_invalid_metadata_keys(tmp_path, meta):
     ([4], lib.Q8, 0, bytes(64)),  # a Q*_ROW tensor must be 2-D
     ([0], 0, 0, b""),  # zero bytes is an invalid size
     ([1], 0, 1 << 63, bytes(4)),
+    ([1], 0, I64_MAX, bytes(4)),  # data start + offset would overflow int64
+    ([1], 0, I64_MAX - 16, bytes(4)),
+    ([1], 0, U64_MAX, bytes(4)),
 ], ids=["too-many-dims", "negative-dim-after-cast", "unknown-type", "offset-exceeds-file", "tensor-exceeds-file",
         "f32-bytes-overflow", "q4-cols-overflow", "q8-cols-overflow", "q6-cols-overflow", "q8-1d", "empty",
-        "offset-too-large"])
+        "offset-too-large", "offset-int64-max", "offset-near-int64-max", "offset-u64-max"])
 def test_open_rejects_invalid_tensor_metadata(tmp_path, dims, typ, offset, data):
     head = _head(1, 0) + _tensor_info("x.weight", dims, typ, offset)
     _rejects(_write(tmp_path, "t.gguf", _with_data(head, data)))
