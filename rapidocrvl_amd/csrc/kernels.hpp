@@ -286,12 +286,20 @@ struct XDigits {
 // v_dot8_i32_i4 per weight dword, combined in integer.
 constexpr int kNibPlanes = 6;
 constexpr float kNibComb = 759375.0f;  // 15⁵
+// The single-vector greedy head scores every row with the first kNibFast
+// planes and rescores only the rows that can still be the group's best with
+// all kNibPlanes (gemv_body): x̃₆ − x̃₄ = S·(e4/15⁴ + e5/15⁵), at most
+// 7·(15⁻⁴ + 15⁻⁵)·S per column.
+constexpr int kNibFast = 4;
+constexpr float kNibTail = 7.0f / 50625.0f + 7.0f / 759375.0f;
 template <int NPL>
 constexpr bool is_nib() { return NPL >= 4; }
 template <int CPL>
 struct XNib {
     int n[CPL][4][kNibPlanes];  // [chunk][dword k: columns 8k..8k+7][plane]
     float scale_comb[CPL];      // S / 15⁵
+    float scale_fast[CPL];      // S / 15³
+    float S[CPL];
 };
 template <int QT, int CPL, int NPL>
 using XDig = typename std::conditional<is_nib<NPL>(), XNib<CPL>, XDigits<QT, CPL>>::type;
@@ -339,24 +347,26 @@ __device__ __forceinline__ int spread6(uint32_t g) {
     return (int)r;
 }
 
-template <int CPL>
+// the first NP nibble planes (NP = kNibPlanes: all of them)
+template <int CPL, int NP = kNibPlanes>
 __device__ __forceinline__ float row_dot_nib(const Chunk (&w)[CPL], const XNib<CPL> &xd) {
     float r = 0.0f;
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
-        int a[kNibPlanes] = {};
+        int a[NP] = {};
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             const int sw = (int)(w[j].d[k] ^ 0x88888888u);  // signed codes, column order
 #pragma unroll
-            for (int pl = 0; pl < kNibPlanes; ++pl) a[pl] = __builtin_amdgcn_sdot8(sw, xd.n[j][k][pl], a[pl], false);
+            for (int pl = 0; pl < NP; ++pl) a[pl] = __builtin_amdgcn_sdot8(sw, xd.n[j][k][pl], a[pl], false);
         }
         // |a_k| ≤ 32·8·7 = 1792 and Σ 15^k (k < 6) = 813616: the base-15
-        // combination stays inside int32 (|comb| < 1.46e9)
+        // combination stays inside int32 (|comb| < 1.46e9; four planes < 2^24,
+        // exact in f32)
         int comb = a[0];
 #pragma unroll
-        for (int pl = 1; pl < kNibPlanes; ++pl) comb = comb * 15 + a[pl];
-        r = fmaf(xd.scale_comb[j], (float)comb, r);
+        for (int pl = 1; pl < NP; ++pl) comb = comb * 15 + a[pl];
+        r = fmaf(NP == kNibPlanes ? xd.scale_comb[j] : xd.scale_fast[j], (float)comb, r);
     }
     return r;
 }
@@ -728,7 +738,10 @@ __device__ __forceinline__ void load_digits(const int *lds, int l, XDig<QT, CPL,
             for (int k = 0; k < 4; ++k)
 #pragma unroll
                 for (int pl = 0; pl < kNibPlanes; ++pl) xd.n[j][k][pl] = v[kNibPlanes * k + pl];
-            xd.scale_comb[j] = __int_as_float(lds[(l + j * LPR) * RS + NDW * 3 + 3]) * (1.0f / kNibComb);
+            const float S = __int_as_float(lds[(l + j * LPR) * RS + NDW * 3 + 3]);
+            xd.scale_comb[j] = S * (1.0f / kNibComb);
+            xd.scale_fast[j] = S * (1.0f / 3375.0f);
+            xd.S[j] = S;
         }
         return;
     } else {
@@ -1096,11 +1109,57 @@ __device__ __forceinline__ void gemv_body(GemvParams p, int pro, int epi, const 
     const bool in_place = epi == EPI_OPROJ ? oproj_in_place(p, st_of(p, q, my_v)) : false;
     float best_v = -INFINITY;
     int best_r = 0x7FFFFFFF;
+    // Two-pass greedy head (Q4 nibble planes, one vector): a row's score from
+    // kNibFast planes differs from its score from all kNibPlanes by at most
+    //   β = xscale·scale·Σ_c S_c·(256·kNibTail + 2·12·2⁻²⁴·1920)
+    // (|code| ≤ 8 on 32 columns per chunk; the second term covers the f32
+    // steps of both scores, |x̃/S| ≤ 7.5).  Within a row group, every row whose
+    // all-plane score is the group's best has s_fast + β ≥ max(s_fast − β), so
+    // rescoring only those rows with all planes finds that best exactly.
+    constexpr bool kTwoPass = is_nib<NPL>() && NV == 1 && NMAT == 1;
+    float kwin = 0.0f;
+    if constexpr (kTwoPass) {
+        float ks[1][1] = {{0.0f}};
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) ks[0][0] += xd.S[j];
+        reduce_scatter<LPR, 1, 1>(ks, lane);  // Σ_c S_c over the row's chunks, in every lane
+        kwin = ks[0][0] * (256.0f * kNibTail + 2.0f * 12.0f * 1920.0f / 16777216.0f) * 1.0001f;
+    }
 
     // one group: row sums, reduce-scatter, epilogue by the writer lanes
     auto compute = [&](int gg, const Chunk (&wc)[U][NMAT][CPL], const float (&sc)[NMAT], float rs) {
         const int r = (gg * U + my_u) * RPW + sub;
         float acc[E > 8 ? E : 8][NMAT];
+        if constexpr (kTwoPass) {
+#pragma unroll
+            for (int u = 0; u < U; ++u) acc[u][0] = row_dot_nib<CPL, kNibFast>(wc[u][0], xd);
+            reduce_scatter<LPR, E, 1>(acc, lane);
+            const bool valid = writer && r < rows;
+            const float f = xscale * sc[0];
+            const float s_fast = acc[0][0] * f;
+            const float beta = f * kwin;
+            const uint32_t lo = wave_max_u32(valid ? ordered_bits(s_fast - beta) : 0u);
+            // with logits requested every row is rescored (they are written)
+            const bool cand = valid && (p.out != nullptr || ordered_bits(s_fast + beta) >= lo);
+            const unsigned long long cm = __ballot(cand);
+            float s_all = 0.0f;
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                unsigned long long bits = 0ull;
+#pragma unroll
+                for (int sb = 0; sb < RPW; ++sb) bits |= 1ull << (sb * LPR + u * SPAN);
+                if (cm & bits) {  // wave-uniform
+                    float a6[1][1] = {{row_dot_nib<CPL, kNibPlanes>(wc[u][0], xd)}};
+                    reduce_scatter<LPR, 1, 1>(a6, lane);
+                    if (my_u == u) s_all = a6[0][0] * f;
+                }
+            }
+            if (cand) {
+                const float sv[1] = {s_all};
+                gemv_epilogue(p, epi, r, my_o + r, sv, rs, in_place, best_v, best_r);
+            }
+            return;
+        }
         if constexpr (NV == 1) {
 #pragma unroll
             for (int u = 0; u < U; ++u)

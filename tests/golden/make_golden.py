@@ -1,6 +1,8 @@
 #!/usr/bin/env python3
 """Writes tests/golden/oracle_streams.json (run from the repository root:
-``python tests/golden/make_golden.py``).
+``python tests/golden/make_golden.py``) and, with ``--full``,
+tests/golden/oracle_streams_full.json: the greedy streams of the two
+image-conditioned workloads at their real sizes (about 15 minutes on 8 cores).
 
 The reference is pure Go and cannot run here, and its tests hold no golden
 token streams, so these streams come from the oracle (the C restatement of the
@@ -74,7 +76,111 @@ def run_case(case, weights):
     return name, rec
 
 
+IMAGE_TOKEN = 100295
+IMAGE_GRID = (1, 72, 74)  # 36 x 37 merged patches = 1332 visual rows
+
+
+def image_prompt(head_seed, n_head, tail_seed, n_tail):
+    """n_head ids, 1332 image placeholders, n_tail ids (ids uniform in [0, 100000))."""
+    return np.concatenate([synth.prompt_ids(n_head, seed=head_seed), np.full(1332, IMAGE_TOKEN, np.int32),
+                           synth.prompt_ids(n_tail, seed=tail_seed)]).astype(np.int32)
+
+
+def full_cases():
+    """(name, qtype, ids, image seed, max_new, (head seed, n_head, tail seed, n_tail)).
+
+    image_q4_1345: 5 ids + 1332 visual rows + 8 ids, one 1345-token prefill and
+    256 greedy tokens (the batch-1 decode workload).  serve_{q4,q6}_{i}: four
+    server-style requests, 5 ids (seed 100+i) + 1332 visual rows (seed i) +
+    11 ids (seed 200+i), 1024 greedy tokens each, caches growing to 2372 rows."""
+    out = [("image_q4_1345", Q4, image_prompt(0, 5, 1, 8), 0, 256, (0, 5, 1, 8))]
+    for qtype in (Q4, Q6):
+        for i in range(4):
+            out.append((f"serve_{QN[qtype]}_{i}", qtype, image_prompt(100 + i, 5, 200 + i, 11), i, 1024,
+                        (100 + i, 5, 200 + i, 11)))
+    # a request whose greedy choice at token 315 is a near tie (top-2 logits
+    # 4.8e-5 apart): 5 ids (seed 314) + 1332 visual rows (seed 314) + 11 ids
+    # (seed 414), through token 315
+    out.append(("near_tie_q4_314", Q4, image_prompt(314, 5, 414, 11), 314, 316, (314, 5, 414, 11)))
+    return out
+
+
+def stream_with_gaps(m, weights, ids, img, max_new):
+    """The oracle's greedy generation (generate_impl's loop: one step per
+    prompt token, then one per new token at position len(out)-1+ropeDelta),
+    keeping each chosen token's top-2 logit gap."""
+    pos, delta = oracle.mm_positions(ids, IMAGE_TOKEN, IMAGE_GRID)
+    s = m.seq(len(ids) + max_new)
+    j = 0
+    for p, t in enumerate(ids):
+        if t == IMAGE_TOKEN:
+            emb = img[j]
+            j += 1
+        else:
+            emb = weights["embed"][t]
+        last = p == len(ids) - 1
+        tok, lg, _ = s.step(emb, pos[p], need_logits=last, want_logits=last)
+    assert j == img.shape[0]
+    toks, gaps = [], []
+    while True:
+        top2 = np.partition(lg, -2)[-2:]
+        assert int(np.argmax(lg)) == tok
+        toks.append(int(tok))
+        gaps.append(float(top2.max() - top2.min()))
+        if len(toks) == max_new:
+            break
+        p = len(ids) + len(toks) - 1 + delta
+        tok, lg, _ = s.step(weights["embed"][tok], (p, p, p))
+    return toks, gaps, len(ids) + delta
+
+
+def main_full():
+    from rapidocrvl_amd.config import ERNIE_0P3B as cfg
+
+    oracle.set_threads(min(16, os.cpu_count() or 1))
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "oracle_streams_full.json")
+    cases = {}
+    if os.path.exists(path) and "--redo" not in sys.argv[1:]:  # keep the cases already written
+        with open(path) as f:
+            cases = json.load(f)["cases"]
+    weights = {}
+    for name, qtype, ids, img_seed, max_new, prompt in full_cases():
+        if name in cases:
+            continue
+        if qtype not in weights:
+            weights = {qtype: synth.make_weights(cfg, qtype, seed=0)}
+            m = oracle.Model(cfg)
+            m.load_weights(weights[qtype])
+        img = synth.image_embeds(1332, cfg.hidden, seed=img_seed)
+        toks, gaps, first_pos = stream_with_gaps(m, weights[qtype], ids, img, max_new)
+        if name == "image_q4_1345":  # the step loop is the oracle's own generation loop
+            assert list(m.generate(ids, 4, eos=(), image_embeds=img, image_token_id=IMAGE_TOKEN,
+                                   grid=IMAGE_GRID)) == toks[:4]
+        near = [[k, g] for k, g in enumerate(gaps) if g < 1e-3]
+        cases[name] = {"qtype": qtype, "weight_seed": 0, "prompt": {"head_seed": prompt[0], "n_head": prompt[1],
+                                                                     "tail_seed": prompt[2], "n_tail": prompt[3]},
+                       "image_rows": 1332, "image_seed": img_seed, "image_token_id": IMAGE_TOKEN,
+                       "grid": list(IMAGE_GRID), "prompt_len": int(ids.size), "first_pos": int(first_pos),
+                       "max_new": max_new, "tokens": toks, "min_top2_gap": min(gaps),
+                       "near_ties": near}
+        print(name, "min gap %.3g" % min(gaps), "near", near, toks[:12], flush=True)
+        write_full(path, cfg, cases)
+
+
+def write_full(path, cfg, cases):
+    out = {"_about": "Greedy streams of the oracle for the ERNIE 0.3B decoder (seeded synthetic weights) on "
+                     "image-conditioned prompts at full size, with each token's top-2 logit gap below 1e-3; "
+                     "written by make_golden.py --full.",
+           "config": dataclasses.asdict(cfg), "cases": cases}
+    with open(path, "w") as f:
+        json.dump(out, f, indent=1)
+    print("wrote", path, flush=True)
+
+
 def main():
+    if "--full" in sys.argv[1:]:
+        main_full()
+        return
     oracle.set_threads(min(16, os.cpu_count() or 1))
     cases = {}
     cache = {}
