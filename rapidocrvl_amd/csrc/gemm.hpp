@@ -114,8 +114,7 @@ static __global__ void __launch_bounds__(kThreads) k_digitize(DigitizeParams p) 
 #pragma unroll
     for (int k = 1; k < kWaves; ++k) m = fmaxf(m, red[k]);
     int ex = 0;
-    (void)frexpf(m * (1.0f / 127.0f), &ex);  // m/127 < 2^ex
-    const float inv = m > 0.0f ? ldexpf(1.0f, -ex) : 1.0f;
+    (void)frexpf(m * (1.0f / 127.0f), &ex);  // m/127 < 2^ex; m = 0 → ex = 0
     const float S = m > 0.0f ? ldexpf(1.0f, ex) : 1.0f;
     int sd[3] = {0, 0, 0};
 #pragma unroll
@@ -124,7 +123,7 @@ static __global__ void __launch_bounds__(kThreads) k_digitize(DigitizeParams p) 
         int sg[3] = {0, 0, 0};
 #pragma unroll
         for (int c = 0; c < 16; ++c) {
-            const float tt = y[g][c] * inv;  // exact: inv is a power of two
+            const float tt = ldexpf(y[g][c], -ex);  // exact (no overflow of 2^-ex for tiny rows)
             const float a = rintf(tt);
             const float t1 = (tt - a) * 128.0f;
             const float b = rintf(t1);

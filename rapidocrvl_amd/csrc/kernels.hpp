@@ -275,34 +275,8 @@ struct XDigits {
     float scale_comb[CPL];
 };
 
-// Q4 nibble planes (NPL = kNibPlanes, the greedy LM head): the activation of
-// a 32-column chunk as six balanced base-15 digit planes
-//   x = S·(e0 + e1/15 + … + e5/15⁵) + e,   e_k ∈ [−7, 7],
-// S a power of two > max|x|/7 over the chunk, |e| ≤ S/(2·15⁵) (≤ 2^-22.3 of
-// the chunk maximum, as fine as the three byte planes of the layer GEMVs).
-// A plane packs 8 columns per dword as signed nibbles in column order — the
-// order of the Q4 codes in a weight dword — and a code nibble u = code + 8
-// becomes the signed nibble code by u ^ 8, so a row dot is one XOR and six
-// v_dot8_i32_i4 per weight dword, combined in integer.
-constexpr int kNibPlanes = 6;
-constexpr float kNibComb = 759375.0f;  // 15⁵
-// The single-vector greedy head scores every row with the first kNibFast
-// planes and rescores only the rows that can still be the group's best with
-// all kNibPlanes (gemv_body): x̃₆ − x̃₄ = S·(e4/15⁴ + e5/15⁵), at most
-// 7·(15⁻⁴ + 15⁻⁵)·S per column.
-constexpr int kNibFast = 4;
-constexpr float kNibTail = 7.0f / 50625.0f + 7.0f / 759375.0f;
-template <int NPL>
-constexpr bool is_nib() { return NPL >= 4; }
-template <int CPL>
-struct XNib {
-    int n[CPL][4][kNibPlanes];  // [chunk][dword k: columns 8k..8k+7][plane]
-    float scale_comb[CPL];      // S / 15⁵
-    float scale_fast[CPL];      // S / 15³
-    float S[CPL];
-};
 template <int QT, int CPL, int NPL>
-using XDig = typename std::conditional<is_nib<NPL>(), XNib<CPL>, XDigits<QT, CPL>>::type;
+using XDig = XDigits<QT, CPL>;
 
 // column (within a chunk) of byte m of digit dword k: Q4 dword 2k' holds the
 // low nibbles of chunk dword k' (cols 8k'+0,2,4,6), dword 2k'+1 the high ones
@@ -347,30 +321,6 @@ __device__ __forceinline__ int spread6(uint32_t g) {
     return (int)r;
 }
 
-// the first NP nibble planes (NP = kNibPlanes: all of them)
-template <int CPL, int NP = kNibPlanes>
-__device__ __forceinline__ float row_dot_nib(const Chunk (&w)[CPL], const XNib<CPL> &xd) {
-    float r = 0.0f;
-#pragma unroll
-    for (int j = 0; j < CPL; ++j) {
-        int a[NP] = {};
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const int sw = (int)(w[j].d[k] ^ 0x88888888u);  // signed codes, column order
-#pragma unroll
-            for (int pl = 0; pl < NP; ++pl) a[pl] = __builtin_amdgcn_sdot8(sw, xd.n[j][k][pl], a[pl], false);
-        }
-        // |a_k| ≤ 32·8·7 = 1792 and Σ 15^k (k < 6) = 813616: the base-15
-        // combination stays inside int32 (|comb| < 1.46e9; four planes < 2^24,
-        // exact in f32)
-        int comb = a[0];
-#pragma unroll
-        for (int pl = 1; pl < NP; ++pl) comb = comb * 15 + a[pl];
-        r = fmaf(NP == kNibPlanes ? xd.scale_comb[j] : xd.scale_fast[j], (float)comb, r);
-    }
-    return r;
-}
-
 template <int QT, int CPL, int NPL = 3>
 __device__ __forceinline__ float row_dot_bytes(const Chunk (&w)[CPL], const XDigits<QT, CPL> &xd) {
     float r = 0.0f;
@@ -410,12 +360,7 @@ __device__ __forceinline__ float row_dot_bytes(const Chunk (&w)[CPL], const XDig
 
 template <int QT, int CPL, int NPL = 3>
 __device__ __forceinline__ float row_dot(const Chunk (&w)[CPL], const XDig<QT, CPL, NPL> &xd) {
-    if constexpr (is_nib<NPL>()) {
-        static_assert(QT == QT_Q4, "nibble planes pair with Q4 codes");
-        return row_dot_nib<CPL>(w, xd);
-    } else {
-        return row_dot_bytes<QT, CPL, NPL>(w, xd);
-    }
+    return row_dot_bytes<QT, CPL, NPL>(w, xd);
 }
 
 // Cross-lane exchanges used by the reduce-scatter.  Each pairs every lane with
@@ -567,12 +512,11 @@ __device__ __forceinline__ void x_digits(const XRegs &r, const XRegs &rw, bool n
         m = fmaxf(m, xchg<XQ1>(m));
         if constexpr (TPC == 4) m = fmaxf(m, xchg<XQ2>(m));
         int ex = 0;
-        (void)frexpf(m * (1.0f / 127.0f), &ex);  // m/127 < 2^ex
-        const float inv = m > 0.0f ? ldexpf(1.0f, -ex) : 1.0f;
+        (void)frexpf(m * (1.0f / 127.0f), &ex);  // m/127 < 2^ex; m = 0 → ex = 0
         int d0[8], d1[8], d2[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const float t = y[i] * inv;  // exact: inv is a power of two
+            const float t = ldexpf(y[i], -ex);  // exact (no overflow of 2^-ex for tiny chunks)
             const float a = rintf(t);
             const float t1 = (t - a) * 128.0f;
             const float b = rintf(t1);
@@ -628,84 +572,6 @@ __device__ __forceinline__ void x_digits(const XRegs &r, const XRegs &rw, bool n
     }
 }
 
-// Nibble-plane prologue (Q4 greedy head): thread t owns 4 consecutive
-// columns per pass (1024 columns a pass), so all 256 threads share the digit
-// work; the 8 threads of a 32-column chunk are adjacent lanes, and lanes 2m,
-// 2m+1 each build half of the chunk's nibble dword m of every plane.
-constexpr int kNibPass = 4 * kThreads;
-__device__ __forceinline__ void x_load_nib(const float *x, const float *nw, bool norm, int cols, XRegs &r) {
-#pragma unroll
-    for (int pp = 0; pp < kMaxCols / kNibPass; ++pp) {
-        if (pp * kNibPass >= cols) break;  // uniform
-        const int cb = min((pp * kThreads + (int)threadIdx.x) * 4, cols - 4);
-        r.x[pp >> 1][pp & 1] = *reinterpret_cast<const float4 *>(x + cb);
-        if (norm) r.w[pp >> 1][pp & 1] = *reinterpret_cast<const float4 *>(nw + cb);
-    }
-}
-
-__device__ __forceinline__ int xchg_i(int v) { return __float_as_int(xchg<XQ1>(__int_as_float(v))); }
-
-__device__ __forceinline__ void x_digits_nib(const XRegs &r, const XRegs &rw, bool norm, int cols, int *lds,
-                                             float *red) {
-    constexpr int NDW = DigitRec<QT_Q4>::NDW, RS = DigitRec<QT_Q4>::RS;
-    const int lane = threadIdx.x & 63;
-    float ss = 0.0f;
-#pragma unroll
-    for (int pp = 0; pp < kMaxCols / kNibPass; ++pp) {
-        if (pp * kNibPass >= cols) break;  // uniform
-        const int G = pp * kThreads + (int)threadIdx.x;  // 4-column group
-        const bool valid = G * 4 < cols;
-        const float4 xv = r.x[pp >> 1][pp & 1];
-        float y[4] = {xv.x, xv.y, xv.z, xv.w};
-        if (norm) {
-            const float4 wv = rw.w[pp >> 1][pp & 1];
-            const float w[4] = {wv.x, wv.y, wv.z, wv.w};
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                ss = valid ? fmaf(y[i], y[i], ss) : ss;
-                y[i] = y[i] * w[i];  // a lone product: nothing to contract
-            }
-        }
-        float m = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) m = fmaxf(m, fabsf(y[i]));
-        m = fmaxf(m, xchg<XQ1>(m));
-        m = fmaxf(m, xchg<XQ2>(m));
-        m = fmaxf(m, xchg<XM8>(m));  // the chunk's 8 lanes
-        int ex = 0;
-        (void)frexpf(m * (1.0f / 7.0f), &ex);  // |x|·2^-ex < 7 (+ rounding)
-        const float inv = m > 0.0f ? ldexpf(1.0f, -ex) : 1.0f;
-        const int sh = 16 * (G & 1);  // this lane's half of the dword
-        int pk[kNibPlanes] = {};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            float t = y[i] * inv;  // exact: inv is a power of two
-#pragma unroll
-            for (int k = 0; k < kNibPlanes; ++k) {
-                // |t| ≤ 7.5 → e ∈ [−7, 7] and |t − e| ≤ 1/2
-                const float e = __builtin_amdgcn_fmed3f(rintf(t), -7.0f, 7.0f);
-                pk[k] |= ((int)e & 15) << (4 * i + sh);
-                t = fmaf(t, 15.0f, -15.0f * e);  // (t − e)·15, one rounding
-            }
-        }
-#pragma unroll
-        for (int k = 0; k < kNibPlanes; ++k) pk[k] |= xchg_i(pk[k]);
-        if (valid && (G & 1) == 0) {
-            // dword q of the chunk: its six planes at record ints 6q..6q+5
-            const int c = G / 8, q = (G & 7) >> 1;
-            int2 *rec = reinterpret_cast<int2 *>(lds + c * RS + kNibPlanes * q);
-            rec[0] = make_int2(pk[0], pk[1]);
-            rec[1] = make_int2(pk[2], pk[3]);
-            rec[2] = make_int2(pk[4], pk[5]);
-            if (q == 0) lds[c * RS + NDW * 3 + 3] = __float_as_int(m > 0.0f ? ldexpf(1.0f, ex) : 1.0f);
-        }
-    }
-    if (norm) {
-        ss = wave_sum(ss);
-        if (lane == 0) red[threadIdx.x >> 6] = ss;
-    }
-}
-
 // RMSNorm (ops.go:1015-1037): x·fastRsqrt(Σx²/n + eps)·w — the factor from
 // the waves' Σx² (after the barrier that follows x_digits)
 __device__ __forceinline__ float x_norm_factor(bool norm, int cols, float eps, const float *red) {
@@ -720,31 +586,6 @@ __device__ __forceinline__ float x_norm_factor(bool norm, int cols, float eps, c
 template <int QT, int LPR, int CPL, int NPL = 3>
 __device__ __forceinline__ void load_digits(const int *lds, int l, XDig<QT, CPL, NPL> &xd) {
     constexpr int NDW = DigitRec<QT>::NDW, RS = DigitRec<QT>::RS;
-    if constexpr (is_nib<NPL>()) {
-        static_assert(4 * kNibPlanes <= NDW * 3 + 3, "nibble planes overlap the chunk scale");
-#pragma unroll
-        for (int j = 0; j < CPL; ++j) {
-            const int4 *rec = reinterpret_cast<const int4 *>(lds + (l + j * LPR) * RS);
-            int v[4 * kNibPlanes];
-#pragma unroll
-            for (int i = 0; i < kNibPlanes; ++i) {
-                const int4 t = rec[i];
-                v[4 * i] = t.x;
-                v[4 * i + 1] = t.y;
-                v[4 * i + 2] = t.z;
-                v[4 * i + 3] = t.w;
-            }
-#pragma unroll
-            for (int k = 0; k < 4; ++k)
-#pragma unroll
-                for (int pl = 0; pl < kNibPlanes; ++pl) xd.n[j][k][pl] = v[kNibPlanes * k + pl];
-            const float S = __int_as_float(lds[(l + j * LPR) * RS + NDW * 3 + 3]);
-            xd.scale_comb[j] = S * (1.0f / kNibComb);
-            xd.scale_fast[j] = S * (1.0f / 3375.0f);
-            xd.S[j] = S;
-        }
-        return;
-    } else {
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
         const int4 *rec = reinterpret_cast<const int4 *>(lds + (l + j * LPR) * RS);
@@ -772,7 +613,6 @@ __device__ __forceinline__ void load_digits(const int *lds, int l, XDig<QT, CPL,
             xd.bias_comb[j] = xd.bias[j][0] * 128 + xd.bias[j][1];
             xd.scale_comb[j] = xd.scale[j] * (1.0f / 128.0f);
         }
-    }
     }
 }
 
@@ -1023,10 +863,8 @@ __device__ __forceinline__ void load_group(const SegSel &sel, int row_bytes, int
 // TAG only separates instances for profiling (TAG=1: the timing entry point).
 // ONE: the grid gives every wave at most one group (no row loop, no prefetch
 // registers), for the large single-matrix launch.
-// NPL: digit planes of the activation (3 byte planes; kNibPlanes nibble
-// planes for the Q4 greedy head).  Both read x to about 2^-22 of each chunk's
-// maximum, so a greedy choice departs from the exact one only where the top
-// two scores lie within that resolution.
+// NPL: byte digit planes of the activation (3: x to 2^-22 of each chunk's
+// maximum; the greedy heads of the shapes head.hpp does not take use 3 too).
 // NV: activation vectors sharing each weight pass (batched decode, M = NV):
 // every chunk is dotted against each vector's digits (read from LDS per
 // group), and the reduce-scatter runs over U·NV entries e = u·NV + v.
@@ -1074,8 +912,7 @@ __device__ __forceinline__ void gemv_body(GemvParams p, int pro, int epi, const 
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
         const float *xv = p.x + (NV > 1 ? v * q.x_stride : 0);
-        if constexpr (is_nib<NPL>()) x_load_nib(xv, p.norm_w, norm && v == 0, cols, xr[v]);
-        else x_load(xv, p.norm_w, norm && v == 0, cols, xr[v]);
+        x_load(xv, p.norm_w, norm && v == 0, cols, xr[v]);
     }
     // first group: weights, then the writer lane's epilogue operands (row
     // scale, residual), all requested before the prologue's first wait
@@ -1094,8 +931,7 @@ __device__ __forceinline__ void gemv_body(GemvParams p, int pro, int epi, const 
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
         // the norm weight was loaded once, with vector 0
-        if constexpr (is_nib<NPL>()) x_digits_nib(xr[v], xr[0], norm, cols, lds + v * recs, red + v * kWaves);
-        else x_digits<QT>(xr[v], xr[0], norm, cols, lds + v * recs, red + v * kWaves);
+        x_digits<QT>(xr[v], xr[0], norm, cols, lds + v * recs, red + v * kWaves);
     }
     __syncthreads();
     float xscale = x_norm_factor(norm, cols, p.eps, red);
@@ -1109,57 +945,11 @@ __device__ __forceinline__ void gemv_body(GemvParams p, int pro, int epi, const 
     const bool in_place = epi == EPI_OPROJ ? oproj_in_place(p, st_of(p, q, my_v)) : false;
     float best_v = -INFINITY;
     int best_r = 0x7FFFFFFF;
-    // Two-pass greedy head (Q4 nibble planes, one vector): a row's score from
-    // kNibFast planes differs from its score from all kNibPlanes by at most
-    //   β = xscale·scale·Σ_c S_c·(256·kNibTail + 2·12·2⁻²⁴·1920)
-    // (|code| ≤ 8 on 32 columns per chunk; the second term covers the f32
-    // steps of both scores, |x̃/S| ≤ 7.5).  Within a row group, every row whose
-    // all-plane score is the group's best has s_fast + β ≥ max(s_fast − β), so
-    // rescoring only those rows with all planes finds that best exactly.
-    constexpr bool kTwoPass = is_nib<NPL>() && NV == 1 && NMAT == 1;
-    float kwin = 0.0f;
-    if constexpr (kTwoPass) {
-        float ks[1][1] = {{0.0f}};
-#pragma unroll
-        for (int j = 0; j < CPL; ++j) ks[0][0] += xd.S[j];
-        reduce_scatter<LPR, 1, 1>(ks, lane);  // Σ_c S_c over the row's chunks, in every lane
-        kwin = ks[0][0] * (256.0f * kNibTail + 2.0f * 12.0f * 1920.0f / 16777216.0f) * 1.0001f;
-    }
 
     // one group: row sums, reduce-scatter, epilogue by the writer lanes
     auto compute = [&](int gg, const Chunk (&wc)[U][NMAT][CPL], const float (&sc)[NMAT], float rs) {
         const int r = (gg * U + my_u) * RPW + sub;
         float acc[E > 8 ? E : 8][NMAT];
-        if constexpr (kTwoPass) {
-#pragma unroll
-            for (int u = 0; u < U; ++u) acc[u][0] = row_dot_nib<CPL, kNibFast>(wc[u][0], xd);
-            reduce_scatter<LPR, E, 1>(acc, lane);
-            const bool valid = writer && r < rows;
-            const float f = xscale * sc[0];
-            const float s_fast = acc[0][0] * f;
-            const float beta = f * kwin;
-            const uint32_t lo = wave_max_u32(valid ? ordered_bits(s_fast - beta) : 0u);
-            // with logits requested every row is rescored (they are written)
-            const bool cand = valid && (p.out != nullptr || ordered_bits(s_fast + beta) >= lo);
-            const unsigned long long cm = __ballot(cand);
-            float s_all = 0.0f;
-#pragma unroll
-            for (int u = 0; u < U; ++u) {
-                unsigned long long bits = 0ull;
-#pragma unroll
-                for (int sb = 0; sb < RPW; ++sb) bits |= 1ull << (sb * LPR + u * SPAN);
-                if (cm & bits) {  // wave-uniform
-                    float a6[1][1] = {{row_dot_nib<CPL, kNibPlanes>(wc[u][0], xd)}};
-                    reduce_scatter<LPR, 1, 1>(a6, lane);
-                    if (my_u == u) s_all = a6[0][0] * f;
-                }
-            }
-            if (cand) {
-                const float sv[1] = {s_all};
-                gemv_epilogue(p, epi, r, my_o + r, sv, rs, in_place, best_v, best_r);
-            }
-            return;
-        }
         if constexpr (NV == 1) {
 #pragma unroll
             for (int u = 0; u < U; ++u)

@@ -8,6 +8,7 @@
 #include <cmath>
 
 #include "gemm.hpp"
+#include "head.hpp"
 #include "internal.hpp"
 
 namespace pocr {
@@ -253,21 +254,14 @@ static bool gemv_fast_kernel(int lpr, int cpl, const void **fn) {
 #define POCR_BIG_GRID 4096  // enough for one group per wave up to 262144 rows
 #endif
 constexpr int kBigU = POCR_BIG_U;
-// digit planes of the greedy LM head: Q4 → the nibble planes (v_dot8),
-// Q8 / Q6 → three byte planes, like every other launch
+// one: every wave gets at most one row group (the big launch covers them all)
 template <int QT>
-constexpr int big_planes() { return QT == QT_Q4 ? kNibPlanes : 3; }
-
-// one: every wave gets at most one row group (the big launch covers them all);
-// argmax: the greedy LM head, whose scores only feed the argmax, takes
-// big_planes<QT>() digit planes, every other launch three byte planes
-template <int QT, int NPL>
 static bool pick_big(int tag, bool one, int lpr, int cpl, const void **fn) {
     if (one)
-        return tag == 1 ? gemv_fast_kernel<QT, 1, kBigU, 1, true, NPL>(lpr, cpl, fn)
-                        : gemv_fast_kernel<QT, 1, kBigU, 0, true, NPL>(lpr, cpl, fn);
-    return tag == 1 ? gemv_fast_kernel<QT, 1, kBigU, 1, false, NPL>(lpr, cpl, fn)
-                    : gemv_fast_kernel<QT, 1, kBigU, 0, false, NPL>(lpr, cpl, fn);
+        return tag == 1 ? gemv_fast_kernel<QT, 1, kBigU, 1, true>(lpr, cpl, fn)
+                        : gemv_fast_kernel<QT, 1, kBigU, 0, true>(lpr, cpl, fn);
+    return tag == 1 ? gemv_fast_kernel<QT, 1, kBigU, 1, false>(lpr, cpl, fn)
+                    : gemv_fast_kernel<QT, 1, kBigU, 0, false>(lpr, cpl, fn);
 }
 
 // NV activation vectors per weight pass (batched decode): the big launch keeps
@@ -275,21 +269,18 @@ static bool pick_big(int tag, bool one, int lpr, int cpl, const void **fn) {
 // count and its activation prologues as for one vector) and gives every wave
 // one group
 template <int QT, int NV>
-static bool pick_nv(int nmat, bool big, int lpr, int cpl, bool argmax, const void **fn) {
+static bool pick_nv(int nmat, bool big, int lpr, int cpl, const void **fn) {
     if (nmat == 2) return gemv_fast_kernel<QT, 2, 2, 0, false, 3, NV>(lpr, cpl, fn);
-    if (big)
-        return argmax ? gemv_fast_kernel<QT, 1, kBigU, 0, true, big_planes<QT>(), NV>(lpr, cpl, fn)
-                      : gemv_fast_kernel<QT, 1, kBigU, 0, true, 3, NV>(lpr, cpl, fn);
+    if (big) return gemv_fast_kernel<QT, 1, kBigU, 0, true, 3, NV>(lpr, cpl, fn);
     return gemv_fast_kernel<QT, 1, 2, 0, false, 3, NV>(lpr, cpl, fn);
 }
 
 template <int QT>
-static bool pick_fast(int nmat, int u, int tag, int lpr, int cpl, bool one, bool argmax, int nv, const void **fn) {
-    if (nv == 2) return pick_nv<QT, 2>(nmat, u != 2, lpr, cpl, argmax, fn);
-    if (nv == 4) return pick_nv<QT, 4>(nmat, u != 2, lpr, cpl, argmax, fn);
+static bool pick_fast(int nmat, int u, int tag, int lpr, int cpl, bool one, int nv, const void **fn) {
+    if (nv == 2) return pick_nv<QT, 2>(nmat, u != 2, lpr, cpl, fn);
+    if (nv == 4) return pick_nv<QT, 4>(nmat, u != 2, lpr, cpl, fn);
     if (nmat == 2) return gemv_fast_kernel<QT, 2, 2>(lpr, cpl, fn);
-    if (u == kBigU)
-        return argmax ? pick_big<QT, big_planes<QT>()>(tag, one, lpr, cpl, fn) : pick_big<QT, 3>(tag, one, lpr, cpl, fn);
+    if (u == kBigU) return pick_big<QT>(tag, one, lpr, cpl, fn);
     return tag == 1 ? gemv_fast_kernel<QT, 1, 2, 1>(lpr, cpl, fn) : gemv_fast_kernel<QT, 1, 2>(lpr, cpl, fn);
 }
 
@@ -345,10 +336,9 @@ static int plan_gemv(int qtype, int nmat, int rows, int cols, const DevMat *mats
         const int want = (groups + kWaves - 1) / kWaves;
         grid = std::max(1, std::min(want, max_grid));
         one = big && grid == want;
-        const bool am = epi == EPI_ARGMAX;
-        if (qtype == POCR_Q4) ok = pick_fast<QT_Q4>(nmat, big ? kBigU : 2, tag, lpr, cpl, one, am, nv, &plan->fn);
-        if (qtype == POCR_Q8) ok = pick_fast<QT_Q8>(nmat, big ? kBigU : 2, tag, lpr, cpl, one, am, nv, &plan->fn);
-        if (qtype == POCR_Q6) ok = pick_fast<QT_Q6>(nmat, big ? kBigU : 2, tag, lpr, cpl, one, am, nv, &plan->fn);
+        if (qtype == POCR_Q4) ok = pick_fast<QT_Q4>(nmat, big ? kBigU : 2, tag, lpr, cpl, one, nv, &plan->fn);
+        if (qtype == POCR_Q8) ok = pick_fast<QT_Q8>(nmat, big ? kBigU : 2, tag, lpr, cpl, one, nv, &plan->fn);
+        if (qtype == POCR_Q6) ok = pick_fast<QT_Q6>(nmat, big ? kBigU : 2, tag, lpr, cpl, one, nv, &plan->fn);
     }
     if (ok) {
         plan->lds = (size_t)nv * (qtype == POCR_Q4 ? gemv_lds_bytes<QT_Q4>(cols)
@@ -382,8 +372,52 @@ GemvParams pocr::gemv_params_1(const pocr_weight *w) {
     return p;
 }
 
+// The greedy head on the matrix cores (head.hpp) for the shapes it takes:
+// one Q4 or Q8 matrix of 1024 or 2048 columns whose rows are 16-byte aligned,
+// 1, 2 or 4 vectors.
+template <int QT>
+static const void *head_fn(int ns, int nv) {
+#define POCR_H(NS, NV) \
+    if (ns == NS && nv == NV) return reinterpret_cast<const void *>(&k_head_mfma<QT, NS, NV>);
+    POCR_H(4, 1) POCR_H(4, 2) POCR_H(4, 4) POCR_H(8, 1) POCR_H(8, 2) POCR_H(8, 4)
+#undef POCR_H
+    return nullptr;
+}
+
+static const void *plan_head(const GemvParams &p, int nmat, int nv) {
+    const DevMat &m = p.m[0];
+    if (nmat != 1 || p.seg_end[0] != p.rows || m.cols != p.cols) return nullptr;
+    if (p.cols != 1024 && p.cols != 2048) return nullptr;
+    if (((uintptr_t)m.data) % 16 != 0 || m.row_bytes % 16 != 0) return nullptr;
+    const int ns = p.cols / 256;
+    if (m.qtype == POCR_Q4) return head_fn<QT_Q4>(ns, nv);
+    if (m.qtype == POCR_Q8) return head_fn<QT_Q8>(ns, nv);
+    return nullptr;  // Q6: 12-byte code groups do not fall on 128-byte lines (GEMV head)
+}
+
+static int launch_head(hipStream_t s, const void *fn, const GemvParams &p, int pro, int nv, const GemvNV *q) {
+    HeadParams h{};
+    h.m = p.m[0];
+    h.rows = p.rows;
+    h.x = p.x;
+    h.x_stride = nv > 1 ? q->x_stride : 0;
+    h.norm_w = pro == PRO_RMSNORM ? p.norm_w : nullptr;
+    h.eps = p.eps;
+    h.out = p.out;
+    h.out_stride = nv > 1 ? q->o_stride : 0;
+    for (int v = 0; v < kHeadMaxVec; ++v) h.st[v] = v == 0 ? p.st : (v < nv ? q->stv[v - 1] : p.st);
+    const int blocks = (p.rows + 15) / 16;
+    void *args[] = {&h};
+    HIP_TRY(hipLaunchKernel(fn, dim3((blocks + kHeadRB - 1) / kHeadRB), dim3(kThreads), args, 0, s));
+    return POCR_OK;
+}
+
 int pocr::gemv_launch(hipStream_t s, GemvParams p, int nmat, int pro, int epi, int max_grid, int nv,
                       const GemvNV *q) {
+    if (nv > 1 && !q) return fail(POCR_ERR_ARG, "gemv: %d vectors need their strides", nv);
+    if (epi == EPI_ARGMAX && p.st) {
+        if (const void *fn = plan_head(p, nmat, nv)) return launch_head(s, fn, p, pro, nv, q);
+    }
     GemvPlan plan;
     const int nm = nmat == 2 ? 2 : (p.seg_end[0] == p.rows ? 1 : (p.seg_end[1] == p.rows ? 2 : 3));
     int rc = plan_gemv(p.m[0].qtype, nmat, p.rows, p.cols, p.m, nm, max_grid, &plan, 0, p.seg_end, epi, nv);
@@ -1233,12 +1267,18 @@ static int time_matvec_impl(pocr_ctx *ctx, const pocr_weight *const *weights, in
         p.st = ctx->state.as<StepState>();  // argmax slots (the key only grows: no reset needed)
         return p;
     };
+    // the greedy head times the kernel the decode runs: the MFMA head where
+    // the shape allows it
+    const void *hfn = argmax ? plan_head(params(0), 1, 1) : nullptr;
+    auto launch = [&](int i) {
+        return hfn ? launch_head(s, hfn, params(i), PRO_COPY, 1, nullptr) : launch_gemv(s, plan, params(i), PRO_COPY, epi);
+    };
     hipEvent_t e0, e1;
     HIP_TRY(hipEventCreate(&e0));
     HIP_TRY(hipEventCreate(&e1));
-    for (int i = 0; i < n_weights; ++i) RC(launch_gemv(s, plan, params(i), PRO_COPY, epi));  // warm-up pass
+    for (int i = 0; i < n_weights; ++i) RC(launch(i));  // warm-up pass
     HIP_TRY(hipEventRecord(e0, s));
-    for (int it = 0; it < iters; ++it) RC(launch_gemv(s, plan, params(it % n_weights), PRO_COPY, epi));
+    for (int it = 0; it < iters; ++it) RC(launch(it % n_weights));
     HIP_TRY(hipEventRecord(e1, s));
     HIP_TRY(hipEventSynchronize(e1));
     float ms = 0.0f;

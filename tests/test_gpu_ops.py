@@ -84,26 +84,36 @@ def test_matvec_vectors_per_pass(ctx, orc, rng, qtype, shape):
             _close(got[i], orc.matvec(qtype, q.scales, q.packed, x[i]))
 
 
-F32_STEPS = 10 * 2.0 ** -24  # convert, chunk fma, ≤ 6 lane-reduction adds, row scale (+1 spare)
+# f32 steps after the exact integer plane sums: the MFMA head (Q4, Q8)
+# combines three planes (2 fma) and applies two scales; the byte-plane GEMV
+# head (Q6) adds a chunk fma and ≤ 6 lane-reduction adds (+2 spare each)
+F32_STEPS = {Q4: 6 * 2.0 ** -24, Q8: 6 * 2.0 ** -24, Q6: 14 * 2.0 ** -24}
+
+
+def head_model(qtype, codes, scales, x):
+    """What the device greedy head computes, exactly, and its f32 magnitude."""
+    if qtype == Q6:
+        return dm.gemv_scores(qtype, codes, scales, x)
+    return dm.head_scores(codes, scales, x)
 
 
 @pytest.mark.parametrize("qtype", [Q8, Q4, Q6], ids=["q8", "q4", "q6"])
 def test_matvec_argmax(ctx, orc, rng, qtype):
-    """The greedy head computes codes · digitize(x) (nibble planes for Q4,
-    byte planes for Q8/Q6, restated in tests/digit_model.py) up to its f32
-    steps; its choice is the exact argmax unless the exact top scores lie
-    within the digitization's actual deviation plus those f32 steps."""
+    """The greedy head computes codes · digits of x (three byte planes: one
+    power-of-two scale for the vector in the MFMA head, one per 16 columns in
+    the Q6 GEMV head; restated in tests/digit_model.py) up to its f32 steps;
+    its choice is the exact argmax unless the exact top scores lie within the
+    digits' actual deviation plus those f32 steps."""
     q = _qmat(rng, 103424, 1024, qtype)
     w = ctx.upload(q)
     codes = lib.unpack_rows(qtype, q.packed, q.cols)
-    nib = qtype == Q4
     for seed in range(3):
         x = np.random.default_rng(seed).standard_normal(1024).astype(np.float32)
         exact, _ = dm.scores(qtype, codes, q.scales, x)
-        dig, mag = dm.scores(qtype, codes, q.scales, dm.digitize(qtype, x, nib))
-        f32b = F32_STEPS * mag
+        dig, mag = head_model(qtype, codes, q.scales, x)
+        f32b = F32_STEPS[qtype] * mag
         dev = np.abs(dig - exact)  # the digit planes' own deviation, per row
-        # about 2^-22 of each chunk's maximum: 1e-6 of the largest score
+        # about 2^-21 of the largest |x|: 1e-6 of the largest score
         assert dev.max() <= 1e-6 * np.abs(exact).max()
         idx, score = ctx.matvec_argmax(w, x)
         assert abs(score - dig[idx]) <= f32b[idx]
@@ -116,10 +126,10 @@ def test_matvec_argmax(ctx, orc, rng, qtype):
 @pytest.mark.parametrize("qtype", [Q8, Q4, Q6], ids=["q8", "q4", "q6"])
 def test_matvec_argmax_planted_near_tie(ctx, orc, qtype):
     """Rows 100 and 200 differ in one code, at a column whose activation is
-    2.2e-5 of its chunk's maximum: row 200 wins by ~3e-6, below what a head
+    2.2e-5 of the vector's maximum: row 200 wins by ~3e-6, below what a head
     reading x to 2^-14.5 (four nibble planes) or 2^-14 (two byte planes)
     resolves (it would see a tie and take row 100) and far above the head's
-    2^-22 resolution and the f32 rounding of these small scores."""
+    2^-21 resolution and the f32 rounding of these small scores."""
     rows, cols, j, i0 = 4096, 1024, 64, 65
     rng = np.random.default_rng(7)
     wf = (rng.standard_normal((rows, cols)) * 1e-4).astype(np.float32)
@@ -130,8 +140,7 @@ def test_matvec_argmax_planted_near_tie(ctx, orc, qtype):
     q = lib.QMatrix.quantize(wf, qtype)
     codes = lib.unpack_rows(qtype, q.packed, cols)
     assert q.scales[100] == q.scales[200] and codes[200, j] > 0 and codes[100, j] == 0
-    x = rng.standard_normal(cols).astype(np.float32)
-    x[64:96] = rng.uniform(-0.9, 0.9, 32).astype(np.float32)
+    x = rng.uniform(-0.9, 0.9, cols).astype(np.float32)
     x[i0] = 1.0
     x[j] = 2.2e-5
     exact, _ = dm.scores(qtype, codes, q.scales, x)
@@ -139,8 +148,8 @@ def test_matvec_argmax_planted_near_tie(ctx, orc, qtype):
     assert int(np.argmax(orc.matvec(qtype, q.scales, q.packed, x))) == 200
     idx, score = ctx.matvec_argmax(ctx.upload(q), x)
     assert idx == 200
-    dig, mag = dm.scores(qtype, codes[[200]], q.scales[[200]], dm.digitize(qtype, x, qtype == Q4))
-    assert abs(score - dig[0]) <= F32_STEPS * mag[0]
+    dig, mag = head_model(qtype, codes[[200]], q.scales[[200]], x)
+    assert abs(score - dig[0]) <= F32_STEPS[qtype] * mag[0]
 
 
 def test_argmax_ties_pick_lowest_index(ctx):
