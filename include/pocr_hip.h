@@ -164,6 +164,17 @@ int pocr_mrope_pair(pocr_ctx *ctx, float *q, float *k, const float *cos_t, const
  * q[heads*dim] over cache_len rows of kv_heads*dim fp32 K/V */
 int pocr_text_attention(pocr_ctx *ctx, const float *q, const float *k_cache, const float *v_cache,
                         int cache_len, int heads, int kv_heads, int head_dim, float *out);
+/* No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops).  The
+ * computation of pocr_text_attention over device buffers the caller owns
+ * (q_dev, the caches, out_dev), allocating nothing: its split records live in
+ * a fixed per-device array of 512 (kv head, split) records, so kv_heads x
+ * splits above 512 (2 kv heads: above 16384 cache rows) is POCR_ERR_ARG.
+ * Synchronous on the context's stream.  Calls that overlap on one GPU race
+ * on the array. */
+int pocr_text_attention_noalloc(pocr_ctx *ctx, const float *q_dev, const float *k_cache_dev,
+                                const float *v_cache_dev, int cache_len, int heads, int kv_heads, int head_dim,
+                                float *out_dev);
 
 /* Average device time (microseconds, HIP events on the context stream) of the
  * M=1 GEMV kernel over `iters` launches that rotate through n_weights copies of

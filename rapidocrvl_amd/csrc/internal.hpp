@@ -65,6 +65,7 @@ struct pocr_ctx {
     std::atomic<int> refs{1};
     int device = 0;
     hipStream_t stream = nullptr;
+    float *scratch = nullptr;  // this device's copy of the allocation-free entry's split records
     std::mutex mu;
     // op-level staging
     DevBuf x, out, out2, out3, res, vbuf, kc, vc, part, tabs, state;

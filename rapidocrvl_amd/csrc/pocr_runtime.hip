@@ -81,6 +81,32 @@ pocr_seq::~pocr_seq() {
 // ---------------------------------------------------------------------------
 // context
 // ---------------------------------------------------------------------------
+// Split records of pocr_text_attention_noalloc: a fixed device array (each
+// GPU holds its own copy until the process ends), so that entry allocates
+// nothing.  Host code never passes the array's name to a kernel: its device
+// address is taken once per device (scratch_setup) and kept in the context.
+constexpr int kNoAllocSplitRecs = 512;  // kv heads × splits
+constexpr size_t kNoAllocScratchFloats = (size_t)kNoAllocSplitRecs * kMaxGroup * kRec;
+static __device__ __align__(256) float scratch[kNoAllocScratchFloats];
+
+static std::mutex g_scratch_mu;
+static float *g_scratch[64];  // per device, set once
+
+// the current device's scratch address (the device must be current)
+static int scratch_setup(int device, float **out) {
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (device < 0 || device >= 64) return fail(POCR_ERR_UNSUPPORTED, "device %d: at most 64 devices", device);
+    if (!g_scratch[device]) {
+        void *ptr = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr)
+            return fail(POCR_ERR_DEVICE, "device %d: scratch address: %s", device, hipGetErrorString(e));
+        g_scratch[device] = static_cast<float *>(ptr);
+    }
+    *out = g_scratch[device];
+    return POCR_OK;
+}
+
 extern "C" int pocr_ctx_create(int device, pocr_ctx **out) {
     if (!out) return fail(POCR_ERR_ARG, "pocr_ctx_create: null out");
     *out = nullptr;
@@ -93,8 +119,11 @@ extern "C" int pocr_ctx_create(int device, pocr_ctx **out) {
     HIP_TRY(hipGetDeviceProperties(&prop, device));
     if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
         return fail(POCR_ERR_UNSUPPORTED, "device %d is %s; this library is built for gfx950", device, prop.gcnArchName);
+    float *scr = nullptr;
+    RC(scratch_setup(device, &scr));
     pocr_ctx *c = new pocr_ctx();
     c->device = device;
+    c->scratch = scr;
     if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
         delete c;
         return fail(POCR_ERR_DEVICE, "hipStreamCreate failed");
@@ -828,6 +857,56 @@ extern "C" int pocr_text_attention(pocr_ctx *ctx, const float *q, const float *k
     }
     HIP_TRY(hipGetLastError());
     RC(d2h(s, out, ctx->out.p, nq * 4));
+    return sync(s);
+}
+
+// The computation of pocr_text_attention over device buffers the caller owns,
+// allocating nothing: the split records go to this device's scratch array,
+// which limits kv_heads × splits to kNoAllocSplitRecs.  Calls that overlap on
+// one GPU race on the array (every call rewrites the records it reads; none
+// needs them zeroed).
+extern "C" int pocr_text_attention_noalloc(pocr_ctx *ctx, const float *q_dev, const float *k_cache_dev,
+                                           const float *v_cache_dev, int cache_len, int heads, int kv_heads,
+                                           int head_dim, float *out_dev) {
+    if (!ctx || !q_dev || !k_cache_dev || !v_cache_dev || !out_dev || cache_len <= 0 || heads <= 0 || kv_heads <= 0 ||
+        head_dim <= 0 || heads % kv_heads)
+        return fail(POCR_ERR_ARG, "pocr_text_attention_noalloc: bad arguments");
+    CHECK_INJECT("text_attention_noalloc");
+    CTX_GUARD(ctx);
+    if (!ctx->scratch) return fail(POCR_ERR_DEVICE, "pocr_text_attention_noalloc: no scratch array");
+    hipStream_t s = ctx->stream;
+    const float scale = (float)(1.0 / std::sqrt((double)head_dim));  // invSqrt, model.go:7391
+    const int group = heads / kv_heads;
+    if (head_dim == kHD && group <= kMaxGroup) {
+        const int rpw = attn_rpw(cache_len);
+        const int nsplit = attn_nsplit(cache_len, rpw);
+        if ((long long)kv_heads * nsplit > kNoAllocSplitRecs)
+            return fail(POCR_ERR_ARG,
+                        "pocr_text_attention_noalloc: %d kv heads x %d splits (%d cache rows) exceed the %d split "
+                        "records of the fixed scratch array",
+                        kv_heads, nsplit, cache_len, kNoAllocSplitRecs);
+        AttnParams p{};
+        p.q = q_dev;
+        p.kc = const_cast<float *>(k_cache_dev);  // read only: no append without a step state
+        p.vc = const_cast<float *>(v_cache_dev);
+        p.st = nullptr;
+        p.len = cache_len;
+        p.has_rope = 0;
+        p.part = ctx->scratch;
+        p.head_out = out_dev;
+        p.heads = heads;
+        p.kvh = kv_heads;
+        attn_shape(p, cache_len, rpw);
+        p.scale = scale;
+        launch_attn_decode(s, rpw, dim3(kv_heads, nsplit), p);
+        hipLaunchKernelGGL(k_attn_merge, dim3(heads), dim3(kMergeThreads), 0, s, p);
+    } else {
+        if ((size_t)cache_len * 4 > 60 * 1024)
+            return fail(POCR_ERR_UNSUPPORTED, "pocr_text_attention_noalloc: cache too long for this head shape");
+        hipLaunchKernelGGL(k_attn_small, dim3(heads), dim3(kThreads), (size_t)cache_len * 4, s, q_dev, k_cache_dev,
+                           v_cache_dev, cache_len, heads, kv_heads, head_dim, scale, out_dev);
+    }
+    HIP_TRY(hipGetLastError());
     return sync(s);
 }
 

@@ -70,6 +70,7 @@ _SIGS = {
     "pocr_rmsnorm": (_i, [_vp, _vp, _vp, _i, C.c_float, _vp]),
     "pocr_mrope_pair": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i]),
     "pocr_text_attention": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
+    "pocr_text_attention_noalloc": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
     "pocr_model_create": (_i, [_vp, C.POINTER(PocrConfig), C.POINTER(_vp)]),
     "pocr_model_destroy": (None, [_vp]),
     "pocr_model_set_weight": (_i, [_vp, _i, _i, _vp]),
@@ -424,6 +425,11 @@ class Context:
         check(load().pocr_text_attention(self.h, _ptr(q), _ptr(kc), _ptr(vc), cache_len, heads, kv_heads, head_dim,
                                          _ptr(out)))
         return out
+
+    def text_attention_noalloc(self, q_dev, k_dev, v_dev, cache_len, heads, kv_heads, head_dim, out_dev):
+        """pocr_text_attention_noalloc over device addresses (ints) the caller owns."""
+        check(load().pocr_text_attention_noalloc(self.h, C.c_void_p(q_dev), C.c_void_p(k_dev), C.c_void_p(v_dev),
+                                                 cache_len, heads, kv_heads, head_dim, C.c_void_p(out_dev)))
 
 
 class Model:
