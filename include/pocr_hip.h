@@ -160,10 +160,53 @@ int pocr_rmsnorm(pocr_ctx *ctx, const float *x, const float *w, int n, float eps
 /* VulkanMRoPEPairF32 (vulkan_exec_stub.go:42), in place */
 int pocr_mrope_pair(pocr_ctx *ctx, float *q, float *k, const float *cos_t, const float *sin_t,
                     int q_heads, int kv_heads, int head_dim);
+/* VulkanSwiGLUDownQ{8,4,6} (vulkan_exec_stub.go:218,266,314):
+ * out = Down·(SiLU(G·x)·(U·x)); the SwiGLU vector stays on the device */
+int pocr_swiglu_down(pocr_ctx *ctx, const pocr_weight *gate, const pocr_weight *up, const pocr_weight *down,
+                     const float *x, float *out);
+/* VulkanSwiGLUDownAddRMSNormQ{8,4,6} (vulkan_exec_stub.go:226,274,322;
+ * in_place = 1) and ...OutOnly (230,278,326; in_place = 0), the MLP half of
+ * mlpDownAddRMSNormCPU (internal/model/model.go:5714-5800):
+ * v = residual + Down·SwiGLU(x); norm_out = RMSNorm(v)·norm_w; residual = v
+ * iff in_place.  The Vulkan functions assume eps 1e-6 (model.go:6869). */
+int pocr_swiglu_down_add_rmsnorm(pocr_ctx *ctx, const pocr_weight *gate, const pocr_weight *up,
+                                 const pocr_weight *down, const float *x, float *residual, const float *norm_w,
+                                 float eps, int in_place, float *norm_out);
+/* VulkanAddRMSNormF32 (vulkan_exec_stub.go:30; in_place = 1: dst += add,
+ * AddRMSNorm ops.go:913-935) and VulkanAddRMSNormF32OutOnly (34; in_place = 0,
+ * fused_matvec2.go:11-33): out = RMSNorm(dst + add)·w */
+int pocr_add_rmsnorm(pocr_ctx *ctx, float *dst, const float *add, const float *w, int n, float eps, int in_place,
+                     float *out);
+/* VulkanMRoPEF32 (vulkan_exec_stub.go:38; ApplyMRoPETable,
+ * internal/tensor/weighted_sum.go:231-250): rotate-half RoPE of x[heads*dim]
+ * in place */
+int pocr_mrope(pocr_ctx *ctx, float *x, const float *cos_t, const float *sin_t, int heads, int head_dim);
 /* VulkanTextAttentionF32 (vulkan_exec_stub.go:134): GQA decode attention of
  * q[heads*dim] over cache_len rows of kv_heads*dim fp32 K/V */
 int pocr_text_attention(pocr_ctx *ctx, const float *q, const float *k_cache, const float *v_cache,
                         int cache_len, int heads, int kv_heads, int head_dim, float *out);
+/* VulkanTextAttentionOutQ{8,6,4} (vulkan_exec_stub.go:162,170,178): the
+ * attention above, then out = Wo·attention (wo: rows × heads·dim) */
+int pocr_text_attention_out(pocr_ctx *ctx, const float *q, const float *k_cache, const float *v_cache,
+                            int cache_len, int heads, int kv_heads, int head_dim, const pocr_weight *wo,
+                            float *out);
+/* VulkanTextAttentionOutAddRMSNormQ{8,6,4} (vulkan_exec_stub.go:166,174,182),
+ * the general branch of attentionWithNorm (internal/model/model.go:4040-4066):
+ * v = residual + Wo·attention; norm_out = RMSNorm(v)·norm_w; residual = v iff
+ * in_place (0 for the Q4/Q6 OutOnly behaviour, model.go:4051-4057) */
+int pocr_text_attention_out_add_rmsnorm(pocr_ctx *ctx, const float *q, const float *k_cache,
+                                        const float *v_cache, int cache_len, int heads, int kv_heads, int head_dim,
+                                        const pocr_weight *wo, float *residual, const float *norm_w, float eps,
+                                        int in_place, float *norm_out);
+/* VulkanTextFirstTokenValueOutAddRMSNormQ{8,6,4} (vulkan_exec_stub.go:150,
+ * 154,158), the first-token branch of attentionWithNorm (model.go:3857-3902):
+ * with one cached row the attention output is its V row per q head
+ * (expandValueHeads, model.go:4603-4621; k_cache is not read for the result),
+ * then v = residual + Wo·that; norm_out = RMSNorm(v)·norm_w; residual = v iff
+ * in_place (0 for the Q4/Q6 OutOnly branch, model.go:3895-3902) */
+int pocr_first_token_value_out_add_rmsnorm(pocr_ctx *ctx, const float *k_cache, const float *v_cache, int heads,
+                                           int kv_heads, int head_dim, const pocr_weight *wo, float *residual,
+                                           const float *norm_w, float eps, int in_place, float *norm_out);
 /* No counterpart in the reference: for callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops).  The
  * computation of pocr_text_attention over device buffers the caller owns

@@ -1104,6 +1104,29 @@ static __global__ void __launch_bounds__(kThreads) k_rmsnorm(const float *x, con
     }
 }
 
+// AddRMSNorm (ops.go:913-935) / AddRMSNormOutOnly (fused_matvec2.go:11-33):
+// v = dst + add into v_out, out = v·fastRsqrt(Σv²/n + eps)·w (one workgroup)
+static __global__ void __launch_bounds__(kThreads) k_add_rmsnorm(const float *dst, const float *add, const float *w,
+                                                            int n, float eps, float *v_out, float *out) {
+    __shared__ float red[2 * kWaves];
+    float ss = 0.0f;
+    for (int i = threadIdx.x; i < n; i += kThreads) {
+        float v;
+        {
+#pragma clang fp contract(off)
+            v = dst[i] + add[i];
+        }
+        v_out[i] = v;
+        ss = fmaf(v, v, ss);
+    }
+    ss = block_sum(ss, red);
+    const float scale = fast_rsqrt_ref(ss / (float)n + eps);
+    for (int i = threadIdx.x; i < n; i += kThreads) {  // each thread reads back its own v
+#pragma clang fp contract(off)
+        out[i] = v_out[i] * scale * w[i];
+    }
+}
+
 // ApplyMRoPETable (internal/tensor/weighted_sum.go:231-250) on q and k in place
 __device__ __forceinline__ void rope_pair(float &a, float &b, float cs, float sn) {
 #pragma clang fp contract(off)

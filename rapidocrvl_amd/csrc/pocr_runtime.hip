@@ -719,31 +719,130 @@ extern "C" int pocr_swiglu_gate_up(pocr_ctx *ctx, const pocr_weight *gate, const
     return sync(s);
 }
 
+// v = residual + W·x_dev (x already on the device), norm_out = RMSNorm(v)·norm_w,
+// residual = v iff in_place; host residual/norm_w/norm_out, synchronous
+static int matvec_add_rmsnorm_dev(pocr_ctx *ctx, const pocr_weight *w, const float *x_dev, float *residual,
+                                  const float *norm_w, float eps, int in_place, float *norm_out) {
+    hipStream_t s = ctx->stream;
+    const int n = w->rows;
+    RC(ctx->res.ensure((size_t)n * 4 * 2));
+    RC(ctx->vbuf.ensure((size_t)n * 4));
+    RC(ctx->out3.ensure((size_t)n * 4));
+    RC(h2d(s, ctx->res.p, residual, (size_t)n * 4));
+    RC(h2d(s, ctx->res.as<float>() + n, norm_w, (size_t)n * 4));
+    GemvParams p = gemv_params_1(w);
+    p.x = x_dev;
+    p.residual = ctx->res.as<float>();
+    p.vbuf = ctx->vbuf.as<float>();
+    RC(gemv_launch(s, p, 1, PRO_COPY, EPI_ADDV, kBigGrid));
+    hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(kThreads), 0, s, ctx->vbuf.as<float>(), ctx->res.as<float>() + n, n,
+                       eps, ctx->out3.as<float>());
+    HIP_TRY(hipGetLastError());
+    RC(d2h(s, norm_out, ctx->out3.p, (size_t)n * 4));
+    if (in_place) RC(d2h(s, residual, ctx->vbuf.p, (size_t)n * 4));
+    return sync(s);
+}
+
 extern "C" int pocr_matvec_add_rmsnorm(pocr_ctx *ctx, const pocr_weight *w, const float *x, float *residual,
                                        const float *norm_w, float eps, int in_place, float *norm_out) {
     if (!ctx || !w || !x || !residual || !norm_w || !norm_out)
         return fail(POCR_ERR_ARG, "pocr_matvec_add_rmsnorm: null argument");
     CHECK_INJECT("matvec_add_rmsnorm");
     CTX_GUARD(ctx);
-    hipStream_t s = ctx->stream;
-    const int n = w->rows;
     RC(ctx->x.ensure((size_t)w->cols * 4));
-    RC(ctx->res.ensure((size_t)n * 4 * 2));
+    RC(h2d(ctx->stream, ctx->x.p, x, (size_t)w->cols * 4));
+    return matvec_add_rmsnorm_dev(ctx, w, ctx->x.as<float>(), residual, norm_w, eps, in_place, norm_out);
+}
+
+// SiLU(G·x)·(U·x) of host x into ctx->out (device), for the SwiGLU-down ops
+static int swiglu_dev(pocr_ctx *ctx, const pocr_weight *gate, const pocr_weight *up, const float *x) {
+    hipStream_t s = ctx->stream;
+    RC(ctx->x.ensure((size_t)gate->cols * 4));
+    RC(ctx->out.ensure((size_t)gate->rows * 4));
+    RC(h2d(s, ctx->x.p, x, (size_t)gate->cols * 4));
+    GemvParams p = gemv_params_1(gate);
+    p.m[1] = dev_mat(up);
+    p.x = ctx->x.as<float>();
+    p.out = ctx->out.as<float>();
+    return gemv_launch(s, p, 2, PRO_COPY, EPI_SWIGLU, kBigGrid);
+}
+
+static int swiglu_down_args(const pocr_weight *gate, const pocr_weight *up, const pocr_weight *down, const char *op) {
+    if (gate->rows != up->rows || gate->cols != up->cols || gate->qtype != up->qtype)
+        return fail(POCR_ERR_ARG, "%s: gate/up shapes differ", op);
+    if (down->cols != gate->rows) return fail(POCR_ERR_ARG, "%s: down takes %d columns, gate gives %d", op, down->cols,
+                                              gate->rows);
+    return POCR_OK;
+}
+
+extern "C" int pocr_swiglu_down(pocr_ctx *ctx, const pocr_weight *gate, const pocr_weight *up, const pocr_weight *down,
+                                const float *x, float *out) {
+    if (!ctx || !gate || !up || !down || !x || !out) return fail(POCR_ERR_ARG, "pocr_swiglu_down: null argument");
+    RC(swiglu_down_args(gate, up, down, "pocr_swiglu_down"));
+    CHECK_INJECT("swiglu_down");
+    CTX_GUARD(ctx);
+    hipStream_t s = ctx->stream;
+    RC(swiglu_dev(ctx, gate, up, x));
+    RC(ctx->out2.ensure((size_t)down->rows * 4));
+    GemvParams p = gemv_params_1(down);
+    p.x = ctx->out.as<float>();
+    p.out = ctx->out2.as<float>();
+    RC(gemv_launch(s, p, 1, PRO_COPY, EPI_PLAIN, kBigGrid));
+    RC(d2h(s, out, ctx->out2.p, (size_t)down->rows * 4));
+    return sync(s);
+}
+
+extern "C" int pocr_swiglu_down_add_rmsnorm(pocr_ctx *ctx, const pocr_weight *gate, const pocr_weight *up,
+                                            const pocr_weight *down, const float *x, float *residual,
+                                            const float *norm_w, float eps, int in_place, float *norm_out) {
+    if (!ctx || !gate || !up || !down || !x || !residual || !norm_w || !norm_out)
+        return fail(POCR_ERR_ARG, "pocr_swiglu_down_add_rmsnorm: null argument");
+    RC(swiglu_down_args(gate, up, down, "pocr_swiglu_down_add_rmsnorm"));
+    CHECK_INJECT("swiglu_down_add_rmsnorm");
+    CTX_GUARD(ctx);
+    RC(swiglu_dev(ctx, gate, up, x));
+    return matvec_add_rmsnorm_dev(ctx, down, ctx->out.as<float>(), residual, norm_w, eps, in_place, norm_out);
+}
+
+extern "C" int pocr_add_rmsnorm(pocr_ctx *ctx, float *dst, const float *add, const float *w, int n, float eps,
+                                int in_place, float *out) {
+    if (!ctx || !dst || !add || !w || !out || n <= 0) return fail(POCR_ERR_ARG, "pocr_add_rmsnorm: bad arguments");
+    CHECK_INJECT("add_rmsnorm");
+    CTX_GUARD(ctx);
+    hipStream_t s = ctx->stream;
+    RC(ctx->x.ensure((size_t)n * 12));
     RC(ctx->vbuf.ensure((size_t)n * 4));
     RC(ctx->out.ensure((size_t)n * 4));
-    RC(h2d(s, ctx->x.p, x, (size_t)w->cols * 4));
-    RC(h2d(s, ctx->res.p, residual, (size_t)n * 4));
-    RC(h2d(s, ctx->res.as<float>() + n, norm_w, (size_t)n * 4));
-    GemvParams p = gemv_params_1(w);
-    p.x = ctx->x.as<float>();
-    p.residual = ctx->res.as<float>();
-    p.vbuf = ctx->vbuf.as<float>();
-    RC(gemv_launch(s, p, 1, PRO_COPY, EPI_ADDV, kBigGrid));
-    hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(kThreads), 0, s, ctx->vbuf.as<float>(), ctx->res.as<float>() + n, n,
-                       eps, ctx->out.as<float>());
+    float *xd = ctx->x.as<float>();
+    RC(h2d(s, xd, dst, (size_t)n * 4));
+    RC(h2d(s, xd + n, add, (size_t)n * 4));
+    RC(h2d(s, xd + 2 * n, w, (size_t)n * 4));
+    hipLaunchKernelGGL(k_add_rmsnorm, dim3(1), dim3(kThreads), 0, s, xd, xd + n, xd + 2 * n, n, eps,
+                       ctx->vbuf.as<float>(), ctx->out.as<float>());
     HIP_TRY(hipGetLastError());
-    RC(d2h(s, norm_out, ctx->out.p, (size_t)n * 4));
-    if (in_place) RC(d2h(s, residual, ctx->vbuf.p, (size_t)n * 4));
+    RC(d2h(s, out, ctx->out.p, (size_t)n * 4));
+    if (in_place) RC(d2h(s, dst, ctx->vbuf.p, (size_t)n * 4));
+    return sync(s);
+}
+
+extern "C" int pocr_mrope(pocr_ctx *ctx, float *x, const float *cos_t, const float *sin_t, int heads, int head_dim) {
+    if (!ctx || !x || !cos_t || !sin_t || head_dim <= 0 || head_dim % 2 || heads <= 0)
+        return fail(POCR_ERR_ARG, "pocr_mrope: bad arguments");
+    CHECK_INJECT("mrope");
+    CTX_GUARD(ctx);
+    hipStream_t s = ctx->stream;
+    const int half = head_dim / 2;
+    const size_t nx = (size_t)heads * head_dim;
+    RC(ctx->x.ensure(nx * 4));
+    RC(ctx->tabs.ensure((size_t)half * 8));
+    RC(h2d(s, ctx->x.p, x, nx * 4));
+    RC(h2d(s, ctx->tabs.p, cos_t, (size_t)half * 4));
+    RC(h2d(s, ctx->tabs.as<float>() + half, sin_t, (size_t)half * 4));
+    const int total = heads * half;
+    hipLaunchKernelGGL(k_rope, dim3((total + kThreads - 1) / kThreads), dim3(kThreads), 0, s, ctx->x.as<float>(),
+                       ctx->x.as<float>(), ctx->tabs.as<float>(), ctx->tabs.as<float>() + half, heads, 0, head_dim);
+    HIP_TRY(hipGetLastError());
+    RC(d2h(s, x, ctx->x.p, nx * 4));
     return sync(s);
 }
 
@@ -810,13 +909,9 @@ static void launch_attn_decode(hipStream_t s, int rpw, dim3 grid, const AttnPara
     else hipLaunchKernelGGL(k_attn_decode<16>, grid, dim3(kThreads), 0, s, a);
 }
 
-extern "C" int pocr_text_attention(pocr_ctx *ctx, const float *q, const float *k_cache, const float *v_cache,
-                                   int cache_len, int heads, int kv_heads, int head_dim, float *out) {
-    if (!ctx || !q || !k_cache || !v_cache || !out || cache_len <= 0 || heads <= 0 || kv_heads <= 0 ||
-        head_dim <= 0 || heads % kv_heads)
-        return fail(POCR_ERR_ARG, "pocr_text_attention: bad arguments");
-    CHECK_INJECT("text_attention");
-    CTX_GUARD(ctx);
+// GQA attention of host q over host caches into ctx->out (device, heads·dim)
+static int text_attention_dev(pocr_ctx *ctx, const float *q, const float *k_cache, const float *v_cache, int cache_len,
+                              int heads, int kv_heads, int head_dim) {
     hipStream_t s = ctx->stream;
     const size_t kvd = (size_t)kv_heads * head_dim;
     const size_t nq = (size_t)heads * head_dim;
@@ -856,8 +951,81 @@ extern "C" int pocr_text_attention(pocr_ctx *ctx, const float *q, const float *k
                            ctx->out.as<float>());
     }
     HIP_TRY(hipGetLastError());
-    RC(d2h(s, out, ctx->out.p, nq * 4));
+    return POCR_OK;
+}
+
+static bool attention_args_ok(const void *q, const void *kc, const void *vc, int cache_len, int heads, int kv_heads,
+                              int head_dim) {
+    return q && kc && vc && cache_len > 0 && heads > 0 && kv_heads > 0 && head_dim > 0 && heads % kv_heads == 0;
+}
+
+extern "C" int pocr_text_attention(pocr_ctx *ctx, const float *q, const float *k_cache, const float *v_cache,
+                                   int cache_len, int heads, int kv_heads, int head_dim, float *out) {
+    if (!ctx || !out || !attention_args_ok(q, k_cache, v_cache, cache_len, heads, kv_heads, head_dim))
+        return fail(POCR_ERR_ARG, "pocr_text_attention: bad arguments");
+    CHECK_INJECT("text_attention");
+    CTX_GUARD(ctx);
+    RC(text_attention_dev(ctx, q, k_cache, v_cache, cache_len, heads, kv_heads, head_dim));
+    RC(d2h(ctx->stream, out, ctx->out.p, (size_t)heads * head_dim * 4));
+    return sync(ctx->stream);
+}
+
+static int attention_out_args(const pocr_weight *wo, int heads, int head_dim, const char *op) {
+    if (!wo) return fail(POCR_ERR_ARG, "%s: null weight", op);
+    if (wo->cols != heads * head_dim)
+        return fail(POCR_ERR_ARG, "%s: o_proj takes %d columns, attention gives %d", op, wo->cols, heads * head_dim);
+    return POCR_OK;
+}
+
+extern "C" int pocr_text_attention_out(pocr_ctx *ctx, const float *q, const float *k_cache, const float *v_cache,
+                                       int cache_len, int heads, int kv_heads, int head_dim, const pocr_weight *wo,
+                                       float *out) {
+    if (!ctx || !out || !attention_args_ok(q, k_cache, v_cache, cache_len, heads, kv_heads, head_dim))
+        return fail(POCR_ERR_ARG, "pocr_text_attention_out: bad arguments");
+    RC(attention_out_args(wo, heads, head_dim, "pocr_text_attention_out"));
+    CHECK_INJECT("text_attention_out");
+    CTX_GUARD(ctx);
+    hipStream_t s = ctx->stream;
+    RC(text_attention_dev(ctx, q, k_cache, v_cache, cache_len, heads, kv_heads, head_dim));
+    RC(ctx->out2.ensure((size_t)wo->rows * 4));
+    GemvParams p = gemv_params_1(wo);
+    p.x = ctx->out.as<float>();
+    p.out = ctx->out2.as<float>();
+    RC(gemv_launch(s, p, 1, PRO_COPY, EPI_PLAIN, kBigGrid));
+    RC(d2h(s, out, ctx->out2.p, (size_t)wo->rows * 4));
     return sync(s);
+}
+
+extern "C" int pocr_text_attention_out_add_rmsnorm(pocr_ctx *ctx, const float *q, const float *k_cache,
+                                                   const float *v_cache, int cache_len, int heads, int kv_heads,
+                                                   int head_dim, const pocr_weight *wo, float *residual,
+                                                   const float *norm_w, float eps, int in_place, float *norm_out) {
+    if (!ctx || !residual || !norm_w || !norm_out ||
+        !attention_args_ok(q, k_cache, v_cache, cache_len, heads, kv_heads, head_dim))
+        return fail(POCR_ERR_ARG, "pocr_text_attention_out_add_rmsnorm: bad arguments");
+    RC(attention_out_args(wo, heads, head_dim, "pocr_text_attention_out_add_rmsnorm"));
+    CHECK_INJECT("text_attention_out_add_rmsnorm");
+    CTX_GUARD(ctx);
+    RC(text_attention_dev(ctx, q, k_cache, v_cache, cache_len, heads, kv_heads, head_dim));
+    return matvec_add_rmsnorm_dev(ctx, wo, ctx->out.as<float>(), residual, norm_w, eps, in_place, norm_out);
+}
+
+extern "C" int pocr_first_token_value_out_add_rmsnorm(pocr_ctx *ctx, const float *k_cache, const float *v_cache,
+                                                      int heads, int kv_heads, int head_dim, const pocr_weight *wo,
+                                                      float *residual, const float *norm_w, float eps, int in_place,
+                                                      float *norm_out) {
+    const std::vector<float> q((size_t)std::max(heads, 1) * std::max(head_dim, 1), 0.0f);
+    if (!ctx || !residual || !norm_w || !norm_out ||
+        !attention_args_ok(q.data(), k_cache, v_cache, 1, heads, kv_heads, head_dim))
+        return fail(POCR_ERR_ARG, "pocr_first_token_value_out_add_rmsnorm: bad arguments");
+    RC(attention_out_args(wo, heads, head_dim, "pocr_first_token_value_out_add_rmsnorm"));
+    CHECK_INJECT("first_token_value_out_add_rmsnorm");
+    CTX_GUARD(ctx);
+    // attention over the one cached row is that row's V, exactly (each head's
+    // single weight is FastExp(0)/FastExp(0) = 1): expandValueHeads
+    // (model.go:4603-4621) on the device, whatever q is
+    RC(text_attention_dev(ctx, q.data(), k_cache, v_cache, 1, heads, kv_heads, head_dim));
+    return matvec_add_rmsnorm_dev(ctx, wo, ctx->out.as<float>(), residual, norm_w, eps, in_place, norm_out);
 }
 
 // The computation of pocr_text_attention over device buffers the caller owns,

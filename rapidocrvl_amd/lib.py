@@ -71,6 +71,14 @@ _SIGS = {
     "pocr_mrope_pair": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i]),
     "pocr_text_attention": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
     "pocr_text_attention_noalloc": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
+    "pocr_text_attention_out": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _vp]),
+    "pocr_text_attention_out_add_rmsnorm": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _vp, _vp, C.c_float, _i,
+                                                 _vp]),
+    "pocr_first_token_value_out_add_rmsnorm": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp, _vp, _vp, C.c_float, _i, _vp]),
+    "pocr_swiglu_down": (_i, [_vp, _vp, _vp, _vp, _vp, _vp]),
+    "pocr_swiglu_down_add_rmsnorm": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, C.c_float, _i, _vp]),
+    "pocr_add_rmsnorm": (_i, [_vp, _vp, _vp, _vp, _i, C.c_float, _i, _vp]),
+    "pocr_mrope": (_i, [_vp, _vp, _vp, _vp, _i, _i]),
     "pocr_model_create": (_i, [_vp, C.POINTER(PocrConfig), C.POINTER(_vp)]),
     "pocr_model_destroy": (None, [_vp]),
     "pocr_model_set_weight": (_i, [_vp, _i, _i, _vp]),
@@ -425,6 +433,63 @@ class Context:
         check(load().pocr_text_attention(self.h, _ptr(q), _ptr(kc), _ptr(vc), cache_len, heads, kv_heads, head_dim,
                                          _ptr(out)))
         return out
+
+    def text_attention_out(self, q, k_cache, v_cache, cache_len, heads, kv_heads, head_dim, wo):
+        q, kc, vc = _f32(q), _f32(k_cache), _f32(v_cache)
+        out = np.zeros(wo.rows, np.float32)
+        check(load().pocr_text_attention_out(self.h, _ptr(q), _ptr(kc), _ptr(vc), cache_len, heads, kv_heads, head_dim,
+                                             wo.h, _ptr(out)))
+        return out
+
+    def text_attention_out_add_rmsnorm(self, q, k_cache, v_cache, cache_len, heads, kv_heads, head_dim, wo, residual,
+                                       norm_w, eps, in_place):
+        """Returns (norm_out, residual after)."""
+        q, kc, vc, nw = _f32(q), _f32(k_cache), _f32(v_cache), _f32(norm_w)
+        res = _f32(residual).copy()
+        out = np.zeros(wo.rows, np.float32)
+        check(load().pocr_text_attention_out_add_rmsnorm(self.h, _ptr(q), _ptr(kc), _ptr(vc), cache_len, heads,
+                                                         kv_heads, head_dim, wo.h, _ptr(res), _ptr(nw), eps,
+                                                         int(in_place), _ptr(out)))
+        return out, res
+
+    def first_token_value_out_add_rmsnorm(self, k_cache, v_cache, heads, kv_heads, head_dim, wo, residual, norm_w,
+                                          eps, in_place):
+        """Returns (norm_out, residual after)."""
+        kc, vc, nw = _f32(k_cache), _f32(v_cache), _f32(norm_w)
+        res = _f32(residual).copy()
+        out = np.zeros(wo.rows, np.float32)
+        check(load().pocr_first_token_value_out_add_rmsnorm(self.h, _ptr(kc), _ptr(vc), heads, kv_heads, head_dim,
+                                                            wo.h, _ptr(res), _ptr(nw), eps, int(in_place),
+                                                            _ptr(out)))
+        return out, res
+
+    def swiglu_down(self, gate, up, down, x):
+        x = _f32(x)
+        out = np.zeros(down.rows, np.float32)
+        check(load().pocr_swiglu_down(self.h, gate.h, up.h, down.h, _ptr(x), _ptr(out)))
+        return out
+
+    def swiglu_down_add_rmsnorm(self, gate, up, down, x, residual, norm_w, eps, in_place):
+        """Returns (norm_out, residual after)."""
+        x, nw = _f32(x), _f32(norm_w)
+        res = _f32(residual).copy()
+        out = np.zeros(down.rows, np.float32)
+        check(load().pocr_swiglu_down_add_rmsnorm(self.h, gate.h, up.h, down.h, _ptr(x), _ptr(res), _ptr(nw), eps,
+                                                  int(in_place), _ptr(out)))
+        return out, res
+
+    def add_rmsnorm(self, dst, add, w, eps, in_place):
+        """Returns (out, dst after)."""
+        d = _f32(dst).copy()
+        a, ww = _f32(add), _f32(w)
+        out = np.zeros(d.size, np.float32)
+        check(load().pocr_add_rmsnorm(self.h, _ptr(d), _ptr(a), _ptr(ww), d.size, eps, int(in_place), _ptr(out)))
+        return out, d
+
+    def mrope(self, x, cos_t, sin_t, heads, head_dim):
+        x = _f32(x).copy()
+        check(load().pocr_mrope(self.h, _ptr(x), _ptr(_f32(cos_t)), _ptr(_f32(sin_t)), heads, head_dim))
+        return x
 
     def text_attention_noalloc(self, q_dev, k_dev, v_dev, cache_len, heads, kv_heads, head_dim, out_dev):
         """pocr_text_attention_noalloc over device addresses (ints) the caller owns."""

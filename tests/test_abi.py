@@ -38,6 +38,17 @@ def test_null_arguments_are_arg_errors():
     assert L.pocr_gguf_read(None, 0, None, 4) == lib.POCR_ERR_ARG
     assert L.pocr_gguf_meta(None, 0, None, None, None, None) == lib.POCR_ERR_ARG
     assert L.pocr_model_load_gguf(None, None, b"x", None) == lib.POCR_ERR_ARG
+    # the fused sublayer mirrors and the allocation-free attention
+    assert L.pocr_swiglu_down(None, None, None, None, None, None) == lib.POCR_ERR_ARG
+    assert L.pocr_swiglu_down_add_rmsnorm(None, None, None, None, None, None, None, 1e-5, 1, None) == lib.POCR_ERR_ARG
+    assert L.pocr_add_rmsnorm(None, None, None, None, 4, 1e-5, 1, None) == lib.POCR_ERR_ARG
+    assert L.pocr_mrope(None, None, None, None, 2, 128) == lib.POCR_ERR_ARG
+    assert L.pocr_text_attention_out(None, None, None, None, 1, 16, 2, 128, None, None) == lib.POCR_ERR_ARG
+    assert L.pocr_text_attention_out_add_rmsnorm(None, None, None, None, 1, 16, 2, 128, None, None, None, 1e-5, 1,
+                                                 None) == lib.POCR_ERR_ARG
+    assert L.pocr_first_token_value_out_add_rmsnorm(None, None, None, 16, 2, 128, None, None, None, 1e-5, 1,
+                                                    None) == lib.POCR_ERR_ARG
+    assert L.pocr_text_attention_noalloc(None, None, None, None, 1, 16, 2, 128, None) == lib.POCR_ERR_ARG
     L.pocr_gguf_close(None)
     assert L.pocr_batch_create(None, None) == lib.POCR_ERR_ARG
     assert L.pocr_batch_join(None, None, 0, 0, 1, None, 0) == lib.POCR_ERR_ARG
