@@ -127,17 +127,27 @@ int pocr_matvec_argmax(pocr_ctx *ctx, const pocr_weight *w, const float *x, int3
 /* VulkanMatVecTopKQ{8,4,6} (vulkan_exec_stub.go:194,242,290; CPU
  * MatVecTopKQ*WithWork, internal/tensor/topk.go:200-275): the k best rows of
  * W·x, score descending, equal scores by lower row (topKSelectWithWork,
- * topk.go:322-345).  1 <= k <= min(64, rows) (the reference's GPU limit,
- * model.go:7143); writes k ids (and scores if non-null), returns k. */
+ * topk.go:322-345).  1 <= k <= rows; k > 64 (past the reference's GPU
+ * limit, model.go:7143, where its CPU path takes over) sorts every score on
+ * the device.  Writes k ids (and scores if non-null), returns k. */
 int pocr_matvec_topk(pocr_ctx *ctx, const pocr_weight *w, const float *x, int k, int32_t *ids,
                      float *scores);
 /* one draw from the top k of n host logits — the candidates path of a
  * sampled token (matVecTopKMaybeCPU, internal/model/model.go:7202-7235, then
  * sampleCandidateScoresScratch 1950-1990) — with the fastRNG state *rng_state
- * (model.go:1829-1840), which is advanced.  temperature > 0, 1 < k < n,
- * k <= 64.  Writes the token and, if non-null, the k candidates. */
+ * (model.go:1829-1840), which is advanced.  temperature > 0, 1 < k < n.
+ * Writes the token and, if non-null, the k candidates. */
 int pocr_sample_topk(pocr_ctx *ctx, const float *logits, int n, int k, double temperature,
                      uint64_t *rng_state, int32_t *token, int32_t *ids, float *scores);
+/* one draw over all n host logits — sampleFullLogitsScratch (internal/model/
+ * model.go:2215-2307), which sampleTokenScratch (1870-1879) takes for top_k
+ * 0 or >= n: FastExpF32 weights of x·(1/T) − max·(1/T) (x − max at T = 1,
+ * T = float32(temperature)), their running f32 sum, CumulativeSum
+ * (internal/tensor/cumsum.go:9-58) and pickCumulativeFloat32 (model.go:
+ * 2326-2340); two logits take sampleTwoLogits (2309-2324).  *rng_state is
+ * the fastRNG state, advanced by one draw.  temperature > 0. */
+int pocr_sample_full(pocr_ctx *ctx, const float *logits, int n, double temperature, uint64_t *rng_state,
+                     int32_t *token);
 /* VulkanFusedMatVec3Q* (vulkan_exec_stub.go:202,250,298) */
 int pocr_fused_matvec3(pocr_ctx *ctx, const pocr_weight *a, const pocr_weight *b, const pocr_weight *c,
                        const float *x, float *out_a, float *out_b, float *out_c);
@@ -275,13 +285,12 @@ int pocr_seq_len(const pocr_seq *s);
 /* token choice of the sequence's step-level generation (GenerateOptions
  * Temperature/TopK/Seed, internal/model/model.go:420-470): temperature <= 0
  * or top_k == 1 is greedy (generationUsesArgmaxSampling, 1858-1860);
- * temperature > 0 with 1 < top_k <= 64 (and < vocab) draws every token,
- * the prefill's first included, from the top_k LM-head candidates on the
- * device (model.go:3632-3638, 1950-1990).  The generator restarts at `seed`
+ * otherwise every token, the prefill's first included, is drawn on the
+ * device: from the top_k LM-head candidates for 1 < top_k < vocab
+ * (model.go:3632-3638, 1950-1990), from every score for top_k 0 or >= vocab
+ * (sampleFullLogitsScratch, 2215-2307).  The generator restarts at `seed`
  * here and at every pocr_generate (samplingRNGInto, 1846-1852);
- * pocr_decode_greedy, pocr_decode_batch and pocr_batch_step continue it.
- * Other sampling settings (top_k 0 or > 64: full-vocabulary or wide draws)
- * return POCR_ERR_UNSUPPORTED. */
+ * pocr_decode_greedy, pocr_decode_batch and pocr_batch_step continue it. */
 int pocr_seq_set_sampling(pocr_seq *s, double temperature, int top_k, uint64_t seed);
 /* copy layer's first len rows of K/V (len*kv_heads*head_dim floats each) */
 int pocr_seq_read_kv(pocr_seq *s, int layer, float *k, float *v);

@@ -97,6 +97,11 @@ def lib():
         L.orc_topk.argtypes = [_f32p, C.c_int, C.c_int, _i32p, _f32p]
         L.orc_sample_candidates.restype = C.c_int32
         L.orc_sample_candidates.argtypes = [_i32p, _f32p, C.c_int, C.c_double, C.POINTER(C.c_uint64)]
+        L.orc_cumsum.restype = C.c_float
+        L.orc_cumsum.argtypes = [_f32p, _f32p, C.c_int]
+        L.orc_pick_cumulative.argtypes = [_f32p, C.c_int, C.c_float]
+        L.orc_sample_full.restype = C.c_int32
+        L.orc_sample_full.argtypes = [_f32p, C.c_int, C.c_double, C.POINTER(C.c_uint64)]
         L.orc_set_threads.argtypes = [C.c_int]
         L.orc_get_threads.restype = C.c_int
         _lib = L
@@ -161,6 +166,26 @@ def sample_candidates(ids, scores, temperature, rng: Rng) -> int:
     """sampleCandidateScoresScratch (model.go:1950-1990) on sorted candidates."""
     ids = np.ascontiguousarray(ids, np.int32)
     return int(lib().orc_sample_candidates(ids, _f32(scores), ids.size, temperature, C.byref(rng.state)))
+
+
+def cumsum(x):
+    """CumulativeSum (cumsum.go:9-58): (prefix array, running block total)."""
+    x = _f32(x)
+    out = np.zeros_like(x)
+    tot = lib().orc_cumsum(out, x, x.size)
+    return out, np.float32(tot)
+
+
+def pick_cumulative(cdf, pick) -> int:
+    """pickCumulativeFloat32 (model.go:2326-2340)."""
+    cdf = _f32(cdf)
+    return int(lib().orc_pick_cumulative(cdf, cdf.size, float(np.float32(pick))))
+
+
+def sample_full(logits, temperature, rng: Rng) -> int:
+    """sampleFullLogitsScratch (model.go:2215-2307): one draw over every logit."""
+    logits = _f32(logits)
+    return int(lib().orc_sample_full(logits, logits.size, float(temperature), C.byref(rng.state)))
 
 
 def row_bytes(qtype: int, cols: int) -> int:

@@ -1084,21 +1084,39 @@ double orc_rng_float64(uint64_t *state) {
     return (double)(z >> 11) * (1.0 / 9007199254740992.0);
 }
 
+/* total order of topKSelectWithWork's comparison: score descending, equal
+ * scores by lower index (no NaN scores) */
+static const float *g_sort_scores;
+static int cmp_score_desc(const void *a, const void *b) {
+    const int32_t i = *(const int32_t *)a, j = *(const int32_t *)b;
+    const float si = g_sort_scores[i], sj = g_sort_scores[j];
+    if (si != sj) return si > sj ? -1 : 1;
+    return i < j ? -1 : (i > j);
+}
+
 int orc_topk(const float *scores, int n, int k, int32_t *ids, float *out_scores) {
-    /* topk.go:322-345: partial selection sort; score desc, ties lower id */
+    /* topk.go:322-345: partial selection sort; score desc, ties lower id.
+     * For k > 64 the same order comes from a full sort under the same total
+     * order (the selection sort's k·n comparisons take minutes at k near the
+     * vocabulary); the two agree for every input without NaN scores. */
     if (k <= 0 || n <= 0) return 0;
     if (k > n) k = n;
     int32_t *idx = (int32_t *)malloc(sizeof(int32_t) * (size_t)n);
     for (int i = 0; i < n; i++) idx[i] = i;
-    for (int i = 0; i < k; i++) {
-        int best = i;
-        for (int j = i + 1; j < n; j++) {
-            const float sj = scores[idx[j]], sb = scores[idx[best]];
-            if (sj > sb || (sj == sb && idx[j] < idx[best])) best = j;
+    if (k > 64) {
+        g_sort_scores = scores;
+        qsort(idx, (size_t)n, sizeof(int32_t), cmp_score_desc);
+    } else {
+        for (int i = 0; i < k; i++) {
+            int best = i;
+            for (int j = i + 1; j < n; j++) {
+                const float sj = scores[idx[j]], sb = scores[idx[best]];
+                if (sj > sb || (sj == sb && idx[j] < idx[best])) best = j;
+            }
+            const int32_t t = idx[i];
+            idx[i] = idx[best];
+            idx[best] = t;
         }
-        const int32_t t = idx[i];
-        idx[i] = idx[best];
-        idx[best] = t;
     }
     for (int i = 0; i < k; i++) {
         ids[i] = idx[i];
@@ -1128,12 +1146,21 @@ static int pick_f64(const float *w, int n, double pick) {
     return -1;
 }
 
+static int32_t sample_candidates_w(const int32_t *ids, const float *sc, int n, double temperature, uint64_t *state,
+                                   float *w, float *wv);
+
 int32_t orc_sample_candidates(const int32_t *ids, const float *sc, int n, double temperature, uint64_t *state) {
     if (n <= 0) return 0;
     if (n == 1) return ids[0];
-    float w[64];
     float wv[4];
-    if (n > 64) return -1;
+    float *w = n > 4 ? (float *)malloc(sizeof(float) * (size_t)n) : NULL;
+    int32_t r = sample_candidates_w(ids, sc, n, temperature, state, w, wv);
+    free(w);
+    return r;
+}
+
+static int32_t sample_candidates_w(const int32_t *ids, const float *sc, int n, double temperature, uint64_t *state,
+                                   float *w, float *wv) {
     if (temperature == 1.0) {
         /* model.go:1954-1963 */
         float mx = sc[0];
@@ -1219,6 +1246,104 @@ int32_t orc_sample_candidates(const int32_t *ids, const float *sc, int n, double
     return idx >= 0 ? ids[idx] : ids[n - 1];
 }
 
+/* ---- full-vocabulary draw ---- */
+
+/* CumulativeSum (internal/tensor/cumsum.go:9-58): below 4096 entries one
+ * running f32 sum; otherwise four blocks of (n+3)/4 entries, each summed from
+ * zero, then every block after the first shifted by the running total of the
+ * block sums before it (offset += blockSums[b] after block b is shifted).
+ * out may be x.  Returns that running total. */
+float orc_cumsum(float *out, const float *x, int n) {
+    if (n <= 0) return 0.0f;
+    if (n < 4096) {
+        float cs = 0.0f;
+        for (int i = 0; i < n; i++) {
+            cs += x[i];
+            out[i] = cs;
+        }
+        return cs;
+    }
+    const int bs = (n + 3) / 4;
+    float bsum[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int b = 0; b < 4; b++) {
+        const int start = b * bs, end = start + bs < n ? start + bs : n;
+        float cs = 0.0f;
+        for (int i = start; i < end; i++) {
+            cs += x[i];
+            out[i] = cs;
+        }
+        bsum[b] = cs;
+    }
+    float offset = bsum[0];
+    for (int b = 1; b < 4; b++) {
+        const int start = b * bs, end = start + bs < n ? start + bs : n;
+        for (int i = start; i < end; i++) out[i] += offset;
+        offset += bsum[b];
+    }
+    return offset;
+}
+
+/* pickCumulativeFloat32 (model.go:2326-2340): binary search for the first
+ * entry with pick <= cdf[i]; -1 when the search runs off the end */
+int orc_pick_cumulative(const float *cdf, int n, float pick) {
+    int lo = 0, hi = n;
+    while (lo < hi) {
+        const int mid = (int)((unsigned)(lo + hi) >> 1);
+        if (pick <= cdf[mid]) hi = mid;
+        else lo = mid + 1;
+    }
+    return lo < n ? lo : -1;
+}
+
+/* sampleTwoLogits (model.go:2309-2324) */
+static int sample_two(const float *x, float inv, uint64_t *state) {
+    const float s0 = x[0], s1 = x[1];
+    if (s0 >= s1) {
+        const double w1 = (double)orc_fast_exp((s1 - s0) * inv);
+        return orc_rng_float64(state) * (1 + w1) <= 1 ? 0 : 1;
+    }
+    const double w0 = (double)orc_fast_exp((s0 - s1) * inv);
+    return orc_rng_float64(state) * (w0 + 1) <= w0 ? 0 : 1;
+}
+
+/* sampleFullLogitsScratch (model.go:2215-2260) and, at temperature 1,
+ * sampleFullLogitsTemp1Scratch (2264-2307), with the weight buffer the
+ * generation scratch provides (makeSampleWeights, 2799-2807):
+ *   T = float32(temperature); two logits → sampleTwoLogits(x, 1/T);
+ *   m = max (tensor.Max); at T == 1 v_i = x_i·1 + (−m), otherwise
+ *   v_i = x_i·(1/T) + (−m·(1/T)), all f32;
+ *   w_i = FastExpF32(v_i), sum = Σ w_i in order from zero (ExpScaledVec,
+ *   weighted_sum.go:314-329, with the portable expScaledVecFMA of
+ *   dot_other.go:398-411);
+ *   cdf = CumulativeSum(w); pick = float32(Float64()) · sum;
+ *   the first i with pick <= cdf[i] by binary search, else n − 1.
+ * Draws one value from *state.  Returns the chosen index. */
+int32_t orc_sample_full(const float *x, int n, double temperature, uint64_t *state) {
+    if (n <= 0) return 0;
+    const float T = (float)temperature;
+    if (n == 2) return sample_two(x, 1.0f / T, state);
+    float m = x[0];
+    for (int i = 1; i < n; i++)
+        if (x[i] > m) m = x[i];
+    float scale = 1.0f, bias = -m;
+    if (T != 1.0f) {
+        scale = 1.0f / T;
+        bias = -(m * scale);
+    }
+    float *w = (float *)malloc(sizeof(float) * (size_t)n);
+    float sum = 0.0f;
+    for (int i = 0; i < n; i++) {
+        const float v = x[i] * scale + bias;
+        w[i] = orc_fast_exp(v);
+        sum += w[i];
+    }
+    orc_cumsum(w, w, n);
+    const float pick = (float)orc_rng_float64(state) * sum;
+    const int idx = orc_pick_cumulative(w, n, pick);
+    free(w);
+    return idx >= 0 ? idx : n - 1;
+}
+
 static int generate_impl(orc_model *m, const int32_t *ids, int n_ids, const float *image_embeds, int n_image,
                          int image_token_id, const int32_t grid[3], int merge, int max_new, const int32_t *eos,
                          int n_eos, double temperature, int top_k, uint64_t seed, int32_t *out_tokens);
@@ -1237,26 +1362,31 @@ int orc_generate_sampled(orc_model *m, const int32_t *ids, int n_ids, const floa
                          temperature, top_k, seed, out_tokens);
 }
 
-/* one token from the step's logits: the candidates path of
- * forwardEmbeddingForSampling (model.go:3632-3638, matVecTopKMaybeCPU
- * 7202-7235) and sampleCandidateScoresScratch; greedy when not sampling */
+/* one token from the step's logits: greedy when not sampling; 1 < top_k <
+ * vocab takes the candidates path of forwardEmbeddingForSampling (model.go:
+ * 3632-3638, matVecTopKMaybeCPU 7202-7235) and sampleCandidateScoresScratch;
+ * top_k 0 or >= vocab the full logits through sampleTokenScratch (1870-1879)
+ * into sampleFullLogitsScratch */
 static int32_t pick_token(const float *logits, int vocab, int sampling, int top_k, double temperature,
                           uint64_t *state, int32_t greedy) {
     if (!sampling) return greedy;
-    int32_t cid[64];
-    float csc[64];
+    if (top_k <= 0 || top_k >= vocab) return orc_sample_full(logits, vocab, temperature, state);
+    int32_t *cid = (int32_t *)malloc(sizeof(int32_t) * (size_t)top_k);
+    float *csc = (float *)malloc(sizeof(float) * (size_t)top_k);
     const int n = orc_topk(logits, vocab, top_k, cid, csc);
-    return orc_sample_candidates(cid, csc, n, temperature, state);
+    const int32_t tok = orc_sample_candidates(cid, csc, n, temperature, state);
+    free(cid);
+    free(csc);
+    return tok;
 }
 
 static int generate_impl(orc_model *m, const int32_t *ids, int n_ids, const float *image_embeds, int n_image,
                          int image_token_id, const int32_t grid[3], int merge, int max_new, const int32_t *eos,
                          int n_eos, double temperature, int top_k, uint64_t seed, int32_t *out_tokens) {
     if (n_ids <= 0 || max_new <= 0) return 0;
-    /* generationCanReturnCandidatesOnly (model.go:1866-1868) with the
-     * candidate width this oracle supports (1 < top_k <= 64, top_k < vocab) */
-    const int sampling = temperature > 0 && top_k > 1;
-    if (sampling && (top_k > 64 || top_k >= m->vocab)) return -5;
+    /* generationUsesArgmaxSampling (model.go:1858-1860): greedy at
+     * temperature <= 0 or top_k == 1, sampled otherwise */
+    const int sampling = temperature > 0 && top_k != 1;
     uint64_t state = seed; /* samplingRNGInto, model.go:1846-1852 */
     float *logits = sampling ? (float *)malloc(sizeof(float) * (size_t)m->vocab) : NULL;
     int32_t *pos = (int32_t *)malloc(sizeof(int32_t) * 3 * (size_t)n_ids);

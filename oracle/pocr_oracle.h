@@ -149,10 +149,22 @@ int orc_topk(const float *scores, int n, int k, int32_t *ids, float *out_scores)
  * f32-stored weights (pickWeightedFloat32 2342-2416).  Draws one value from
  * *state unless n <= 1.  Returns the chosen id. */
 int32_t orc_sample_candidates(const int32_t *ids, const float *scores, int n, double temperature, uint64_t *state);
-/* orc_generate with GenerateOptions sampling (model.go:1538-1568, 1846-1868,
- * 3632-3638): temperature > 0 with 1 < top_k < vocab samples every token
- * from the top_k candidates of the LM-head scores with a generator seeded
- * by seed; otherwise greedy.  Returns as orc_generate. */
+/* CumulativeSum (cumsum.go:9-58): one running sum below 4096 entries, else
+ * four zero-based block sums shifted by the running block totals.  out may
+ * be x.  Returns the running total of the block sums. */
+float orc_cumsum(float *out, const float *x, int n);
+/* pickCumulativeFloat32 (model.go:2326-2340): first i with pick <= cdf[i] by
+ * binary search, -1 past the end */
+int orc_pick_cumulative(const float *cdf, int n, float pick);
+/* sampleFullLogitsScratch (model.go:2215-2307) with the generation scratch's
+ * weight buffer and the portable ExpScaledVec (FastExpF32 per entry, f32
+ * running sum); draws one value from *state.  Returns the chosen index. */
+int32_t orc_sample_full(const float *logits, int n, double temperature, uint64_t *state);
+/* orc_generate with GenerateOptions sampling (model.go:1538-1568, 1846-1879,
+ * 3632-3638): temperature > 0 and top_k != 1 samples every token with a
+ * generator seeded by seed — from the top_k candidates of the LM-head scores
+ * when 1 < top_k < vocab, from all of them (orc_sample_full) when top_k is 0
+ * or >= vocab; otherwise greedy.  Returns as orc_generate. */
 int orc_generate_sampled(orc_model *m, const int32_t *ids, int n_ids, const float *image_embeds, int n_image,
                          int image_token_id, const int32_t grid[3], int merge, int max_new, const int32_t *eos,
                          int n_eos, double temperature, int top_k, uint64_t seed, int32_t *out_tokens);

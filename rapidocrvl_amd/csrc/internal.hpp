@@ -17,6 +17,7 @@
 #include "../../include/pocr_hip.h"
 #include "kernels.hpp"
 #include "sample.hpp"
+#include "sample_wide.hpp"
 
 namespace pocr {
 int fail(int code, const char *fmt, ...);
@@ -71,6 +72,7 @@ struct pocr_ctx {
     DevBuf x, out, out2, out3, res, vbuf, kc, vc, part, tabs, state;
     DevBuf gxd, gxs, gxb;  // batched GEMV activation digits
     DevBuf topk_part, samp;  // top-k partial keys, sampler state
+    DevBuf wide;             // wide sampler buffers (pocr::WideBufs)
     // pinned host staging for large host→device uploads: two halves, each
     // reused once the copy recorded on its event has finished
     uint8_t *pin = nullptr;
@@ -139,13 +141,14 @@ struct pocr_seq {
     int nsplit = 32;  // attention splits for rpw rows per wave
     int rpw = 16;
     pocr_batch *batch = nullptr;  // the continuous batch this sequence decodes in (ctx lock)
-    // sampling head (temperature > 0, 1 < top_k ≤ 64); greedy otherwise
+    // sampling head (temperature > 0, top_k != 1); greedy otherwise
     bool sampling = false;
     double temperature = 0.0;
-    int top_k = 0;
+    int top_k = 0;  // 0: every score (top_k 0 or >= vocab)
     uint64_t seed = 0;
     pocr::SampleState *samp = nullptr;
     unsigned long long *topk_part = nullptr;  // [kTopKMaxParts][kTopKMax] keys
+    DevBuf wide;                              // wide sampler buffers (top_k 0 or > 64)
     hipGraphExec_t decode_exec = nullptr;
     hipGraph_t decode_graph = nullptr;
     PrefillBufs pf;

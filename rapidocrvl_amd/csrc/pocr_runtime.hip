@@ -567,6 +567,112 @@ static int enqueue_topk(hipStream_t s, const float *scores, int rows, int k, uns
     return POCR_OK;
 }
 
+// ---- wide sampler: every score (top_k 0 or >= rows) or more than 64 candidates
+
+static int pow2_at_least(int n) {
+    int N = 2;
+    while (N < n) N <<= 1;
+    return N;
+}
+
+static size_t align16(size_t b) { return (b + 15) & ~(size_t)15; }
+
+static size_t wide_bytes(int n) {
+    return align16((size_t)pow2_at_least(n) * 8) + align16((size_t)n * 8) + 2 * align16((size_t)n * 4) +
+           align16(kChainJobs * 8);
+}
+
+// the buffers for n scores, carved from buf (grown as needed)
+static int wide_bufs(DevBuf &buf, int n, WideBufs *b) {
+    RC(buf.ensure(wide_bytes(n)));
+    uint8_t *p = buf.as<uint8_t>();
+    b->keys = reinterpret_cast<unsigned long long *>(p);
+    p += align16((size_t)pow2_at_least(n) * 8);
+    b->pre64 = reinterpret_cast<double *>(p);
+    p += align16((size_t)n * 8);
+    b->w = reinterpret_cast<float *>(p);
+    p += align16((size_t)n * 4);
+    b->pre32 = reinterpret_cast<float *>(p);
+    p += align16((size_t)n * 4);
+    b->totals = reinterpret_cast<double *>(p);
+    return POCR_OK;
+}
+
+// every (score, row) key of scores[0..n) sorted descending into b.keys
+static int enqueue_sort(hipStream_t s, const float *scores, int n, const WideBufs &b, StepState *st) {
+    const int N = pow2_at_least(n);
+    const int tiles = N > kSortTile ? N / kSortTile : 1;
+    hipLaunchKernelGGL(k_sort_tile, dim3(tiles), dim3(kWideThreads), 0, s, scores, n, b.keys, N, st);
+    for (int size = 2 * kSortTile; size <= N; size <<= 1) {
+        for (int j = size / 2; j >= kSortTile; j >>= 1)
+            hipLaunchKernelGGL(k_sort_stage, dim3(N / 2 / kWideThreads), dim3(kWideThreads), 0, s, b.keys, N, size,
+                               j, st);
+        hipLaunchKernelGGL(k_sort_merge, dim3(tiles), dim3(kWideThreads), 0, s, b.keys, N, size, st);
+    }
+    HIP_TRY(hipGetLastError());
+    return POCR_OK;
+}
+
+// sampleFullLogitsScratch over scores[0..n): one draw into ss and argmax
+// slot 0 of st
+static int enqueue_sample_full(hipStream_t s, const float *x, int n, const WideBufs &b, SampleState *ss,
+                               StepState *st) {
+    if (n > 2) {
+        hipLaunchKernelGGL(k_full_weights, dim3(1), dim3(kWideThreads), 0, s, x, n, ss, b.w, st);
+        ChainJobs J{};
+        int nj = 1;
+        if (n < 4096) {
+            J.j[0] = ChainJob{b.w, n, n, b.pre32, nullptr, b.totals};
+        } else {
+            // the sum from index 0 (its first block is CumulativeSum's block 0)
+            // and the blocks 1..3 from zero
+            const int bs = (n + 3) / 4;
+            J.j[0] = ChainJob{b.w, n, bs, b.pre32, nullptr, b.totals};
+            for (int q = 1; q < 4; ++q) {
+                const int a = q * bs, len = std::min(bs, n - a);
+                J.j[q] = ChainJob{b.w + a, len, len, b.pre32 + a, nullptr, b.totals + q};
+            }
+            nj = 4;
+        }
+        hipLaunchKernelGGL(k_chain, dim3(nj), dim3(kWideThreads), 0, s, J, (const SampleState *)ss, 0,
+                           (const StepState *)st);
+    }
+    hipLaunchKernelGGL(k_full_pick, dim3(1), dim3(64), 0, s, x, n, b.pre32, b.totals, ss, st);
+    HIP_TRY(hipGetLastError());
+    return POCR_OK;
+}
+
+// the k (> 4) best of scores[0..n) sorted into b.keys, then, with sample,
+// sampleCandidateScoresScratch's draw among them into ss and st
+static int enqueue_sample_sorted(hipStream_t s, const float *x, int n, int k, const WideBufs &b, SampleState *ss,
+                                 StepState *st, int sample) {
+    RC(enqueue_sort(s, x, n, b, st));
+    if (!sample) return POCR_OK;
+    hipLaunchKernelGGL(k_cand_weights, dim3(1), dim3(kWideThreads), 0, s, (const unsigned long long *)b.keys, k,
+                       (const SampleState *)ss, b.w, (const StepState *)st);
+    ChainJobs J{};
+    J.j[0] = ChainJob{b.w, k, k, b.pre32, b.pre64, b.totals};
+    hipLaunchKernelGGL(k_chain, dim3(1), dim3(kWideThreads), 0, s, J, (const SampleState *)ss, 1,
+                       (const StepState *)st);
+    hipLaunchKernelGGL(k_cand_pick, dim3(1), dim3(kWideThreads), 0, s, (const unsigned long long *)b.keys, k,
+                       (const float *)b.pre32, (const double *)b.pre64, (const double *)b.totals, ss, st);
+    HIP_TRY(hipGetLastError());
+    return POCR_OK;
+}
+
+// ids and scores of the first k sorted keys (host)
+static void keys_to_host(const std::vector<unsigned long long> &keys, int k, int32_t *ids, float *scores) {
+    for (int i = 0; i < k; ++i) {
+        const unsigned long long key = keys[i];
+        if (ids) ids[i] = (int32_t)(0xFFFFFFFFu - (uint32_t)key);
+        if (scores) {
+            uint32_t o = (uint32_t)(key >> 32);
+            o = (o & 0x80000000u) ? (o & 0x7FFFFFFFu) : ~o;
+            std::memcpy(&scores[i], &o, 4);
+        }
+    }
+}
+
 // top-k of `rows` device scores in ctx->out through ctx's sampler state;
 // returns the state read back
 static int ctx_topk(pocr_ctx *ctx, int rows, int k, int sample, const SampleState &in, SampleState *out) {
@@ -583,7 +689,7 @@ static int ctx_topk(pocr_ctx *ctx, int rows, int k, int sample, const SampleStat
 extern "C" int pocr_matvec_topk(pocr_ctx *ctx, const pocr_weight *w, const float *x, int k, int32_t *ids,
                                 float *scores) {
     if (!ctx || !w || !x || !ids || k < 1) return fail(POCR_ERR_ARG, "pocr_matvec_topk: bad arguments");
-    if (k > kTopKMax || k > w->rows) return fail(POCR_ERR_UNSUPPORTED, "pocr_matvec_topk: k %d (<= 64, <= rows)", k);
+    if (k > w->rows) return fail(POCR_ERR_ARG, "pocr_matvec_topk: k %d > rows %d", k, w->rows);
     CHECK_INJECT("matvec_topk");
     CTX_GUARD(ctx);
     hipStream_t s = ctx->stream;
@@ -594,6 +700,16 @@ extern "C" int pocr_matvec_topk(pocr_ctx *ctx, const pocr_weight *w, const float
     p.x = ctx->x.as<float>();
     p.out = ctx->out.as<float>();
     RC(gemv_launch(s, p, 1, PRO_COPY, EPI_PLAIN, kBigGrid));
+    if (k > kTopKMax) {
+        WideBufs b;
+        RC(wide_bufs(ctx->wide, w->rows, &b));
+        RC(enqueue_sample_sorted(s, ctx->out.as<float>(), w->rows, k, b, nullptr, nullptr, 0));
+        std::vector<unsigned long long> keys((size_t)k);
+        RC(d2h(s, keys.data(), b.keys, (size_t)k * 8));
+        RC(sync(s));
+        keys_to_host(keys, k, ids, scores);
+        return k;
+    }
     SampleState in{}, out;
     RC(ctx_topk(ctx, w->rows, k, 0, in, &out));
     for (int i = 0; i < out.n; ++i) {
@@ -608,15 +724,30 @@ extern "C" int pocr_sample_topk(pocr_ctx *ctx, const float *logits, int n, int k
     if (!ctx || !logits || !rng_state || !token || n <= 0) return fail(POCR_ERR_ARG, "pocr_sample_topk: bad arguments");
     if (!(temperature > 0.0) || std::isinf(temperature) || k < 2 || k >= n)
         return fail(POCR_ERR_ARG, "pocr_sample_topk: needs temperature > 0 and 1 < k < n");
-    if (k > kTopKMax) return fail(POCR_ERR_UNSUPPORTED, "pocr_sample_topk: k %d > 64", k);
     CHECK_INJECT("sample_topk");
     CTX_GUARD(ctx);
+    hipStream_t s = ctx->stream;
     RC(ctx->out.ensure((size_t)n * 4));
-    RC(h2d(ctx->stream, ctx->out.p, logits, (size_t)n * 4));
+    RC(h2d(s, ctx->out.p, logits, (size_t)n * 4));
     SampleState in{}, out;
     in.rng = *rng_state;
     in.temperature = temperature;
     in.top_k = k;
+    if (k > kTopKMax) {
+        WideBufs b;
+        RC(wide_bufs(ctx->wide, n, &b));
+        RC(ctx->samp.ensure(sizeof(SampleState)));
+        RC(h2d(s, ctx->samp.p, &in, sizeof(SampleState)));
+        RC(enqueue_sample_sorted(s, ctx->out.as<float>(), n, k, b, ctx->samp.as<SampleState>(), nullptr, 1));
+        std::vector<unsigned long long> keys((size_t)k);
+        RC(d2h(s, keys.data(), b.keys, (size_t)k * 8));
+        RC(d2h(s, &out, ctx->samp.p, sizeof(SampleState)));
+        RC(sync(s));
+        keys_to_host(keys, k, ids, scores);
+        *rng_state = out.rng;
+        *token = out.token;
+        return POCR_OK;
+    }
     RC(ctx_topk(ctx, n, k, 1, in, &out));
     *rng_state = out.rng;
     *token = out.token;
@@ -624,6 +755,31 @@ extern "C" int pocr_sample_topk(pocr_ctx *ctx, const float *logits, int n, int k
         if (ids) ids[i] = out.ids[i];
         if (scores) scores[i] = out.scores[i];
     }
+    return POCR_OK;
+}
+
+extern "C" int pocr_sample_full(pocr_ctx *ctx, const float *logits, int n, double temperature, uint64_t *rng_state,
+                                int32_t *token) {
+    if (!ctx || !logits || !rng_state || !token || n <= 0) return fail(POCR_ERR_ARG, "pocr_sample_full: bad arguments");
+    if (!(temperature > 0.0) || std::isinf(temperature))
+        return fail(POCR_ERR_ARG, "pocr_sample_full: needs a finite temperature > 0");
+    CHECK_INJECT("sample_full");
+    CTX_GUARD(ctx);
+    hipStream_t s = ctx->stream;
+    RC(ctx->out.ensure((size_t)n * 4));
+    RC(h2d(s, ctx->out.p, logits, (size_t)n * 4));
+    SampleState in{}, out;
+    in.rng = *rng_state;
+    in.temperature = temperature;
+    WideBufs b;
+    RC(wide_bufs(ctx->wide, n, &b));
+    RC(ctx->samp.ensure(sizeof(SampleState)));
+    RC(h2d(s, ctx->samp.p, &in, sizeof(SampleState)));
+    RC(enqueue_sample_full(s, ctx->out.as<float>(), n, b, ctx->samp.as<SampleState>(), nullptr));
+    RC(d2h(s, &out, ctx->samp.p, sizeof(SampleState)));
+    RC(sync(s));
+    *rng_state = out.rng;
+    *token = out.token;
     return POCR_OK;
 }
 
@@ -1426,14 +1582,19 @@ extern "C" int pocr_seq_set_sampling(pocr_seq *s, double temperature, int top_k,
     if (!(temperature >= 0.0) || std::isinf(temperature)) return fail(POCR_ERR_ARG, "temperature must be finite and >= 0");
     if (top_k < 0) return fail(POCR_ERR_ARG, "top_k must be >= 0");
     // generationUsesArgmaxSampling (model.go:1858-1860) → greedy; otherwise
-    // the candidates path (1866-1868, topK < vocab) with at most 64 of them
+    // the candidates path (1866-1868) for 1 < top_k < vocab, and every score
+    // (sampleTokenScratch → sampleFullLogitsScratch, 1877-1879) for top_k 0
+    // or >= vocab, kept here as top_k 0
     const bool greedy = temperature <= 0.0 || top_k == 1;
-    if (!greedy && (top_k == 0 || top_k > kTopKMax || top_k >= s->m->cfg.vocab))
-        return fail(POCR_ERR_UNSUPPORTED, "sampling: top_k %d (device sampling takes 1 < top_k <= 64 < vocab)", top_k);
+    if (!greedy && top_k >= s->m->cfg.vocab) top_k = 0;
     std::lock_guard<std::mutex> lk(s->m->ctx->mu);
     RC(seq_idle(s, "pocr_seq_set_sampling"));
     HIP_TRY(hipSetDevice(s->m->ctx->device));
     HIP_TRY(hipStreamSynchronize(s->m->ctx->stream));
+    if (!greedy && (top_k == 0 || top_k > kTopKMax)) {
+        WideBufs b;
+        RC(wide_bufs(s->wide, s->m->cfg.vocab, &b));  // allocated before any capture
+    }
     if (s->sampling != !greedy || (!greedy && s->top_k != top_k)) {
         // the captured step ends in the other LM head: capture again
         if (s->decode_exec) (void)hipGraphExecDestroy(s->decode_exec);
@@ -1826,7 +1987,14 @@ int pocr::enqueue_lm_head(pocr_seq *s, const float *x, bool want_logits) {
     // and the draw (sampleCandidateScoresScratch, 1950-1990)
     p.out = s->logits;
     RC(gemv_launch(st, p, 1, PRO_RMSNORM, EPI_PLAIN, kBigGrid));
-    return enqueue_topk(st, s->logits, m->cfg.vocab, s->top_k, s->topk_part, s->samp, s->st, 1);
+    const int vocab = m->cfg.vocab;
+    if (s->top_k >= 2 && s->top_k <= kTopKMax)
+        return enqueue_topk(st, s->logits, vocab, s->top_k, s->topk_part, s->samp, s->st, 1);
+    WideBufs b;
+    RC(wide_bufs(s->wide, vocab, &b));
+    // top_k 0: every score through sampleTokenScratch (model.go:1877-1879)
+    if (s->top_k == 0) return enqueue_sample_full(st, s->logits, vocab, b, s->samp, s->st);
+    return enqueue_sample_sorted(st, s->logits, vocab, s->top_k, b, s->samp, s->st, 1);
 }
 
 static int enqueue_step(pocr_seq *s, int mode, bool need_logits, bool want_logits) {

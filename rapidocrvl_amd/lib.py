@@ -63,6 +63,7 @@ _SIGS = {
     "pocr_matvec_argmax": (_i, [_vp, _vp, _vp, _vp, _vp]),
     "pocr_matvec_topk": (_i, [_vp, _vp, _vp, _i, _vp, _vp]),
     "pocr_sample_topk": (_i, [_vp, _vp, _i, _i, C.c_double, C.POINTER(C.c_uint64), _vp, _vp, _vp]),
+    "pocr_sample_full": (_i, [_vp, _vp, _i, C.c_double, C.POINTER(C.c_uint64), _vp]),
     "pocr_fused_matvec3": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "pocr_fused_matvec3_mrope": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp, _vp, _vp]),
     "pocr_swiglu_gate_up": (_i, [_vp, _vp, _vp, _vp, _vp]),
@@ -350,6 +351,15 @@ class Context:
         check(load().pocr_sample_topk(self.h, _ptr(logits), logits.size, k, float(temperature), C.byref(st),
                                       _ptr(tok), _ptr(ids), _ptr(sc)))
         return int(tok[0]), int(st.value), ids, sc
+
+    def sample_full(self, logits, temperature: float, rng_state: int):
+        """One draw over every logit (sampleFullLogitsScratch) with the
+        fastRNG state rng_state; returns (token, advanced state)."""
+        logits = _f32(logits)
+        st = C.c_uint64(rng_state & ((1 << 64) - 1))
+        tok = np.zeros(1, np.int32)
+        check(load().pocr_sample_full(self.h, _ptr(logits), logits.size, float(temperature), C.byref(st), _ptr(tok)))
+        return int(tok[0]), int(st.value)
 
     def fused_matvec3(self, a: Weight, b: Weight, c: Weight, x):
         x = _f32(x)

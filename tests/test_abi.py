@@ -30,6 +30,7 @@ def test_null_arguments_are_arg_errors():
     assert b"pocr_step" in L.pocr_last_error()
     assert L.pocr_matvec_topk(None, None, None, 4, None, None) == lib.POCR_ERR_ARG
     assert L.pocr_sample_topk(None, None, 8, 4, 1.0, None, None, None, None) == lib.POCR_ERR_ARG
+    assert L.pocr_sample_full(None, None, 8, 1.0, None, None) == lib.POCR_ERR_ARG
     assert L.pocr_seq_set_sampling(None, 1.0, 4, 0) == lib.POCR_ERR_ARG
     assert L.pocr_gguf_open(None, None) == lib.POCR_ERR_ARG
     assert L.pocr_gguf_tensor_count(None) == lib.POCR_ERR_ARG

@@ -399,3 +399,27 @@ def test_decode_batch_mfma_lm_head_with_sampling(orc, ctx):
     got = lib.decode_batch(seqs, firsts, lens, 10, eos=())
     for i in range(nseq):
         assert list(got[i]) == want[i], (i, opts[i])
+
+
+def test_decode_batch_long_and_wide_sampling_members(orc, ctx):
+    # six sequences (the wide MFMA step), 128 tokens each: greedy members
+    # beside members drawing from every logit (top_k 0, top_k >= vocab), from
+    # 300 sorted candidates and from 20; each stream equals its
+    # single-sequence stream
+    om, gm = _models(orc, ctx, MID, Q4, seed=16)
+    opts = [(0.0, 0, 0), (0.8, 0, 31), (1.0, 300, 32), (0.0, 0, 0), (1.1, MID.vocab, 33), (0.9, 20, 34)]
+    nseq = len(opts)
+    lens = [6 + 5 * i for i in range(nseq)]
+    prompts = [synth.prompt_ids(n, seed=800 + i, high=MID.vocab) for i, n in enumerate(lens)]
+    n_new = 128
+    want = _single_streams(om, gm, prompts, [n_new] * nseq, opts)
+    seqs, firsts = [], []
+    for ids, (t, k, sd) in zip(prompts, opts):
+        s, f = _sampled_prefill(gm, ids, n_new, t, k, sd) if t > 0 else _prefilled(gm, ids, n_new)
+        seqs.append(s)
+        firsts.append(f)
+    got = lib.decode_batch(seqs, firsts, lens, n_new, eos=())
+    for i in range(nseq):
+        assert list(got[i]) == want[i], (i, opts[i])
+    for s in seqs:
+        s.close()

@@ -1,6 +1,7 @@
-"""Sampling LM head on the device: top-k candidates and the draw among them
-against the oracle (topKSelectWithWork + sampleCandidateScoresScratch with
-fastRNG), at op level and inside generation."""
+"""Sampling LM head on the device against the oracle, at op level and inside
+generation: top-k candidates and the draw among them (topKSelectWithWork +
+sampleCandidateScoresScratch with fastRNG) for any 1 < k < n, and the draw
+over every logit (sampleFullLogitsScratch) for top_k 0 or >= vocab."""
 import json
 import os
 
@@ -28,7 +29,7 @@ def _exact_q8(rng, rows, cols):
     return codes * (2.0 ** e)[:, None]
 
 
-@pytest.mark.parametrize("k", [1, 2, 7, 50, 64])
+@pytest.mark.parametrize("k", [1, 2, 7, 50, 64, 65, 300, 9000])
 def test_matvec_topk_exact_scores_with_ties(ctx, orc, k):
     rng = np.random.default_rng(k)
     w = _exact_q8(rng, 9000, 256)
@@ -111,8 +112,77 @@ def test_sample_topk_rejects_bad_arguments(ctx):
     for k, temp in ((1, 1.0), (100, 1.0), (4, 0.0), (4, -1.0), (4, float("nan"))):
         with pytest.raises(lib.PocrError):
             ctx.sample_topk(logits, k, temp, 1)
+    for temp in (0.0, -1.0, float("nan"), float("inf")):
+        with pytest.raises(lib.PocrError) as e:
+            ctx.sample_full(logits, temp, 1)
+        assert e.value.code == lib.POCR_ERR_ARG
     with pytest.raises(lib.PocrError):
-        ctx.sample_topk(np.zeros(200, np.float32), 65, 1.0, 1)
+        ctx.sample_full(np.zeros(0, np.float32), 1.0, 1)
+
+
+@pytest.mark.parametrize("n", [1, 3, 7, 4095, 4096, 4097, 103424])
+@pytest.mark.parametrize("temp", [1.0, 0.8, 1.7, 0.05])
+def test_sample_full_matches_oracle(ctx, orc, n, temp):
+    # every logit: the weights, the f32 running sums in the reference's order
+    # (CumulativeSum's four blocks from 4096 on), the pick and the binary
+    # search are bit-identical, so token and generator state are too
+    # (temperature 0.05 reaches FastExp's wrap below −88.7 for most logits)
+    rng = np.random.default_rng(n * 10 + int(temp * 100))
+    logits = (rng.standard_normal(n) * 3).astype(np.float32)
+    state = 0x0DDB_A11_5EED + n
+    r = orc.Rng(state)
+    for _ in range(10):
+        want = orc.sample_full(logits, temp, r)
+        tok, state = ctx.sample_full(logits, temp, state)
+        assert tok == want and state == r.state.value
+        logits = np.roll(logits, 977)
+
+
+def test_sample_full_two_logits(ctx, orc):
+    state = 99
+    r = orc.Rng(state)
+    for a, b, temp in ((2.0, 1.0, 0.7), (1.0, 2.0, 1.0), (0.5, 0.5, 1.3), (-300.0, 0.0, 1.0)):
+        for _ in range(20):
+            want = orc.sample_full(np.array([a, b], np.float32), temp, r)
+            tok, state = ctx.sample_full(np.array([a, b], np.float32), temp, state)
+            assert tok == want and state == r.state.value
+
+
+def test_sample_full_lm_head_shapes(ctx, orc):
+    # 103,424 logits shaped like an LM head's (a few dominant rows, a long
+    # tail, exact ties at the top), 40 consecutive draws per temperature
+    rng = np.random.default_rng(77)
+    logits = (rng.standard_normal(103424) * 2.5).astype(np.float32)
+    logits[rng.integers(0, 103424, 6)] = logits.max() + 4.0
+    logits[rng.integers(0, 103424, 200)] -= 60.0
+    for temp in (1.0, 0.7, 1.3):
+        state = 12345
+        r = orc.Rng(state)
+        for _ in range(40):
+            want = orc.sample_full(logits, temp, r)
+            tok, state = ctx.sample_full(logits, temp, state)
+            assert tok == want and state == r.state.value
+
+
+@pytest.mark.parametrize("k", [65, 100, 1000, 49999])
+@pytest.mark.parametrize("temp", [1.0, 0.7, 0.04])
+def test_sample_topk_wide_matches_oracle(ctx, orc, k, temp):
+    # more than 64 candidates: every score sorted on the device, the draw's
+    # running sums (f32 at temperature 1, f64 otherwise) in candidate order
+    rng = np.random.default_rng(k * 10 + int(temp * 100))
+    logits = (rng.standard_normal(50000) * 3).astype(np.float32)
+    logits[rng.integers(0, 50000, 8)] = logits.max()  # ties at the top
+    logits[rng.integers(0, 50000, 400)] = np.float32(0.25)  # ties inside
+    state = 0x1234_5678_9ABC_DEF0 + k
+    r = orc.Rng(state)
+    for _ in range(6):
+        want_ids, want_sc = orc.topk(logits, k)
+        want_tok = orc.sample_candidates(want_ids, want_sc, temp, r)
+        tok, state, ids, sc = ctx.sample_topk(logits, k, temp, state)
+        assert np.array_equal(ids, want_ids) and np.array_equal(sc, want_sc)
+        assert tok == want_tok
+        assert state == r.state.value
+        logits = np.roll(logits, 977)
 
 
 def _models(orc, ctx, cfg, qtype, seed):
@@ -154,6 +224,86 @@ def test_generate_sampled_ernie_image(orc, ctx):
     assert list(s.generate(ids, 12, eos=(), use_prefill=True, **kw)) == want
 
 
+def _oracle_draw(orc, logits, temp, top_k, state):
+    """The oracle's token for one draw over a logits row at generator state."""
+    r = orc.Rng(state)
+    if top_k <= 0 or top_k >= logits.size:
+        return orc.sample_full(logits, temp, r)
+    ids, sc = orc.topk(logits, top_k)
+    return orc.sample_candidates(ids, sc, temp, r)
+
+
+def _check_sampled_stream(orc, om, gm, w, ids, got, want, temp, top_k, seed):
+    """A device sampled stream against the oracle's.  Where they split, the
+    split must come from the logits alone: at the first differing draw m, the
+    device's logits row for that draw (the prefill's last row, then one step
+    per token, the sampling head's own scores) and the oracle's row give
+    their own tokens through the oracle sampler at the generator state before
+    draw m, and the two rows agree to 2e-4 of the largest logit.  The sampler
+    itself is bit-exact on equal rows (the op-level tests above); with
+    thousands of comparable weights a pick lands within the rows' last-bit
+    differences of a cumulative boundary every few hundred draws."""
+    m = next((i for i, (a, b) in enumerate(zip(got, want)) if a != b), None)
+    if m is None:
+        assert len(got) == len(want)
+        return None
+    cfg = gm.cfg
+    n = ids.size
+    state = orc.Rng(seed)
+    for _ in range(m):
+        state.float64()
+    st = state.state.value
+    s = gm.seq(n + m + 2)
+    s.set_sampling(temp, top_k, seed)
+    _, dl = s.prefill(w["embed"][ids], np.repeat(np.arange(n, dtype=np.int32)[:, None], 3, axis=1), True)
+    for j in range(m):
+        _, dl = s.step(w["embed"][want[j]], (n + j,) * 3)
+    s.close()
+    os_ = om.seq(n + m + 2)
+    for p in range(n):
+        _, ol, _ = os_.step(w["embed"][ids[p]], (p, p, p), need_logits=p == n - 1, want_logits=p == n - 1)
+    for j in range(m):
+        _, ol, _ = os_.step(w["embed"][want[j]], (n + j,) * 3)
+    scale = max(1.0, float(np.max(np.abs(ol))))
+    diff = float(np.max(np.abs(dl.astype(np.float64) - ol)))
+    assert _oracle_draw(orc, ol, temp, top_k, st) == want[m]
+    assert _oracle_draw(orc, dl, temp, top_k, st) == got[m], f"draw {m}: device token not the sampler's on its logits"
+    assert diff <= 2e-4 * scale, f"draw {m}: logits differ by {diff}"
+    return m
+
+
+@pytest.mark.parametrize("qtype", [Q4, Q8], ids=["q4", "q8"])
+@pytest.mark.parametrize("temp,top_k", [(0.8, 0), (1.0, 0), (0.9, 300), (1.0, 4999), (1.2, 5000)])
+def test_generate_sampled_wide_matches_oracle(orc, ctx, qtype, temp, top_k):
+    # top_k 0 and top_k >= vocab (5000) draw from every logit, 300 and 4999
+    # from sorted candidates: the stream equals the oracle's up to a split
+    # that the logits rows explain
+    w = synth.make_weights(MID, qtype, seed=9)
+    om = orc.Model(MID)
+    om.load_weights(w)
+    gm = lib.Model(ctx, MID)
+    gm.load_weights(w)
+    ids = synth.prompt_ids(23, seed=4, high=MID.vocab)
+    for seed in (1, 2024):
+        want = list(om.generate(ids, 24, eos=(), temperature=temp, top_k=top_k, seed=seed))
+        s = gm.seq(ids.size + 24)
+        s.set_sampling(temp, top_k, seed)
+        got = list(s.generate(ids, 24, eos=(), use_prefill=True))
+        s.close()
+        _check_sampled_stream(orc, om, gm, w, ids, got, want, temp, top_k, seed)
+
+
+def test_generate_full_vocabulary_ernie(orc, ctx):
+    cfg = ERNIE_0P3B
+    om, gm = _models(orc, ctx, cfg, Q4, seed=0)
+    orc.set_threads(16)
+    ids = synth.prompt_ids(21, seed=10)
+    want = list(om.generate(ids, 16, eos=(), temperature=0.8, top_k=0, seed=5))
+    s = gm.seq(ids.size + 16)
+    s.set_sampling(0.8, 0, 5)
+    assert list(s.generate(ids, 16, eos=(), use_prefill=True)) == want
+
+
 def test_greedy_settings_stay_greedy(orc, ctx):
     om, gm = _models(orc, ctx, MID, Q4, seed=3)
     ids = synth.prompt_ids(17, seed=8, high=MID.vocab)
@@ -177,10 +327,9 @@ def test_sampling_settings_errors(ctx):
         with pytest.raises(lib.PocrError) as e:
             s.set_sampling(temp, top_k, 0)
         assert e.value.code == lib.POCR_ERR_ARG
-    for top_k in (0, 65, MID.vocab):
-        with pytest.raises(lib.PocrError) as e:
-            s.set_sampling(0.7, top_k, 0)
-        assert e.value.code == lib.POCR_ERR_UNSUPPORTED
-    # a sampling sequence decodes in a batch too (its own generator)
-    s.set_sampling(0.7, 8, 0)
-    assert len(lib.decode_batch([s], [1], [0], 2, eos=())[0]) == 2
+    # a sampling sequence decodes in a batch too (its own generator), with
+    # any candidate width
+    for top_k in (8, 0, 65, MID.vocab):
+        s.set_sampling(0.7, top_k, 0)
+        s.reset()
+        assert len(lib.decode_batch([s], [1], [0], 2, eos=())[0]) == 2

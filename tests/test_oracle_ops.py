@@ -261,3 +261,26 @@ def test_positions_config4_grid(orc):
     assert delta == 50 - 1345
     p2, d2 = lib.mm_positions(ids, img, (1, 72, 74))
     assert np.array_equal(pos, p2) and d2 == delta
+
+
+@pytest.mark.parametrize("x", [-88.0, -100.0, -150.0, -300.0])
+def test_fast_exp_exponent_wrap(orc, x):
+    # ops.go:1099-1112 adds n<<23 to the bits of the 2^f polynomial in uint32
+    # arithmetic: below n = -126 the exponent field runs out and the carry
+    # lands in the sign bit.  The wrapped value follows from 2^f alone: sign
+    # and exponent field from (bits(2^f) + n·2^23) mod 2^32, the mantissa of
+    # 2^f (to the polynomial's 4e-6).  A clamp or an ldexp would give a tiny
+    # positive number instead.
+    import struct
+    t = float(np.float32(np.float32(x) * np.float32(1.4426950408889634)))
+    n = int(np.rint(t))
+    p = float(np.float32(2.0 ** (t - n)))
+    bits = (struct.unpack("<I", struct.pack("<f", p))[0] + (n << 23)) % (1 << 32)
+    got = orc.fast_exp(x)
+    gbits = struct.unpack("<I", struct.pack("<f", np.float32(got)))[0]
+    assert gbits >> 23 == bits >> 23  # sign and exponent field
+    if (bits >> 23) & 0xFF not in (0, 0xFF):
+        want = struct.unpack("<f", struct.pack("<I", bits))[0]
+        assert abs(got / want - 1) < 4e-6
+    if x <= -100.0 and x > -260.0:
+        assert got < 0  # the carry reached the sign bit
