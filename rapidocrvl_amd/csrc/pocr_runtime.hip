@@ -577,9 +577,24 @@ static int pow2_at_least(int n) {
 
 static size_t align16(size_t b) { return (b + 15) & ~(size_t)15; }
 
+static int wide_tiles(int n) { return n / kCTile + 8; }
+
 static size_t wide_bytes(int n) {
+    const size_t nt = (size_t)wide_tiles(n);
     return align16((size_t)pow2_at_least(n) * 8) + align16((size_t)n * 8) + 2 * align16((size_t)n * 4) +
-           align16(kChainJobs * 8);
+           align16(4 * 8) + align16(4 * 4) + align16((size_t)(n / kFullSpan + 1) * 4) + align16(nt * 8) +
+           align16(nt * 4) + align16(nt * 16) + align16(nt * 16) + align16((size_t)n * 8) + align16((size_t)n * 16) +
+           4 * chain_work_bytes(n) + 512;
+}
+
+// POCR_CHAIN=serial: running sums one add after another; =check: both ways,
+// differences counted (op-level calls fail on any)
+static int chain_mode() {
+    const char *e = getenv("POCR_CHAIN");
+    if (!e) return 0;
+    if (!strcmp(e, "serial")) return 1;
+    if (!strcmp(e, "check")) return 2;
+    return 0;
 }
 
 // the buffers for n scores, carved from buf (grown as needed)
@@ -595,6 +610,67 @@ static int wide_bufs(DevBuf &buf, int n, WideBufs *b) {
     b->pre32 = reinterpret_cast<float *>(p);
     p += align16((size_t)n * 4);
     b->totals = reinterpret_cast<double *>(p);
+    p += align16(4 * 8);
+    b->checks = reinterpret_cast<int *>(p);
+    p += align16(4 * 4);
+    b->bmax = reinterpret_cast<float *>(p);
+    p += align16((size_t)(n / kFullSpan + 1) * 4);
+    const size_t nt = (size_t)wide_tiles(n);
+    b->tsum = reinterpret_cast<double *>(p);
+    p += align16(nt * 8);
+    b->tbad = reinterpret_cast<int *>(p);
+    p += align16(nt * 4);
+    b->tcnt = reinterpret_cast<int *>(p);
+    p += align16(nt * 16);
+    b->trs = reinterpret_cast<unsigned long long *>(p);
+    p += align16(nt * 16);
+    b->cls = reinterpret_cast<int *>(p);
+    p += align16((size_t)n * 8);
+    b->rr = reinterpret_cast<unsigned long long *>(p);
+    p += align16((size_t)n * 16);
+    b->ev = reinterpret_cast<uint8_t *>(((uintptr_t)p + 255) & ~(uintptr_t)255);
+    b->ev_stride = chain_work_bytes(n);
+    return POCR_OK;
+}
+
+// n weights in b.w as one sum (nseg 1, sums below pre_lim0) or as
+// CumulativeSum's four blocks plus the sum from index 0 (nseg 4)
+static ChainSet chain_set(const WideBufs &b, int n, int nseg, int pre_lim0) {
+    ChainSet S{};
+    S.w = b.w;
+    S.n = n;
+    S.nseg = nseg;
+    S.seg_len = nseg == 1 ? n : (n + 3) / 4;
+    S.seg_tiles = (S.seg_len + kCTile - 1) / kCTile;
+    S.ntiles = nseg == 1 ? S.seg_tiles : 3 * S.seg_tiles + (n - 3 * S.seg_len + kCTile - 1) / kCTile;
+    S.pre_lim0 = pre_lim0;
+    S.pre32 = b.pre32;
+    S.pre64 = b.pre64;
+    S.totals = b.totals;
+    S.tsum = b.tsum;
+    S.tbad = b.tbad;
+    S.tcnt = b.tcnt;
+    S.trs = b.trs;
+    S.cls = b.cls;
+    S.rr = b.rr;
+    S.ev = b.ev;
+    S.ev_stride = b.ev_stride;
+    S.check = b.checks;
+    return S;
+}
+
+// the running sums of a chain set whose weights (and tile sums) are written
+static int enqueue_chain(hipStream_t s, const ChainSet &S, SampleState *ss, int by_temperature, StepState *st) {
+    const int mode = chain_mode();
+    const dim3 grid(S.ntiles, S.nseg > 1 ? 2 : 1);
+    const SampleState *cs = ss;
+    const StepState *cst = st;
+    hipLaunchKernelGGL(k_chain_cls, grid, dim3(kCThreads), 0, s, S, cs, by_temperature, mode, cst);
+    hipLaunchKernelGGL(k_chain_compact, grid, dim3(kCThreads), 0, s, S, mode, cst);
+    hipLaunchKernelGGL(k_chain_walk, dim3(S.nseg), dim3(kCThreads), 0, s, S, cs, by_temperature, mode, cst);
+    hipLaunchKernelGGL(k_chain_fin, grid, dim3(kCThreads), 0, s, S, cs, by_temperature, mode, cst);
+    if (mode == 2) hipLaunchKernelGGL(k_chain_check, dim3(S.nseg), dim3(kCThreads), 0, s, S, cs, by_temperature, cst);
+    HIP_TRY(hipGetLastError());
     return POCR_OK;
 }
 
@@ -618,24 +694,14 @@ static int enqueue_sort(hipStream_t s, const float *scores, int n, const WideBuf
 static int enqueue_sample_full(hipStream_t s, const float *x, int n, const WideBufs &b, SampleState *ss,
                                StepState *st) {
     if (n > 2) {
-        hipLaunchKernelGGL(k_full_weights, dim3(1), dim3(kWideThreads), 0, s, x, n, ss, b.w, st);
-        ChainJobs J{};
-        int nj = 1;
-        if (n < 4096) {
-            J.j[0] = ChainJob{b.w, n, n, b.pre32, nullptr, b.totals};
-        } else {
-            // the sum from index 0 (its first block is CumulativeSum's block 0)
-            // and the blocks 1..3 from zero
-            const int bs = (n + 3) / 4;
-            J.j[0] = ChainJob{b.w, n, bs, b.pre32, nullptr, b.totals};
-            for (int q = 1; q < 4; ++q) {
-                const int a = q * bs, len = std::min(bs, n - a);
-                J.j[q] = ChainJob{b.w + a, len, len, b.pre32 + a, nullptr, b.totals + q};
-            }
-            nj = 4;
-        }
-        hipLaunchKernelGGL(k_chain, dim3(nj), dim3(kWideThreads), 0, s, J, (const SampleState *)ss, 0,
-                           (const StepState *)st);
+        const int nb = (n + kFullSpan - 1) / kFullSpan;
+        hipLaunchKernelGGL(k_full_max, dim3(nb), dim3(kFullThreads), 0, s, x, n, b.bmax, (const StepState *)st);
+        // the sum from index 0 (its first block is CumulativeSum's block 0)
+        // and, from 4096 entries on, the blocks 1..3 from zero
+        const ChainSet S = n < 4096 ? chain_set(b, n, 1, n) : chain_set(b, n, 4, (n + 3) / 4);
+        hipLaunchKernelGGL(k_full_weights, dim3(S.ntiles), dim3(kCThreads), 0, s, x, (const float *)b.bmax, nb,
+                           (const SampleState *)ss, S, (const StepState *)st);
+        RC(enqueue_chain(s, S, ss, 0, st));
     }
     hipLaunchKernelGGL(k_full_pick, dim3(1), dim3(64), 0, s, x, n, b.pre32, b.totals, ss, st);
     HIP_TRY(hipGetLastError());
@@ -648,15 +714,24 @@ static int enqueue_sample_sorted(hipStream_t s, const float *x, int n, int k, co
                                  StepState *st, int sample) {
     RC(enqueue_sort(s, x, n, b, st));
     if (!sample) return POCR_OK;
-    hipLaunchKernelGGL(k_cand_weights, dim3(1), dim3(kWideThreads), 0, s, (const unsigned long long *)b.keys, k,
-                       (const SampleState *)ss, b.w, (const StepState *)st);
-    ChainJobs J{};
-    J.j[0] = ChainJob{b.w, k, k, b.pre32, b.pre64, b.totals};
-    hipLaunchKernelGGL(k_chain, dim3(1), dim3(kWideThreads), 0, s, J, (const SampleState *)ss, 1,
-                       (const StepState *)st);
+    const ChainSet S = chain_set(b, k, 1, k);
+    hipLaunchKernelGGL(k_cand_weights, dim3(S.ntiles), dim3(kCThreads), 0, s, (const unsigned long long *)b.keys,
+                       (const SampleState *)ss, S, (const StepState *)st);
+    RC(enqueue_chain(s, S, ss, 1, st));
     hipLaunchKernelGGL(k_cand_pick, dim3(1), dim3(kWideThreads), 0, s, (const unsigned long long *)b.keys, k,
                        (const float *)b.pre32, (const double *)b.pre64, (const double *)b.totals, ss, st);
     HIP_TRY(hipGetLastError());
+    return POCR_OK;
+}
+
+// synchronize; in check mode, fail when the parallel running sums differed
+// from the one-by-one sums anywhere
+static int chain_checked(hipStream_t s, const WideBufs &b) {
+    int chk[4] = {0, 0, 0, 0};
+    if (chain_mode() == 2) RC(d2h(s, chk, b.checks, sizeof(chk)));
+    RC(sync(s));
+    const int d = chk[0] + chk[1] + chk[2] + chk[3];
+    if (d) return fail(POCR_ERR_DEVICE, "running sums: %d differ from the one-by-one sums", d);
     return POCR_OK;
 }
 
@@ -738,11 +813,12 @@ extern "C" int pocr_sample_topk(pocr_ctx *ctx, const float *logits, int n, int k
         RC(wide_bufs(ctx->wide, n, &b));
         RC(ctx->samp.ensure(sizeof(SampleState)));
         RC(h2d(s, ctx->samp.p, &in, sizeof(SampleState)));
+        HIP_TRY(hipMemsetAsync(b.checks, 0, 4 * 4, s));
         RC(enqueue_sample_sorted(s, ctx->out.as<float>(), n, k, b, ctx->samp.as<SampleState>(), nullptr, 1));
         std::vector<unsigned long long> keys((size_t)k);
         RC(d2h(s, keys.data(), b.keys, (size_t)k * 8));
         RC(d2h(s, &out, ctx->samp.p, sizeof(SampleState)));
-        RC(sync(s));
+        RC(chain_checked(s, b));
         keys_to_host(keys, k, ids, scores);
         *rng_state = out.rng;
         *token = out.token;
@@ -775,9 +851,10 @@ extern "C" int pocr_sample_full(pocr_ctx *ctx, const float *logits, int n, doubl
     RC(wide_bufs(ctx->wide, n, &b));
     RC(ctx->samp.ensure(sizeof(SampleState)));
     RC(h2d(s, ctx->samp.p, &in, sizeof(SampleState)));
+    HIP_TRY(hipMemsetAsync(b.checks, 0, 4 * 4, s));
     RC(enqueue_sample_full(s, ctx->out.as<float>(), n, b, ctx->samp.as<SampleState>(), nullptr));
     RC(d2h(s, &out, ctx->samp.p, sizeof(SampleState)));
-    RC(sync(s));
+    RC(chain_checked(s, b));
     *rng_state = out.rng;
     *token = out.token;
     return POCR_OK;

@@ -333,3 +333,64 @@ def test_sampling_settings_errors(ctx):
         s.set_sampling(0.7, top_k, 0)
         s.reset()
         assert len(lib.decode_batch([s], [1], [0], 2, eos=())[0]) == 2
+
+
+def _tie_prone_logit(orc):
+    """A logit whose FastExp weight ends its mantissa in 1 and nine zeros: once
+    a running sum of such weights reaches the binade where the grid is
+    2^10 weight-ulps, every add of it is a rounding tie."""
+    import struct
+    for i in range(200000):
+        v = float(np.float32(-0.7 + i * 1e-6))
+        m = struct.unpack("<I", struct.pack("<f", np.float32(orc.fast_exp(v))))[0] & 0x7FFFFF
+        if m and (m & -m).bit_length() - 1 >= 9:
+            return v
+    raise AssertionError("no tie-prone logit found")
+
+
+def _chain_logits(orc, case, n, rng):
+    if case == "normal":
+        return (rng.standard_normal(n) * 3).astype(np.float32)
+    if case == "peaked":
+        x = (rng.standard_normal(n) * 2).astype(np.float32)
+        x[rng.integers(0, n, 3)] += 25.0
+        return x
+    if case == "flat":
+        x = np.zeros(n, np.float32)
+        x[n // 3] = 0.5
+        return x
+    if case == "coarse":
+        return (np.round(rng.standard_normal(n) * 4) / 2).astype(np.float32)
+    if case == "ties":
+        x = np.full(n, _tie_prone_logit(orc), np.float32)
+        x[0] = 0.0
+        return x
+    if case == "tiny":  # weights near the bottom of the normal range first
+        x = (rng.standard_normal(n) * 0.5).astype(np.float32)
+        x[: n // 8] -= 80.0
+        return x
+    raise ValueError(case)
+
+
+@pytest.mark.parametrize("n", [5000, 103424])
+@pytest.mark.parametrize("case", ["normal", "peaked", "flat", "coarse", "ties", "tiny"])
+def test_parallel_running_sums_equal_one_by_one(ctx, orc, monkeypatch, case, n):
+    # POCR_CHAIN=check: every draw also evaluates its running sums one add
+    # after another and the call fails if any sum differs in any bit; the
+    # draws equal the oracle's
+    monkeypatch.setenv("POCR_CHAIN", "check")
+    rng = np.random.default_rng(n + len(case))
+    logits = _chain_logits(orc, case, n, rng)
+    for temp in (1.0, 0.8, 2.0):
+        state = 5 + n
+        r = orc.Rng(state)
+        for _ in range(3):
+            want = orc.sample_full(logits, temp, r)
+            tok, state = ctx.sample_full(logits, temp, state)
+            assert tok == want and state == r.state.value
+        k = min(n - 1, 3000)
+        for _ in range(2):  # f32 (temperature 1) or f64 candidate sums
+            want_ids, want_sc = orc.topk(logits, k)
+            want = orc.sample_candidates(want_ids, want_sc, temp, r)
+            tok, state, ids, _ = ctx.sample_topk(logits, k, temp, state)
+            assert tok == want and state == r.state.value
