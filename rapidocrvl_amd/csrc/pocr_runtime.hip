@@ -1799,14 +1799,16 @@ extern "C" int pocr_time_matvec_batched(pocr_ctx *ctx, const pocr_weight *const 
     RC(ctx->x.ensure((size_t)m * w0->cols * 4));
     RC(ctx->out.ensure((size_t)m * w0->rows * 4));
     RC(h2d(s, ctx->x.p, x, (size_t)m * w0->cols * 4));
+    // the launches pocr_matvec makes for m rows: the vector GEMV with 2 or 4
+    // vectors per pass up to m = 4, the digit-plane MFMA GEMM above
     for (int i = 0; i < n_weights; ++i)  // warm-up pass (allocates the digit buffers)
-        RC(batched_gemv(ctx, dev_mat(weights[i]), ctx->x.as<float>(), m, ctx->out.as<float>()));
+        RC(matvec_rows(ctx, weights[i], ctx->x.as<float>(), m, ctx->out.as<float>()));
     hipEvent_t e0, e1;
     HIP_TRY(hipEventCreate(&e0));
     HIP_TRY(hipEventCreate(&e1));
     HIP_TRY(hipEventRecord(e0, s));
     for (int it = 0; it < iters; ++it)
-        RC(batched_gemv(ctx, dev_mat(weights[it % n_weights]), ctx->x.as<float>(), m, ctx->out.as<float>()));
+        RC(matvec_rows(ctx, weights[it % n_weights], ctx->x.as<float>(), m, ctx->out.as<float>()));
     HIP_TRY(hipEventRecord(e1, s));
     HIP_TRY(hipEventSynchronize(e1));
     float ms = 0.0f;
