@@ -13,7 +13,9 @@ import subprocess
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "_build", "libpocr_oracle.so")
+# POCR_ORACLE_LIB names another build of the same sources (the sanitizer
+# build of tests/sanitize.py)
+LIB_PATH = os.environ.get("POCR_ORACLE_LIB") or os.path.join(HERE, "_build", "libpocr_oracle.so")
 
 Q8, Q4, Q6 = 1000, 1001, 1002
 TIE_HALF_AWAY, TIE_AMD64 = 0, 1

@@ -27,7 +27,7 @@ HIP_FLAGS = [
 HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-ffp-contract=off"]
 
 HIP_SOURCES = ["pocr_runtime.hip", "prefill.hip", "projector.hip"]
-HOST_SOURCES = ["quant_host.cpp", "gguf.cpp"]
+HOST_SOURCES = ["quant_host.cpp", "gguf.cpp", "errors.cpp"]
 
 
 def _run(cmd):
@@ -35,6 +35,22 @@ def _run(cmd):
     if r.returncode != 0:
         raise RuntimeError(f"build failed: {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
     return r
+
+
+SAN_FLAGS = ["-O1", "-g", "-fno-omit-frame-pointer", "-fsanitize=address,undefined", "-fno-sanitize-recover=undefined"]
+
+
+def build_host_sanitized() -> str:
+    """The host-only sources as their own library under AddressSanitizer and
+    UndefinedBehaviorSanitizer (g++, no device code): the functions lib.py
+    takes from it when POCR_HOST_LIB names it."""
+    out = os.path.join(BUILD, "san")
+    os.makedirs(out, exist_ok=True)
+    lib = os.path.join(out, "libpocr_host.so")
+    srcs = [os.path.join(CSRC, s) for s in HOST_SOURCES]
+    _run(["g++", "-std=c++17", "-fPIC", "-Wall", "-ffp-contract=off", *SAN_FLAGS, "-shared", "-o", lib + ".tmp", *srcs])
+    shutil.move(lib + ".tmp", lib)
+    return lib
 
 
 def build(verbose: bool = False) -> str:

@@ -13,18 +13,6 @@
 
 namespace pocr {
 
-static thread_local std::string g_err;
-
-int fail(int code, const char *fmt, ...) {
-    char buf[512];
-    va_list ap;
-    va_start(ap, fmt);
-    vsnprintf(buf, sizeof(buf), fmt, ap);
-    va_end(ap);
-    g_err = buf;
-    return code;
-}
-
 // POCR_HIP_FAIL_OP=<op>[,<op>...] makes the named ops return POCR_ERR_INJECTED
 // before touching the device, so a caller's CPU fallback can be exercised
 // (the reference disables a failing op and uses the CPU kernel,
@@ -48,7 +36,6 @@ bool injected(const char *op) {
 using namespace pocr;
 
 extern "C" int pocr_abi_version(void) { return POCR_ABI_VERSION; }
-extern "C" const char *pocr_last_error(void) { return g_err.c_str(); }
 
 extern "C" int pocr_device_count(void) {
     int n = 0;

@@ -17,6 +17,10 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "_lib", "libpocr_hip.so")
 HEADER = os.path.join(os.path.dirname(HERE), "include", "pocr_hip.h")
+# POCR_HOST_LIB names a build of the host-only sources (quant_host.cpp,
+# gguf.cpp) whose functions then replace the library's own: the sanitizer
+# build of tests/sanitize.py
+HOST_LIB_PATH = os.environ.get("POCR_HOST_LIB")
 
 POCR_OK = 0
 POCR_ERR_ARG = -1
@@ -132,6 +136,12 @@ _SIGS = {
 _lib = None
 
 
+# the entry points implemented by the host-only sources
+HOST_SYMBOLS = frozenset(["pocr_row_bytes", "pocr_quantize_rows", "pocr_unpack_rows", "pocr_mm_positions",
+                          "pocr_gguf_open", "pocr_gguf_close", "pocr_gguf_tensor_count", "pocr_gguf_find",
+                          "pocr_gguf_tensor_info", "pocr_gguf_read", "pocr_gguf_meta_count", "pocr_gguf_meta"])
+
+
 def header_symbols(path: str = HEADER):
     """Function names declared in include/pocr_hip.h."""
     text = open(path).read()
@@ -148,8 +158,35 @@ def load():
             fn = getattr(L, name)
             fn.restype = res
             fn.argtypes = args
+        if HOST_LIB_PATH:
+            _use_host_lib(L, C.CDLL(HOST_LIB_PATH))
         _lib = L
     return _lib
+
+
+_host_error = None  # the host library's message after its last failed call
+
+
+def _use_host_lib(L, H):
+    """Route the host-only entry points to H; a failure there keeps H's
+    last-error text for check()."""
+    H.pocr_last_error.restype = C.c_char_p
+    H.pocr_last_error.argtypes = []
+
+    def route(fn):
+        def call(*a):
+            global _host_error
+            rc = fn(*a)
+            _host_error = H.pocr_last_error() if isinstance(rc, int) and rc < 0 else None
+            return rc
+        return call
+
+    for name in HOST_SYMBOLS:
+        res, args = _SIGS[name]
+        fn = getattr(H, name)
+        fn.restype = res
+        fn.argtypes = args
+        setattr(L, name, route(fn))
 
 
 def _ptr(a):
@@ -157,8 +194,10 @@ def _ptr(a):
 
 
 def check(rc: int):
+    global _host_error
     if rc < 0:
-        raise PocrError(rc, load().pocr_last_error().decode(errors="replace"))
+        msg, _host_error = _host_error or load().pocr_last_error(), None
+        raise PocrError(rc, msg.decode(errors="replace"))
     return rc
 
 
