@@ -42,7 +42,7 @@ struct HeadParams {
     float eps;
     float *out;            // optional: scores of vector v at out + v·out_stride
     int out_stride;
-    StepState *st[kHeadMaxVec];  // argmax slots of vector v
+    StepState *st[kHeadMaxVec];  // argmax slots of vector v (null: scores only)
 };
 
 // The shape of the work.  Every load instruction of a wave reads 8 weight
@@ -315,7 +315,348 @@ __global__ void __launch_bounds__(kThreads) k_head_mfma(HeadParams p) {
         StepState *st = p.st[0];
 #pragma unroll
         for (int u = 1; u < NV; ++u) st = vv == u ? p.st[u] : st;
-        if (m) atomicMax(&st->argmax_slot[(blockIdx.x % kArgSlots) * kSlotPitch], m);
+        if (m && st) atomicMax(&st->argmax_slot[(blockIdx.x % kArgSlots) * kSlotPitch], m);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// The same head for 2 to 16 vectors (the batched decode's greedy members, or
+// M rows of scores), in two launches.
+//
+// k_head_digits (one workgroup per vector) writes each vector's three digit
+// planes, its score scale and its plane biases exactly as k_head_mfma makes
+// them (same thread → column map and reduction order), so a vector's scores
+// are bit-identical to that kernel's: a row's three plane sums are exact.
+// The planes land in the order the head's B operands are read, 16 bytes per
+// (step, plane, lane group, vector), so a B read is 64 consecutive 16-byte
+// pieces in LDS and the head copies only the live vectors' pieces.
+//
+// k_head_wide: one B tile per digit plane holds all 16 vectors (column =
+// vector), so every MFMA column is used and the A operand is 16 distinct
+// weight rows.  Weights are read as whole 128-byte lines (8 rows per load
+// instruction; a 16-rows × 64-byte pattern streams at two thirds of the
+// rate on MI355X) and one DPP rotate per dword forms the A operands.  A wave
+// owns R blocks of 16 rows over all the columns (no cross-wave sums) and
+// requests every weight byte of its rows at once (R·row bytes/4 per lane,
+// 512 at most), right behind the digit planes.
+// ---------------------------------------------------------------------------
+constexpr int kHeadWideVec = 16;
+#ifndef POCR_HEAD_WIDE_LANE_BYTES
+#define POCR_HEAD_WIDE_LANE_BYTES 512  // weight bytes a lane requests at once
+#endif
+
+template <int QT, int NS>
+struct HeadWideShape {
+    static constexpr int COLS = 256 * NS;
+    static constexpr int ROW_BYTES = QT == QT_Q4 ? COLS / 2 : COLS;
+    static constexpr int LINES = ROW_BYTES / 128;  // 128-byte lines per row
+    static constexpr int CP = QT == QT_Q4 ? 32 : 16;  // codes per 16-byte piece
+    static constexpr int SPL = head_steps_per_load<QT>();
+    static constexpr int STEPS = LINES * 2 * SPL;  // MFMA steps of 64 columns
+    static constexpr int PLANE_BYTES = STEPS * 3 * 4 * kHeadWideVec * 16;
+    static constexpr int R0 = POCR_HEAD_WIDE_LANE_BYTES * 4 / ROW_BYTES;
+    static constexpr int R = R0 > 1 ? R0 : 1;  // row blocks per wave
+    static constexpr int ROWS_PER_WG = 16 * R * kWaves;
+};
+
+// byte offset of column c's digit (plane pl, vector v) in the planes buffer:
+// step (line ln, piece parity par, half h), lane group g of K slice
+// 8·CP·ln + 2·CP·g + CP·par + 16·h, digit_pos16 order inside the 16 columns
+template <int QT, int NS>
+__device__ __forceinline__ int head_plane_off(int c, int pl, int v) {
+    using SH = HeadWideShape<QT, NS>;
+    const int ln = c / (8 * SH::CP), rem = c % (8 * SH::CP);
+    const int g = rem / (2 * SH::CP), rem2 = rem % (2 * SH::CP);
+    const int par = rem2 / SH::CP, h = (rem2 % SH::CP) / 16;
+    const int st = (ln * 2 + par) * SH::SPL + h;
+    return ((st * 3 + pl) * 4 + g) * 256 + v * 16 + digit_pos16<QT>(c % 16);
+}
+
+struct HeadDigitParams {
+    const float *x;        // vector v at x + v·x_stride (cols floats)
+    int x_stride;
+    const float *norm_w;   // null → the scores use x as given
+    float eps;
+    int8_t *planes;        // HeadWideShape::PLANE_BYTES
+    float *vscale;         // [16] S·(RMSNorm factor)
+    int *vbias;            // [16][3] IBIAS·Σd per plane
+};
+
+template <int QT, int NS>
+__global__ void __launch_bounds__(kThreads) k_head_digits(HeadDigitParams p) {
+    constexpr int COLS = 256 * NS;
+    constexpr int PER_T = COLS / kThreads;
+    constexpr int IB = DigitTraits<QT>::IBIAS;
+    __shared__ float redf[2][kWaves];
+    __shared__ int redi[3][kWaves];
+    const int v = blockIdx.x;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int cb = PER_T * (int)threadIdx.x;
+    const bool norm = p.norm_w != nullptr;
+    float xr[PER_T], y[PER_T];
+    float ss = 0.0f, mx = 0.0f;
+#pragma unroll
+    for (int i = 0; i < PER_T; i += 4) {
+        const float4 x4 = *reinterpret_cast<const float4 *>(p.x + (size_t)v * p.x_stride + cb + i);
+        const float4 w4 = norm ? *reinterpret_cast<const float4 *>(p.norm_w + cb + i) : make_float4(1, 1, 1, 1);
+        xr[i] = x4.x;
+        xr[i + 1] = x4.y;
+        xr[i + 2] = x4.z;
+        xr[i + 3] = x4.w;
+        y[i] = norm ? x4.x * w4.x : x4.x;  // a lone product: nothing to contract
+        y[i + 1] = norm ? x4.y * w4.y : x4.y;
+        y[i + 2] = norm ? x4.z * w4.z : x4.z;
+        y[i + 3] = norm ? x4.w * w4.w : x4.w;
+    }
+#pragma unroll
+    for (int i = 0; i < PER_T; ++i) {
+        ss = fmaf(xr[i], xr[i], ss);
+        mx = fmaxf(mx, fabsf(y[i]));
+    }
+    ss = wave_sum(ss);
+    mx = wave_max(mx);
+    if (lane == 0) {
+        redf[0][wave] = mx;
+        redf[1][wave] = ss;
+    }
+    __syncthreads();
+    float m = redf[0][0], tot = redf[1][0];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) {
+        m = fmaxf(m, redf[0][w]);
+        tot += redf[1][w];
+    }
+    int ex = 0;
+    (void)frexpf(m * (1.0f / 127.0f), &ex);  // m/127 < 2^ex; m = 0 → ex = 0
+    const float S = m > 0.0f ? ldexpf(1.0f, ex) : 1.0f;
+    int sd[3] = {0, 0, 0};
+#pragma unroll
+    for (int i = 0; i < PER_T; ++i) {
+        const int c = cb + i;
+        const float t = ldexpf(y[i], -ex);  // exact
+        const float a = rintf(t);
+        const float t1 = (t - a) * 128.0f;  // exact: |t − a| ≤ 1/2
+        const float b = rintf(t1);
+        const int d0 = (int)a, d1 = (int)b, d2 = (int)rintf((t1 - b) * 128.0f);
+        p.planes[head_plane_off<QT, NS>(c, 0, v)] = (int8_t)d0;
+        p.planes[head_plane_off<QT, NS>(c, 1, v)] = (int8_t)d1;
+        p.planes[head_plane_off<QT, NS>(c, 2, v)] = (int8_t)d2;
+        sd[0] += d0;
+        sd[1] += d1;
+        sd[2] += d2;
+    }
+#pragma unroll
+    for (int pl = 0; pl < 3; ++pl) {
+        const int s = (int)wave_sum((float)sd[pl]);  // |Σ| ≤ 512·127: exact in f32
+        if (lane == 0) redi[pl][wave] = s;
+    }
+    __syncthreads();
+    if (threadIdx.x < 3) {
+        const int pl = threadIdx.x;
+        p.vbias[v * 3 + pl] = IB * (redi[pl][0] + redi[pl][1] + redi[pl][2] + redi[pl][3]);
+    }
+    if (threadIdx.x == 3) p.vscale[v] = norm ? S * fast_rsqrt_ref(tot / (float)COLS + p.eps) : S;
+}
+
+struct HeadWideParams {
+    DevMat m;
+    int rows;
+    int nvec;              // 1..16; B columns of other vectors are never read into C
+    const int8_t *planes;  // k_head_digits' output
+    const float *vscale;
+    const int *vbias;
+    float *out;            // optional: scores of vector v at out + v·out_stride
+    int out_stride;
+    int out_vec4;          // out 16-byte aligned, out_stride % 4 == 0, rows % 16 == 0
+    StepState *st[kHeadWideVec];  // argmax slots of vector v (null: no argmax)
+};
+
+template <int QT, int NS>
+__global__ void __launch_bounds__(kThreads, 2) k_head_wide(HeadWideParams p) {
+    static_assert(QT == QT_Q4 || QT == QT_Q8, "codes in 16-byte pieces of 16 or 32 columns");
+    using SH = HeadWideShape<QT, NS>;
+    constexpr int LINES = SH::LINES, R = SH::R, CP = SH::CP, SPL = SH::SPL;
+    constexpr int NV = kHeadWideVec;
+    static_assert(R >= 1 && LINES >= 1, "rows of whole 128-byte lines");
+    static_assert(SH::PLANE_BYTES % (16 * NV) == 0, "planes in 16-vector groups of 16 bytes");
+    __shared__ __attribute__((aligned(16))) int8_t xdig[SH::PLANE_BYTES];
+    __shared__ unsigned long long kred[NV][kWaves];
+    asm volatile("" ::"s"(p.m.data), "s"(p.m.scale), "s"(p.planes), "s"(p.vscale), "s"(p.vbias), "s"(p.out),
+                 "s"(p.rows), "s"(p.m.row_bytes), "s"(p.out_stride), "s"(p.nvec), "s"(p.out_vec4));
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lr = lane & 15, lg = lane >> 4;
+    const int rows = p.rows;
+    const int nvec = p.nvec;
+    const int r0 = (blockIdx.x * kWaves + wave) * 16 * R;  // this wave's first row
+
+    // 1. the live vectors' digit pieces (16 bytes each), requested first so
+    // that filling LDS waits for them alone
+    constexpr int GROUPS = SH::PLANE_BYTES / (16 * NV);  // (step, plane, lane group) groups
+    constexpr int MAXK = (GROUPS * NV + kThreads - 1) / kThreads;
+    const int npieces = GROUPS * nvec;
+    v4i piece[MAXK];
+#pragma unroll
+    for (int k = 0; k < MAXK; ++k) {
+        const int id = (int)threadIdx.x + k * kThreads;
+        if (id < npieces) {
+            const int off = (id / nvec) * 256 + (id % nvec) * 16;
+            piece[k] = *reinterpret_cast<const v4i *>(p.planes + off);
+        }
+    }
+    asm volatile("" ::: "memory");  // the weight requests stay behind the pieces
+
+    // 2. every weight byte of the wave's rows (past the end: the last row,
+    // loaded and never scored), in the order the MFMAs consume them.  A load
+    // instruction reads 8 rows × one 128-byte line: lane L takes the 16
+    // bytes at 16·(L/8) of row 8·hf + L%8 of its block (half hf), so each
+    // piece k = L/8 of a line holds CP codes.
+    typedef unsigned u4v __attribute__((ext_vector_type(4)));
+    u4v raw[R][2][LINES];
+    const uint8_t *wrow[R][2];
+#pragma unroll
+    for (int rb = 0; rb < R; ++rb)
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf)
+            wrow[rb][hf] = p.m.data + (size_t)min(r0 + 16 * rb + 8 * hf + (lane & 7), rows - 1) * p.m.row_bytes +
+                           16 * (lane >> 3);
+#pragma unroll
+    for (int ln = 0; ln < LINES; ++ln)
+#pragma unroll
+        for (int rb = 0; rb < R; ++rb)
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf)
+                raw[rb][hf][ln] = __builtin_nontemporal_load(reinterpret_cast<const u4v *>(wrow[rb][hf] + 128 * ln));
+    // LDS gets the pieces; every thread then passes the barrier
+#pragma unroll
+    for (int k = 0; k < MAXK; ++k) {
+        const int id = (int)threadIdx.x + k * kThreads;
+        if (id < npieces) {
+            const int off = (id / nvec) * 256 + (id % nvec) * 16;
+            *reinterpret_cast<v4i *>(xdig + off) = piece[k];
+        }
+    }
+    float rsc[R][4];  // row scales, first used after the MFMAs
+#pragma unroll
+    for (int rb = 0; rb < R; ++rb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) rsc[rb][i] = p.m.scale[min(r0 + 16 * rb + 4 * lg + i, rows - 1)];
+    __syncthreads();
+
+    // 3. the MFMAs.  The A operand wants lane L = (lr, lg) to hold row lr's
+    // K slice lg.  Of a line, the even pieces 2g of rows 0..7 sit in lanes
+    // with L%16 < 8 of half 0, those of rows 8..15 in lanes L ^ 8 of half 1
+    // (one DPP row rotate away); odd pieces 2g + 1 the other way round.  So
+    // set par (0: even, 1: odd) is own data where bit 3 of L equals par and
+    // the rotated other half elsewhere, and K slice lg of set par is piece
+    // 2·lg + par: columns 8·CP·ln + 2·CP·lg + CP·par + 16·h for step h.
+    // B column lr = vector lr.
+    v4i acc[R][3];
+#pragma unroll
+    for (int rb = 0; rb < R; ++rb)
+#pragma unroll
+        for (int pl = 0; pl < 3; ++pl) acc[rb][pl] = v4i{0, 0, 0, 0};
+    const int bit3 = (lane >> 3) & 1;
+#pragma unroll
+    for (int ln = 0; ln < LINES; ++ln)
+#pragma unroll
+        for (int par = 0; par < 2; ++par) {
+            u4v aset[R];
+#pragma unroll
+            for (int rb = 0; rb < R; ++rb) {
+                const u4v own = raw[rb][par][ln];
+                const u4v far = raw[rb][1 - par][ln];
+#pragma unroll
+                for (int w = 0; w < 4; ++w) {
+                    const unsigned rot = (unsigned)__builtin_amdgcn_update_dpp(0, (int)far[w], 0x128, 0xF, 0xF, false);
+                    aset[rb][w] = bit3 == par ? own[w] : rot;
+                }
+            }
+#pragma unroll
+            for (int h = 0; h < SPL; ++h) {
+                const int st = (ln * 2 + par) * SPL + h;
+                v4i b[3];  // lane (lr, lg): vector lr's K slice lg, 16 consecutive bytes per lane
+#pragma unroll
+                for (int pl = 0; pl < 3; ++pl)
+                    b[pl] = *reinterpret_cast<const v4i *>(xdig + (st * 3 + pl) * 1024 + 16 * lane);
+#pragma unroll
+                for (int rb = 0; rb < R; ++rb) {
+                    RawCodes<QT> rc;
+                    if constexpr (QT == QT_Q4) {
+                        rc.d[0] = aset[rb][2 * h];
+                        rc.d[1] = aset[rb][2 * h + 1];
+                    } else {
+#pragma unroll
+                        for (int w = 0; w < 4; ++w) rc.d[w] = aset[rb][w];
+                    }
+                    const v4i a = unpack_codes16<QT>(rc);
+#pragma unroll
+                    for (int pl = 0; pl < 3; ++pl)
+                        acc[rb][pl] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b[pl], acc[rb][pl], 0, 0, 0);
+                }
+            }
+        }
+
+    // 4. lane (lr, lg) holds C[4lg + i][lr]: rows r0 + 16rb + 4lg + i of
+    // vector lr.  Scores as k_head_mfma forms them.
+    const int v = lr;
+    const bool live = v < nvec;
+    int b0 = 0, b1 = 0, b2 = 0;
+    float my_sx = 1.0f;
+    if (live) {
+        b0 = p.vbias[v * 3];
+        b1 = p.vbias[v * 3 + 1];
+        b2 = p.vbias[v * 3 + 2];
+        my_sx = p.vscale[v];
+    }
+    unsigned long long key = 0ull;
+#pragma unroll
+    for (int rb = 0; rb < R; ++rb) {
+        const int rr = r0 + 16 * rb + 4 * lg;
+        float sc[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            // |Σ u·d| < 2^24 per plane (cols ≤ 2048): exact converts
+            const float f0 = (float)(acc[rb][0][i] - b0);
+            const float f1 = (float)(acc[rb][1][i] - b1);
+            const float f2 = (float)(acc[rb][2][i] - b2);
+            sc[i] = fmaf(f2, 1.0f / 16384.0f, fmaf(f1, 1.0f / 128.0f, f0)) * my_sx * rsc[rb][i];
+            if (live && rr + i < rows) {
+                const unsigned long long k = argmax_key(sc[i], rr + i);
+                key = k > key ? k : key;
+            }
+        }
+        if (p.out && live) {
+            float *o = p.out + (size_t)v * p.out_stride + rr;
+            if (p.out_vec4) {
+                if (rr < rows) *reinterpret_cast<float4 *>(o) = make_float4(sc[0], sc[1], sc[2], sc[3]);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    if (rr + i < rows) o[i] = sc[i];
+            }
+        }
+    }
+    // the best key of vector lr over the four lane groups, then the waves
+    {
+        const unsigned long long o16 = shfl_xor_u64(key, 16);
+        key = o16 > key ? o16 : key;
+        const unsigned long long o32 = shfl_xor_u64(key, 32);
+        key = o32 > key ? o32 : key;
+    }
+    if (lg == 0) kred[lr][wave] = key;
+    __syncthreads();
+    if ((int)threadIdx.x < nvec) {
+        const int vv = threadIdx.x;
+        unsigned long long m = kred[vv][0];
+#pragma unroll
+        for (int w = 1; w < kWaves; ++w) m = kred[vv][w] > m ? kred[vv][w] : m;
+        StepState *st = p.st[0];
+#pragma unroll
+        for (int u = 1; u < NV; ++u) st = vv == u ? p.st[u] : st;
+        if (m && st) atomicMax(&st->argmax_slot[(blockIdx.x % kArgSlots) * kSlotPitch], m);
     }
 }
 

@@ -186,6 +186,13 @@ int seq_idle(const pocr_seq *s, const char *op);
 // sampling head (logits, top-k, one draw into argmax slot 0) when the
 // sequence samples
 int enqueue_lm_head(pocr_seq *s, const float *x, bool want_logits);
+// the matrix-core head for 2 to 16 vectors (head.hpp, k_head_wide)
+constexpr int kHeadWideMinRows = 16384;  // plain scores of fewer rows stay on the GEMV
+bool head_wide_ok(const pocr_weight *w);
+size_t head_wide_plane_bytes(const pocr_weight *w);
+int launch_head_wide(hipStream_t s, const pocr_weight *w, const float *x, int x_stride, int nvec, const float *norm_w,
+                     float eps, float *out, int out_stride, StepState *const *st, int8_t *planes, float *vscale,
+                     int *vbias);
 // batched building blocks (prefill.hip): digit planes of n rows, and the
 // MFMA GEMM over them (npad = n rounded up to 32 tokens)
 struct DigitizeParams;

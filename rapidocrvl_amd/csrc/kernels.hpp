@@ -427,6 +427,13 @@ __device__ __forceinline__ void reduce_scatter(float (&v)[CAP][NM], int lane) {
 
 // Sum over the 64 lanes of a wave, the same value in every lane (DPP within
 // rows of 16, then swizzle and bpermute across them).
+// 64-bit lane exchange
+__device__ __forceinline__ unsigned long long shfl_xor_u64(unsigned long long v, int m) {
+    const unsigned lo = __shfl_xor((unsigned)v, m, 64);
+    const unsigned hi = __shfl_xor((unsigned)(v >> 32), m, 64);
+    return ((unsigned long long)hi << 32) | lo;
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
     v += xchg<XQ1>(v);
     v += xchg<XQ2>(v);

@@ -428,6 +428,81 @@ static int launch_head(hipStream_t s, const void *fn, const GemvParams &p, int p
     return POCR_OK;
 }
 
+// The head for 2 to 16 vectors (head.hpp: k_head_digits, then k_head_wide):
+// Q4 or Q8 rows of 1024 or 2048 columns on 16-byte boundaries.
+struct HeadWidePlan {
+    const void *digits = nullptr, *head = nullptr;
+    int rows_per_wg = 0, plane_bytes = 0;
+};
+
+template <int QT, int NS>
+static HeadWidePlan head_wide_plan() {
+    HeadWidePlan h;
+    h.digits = reinterpret_cast<const void *>(&k_head_digits<QT, NS>);
+    h.head = reinterpret_cast<const void *>(&k_head_wide<QT, NS>);
+    h.rows_per_wg = HeadWideShape<QT, NS>::ROWS_PER_WG;
+    h.plane_bytes = HeadWideShape<QT, NS>::PLANE_BYTES;
+    return h;
+}
+
+static bool plan_head_wide(const DevMat &m, HeadWidePlan *h) {
+    if (m.cols != 1024 && m.cols != 2048) return false;
+    if (((uintptr_t)m.data) % 16 != 0 || m.row_bytes % 16 != 0) return false;
+    const bool ns4 = m.cols == 1024;
+    if (m.qtype == POCR_Q4) *h = ns4 ? head_wide_plan<QT_Q4, 4>() : head_wide_plan<QT_Q4, 8>();
+    else if (m.qtype == POCR_Q8) *h = ns4 ? head_wide_plan<QT_Q8, 4>() : head_wide_plan<QT_Q8, 8>();
+    else return false;
+    return true;
+}
+
+bool pocr::head_wide_ok(const pocr_weight *w) {
+    HeadWidePlan h;
+    return plan_head_wide(dev_mat(w), &h);
+}
+
+size_t pocr::head_wide_plane_bytes(const pocr_weight *w) {
+    HeadWidePlan h;
+    return plan_head_wide(dev_mat(w), &h) ? (size_t)h.plane_bytes : 0;
+}
+
+// nvec (≤ 16) vectors at x + v·x_stride against w: optional scores at out +
+// v·out_stride, optional argmax into st[v] (null entries: none).  planes
+// (head_wide_plane_bytes), vscale (16 floats) and vbias (48 ints) are the
+// caller's device scratch.
+int pocr::launch_head_wide(hipStream_t s, const pocr_weight *w, const float *x, int x_stride, int nvec,
+                           const float *norm_w, float eps, float *out, int out_stride, StepState *const *st,
+                           int8_t *planes, float *vscale, int *vbias) {
+    if (nvec < 1 || nvec > kHeadWideVec) return fail(POCR_ERR_ARG, "head: %d vectors", nvec);
+    const DevMat m = dev_mat(w);
+    HeadWidePlan plan;
+    if (!plan_head_wide(m, &plan)) return fail(POCR_ERR_UNSUPPORTED, "head: %d columns of qtype %d", m.cols, m.qtype);
+    HeadDigitParams d{};
+    d.x = x;
+    d.x_stride = x_stride;
+    d.norm_w = norm_w;
+    d.eps = eps;
+    d.planes = planes;
+    d.vscale = vscale;
+    d.vbias = vbias;
+    void *dargs[] = {&d};
+    HIP_TRY(hipLaunchKernel(plan.digits, dim3(nvec), dim3(kThreads), dargs, 0, s));
+    HeadWideParams h{};
+    h.m = m;
+    h.rows = m.rows;
+    h.nvec = nvec;
+    h.planes = planes;
+    h.vscale = vscale;
+    h.vbias = vbias;
+    h.out = out;
+    h.out_stride = out_stride;
+    h.out_vec4 = out && ((uintptr_t)out % 16 == 0) && out_stride % 4 == 0 && h.rows % 16 == 0;
+    for (int v = 0; v < kHeadWideVec; ++v) h.st[v] = (st && v < nvec) ? st[v] : nullptr;
+    void *args[] = {&h};
+    HIP_TRY(hipLaunchKernel(plan.head, dim3((h.rows + plan.rows_per_wg - 1) / plan.rows_per_wg), dim3(kThreads), args,
+                            0, s));
+    return POCR_OK;
+}
+
 int pocr::gemv_launch(hipStream_t s, GemvParams p, int nmat, int pro, int epi, int max_grid, int nv,
                       const GemvNV *q) {
     if (nv > 1 && !q) return fail(POCR_ERR_ARG, "gemv: %d vectors need their strides", nv);
@@ -467,6 +542,27 @@ static int sync(hipStream_t s) {
 // digit-plane MFMA GEMM; shapes the vector kernel does not take fall back too.
 static int matvec_rows(pocr_ctx *ctx, const pocr_weight *w, const float *x, int m, float *out) {
     hipStream_t s = ctx->stream;
+    // LM-head-sized matrices: up to 16 rows of x per weight pass on the matrix
+    // cores (one power-of-two digit scale per row of x)
+    if (m > 1 && w->rows >= kHeadWideMinRows && head_wide_ok(w)) {
+        RC(ctx->gxd.ensure(head_wide_plane_bytes(w)));
+        RC(ctx->gxs.ensure(kHeadWideVec * sizeof(float)));
+        RC(ctx->gxb.ensure(3 * kHeadWideVec * sizeof(int)));
+        for (int r0 = 0; r0 < m; r0 += kHeadWideVec) {
+            const int nv = std::min(kHeadWideVec, m - r0);
+            if (nv > 1) {
+                RC(launch_head_wide(s, w, x + (size_t)r0 * w->cols, w->cols, nv, nullptr, 0.0f,
+                                    out + (size_t)r0 * w->rows, w->rows, nullptr, ctx->gxd.as<int8_t>(),
+                                    ctx->gxs.as<float>(), ctx->gxb.as<int>()));
+                continue;
+            }
+            GemvParams p = gemv_params_1(w);
+            p.x = x + (size_t)r0 * w->cols;
+            p.out = out + (size_t)r0 * w->rows;
+            RC(gemv_launch(s, p, 1, PRO_COPY, EPI_PLAIN, kBigGrid));
+        }
+        return POCR_OK;
+    }
     if (m <= 4) {
         for (int r0 = 0; r0 < m;) {
             const int nv = m - r0 >= 4 ? 4 : (m - r0 >= 2 ? 2 : 1);
@@ -2512,7 +2608,12 @@ int enqueue_batch_step(DecodeBatch &b) {
     // otherwise one GEMV pass per 4 of them (the last pass padded to 1, 2 or 4
     // vectors).  Sampling sequences: each its own logits, top-k and draw (the
     // draw lands in argmax slot 0, where the next step reads it).
-    if (wide && b.ng > kMaxNV && b.logits) {
+    if (wide && b.ng > kMaxNV && head_wide_ok(m->lm)) {
+        // one launch for every greedy sequence (rows 0..ng-1 of v)
+        StepState *sts[kHeadWideVec];
+        for (int i = 0; i < b.ng; ++i) sts[i] = b.seq[i]->st;
+        RC(launch_head_wide(st, m->lm, b.v, H, b.ng, m->final_norm, eps, nullptr, 0, sts, b.xd, b.xs, b.xb));
+    } else if (wide && b.ng > kMaxNV && b.logits) {
         const int V = c.vocab;
         RC(batch_digitize(b, m->lm->qtype, b.v, H, m->final_norm));
         GemmParams lp = batch_gemm(b, m->lm, H);
@@ -2525,7 +2626,8 @@ int enqueue_batch_step(DecodeBatch &b) {
                            kSlice, b.rst);
         HIP_TRY(hipGetLastError());
     }
-    for (int base = 0; base < b.ng && !(wide && b.ng > kMaxNV && b.logits); base += kMaxNV) {
+    for (int base = 0; base < b.ng && !(wide && b.ng > kMaxNV && (b.logits || head_wide_ok(m->lm)));
+         base += kMaxNV) {
         const int left = b.ng - base;
         const int nv = left == 1 ? 1 : (left == 2 ? 2 : 4);
         GemvParams lm = gemv_params_1(m->lm);

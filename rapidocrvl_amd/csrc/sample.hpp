@@ -265,13 +265,6 @@ static __device__ int draw_candidate(const float *sc, const float *w, int n, dou
     return n - 1;
 }
 
-// 64-bit lane exchange
-__device__ __forceinline__ unsigned long long shfl_xor_u64(unsigned long long v, int m) {
-    const unsigned lo = __shfl_xor((unsigned)v, m, 64);
-    const unsigned hi = __shfl_xor((unsigned)(v >> 32), m, 64);
-    return ((unsigned long long)hi << 32) | lo;
-}
-
 // The k best of the partials → ss->ids/scores (sorted); with `sample`, one
 // draw (k ≥ 2) into ss->token, ss->rng and argmax slot 0 of st (if any).
 static __global__ void __launch_bounds__(kTopKThreads) k_topk_final(const unsigned long long *part, int nparts, int k,

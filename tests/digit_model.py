@@ -81,6 +81,24 @@ def head_scores(codes, scales, x, rows_per_block=8192):
     return out * sc, mag * sc
 
 
+def head_scores_rows(codes, scales, X):
+    """head_scores for every row of X at once: ([m, rows], [m, rows]).  The
+    integer plane sums are formed in f32, exact while |Σ| < 2^24 (codes ≤ 128
+    in magnitude, digits ≤ 127, 1024 columns)."""
+    X = np.asarray(X, np.float32)
+    m, cols = X.shape
+    assert cols <= 1024
+    S = np.zeros(m)
+    D = np.zeros((cols, 3 * m), np.float32)
+    for i in range(m):
+        S[i], d = planes_whole(X[i])
+        D[:, 3 * i:3 * i + 3] = d.T
+    A = (codes.astype(np.float32) @ D).astype(np.float64).reshape(codes.shape[0], m, 3)
+    w = np.array([1.0, 1.0 / 128, 1.0 / 16384])
+    sc = np.asarray(scales, np.float64)[None, :] * S[:, None]
+    return (A @ w).T * sc, (np.abs(A) @ w).T * sc
+
+
 def scores(qtype, codes, scales, xv, rows_per_block=4096):
     """scale·(codes · xv) in float64 (xv: x or a digitized x)."""
     out = np.zeros(codes.shape[0])

@@ -152,6 +152,35 @@ def test_matvec_argmax_planted_near_tie(ctx, orc, qtype):
     assert abs(score - dig[0]) <= F32_STEPS[qtype] * mag[0]
 
 
+@pytest.mark.parametrize("qtype", [Q8, Q4], ids=["q8", "q4"])
+@pytest.mark.parametrize("m", [2, 3, 5, 16, 17])
+def test_lm_head_rows_on_matrix_cores(ctx, orc, qtype, m):
+    """M rows of x against the 103424×1024 LM head: up to 16 rows per weight
+    pass on the matrix cores.  Each row's scores are what the MFMA greedy head
+    computes for that row alone (one power-of-two digit scale per row, exact
+    plane sums: tests/digit_model.py) up to the f32 steps, within the f32
+    matvec tolerance of the oracle, and each row's best score and row are
+    pocr_matvec_argmax's for that row, to the bit.  A 17th row goes through
+    the single-vector GEMV."""
+    rng = np.random.default_rng(40 + m)
+    q = _qmat(rng, 103424, 1024, qtype)
+    w = ctx.upload(q)
+    codes = lib.unpack_rows(qtype, q.packed, q.cols)
+    x = rng.standard_normal((m, 1024)).astype(np.float32)
+    x[1] *= np.float32(1e-3)  # rows of different magnitude: each its own digit scale
+    got = ctx.matvec(w, x)
+    nw = min(m, 16)
+    dig, mag = dm.head_scores_rows(codes, q.scales, x[:nw])
+    for i in range(m):
+        _close(got[i], orc.matvec(qtype, q.scales, q.packed, x[i]))
+        if i >= 16:
+            continue
+        assert np.all(np.abs(got[i] - dig[i]) <= F32_STEPS[qtype] * mag[i]), i
+        idx, score = ctx.matvec_argmax(w, x[i])
+        assert int(np.argmax(got[i])) == idx, i
+        assert got[i][idx] == np.float32(score), i
+
+
 def test_argmax_ties_pick_lowest_index(ctx):
     # identical rows give bit-identical scores: ties → lowest index
     w = np.zeros((64, 32), np.float32)
