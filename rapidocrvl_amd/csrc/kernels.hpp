@@ -9,6 +9,8 @@
 // fp32-activation semantics of MatVecQ{8,4,6} (internal/tensor/quant.go:443-561).
 #pragma once
 
+#include <cstddef>
+
 #include <hip/hip_runtime.h>
 #include <type_traits>
 #include <stdint.h>
@@ -60,6 +62,9 @@ struct StepState {
     // the max over the slots (0 = no candidate).
     alignas(128) unsigned long long argmax_slot[kArgSlots * kSlotPitch];
 };
+// kernels read len, clen, cap and err as one 16-byte load
+static_assert(offsetof(StepState, len) == 0 && offsetof(StepState, clen) == 4 && offsetof(StepState, err) == 12,
+              "step state header layout");
 
 // ---------------------------------------------------------------------------
 // reference numerics (internal/tensor/ops.go)
@@ -1340,13 +1345,15 @@ __device__ __forceinline__ void f4_to(float (&d)[8], const float4 &a, const floa
     d[4] = b.x; d[5] = b.y; d[6] = b.z; d[7] = b.w;
 }
 
-// Kernel arguments pinned in SGPRs: one batch of scalar loads at entry (the
-// in/out asm operands stop the compiler from reloading a field from the
-// argument segment at its first use, a round trip each).
-__device__ __forceinline__ void pin_args(AttnParams &p) {
-    asm volatile("" : "+s"(p.q), "+s"(p.k_new), "+s"(p.v_new), "+s"(p.kc), "+s"(p.vc), "+s"(p.st), "+s"(p.part),
-                 "+s"(p.head_out));
-    asm volatile("" : "+s"(p.cos_t), "+s"(p.sin_t), "+s"(p.heads), "+s"(p.kvh), "+s"(p.nsplit), "+s"(p.rows_cap));
+// Kernel arguments made live at entry: one batch of scalar loads instead of
+// one argument round trip at each field's first use.  Input operands only:
+// an in/out operand would hide the pointers' provenance, turning every load
+// through them into a flat load (tracked by the 4-bit LGKM counter too, so
+// the loads would drain in rounds of 15).
+__device__ __forceinline__ void pin_args(const AttnParams &p) {
+    asm volatile("" ::"s"(p.q), "s"(p.k_new), "s"(p.v_new), "s"(p.kc), "s"(p.vc), "s"(p.st), "s"(p.part),
+                 "s"(p.head_out));
+    asm volatile("" ::"s"(p.cos_t), "s"(p.sin_t), "s"(p.heads), "s"(p.kvh), "s"(p.nsplit), "s"(p.rows_cap));
     asm volatile("" ::"s"(p.len), "s"(p.has_rope), "s"(p.chunk));
 }
 
@@ -1380,8 +1387,15 @@ __device__ __forceinline__ void attn_decode_body(AttnParams p) {
     const int wr0 = t0 + RPW * wave;  // first row of this wave
     const int tmax = p.rows_cap - 1;
 
-    // ---- 1. requests.  Rows past the capacity are clamped to the last row
-    // (loaded, masked below); every lane issues the same loads.
+    // ---- 1. requests.  The step state's fields first (len, clen, cap, err
+    // are its first 16 bytes): they are then the oldest loads in flight, so
+    // waiting for them later waits for nothing else.  Without a step state
+    // the loads read q (a readable stand-in, replaced at use).  Rows past the
+    // capacity are clamped to the last row (loaded, masked below); every lane
+    // issues the same loads.
+    int4 st4 = *reinterpret_cast<const int4 *>(st ? reinterpret_cast<const float *>(st) : p.q);
+    int st_rope = *(st ? &st->has_rope : reinterpret_cast<const int *>(p.q));
+    asm volatile("" ::: "memory");  // these two loads go out first
     float4 ka[NJ][2];  // K, score layout: pass j → row wr0 + 4j + rg, dims 8·l16..
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
@@ -1396,48 +1410,59 @@ __device__ __forceinline__ void attn_decode_body(AttnParams p) {
         const int t = min(wr0 + i, tmax);
         va[i] = *reinterpret_cast<const float2 *>(p.vc + (size_t)t * kvd + g * kHD + 2 * lane);
     }
+    // Branch-free requests (a load inside a branch makes the register merge
+    // after it wait for that load): heads past the group load the group's
+    // last head again (their scores are never used), and without a RoPE
+    // table or a new row the loads read q instead (replaced below / unused).
     float4 qr[kMaxGroup][2];
 #pragma unroll
     for (int h = 0; h < kMaxGroup; ++h) {
-        if (h < group) {  // uniform
-            const float4 *src = reinterpret_cast<const float4 *>(p.q + (size_t)(g * group + h) * kHD + 8 * l16);
-            qr[h][0] = src[0];
-            qr[h][1] = src[1];
-        } else {
-            qr[h][0] = qr[h][1] = make_float4(0.f, 0.f, 0.f, 0.f);
-        }
+        const int hh = min(h, group - 1);
+        const float4 *src = reinterpret_cast<const float4 *>(p.q + (size_t)(g * group + hh) * kHD + 8 * l16);
+        qr[h][0] = src[0];
+        qr[h][1] = src[1];
     }
     float cs[8], sn[8];
-    if (cos_t) {
+    {
         const int tb = (8 * l16) & (kHD / 2 - 1);
-        const float4 *cp = reinterpret_cast<const float4 *>(cos_t + tb);
-        const float4 *sp = reinterpret_cast<const float4 *>(sin_t + tb);
+        const float4 *cp = reinterpret_cast<const float4 *>((cos_t ? cos_t : p.q) + tb);
+        const float4 *sp = reinterpret_cast<const float4 *>((cos_t ? sin_t : p.q) + tb);
         f4_to(cs, cp[0], cp[1]);
         f4_to(sn, sp[0], sp[1]);
-    } else {
+    }
+    float4 kn[2];
+    float2 vn;
+    {
+        const float *kb = p.k_new ? p.k_new : p.q;  // q: a readable stand-in, never used
+        const float *vb = p.k_new ? p.v_new : p.q;
+        const float4 *kp = reinterpret_cast<const float4 *>(kb + (size_t)g * kHD + 8 * l16);
+        kn[0] = kp[0];
+        kn[1] = kp[1];
+        vn = *reinterpret_cast<const float2 *>(vb + (size_t)g * kHD + 2 * lane);
+    }
+
+    // every request above is issued before the step state is examined: the
+    // memory clobber keeps the loads above this point (the exits below would
+    // otherwise let the compiler sink them past), and passing the step
+    // state's values through it keeps their first use (and the wait for
+    // them) below it
+    asm volatile("" : "+v"(st4.x), "+v"(st4.y), "+v"(st4.z), "+v"(st4.w), "+v"(st_rope)::"memory");
+
+    // ---- 2. step state
+    if (st && st4.w) return;  // err: a failed step appends nothing
+    const int L = st ? st4.x : p.len;
+    const int newest = st ? st4.y : -1;  // row appended by this step (clen)
+    const int rope = st ? st_rope : p.has_rope;
+    const int t1 = min(L, t0 + chunk);
+    if (t1 <= t0) return;  // split past the step's rows: the merge skips it
+    const bool upper = l16 >= 8;
+    if (!cos_t) {  // no RoPE table: the identity rotation
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
             cs[e] = 1.0f;
             sn[e] = 0.0f;
         }
     }
-    float4 kn[2] = {make_float4(0.f, 0.f, 0.f, 0.f), make_float4(0.f, 0.f, 0.f, 0.f)};
-    float2 vn = make_float2(0.f, 0.f);
-    if (p.k_new) {
-        const float4 *kp = reinterpret_cast<const float4 *>(p.k_new + (size_t)g * kHD + 8 * l16);
-        kn[0] = kp[0];
-        kn[1] = kp[1];
-        vn = *reinterpret_cast<const float2 *>(p.v_new + (size_t)g * kHD + 2 * lane);
-    }
-
-    // ---- 2. step state
-    if (st && st->err) return;  // a failed step appends nothing
-    const int L = st ? st->len : p.len;
-    const int newest = st ? st->clen : -1;  // row appended by this step
-    const int rope = st ? st->has_rope : p.has_rope;
-    const int t1 = min(L, t0 + chunk);
-    if (t1 <= t0) return;  // split past the step's rows: the merge skips it
-    const bool upper = l16 >= 8;
 
     // ---- 3. rotated q; the owner wave rotates and appends the newest row
     float q[kMaxGroup][8];
@@ -1594,18 +1619,21 @@ __device__ __forceinline__ void attn_merge_body(AttnParams p) {
     const float *base = p.part + ((size_t)g * p.nsplit * kMaxGroup + h) * kRec;
     constexpr size_t RS = (size_t)kMaxGroup * kRec;  // split stride
     auto acc = [&](int sidx) { return *reinterpret_cast<const float4 *>(base + sidx * RS + 4 + 4 * j); };
+    // the step state's header first (len, clen, cap, err; without a step
+    // state a readable stand-in), so waiting for it waits for nothing else
+    int4 st4 = *reinterpret_cast<const int4 *>(p.st ? reinterpret_cast<const float *>(p.st) : p.part);
+    // then (max, Σexp) of splits lane, lane + 64 (every wave loads them, only
+    // wave 0 uses them: no load inside a branch), then the acc vectors
+    const float2 ml = *reinterpret_cast<const float2 *>(base + min(lane, p.nsplit - 1) * RS);
+    asm volatile("" ::: "memory");
     constexpr int B = 8;  // acc vectors requested up front (splits sg + 8b)
     float4 av[B];
 #pragma unroll
     for (int b = 0; b < B; ++b) av[b] = acc(min(sg + kMergeGroups * b, p.nsplit - 1));
-    float m0 = 0.0f, l0 = 0.0f;
-    if (wave0) {
-        const float2 ml = *reinterpret_cast<const float2 *>(base + min(lane, p.nsplit - 1) * RS);
-        m0 = ml.x;
-        l0 = ml.y;
-    }
-    if (p.st && p.st->err) return;
-    const int L = p.st ? p.st->len : p.len;
+    const float m0 = ml.x, l0 = ml.y;
+    asm volatile("" : "+v"(st4.x), "+v"(st4.y), "+v"(st4.z), "+v"(st4.w)::"memory");  // requests above, uses below
+    if (p.st && st4.w) return;  // err
+    const int L = p.st ? st4.x : p.len;
     const int used = min(p.nsplit, (L + p.chunk - 1) / p.chunk);  // ≥ 1 for L ≥ 1
     if (wave0) {  // split weights, lane s + 64k ↔ split
         float M = lane < used ? m0 : -INFINITY;
