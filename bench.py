@@ -488,6 +488,146 @@ def cpu_baseline(cfg, weights, gpu_seq, first_tok, first_pos, gpu_tokens, n_pref
                                "tokens_match_gpu": toksv[: nv + 1] == list(gpu_tokens[: nv + 1])}}
 
 
+GEMV_SHAPES = {"gate_up": (3072, 1024), "down": (1024, 3072), "qkv": (2560, 1024), "lm_head": (103424, 1024)}
+
+
+def cpu_gemv_sweep(rng, budget_s=0.2):
+    """The GEMV sweep on the CPU: the oracle's matvec (plain-mode MatVecQ*,
+    quant.go:443-561) at the sweep's shapes × Q8/Q6/Q4, one vector per call
+    (M rows cost M calls on the CPU path); µs per call and GB/s of weight
+    bytes, each cell timed for about budget_s."""
+    import oracle
+    from rapidocrvl_amd import lib
+
+    threads = min(16, os.cpu_count() or 1)
+    oracle.set_threads(threads)
+    cells = {}
+    for qname, qtype in (("q8", lib.Q8), ("q6", lib.Q6), ("q4", lib.Q4)):
+        for sname, (rows, cols) in GEMV_SHAPES.items():
+            w = rng.standard_normal((rows, cols), dtype=np.float32) * np.float32(0.02)
+            q = lib.QMatrix.quantize(w, qtype)
+            x = rng.standard_normal(cols).astype(np.float32)
+            pm = oracle.Prepared(qtype, q.scales, q.packed, cols)  # unpacked once, as the model holds it
+            y = np.zeros(rows, np.float32)
+            pm.matvec(x, y)
+            n, t = 0, time.perf_counter()
+            while n < 2 or time.perf_counter() - t < budget_s:
+                pm.matvec(x, y)
+                n += 1
+            us = (time.perf_counter() - t) / n * 1e6
+            pm.close()
+            cells[f"{qname}_{sname}_m1"] = {"us": round(us, 1),
+                                            "GB/s": round((q.packed.nbytes + q.scales.nbytes) / us / 1e3, 2)}
+    return {"threads": threads, "kind": "port", "cells": cells,
+            "note": "M = 4 and 16 cost 4 and 16 calls of the m1 cell on the CPU path"}
+
+
+def cpu_attention_sweep(cfg, rng, budget_s=0.3):
+    """Decode attention on the CPU at L = 1k/4k/8k: the oracle's cache
+    attention (model.go:4623-5590: 16 q heads over 2 kv heads, head_dim 128,
+    FastExp softmax) over N(0,1) K/V, one layer per call."""
+    import oracle
+
+    threads = min(16, os.cpu_count() or 1)
+    oracle.set_threads(threads)
+    kvd = cfg.kv_heads * cfg.head_dim
+    out = {}
+    for L in (1024, 4096, 8192):
+        k = rng.standard_normal(L * kvd).astype(np.float32)
+        v = rng.standard_normal(L * kvd).astype(np.float32)
+        q = rng.standard_normal(cfg.heads * cfg.head_dim).astype(np.float32)
+        n, t = 0, time.perf_counter()
+        while n < 2 or time.perf_counter() - t < budget_s:
+            oracle.cache_attention(q, k, v, L, cfg.heads, cfg.kv_heads, cfg.head_dim)
+            n += 1
+        us = (time.perf_counter() - t) / n * 1e6
+        out[f"L{L}"] = {"us": round(us, 1), "GB/s": round(2 * L * kvd * 4 / us / 1e3, 2)}
+    return {"threads": threads, "kind": "port", "per_layer": out}
+
+
+def cpu_worker_main(args):
+    """One CPU decode worker of cpu_concurrent_workers (a child process: no
+    GPU use).  Loads the Q4 weights and the KV state the parent saved, waits
+    for the start file, decodes greedily for args.worker_seconds, prints one
+    JSON line."""
+    import oracle
+    from rapidocrvl_amd import synth
+    from rapidocrvl_amd.config import ERNIE_0P3B as cfg
+
+    d = args.cpu_worker
+    oracle.set_threads(args.worker_threads)
+    st = np.load(os.path.join(d, "state.npz"))
+    n_prefix, first_tok, first_pos = (int(v) for v in st["meta"])
+    weights = synth.make_weights(cfg, synth.lib.Q4, seed=0)
+    om = oracle.Model(cfg)
+    om.load_weights(weights)
+    s = om.seq(n_prefix + 1100)
+    for li in range(cfg.layers):
+        s.load(li, st[f"k{li}"], st[f"v{li}"], n_prefix)
+    open(os.path.join(d, f"ready{args.worker_id}"), "w").close()
+    while not os.path.exists(os.path.join(d, "go")):
+        time.sleep(0.01)
+    toks, n, t = [first_tok], 0, time.perf_counter()
+    while n < 1024 and (n < 2 or time.perf_counter() - t < args.worker_seconds):
+        p = first_pos + n
+        tok, _, _ = s.step(weights["embed"][toks[-1]], (p, p, p), want_logits=False)
+        toks.append(tok)
+        n += 1
+    dt = time.perf_counter() - t
+    print(json.dumps({"worker": args.worker_id, "steps": n, "s": dt, "tokens": toks[:9]}), flush=True)
+
+
+def cpu_concurrent_workers(cfg, gpu_seq, first_tok, first_pos, n_prefix, gpu_tokens, workers=4, seconds=8.0):
+    """Four single-sequence CPU decode workers at once, as the reference
+    server runs one GenerateWithOptions per acquired slot
+    (cmd/paddleocrvl-server/main.go:1106-1124): four child processes of the
+    oracle sharing the host's cores (each with cores/4 threads), each decoding
+    from the same 1,345-row Q4 KV state the GPU produced.  Aggregate tok/s over
+    the common decode window (the workers start together once all are
+    loaded)."""
+    import subprocess
+    import tempfile
+
+    threads = max(1, min(16, os.cpu_count() or 1) // workers)
+    with tempfile.TemporaryDirectory(dir="/tmp") as d:
+        arrs = {"meta": np.array([n_prefix, first_tok, first_pos], np.int64)}
+        for li in range(cfg.layers):
+            k, v = gpu_seq.read_kv(li)
+            arrs[f"k{li}"] = k[: n_prefix * cfg.kv_rows]
+            arrs[f"v{li}"] = v[: n_prefix * cfg.kv_rows]
+        np.savez(os.path.join(d, "state.npz"), **arrs)
+        env = dict(os.environ, OMP_NUM_THREADS=str(threads))
+        procs = [subprocess.Popen([sys.executable, os.path.abspath(__file__), "--cpu-worker", d,
+                                   "--worker-id", str(i), "--worker-threads", str(threads),
+                                   "--worker-seconds", str(seconds)],
+                                  stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True, env=env)
+                 for i in range(workers)]
+        t0 = time.time()
+        while not all(os.path.exists(os.path.join(d, f"ready{i}")) for i in range(workers)):
+            if any(p.poll() is not None for p in procs) or time.time() - t0 > 300:
+                for p in procs:
+                    p.kill()
+                raise RuntimeError("a CPU worker did not get ready: "
+                                   + " | ".join((p.stderr.read() or "")[-300:] for p in procs if p.poll() is not None))
+            time.sleep(0.05)
+        open(os.path.join(d, "go"), "w").close()
+        outs = []
+        for p in procs:
+            o, e = p.communicate(timeout=seconds + 120)
+            if p.returncode != 0:
+                raise RuntimeError(f"CPU worker failed: {e[-500:]}")
+            outs.append(json.loads(o.strip().splitlines()[-1]))
+    steps = sum(o["steps"] for o in outs)
+    window = max(o["s"] for o in outs)
+    match = all(o["tokens"] == list(gpu_tokens[: len(o["tokens"])]) for o in outs)
+    return {"value": round(steps / window, 2), "unit": "tok/s", "cores": threads * workers, "kind": "port",
+            "workers": workers, "threads_per_worker": threads,
+            "per_worker_tok_s": [round(o["steps"] / o["s"], 2) for o in outs],
+            "sample": f"{workers} oracle processes, each {threads} threads, decoding greedily for ≈{seconds:.0f} s "
+                      f"from the same 1345-token Q4 KV state",
+            "tokens_match_gpu": bool(match)}
+
+
 def host_cpu():
     try:
         with open("/proc/cpuinfo") as f:
@@ -544,7 +684,14 @@ def main():
     ap.add_argument("--serve-only", action="store_true", help="time only the 8-request serving comparison")
     ap.add_argument("--batch-tokens", type=int, default=1024, help="tokens per sequence of the batched decode")
     ap.add_argument("--batch-seqs", default="4,8,16", help="with --batch-only: batch sizes to time")
+    ap.add_argument("--cpu-worker", help=argparse.SUPPRESS)  # one process of cpu_concurrent_workers
+    ap.add_argument("--worker-id", type=int, default=0, help=argparse.SUPPRESS)
+    ap.add_argument("--worker-threads", type=int, default=4, help=argparse.SUPPRESS)
+    ap.add_argument("--worker-seconds", type=float, default=8.0, help=argparse.SUPPRESS)
     args = ap.parse_args()
+    if args.cpu_worker:  # a child of cpu_concurrent_workers: CPU only
+        cpu_worker_main(args)
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the decoder step runs on a single MI355X "
               "(multi-GPU sharding is a design note, not built)", file=sys.stderr)
@@ -626,6 +773,13 @@ def main():
     if not args.no_cpu:
         cpu = cpu_baseline(cfg, weights, seq, first_tok, first_pos, toks, n_prefix)
         log(f"[bench] cpu baseline {cpu}")
+        # the other configurations' CPU legs: GEMV sweep, decode attention,
+        # four concurrent single-sequence workers
+        cpu["per_config"] = {"gemv_sweep": cpu_gemv_sweep(np.random.default_rng(0)),
+                             "attention": cpu_attention_sweep(cfg, np.random.default_rng(1)),
+                             "concurrent_workers_q4": cpu_concurrent_workers(cfg, seq, first_tok, first_pos,
+                                                                             n_prefix, toks)}
+        log(f"[bench] cpu per-config baselines {cpu['per_config']}")
 
     extra = {}
     if not args.no_batch:

@@ -104,6 +104,10 @@ def lib():
         L.orc_pick_cumulative.argtypes = [_f32p, C.c_int, C.c_float]
         L.orc_sample_full.restype = C.c_int32
         L.orc_sample_full.argtypes = [_f32p, C.c_int, C.c_double, C.POINTER(C.c_uint64)]
+        L.orc_prepare.restype = C.c_void_p
+        L.orc_prepare.argtypes = [C.c_void_p]
+        L.orc_prepared_matvec.argtypes = [C.c_void_p, _f32p, _f32p]
+        L.orc_prepared_free.argtypes = [C.c_void_p]
         L.orc_set_threads.argtypes = [C.c_int]
         L.orc_get_threads.restype = C.c_int
         _lib = L
@@ -245,6 +249,33 @@ def matvec(qtype, scales, data, x, cols=None, vnni=False):
     out = np.zeros(rows, np.float32)
     (lib().orc_matvec_vnni if vnni else lib().orc_matvec)(C.byref(q), x, out)
     return out
+
+
+class Prepared:
+    """A matrix unpacked once for repeated plain matvecs (timing the CPU path
+    the way the model runs it, without the per-call unpack of matvec)."""
+
+    def __init__(self, qtype, scales, data, cols):
+        self._scales = _f32(scales)
+        self._data = np.ascontiguousarray(data, dtype=np.uint8)
+        self.rows = self._scales.size
+        q = _QMat(qtype, self.rows, cols, self._scales.ctypes.data, self._data.ctypes.data)
+        self.h = lib().orc_prepare(C.byref(q))
+        if not self.h:
+            raise MemoryError("orc_prepare")
+
+    def matvec(self, x, out=None):
+        out = np.zeros(self.rows, np.float32) if out is None else out
+        lib().orc_prepared_matvec(self.h, _f32(x), out)
+        return out
+
+    def close(self):
+        if self.h:
+            lib().orc_prepared_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
 
 
 def quantize_x_vnni(x):

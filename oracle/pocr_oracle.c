@@ -386,6 +386,24 @@ void orc_matvec(const orc_qmat *m, const float *x, float *out) {
     umat_free(&u);
 }
 
+struct orc_prepared {
+    umat u;
+};
+
+orc_prepared *orc_prepare(const orc_qmat *m) {
+    orc_prepared *p = (orc_prepared *)malloc(sizeof(orc_prepared));
+    if (p) umat_build(&p->u, m);
+    return p;
+}
+
+void orc_prepared_matvec(const orc_prepared *p, const float *x, float *out) { umat_matvec(&p->u, x, out, 0); }
+
+void orc_prepared_free(orc_prepared *p) {
+    if (!p) return;
+    umat_free(&p->u);
+    free(p);
+}
+
 void orc_matvec_vnni(const orc_qmat *m, const float *x, float *out) {
     umat u;
     umat_build(&u, m);

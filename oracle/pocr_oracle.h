@@ -52,6 +52,13 @@ void orc_matvec(const orc_qmat *m, const float *x, float *out);
 /* VNNI-emulation semantics (dot_amd64.go:140-167, dot_vnni_amd64.s:434-500,1043-1080) */
 float orc_quantize_x_vnni(const float *x, int n, uint8_t *xq);
 void orc_matvec_vnni(const orc_qmat *m, const float *x, float *out);
+/* the same plain matvec on a matrix unpacked once (as the model keeps its
+ * weights), for timing the CPU path without the per-call unpack; the handle
+ * borrows m's scale array */
+typedef struct orc_prepared orc_prepared;
+orc_prepared *orc_prepare(const orc_qmat *m);
+void orc_prepared_matvec(const orc_prepared *p, const float *x, float *out);
+void orc_prepared_free(orc_prepared *p);
 
 /* ---- small vector ops (a6-a13 pieces) ---- */
 float orc_fast_exp(float x);

@@ -156,3 +156,45 @@ def test_ernie_q8_prompt64_greedy16(orc, ctx):
     want = om.generate(ids, 16, eos=())
     got = gm.seq(128).generate(ids, 16, eos=())
     assert list(got) == list(want)
+
+
+def test_graph_replay_equals_direct_launches(ctx, monkeypatch):
+    """The decode loop replays one captured HIP graph per token; with
+    POCR_HIP_GRAPH=0 it launches the same kernels directly.  Both must give
+    the same tokens and bit-identical caches, single and batched."""
+    from rapidocrvl_amd import synth
+    from rapidocrvl_amd.config import DecoderConfig
+
+    cfg = DecoderConfig(hidden=1024, inter=3072, layers=3, heads=16, kv_heads=2, head_dim=128, vocab=5000,
+                        eps=1e-5, rope_theta=500000.0)
+    gm = lib.Model(ctx, cfg)
+    gm.load_weights(synth.make_weights(cfg, lib.Q4, seed=21))
+    prompts = [synth.prompt_ids(n, seed=60 + n, high=cfg.vocab) for n in (17, 30, 9, 24, 12)]
+
+    def run():
+        single = []
+        for ids in prompts[:2]:
+            s = gm.seq(len(ids) + 40)
+            toks = list(s.generate(ids, 32, eos=(), use_prefill=True))
+            single.append((toks, [s.read_kv(li) for li in (0, cfg.layers - 1)]))
+            s.close()
+        seqs = [gm.seq(len(ids) + 40) for ids in prompts]
+        firsts = [int(s.generate(ids, 1, eos=(), use_prefill=True)[0]) for s, ids in zip(seqs, prompts)]
+        batched = [list(t) for t in lib.decode_batch(seqs, firsts, [len(i) for i in prompts], 24, eos=())]
+        kv = [seqs[i].read_kv(cfg.layers - 1) for i in range(len(seqs))]
+        for s in seqs:
+            s.close()
+        return single, batched, kv
+
+    monkeypatch.setenv("POCR_HIP_GRAPH", "1")
+    g_single, g_batched, g_kv = run()
+    monkeypatch.setenv("POCR_HIP_GRAPH", "0")
+    d_single, d_batched, d_kv = run()
+    for (gt, gkv), (dt, dkv) in zip(g_single, d_single):
+        assert gt == dt
+        for (gk, gv), (dk, dv) in zip(gkv, dkv):
+            assert np.array_equal(gk, dk) and np.array_equal(gv, dv)
+    assert g_batched == d_batched
+    for (gk, gv), (dk, dv) in zip(g_kv, d_kv):
+        assert np.array_equal(gk, dk) and np.array_equal(gv, dv)
+    gm.close()

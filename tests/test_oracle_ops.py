@@ -284,3 +284,17 @@ def test_fast_exp_exponent_wrap(orc, x):
         assert abs(got / want - 1) < 4e-6
     if x <= -100.0 and x > -260.0:
         assert got < 0  # the carry reached the sign bit
+
+
+@pytest.mark.parametrize("qtype", [1000, 1001, 1002], ids=["q8", "q4", "q6"])
+def test_prepared_matvec_equals_matvec(orc, qtype):
+    # the timing entry (matrix unpacked once) computes the same plain matvec
+    from rapidocrvl_amd import lib
+
+    rng = np.random.default_rng(9)
+    q = lib.QMatrix.quantize((rng.standard_normal((700, 96)) * 0.02).astype(np.float32), qtype)
+    p = orc.Prepared(qtype, q.scales, q.packed, 96)
+    for _ in range(3):
+        x = rng.standard_normal(96).astype(np.float32)
+        assert np.array_equal(p.matvec(x), orc.matvec(qtype, q.scales, q.packed, x))
+    p.close()
