@@ -134,6 +134,7 @@ struct pocr_seq {
     int len = 0;  // host mirror
     float *kv = nullptr;  // [layers][2][cap][kvd]
     float *h = nullptr, *qkv = nullptr, *head_out = nullptr, *vbuf = nullptr, *g = nullptr, *logits = nullptr;
+    float *opart = nullptr;  // [heads][hidden] o_proj partials of the fused merge (k_attn_merge_oproj)
     float *part = nullptr;
     pocr::StepState *st = nullptr;
     int32_t *tokens = nullptr;

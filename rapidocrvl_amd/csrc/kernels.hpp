@@ -493,6 +493,39 @@ __device__ __forceinline__ void x_load(const float *x, const float *nw, bool nor
     }
 }
 
+// PRO_OPART's activation, staged through LDS: thread t sums 4 columns
+// (4t..4t+3: every thread takes part, 1024 columns at most) of the residual
+// and up to kMaxOparts partial rows, each added in row order; the loads are
+// requested together (branch-free: rows past nparts re-read the last one and
+// are not added).
+constexpr int kMaxOparts = 16;
+struct OpartRegs {
+    float4 p[kMaxOparts];
+    float4 h;
+};
+__device__ __forceinline__ void opart_issue(const float *part, int nparts, const float *resid, int cols,
+                                            OpartRegs &r) {
+    const int c = min(4 * (int)threadIdx.x, cols - 4);
+#pragma unroll
+    for (int k = 0; k < kMaxOparts; ++k)
+        r.p[k] = *reinterpret_cast<const float4 *>(part + (size_t)min(k, nparts - 1) * cols + c);
+    r.h = *reinterpret_cast<const float4 *>(resid + c);
+}
+// the sum into LDS (stage[cols]) and, for vbuf != null, into vbuf
+__device__ __forceinline__ void opart_stage(const OpartRegs &r, int nparts, int cols, float *stage, float *vbuf) {
+    float4 o = r.p[0];
+#pragma unroll
+    for (int k = 1; k < kMaxOparts; ++k)
+        if (k < nparts)  // uniform
+            o = make_float4(o.x + r.p[k].x, o.y + r.p[k].y, o.z + r.p[k].z, o.w + r.p[k].w);
+    const float4 v = make_float4(r.h.x + o.x, r.h.y + o.y, r.h.z + o.z, r.h.w + o.w);
+    const int c = 4 * (int)threadIdx.x;
+    if (c < cols) {
+        *reinterpret_cast<float4 *>(stage + c) = v;
+        if (vbuf) *reinterpret_cast<float4 *>(vbuf + c) = v;
+    }
+}
+
 // Digit planes of the thread's columns → LDS records, and the wave's Σx²
 // into red[wave] (with the norm on, the digits encode x·w and the row sums
 // are scaled by fastRsqrt(Σx²/n + eps) afterwards: x_norm_factor after the
@@ -631,7 +664,11 @@ __device__ __forceinline__ void load_digits(const int *lds, int l, XDig<QT, CPL,
 // ---------------------------------------------------------------------------
 // GEMV family
 // ---------------------------------------------------------------------------
-enum : int { PRO_COPY = 0, PRO_RMSNORM = 1 };
+// PRO_OPART: x = residual + (((x[0·cols..] + x[1·cols..]) + …) + x[(flag−1)·cols..])
+// (the o_proj partials of k_attn_merge_oproj), then RMSNorm as PRO_RMSNORM;
+// workgroup 0 also writes that x (residual + attention) to vbuf, where the
+// down GEMV (EPI_DOWNV) takes it as its residual when the o_proj runs in place.
+enum : int { PRO_COPY = 0, PRO_RMSNORM = 1, PRO_OPART = 2 };
 enum : int {
     EPI_PLAIN = 0,   // out[r] = s
     EPI_SWIGLU = 1,  // out[r] = SiLU(s_gate)·s_up            (NMAT = 2)
@@ -639,6 +676,7 @@ enum : int {
     EPI_DOWN = 3,    // residual += s, or vbuf = residual + s on the last layer
     EPI_ARGMAX = 4,  // greedy LM head (+ optional logits)
     EPI_ADDV = 5,    // vbuf = residual + s (op-level AddRMSNorm, norm in a 2nd kernel)
+    EPI_DOWNV = 6,   // EPI_DOWN over residual = (o_proj in place ? vbuf : residual), after PRO_OPART
 };
 
 struct GemvParams {
@@ -732,6 +770,12 @@ __device__ __forceinline__ void gemv_epilogue(const GemvParams &p, int epi, int 
         break;
     }
     case EPI_ADDV: p.vbuf[o] = resid + s[0]; break;
+    case EPI_DOWNV: {  // resid was picked from vbuf or residual by the o_proj rule
+        const float v = resid + s[0];
+        if (p.flag) p.vbuf[o] = v;
+        else p.residual[o] = v;
+        break;
+    }
     default:  // EPI_ARGMAX
         if (p.out) p.out[o] = s[0];
         if (s[0] > best_v || (s[0] == best_v && r < best_r)) {
@@ -742,7 +786,7 @@ __device__ __forceinline__ void gemv_epilogue(const GemvParams &p, int epi, int 
 }
 
 __device__ __forceinline__ bool epi_reads_residual(int epi) {
-    return epi == EPI_OPROJ || epi == EPI_DOWN || epi == EPI_ADDV;
+    return epi == EPI_OPROJ || epi == EPI_DOWN || epi == EPI_ADDV || epi == EPI_DOWNV;
 }
 
 __device__ __forceinline__ StepState *st_of(const GemvParams &p, const GemvNV &q, int v) {
@@ -919,17 +963,31 @@ __device__ __forceinline__ void gemv_body(GemvParams p, int pro, int epi, const 
 
     // activations first, so that waiting for them does not wait for weights
     const int cols = p.cols;
-    const bool norm = pro == PRO_RMSNORM;
+    const bool norm = pro == PRO_RMSNORM || pro == PRO_OPART;
     XRegs xr[NV];
+    OpartRegs opr;
+    const bool opart = NV == 1 && pro == PRO_OPART;  // uniform
+    if (opart) {
+        opart_issue(p.x, p.flag, p.residual, cols, opr);
 #pragma unroll
-    for (int v = 0; v < NV; ++v) {
-        const float *xv = p.x + (NV > 1 ? v * q.x_stride : 0);
-        x_load(xv, p.norm_w, norm && v == 0, cols, xr[v]);
+        for (int pp = 0; pp < kXPasses; ++pp) {  // the norm weight; x itself comes from LDS below
+            if (pp * kXPass >= cols) break;      // uniform
+            const float4 *wp =
+                reinterpret_cast<const float4 *>(p.norm_w + min((pp * kThreads + (int)threadIdx.x) * 8, cols - 8));
+            xr[0].w[pp][0] = wp[0];
+            xr[0].w[pp][1] = wp[1];
+        }
+    } else {
+#pragma unroll
+        for (int v = 0; v < NV; ++v) {
+            const float *xv = p.x + (NV > 1 ? v * q.x_stride : 0);
+            x_load(xv, p.norm_w, norm && v == 0, cols, xr[v]);
+        }
     }
     // first group: weights, then the writer lane's epilogue operands (row
     // scale, residual), all requested before the prologue's first wait
     Chunk w[U][NMAT][CPL];
-    float scl[NMAT], resid;
+    float scl[NMAT], resid, residv;
     {
         const int gc = min(g, ngroups - 1);
         const SegSel sel = seg_select<NMAT>(p, gc * RG);
@@ -938,8 +996,24 @@ __device__ __forceinline__ void gemv_body(GemvParams p, int pro, int epi, const 
 #pragma unroll
         for (int mi = 0; mi < NMAT; ++mi) scl[mi] = (mi == 0 ? sel.scale0 : sel.scale1)[rc - sel.start];
         resid = need_resid ? p.residual[my_o + rc] : 0.0f;
+        residv = epi == EPI_DOWNV ? p.vbuf[rc] : 0.0f;
     }
     const int recs = QT == QT_Q4 ? (cols / 32) * DigitRec<QT>::RS : (cols / 16) * DigitRec<QT>::RS;
+    if (opart) {
+        // residual + Σ partials → LDS after the digit records (and, in
+        // workgroup 0, to vbuf for the down GEMV), then each prologue thread
+        // takes its 8 columns as x_load would have
+        float *stage = reinterpret_cast<float *>(lds + recs);
+        opart_stage(opr, p.flag, cols, stage, blockIdx.x == 0 ? p.vbuf : nullptr);
+        __syncthreads();
+#pragma unroll
+        for (int pp = 0; pp < kXPasses; ++pp) {
+            if (pp * kXPass >= cols) break;  // uniform
+            const int cb = min((pp * kThreads + (int)threadIdx.x) * 8, cols - 8);
+            xr[0].x[pp][0] = *reinterpret_cast<const float4 *>(stage + cb);
+            xr[0].x[pp][1] = *reinterpret_cast<const float4 *>(stage + cb + 4);
+        }
+    }
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
         // the norm weight was loaded once, with vector 0
@@ -954,7 +1028,8 @@ __device__ __forceinline__ void gemv_body(GemvParams p, int pro, int epi, const 
     }
     XDig<QT, CPL, NPL> xd;  // NV = 1: the vector's digits stay in registers across groups
     if constexpr (NV == 1) load_digits<QT, LPR, CPL, NPL>(lds, l, xd);
-    const bool in_place = epi == EPI_OPROJ ? oproj_in_place(p, st_of(p, q, my_v)) : false;
+    const bool in_place = (epi == EPI_OPROJ || epi == EPI_DOWNV) ? oproj_in_place(p, st_of(p, q, my_v)) : false;
+    const bool use_v = epi == EPI_DOWNV && in_place;  // the residual includes this layer's attention
     float best_v = -INFINITY;
     int best_r = 0x7FFFFFFF;
 
@@ -995,7 +1070,7 @@ __device__ __forceinline__ void gemv_body(GemvParams p, int pro, int epi, const 
     // use and every path keeps static wait counts.
     if constexpr (!ONE) for (; g + gstride < ngroups; g += gstride) {
         Chunk wn[U][NMAT][CPL];
-        float scln[NMAT], residn;
+        float scln[NMAT], residn, residvn;
         {
             const int gn = g + gstride;
             const SegSel seln = seg_select<NMAT>(p, gn * RG);
@@ -1004,8 +1079,9 @@ __device__ __forceinline__ void gemv_body(GemvParams p, int pro, int epi, const 
 #pragma unroll
             for (int mi = 0; mi < NMAT; ++mi) scln[mi] = (mi == 0 ? seln.scale0 : seln.scale1)[rn - seln.start];
             residn = need_resid ? p.residual[my_o + rn] : 0.0f;
+            residvn = epi == EPI_DOWNV ? p.vbuf[rn] : 0.0f;
         }
-        compute(g, w, scl, resid);
+        compute(g, w, scl, use_v ? residv : resid);
 #pragma unroll
         for (int u = 0; u < U; ++u)
 #pragma unroll
@@ -1015,8 +1091,9 @@ __device__ __forceinline__ void gemv_body(GemvParams p, int pro, int epi, const 
 #pragma unroll
         for (int mi = 0; mi < NMAT; ++mi) scl[mi] = scln[mi];
         resid = residn;
+        residv = residvn;
     }
-    if (g < ngroups) compute(g, w, scl, resid);
+    if (g < ngroups) compute(g, w, scl, use_v ? residv : resid);
     if (epi == EPI_ARGMAX) {
 #pragma unroll
         for (int v = 0; v < NV; ++v)
@@ -1606,7 +1683,9 @@ constexpr int kMaxSplits = 1024;  // cache capacity ≤ 65536 rows
 constexpr int kMergeThreads = 256;
 constexpr int kMergeGroups = kMergeThreads / 32;
 
-__device__ __forceinline__ void attn_merge_body(AttnParams p) {
+// Returns false when the step has failed (nothing written).  The merged head
+// (128 floats, 16-byte aligned) goes to dst, by default its head_out slot.
+__device__ __forceinline__ bool attn_merge_body(AttnParams p, float *dst = nullptr) {
     __shared__ float e_lds[kMaxSplits];
     __shared__ float4 o_lds[kMergeGroups][32];
     __shared__ float l_lds;
@@ -1632,7 +1711,7 @@ __device__ __forceinline__ void attn_merge_body(AttnParams p) {
     for (int b = 0; b < B; ++b) av[b] = acc(min(sg + kMergeGroups * b, p.nsplit - 1));
     const float m0 = ml.x, l0 = ml.y;
     asm volatile("" : "+v"(st4.x), "+v"(st4.y), "+v"(st4.z), "+v"(st4.w)::"memory");  // requests above, uses below
-    if (p.st && st4.w) return;  // err
+    if (p.st && st4.w) return false;  // err
     const int L = p.st ? st4.x : p.len;
     const int used = min(p.nsplit, (L + p.chunk - 1) / p.chunk);  // ≥ 1 for L ≥ 1
     if (wave0) {  // split weights, lane s + 64k ↔ split
@@ -1680,9 +1759,10 @@ __device__ __forceinline__ void attn_merge_body(AttnParams p) {
             r.w += a.w;
         }
         const float inv = 1.0f / l_lds;
-        *reinterpret_cast<float4 *>(p.head_out + (size_t)hq * kHD + 4 * t) =
-            make_float4(r.x * inv, r.y * inv, r.z * inv, r.w * inv);
+        float *o = dst ? dst : p.head_out + (size_t)hq * kHD;
+        *reinterpret_cast<float4 *>(o + 4 * t) = make_float4(r.x * inv, r.y * inv, r.z * inv, r.w * inv);
     }
+    return true;
 }
 
 template <int RPW>
@@ -1695,6 +1775,91 @@ static __global__ void __launch_bounds__(kMergeThreads) k_attn_merge(AttnParams 
     AttnParams p = args;
     pin_args(p);
     attn_merge_body(p);
+}
+
+// ---------------------------------------------------------------------------
+// The merge with o_proj folded in, as a split over heads.  Workgroup (q head
+// h, row slice s) merges head h exactly as k_attn_merge does, writes its 128
+// values as the o_proj GEMV's digit records (x_digits over the head's
+// columns: the GEMV's chunks never straddle a head), and multiplies them by
+// W_o's columns of head h for its rows:
+//   part[h][r] = (Σ over the head's chunks of the GEMV's chunk value)·scale[r].
+// The consumer (the gate/up GEMV prologue, PRO_OPART) forms
+//   v = h_res + (((part[0] + part[1]) + …) + part[heads−1])
+// and RMSNorm(v).  So one launch per layer goes: the o_proj GEMV's.
+// ---------------------------------------------------------------------------
+constexpr int kOprojSlices = 8;  // row slices per head: heads × 8 workgroups
+
+struct OprojParts {
+    DevMat w;      // W_o [rows][heads·128]
+    float *part;   // [heads][rows]
+};
+
+template <int QT>
+__global__ void __launch_bounds__(kMergeThreads) k_attn_merge_oproj(AttnParams args, OprojParts op) {
+    constexpr int LPROW = 128 / QTraits<QT>::W;  // lanes per row: one chunk each (Q4 4, Q8/Q6 8)
+    constexpr int ROWS_PASS = kMergeThreads / LPROW;
+    constexpr int RS = DigitRec<QT>::RS;
+    constexpr int MAXP = 4;  // passes of ROWS_PASS rows: up to 4·64 (Q4) / 4·32 rows per slice
+    static_assert(kMergeThreads == kThreads, "x_digits runs on kThreads threads");
+    __shared__ __attribute__((aligned(16))) float merged[kHD];
+    __shared__ __attribute__((aligned(16))) int recs[LPROW * RS];
+    __shared__ float red[kWaves];
+    AttnParams p = args;
+    pin_args(p);
+    asm volatile("" ::"s"(op.w.data), "s"(op.w.scale), "s"(op.w.row_bytes), "s"(op.w.rows), "s"(op.part));
+    const int hq = blockIdx.x;
+    const int t = threadIdx.x;
+    const int rows = op.w.rows;
+    const int per_slice = (rows + kOprojSlices - 1) / kOprojSlices;
+    const int r_begin = blockIdx.y * per_slice;
+    const int j = t % LPROW;  // this lane's chunk of the head
+    // the weight chunks and row scales of this workgroup's rows, requested
+    // before the merge waits for its records (rows past the slice: the last
+    // row, loaded and never written)
+    Chunk w[MAXP];
+    float sc[MAXP];
+#pragma unroll
+    for (int ps = 0; ps < MAXP; ++ps) {
+        if (ps * ROWS_PASS >= per_slice) break;  // uniform
+        const int rr = r_begin + ps * ROWS_PASS + t / LPROW;
+        const int r = min(rr, rows - 1);
+        w[ps] = load_chunk<QT>(op.w.data + (size_t)r * op.w.row_bytes +
+                               (size_t)(hq * LPROW + j) * QTraits<QT>::CB);
+        sc[ps] = op.w.scale[r];
+    }
+    if (!attn_merge_body(p, merged)) return;
+    __syncthreads();
+    // digit records of the head's 128 values (threads 0..15 hold 8 columns each)
+    XRegs xr;
+    {
+        const float4 *mp = reinterpret_cast<const float4 *>(merged);
+        const int g = min(t, kHD / 8 - 1);
+        xr.x[0][0] = mp[2 * g];
+        xr.x[0][1] = mp[2 * g + 1];
+#pragma unroll
+        for (int pp = 1; pp < kXPasses; ++pp) xr.x[pp][0] = xr.x[pp][1] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    x_digits<QT>(xr, xr, false, kHD, recs, red);
+    __syncthreads();
+    XDig<QT, 1, 3> xd;
+    load_digits<QT, LPROW, 1, 3>(recs, j, xd);
+#pragma unroll
+    for (int ps = 0; ps < MAXP; ++ps) {
+        const int rr = r_begin + ps * ROWS_PASS + t / LPROW;
+        if (ps * ROWS_PASS >= per_slice) break;  // uniform
+        Chunk wc[1] = {w[ps]};
+        const float v = row_dot<QT, 1, 3>(wc, xd);
+        // the head's chunk values in chunk order, on the row's first lane
+        float acc = 0.0f;
+        const int base = (t & 63) - j;
+#pragma unroll
+        for (int k = 0; k < LPROW; ++k) {
+            const float vk = __shfl(v, base + k, 64);
+            acc = k == 0 ? vk : acc + vk;
+        }
+        if (j == 0 && rr < min(rows, r_begin + per_slice)) op.part[(size_t)hq * rows + rr] = acc * sc[ps];
+    }
 }
 
 // Several sequences in one launch (batched decode): blockIdx.z picks the

@@ -54,6 +54,7 @@ pocr_seq::~pocr_seq() {
     free_dev(h);
     free_dev(qkv);
     free_dev(head_out);
+    free_dev(opart);
     free_dev(vbuf);
     free_dev(g);
     free_dev(logits);
@@ -513,6 +514,14 @@ int pocr::gemv_launch(hipStream_t s, GemvParams p, int nmat, int pro, int epi, i
     const int nm = nmat == 2 ? 2 : (p.seg_end[0] == p.rows ? 1 : (p.seg_end[1] == p.rows ? 2 : 3));
     int rc = plan_gemv(p.m[0].qtype, nmat, p.rows, p.cols, p.m, nm, max_grid, &plan, 0, p.seg_end, epi, nv);
     if (rc) return rc;
+    if ((pro == PRO_OPART || epi == EPI_DOWNV) && (plan.fn == reinterpret_cast<const void *>(&k_gemv_any<1>) ||
+                                                   plan.fn == reinterpret_cast<const void *>(&k_gemv_any<2>)))
+        return fail(POCR_ERR_UNSUPPORTED, "gemv: the partial-sum prologue needs the streaming kernel's shapes");
+    if (pro == PRO_OPART) {
+        if (nv != 1 || p.cols > 4 * kThreads || p.cols % 8 != 0 || p.flag < 1 || p.flag > kMaxOparts)
+            return fail(POCR_ERR_UNSUPPORTED, "gemv: partial-sum prologue for %d columns, %d rows", p.cols, p.flag);
+        plan.lds += (size_t)p.cols * 4;  // the staged activation after the digit records
+    }
     if (nv > 1 && !q) return fail(POCR_ERR_ARG, "gemv: %d vectors need their strides", nv);
     return launch_gemv(s, plan, p, pro, epi, nv > 1 ? *q : GemvNV{});
 }
@@ -1651,6 +1660,7 @@ extern "C" int pocr_seq_create(pocr_model *m, int capacity, pocr_seq **out) {
     if (e == hipSuccess) e = hipMalloc(&s->h, (size_t)c.hidden * 4);
     if (e == hipSuccess) e = hipMalloc(&s->qkv, qkv * 4);
     if (e == hipSuccess) e = hipMalloc(&s->head_out, q_rows * 4);
+    if (e == hipSuccess) e = hipMalloc(&s->opart, (size_t)c.heads * c.hidden * 4);
     if (e == hipSuccess) e = hipMalloc(&s->vbuf, (size_t)c.hidden * 4);
     if (e == hipSuccess) e = hipMalloc(&s->g, (size_t)c.intermediate * 4);
     if (e == hipSuccess) e = hipMalloc(&s->logits, (size_t)c.vocab * 4);
@@ -2058,6 +2068,47 @@ extern "C" int pocr_time_stream_read(pocr_ctx *ctx, int64_t bytes, int n_buffers
 // One layer (model.go:3492-3603 with attentionWithNorm 3850-4066 and
 // mlpDownAddRMSNormCPU 5714-5800).  last/kv_only select the final-layer
 // variants.
+// The o_proj folded into the attention merge (k_attn_merge_oproj, the
+// consumers' PRO_OPART / EPI_DOWNV): head_dim 128, o_proj columns = heads·128,
+// and gate/up/down on the streaming GEMV's shapes (their prologue and
+// epilogue carry the partial sums).  POCR_FUSED_OPROJ=0 keeps the separate
+// merge and o_proj launches.
+static bool gemv_fast_shape(const DevMat &m) {
+    const int W = m.qtype == POCR_Q4 ? 32 : 16, CB = m.qtype == POCR_Q6 ? 12 : 16;
+    if (m.cols % W != 0 || m.cols > kMaxCols || ((uintptr_t)m.data) % 16 != 0) return false;
+    const int C = m.cols / W;
+    if (m.row_bytes != C * CB) return false;
+    const int lpr = C % 64 == 0 ? 64 : (C % 32 == 0 ? 32 : 0);
+    return lpr != 0 && !(C / lpr > 4 || (lpr == 32 && C / lpr > 3));
+}
+
+static bool fused_oproj(const pocr_model *m, const LayerW &L) {
+    const char *env = getenv("POCR_FUSED_OPROJ");
+    if (env && env[0] == '0') return false;
+    const pocr_config &c = m->cfg;
+    const DevMat o = dev_mat(L.w[POCR_W_O]);
+    if (c.head_dim != kHD || o.cols != c.heads * kHD || o.rows != c.hidden || c.heads > kMaxOparts ||
+        c.hidden > 4 * kThreads || c.hidden % 8 != 0)
+        return false;
+    if (((uintptr_t)o.data) % 16 != 0 || o.row_bytes % 4 != 0) return false;
+    if (o.qtype == POCR_Q6 ? o.row_bytes != o.cols / 16 * 12 : o.row_bytes != o.cols * (o.qtype == POCR_Q4 ? 1 : 2) / 2)
+        return false;
+    return gemv_fast_shape(dev_mat(L.w[POCR_W_GATE])) && gemv_fast_shape(dev_mat(L.w[POCR_W_UP])) &&
+           gemv_fast_shape(dev_mat(L.w[POCR_W_DOWN]));
+}
+
+static int launch_merge_oproj(hipStream_t st, const AttnParams &a, const pocr_weight *wo, float *part, int heads) {
+    OprojParts op{dev_mat(wo), part};
+    const dim3 grid(heads, kOprojSlices);
+    switch (wo->qtype) {
+    case POCR_Q4: hipLaunchKernelGGL(k_attn_merge_oproj<QT_Q4>, grid, dim3(kMergeThreads), 0, st, a, op); break;
+    case POCR_Q8: hipLaunchKernelGGL(k_attn_merge_oproj<QT_Q8>, grid, dim3(kMergeThreads), 0, st, a, op); break;
+    default: hipLaunchKernelGGL(k_attn_merge_oproj<QT_Q6>, grid, dim3(kMergeThreads), 0, st, a, op); break;
+    }
+    HIP_TRY(hipGetLastError());
+    return POCR_OK;
+}
+
 static int enqueue_layer(pocr_seq *s, int li, bool last, bool kv_only) {
     pocr_model *m = s->m;
     const pocr_config &c = m->cfg;
@@ -2098,18 +2149,43 @@ static int enqueue_layer(pocr_seq *s, int li, bool last, bool kv_only) {
     attn_shape(a, s->cap, s->rpw);
     a.scale = (float)(1.0 / std::sqrt((double)c.head_dim));
     launch_attn_decode(st, s->rpw, dim3(c.kv_heads, s->nsplit), a);
+    const pocr_weight *wo = L.w[POCR_W_O];
+    const int quirk = (m->quirk && (wo->qtype == POCR_Q4 || wo->qtype == POCR_Q6)) ? 1 : 0;
+    if (!kv_only && fused_oproj(m, L)) {
+        // 2'. merge + o_proj partials per head; gate/up sums them with the
+        // residual (PRO_OPART), down takes residual + attention when in place
+        RC(launch_merge_oproj(st, a, wo, s->opart, c.heads));
+        GemvParams gu = gemv_params_1(L.w[POCR_W_GATE]);
+        gu.m[1] = dev_mat(L.w[POCR_W_UP]);
+        gu.x = s->opart;
+        gu.flag = c.heads;  // partial rows
+        gu.residual = s->h;
+        gu.vbuf = s->vbuf;
+        gu.norm_w = L.ln2;
+        gu.eps = eps;
+        gu.out = s->g;
+        gu.st = s->st;
+        RC(gemv_launch(st, gu, 2, PRO_OPART, EPI_SWIGLU, kBigGrid));
+        GemvParams d = gemv_params_1(L.w[POCR_W_DOWN]);
+        d.x = s->g;
+        d.residual = s->h;
+        d.vbuf = s->vbuf;
+        d.st = s->st;
+        d.flag = last ? 1 : 0;
+        d.quirk = quirk;
+        return gemv_launch(st, d, 1, PRO_COPY, EPI_DOWNV, kBigGrid);
+    }
     hipLaunchKernelGGL(k_attn_merge, dim3(c.heads), dim3(kMergeThreads), 0, st, a);
     HIP_TRY(hipGetLastError());
     if (kv_only) return POCR_OK;
 
     // 3. o_proj + residual (+quirk) → vbuf (= h + attn), h updated if in place
-    const pocr_weight *wo = L.w[POCR_W_O];
     GemvParams o = gemv_params_1(wo);
     o.x = s->head_out;
     o.residual = s->h;
     o.vbuf = s->vbuf;
     o.st = s->st;
-    o.quirk = (m->quirk && (wo->qtype == POCR_Q4 || wo->qtype == POCR_Q6)) ? 1 : 0;
+    o.quirk = quirk;
     RC(gemv_launch(st, o, 1, PRO_COPY, EPI_OPROJ, kBigGrid));
 
     // 4. RMSNorm(vbuf)·ln2 → gate/up → SiLU(g)·u
