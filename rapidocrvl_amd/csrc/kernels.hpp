@@ -1344,16 +1344,17 @@ static __global__ void __launch_bounds__(kThreads) k_step_begin_multi(StepBatch 
 // chunk ≤ 4·RPW; wave w of it owns the RPW rows from s·chunk + RPW·w and is
 // a softmax split of its own.  RPW (8 or 16 rows per wave) trades workgroups
 // in flight against split records to merge: the host picks it from the cache
-// capacity.  Every request (the wave's K and V rows, the q
-// heads of the group, the RoPE table entries, the new K/V row) is issued
-// before the step state is read, in one memory round trip.  q (and the new k)
-// are rotated in registers: the pair (d, d+64) of RoPE sits in lanes l and
-// l^8 of a 16-lane row, one DPP rotate apart.  Scores for all GROUP q heads
-// share each K row (16 lanes × 8 dims per row, reduced by a DPP
-// reduce-scatter); the wave's softmax uses lane exchanges only, its
-// probabilities reach the P·V lanes through a wave-private LDS slot, and one
-// barrier combines the four waves into the split's record (max, Σexp,
-// Σexp·V), which k_attn_merge combines across splits.  The owner wave of the
+// capacity.  Every request (the q heads of the group and the RoPE table
+// entries first, the new K/V row, the wave's K rows by score pass, then its V
+// rows) is issued before the step state is read, in one memory round trip;
+// scores start as soon as their K rows have arrived.  The group's q is
+// rotated once per workgroup (each thread holds a RoPE pair (d, d+64) in its
+// own registers) and shared through LDS.  Scores for all GROUP q heads share
+// each K row (16 lanes × 8 dims per row, reduced by a DPP reduce-scatter);
+// the wave's softmax uses lane exchanges only, its probabilities reach the
+// P·V lanes through a wave-private LDS slot, and one barrier combines the
+// four waves into the split's record (max, Σexp, Σexp·V), which
+// k_attn_merge combines across splits.  The owner wave of the
 // newest row appends it (kvCache.append, model.go:5593-5612: row t at
 // t·kvDim + g·128).  Scores: dot(q,k)·f32(1/√128) (model.go:4623-4795, 7391);
 // softmax with FastExp (ops.go:1199-1363); out = Σ p·V (model.go:5201-5590).
@@ -1399,29 +1400,6 @@ __device__ __forceinline__ float rs16_heads(float (&v)[8][1], int lane) {
     return v[0][0];
 }
 
-// value of lane l ^ 8 within each row of 16 (DPP row_ror:8)
-__device__ __forceinline__ float xchg8(float v) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false));
-}
-
-// RoPE of 8 consecutive dims held by a lane (rope_pair across lanes l, l^8):
-// lower half a' = a·cos − b·sin, upper half b' = b·cos + a·sin
-__device__ __forceinline__ void rope8(float (&v)[8], const float (&cs)[8], const float (&sn)[8], bool upper) {
-#pragma clang fp contract(off)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        const float partner = xchg8(v[e]);
-        const float a = v[e] * cs[e];
-        const float b = partner * sn[e];
-        v[e] = upper ? a + b : a - b;
-    }
-}
-
-__device__ __forceinline__ void f4_to(float (&d)[8], const float4 &a, const float4 &b) {
-    d[0] = a.x; d[1] = a.y; d[2] = a.z; d[3] = a.w;
-    d[4] = b.x; d[5] = b.y; d[6] = b.z; d[7] = b.w;
-}
-
 // Kernel arguments made live at entry: one batch of scalar loads instead of
 // one argument round trip at each field's first use.  Input operands only:
 // an in/out operand would hide the pointers' provenance, turning every load
@@ -1434,6 +1412,26 @@ __device__ __forceinline__ void pin_args(const AttnParams &p) {
     asm volatile("" ::"s"(p.len), "s"(p.has_rope), "s"(p.chunk));
 }
 
+// in-lane RoPE of pairs (a = dim d, b = dim d + 64): a' = a·cos − b·sin,
+// b' = b·cos + a·sin, products rounded before the add
+__device__ __forceinline__ void rope_pair4(float4 &a, float4 &b, const float4 &c, const float4 &s) {
+#pragma clang fp contract(off)
+    const float4 a0 = a, b0 = b;
+    a = make_float4(a0.x * c.x - b0.x * s.x, a0.y * c.y - b0.y * s.y, a0.z * c.z - b0.z * s.z, a0.w * c.w - b0.w * s.w);
+    b = make_float4(b0.x * c.x + a0.x * s.x, b0.y * c.y + a0.y * s.y, b0.z * c.z + a0.z * s.z, b0.w * c.w + a0.w * s.w);
+}
+__device__ __forceinline__ void rope_pair2(float2 &a, float2 &b, const float2 &c, const float2 &s) {
+#pragma clang fp contract(off)
+    const float2 a0 = a, b0 = b;
+    a = make_float2(a0.x * c.x - b0.x * s.x, a0.y * c.y - b0.y * s.y);
+    b = make_float2(b0.x * c.x + a0.x * s.x, b0.y * c.y + a0.y * s.y);
+}
+
+// Lane layouts.  Scores: a 16-lane row (rg = lane / 16) takes one K row per
+// pass, lane l16 holding dims 4·l16..4·l16+3 and their RoPE partners 64 + the
+// same (two 16-byte loads that together read the row's 512 bytes as two
+// contiguous 256-byte halves).  P·V: lanes 0-31 and 32-63 take alternate rows,
+// lane holding dims 4·(lane & 31)..+3 (one 16-byte load per lane per two rows).
 template <int RPW>
 __device__ __forceinline__ void attn_decode_body(AttnParams p) {
     // products round before any later add (scores: s·scale, then s − max, as
@@ -1441,10 +1439,12 @@ __device__ __forceinline__ void attn_decode_body(AttnParams p) {
 #pragma clang fp contract(off)
     static_assert(RPW == 8 || RPW == 16, "rows per wave");
     constexpr int NJ = RPW / 4;  // score passes of 4 rows
+    constexpr int NV = RPW / 2;  // P·V loads: two rows each
     StepState *st = p.st;
-    __shared__ float4 e_lds[kWaves][kMaxGroup][NJ];     // wave-private probabilities [head][RPW rows]
+    __shared__ float4 q_lds[kMaxGroup][kHD / 4];          // the group's rotated q
+    __shared__ __align__(16) float e_lds[kWaves][kMaxGroup][2][NV];  // wave-private probabilities [head][row parity][row / 2]
     __shared__ float w_m[kWaves][kMaxGroup], w_l[kWaves][kMaxGroup];
-    __shared__ float2 w_acc[kWaves][kMaxGroup][kHD / 2];
+    __shared__ float4 w_acc[kWaves][kMaxGroup][2][kHD / 4];
 
     const int g = blockIdx.x;  // kv head
     const int split = blockIdx.y;
@@ -1453,6 +1453,7 @@ __device__ __forceinline__ void attn_decode_body(AttnParams p) {
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int l16 = lane & 15, rg = lane >> 4;
+    const int half = lane >> 5, l32 = lane & 31;
     const float *cos_t = st ? st->cos_t : p.cos_t;
     const float *sin_t = st ? st->sin_t : p.sin_t;
     const int kvd = p.kvh * kHD;
@@ -1464,58 +1465,50 @@ __device__ __forceinline__ void attn_decode_body(AttnParams p) {
     const int wr0 = t0 + RPW * wave;  // first row of this wave
     const int tmax = p.rows_cap - 1;
 
-    // ---- 1. requests.  The step state's fields first (len, clen, cap, err
-    // are its first 16 bytes): they are then the oldest loads in flight, so
-    // waiting for them later waits for nothing else.  Without a step state
-    // the loads read q (a readable stand-in, replaced at use).  Rows past the
-    // capacity are clamped to the last row (loaded, masked below); every lane
-    // issues the same loads.
+    // ---- 1. requests, oldest first, in the order they are used: the step
+    // state's header (len, clen, cap, err) and RoPE flag; this thread's q pair
+    // (head tid / 32, dims 2i, 2i+1 and 64 + the same) with its cos/sin; the
+    // new K/V row and its cos/sin (score layout); then K by score pass, then
+    // V.  Without a step state, RoPE table or new row the loads read q (a
+    // readable stand-in, replaced at use); heads past the group re-read the
+    // group's last head; rows past the capacity are clamped to the last row
+    // (loaded, masked below).  Every lane issues the same loads.
     int4 st4 = *reinterpret_cast<const int4 *>(st ? reinterpret_cast<const float *>(st) : p.q);
     int st_rope = *(st ? &st->has_rope : reinterpret_cast<const int *>(p.q));
-    asm volatile("" ::: "memory");  // these two loads go out first
-    float4 ka[NJ][2];  // K, score layout: pass j → row wr0 + 4j + rg, dims 8·l16..
+    asm volatile("" ::: "memory");
+    const int qh = tid >> 5, qi = tid & 31;
+    float2 qa, qb, qc, qs;
+    {
+        const float *qp = p.q + (size_t)(g * group + min(qh, group - 1)) * kHD + 2 * qi;
+        qa = *reinterpret_cast<const float2 *>(qp);
+        qb = *reinterpret_cast<const float2 *>(qp + kHD / 2);
+        qc = *reinterpret_cast<const float2 *>((cos_t ? cos_t : p.q) + 2 * qi);
+        qs = *reinterpret_cast<const float2 *>((cos_t ? sin_t : p.q) + 2 * qi);
+    }
+    float4 kc4, ks4, kn0, kn1, vn;
+    {
+        kc4 = *reinterpret_cast<const float4 *>((cos_t ? cos_t : p.q) + 4 * l16);
+        ks4 = *reinterpret_cast<const float4 *>((cos_t ? sin_t : p.q) + 4 * l16);
+        const float *kb = p.k_new ? p.k_new : p.q;
+        const float *vb = p.k_new ? p.v_new : p.q;
+        kn0 = *reinterpret_cast<const float4 *>(kb + (size_t)g * kHD + 4 * l16);
+        kn1 = *reinterpret_cast<const float4 *>(kb + (size_t)g * kHD + kHD / 2 + 4 * l16);
+        vn = *reinterpret_cast<const float4 *>(vb + (size_t)g * kHD + 4 * l32);
+    }
+    asm volatile("" ::: "memory");
+    float4 ka[NJ][2];  // K: pass j → row wr0 + 4j + rg
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
         const int t = min(wr0 + 4 * j + rg, tmax);
-        const float4 *src = reinterpret_cast<const float4 *>(p.kc + (size_t)t * kvd + g * kHD + 8 * l16);
-        ka[j][0] = src[0];
-        ka[j][1] = src[1];
+        const float *src = p.kc + (size_t)t * kvd + g * kHD + 4 * l16;
+        ka[j][0] = *reinterpret_cast<const float4 *>(src);
+        ka[j][1] = *reinterpret_cast<const float4 *>(src + kHD / 2);
     }
-    float2 va[RPW];  // V, P·V layout: row wr0 + i, dims 2·lane, 2·lane+1
+    float4 va[NV];  // V: load k → row wr0 + 2k + half
 #pragma unroll
-    for (int i = 0; i < RPW; ++i) {
-        const int t = min(wr0 + i, tmax);
-        va[i] = *reinterpret_cast<const float2 *>(p.vc + (size_t)t * kvd + g * kHD + 2 * lane);
-    }
-    // Branch-free requests (a load inside a branch makes the register merge
-    // after it wait for that load): heads past the group load the group's
-    // last head again (their scores are never used), and without a RoPE
-    // table or a new row the loads read q instead (replaced below / unused).
-    float4 qr[kMaxGroup][2];
-#pragma unroll
-    for (int h = 0; h < kMaxGroup; ++h) {
-        const int hh = min(h, group - 1);
-        const float4 *src = reinterpret_cast<const float4 *>(p.q + (size_t)(g * group + hh) * kHD + 8 * l16);
-        qr[h][0] = src[0];
-        qr[h][1] = src[1];
-    }
-    float cs[8], sn[8];
-    {
-        const int tb = (8 * l16) & (kHD / 2 - 1);
-        const float4 *cp = reinterpret_cast<const float4 *>((cos_t ? cos_t : p.q) + tb);
-        const float4 *sp = reinterpret_cast<const float4 *>((cos_t ? sin_t : p.q) + tb);
-        f4_to(cs, cp[0], cp[1]);
-        f4_to(sn, sp[0], sp[1]);
-    }
-    float4 kn[2];
-    float2 vn;
-    {
-        const float *kb = p.k_new ? p.k_new : p.q;  // q: a readable stand-in, never used
-        const float *vb = p.k_new ? p.v_new : p.q;
-        const float4 *kp = reinterpret_cast<const float4 *>(kb + (size_t)g * kHD + 8 * l16);
-        kn[0] = kp[0];
-        kn[1] = kp[1];
-        vn = *reinterpret_cast<const float2 *>(vb + (size_t)g * kHD + 2 * lane);
+    for (int k = 0; k < NV; ++k) {
+        const int t = min(wr0 + 2 * k + half, tmax);
+        va[k] = *reinterpret_cast<const float4 *>(p.vc + (size_t)t * kvd + g * kHD + 4 * l32);
     }
 
     // every request above is issued before the step state is examined: the
@@ -1529,63 +1522,67 @@ __device__ __forceinline__ void attn_decode_body(AttnParams p) {
     if (st && st4.w) return;  // err: a failed step appends nothing
     const int L = st ? st4.x : p.len;
     const int newest = st ? st4.y : -1;  // row appended by this step (clen)
-    const int rope = st ? st_rope : p.has_rope;
+    const bool rope = (st ? st_rope : p.has_rope) && cos_t;
     const int t1 = min(L, t0 + chunk);
-    if (t1 <= t0) return;  // split past the step's rows: the merge skips it
-    const bool upper = l16 >= 8;
-    if (!cos_t) {  // no RoPE table: the identity rotation
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            cs[e] = 1.0f;
-            sn[e] = 0.0f;
-        }
-    }
+    if (t1 <= t0) return;  // split past the step's rows (uniform): the merge skips it
 
-    // ---- 3. rotated q; the owner wave rotates and appends the newest row
-    float q[kMaxGroup][8];
+    // ---- 3. the group's q, rotated once per workgroup (thread → one head's
+    // pairs 2i, 2i+1) and shared through LDS; the owner wave rotates and
+    // appends the newest row
+    if (qh < group) {
+        if (rope) rope_pair2(qa, qb, qc, qs);
+        float *qrow = reinterpret_cast<float *>(&q_lds[qh][0]);
+        *reinterpret_cast<float2 *>(qrow + 2 * qi) = qa;
+        *reinterpret_cast<float2 *>(qrow + kHD / 2 + 2 * qi) = qb;
+    }
+    // the newest row's place in this wave (ni = -1: not here); its loaded
+    // K/V registers are replaced where they are used, so that no wave waits
+    // for its rows before the barrier below
+    const int ni = newest >= wr0 && newest < wr0 + RPW && newest < t1 ? newest - wr0 : -1;  // uniform per wave
+    if (ni >= 0) {
+        if (rope) rope_pair4(kn0, kn1, kc4, ks4);
+        if (rg == 0) {
+            float *kd = p.kc + (size_t)newest * kvd + g * kHD + 4 * l16;
+            *reinterpret_cast<float4 *>(kd) = kn0;
+            *reinterpret_cast<float4 *>(kd + kHD / 2) = kn1;
+        }
+        if (half == 0) *reinterpret_cast<float4 *>(p.vc + (size_t)newest * kvd + g * kHD + 4 * l32) = vn;
+    }
+    __syncthreads();
+    float4 q[kMaxGroup][2];  // score layout
 #pragma unroll
     for (int h = 0; h < kMaxGroup; ++h) {
-        f4_to(q[h], qr[h][0], qr[h][1]);
-        if (rope && h < group) rope8(q[h], cs, sn, upper);
-    }
-    if (newest >= wr0 && newest < wr0 + RPW && newest < t1) {  // uniform per wave
-        float k8[8];
-        f4_to(k8, kn[0], kn[1]);
-        if (rope) rope8(k8, cs, sn, upper);
-        const int i = newest - wr0;
-        if (rg == (i & 3)) {
-#pragma unroll
-            for (int j = 0; j < NJ; ++j)
-                if (j == (i >> 2)) {
-                    ka[j][0] = make_float4(k8[0], k8[1], k8[2], k8[3]);
-                    ka[j][1] = make_float4(k8[4], k8[5], k8[6], k8[7]);
-                }
-        }
-#pragma unroll
-        for (int ii = 0; ii < RPW; ++ii)
-            if (ii == i) va[ii] = vn;
-        if (rg == 0) {
-            float4 *kd = reinterpret_cast<float4 *>(p.kc + (size_t)newest * kvd + g * kHD + 8 * l16);
-            kd[0] = make_float4(k8[0], k8[1], k8[2], k8[3]);
-            kd[1] = make_float4(k8[4], k8[5], k8[6], k8[7]);
-        }
-        *reinterpret_cast<float2 *>(p.vc + (size_t)newest * kvd + g * kHD + 2 * lane) = vn;
+        const int hh = min(h, group - 1);
+        q[h][0] = q_lds[hh][l16];
+        q[h][1] = q_lds[hh][kHD / 8 + l16];
     }
 
     // ---- 4. scores; lanes 2h, 2h+1 of each 16-lane row hold head h's score
     const int hs = l16 >> 1;  // this lane's head after the reduce-scatter
+    const int jn = ni >= 0 && rg == (ni & 3) ? ni >> 2 : -1;  // pass holding the newest row in this lane
     float sj[NJ];
     bool ok[NJ];
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
-        float kv[8];
-        f4_to(kv, ka[j][0], ka[j][1]);
+        // the newest row's K: a per-lane select (an indexed store would send
+        // ka to scratch memory)
+        const bool r = jn == j;
+        const float4 k0 = make_float4(r ? kn0.x : ka[j][0].x, r ? kn0.y : ka[j][0].y, r ? kn0.z : ka[j][0].z,
+                                      r ? kn0.w : ka[j][0].w);
+        const float4 k1 = make_float4(r ? kn1.x : ka[j][1].x, r ? kn1.y : ka[j][1].y, r ? kn1.z : ka[j][1].z,
+                                      r ? kn1.w : ka[j][1].w);
         float part[8][1];
 #pragma unroll
         for (int h = 0; h < kMaxGroup; ++h) {
             float a = 0.0f;
-#pragma unroll
-            for (int d = 0; d < 8; ++d) a = fmaf(q[h][d], kv[d], a);
+            a = fmaf(q[h][0].x, k0.x, a);
+            a = fmaf(q[h][0].y, k0.y, a);
+            a = fmaf(q[h][0].z, k0.z, a);
+            a = fmaf(q[h][0].w, k0.w, a);
+            a = fmaf(q[h][1].x, k1.x, a);
+            a = fmaf(q[h][1].y, k1.y, a);
+            a = fmaf(q[h][1].z, k1.z, a);
+            a = fmaf(q[h][1].w, k1.w, a);
             part[h][0] = a;
         }
         const float sdot = rs16_heads(part, lane);
@@ -1607,10 +1604,12 @@ __device__ __forceinline__ void attn_decode_body(AttnParams p) {
     }
     lsum += xchg<XS16>(lsum);
     lsum += xchg<XS32>(lsum);
-    float *erow = reinterpret_cast<float *>(&e_lds[wave][0][0]);
     if ((l16 & 1) == 0 && hs < group) {
 #pragma unroll
-        for (int j = 0; j < NJ; ++j) erow[hs * RPW + 4 * j + rg] = ej[j];
+        for (int j = 0; j < NJ; ++j) {
+            const int r = 4 * j + rg;  // row within the wave
+            e_lds[wave][hs][r & 1][r >> 1] = ej[j];
+        }
         if (rg == 0) {
             w_m[wave][hs] = m;
             w_l[wave][hs] = lsum;
@@ -1620,32 +1619,51 @@ __device__ __forceinline__ void attn_decode_body(AttnParams p) {
     // accesses in order, the fence keeps the compiler from reordering them
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
 
-    // ---- 6. Σ e·V for every head over the wave's RPW rows (2 dims per lane)
+    // ---- 6. Σ e·V for every head over this lane's half of the wave's rows;
+    // every head's probabilities are read before the first product
+    float4 ev[kMaxGroup][NV / 4];
+#pragma unroll
+    for (int h = 0; h < kMaxGroup; ++h)
+#pragma unroll
+        for (int k = 0; k < NV / 4; ++k)
+            ev[h][k] = reinterpret_cast<const float4 *>(&e_lds[wave][min(h, group - 1)][half][0])[k];
+    asm volatile("" ::: "memory");  // all of them issued here, not one per head
+    {
+        // the newest row's V: a per-lane select on each register (an
+        // indexed store would send va to scratch memory)
+        const int nk = ni >= 0 && half == (ni & 1) ? ni >> 1 : -1;
+#pragma unroll
+        for (int k = 0; k < NV; ++k) {
+            const bool r = nk == k;
+            va[k] = make_float4(r ? vn.x : va[k].x, r ? vn.y : va[k].y, r ? vn.z : va[k].z, r ? vn.w : va[k].w);
+        }
+    }
 #pragma unroll
     for (int h = 0; h < kMaxGroup; ++h) {
         if (h >= group) break;
-        float ev[RPW];
+        float e[NV];
 #pragma unroll
-        for (int k = 0; k < NJ; ++k) {
-            const float4 t = e_lds[wave][h][k];
-            ev[4 * k] = t.x;
-            ev[4 * k + 1] = t.y;
-            ev[4 * k + 2] = t.z;
-            ev[4 * k + 3] = t.w;
+        for (int k = 0; k < NV / 4; ++k) {
+            e[4 * k] = ev[h][k].x;
+            e[4 * k + 1] = ev[h][k].y;
+            e[4 * k + 2] = ev[h][k].z;
+            e[4 * k + 3] = ev[h][k].w;
         }
-        float a0 = 0.0f, a1 = 0.0f;
+        float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-        for (int i = 0; i < RPW; ++i) {
-            a0 = fmaf(ev[i], va[i].x, a0);
-            a1 = fmaf(ev[i], va[i].y, a1);
+        for (int k = 0; k < NV; ++k) {
+            a.x = fmaf(e[k], va[k].x, a.x);
+            a.y = fmaf(e[k], va[k].y, a.y);
+            a.z = fmaf(e[k], va[k].z, a.z);
+            a.w = fmaf(e[k], va[k].w, a.w);
         }
-        w_acc[wave][h][lane] = make_float2(a0, a1);
+        w_acc[wave][h][half][l32] = a;
     }
     __syncthreads();
 
-    // ---- 7. combine the four waves → the split's record per head
-    const int h = tid >> 5;          // head
-    const int d4 = (tid & 31) * 4;   // dims d4..d4+3
+    // ---- 7. combine the four waves (two row halves each) → the split's record per head
+    const int h = tid >> 5;     // head
+    const int d4 = tid & 31;    // dims 4·d4..4·d4+3
     if (h < group) {
         float M = w_m[0][h];
 #pragma unroll
@@ -1657,16 +1675,16 @@ __device__ __forceinline__ void attn_decode_body(AttnParams p) {
             const float mw = w_m[w][h];
             const float f = mw == -INFINITY ? 0.0f : fast_exp_ref(mw - M);
             lt = fmaf(f, w_l[w][h], lt);
-            const float2 a = w_acc[w][h][d4 / 2];
-            const float2 b = w_acc[w][h][d4 / 2 + 1];
-            o.x = fmaf(f, a.x, o.x);
-            o.y = fmaf(f, a.y, o.y);
-            o.z = fmaf(f, b.x, o.z);
-            o.w = fmaf(f, b.y, o.w);
+            const float4 a = w_acc[w][h][0][d4];
+            const float4 b = w_acc[w][h][1][d4];
+            o.x = fmaf(f, a.x + b.x, o.x);
+            o.y = fmaf(f, a.y + b.y, o.y);
+            o.z = fmaf(f, a.z + b.z, o.z);
+            o.w = fmaf(f, a.w + b.w, o.w);
         }
         float *rh = p.part + ((size_t)(g * p.nsplit + split) * kMaxGroup + h) * kRec;
         if (d4 == 0) *reinterpret_cast<float2 *>(rh) = make_float2(M, lt);
-        *reinterpret_cast<float4 *>(rh + 4 + d4) = o;
+        *reinterpret_cast<float4 *>(rh + 4 + 4 * d4) = o;
     }
 }
 
