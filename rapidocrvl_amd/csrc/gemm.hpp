@@ -549,7 +549,7 @@ __device__ __forceinline__ void lds_barrier() {
 
 template <int QT, int NMAT, int NST>
 static __global__ void __launch_bounds__(kThreads) k_gemm_lds(GemmParams p, int epi) {
-    static_assert(NST == 3, "the main loop is unrolled over three slots");
+    static_assert(NST == 2 || NST == 3, "the main loop is unrolled over two or three slots");
     using Lay = GemmLdsLayout<QT, NMAT, NST>;
     constexpr int RB = Lay::RB;
     constexpr int WR = 16 * RB;                 // rows per matrix and wave
@@ -558,7 +558,7 @@ static __global__ void __launch_bounds__(kThreads) k_gemm_lds(GemmParams p, int 
     constexpr int LPS = 3 + NMAT * RB * CH;     // loads per stage and wave
     __shared__ __attribute__((aligned(16))) uint8_t slot0[Lay::stage];
     __shared__ __attribute__((aligned(16))) uint8_t slot1[Lay::stage];
-    __shared__ __attribute__((aligned(16))) uint8_t slot2[Lay::stage];
+    __shared__ __attribute__((aligned(16))) uint8_t slot2[NST == 3 ? Lay::stage : 16];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lr = lane & 15, lg = lane >> 4;
@@ -669,12 +669,29 @@ static __global__ void __launch_bounds__(kThreads) k_gemm_lds(GemmParams p, int 
         if (on) compute(cur);
     };
 
-    issue(0, slot0);
-    if (nst > 1) issue(1, slot1);
-    for (int u = 0; u < nst; u += 3) {
-        body(u, slot0, slot2);
-        if (u + 1 < nst) body(u + 1, slot1, slot0);
-        if (u + 2 < nst) body(u + 2, slot2, slot1);
+    if constexpr (NST == 3) {
+        issue(0, slot0);
+        if (nst > 1) issue(1, slot1);
+        for (int u = 0; u < nst; u += 3) {
+            body(u, slot0, slot2);
+            if (u + 1 < nst) body(u + 1, slot1, slot0);
+            if (u + 2 < nst) body(u + 2, slot2, slot1);
+        }
+    } else {
+        // two slots: stage u+1 is requested after the barrier of stage u
+        // (every wave is done with u−1, whose slot it takes) and lands while
+        // u is computed; the smaller ring lets two workgroups share a CU
+        auto body2 = [&](int u, const uint8_t *cur, uint8_t *next) {
+            wait_vm<0>();
+            lds_barrier();
+            if (u + 1 < nst) issue(u + 1, next);
+            if (on) compute(cur);
+        };
+        issue(0, slot0);
+        for (int u = 0; u < nst; u += 2) {
+            body2(u, slot0, slot1);
+            if (u + 1 < nst) body2(u + 1, slot1, slot0);
+        }
     }
     if (!on) return;
 

@@ -69,7 +69,12 @@ int launch_gemm_lds_t(hipStream_t s, int qtype, const GemmParams &p, int epi, in
     const dim3 grid((p.rows + kGemmRows / NMAT - 1) / (kGemmRows / NMAT), npad / 32);
     switch (qtype) {
     case QT_Q8: hipLaunchKernelGGL((k_gemm_lds<QT_Q8, NMAT, 3>), grid, dim3(kThreads), 0, s, p, epi); break;
-    case QT_Q4: hipLaunchKernelGGL((k_gemm_lds<QT_Q4, NMAT, 3>), grid, dim3(kThreads), 0, s, p, epi); break;
+    // Q4 gate/up: a two-slot ring (56 KB of LDS) fits two workgroups per CU,
+    // which pays for its shallower prefetch; the single-matrix products keep
+    // three slots
+    case QT_Q4:
+        hipLaunchKernelGGL((k_gemm_lds<QT_Q4, NMAT, NMAT == 2 ? 2 : 3>), grid, dim3(kThreads), 0, s, p, epi);
+        break;
     case QT_Q6: hipLaunchKernelGGL((k_gemm_lds<QT_Q6, NMAT, 3>), grid, dim3(kThreads), 0, s, p, epi); break;
     default: return fail(POCR_ERR_UNSUPPORTED, "gemm: qtype %d", qtype);
     }
