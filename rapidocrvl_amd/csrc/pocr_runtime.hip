@@ -298,6 +298,7 @@ static bool pick_fast(int nmat, int u, int tag, int lpr, int cpl, bool one, int 
     if (nv == 4) return pick_nv<QT, 4>(nmat, u != 2, lpr, cpl, fn);
     if (nmat == 2) return gemv_fast_kernel<QT, 2, 2>(lpr, cpl, fn);
     if (u == kBigU) return pick_big<QT>(tag, one, lpr, cpl, fn);
+    if (u == 1) return tag == 1 ? gemv_fast_kernel<QT, 1, 1, 1>(lpr, cpl, fn) : gemv_fast_kernel<QT, 1, 1>(lpr, cpl, fn);
     return tag == 1 ? gemv_fast_kernel<QT, 1, 2, 1>(lpr, cpl, fn) : gemv_fast_kernel<QT, 1, 2>(lpr, cpl, fn);
 }
 
@@ -337,7 +338,14 @@ static int plan_gemv(int qtype, int nmat, int rows, int cols, const DevMat *mats
     bool ok = false;
     // big row counts: 8 rows per lane group and step (more bytes in flight)
     const bool big = fast && nmat == 1 && cpl == 1 && rows >= 8192;
-    const int u = big ? kBigU : 2;
+    // one row per lane group and step when two would leave fewer than 128
+    // workgroups (the down projection's 1024 rows of 3072 columns): the
+    // shorter rows of work per wave beat the longer pipeline there
+    int u = big ? kBigU : 2;
+    if (fast && !big && nmat == 1 && nv == 1) {
+        const int groups2 = (rows + (64 / lpr) * 2 - 1) / ((64 / lpr) * 2);
+        if ((groups2 + kWaves - 1) / kWaves < 128) u = 1;
+    }
     if (big) max_grid = nv > 1 ? 1 << 30 : std::max(max_grid, POCR_BIG_GRID);
     // row groups must not straddle segments
     if (fast && nmat == 1 && seg_end) {
@@ -353,9 +361,9 @@ static int plan_gemv(int qtype, int nmat, int rows, int cols, const DevMat *mats
         const int want = (groups + kWaves - 1) / kWaves;
         grid = std::max(1, std::min(want, max_grid));
         one = big && grid == want;
-        if (qtype == POCR_Q4) ok = pick_fast<QT_Q4>(nmat, big ? kBigU : 2, tag, lpr, cpl, one, nv, &plan->fn);
-        if (qtype == POCR_Q8) ok = pick_fast<QT_Q8>(nmat, big ? kBigU : 2, tag, lpr, cpl, one, nv, &plan->fn);
-        if (qtype == POCR_Q6) ok = pick_fast<QT_Q6>(nmat, big ? kBigU : 2, tag, lpr, cpl, one, nv, &plan->fn);
+        if (qtype == POCR_Q4) ok = pick_fast<QT_Q4>(nmat, u, tag, lpr, cpl, one, nv, &plan->fn);
+        if (qtype == POCR_Q8) ok = pick_fast<QT_Q8>(nmat, u, tag, lpr, cpl, one, nv, &plan->fn);
+        if (qtype == POCR_Q6) ok = pick_fast<QT_Q6>(nmat, u, tag, lpr, cpl, one, nv, &plan->fn);
     }
     if (ok) {
         plan->lds = (size_t)nv * (qtype == POCR_Q4 ? gemv_lds_bytes<QT_Q4>(cols)
