@@ -681,6 +681,8 @@ def main():
     ap.add_argument("--no-batch", action="store_true", help="skip the 4-sequence batched decode")
     ap.add_argument("--batch-only", action="store_true", help="time only the 4-sequence Q4 batched decode")
     ap.add_argument("--projector-only", action="store_true", help="time only the vision projector")
+    ap.add_argument("--attention-only", action="store_true",
+                    help="time only the decode attention + merge at 1k/4k/8k cache rows")
     ap.add_argument("--serve-only", action="store_true", help="time only the 8-request serving comparison")
     ap.add_argument("--batch-tokens", type=int, default=1024, help="tokens per sequence of the batched decode")
     ap.add_argument("--batch-seqs", default="4,8,16", help="with --batch-only: batch sizes to time")
@@ -706,6 +708,10 @@ def main():
     ctx = lib.Context(0)
     if args.projector_only:
         print(json.dumps(projector_bench(ctx, with_cpu=not args.no_cpu)), flush=True)
+        return
+    if args.attention_only:
+        print(json.dumps({"workload": "decode attention (RoPE, K/V append, split attention + merge), 16q/2kv "
+                                      "heads, 18 layer caches rotated", **attention_sweep(ctx, cfg)}), flush=True)
         return
     if args.batch_only:
         _, model = build_model(ctx, cfg, lib.Q4)

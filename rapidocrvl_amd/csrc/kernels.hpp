@@ -1806,7 +1806,7 @@ static __global__ void __launch_bounds__(kMergeThreads) k_attn_merge(AttnParams 
 //   v = h_res + (((part[0] + part[1]) + …) + part[heads−1])
 // and RMSNorm(v).  So one launch per layer goes: the o_proj GEMV's.
 // ---------------------------------------------------------------------------
-constexpr int kOprojSlices = 8;  // row slices per head: heads × 8 workgroups
+constexpr int kOprojSlices = 16;  // row slices per head: heads × 16 workgroups
 
 struct OprojParts {
     DevMat w;      // W_o [rows][heads·128]
