@@ -1223,11 +1223,11 @@ extern "C" int pocr_mrope_pair(pocr_ctx *ctx, float *q, float *k, const float *c
 // Rows per wave of the decode attention for a cache capacity: short caches
 // take 32-row splits (more workgroups in flight), longer ones 64-row splits
 // (half the records to merge); the split count stays ≤ kMaxSplits.  On
-// MI355X (18 layers, 16 q / 2 kv heads; rocprofv3 durations of attention +
-// merge) 8 rows per wave lead up to 4k rows of capacity (4096: 5.1 + 4.7 µs
-// against 6.5 + 4.0 µs) and tie the attention at 8k, where 16 rows per wave
-// halve the merge (4.7 against 7.3 µs).
-static int attn_rpw(int cap) { return cap <= 4096 ? 8 : 16; }
+// MI355X (18 layers, 16 q / 2 kv heads; attention + merge back to back) 8
+// rows per wave lead up to ~2k rows of capacity; at 4096 rows 16 per wave
+// are ahead (8.7 against 9.3 µs) and at 8192 they tie the attention while
+// halving the records to merge.
+static int attn_rpw(int cap) { return cap <= 2048 ? 8 : 16; }
 // one split per 4·rpw rows of capacity
 static int attn_nsplit(int cap, int rpw) { return std::max(1, (cap + 4 * rpw - 1) / (4 * rpw)); }
 
