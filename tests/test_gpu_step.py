@@ -65,6 +65,33 @@ def test_step_logits_and_kv(orc, ctx, cfg, qtype, quirk):
         _close(gv.reshape(10, -1), ov.reshape(10, -1), 1e-4)
 
 
+@pytest.mark.parametrize("qtype", [Q4, Q6], ids=["q4", "q6"])
+@pytest.mark.parametrize("quirk", [True, False], ids=["quirk", "noquirk"])
+def test_step_unfused_oproj(orc, ctx, monkeypatch, qtype, quirk):
+    """At the decoder's shape the step folds the attention merge into o_proj
+    (per-head partial rows summed by the gate/up prologue).  The two-launch
+    path (merge, then the o_proj GEMV with its residual epilogue) must meet
+    the same bar against the oracle, and both paths must pick the same
+    tokens."""
+    w, om, gm = _pair(orc, ctx, MID, qtype, quirk=quirk)
+    monkeypatch.setenv("POCR_FUSED_OPROJ", "0")
+    os_, gs = om.seq(16), gm.seq(16)
+    monkeypatch.delenv("POCR_FUSED_OPROJ")
+    fs = gm.seq(16)
+    for p in range(8):  # first-token, 1..5 and >=6 branches
+        emb = w["embed"][(5 * p + 1) % MID.vocab]
+        ot, ol, _ = os_.step(emb, (p, p, p))
+        monkeypatch.setenv("POCR_FUSED_OPROJ", "0")
+        gt, gl = gs.step(emb, (p, p, p))
+        monkeypatch.delenv("POCR_FUSED_OPROJ")
+        ft, fl = fs.step(emb, (p, p, p))
+        for t, l in ((gt, gl), (ft, fl)):
+            assert np.max(np.abs(l - ol)) < 1e-2
+            assert np.sqrt(np.mean((l - ol) ** 2)) <= 1e-3 * np.sqrt(np.mean(ol ** 2))
+            assert_same_choice(t, ot, l, ol)
+        assert gt == ft or abs(float(fl[ft]) - float(fl[gt])) <= 2 * float(np.max(np.abs(fl - gl))), (gt, ft)
+
+
 @pytest.mark.parametrize("qtype", [Q8, Q4, Q6], ids=["q8", "q4", "q6"])
 def test_non_final_prompt_tokens(orc, ctx, qtype):
     w, om, gm = _pair(orc, ctx, MID, qtype)
