@@ -286,16 +286,21 @@ static bool pick_big(int tag, bool one, int lpr, int cpl, const void **fn) {
 // count and its activation prologues as for one vector) and gives every wave
 // one group
 template <int QT, int NV>
-static bool pick_nv(int nmat, bool big, int lpr, int cpl, const void **fn) {
+static bool pick_nv(int nmat, int u, int lpr, int cpl, const void **fn) {
     if (nmat == 2) return gemv_fast_kernel<QT, 2, 2, 0, false, 3, NV>(lpr, cpl, fn);
-    if (big) return gemv_fast_kernel<QT, 1, kBigU, 0, true, 3, NV>(lpr, cpl, fn);
+    if (u == kBigU) return gemv_fast_kernel<QT, 1, kBigU, 0, true, 3, NV>(lpr, cpl, fn);
+    if (u == 1) {  // only the down projection's shape takes one row per lane group here
+        if (lpr != 32 || cpl != 3) return false;
+        *fn = gemv_fn<QT, 32, 3, 1, 1, 0, false, 3, NV>();
+        return true;
+    }
     return gemv_fast_kernel<QT, 1, 2, 0, false, 3, NV>(lpr, cpl, fn);
 }
 
 template <int QT>
 static bool pick_fast(int nmat, int u, int tag, int lpr, int cpl, bool one, int nv, const void **fn) {
-    if (nv == 2) return pick_nv<QT, 2>(nmat, u != 2, lpr, cpl, fn);
-    if (nv == 4) return pick_nv<QT, 4>(nmat, u != 2, lpr, cpl, fn);
+    if (nv == 2) return pick_nv<QT, 2>(nmat, u, lpr, cpl, fn);
+    if (nv == 4) return pick_nv<QT, 4>(nmat, u, lpr, cpl, fn);
     if (nmat == 2) return gemv_fast_kernel<QT, 2, 2>(lpr, cpl, fn);
     if (u == kBigU) return pick_big<QT>(tag, one, lpr, cpl, fn);
     if (u == 1) return tag == 1 ? gemv_fast_kernel<QT, 1, 1, 1>(lpr, cpl, fn) : gemv_fast_kernel<QT, 1, 1>(lpr, cpl, fn);
@@ -342,7 +347,7 @@ static int plan_gemv(int qtype, int nmat, int rows, int cols, const DevMat *mats
     // workgroups (the down projection's 1024 rows of 3072 columns): the
     // shorter rows of work per wave beat the longer pipeline there
     int u = big ? kBigU : 2;
-    if (fast && !big && nmat == 1 && nv == 1) {
+    if (fast && !big && nmat == 1 && (nv == 1 || (lpr == 32 && cpl == 3))) {
         const int groups2 = (rows + (64 / lpr) * 2 - 1) / ((64 / lpr) * 2);
         if ((groups2 + kWaves - 1) / kWaves < 128) u = 1;
     }
