@@ -120,6 +120,14 @@ void pocr_weight_free(pocr_weight *w);
 /* VulkanMatVecQ{8,6,4} (vulkan_exec_stub.go:186,234,282): out[m][rows] = W·x[m].
  * m > 1 is the batched GEMV (M rows of activations sharing one weight stream). */
 int pocr_matvec(pocr_ctx *ctx, const pocr_weight *w, const float *x, int m, float *out);
+/* MatVecQ4/MatVecQ6 as the reference's CPU path computes them on an
+ * AVX512-VNNI host (quantizeXForVNNI internal/tensor/quant.go:2087-2115,
+ * quantizeXForVNNIAVX2 dot_amd64.go:228-252, dotQ8VNNI dot_amd64.go:150-167,
+ * finalizeDotQ8VNNI dot_vnni_amd64.s:1043-1080): each row of x quantized to
+ * u8 with one scale, exact int32 dots, out = ((dot - 128*rowSum)*scaleX)*scale[r].
+ * Bit-identical to that path.  Q8 matrices and inputs of fewer than 32
+ * columns are computed in plain mode, as there. */
+int pocr_matvec_vnni(pocr_ctx *ctx, const pocr_weight *w, const float *x, int m, float *out);
 /* VulkanMatVecArgmaxQ* (vulkan_exec_stub.go:190,238,286): greedy LM head,
  * ties → lowest index (internal/tensor/argmax_quant.go:255-262) */
 int pocr_matvec_argmax(pocr_ctx *ctx, const pocr_weight *w, const float *x, int32_t *index,
@@ -275,6 +283,14 @@ int pocr_model_set_embed(pocr_model *m, const float *embed);
 /* reproduce the reference's Q4/Q6 attention-residual behaviour
  * (internal/model/model.go:3895-3902, 4051-4057); default on */
 int pocr_model_set_residual_quirk(pocr_model *m, int on);
+/* Every Q4/Q6 matvec of the model's decode steps and LM head in the VNNI
+ * activation mode above, as the reference's CPU path runs on an
+ * AVX512-VNNI host (dot_amd64.go:12 selects it; UnpackQ4Matrix/Q6 keep the
+ * row sums it needs, quant.go:2325); default off (plain mode).  Set it before
+ * the model's first sequence (POCR_ERR_ARG after).  In this mode prompts run
+ * token by token (pocr_prefill and the batched decode return
+ * POCR_ERR_UNSUPPORTED). */
+int pocr_model_set_vnni(pocr_model *m, int on);
 
 /* per-sequence state: per-layer fp32 K/V in HBM preallocated for `capacity`
  * tokens (getKVCaches, internal/model/model.go:3286-3327) */

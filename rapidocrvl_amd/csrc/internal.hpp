@@ -108,6 +108,7 @@ struct pocr_model {
     std::vector<double> h_freq;
     std::vector<uint8_t> h_axis;
     int quirk = 1;
+    int vnni = 0;  // Q4/Q6 matvecs in the reference's VNNI activation mode (vnni.hpp)
 };
 
 
@@ -165,6 +166,9 @@ DevMat dev_mat(const pocr_weight *w);
 int gemv_launch(hipStream_t s, GemvParams p, int nmat, int pro, int epi, int max_grid, int nv = 1,
                 const GemvNV *q = nullptr);
 GemvParams gemv_params_1(const pocr_weight *w);
+// the same GEMV in the reference's VNNI activation mode for Q4/Q6 matrices of
+// at least 32 columns (vnni.hpp); other matrices take gemv_launch
+int gemv_launch_vnni(hipStream_t s, const GemvParams &p, int nmat, int pro, int epi, int max_grid);
 int step_locked(pocr_seq *s, const float *emb, const int32_t pos3[3], int need_logits, float *logits,
                 int32_t *token);
 int prefill_locked(pocr_seq *s, int n, const float *emb, const int32_t *pos3, float *logits, int32_t *token);

@@ -8,6 +8,7 @@
 #include <cmath>
 
 #include "gemm.hpp"
+#include "vnni.hpp"
 #include "head.hpp"
 #include "internal.hpp"
 
@@ -539,6 +540,46 @@ int pocr::gemv_launch(hipStream_t s, GemvParams p, int nmat, int pro, int epi, i
     return launch_gemv(s, plan, p, pro, epi, nv > 1 ? *q : GemvNV{});
 }
 
+// VNNI mode: rows on 16-byte (Q4) or 4-byte (Q6) boundaries in whole chunks
+// take the chunked row loop, anything else the code-at-a-time one.
+static bool vnni_fast_shape(const DevMat &m) {
+    if (m.qtype == POCR_Q4)
+        return m.cols % 32 == 0 && m.row_bytes == m.cols / 2 && ((uintptr_t)m.data) % 16 == 0;
+    return m.cols % 16 == 0 && m.row_bytes == m.cols / 16 * 12 && ((uintptr_t)m.data) % 4 == 0;
+}
+
+template <int QT>
+static const void *vnni_fn(int nmat, bool fast) {
+    if (nmat == 2)
+        return fast ? reinterpret_cast<const void *>(&k_gemv_vnni<QT, 2, true>)
+                    : reinterpret_cast<const void *>(&k_gemv_vnni<QT, 2, false>);
+    return fast ? reinterpret_cast<const void *>(&k_gemv_vnni<QT, 1, true>)
+                : reinterpret_cast<const void *>(&k_gemv_vnni<QT, 1, false>);
+}
+
+int pocr::gemv_launch_vnni(hipStream_t s, const GemvParams &p, int nmat, int pro, int epi, int max_grid) {
+    const int qt = p.m[0].qtype;
+    // Q8 and inputs under 32 columns stay in plain mode (quant.go:2087-2115)
+    if (qt == POCR_Q8 || p.cols < 32) return gemv_launch(s, p, nmat, pro, epi, max_grid);
+    if (pro == PRO_OPART || epi == EPI_DOWNV)
+        return fail(POCR_ERR_UNSUPPORTED, "gemv (VNNI mode): the partial-sum prologue is plain-mode only");
+    if (p.cols > kVnniMaxCols) return fail(POCR_ERR_UNSUPPORTED, "gemv (VNNI mode): cols %d > %d", p.cols, kVnniMaxCols);
+    const int nm = nmat == 2 ? 2 : (p.seg_end[0] == p.rows ? 1 : (p.seg_end[1] == p.rows ? 2 : 3));
+    bool fast = true;
+    for (int i = 0; i < nm; ++i) {
+        if (p.m[i].qtype != qt || p.m[i].cols != p.cols)
+            return fail(POCR_ERR_ARG, "gemv (VNNI mode): matrices of one launch differ in type or columns");
+        fast = fast && vnni_fast_shape(p.m[i]);
+    }
+    const void *fn = qt == POCR_Q4 ? vnni_fn<QT_Q4>(nmat, fast) : vnni_fn<QT_Q6>(nmat, fast);
+    const int grid = std::max(1, std::min({(p.rows + 2 * kWaves - 1) / (2 * kWaves), kVnniMaxGrid, max_grid}));
+    const size_t lds = (size_t)p.cols * 4 + (((size_t)p.cols + 15) & ~(size_t)15);
+    GemvParams a = p;
+    void *args[] = {&a, &pro, &epi};
+    HIP_TRY(hipLaunchKernel(fn, dim3(grid), dim3(kThreads), args, lds, s));
+    return POCR_OK;
+}
+
 
 // ---------------------------------------------------------------------------
 // op level
@@ -614,6 +655,26 @@ extern "C" int pocr_matvec(pocr_ctx *ctx, const pocr_weight *w, const float *x, 
     RC(ctx->out.ensure((size_t)m * w->rows * 4));
     RC(h2d(s, ctx->x.p, x, (size_t)m * w->cols * 4));
     RC(matvec_rows(ctx, w, ctx->x.as<float>(), m, ctx->out.as<float>()));
+    RC(d2h(s, out, ctx->out.p, (size_t)m * w->rows * 4));
+    return sync(s);
+}
+
+// m rows of x against one weight in the VNNI activation mode (Q8: plain)
+extern "C" int pocr_matvec_vnni(pocr_ctx *ctx, const pocr_weight *w, const float *x, int m, float *out) {
+    if (!ctx || !w || !x || !out || m <= 0) return fail(POCR_ERR_ARG, "pocr_matvec_vnni: bad arguments");
+    if (w->ctx != ctx) return fail(POCR_ERR_ARG, "pocr_matvec_vnni: weight from another context");
+    CHECK_INJECT("matvec_vnni");
+    CTX_GUARD(ctx);
+    hipStream_t s = ctx->stream;
+    RC(ctx->x.ensure((size_t)m * w->cols * 4));
+    RC(ctx->out.ensure((size_t)m * w->rows * 4));
+    RC(h2d(s, ctx->x.p, x, (size_t)m * w->cols * 4));
+    for (int r = 0; r < m; ++r) {
+        GemvParams p = gemv_params_1(w);
+        p.x = ctx->x.as<float>() + (size_t)r * w->cols;
+        p.out = ctx->out.as<float>() + (size_t)r * w->rows;
+        RC(gemv_launch_vnni(s, p, 1, PRO_COPY, EPI_PLAIN, kBigGrid));
+    }
     RC(d2h(s, out, ctx->out.p, (size_t)m * w->rows * 4));
     return sync(s);
 }
@@ -1629,6 +1690,15 @@ extern "C" int pocr_model_set_residual_quirk(pocr_model *m, int on) {
     return POCR_OK;
 }
 
+// The activation mode is fixed before the model's first sequence: captured
+// decode graphs hold the mode's kernels.
+extern "C" int pocr_model_set_vnni(pocr_model *m, int on) {
+    if (!m) return fail(POCR_ERR_ARG, "pocr_model_set_vnni: null model");
+    if (m->refs.load() != 1) return fail(POCR_ERR_ARG, "pocr_model_set_vnni: set the mode before creating sequences");
+    m->vnni = on ? 1 : 0;
+    return POCR_OK;
+}
+
 static int model_ready(const pocr_model *m) {
     for (int l = 0; l < m->cfg.layers; ++l) {
         for (int r = 0; r < 7; ++r)
@@ -2123,11 +2193,19 @@ static int launch_merge_oproj(hipStream_t st, const AttnParams &a, const pocr_we
     return POCR_OK;
 }
 
+// the model's GEMV: plain mode, or the VNNI activation mode (vnni.hpp)
+static int model_gemv(const pocr_model *m, hipStream_t st, const GemvParams &p, int nmat, int pro, int epi) {
+    return m->vnni ? gemv_launch_vnni(st, p, nmat, pro, epi, kBigGrid) : gemv_launch(st, p, nmat, pro, epi, kBigGrid);
+}
+
 static int enqueue_layer(pocr_seq *s, int li, bool last, bool kv_only) {
     pocr_model *m = s->m;
     const pocr_config &c = m->cfg;
     hipStream_t st = m->ctx->stream;
     const LayerW &L = m->layers[li];
+    if (m->vnni && (c.head_dim != kHD || s->cap > kOrdMaxRows))
+        return fail(POCR_ERR_UNSUPPORTED, "VNNI mode: head_dim %d, capacity %d (128 and at most %d)", c.head_dim,
+                    s->cap, kOrdMaxRows);
     const int q_rows = c.heads * c.head_dim, kv_rows = c.kv_heads * c.head_dim;
     const float eps = c.rms_norm_eps;
 
@@ -2146,7 +2224,7 @@ static int enqueue_layer(pocr_seq *s, int li, bool last, bool kv_only) {
     p.eps = eps;
     p.out = s->qkv;
     p.st = s->st;
-    RC(gemv_launch(st, p, 1, PRO_RMSNORM, EPI_PLAIN, kBigGrid));
+    RC(model_gemv(m, st, p, 1, PRO_RMSNORM, EPI_PLAIN));
 
     // 2. RoPE + KV append + split-K attention → head_out
     AttnParams a{};
@@ -2165,7 +2243,7 @@ static int enqueue_layer(pocr_seq *s, int li, bool last, bool kv_only) {
     launch_attn_decode(st, s->rpw, dim3(c.kv_heads, s->nsplit), a);
     const pocr_weight *wo = L.w[POCR_W_O];
     const int quirk = (m->quirk && (wo->qtype == POCR_Q4 || wo->qtype == POCR_Q6)) ? 1 : 0;
-    if (!kv_only && fused_oproj(m, L)) {
+    if (!kv_only && !m->vnni && fused_oproj(m, L)) {
         // 2'. merge + o_proj partials per head; gate/up sums them with the
         // residual (PRO_OPART), down takes residual + attention when in place
         RC(launch_merge_oproj(st, a, wo, s->opart, c.heads));
@@ -2189,7 +2267,12 @@ static int enqueue_layer(pocr_seq *s, int li, bool last, bool kv_only) {
         d.quirk = quirk;
         return gemv_launch(st, d, 1, PRO_COPY, EPI_DOWNV, kBigGrid);
     }
-    hipLaunchKernelGGL(k_attn_merge, dim3(c.heads), dim3(kMergeThreads), 0, st, a);
+    if (m->vnni) {
+        // the reference's summation order (vnni.hpp): the split records are unused
+        if (!kv_only) hipLaunchKernelGGL(k_attn_ordered, dim3(c.heads), dim3(kThreads), (size_t)s->cap * 4, st, a);
+    } else {
+        hipLaunchKernelGGL(k_attn_merge, dim3(c.heads), dim3(kMergeThreads), 0, st, a);
+    }
     HIP_TRY(hipGetLastError());
     if (kv_only) return POCR_OK;
 
@@ -2200,7 +2283,7 @@ static int enqueue_layer(pocr_seq *s, int li, bool last, bool kv_only) {
     o.vbuf = s->vbuf;
     o.st = s->st;
     o.quirk = quirk;
-    RC(gemv_launch(st, o, 1, PRO_COPY, EPI_OPROJ, kBigGrid));
+    RC(model_gemv(m, st, o, 1, PRO_COPY, EPI_OPROJ));
 
     // 4. RMSNorm(vbuf)·ln2 → gate/up → SiLU(g)·u
     GemvParams gu = gemv_params_1(L.w[POCR_W_GATE]);
@@ -2210,7 +2293,7 @@ static int enqueue_layer(pocr_seq *s, int li, bool last, bool kv_only) {
     gu.eps = eps;
     gu.out = s->g;
     gu.st = s->st;
-    RC(gemv_launch(st, gu, 2, PRO_RMSNORM, EPI_SWIGLU, kBigGrid));
+    RC(model_gemv(m, st, gu, 2, PRO_RMSNORM, EPI_SWIGLU));
 
     // 5. down + residual: h += W_down·g (in place); last layer: vbuf = h + down (OutOnly)
     GemvParams d = gemv_params_1(L.w[POCR_W_DOWN]);
@@ -2219,7 +2302,7 @@ static int enqueue_layer(pocr_seq *s, int li, bool last, bool kv_only) {
     d.vbuf = s->vbuf;
     d.st = s->st;
     d.flag = last ? 1 : 0;
-    RC(gemv_launch(st, d, 1, PRO_COPY, EPI_DOWN, kBigGrid));
+    RC(model_gemv(m, st, d, 1, PRO_COPY, EPI_DOWN));
     return POCR_OK;
 }
 
@@ -2233,12 +2316,12 @@ int pocr::enqueue_lm_head(pocr_seq *s, const float *x, bool want_logits) {
     p.st = s->st;
     if (!s->sampling) {
         p.out = want_logits ? s->logits : nullptr;
-        return gemv_launch(st, p, 1, PRO_RMSNORM, EPI_ARGMAX, kBigGrid);
+        return model_gemv(m, st, p, 1, PRO_RMSNORM, EPI_ARGMAX);
     }
     // matVecTopKMaybeCPU (model.go:7202-7235): every score, then the top-k
     // and the draw (sampleCandidateScoresScratch, 1950-1990)
     p.out = s->logits;
-    RC(gemv_launch(st, p, 1, PRO_RMSNORM, EPI_PLAIN, kBigGrid));
+    RC(model_gemv(m, st, p, 1, PRO_RMSNORM, EPI_PLAIN));
     const int vocab = m->cfg.vocab;
     if (s->top_k >= 2 && s->top_k <= kTopKMax)
         return enqueue_topk(st, s->logits, vocab, s->top_k, s->topk_part, s->samp, s->st, 1);
@@ -2807,6 +2890,7 @@ extern "C" int pocr_decode_batch(pocr_seq *const *seqs, int n_seq, const int32_t
     for (int i = 0; i < n_seq; ++i) out_counts[i] = 0;
     if (max_new <= 0) return POCR_OK;
     RC(model_ready(m));
+    if (m->vnni) return fail(POCR_ERR_UNSUPPORTED, "pocr_decode_batch: the batched kernels compute plain mode only");
     CHECK_INJECT("decode_batch");
     std::lock_guard<std::mutex> lk(m->ctx->mu);
     for (int i = 0; i < n_seq; ++i) RC(seq_idle(seqs[i], "pocr_decode_batch"));
@@ -2972,6 +3056,7 @@ extern "C" int pocr_batch_join(pocr_batch *b, pocr_seq *s, int32_t first_token, 
     if (s->m != b->m) return fail(POCR_ERR_ARG, "pocr_batch_join: the sequence belongs to another model");
     if (first_token < 0 || first_token >= b->m->cfg.vocab) return fail(POCR_ERR_ARG, "pocr_batch_join: token out of vocab");
     RC(model_ready(b->m));
+    if (b->m->vnni) return fail(POCR_ERR_UNSUPPORTED, "pocr_batch_join: the batched kernels compute plain mode only");
     CHECK_INJECT("batch_join");
     std::lock_guard<std::mutex> lk(b->m->ctx->mu);
     HIP_TRY(hipSetDevice(b->m->ctx->device));
@@ -3118,6 +3203,7 @@ extern "C" int pocr_prefill(pocr_seq *s, int n, const float *emb, const int32_t 
     RC(seq_idle(s, "pocr_prefill"));
     HIP_TRY(hipSetDevice(s->m->ctx->device));
     if (s->len + n > s->cap) return fail(POCR_ERR_ARG, "pocr_prefill: %d rows exceed capacity", n);
+    if (s->m->vnni) return fail(POCR_ERR_UNSUPPORTED, "pocr_prefill: the batched prefill computes plain mode only");
     return prefill_locked(s, n, emb, pos3, logits, token);
 }
 
@@ -3162,6 +3248,9 @@ int pocr::generate_locked(pocr_seq *s, const int32_t *ids, int n_ids, const floa
     if (n_ids + max_new - 1 > s->cap) return fail(POCR_ERR_ARG, "pocr_generate: capacity %d too small", s->cap);
     if (s->sampling) RC(seed_sampler(s));  // one generator per generation call
     int32_t next = -1;
+    // VNNI mode: the prompt goes token by token, as the reference's CPU path
+    // takes it (the batched prefill computes plain mode only)
+    if (m->vnni) use_prefill = 0;
     if (use_prefill) {
         const int rc = prefill_ids_locked(s, ids, n_ids, n_image > 0 ? image_embeds : nullptr,
                                           n_image > 0 ? image_token_id : -1, pos.data(), nullptr, &next, image_dev);

@@ -64,6 +64,7 @@ _SIGS = {
     "pocr_weight_upload": (_i, [_vp, _i, _i, _i, _vp, _vp, C.POINTER(_vp)]),
     "pocr_weight_free": (None, [_vp]),
     "pocr_matvec": (_i, [_vp, _vp, _vp, _i, _vp]),
+    "pocr_matvec_vnni": (_i, [_vp, _vp, _vp, _i, _vp]),
     "pocr_matvec_argmax": (_i, [_vp, _vp, _vp, _vp, _vp]),
     "pocr_matvec_topk": (_i, [_vp, _vp, _vp, _i, _vp, _vp]),
     "pocr_sample_topk": (_i, [_vp, _vp, _i, _i, C.c_double, C.POINTER(C.c_uint64), _vp, _vp, _vp]),
@@ -90,6 +91,7 @@ _SIGS = {
     "pocr_model_set_norm": (_i, [_vp, _i, _i, _vp]),
     "pocr_model_set_embed": (_i, [_vp, _vp]),
     "pocr_model_set_residual_quirk": (_i, [_vp, _i]),
+    "pocr_model_set_vnni": (_i, [_vp, _i]),
     "pocr_seq_create": (_i, [_vp, _i, C.POINTER(_vp)]),
     "pocr_seq_destroy": (None, [_vp]),
     "pocr_seq_reset": (_i, [_vp]),
@@ -364,6 +366,14 @@ class Context:
         check(load().pocr_matvec(self.h, w.h, _ptr(x), m, _ptr(out)))
         return out[0] if x.ndim == 1 else out
 
+    def matvec_vnni(self, w: Weight, x):
+        """W·x in the reference's VNNI activation mode (Q8: plain)."""
+        x = _f32(x)
+        m = 1 if x.ndim == 1 else x.shape[0]
+        out = np.zeros((m, w.rows), np.float32)
+        check(load().pocr_matvec_vnni(self.h, w.h, _ptr(x), m, _ptr(out)))
+        return out[0] if x.ndim == 1 else out
+
     def matvec_argmax(self, w: Weight, x):
         x = _f32(x)
         idx = np.zeros(1, np.int32)
@@ -592,6 +602,10 @@ class Model:
 
     def set_residual_quirk(self, on: bool):
         check(load().pocr_model_set_residual_quirk(self.h, int(on)))
+
+    def set_vnni(self, on: bool):
+        """Q4/Q6 matvecs in the reference's VNNI activation mode (before any sequence)."""
+        check(load().pocr_model_set_vnni(self.h, int(on)))
 
     def load_weights(self, weights):
         roles = {"q": W_Q, "k": W_K, "v": W_V, "o": W_O, "gate": W_GATE, "up": W_UP, "down": W_DOWN}

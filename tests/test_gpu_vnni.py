@@ -1,0 +1,152 @@
+"""The reference's VNNI activation mode on the GPU (pocr_matvec_vnni,
+pocr_model_set_vnni) against the oracle's VNNI mode.
+
+The mode quantizes x once per matvec to u8 with one scale (quant.go:2087-2115,
+dot_amd64.go:228-252) and finishes each row from exact int32 sums
+(dot_vnni_amd64.s:1043-1080).  Every step is exact or one IEEE operation, so a
+matvec must equal the oracle bit for bit.  In this mode the step also sums
+RMSNorm's squares and the attention in the reference's order, so whole decode
+steps (logits, K/V rows) and greedy streams are bit-identical too: an ulp of
+difference upstream of a matvec would move an activation byte, and with it a
+whole row, by a step of the weights."""
+import numpy as np
+import pytest
+
+from rapidocrvl_amd import lib, synth
+from rapidocrvl_amd.config import ERNIE_0P3B, DecoderConfig
+
+pytestmark = pytest.mark.gpu
+
+Q8, Q4, Q6 = 1000, 1001, 1002
+MID = DecoderConfig(hidden=1024, inter=3072, layers=3, heads=16, kv_heads=2, head_dim=128, vocab=5000, eps=1e-5,
+                    rope_theta=500000.0)
+
+
+def _qmat(rng, rows, cols, qtype, std=0.02):
+    w = (rng.standard_normal((rows, cols)) * std).astype(np.float32)
+    return lib.QMatrix.quantize(w, qtype)
+
+
+@pytest.mark.parametrize("qtype", [Q4, Q6], ids=["q4", "q6"])
+@pytest.mark.parametrize("shape", [(3072, 1024), (1024, 3072), (2560, 1024), (103424, 1024)],
+                         ids=lambda s: f"{s[0]}x{s[1]}")
+def test_matvec_vnni_bit_exact_decoder_shapes(ctx, orc, rng, qtype, shape):
+    q = _qmat(rng, *shape, qtype)
+    x = rng.standard_normal(shape[1]).astype(np.float32)
+    got = ctx.matvec_vnni(ctx.upload(q), x)
+    want = orc.matvec(qtype, q.scales, q.packed, x, vnni=True)
+    assert np.array_equal(got, want)
+    # the mode is really a different arithmetic from plain mode
+    plain = orc.matvec(qtype, q.scales, q.packed, x)
+    assert not np.array_equal(want, plain)
+
+
+@pytest.mark.parametrize("qtype", [Q4, Q6], ids=["q4", "q6"])
+@pytest.mark.parametrize("shape", [(7, 33), (130, 100), (65, 96), (40, 4000), (17, 48), (9, 8192)])
+def test_matvec_vnni_bit_exact_odd_shapes(ctx, orc, rng, qtype, shape):
+    """Columns off the 32/16-column chunks take the code-at-a-time rows; both
+    loops produce the same integers."""
+    q = _qmat(rng, *shape, qtype, std=1.0)
+    x = (rng.standard_normal(shape[1]) * 3).astype(np.float32)
+    got = ctx.matvec_vnni(ctx.upload(q), x)
+    assert np.array_equal(got, orc.matvec(qtype, q.scales, q.packed, x, vnni=True))
+
+
+@pytest.mark.parametrize("qtype", [Q4, Q6], ids=["q4", "q6"])
+def test_matvec_vnni_rows_and_special_vectors(ctx, orc, rng, qtype):
+    q = _qmat(rng, 300, 1024, qtype)
+    w = ctx.upload(q)
+    xs = np.stack([
+        np.zeros(1024, np.float32),                          # m = 0: every byte 128, scaleX 1
+        rng.standard_normal(1024).astype(np.float32),
+        np.where(np.arange(1024) == 5, 7.5, 0.0).astype(np.float32),  # one spike: other bytes 128
+        (rng.standard_normal(1024) * 1e-30).astype(np.float32),       # tiny scale
+        np.full(1024, -2.0, np.float32),                     # |x| = max everywhere: bytes 1
+    ])
+    got = ctx.matvec_vnni(w, xs)
+    for i in range(xs.shape[0]):
+        assert np.array_equal(got[i], orc.matvec(qtype, q.scales, q.packed, xs[i], vnni=True)), i
+
+
+def test_matvec_vnni_plain_for_q8_and_narrow_inputs(ctx, orc, rng):
+    """Q8 has no row sums in the reference and keeps plain mode, as do inputs
+    of fewer than 32 columns."""
+    q = _qmat(rng, 512, 1024, Q8)
+    w = ctx.upload(q)
+    x = rng.standard_normal(1024).astype(np.float32)
+    assert np.array_equal(ctx.matvec_vnni(w, x), ctx.matvec(w, x))
+    for qt in (Q4, Q6):
+        q = _qmat(rng, 64, 31, qt, std=1.0)
+        w = ctx.upload(q)
+        x = rng.standard_normal(31).astype(np.float32)
+        assert np.array_equal(ctx.matvec_vnni(w, x), ctx.matvec(w, x))
+
+
+def _pair(orc, ctx, cfg, qtype, seed=3):
+    w = synth.make_weights(cfg, qtype, seed=seed)
+    om = orc.Model(cfg)
+    om.load_weights(w)
+    om.set_vnni(True)
+    gm = lib.Model(ctx, cfg)
+    gm.load_weights(w)
+    gm.set_vnni(True)
+    return w, om, gm
+
+
+@pytest.mark.parametrize("qtype", [Q4, Q6], ids=["q4", "q6"])
+@pytest.mark.parametrize("seed", [3, 4])
+def test_vnni_steps_match_oracle(orc, ctx, qtype, seed):
+    w, om, gm = _pair(orc, ctx, MID, qtype, seed=seed)
+    os_, gs = om.seq(16), gm.seq(16)
+    for p in range(10):  # first-token, 1..5 and >= 6 branches
+        emb = w["embed"][(7 * p + 3) % MID.vocab]
+        ot, ol, _ = os_.step(emb, (p, p, p))
+        gt, gl = gs.step(emb, (p, p, p))
+        # bit-identical logits: rows 1..10 of the cache cover the single row,
+        # the pair form, the 3-8 row trees and the running sum of Softmax
+        assert np.array_equal(gl, ol), (p, float(np.max(np.abs(gl - ol))))
+        assert gt == ot
+    for li in range(MID.layers):
+        gk, gv = gs.read_kv(li)
+        ok, ov = os_.kv(li)
+        assert np.array_equal(gk.reshape(10, -1), ok.reshape(10, -1))
+        assert np.array_equal(gv.reshape(10, -1), ov.reshape(10, -1))
+    gs.close()
+    gm.close()
+
+
+@pytest.mark.parametrize("qtype", [Q4, Q6], ids=["q4", "q6"])
+def test_vnni_generation_ernie(orc, ctx, qtype):
+    """The 0.3B decoder, 64 prompt ids from [0, 100000) with seed 0, 16 greedy
+    tokens in VNNI mode: the oracle's stream in the same mode (the prompt goes
+    token by token in this mode, even when the prefill is asked for)."""
+    cfg = ERNIE_0P3B
+    w, om, gm = _pair(orc, ctx, cfg, qtype, seed=0)
+    ids = synth.prompt_ids(64, seed=0)
+    want = om.generate(ids, 16, eos=())
+    s = gm.seq(96)
+    got = s.generate(ids, 16, eos=(), use_prefill=True)
+    assert list(got) == list(want)
+    assert len(s) == 64 + 15
+    s.close()
+    gm.close()
+
+
+def test_vnni_mode_rules(ctx, rng):
+    cfg = DecoderConfig(hidden=128, inter=192, layers=2, heads=4, kv_heads=2, head_dim=128, vocab=300, eps=1e-5,
+                        rope_theta=500000.0)
+    w = synth.make_weights(cfg, Q4, seed=1)
+    gm = lib.Model(ctx, cfg)
+    gm.load_weights(w)
+    gm.set_vnni(True)
+    s = gm.seq(16)
+    # fixed before the first sequence
+    with pytest.raises(lib.PocrError) as e:
+        gm.set_vnni(False)
+    assert e.value.code == lib.POCR_ERR_ARG
+    # the batched prefill and decode compute plain mode only
+    with pytest.raises(lib.PocrError) as e:
+        s.prefill(w["embed"][:3], np.zeros((3, 3), np.int32))
+    assert e.value.code == lib.POCR_ERR_UNSUPPORTED
+    s.close()
+    gm.close()
