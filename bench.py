@@ -445,7 +445,31 @@ def roofline_only(args):
                       "frac_of_stream_read": round(stream_us / us, 4)}), flush=True)
 
 
-def cpu_baseline(cfg, weights, gpu_seq, first_tok, first_pos, gpu_tokens, n_prefix, budget_s=12.0):
+def vnni_decode(ctx, cfg, weights, seq, first_tok, first_pos, n_prefix, n_tokens, steps):
+    """The same Q4 greedy decode in the reference's VNNI activation mode
+    (pocr_model_set_vnni: u8 activations for every Q4 matvec, bit-identical
+    to the reference's CPU numerics on an AVX512-VNNI host), from the same
+    1345-row KV state, on its own copy of the weights."""
+    from rapidocrvl_amd import lib
+
+    m = lib.Model(ctx, cfg)
+    m.load_weights(weights)
+    m.set_vnni(True)
+    s = m.seq(n_prefix + n_tokens + 8)
+    rows = n_prefix * cfg.kv_heads * cfg.head_dim
+    for li in range(cfg.layers):
+        k, v = seq.read_kv(li)
+        s.write_kv(li, k[:rows], v[:rows], n_prefix)
+    dt, toks = time_decode(s, n_prefix, first_tok, first_pos, n_tokens, 1, steps)
+    s.close()
+    m.close()
+    computed = n_tokens - 1
+    return {"value": round(computed * steps / dt, 1), "unit": "tok/s",
+            "us_per_token": round(dt / steps / computed * 1e6, 1)}, [int(t) for t in toks]
+
+
+def cpu_baseline(cfg, weights, gpu_seq, first_tok, first_pos, gpu_tokens, n_prefix, budget_s=12.0,
+                 gpu_vnni_tokens=None):
     import oracle
 
     threads = min(16, os.cpu_count() or 1)
@@ -485,7 +509,8 @@ def cpu_baseline(cfg, weights, gpu_seq, first_tok, first_pos, gpu_tokens, n_pref
                       f"(oracle, C restatement of the pure-Go CPU path, {threads} threads)",
             "tokens_match_gpu": bool(match),
             "vnni_emulation": {"value": round(nv / dtv, 2), "unit": "tok/s", "steps": nv,
-                               "tokens_match_gpu": toksv[: nv + 1] == list(gpu_tokens[: nv + 1])}}
+                               "tokens_match_gpu_vnni_mode": (None if gpu_vnni_tokens is None else
+                                                              toksv[: nv + 1] == list(gpu_vnni_tokens[: nv + 1]))}}
 
 
 GEMV_SHAPES = {"gate_up": (3072, 1024), "down": (1024, 3072), "qkv": (2560, 1024), "lm_head": (103424, 1024)}
@@ -775,9 +800,13 @@ def main():
     stream_us = stream_read_ceiling(ctx, int(alg))
     log(f"[bench] plain streaming read of the same {alg} bytes: {stream_us:.2f} us")
 
+    extra = {}
+    extra["vnni_decode"], vnni_toks = vnni_decode(ctx, cfg, weights, seq, first_tok, first_pos, n_prefix,
+                                                  args.decode_tokens, max(1, args.steps // 2))
+    log(f"[bench] q4 decode in the VNNI activation mode {extra['vnni_decode']}")
     cpu = None
     if not args.no_cpu:
-        cpu = cpu_baseline(cfg, weights, seq, first_tok, first_pos, toks, n_prefix)
+        cpu = cpu_baseline(cfg, weights, seq, first_tok, first_pos, toks, n_prefix, gpu_vnni_tokens=vnni_toks)
         log(f"[bench] cpu baseline {cpu}")
         # the other configurations' CPU legs: GEMV sweep, decode attention,
         # four concurrent single-sequence workers
@@ -787,7 +816,6 @@ def main():
                                                                              n_prefix, toks)}
         log(f"[bench] cpu per-config baselines {cpu['per_config']}")
 
-    extra = {}
     if not args.no_batch:
         extra["batch4_decode"] = {"q4": batch_decode(model, cfg, n_new=args.batch_tokens)}
         log(f"[bench] 4-sequence batched decode q4 {extra['batch4_decode']['q4']}")
