@@ -709,6 +709,8 @@ def main():
     ap.add_argument("--attention-only", action="store_true",
                     help="time only the decode attention + merge at 1k/4k/8k cache rows")
     ap.add_argument("--serve-only", action="store_true", help="time only the 8-request serving comparison")
+    ap.add_argument("--vnni-only", action="store_true",
+                    help="time only the Q4 decode in the VNNI activation mode (after the plain-mode prefill)")
     ap.add_argument("--batch-tokens", type=int, default=1024, help="tokens per sequence of the batched decode")
     ap.add_argument("--batch-seqs", default="4,8,16", help="with --batch-only: batch sizes to time")
     ap.add_argument("--cpu-worker", help=argparse.SUPPRESS)  # one process of cpu_concurrent_workers
@@ -767,6 +769,12 @@ def main():
                           "prefill_tok_s": round(n_prefix / t_prefill, 1),
                           "prefill_TFLOP_s": round(prefill_flops(cfg, n_prefix) / t_prefill / 1e12, 2),
                           "first_token": first_tok}), flush=True)
+        return
+    if args.vnni_only:
+        vd, _ = vnni_decode(ctx, cfg, weights, seq, first_tok, first_pos, n_prefix, args.decode_tokens,
+                            max(1, args.steps // 2))
+        print(json.dumps({"workload": f"q4 greedy decode in the VNNI activation mode, {args.decode_tokens - 1} token "
+                                      f"steps after a {n_prefix}-token prefill", **vd}), flush=True)
         return
     dt, toks = time_decode(seq, n_prefix, first_tok, first_pos, args.decode_tokens, args.warmup, args.steps)
     # a step returns decode_tokens tokens, the first of them the prefill's: it

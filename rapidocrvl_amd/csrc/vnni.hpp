@@ -113,9 +113,17 @@ __device__ __forceinline__ void stage_x_rms_ordered(float *xs, const float *x, c
     for (int i = threadIdx.x; i < n; i += kThreads) xs[i] = x[i];
     __syncthreads();
     const int n8 = n & ~7;
-    if (threadIdx.x < 8) {
+    if (threadIdx.x < 8) {  // sum j: columns j, j + 8, … in order, 16 reads in flight
         float s = 0.0f;
-        for (int i = threadIdx.x; i < n8; i += 8) s = s + xs[i] * xs[i];
+        int i = threadIdx.x;
+        for (; i + 8 * 15 < n8; i += 8 * 16) {
+            float v[16];
+#pragma unroll
+            for (int k = 0; k < 16; ++k) v[k] = xs[i + 8 * k];
+#pragma unroll
+            for (int k = 0; k < 16; ++k) s = s + v[k] * v[k];
+        }
+        for (; i < n8; i += 8) s = s + xs[i] * xs[i];
         red[threadIdx.x] = s;
     }
     __syncthreads();
@@ -306,9 +314,17 @@ __global__ void __launch_bounds__(kThreads) k_attn_ordered(AttnParams a) {
                 if (len >= 6) sum = sum + (sc[4] + sc[5]);
                 if (len == 7) sum = sum + sc[6];
                 if (len == 8) sum = sum + (sc[6] + sc[7]);
-            } else {
+            } else {  // one running sum in row order, 16 reads in flight
                 sum = 0.0f;
-                for (int t = 0; t < len; ++t) sum = sum + sc[t];
+                int t = 0;
+                for (; t + 16 <= len; t += 16) {
+                    float v[16];
+#pragma unroll
+                    for (int k = 0; k < 16; ++k) v[k] = sc[t + k];
+#pragma unroll
+                    for (int k = 0; k < 16; ++k) sum = sum + v[k];
+                }
+                for (; t < len; ++t) sum = sum + sc[t];
             }
             s_inv = 1.0f / sum;
         }
@@ -320,7 +336,15 @@ __global__ void __launch_bounds__(kThreads) k_attn_ordered(AttnParams a) {
     if (threadIdx.x < 128) {
         const int d = threadIdx.x;
         float acc = sc[0] * vc[d];
-        for (int t = 1; t < len; ++t) acc = acc + sc[t] * vc[(size_t)t * kvd + d];
+        int t = 1;
+        for (; t + 32 <= len; t += 32) {  // 32 value rows in flight, added in row order
+            float v[32];
+#pragma unroll
+            for (int k = 0; k < 32; ++k) v[k] = vc[(size_t)(t + k) * kvd + d];
+#pragma unroll
+            for (int k = 0; k < 32; ++k) acc = acc + sc[t + k] * v[k];
+        }
+        for (; t < len; ++t) acc = acc + sc[t] * vc[(size_t)t * kvd + d];
         out[d] = acc;
     }
 }
