@@ -150,3 +150,21 @@ def test_vnni_mode_rules(ctx, rng):
     assert e.value.code == lib.POCR_ERR_UNSUPPORTED
     s.close()
     gm.close()
+
+
+@pytest.mark.parametrize("top_k", [40, 0, 200], ids=["top40", "full", "top200"])
+def test_vnni_sampled_generation_ernie(orc, ctx, top_k):
+    """Sampled decoding in the VNNI mode: the logits are the oracle's to the
+    bit, so the candidate sets and draws (top-k ≤ 64, every logit, and the
+    wide sorted set) give the oracle's stream."""
+    cfg = ERNIE_0P3B
+    w, om, gm = _pair(orc, ctx, cfg, Q4, seed=0)
+    orc.set_threads(16)
+    ids = synth.prompt_ids(21, seed=10)
+    want = list(om.generate(ids, 16, eos=(), temperature=0.8, top_k=top_k, seed=5))
+    s = gm.seq(ids.size + 16)
+    s.set_sampling(0.8, top_k, 5)
+    got = list(s.generate(ids, 16, eos=(), use_prefill=True))
+    s.close()
+    gm.close()
+    assert got == want
