@@ -74,8 +74,21 @@ def batch_decode(model, cfg, n_seq=4, n_new=1024, reps=2):
         out = lib.decode_batch(seqs, firsts, poss, n_new, eos=())
         dt = time.perf_counter() - t
         assert all(len(o) == n_new for o in out)
+    # every member's first tokens against the same request decoded alone
+    # (pocr_decode_greedy, one sequence per step), after the timed runs
+    n_check = min(n_new, 256)
+    splits = []
+    for i, (s, n) in enumerate(zip(seqs, n_pre)):
+        s.truncate(n)
+        alone = s.decode_greedy(firsts[i], poss[i], n_check, eos=())
+        diff = np.nonzero(np.asarray(alone[:n_check]) != np.asarray(out[i][:n_check]))[0]
+        if diff.size:
+            splits.append({"sequence": i, "index": int(diff[0])})
+    for s in seqs:
+        s.close()
     return {"sequences": n_seq, "tokens_each": n_new, "context": f"{n_pre[0]}->{n_pre[0] + n_new}",
-            "tok_s": round(n_seq * n_new / dt, 1), "ms_per_step": round(dt / (n_new - 1) * 1e3, 4)}
+            "tok_s": round(n_seq * n_new / dt, 1), "ms_per_step": round(dt / (n_new - 1) * 1e3, 4),
+            "tokens_match_alone": not splits, "checked_tokens_each": n_check, "splits": splits}
 
 
 SERVE_BUDGETS = (512, 128, 384, 256, 640, 192, 448, 320)
