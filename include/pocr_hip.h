@@ -288,8 +288,8 @@ int pocr_model_set_residual_quirk(pocr_model *m, int on);
  * AVX512-VNNI host (dot_amd64.go:12 selects it; UnpackQ4Matrix/Q6 keep the
  * row sums it needs, quant.go:2325); default off (plain mode).  Set it before
  * the model's first sequence (POCR_ERR_ARG after).  In this mode prompts run
- * token by token (pocr_prefill and the batched decode return
- * POCR_ERR_UNSUPPORTED). */
+ * token by token (pocr_prefill and pocr_generate take their rows as token
+ * steps; the batched decode returns POCR_ERR_UNSUPPORTED). */
 int pocr_model_set_vnni(pocr_model *m, int on);
 
 /* per-sequence state: per-layer fp32 K/V in HBM preallocated for `capacity`

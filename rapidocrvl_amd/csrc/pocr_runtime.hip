@@ -3203,7 +3203,17 @@ extern "C" int pocr_prefill(pocr_seq *s, int n, const float *emb, const int32_t 
     RC(seq_idle(s, "pocr_prefill"));
     HIP_TRY(hipSetDevice(s->m->ctx->device));
     if (s->len + n > s->cap) return fail(POCR_ERR_ARG, "pocr_prefill: %d rows exceed capacity", n);
-    if (s->m->vnni) return fail(POCR_ERR_UNSUPPORTED, "pocr_prefill: the batched prefill computes plain mode only");
+    if (s->m->vnni) {
+        // VNNI mode: the rows go through token steps (the batched prefill
+        // computes plain mode), as the reference's CPU path takes a prompt
+        const int H = s->m->cfg.hidden;
+        for (int i = 0; i < n; ++i) {
+            const bool last = i == n - 1;
+            RC(step_locked(s, emb + (size_t)i * H, pos3 + 3 * i, last, last ? logits : nullptr,
+                           last ? token : nullptr));
+        }
+        return POCR_OK;
+    }
     return prefill_locked(s, n, emb, pos3, logits, token);
 }
 

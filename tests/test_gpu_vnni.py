@@ -144,11 +144,22 @@ def test_vnni_mode_rules(ctx, rng):
     with pytest.raises(lib.PocrError) as e:
         gm.set_vnni(False)
     assert e.value.code == lib.POCR_ERR_ARG
-    # the batched prefill and decode compute plain mode only
+    # the batched decode computes plain mode only
+    s2 = gm.seq(16)
     with pytest.raises(lib.PocrError) as e:
-        s.prefill(w["embed"][:3], np.zeros((3, 3), np.int32))
+        lib.decode_batch([s, s2], [1, 2], [0, 0], 4, eos=())
     assert e.value.code == lib.POCR_ERR_UNSUPPORTED
+    # pocr_prefill takes its rows as token steps: the same cache and logits
+    pos = np.array([[p, p, p] for p in range(3)], np.int32)
+    tok, lp = s.prefill(w["embed"][[5, 6, 7]], pos, want_logits=True)
+    for p in range(3):
+        ts, ls = s2.step(w["embed"][5 + p], pos[p])
+    assert tok == ts and np.array_equal(lp, ls)
+    for li in range(cfg.layers):
+        for a, b in zip(s.read_kv(li), s2.read_kv(li)):
+            assert np.array_equal(a, b)
     s.close()
+    s2.close()
     gm.close()
 
 
