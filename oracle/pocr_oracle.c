@@ -28,7 +28,6 @@
 
 #include <math.h>
 #include <pthread.h>
-#include <sched.h>
 #include <stdatomic.h>
 #include <stdlib.h>
 #include <string.h>
@@ -36,60 +35,113 @@
 /* ------------------------------------------------------------------ */
 /* thread pool — parallelForMax (ops.go:596-614): worker w gets rows   */
 /* [w*n/workers, (w+1)*n/workers)                                      */
+/*                                                                     */
+/* Goroutines cannot lose a job; this pool keeps that property:        */
+/*  - each worker is created knowing the job generation current at its */
+/*    creation, so a job posted before it first runs is still seen;    */
+/*  - an idle worker spins briefly, then parks on job_cv; the poster   */
+/*    bumps gen and broadcasts under mu, and a parking worker re-checks */
+/*    gen under mu, so no wake-up falls between check and wait;        */
+/*  - the caller waits for every worker to report the job (done_cv,    */
+/*    same discipline), so a worker never skips a generation;          */
+/*  - concurrent callers (ctypes releases the GIL) serialize on api,   */
+/*    and a call made from inside a job runs inline.                   */
 /* ------------------------------------------------------------------ */
 typedef void (*range_fn)(void *ctx, int start, int end);
 
 #define ORC_MAX_THREADS 256
+#define ORC_SPIN 4000
 static struct {
     int nthreads;
     pthread_t th[ORC_MAX_THREADS];
-    atomic_int gen;
+    atomic_uint gen;
     atomic_int done;
     atomic_int stop;
     range_fn fn;
     void *ctx;
     int n, workers;
-    pthread_mutex_t mu;
-} P = {.nthreads = 1, .mu = PTHREAD_MUTEX_INITIALIZER};
+    pthread_mutex_t api; /* one job (or one resize) at a time */
+    pthread_mutex_t mu;  /* guards the parks on job_cv / done_cv */
+    pthread_cond_t job_cv, done_cv;
+} P = {.nthreads = 1,
+       .api = PTHREAD_MUTEX_INITIALIZER,
+       .mu = PTHREAD_MUTEX_INITIALIZER,
+       .job_cv = PTHREAD_COND_INITIALIZER,
+       .done_cv = PTHREAD_COND_INITIALIZER};
+
+static _Thread_local int tl_in_job;
+
+typedef struct {
+    int id;
+    unsigned start_gen;
+} worker_arg;
+static worker_arg P_args[ORC_MAX_THREADS];
+
+static unsigned wait_gen_change(unsigned seen) {
+    unsigned g;
+    for (int spins = 0; spins < ORC_SPIN; spins++) {
+        g = atomic_load_explicit(&P.gen, memory_order_acquire);
+        if (g != seen) return g;
+    }
+    pthread_mutex_lock(&P.mu);
+    while ((g = atomic_load_explicit(&P.gen, memory_order_acquire)) == seen) pthread_cond_wait(&P.job_cv, &P.mu);
+    pthread_mutex_unlock(&P.mu);
+    return g;
+}
 
 static void *pool_worker(void *arg) {
-    int id = (int)(intptr_t)arg;
-    int seen = atomic_load(&P.gen);
+    const worker_arg *a = (const worker_arg *)arg;
+    const int id = a->id;
+    unsigned seen = a->start_gen;
+    tl_in_job = 1;
     for (;;) {
-        int spins = 0;
-        int g;
-        while ((g = atomic_load_explicit(&P.gen, memory_order_acquire)) == seen) {
-            if (atomic_load(&P.stop)) return NULL;
-            if (++spins > 2000) sched_yield();
-        }
-        seen = g;
+        seen = wait_gen_change(seen);
         if (atomic_load(&P.stop)) return NULL;
         if (id < P.workers) {
             int s = (int)((long)id * P.n / P.workers);
             int e = (int)((long)(id + 1) * P.n / P.workers);
             P.fn(P.ctx, s, e);
         }
-        atomic_fetch_add_explicit(&P.done, 1, memory_order_release);
+        if (atomic_fetch_add_explicit(&P.done, 1, memory_order_acq_rel) + 1 == P.nthreads - 1) {
+            pthread_mutex_lock(&P.mu);
+            pthread_cond_broadcast(&P.done_cv);
+            pthread_mutex_unlock(&P.mu);
+        }
     }
 }
 
+static void post_gen(void) {
+    pthread_mutex_lock(&P.mu);
+    atomic_fetch_add_explicit(&P.gen, 1, memory_order_acq_rel);
+    pthread_cond_broadcast(&P.job_cv);
+    pthread_mutex_unlock(&P.mu);
+}
+
+/* caller holds P.api */
 static void pool_stop(void) {
     if (P.nthreads <= 1) return;
     atomic_store(&P.stop, 1);
-    atomic_fetch_add(&P.gen, 1);
+    post_gen();
     for (int i = 1; i < P.nthreads; i++) pthread_join(P.th[i], NULL);
     atomic_store(&P.stop, 0);
     P.nthreads = 1;
 }
 
 void orc_set_threads(int n) {
-    pthread_mutex_lock(&P.mu);
+    pthread_mutex_lock(&P.api);
     if (n < 1) n = 1;
     if (n > ORC_MAX_THREADS) n = ORC_MAX_THREADS;
     pool_stop();
-    P.nthreads = n;
-    for (int i = 1; i < n; i++) pthread_create(&P.th[i], NULL, pool_worker, (void *)(intptr_t)i);
-    pthread_mutex_unlock(&P.mu);
+    const unsigned g = atomic_load(&P.gen);
+    int made = 1;
+    for (int i = 1; i < n; i++) {
+        P_args[i].id = i;
+        P_args[i].start_gen = g;
+        if (pthread_create(&P.th[i], NULL, pool_worker, &P_args[i]) != 0) break;
+        made++;
+    }
+    P.nthreads = made;
+    pthread_mutex_unlock(&P.api);
 }
 
 int orc_get_threads(void) { return P.nthreads; }
@@ -97,7 +149,14 @@ int orc_get_threads(void) { return P.nthreads; }
 static void parallel_for_max(int n, int max_workers, range_fn fn, void *ctx) {
     int workers = max_workers < n ? max_workers : n;
     if (workers > P.nthreads) workers = P.nthreads;
+    if (workers <= 1 || tl_in_job) {
+        fn(ctx, 0, n);
+        return;
+    }
+    pthread_mutex_lock(&P.api);
+    if (workers > P.nthreads) workers = P.nthreads; /* resized while we waited */
     if (workers <= 1) {
+        pthread_mutex_unlock(&P.api);
         fn(ctx, 0, n);
         return;
     }
@@ -106,11 +165,20 @@ static void parallel_for_max(int n, int max_workers, range_fn fn, void *ctx) {
     P.n = n;
     P.workers = workers;
     atomic_store(&P.done, 0);
-    atomic_fetch_add_explicit(&P.gen, 1, memory_order_release);
+    post_gen();
+    tl_in_job = 1;
     fn(ctx, 0, n / workers);
+    tl_in_job = 0;
+    const int need = P.nthreads - 1;
     int spins = 0;
-    while (atomic_load_explicit(&P.done, memory_order_acquire) < P.nthreads - 1)
-        if (++spins > 2000) sched_yield();
+    while (atomic_load_explicit(&P.done, memory_order_acquire) < need && ++spins < ORC_SPIN) {
+    }
+    if (atomic_load_explicit(&P.done, memory_order_acquire) < need) {
+        pthread_mutex_lock(&P.mu);
+        while (atomic_load_explicit(&P.done, memory_order_acquire) < need) pthread_cond_wait(&P.done_cv, &P.mu);
+        pthread_mutex_unlock(&P.mu);
+    }
+    pthread_mutex_unlock(&P.api);
 }
 
 /* ------------------------------------------------------------------ */
@@ -1103,13 +1171,21 @@ double orc_rng_float64(uint64_t *state) {
 }
 
 /* total order of topKSelectWithWork's comparison: score descending, equal
- * scores by lower index (no NaN scores) */
-static const float *g_sort_scores;
-static int cmp_score_desc(const void *a, const void *b) {
-    const int32_t i = *(const int32_t *)a, j = *(const int32_t *)b;
-    const float si = g_sort_scores[i], sj = g_sort_scores[j];
-    if (si != sj) return si > sj ? -1 : 1;
-    return i < j ? -1 : (i > j);
+ * scores by lower index (no NaN scores). Each candidate becomes one u64 key
+ * whose ascending order is that order: the high word is the complement of the
+ * score's order-preserving bits (-0 folded onto +0, which compare equal), the
+ * low word the index. The keys carry everything, so the sort needs no shared
+ * state and concurrent calls cannot interfere. */
+static uint64_t score_key(float s, int32_t i) {
+    uint32_t u;
+    if (s == 0.0f) s = 0.0f;
+    memcpy(&u, &s, 4);
+    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((uint64_t)(~u) << 32) | (uint32_t)i;
+}
+static int cmp_u64(const void *a, const void *b) {
+    const uint64_t x = *(const uint64_t *)a, y = *(const uint64_t *)b;
+    return x < y ? -1 : (x > y);
 }
 
 int orc_topk(const float *scores, int n, int k, int32_t *ids, float *out_scores) {
@@ -1122,8 +1198,11 @@ int orc_topk(const float *scores, int n, int k, int32_t *ids, float *out_scores)
     int32_t *idx = (int32_t *)malloc(sizeof(int32_t) * (size_t)n);
     for (int i = 0; i < n; i++) idx[i] = i;
     if (k > 64) {
-        g_sort_scores = scores;
-        qsort(idx, (size_t)n, sizeof(int32_t), cmp_score_desc);
+        uint64_t *keys = (uint64_t *)malloc(sizeof(uint64_t) * (size_t)n);
+        for (int i = 0; i < n; i++) keys[i] = score_key(scores[i], i);
+        qsort(keys, (size_t)n, sizeof(uint64_t), cmp_u64);
+        for (int i = 0; i < n; i++) idx[i] = (int32_t)(uint32_t)keys[i];
+        free(keys);
     } else {
         for (int i = 0; i < k; i++) {
             int best = i;
