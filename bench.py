@@ -460,8 +460,9 @@ def roofline_only(args):
 
 def vnni_decode(ctx, cfg, weights, seq, first_tok, first_pos, n_prefix, n_tokens, steps):
     """The same Q4 greedy decode in the reference's VNNI activation mode
-    (pocr_model_set_vnni: u8 activations for every Q4 matvec, bit-identical
-    to the reference's CPU numerics on an AVX512-VNNI host), from the same
+    (pocr_model_set_vnni: u8 activations for every Q4 matvec, the
+    reference's VNNI matvec arithmetic, with the portable scalar orders
+    around it), from the same
     1345-row KV state, on its own copy of the weights."""
     from rapidocrvl_amd import lib
 

@@ -125,8 +125,8 @@ int pocr_matvec(pocr_ctx *ctx, const pocr_weight *w, const float *x, int m, floa
  * quantizeXForVNNIAVX2 dot_amd64.go:228-252, dotQ8VNNI dot_amd64.go:150-167,
  * finalizeDotQ8VNNI dot_vnni_amd64.s:1043-1080): each row of x quantized to
  * u8 with one scale, exact int32 dots, out = ((dot - 128*rowSum)*scaleX)*scale[r].
- * Bit-identical to that path.  Q8 matrices and inputs of fewer than 32
- * columns are computed in plain mode, as there. */
+ * Bit-identical to that matvec for the same x.  Q8 matrices and inputs of
+ * fewer than 32 columns are computed in plain mode, as there. */
 int pocr_matvec_vnni(pocr_ctx *ctx, const pocr_weight *w, const float *x, int m, float *out);
 /* VulkanMatVecArgmaxQ* (vulkan_exec_stub.go:190,238,286): greedy LM head,
  * ties → lowest index (internal/tensor/argmax_quant.go:255-262) */
@@ -289,7 +289,12 @@ int pocr_model_set_residual_quirk(pocr_model *m, int on);
  * row sums it needs, quant.go:2325); default off (plain mode).  Set it before
  * the model's first sequence (POCR_ERR_ARG after).  In this mode prompts run
  * token by token (pocr_prefill and pocr_generate take their rows as token
- * steps; the batched decode returns POCR_ERR_UNSUPPORTED). */
+ * steps; the batched decode returns POCR_ERR_UNSUPPORTED).  The ops around
+ * the matvecs keep the portable scalar accumulation orders
+ * (sumSquaresScalar, dotF32's running sums); an x86-64 host takes its
+ * FMA/AVX kernels for those (dot_amd64.go:11), so steps are bit-identical to
+ * the scalar-order restatement of the mode and agree with such a host to
+ * rounding. */
 int pocr_model_set_vnni(pocr_model *m, int on);
 
 /* per-sequence state: per-layer fp32 K/V in HBM preallocated for `capacity`

@@ -50,6 +50,9 @@ def lib():
         L.orc_matvec.argtypes = [C.c_void_p, _f32p, _f32p]
         L.orc_matvec_vnni.argtypes = [C.c_void_p, _f32p, _f32p]
         L.orc_quantize_x_vnni.restype = C.c_float
+        L.orc_vnni_core.restype = C.c_int32
+        L.orc_vnni_core.argtypes = [_i8p, _u8p, C.c_int]
+        L.orc_finalize_vnni.argtypes = [_i32p, _i32p, _f32p, _f32p, C.c_int, C.c_float]
         L.orc_quantize_x_vnni.argtypes = [_f32p, C.c_int, _u8p]
         for fn in ("orc_fast_exp", "orc_fast_rsqrt", "orc_silu"):
             getattr(L, fn).restype = C.c_float
@@ -283,6 +286,21 @@ def quantize_x_vnni(x):
     xq = np.zeros(x.size, np.uint8)
     s = lib().orc_quantize_x_vnni(x, x.size, xq)
     return np.float32(s), xq
+
+
+def vnni_core(a, xq) -> int:
+    a = np.ascontiguousarray(a, dtype=np.int8)
+    xq = np.ascontiguousarray(xq, dtype=np.uint8)
+    return int(lib().orc_vnni_core(a, xq, min(a.size, xq.size)))
+
+
+def finalize_vnni(dots, rowsum, scale, scale_x):
+    dots = np.ascontiguousarray(dots, dtype=np.int32)
+    rowsum = np.ascontiguousarray(rowsum, dtype=np.int32)
+    scale = _f32(scale)
+    out = np.zeros(dots.size, np.float32)
+    lib().orc_finalize_vnni(dots, rowsum, scale, out, dots.size, np.float32(scale_x))
+    return out
 
 
 def fast_exp(x: float) -> np.float32:

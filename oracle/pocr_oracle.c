@@ -387,19 +387,48 @@ static void mv_plain_range(void *vctx, int s, int e) {
         c->out[r] = dot_i8(u->codes + (size_t)r * u->q.cols, c->x, u->q.cols) * u->q.scale[r];
 }
 
-/* VNNI: (f32(dot) - f32(rowSum)*128) * scaleX * scale[r]
- * (dot_vnni_amd64.s:1043-1080 16-wide finalize; dot = Σ q·xq with xq u8) */
+/* dotQ8VNNICore (dot_amd64.go:150-167 with useVNNI; VPDPBUSD in
+ * dot_vnni_amd64.s): Σ a[i]·xq[i], s8 × u8 products summed in int32 */
+int32_t orc_vnni_core(const int8_t *a, const uint8_t *xq, int n) {
+    int32_t dot = 0;
+    for (int i = 0; i < n; i++) dot += (int32_t)a[i] * (int32_t)xq[i];
+    return dot;
+}
+
+/* finalizeDotQ8VNNI (dot_vnni_amd64.s:1043-1095) over one worker's row range:
+ * blocks of 16 rows convert dot and rowSum to f32 and subtract in f32
+ * (VCVTDQ2PS, VMULPS 128, VSUBPS); the n mod 16 tail rows subtract in int32
+ * (IMULL 128, SUBL, wrapping) and convert the difference. Both then multiply
+ * by scaleX, then by scale[i]. The forms agree while |dot| and |128·rowSum|
+ * stay below 2^24. */
+void orc_finalize_vnni(const int32_t *dots, const int32_t *rowsum, const float *scale, float *out, int n,
+                       float scale_x) {
+    int i = 0;
+    for (; i + 16 <= n; i += 16)
+        for (int j = i; j < i + 16; j++) {
+            float v = (float)dots[j] - (float)rowsum[j] * 128.0f;
+            v = v * scale_x;
+            out[j] = v * scale[j];
+        }
+    for (; i < n; i++) {
+        int32_t d = (int32_t)((uint32_t)dots[i] - (uint32_t)rowsum[i] * 128u);
+        float v = (float)d * scale_x;
+        out[i] = v * scale[i];
+    }
+}
+
+/* matVecQ8Serial's VNNI branch (quant.go:1356-1373; the Q4/Q6 serial
+ * functions 1816-1851, 1853-1888 have the same shape): the integer core for
+ * the worker's rows into scratch, then one finalize over the range */
 static void mv_vnni_range(void *vctx, int s, int e) {
     mv_ctx *c = (mv_ctx *)vctx;
     const umat *u = c->u;
     int cols = u->q.cols;
-    for (int r = s; r < e; r++) {
-        const int8_t *a = u->codes + (size_t)r * cols;
-        int32_t dot = 0;
-        for (int i = 0; i < cols; i++) dot += (int32_t)a[i] * (int32_t)c->xq[i];
-        float v = (float)dot - (float)u->rowsum[r] * 128.0f;
-        c->out[r] = v * c->scale_x * u->q.scale[r];
-    }
+    if (e <= s) return;
+    int32_t *dots = (int32_t *)malloc(sizeof(int32_t) * (size_t)(e - s));
+    for (int r = s; r < e; r++) dots[r - s] = orc_vnni_core(u->codes + (size_t)r * cols, c->xq, cols);
+    orc_finalize_vnni(dots, u->rowsum + s, u->q.scale + s, c->out + s, e - s, c->scale_x);
+    free(dots);
 }
 
 /* shouldParallelQuantMatVec / parallelForQuantMatVec (quant.go:563-599):

@@ -52,6 +52,12 @@ void orc_matvec(const orc_qmat *m, const float *x, float *out);
 /* VNNI-emulation semantics (dot_amd64.go:140-167, dot_vnni_amd64.s:434-500,1043-1080) */
 float orc_quantize_x_vnni(const float *x, int n, uint8_t *xq);
 void orc_matvec_vnni(const orc_qmat *m, const float *x, float *out);
+/* dotQ8VNNICore: Σ a·xq in int32 */
+int32_t orc_vnni_core(const int8_t *a, const uint8_t *xq, int n);
+/* finalizeDotQ8VNNI over one row range: 16-row blocks subtract in f32, the
+ * tail in int32; then ·scaleX, then ·scale[i] */
+void orc_finalize_vnni(const int32_t *dots, const int32_t *rowsum, const float *scale, float *out, int n,
+                       float scale_x);
 /* the same plain matvec on a matrix unpacked once (as the model keeps its
  * weights), for timing the CPU path without the per-call unpack; the handle
  * borrows m's scale array */

@@ -23,8 +23,17 @@
 //   all int32 (|Σ u·d| ≤ 63·128·8192 < 2³¹);
 // * only the finalize is f32, in the reference's order.
 // RMSNorm prologues form the normalised vector first (x·factor·w, as
-// RMSNorm does, ops.go:1015-1037, with Σx² in the reference's order) and
-// quantize that.
+// RMSNorm does, ops.go:1015-1037, with Σx² in sumSquaresScalar's order,
+// ops.go:1039-1058) and quantize that.
+//
+// A matvec is bit-identical to the reference's VNNI matvec for the same x.
+// Around the matvecs the mode keeps the portable scalar orders (RMSNorm's
+// sumSquaresScalar, dotF32's eight running sums, the scalar Softmax). An
+// x86-64 AVX512-VNNI host runs those ops through its FMA/AVX kernels instead
+// (useDotFMA is fixed true there, dot_amd64.go:11: sumSquaresF32FMA,
+// mulScaleFMA, dotF32AVX, expScaledVecFMA), whose accumulation orders are not
+// restated here. Whole steps and streams are therefore bit-identical to the
+// CPU port's VNNI mode, and agree with such a host to rounding only.
 #pragma once
 
 #include "kernels.hpp"

@@ -117,16 +117,131 @@ def test_positions(orc, impl):
         assert np.asarray(pos).tolist() == c["pos"] and delta == c["delta"]
 
 
-def test_vnni_core(orc):
-    # ones against xq = 129 on n columns, plus one column of weight 0 that sets
-    # the x scale: x = c, …, c, 127c → scaleX = c, xq = 129, …, 129, 255.
-    # (core − 128·rowSum)·scaleX·scale = (core − 128n)·c.
+def _vnni_kat_core(orc, n, core):
+    """A Q6 row that takes the VNNI branch (>= 32 columns) and whose integer
+    core over its first n columns is the KAT's: n ones against xq = 129, a
+    code-31 column against x = 0 (xq = 128, sets the row scale to exactly 1),
+    zero codes elsewhere and one x = 127c in a zero column (sets scaleX = c).
+    dot = core + 31·128 and rowSum = n + 31, so the finalize leaves
+    (core − 128n)·c."""
+    cols = 40
     c = 1.0 / 64
+    w = np.zeros((1, cols), np.float32)
+    w[0, :n] = 1.0
+    w[0, n] = 31.0
+    x = np.zeros(cols, np.float32)
+    x[:n] = c
+    x[cols - 1] = 127 * c
+    sc, data = orc.quantize_matrix(Q6, w)
+    assert sc[0] == 1.0
+    assert list(orc.unpack_matrix(Q6, data, cols)[0, :n + 1]) == [1] * n + [31]
+    out = orc.matvec(Q6, sc, data, x, vnni=True)
+    return out[0], np.float32((core - 128 * n) * c)
+
+
+def test_vnni_core(orc):
+    # vnni_test.go:8-25: all-ones codes against xq = 129
     for n, core in KAT["vnni_core"]["cases"]:
-        data = np.array([[1] * n + [0]], np.int8).view(np.uint8)
-        x = np.array([c] * n + [127 * c], np.float32)
-        out = orc.matvec(Q8, np.array([1.0], np.float32), data, x, vnni=True)
-        assert out[0] == np.float32((core - 128 * n) * c)
+        assert orc.vnni_core([1] * n, [129] * n) == core
+        got, want = _vnni_kat_core(orc, n, core)
+        assert got == want
+
+
+def _finalize_case(form, n):
+    i = np.arange(n)
+    if form.startswith("dots=i*100+128"):
+        return (i * 100 + 128).astype(np.int32), i.astype(np.int32), np.float32(i + 1) * np.float32(0.1)
+    assert form.startswith("dots=i*37-128*(i%5)")
+    return (i * 37 - 128 * (i % 5)).astype(np.int32), (i % 5).astype(np.int32), np.float32(i + 1) * np.float32(0.003)
+
+
+def _round_each_step(v, sx, s):
+    """f32(f32(v·sx)·s) with each product formed exactly in f64 (24-bit by
+    24-bit mantissas fit its 53 bits) and rounded once to f32."""
+    t = (np.asarray(v, np.float64) * np.float64(sx)).astype(np.float32)
+    return (t.astype(np.float64) * np.asarray(s, np.float64)).astype(np.float32)
+
+
+def test_vnni_finalize_reference_vectors(orc):
+    """finalize_test.go:7-58 at the reference's bar (0.001), then exactly:
+    the asm multiplies by scaleX first, then by scale[i]
+    (dot_vnni_amd64.s:1062-1065), each an f32 rounding."""
+    rec = KAT["vnni_finalize"]
+    order_seen = False
+    for case in rec["cases"]:
+        sx = np.float32(case["scale_x"])
+        for n in case["ns"]:
+            dots, rs, sc = _finalize_case(case["form"], n)
+            out = orc.finalize_vnni(dots, rs, sc, sx)
+            v = dots.astype(np.int64) - 128 * rs.astype(np.int64)
+            ref = (v.astype(np.float32) * sx) * sc
+            assert np.all(np.abs(out - ref) <= rec["tolerance"]), (n, out, ref)
+            assert np.array_equal(out, _round_each_step(v, sx, sc)), n
+            # the other multiplication order rounds differently somewhere,
+            # so the exact check above fixes the order
+            other = (v.astype(np.float64) * (np.float64(sx) * sc.astype(np.float64)).astype(np.float32)
+                     .astype(np.float64)).astype(np.float32)
+            order_seen |= not np.array_equal(other, out)
+    assert order_seen
+
+
+def test_vnni_finalize_block_and_tail_forms(orc):
+    """The 16-row blocks subtract in f32 after converting dot and 128·rowSum,
+    the tail subtracts in int32 and converts once. dot = 2^25 + 3 converts to
+    2^25 + 4 (spacing 4, nearest), 128·rowSum = 2^25 exactly: the blocks give
+    4, the tail 3."""
+    for n in (1, 15, 16, 17, 33):
+        dots = np.full(n, (1 << 25) + 3, np.int32)
+        rs = np.full(n, 1 << 18, np.int32)
+        out = orc.finalize_vnni(dots, rs, np.ones(n, np.float32), 1.0)
+        blocks = (n // 16) * 16
+        assert list(out) == [4.0] * blocks + [3.0] * (n - blocks), n
+    # int32 wrap in the tail (IMULL/SUBL): -2^31 - 128 wraps to 2^31 - 128
+    out = orc.finalize_vnni(np.array([-(1 << 31)], np.int32), np.array([1], np.int32), np.ones(1, np.float32), 1.0)
+    assert out[0] == np.float32((1 << 31) - 128)
+
+
+@pytest.mark.parametrize("qtype", [Q4, Q6], ids=["q4", "q6"])
+@pytest.mark.parametrize("cols", [32, 96, 1024])
+def test_vnni_matvec_closed_form(orc, qtype, cols):
+    """Power-of-two scales make every step exact: with codes q (one ±qmax per
+    row, so scale = 2^m exactly) and x = k·2^j (one |k| = 127, so scaleX =
+    2^j and xq = k + 128 exactly), the VNNI result must equal
+    Σ q·k · 2^(j+m) computed in integers — a wrong byte offset, a missing
+    128·rowSum term or a lost scale fails it."""
+    rng = np.random.default_rng(cols + qtype)
+    qmax = 7 if qtype == Q4 else 31
+    rows = 37
+    codes = rng.integers(-qmax, qmax + 1, size=(rows, cols))
+    codes[np.arange(rows), rng.integers(0, cols, rows)] = qmax * rng.choice([-1, 1], rows)
+    m = rng.integers(-12, 4, size=rows)
+    w = (codes * np.exp2(m)[:, None]).astype(np.float32)
+    k = rng.integers(-127, 128, size=cols)
+    k[rng.integers(0, cols)] = -127
+    j = -5
+    x = (k * 2.0 ** j).astype(np.float32)
+    sc, data = orc.quantize_matrix(qtype, w)
+    assert np.array_equal(sc, np.exp2(m).astype(np.float32))
+    want = ((codes @ k).astype(np.float64) * np.exp2(m + j)).astype(np.float32)
+    assert np.array_equal(orc.matvec(qtype, sc, data, x, vnni=True), want)
+    assert np.array_equal(orc.matvec(qtype, sc, data, x), want)
+
+
+@pytest.mark.parametrize("qtype", [Q4, Q6], ids=["q4", "q6"])
+def test_vnni_correctness_reference(orc, qtype):
+    """vnni_test.go:27-60 on a Q4/Q6 row (>= 32 columns, so the VNNI branch
+    runs): within 5 % (or 0.01) of the f32 dot times the row scale. The
+    reference draws codes i%17-8; Q4 codes stop at ±7, so its row uses
+    i%15-7."""
+    rec = KAT["vnni_correctness"]
+    for n in rec["ns"]:
+        i = np.arange(n)
+        a = (i % 17 - 8) if qtype == Q6 else (i % 15 - 7)
+        x = (np.float32(1) * (i % rec["x_mod"] - rec["x_off"]).astype(np.float32)) / np.float32(rec["x_den"])
+        sc, data = orc.quantize_matrix(qtype, a.astype(np.float32)[None, :])
+        vn = orc.matvec(qtype, sc, data, x, vnni=True)[0]
+        ref = orc.matvec(qtype, sc, data, x)[0]
+        assert abs(vn - ref) <= max(rec["rel_tol"] * abs(ref), rec["abs_tol"]), (n, vn, ref)
 
 
 # ---------------------------------------------------------------- streams (oracle)

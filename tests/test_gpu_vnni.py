@@ -5,10 +5,11 @@ The mode quantizes x once per matvec to u8 with one scale (quant.go:2087-2115,
 dot_amd64.go:228-252) and finishes each row from exact int32 sums
 (dot_vnni_amd64.s:1043-1080).  Every step is exact or one IEEE operation, so a
 matvec must equal the oracle bit for bit.  In this mode the step also sums
-RMSNorm's squares and the attention in the reference's order, so whole decode
-steps (logits, K/V rows) and greedy streams are bit-identical too: an ulp of
-difference upstream of a matvec would move an activation byte, and with it a
-whole row, by a step of the weights."""
+RMSNorm's squares and the attention in the oracle's order (the reference's
+portable scalar sums, sumSquaresScalar and dotF32's running sums), so whole
+decode steps (logits, K/V rows) and greedy streams are bit-identical to the
+oracle's VNNI mode too: an ulp of difference upstream of a matvec would move
+an activation byte, and with it a whole row, by a step of the weights."""
 import numpy as np
 import pytest
 
