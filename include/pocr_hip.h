@@ -303,6 +303,14 @@ int pocr_seq_create(pocr_model *m, int capacity, pocr_seq **out);
 void pocr_seq_destroy(pocr_seq *s);
 int pocr_seq_reset(pocr_seq *s);
 int pocr_seq_len(const pocr_seq *s);
+/* Tokens the device decode loop took in the sequence's last greedy decode
+ * (pocr_decode_greedy, pocr_generate, pocr_generate_vision,
+ * pocr_decode_batch): each step prologue takes the previous step's token.
+ * A loop that met an EOS id took it and ran no step after it
+ * (model.go:1545-1548), so this is the EOS's output index + 1 there, where a
+ * loop that kept stepping would show its whole chunk of steps.  No reference
+ * counterpart: accounting for callers and tests. */
+int pocr_seq_device_tokens(const pocr_seq *s);
 /* token choice of the sequence's step-level generation (GenerateOptions
  * Temperature/TopK/Seed, internal/model/model.go:420-470): temperature <= 0
  * or top_k == 1 is greedy (generationUsesArgmaxSampling, 1858-1860);
@@ -334,7 +342,12 @@ int pocr_prefill(pocr_seq *s, int n, const float *emb, const int32_t *pos3, floa
 /* greedy decode loop kept on the device (decode loop, model.go:1538-1568):
  * feeds first_token at position first_pos, first_pos+1, ...; writes up to
  * max_new tokens (first_token first) and stops after an EOS id.  Returns the
- * number of tokens written (>=0) or an error status (<0). */
+ * number of tokens written (>=0) or an error status (<0).
+ * EOS lists, here and in every generate/decode entry point: at most 1,024 ids
+ * and none negative, else POCR_ERR_ARG (maxEOSTokenIDs and
+ * ValidateGenerateOptions, model.go:432, 461-467).  The device loop stops on
+ * every listed id (up to 16 in the step state, longer lists as a bitmap over
+ * the vocabulary). */
 int pocr_decode_greedy(pocr_seq *s, int32_t first_token, int32_t first_pos, int max_new,
                        const int32_t *eos, int n_eos, int32_t *out_tokens);
 /* decode of n_seq (1..16) sequences of one model together: the

@@ -53,8 +53,20 @@ struct HeadParams {
 // separate B columns (6 per vector: half hb, plane pl → 6v + 3hb + pl), and
 // a row's partial sums are C[lr][3hb+pl] with lr/8 = hb, added afterwards.
 // Q4: a 16-byte piece is 32 codes, two MFMA steps of 8 bytes; Q8: one step.
+//
+// Q6 rows (3 bytes per 4 codes) do not fall on 128-byte lines, so Q6 reads
+// 4 rows × 192 contiguous bytes (256 codes) per load instruction: lane
+// (lr, lg) reads the 12 bytes (16 codes) at 48·(lr/4) + 12·lg of row lr % 4's
+// 192-byte unit. A-row lr thus carries part lr/4 of row lr % 4, and B
+// columns are (part, plane) → 3·part + pl (12 per vector, one vector per B
+// tile); a row's partial sums are C[lr][3·(lr/4) + pl], added afterwards.
+// One MFMA step per load; a wave's quarter of the columns is NS/4 units.
 template <int QT>
 constexpr int head_steps_per_load() { return QT == QT_Q4 ? 2 : 1; }
+// A-rows per weight row within one load instruction: halves (Q4, Q8) or
+// parts (Q6)
+template <int QT>
+constexpr int head_parts() { return QT == QT_Q6 ? 4 : 2; }
 // first column (relative to the wave's quarter) of step h of line ℓ, half hb,
 // lane group lg: 16 columns in the MFMA K order (digit_pos16)
 template <int QT>
@@ -76,20 +88,25 @@ __device__ __forceinline__ unsigned long long key_max_dpp(unsigned long long k) 
 // of every row.  NV vectors need ⌈6·NV/16⌉ B tiles (two vectors per tile).
 template <int QT, int NS, int NV>
 __global__ void __launch_bounds__(kThreads) k_head_mfma(HeadParams p) {
-    static_assert(QT == QT_Q4 || QT == QT_Q8, "Q6 rows do not fall on 128-byte lines");
+    static_assert(QT != QT_Q6 || NS % 4 == 0, "Q6: whole 192-byte units per wave quarter");
     static_assert(NV == 1 || NV == 2 || NV == 4, "vectors per launch");
+    constexpr bool Q6 = QT == QT_Q6;
     constexpr int COLS = 256 * NS;
-    constexpr int LINES = (QT == QT_Q4 ? 32 * NS : 64 * NS) / 128;  // per row, per wave
+    // loads per row group and wave: 128-byte lines (Q4, Q8) or 192-byte
+    // units (Q6) of the wave's quarter of every row
+    constexpr int LINES = Q6 ? NS / 4 : (QT == QT_Q4 ? 32 * NS : 64 * NS) / 128;
     constexpr int SPL = head_steps_per_load<QT>();
-    constexpr int T = (NV + 1) / 2;  // B tiles
+    constexpr int NP = head_parts<QT>();
+    constexpr int G = NP;            // row groups of 16/NP rows per block of 16
+    constexpr int T = Q6 ? NV : (NV + 1) / 2;  // B tiles
     constexpr int RB = kHeadRB;
     constexpr int PER_T = COLS / kThreads;  // prologue columns per thread
     static_assert(PER_T == 4 || PER_T == 8, "prologue handles 4 or 8 columns per thread");
     static_assert(LINES >= 1, "a wave's quarter is a whole number of lines");
     constexpr int IB = DigitTraits<QT>::IBIAS;
     __shared__ __attribute__((aligned(16))) int8_t xdig[3][NV][COLS];
-    // partial plane sums: [wave][row block][row 0..15][vector][half][plane]
-    __shared__ int part[kWaves][RB][16][NV][2][3];
+    // partial plane sums: [wave][row block][row 0..15][vector][half/part][plane]
+    __shared__ int part[kWaves][RB][16][NV][NP][3];
     __shared__ float redf[2][NV][kWaves];
     __shared__ int redi[3][NV][kWaves];
     __shared__ unsigned long long kred[NV][kWaves];
@@ -129,21 +146,39 @@ __global__ void __launch_bounds__(kThreads) k_head_mfma(HeadParams p) {
         nw[i + 3] = w4.w;
     }
 
-    // 2. this wave's weight lines: row block rb, row group g (8 rows), line l
+    // 2. this wave's weight lines: row block rb, row group g (16/NP rows),
+    // line or unit l
     typedef unsigned u4v __attribute__((ext_vector_type(4)));
-    u4v raw[RB][2][LINES];
+    // Q6 pieces: 12 bytes on 4-byte boundaries, three dword loads (a 3-wide
+    // vector type is padded to 16 bytes and could read past the last row)
+    struct U3 {
+        uint32_t d[3];
+        __device__ __forceinline__ uint32_t operator[](int i) const { return d[i]; }
+    };
+    using RawT = std::conditional_t<Q6, U3, u4v>;
+    RawT raw[RB][G][LINES];
     {
-        const int qbyte = QT == QT_Q4 ? kbeg / 2 : kbeg;
-        const int lb = 64 * (lr >> 3) + 16 * lg;
+        constexpr int RPG = 16 / NP;  // rows per load instruction
+        const int qbyte = Q6 ? kbeg / 4 * 3 : (QT == QT_Q4 ? kbeg / 2 : kbeg);
+        const int lb = Q6 ? 48 * (lr >> 2) + 12 * lg : 64 * (lr >> 3) + 16 * lg;
+        constexpr int STRIDE = Q6 ? 192 : 128;
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-            for (int g = 0; g < 2; ++g) {
-                const int r = min(16 * (rb0 + rb) + 8 * g + (lr & 7), rows - 1);  // past the end: loaded, never scored
+            for (int g = 0; g < G; ++g) {
+                // past the end: loaded, never scored
+                const int r = min(16 * (rb0 + rb) + RPG * g + (lr % RPG), rows - 1);
                 const uint8_t *row = p.m.data + (size_t)r * p.m.row_bytes + qbyte + lb;
 #pragma unroll
-                for (int l = 0; l < LINES; ++l)
-                    raw[rb][g][l] = __builtin_nontemporal_load(reinterpret_cast<const u4v *>(row + 128 * l));
+                for (int l = 0; l < LINES; ++l) {
+                    if constexpr (Q6) {
+                        const uint32_t *q = reinterpret_cast<const uint32_t *>(row + STRIDE * l);
+#pragma unroll
+                        for (int w = 0; w < 3; ++w) raw[rb][g][l].d[w] = __builtin_nontemporal_load(q + w);
+                    } else {
+                        raw[rb][g][l] = __builtin_nontemporal_load(reinterpret_cast<const u4v *>(row + STRIDE * l));
+                    }
+                }
             }
     }
 
@@ -205,27 +240,32 @@ __global__ void __launch_bounds__(kThreads) k_head_mfma(HeadParams p) {
     }
     __syncthreads();
 
-    // 4. B operands: tile t, column lr = vector 2t + lr/6, half (lr%6)/3, plane lr%3
+    // 4. B operands: Q4/Q8 tile t, column lr = vector 2t + lr/6, half
+    // (lr%6)/3, plane lr%3; Q6 tile t = vector t, column lr = part lr/3,
+    // plane lr%3 (unit l of the quarter: columns 256·l + 64·part + 16·lg)
     v4i b[LINES][SPL][T];
 #pragma unroll
     for (int t = 0; t < T; ++t) {
-        const int v = 2 * t + lr / 6, hb = (lr % 6) / 3, pl = lr % 3;
+        const int v = Q6 ? t : 2 * t + lr / 6, hb = Q6 ? lr / 3 : (lr % 6) / 3, pl = lr % 3;
         const bool col = lr < 12 && v < NV;
 #pragma unroll
         for (int l = 0; l < LINES; ++l)
 #pragma unroll
-            for (int h = 0; h < SPL; ++h)
-                b[l][h][t] = col ? *reinterpret_cast<const v4i *>(&xdig[pl][min(v, NV - 1)][kbeg + head_col<QT>(l, hb, lg, h)])
+            for (int h = 0; h < SPL; ++h) {
+                const int c = Q6 ? 256 * l + 64 * hb + 16 * lg : head_col<QT>(l, hb, lg, h);
+                b[l][h][t] = col ? *reinterpret_cast<const v4i *>(&xdig[pl][min(v, NV - 1)][kbeg + c])
                                  : v4i{0, 0, 0, 0};
+            }
     }
 
     // 5. the MFMAs: exact int32 partial sums of this wave's columns; lane
     // (lr, lg) ends with C[4lg + i][lr]: row 4lg+i of the block's row group
-    // when (4lg + i)/8 is the half of B column lr
+    // when (4lg + i)/8 is the half of B column lr (Q6: row i of the group
+    // when lg is the part of B column lr)
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-        for (int g = 0; g < 2; ++g) {
+        for (int g = 0; g < G; ++g) {
             v4i acc[T];
 #pragma unroll
             for (int t = 0; t < T; ++t) acc[t] = v4i{0, 0, 0, 0};
@@ -237,6 +277,9 @@ __global__ void __launch_bounds__(kThreads) k_head_mfma(HeadParams p) {
                     if constexpr (QT == QT_Q4) {
                         rc.d[0] = raw[rb][g][l][2 * h];
                         rc.d[1] = raw[rb][g][l][2 * h + 1];
+                    } else if constexpr (Q6) {
+#pragma unroll
+                        for (int w = 0; w < 3; ++w) rc.d[w] = raw[rb][g][l][w];
                     } else {
 #pragma unroll
                         for (int w = 0; w < 4; ++w) rc.d[w] = raw[rb][g][l][w];
@@ -246,13 +289,22 @@ __global__ void __launch_bounds__(kThreads) k_head_mfma(HeadParams p) {
                     for (int t = 0; t < T; ++t) acc[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b[l][h][t], acc[t], 0, 0, 0);
                 }
             // keep C[i][col] where i/8 is col's half: rows of lane group lg
-            // are 4lg..4lg+3, half (lg ≥ 2)
+            // are 4lg..4lg+3, half (lg ≥ 2); Q6: A-rows 4lg..4lg+3 are part
+            // lg of the group's rows 0..3
 #pragma unroll
             for (int t = 0; t < T; ++t) {
-                const int v = 2 * t + lr / 6, hb = (lr % 6) / 3, pl = lr % 3;
-                if (lr < 12 && v < NV && hb == (lg >> 1)) {
+                if constexpr (Q6) {
+                    const int v = t, pt = lr / 3, pl = lr % 3;
+                    if (lr < 12 && pt == lg) {
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) part[wave][rb][8 * g + ((4 * lg + i) & 7)][v][hb][pl] = acc[t][i];
+                        for (int i = 0; i < 4; ++i) part[wave][rb][4 * g + i][v][pt][pl] = acc[t][i];
+                    }
+                } else {
+                    const int v = 2 * t + lr / 6, hb = (lr % 6) / 3, pl = lr % 3;
+                    if (lr < 12 && v < NV && hb == (lg >> 1)) {
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) part[wave][rb][8 * g + ((4 * lg + i) & 7)][v][hb][pl] = acc[t][i];
+                    }
                 }
             }
         }
@@ -282,7 +334,7 @@ __global__ void __launch_bounds__(kThreads) k_head_mfma(HeadParams p) {
 #pragma unroll
             for (int w = 0; w < kWaves; ++w)
 #pragma unroll
-                for (int hb = 0; hb < 2; ++hb) {
+                for (int hb = 0; hb < NP; ++hb) {
                     c0 += part[w][rb][lr][v][hb][0];
                     c1 += part[w][rb][lr][v][hb][1];
                     c2 += part[w][rb][lr][v][hb][2];

@@ -140,6 +140,8 @@ struct pocr_seq {
     pocr::StepState *st = nullptr;
     int32_t *tokens = nullptr;
     int max_tokens = 0;
+    uint32_t *eos_bits = nullptr;  // [ceil(vocab/32)] EOS bitmap for lists over kMaxEos ids
+    int device_tokens = 0;         // tokens the device decode loop took in the last greedy decode
     int nsplit = 32;  // attention splits for rpw rows per wave
     int rpw = 16;
     pocr_batch *batch = nullptr;  // the continuous batch this sequence decodes in (ctx lock)

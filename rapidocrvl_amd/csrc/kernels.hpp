@@ -37,7 +37,8 @@ struct DevMat {
 // token after token.
 constexpr int kArgSlots = 64;
 constexpr int kSlotPitch = 16;  // u64 per slot: 128 bytes
-constexpr int kMaxEos = 16;     // EOS ids the device decode loop stops on
+constexpr int kMaxEos = 16;     // EOS ids held in the step state itself
+constexpr int kMaxEosIds = 1024;  // maxEOSTokenIDs (internal/model/model.go:432)
 // err value of a decode loop that took an EOS token: not a failure, but like
 // one every later kernel of the sequence returns at once (nothing appended)
 constexpr int kErrStopped = -1;
@@ -54,6 +55,9 @@ struct StepState {
     int32_t half;
     int32_t n_eos;     // decode loop: a taken token equal to eos[i < n_eos] stops it
     int32_t eos[kMaxEos];
+    // longer lists: bit t of this vocabulary bitmap set ⇔ token t is an EOS
+    // id (the sequence's own buffer; null when the list fits eos[])
+    const uint32_t *eos_bits;
     alignas(16) float cos_t[kMaxHalf];
     float sin_t[kMaxHalf];
     // greedy argmax: workgroup b of the LM head folds its best (score, row)
@@ -70,9 +74,31 @@ static_assert(offsetof(StepState, len) == 0 && offsetof(StepState, clen) == 4 &&
 // reference numerics (internal/tensor/ops.go)
 // ---------------------------------------------------------------------------
 
-// FastExpF32 (ops.go:1099-1112).  The reference wraps for x < -87 (its integer
-// exponent add underflows); the input is clamped there, where exp() is below
-// FLT_MIN anyway.
+// FastExpF32 exactly as the reference computes it (ops.go:1099-1112),
+// including the exponent add that wraps below about −88.7 (the result's bits
+// then carry into the sign: −90 gives −9.5e37). Pointwise uses (SiLU,
+// low-temperature draws, the reference-order softmax of the VNNI mode) take
+// this form so their results equal the reference's there too.
+__device__ __forceinline__ float fast_exp_wrap(float x) {
+#pragma clang fp contract(off)
+    const float log2e = 1.4426950408889634f;
+    const float magic = 12582912.0f;
+    const float t = x * log2e;
+    const int32_t n = (int32_t)((t + magic) - magic);
+    const float f = t - (float)n;
+    const float f2 = f * f;
+    const float poly = (1.0f + 0.6931471824645996f * f) +
+                       f2 * (0.24022650718688965f + 0.05550410971045494f * f +
+                             f2 * (0.009618128649890423f + 0.0013352063251659274f * f));
+    return __uint_as_float(__float_as_uint(poly) + ((uint32_t)n << 23));
+}
+
+// FastExpF32 with its input clamped at −87, where exp() is below FLT_MIN.
+// The split softmaxes (decode and prefill attention, their merges) take this
+// form: they rescale partial sums by exp(m_split − m) terms that the
+// reference's one-pass softmax never forms, so no choice of theirs could
+// reproduce its wrapped weights for score gaps beyond 88; the clamp keeps
+// those rows at weight ≈ 0, the mathematical softmax.
 __device__ __forceinline__ float fast_exp_ref(float x) {
 #pragma clang fp contract(off)
     x = fmaxf(x, -87.0f);
@@ -97,10 +123,11 @@ __device__ __forceinline__ float fast_rsqrt_ref(float x) {
     return y * (1.5f - half * y * y);
 }
 
-// SiLU (ops.go:1092-1094)
+// SiLU (ops.go:1092-1094), FastExp's wrap included: a gate above ≈ 88.7
+// gives x / (1 + (negative huge)) ≈ −0, as in the reference
 __device__ __forceinline__ float silu_ref(float x) {
 #pragma clang fp contract(off)
-    return x / (1.0f + fast_exp_ref(-x));
+    return x / (1.0f + fast_exp_wrap(-x));
 }
 
 // fastExpF32T (ops.go:1152-1164): 2^x for x already scaled by log2(e); the
@@ -1274,9 +1301,14 @@ __device__ __forceinline__ void step_begin_body(StepState *st, const float *embe
                 st->pos[0] = st->pos[1] = st->pos[2] = p;
                 // the generation loop stops at an EOS token once it is in the
                 // output, before any step for it (model.go:1545-1548)
-                const int ne = min(st->n_eos, kMaxEos);
-                for (int i = 0; i < ne; ++i)
-                    if (st->eos[i] == tok) err = kErrStopped;
+                const uint32_t *bits = st->eos_bits;
+                if (bits) {
+                    if ((bits[tok >> 5] >> (tok & 31)) & 1u) err = kErrStopped;
+                } else {
+                    const int ne = min(st->n_eos, kMaxEos);
+                    for (int i = 0; i < ne; ++i)
+                        if (st->eos[i] == tok) err = kErrStopped;
+                }
             }
         }
         if (!err) {

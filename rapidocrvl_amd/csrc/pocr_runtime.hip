@@ -62,6 +62,7 @@ pocr_seq::~pocr_seq() {
     free_dev(part);
     free_dev(st);
     free_dev(tokens);
+    free_dev(eos_bits);
     free_dev(samp);
     free_dev(topk_part);
     prefill_free(pf);
@@ -404,8 +405,8 @@ GemvParams pocr::gemv_params_1(const pocr_weight *w) {
 }
 
 // The greedy head on the matrix cores (head.hpp) for the shapes it takes:
-// one Q4 or Q8 matrix of 1024 or 2048 columns whose rows are 16-byte aligned,
-// 1, 2 or 4 vectors.
+// one Q4, Q8 or Q6 matrix of 1024 or 2048 columns whose rows are 16-byte
+// aligned, 1, 2 or 4 vectors.
 template <int QT>
 static const void *head_fn(int ns, int nv) {
 #define POCR_H(NS, NV) \
@@ -423,7 +424,8 @@ static const void *plan_head(const GemvParams &p, int nmat, int nv) {
     const int ns = p.cols / 256;
     if (m.qtype == POCR_Q4) return head_fn<QT_Q4>(ns, nv);
     if (m.qtype == POCR_Q8) return head_fn<QT_Q8>(ns, nv);
-    return nullptr;  // Q6: 12-byte code groups do not fall on 128-byte lines (GEMV head)
+    if (m.qtype == POCR_Q6) return head_fn<QT_Q6>(ns, nv);
+    return nullptr;
 }
 
 static int launch_head(hipStream_t s, const void *fn, const GemvParams &p, int pro, int nv, const GemvNV *q) {
@@ -1822,6 +1824,8 @@ extern "C" int pocr_seq_reset(pocr_seq *s) {
 
 extern "C" int pocr_seq_len(const pocr_seq *s) { return s ? s->len : POCR_ERR_ARG; }
 
+extern "C" int pocr_seq_device_tokens(const pocr_seq *s) { return s ? s->device_tokens : POCR_ERR_ARG; }
+
 // the generator at its seed (samplingRNGInto, model.go:1846-1852)
 static int seed_sampler(pocr_seq *s) {
     hipStream_t st = s->m->ctx->stream;
@@ -2069,7 +2073,11 @@ extern "C" int pocr_time_attention(pocr_ctx *ctx, int heads, int kv_heads, int h
 
 // The read ceiling a weight-streaming kernel is measured against: every
 // workgroup reads 16-byte nontemporal chunks of one buffer in a grid-stride
-// loop (4 in flight per lane) and folds them into one xor per workgroup.
+// loop (4 in flight per lane) and folds them into one xor per lane, stored
+// only if it equals a constant (never, for the filled buffers), so the reads
+// stay and nothing else costs time.  (An earlier form reduced the xors
+// through LDS with one thread per workgroup: that tail cost about 2 µs of a
+// 53 MB launch and made the ceiling look 20 % lower than it is.)
 static __global__ void __launch_bounds__(kThreads) k_stream_read(const uint4 *p, size_t n16, unsigned *out) {
     constexpr int U = 4;
     typedef unsigned u4v __attribute__((ext_vector_type(4)));
@@ -2085,14 +2093,7 @@ static __global__ void __launch_bounds__(kThreads) k_stream_read(const uint4 *p,
         for (int u = 0; u < U; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
     }
     for (; i < n16; i += kThreads) acc ^= q[i].x ^ q[i].y ^ q[i].z ^ q[i].w;
-    __shared__ unsigned sh[kThreads];
-    sh[threadIdx.x] = acc;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        unsigned a = 0;
-        for (int t = 0; t < kThreads; ++t) a ^= sh[t];
-        out[blockIdx.x] = a;
-    }
+    if (acc == 0x9E3779B9u) out[blockIdx.x] = acc;
 }
 
 extern "C" int pocr_time_stream_read(pocr_ctx *ctx, int64_t bytes, int n_buffers, int iters, float *avg_us) {
@@ -2416,11 +2417,42 @@ static bool is_eos(int32_t t, const int32_t *eos, int n) {
     return false;
 }
 
-// the decode loop's EOS ids in the step state; a list longer than the state
-// holds leaves the device loop running and the host cuts the cache at the EOS
-static void set_state_eos(StepState &hs, const int32_t *eos, int n_eos) {
-    hs.n_eos = n_eos <= kMaxEos ? n_eos : 0;
-    for (int i = 0; i < kMaxEos; ++i) hs.eos[i] = i < hs.n_eos ? eos[i] : 0;
+// The decode loop's EOS ids in the step state. Up to kMaxEos ids sit in the
+// state itself; a longer list (up to maxEOSTokenIDs) becomes a bitmap over the
+// vocabulary in the sequence's own buffer, which the step prologue tests with
+// one load. Ids at or past the vocabulary can never be taken and are left out.
+// The caller uploads hs and synchronizes the stream before the bitmap's host
+// copy could change.
+static int set_state_eos(pocr_seq *s, StepState &hs, const int32_t *eos, int n_eos) {
+    hs.eos_bits = nullptr;
+    if (n_eos <= kMaxEos) {
+        hs.n_eos = n_eos;
+        for (int i = 0; i < kMaxEos; ++i) hs.eos[i] = i < n_eos ? eos[i] : 0;
+        return POCR_OK;
+    }
+    const int vocab = s->m->cfg.vocab;
+    const size_t words = ((size_t)vocab + 31) / 32;
+    if (!s->eos_bits) HIP_TRY(hipMalloc((void **)&s->eos_bits, words * 4));
+    std::vector<uint32_t> bits(words, 0u);
+    for (int i = 0; i < n_eos; ++i)
+        if (eos[i] < vocab) bits[(size_t)eos[i] >> 5] |= 1u << (eos[i] & 31);
+    HIP_TRY(hipMemcpyAsync(s->eos_bits, bits.data(), words * 4, hipMemcpyHostToDevice, s->m->ctx->stream));
+    HIP_TRY(hipStreamSynchronize(s->m->ctx->stream));
+    hs.n_eos = 0;
+    for (int i = 0; i < kMaxEos; ++i) hs.eos[i] = 0;
+    hs.eos_bits = s->eos_bits;
+    return POCR_OK;
+}
+
+// ValidateGenerateOptions (internal/model/model.go:461-467): at most
+// maxEOSTokenIDs ids, none negative
+static int check_eos(const char *fn, const int32_t *eos, int n_eos) {
+    if (n_eos < 0 || (n_eos > 0 && !eos)) return fail(POCR_ERR_ARG, "%s: bad EOS list", fn);
+    if (n_eos > kMaxEosIds)
+        return fail(POCR_ERR_ARG, "%s: eos_token_ids length %d exceeds limit %d", fn, n_eos, kMaxEosIds);
+    for (int i = 0; i < n_eos; ++i)
+        if (eos[i] < 0) return fail(POCR_ERR_ARG, "%s: eos_token_ids must not contain negative ids", fn);
+    return POCR_OK;
 }
 
 static bool state_failed(const StepState &hs) { return hs.err != 0 && hs.err != kErrStopped; }
@@ -2456,7 +2488,7 @@ static int decode_locked(pocr_seq *s, int32_t first_token, int32_t first_pos, in
     hs.err = 0;
     hs.n_out = 0;
     hs.next_pos = first_pos;
-    set_state_eos(hs, eos, n_eos);
+    RC(set_state_eos(s, hs, eos, n_eos));
     for (int i = 0; i < kArgSlots; ++i) hs.argmax_slot[i * kSlotPitch] = 0ull;
     hs.argmax_slot[0] = (1ull << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)first_token);
     HIP_TRY(hipMemcpyAsync(s->st, &hs, sizeof(hs), hipMemcpyHostToDevice, st));
@@ -2465,6 +2497,7 @@ static int decode_locked(pocr_seq *s, int32_t first_token, int32_t first_pos, in
     int launched = 0;
     const int batch = 16;
     std::vector<int32_t> tok;
+    s->device_tokens = 0;
     while (launched < steps_needed) {
         const int n = std::min(batch, steps_needed - launched);
         for (int i = 0; i < n; ++i) {
@@ -2473,6 +2506,7 @@ static int decode_locked(pocr_seq *s, int32_t first_token, int32_t first_pos, in
         }
         launched += n;
         RC(read_state(s, &hs));
+        s->device_tokens = hs.n_out;
         if (state_failed(hs)) return fail(POCR_ERR_DEVICE, "decode: device state error %d", hs.err);
         tok.resize(hs.n_out);
         HIP_TRY(hipMemcpy(tok.data(), s->tokens, (size_t)hs.n_out * 4, hipMemcpyDeviceToHost));
@@ -2494,6 +2528,7 @@ static int decode_locked(pocr_seq *s, int32_t first_token, int32_t first_pos, in
 extern "C" int pocr_decode_greedy(pocr_seq *s, int32_t first_token, int32_t first_pos, int max_new,
                                   const int32_t *eos, int n_eos, int32_t *out_tokens) {
     if (!s || !out_tokens || (n_eos > 0 && !eos)) return fail(POCR_ERR_ARG, "pocr_decode_greedy: null argument");
+    RC(check_eos("pocr_decode_greedy", eos, n_eos));
     RC(model_ready(s->m));
     CHECK_INJECT("decode");
     std::lock_guard<std::mutex> lk(s->m->ctx->mu);
@@ -2823,7 +2858,7 @@ int seed_first_token(pocr_seq *s, int32_t first_token, int32_t first_pos, const 
     hs.err = 0;
     hs.n_out = 0;
     hs.next_pos = first_pos;
-    set_state_eos(hs, eos, n_eos);
+    RC(set_state_eos(s, hs, eos, n_eos));
     for (int k = 0; k < kArgSlots; ++k) hs.argmax_slot[k * kSlotPitch] = 0ull;
     hs.argmax_slot[0] = (1ull << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)first_token);
     HIP_TRY(hipMemcpyAsync(s->st, &hs, sizeof(StepState), hipMemcpyHostToDevice, s->m->ctx->stream));
@@ -2879,6 +2914,7 @@ extern "C" int pocr_decode_batch(pocr_seq *const *seqs, int n_seq, const int32_t
     if (!seqs || n_seq <= 0 || n_seq > kMaxBatch || !first_tokens || !first_positions || !out_tokens || !out_counts ||
         (n_eos > 0 && !eos))
         return fail(POCR_ERR_ARG, "pocr_decode_batch: bad arguments (1..%d sequences)", kMaxBatch);
+    RC(check_eos("pocr_decode_batch", eos, n_eos));
     pocr_model *m = seqs[0] ? seqs[0]->m : nullptr;
     for (int i = 0; i < n_seq; ++i) {
         if (!seqs[i] || seqs[i]->m != m) return fail(POCR_ERR_ARG, "pocr_decode_batch: sequences of one model");
@@ -2957,6 +2993,7 @@ extern "C" int pocr_decode_batch(pocr_seq *const *seqs, int n_seq, const int32_t
         if (all_done) break;
     }
     for (int i = 0; i < n_seq; ++i) {
+        seqs[i]->device_tokens = hs[i].n_out;
         if (!done[i]) {  // the token chosen by the last step
             out_tokens[(size_t)i * max_new + produced[i]] = pending_token(hs[i]);
             ++produced[i];
@@ -3053,6 +3090,7 @@ extern "C" int pocr_batch_join(pocr_batch *b, pocr_seq *s, int32_t first_token, 
                                const int32_t *eos, int n_eos) {
     if (!b || !s || max_new <= 0 || n_eos < 0 || (n_eos > 0 && !eos))
         return fail(POCR_ERR_ARG, "pocr_batch_join: bad arguments");
+    RC(check_eos("pocr_batch_join", eos, n_eos));
     if (s->m != b->m) return fail(POCR_ERR_ARG, "pocr_batch_join: the sequence belongs to another model");
     if (first_token < 0 || first_token >= b->m->cfg.vocab) return fail(POCR_ERR_ARG, "pocr_batch_join: token out of vocab");
     RC(model_ready(b->m));
@@ -3222,6 +3260,7 @@ extern "C" int pocr_generate(pocr_seq *s, const int32_t *ids, int n_ids, const f
                              const int32_t *eos, int n_eos, int use_prefill, int32_t *out_tokens) {
     if (!s || !ids || n_ids <= 0 || !out_tokens || (n_image > 0 && (!image_embeds || !grid)))
         return fail(POCR_ERR_ARG, "pocr_generate: bad arguments");
+    RC(check_eos("pocr_generate", eos, n_eos));
     if (max_new <= 0) return 0;
     RC(model_ready(s->m));
     CHECK_INJECT("generate");
@@ -3305,6 +3344,7 @@ extern "C" int pocr_generate_vision(pocr_seq *s, pocr_projector *proj, const int
     if (!s || !proj || !ids || n_ids <= 0 || !out_tokens || !vision_rows || !grid || grid[0] <= 0 || grid[1] <= 0 ||
         grid[2] <= 0)
         return fail(POCR_ERR_ARG, "pocr_generate_vision: bad arguments");
+    RC(check_eos("pocr_generate_vision", eos, n_eos));
     if (projector_ctx(proj) != s->m->ctx) return fail(POCR_ERR_ARG, "pocr_generate_vision: projector of another context");
     if (projector_text_dim(proj) != s->m->cfg.hidden)
         return fail(POCR_ERR_ARG, "pocr_generate_vision: projector width %d, model hidden %d",

@@ -143,22 +143,8 @@ static __global__ void __launch_bounds__(kTopKThreads) k_topk_partial(const floa
     for (int j = count + tid; j < k; j += kTopKThreads) out[j] = 0ull;
 }
 
-// FastExpF32 exactly as the reference computes it (ops.go:1099-1112),
-// including the exponent add that wraps below about −88.7: low-temperature
-// draws reach it, and the reference's picks depend on it
-__device__ __forceinline__ float fast_exp_wrap(float x) {
-#pragma clang fp contract(off)
-    const float log2e = 1.4426950408889634f;
-    const float magic = 12582912.0f;
-    const float t = x * log2e;
-    const int32_t n = (int32_t)((t + magic) - magic);
-    const float f = t - (float)n;
-    const float f2 = f * f;
-    const float poly = (1.0f + 0.6931471824645996f * f) +
-                       f2 * (0.24022650718688965f + 0.05550410971045494f * f +
-                             f2 * (0.009618128649890423f + 0.0013352063251659274f * f));
-    return __uint_as_float(__float_as_uint(poly) + ((uint32_t)n << 23));
-}
+// FastExpF32 with its wrap (fast_exp_wrap, kernels.hpp): low-temperature
+// draws reach the wrap, and the reference's picks depend on it
 
 // fastRNG.Float64 (model.go:1833-1840)
 __device__ __forceinline__ double rng_float64(unsigned long long &s) {

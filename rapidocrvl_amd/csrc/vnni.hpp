@@ -305,13 +305,13 @@ __global__ void __launch_bounds__(kThreads) k_attn_ordered(AttnParams a) {
     if (len == 2) {
         if (threadIdx.x == 0) {
             const float x0 = sc[0], x1 = sc[1];
-            const float e = x0 >= x1 ? fast_exp_ref(x1 - x0) : fast_exp_ref(x0 - x1);
+            const float e = x0 >= x1 ? fast_exp_wrap(x1 - x0) : fast_exp_wrap(x0 - x1);
             const float inv = 1.0f / (1.0f + e);
             sc[0] = x0 >= x1 ? inv : e * inv;
             sc[1] = x0 >= x1 ? e * inv : inv;
         }
     } else {
-        for (int t = threadIdx.x; t < len; t += kThreads) sc[t] = fast_exp_ref(sc[t] - m);
+        for (int t = threadIdx.x; t < len; t += kThreads) sc[t] = fast_exp_wrap(sc[t] - m);
         __syncthreads();
         if (threadIdx.x == 0) {
             float sum;

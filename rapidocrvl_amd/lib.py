@@ -102,6 +102,7 @@ _SIGS = {
     "pocr_generate_vision": (_i, [_vp, _vp, _vp, _i, _vp, _i, _vp, _i, _vp, _i, _vp]),
     "pocr_time_project": (_i, [_vp, _i, _i, _i, _i, _vp]),
     "pocr_seq_len": (_i, [_vp]),
+    "pocr_seq_device_tokens": (_i, [_vp]),
     "pocr_seq_read_kv": (_i, [_vp, _i, _vp, _vp]),
     "pocr_seq_truncate": (_i, [_vp, _i]),
     "pocr_time_matvec": (_i, [_vp, _vp, _i, _vp, _i, _vp]),
@@ -238,6 +239,13 @@ def mm_positions(ids, image_token_id: int, grid, merge: int = 2):
     return pos[:n], int(delta[0])
 
 
+def _eos_list(eos):
+    """EOS ids as int32 (an empty list passes a count of zero; the library
+    rejects negative ids and more than 1,024, as ValidateGenerateOptions
+    does, internal/model/model.go:461-467)."""
+    return np.ascontiguousarray(list(eos) if eos else [], dtype=np.int32)
+
+
 def decode_batch(seqs, first_tokens, first_positions, max_new: int, eos=(2,)):
     """Decode of 1..16 sequences of one model together (pocr_decode_batch):
     returns one token array per sequence, first token first."""
@@ -245,11 +253,11 @@ def decode_batch(seqs, first_tokens, first_positions, max_new: int, eos=(2,)):
     handles = (C.c_void_p * n)(*[s.h for s in seqs])
     ft = np.ascontiguousarray(first_tokens, dtype=np.int32)
     fp = np.ascontiguousarray(first_positions, dtype=np.int32)
-    eos = np.ascontiguousarray(list(eos) if eos else [-(1 << 30)], dtype=np.int32)
+    eos = _eos_list(eos)
     out = np.zeros((n, max(max_new, 1)), np.int32)
     counts = np.zeros(n, np.int32)
-    check(load().pocr_decode_batch(C.cast(handles, C.c_void_p), n, _ptr(ft), _ptr(fp), max_new, _ptr(eos),
-                                   eos.size, _ptr(out), _ptr(counts)))
+    check(load().pocr_decode_batch(C.cast(handles, C.c_void_p), n, _ptr(ft), _ptr(fp), max_new,
+                                   _ptr(eos) if eos.size else None, eos.size, _ptr(out), _ptr(counts)))
     return [out[i, :counts[i]] for i in range(n)]
 
 
@@ -756,6 +764,10 @@ class Sequence:
     def __len__(self):
         return check(load().pocr_seq_len(self.h))
 
+    def device_tokens(self) -> int:
+        """Tokens the device decode loop took in the last greedy decode."""
+        return check(load().pocr_seq_device_tokens(self.h))
+
     def reset(self):
         check(load().pocr_seq_reset(self.h))
 
@@ -800,30 +812,33 @@ class Sequence:
 
     def generate_vision(self, proj: Projector, ids, vision_rows, image_token_id: int, grid, max_new, eos=(2,)):
         ids = np.ascontiguousarray(ids, dtype=np.int32)
-        eos = np.ascontiguousarray(list(eos) if eos else [-(1 << 30)], dtype=np.int32)
+        eos = _eos_list(eos)
         out = np.zeros(max(max_new, 1), np.int32)
         x = _f32(vision_rows)
         g = np.ascontiguousarray(grid, dtype=np.int32)
         if x.ndim != 2 or x.shape[0] < int(np.prod(g)) or x.shape[1] != proj.vd:
             raise ValueError(f"vision rows {x.shape}: need [{int(np.prod(g))}][{proj.vd}]")
         n = check(load().pocr_generate_vision(self.h, proj.h, _ptr(ids), ids.size, _ptr(x), image_token_id, _ptr(g),
-                                              max_new, _ptr(eos), eos.size, _ptr(out)))
+                                              max_new, _ptr(eos) if eos.size else None, eos.size,
+                                              _ptr(out)))
         return out[:n]
 
     def decode_greedy(self, first_token: int, first_pos: int, max_new: int, eos=(2,)):
-        eos = np.ascontiguousarray(list(eos) if eos else [-(1 << 30)], dtype=np.int32)
+        eos = _eos_list(eos)
         out = np.zeros(max(max_new, 1), np.int32)
-        n = check(load().pocr_decode_greedy(self.h, first_token, first_pos, max_new, _ptr(eos), eos.size, _ptr(out)))
+        n = check(load().pocr_decode_greedy(self.h, first_token, first_pos, max_new,
+                                            _ptr(eos) if eos.size else None, eos.size, _ptr(out)))
         return out[:n]
 
     def generate(self, ids, max_new, eos=(2,), image_embeds=None, image_token_id=-1, grid=(1, 1, 1), merge=2,
                  use_prefill=False):
         ids = np.ascontiguousarray(ids, dtype=np.int32)
-        eos = np.ascontiguousarray(list(eos) if eos else [-(1 << 30)], dtype=np.int32)
+        eos = _eos_list(eos)
         out = np.zeros(max(max_new, 1), np.int32)
         img = _f32(image_embeds) if image_embeds is not None else None
         n_img = 0 if img is None else img.shape[0]
         g = np.ascontiguousarray(grid, dtype=np.int32)
         n = check(load().pocr_generate(self.h, _ptr(ids), ids.size, _ptr(img), n_img, image_token_id, _ptr(g), merge,
-                                       max_new, _ptr(eos), eos.size, int(use_prefill), _ptr(out)))
+                                       max_new, _ptr(eos) if eos.size else None, eos.size, int(use_prefill),
+                                       _ptr(out)))
         return out[:n]

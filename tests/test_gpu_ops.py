@@ -84,24 +84,22 @@ def test_matvec_vectors_per_pass(ctx, orc, rng, qtype, shape):
             _close(got[i], orc.matvec(qtype, q.scales, q.packed, x[i]))
 
 
-# f32 steps after the exact integer plane sums: the MFMA head (Q4, Q8)
-# combines three planes (2 fma) and applies two scales; the byte-plane GEMV
-# head (Q6) adds a chunk fma and ≤ 6 lane-reduction adds (+2 spare each)
-F32_STEPS = {Q4: 6 * 2.0 ** -24, Q8: 6 * 2.0 ** -24, Q6: 14 * 2.0 ** -24}
+# f32 steps after the exact integer plane sums: the MFMA head combines three
+# planes (2 fma) and applies two scales (+2 spare)
+F32_STEPS = {Q4: 6 * 2.0 ** -24, Q8: 6 * 2.0 ** -24, Q6: 6 * 2.0 ** -24}
 
 
 def head_model(qtype, codes, scales, x):
-    """What the device greedy head computes, exactly, and its f32 magnitude."""
-    if qtype == Q6:
-        return dm.gemv_scores(qtype, codes, scales, x)
+    """What the device greedy head computes, exactly, and its f32 magnitude:
+    the MFMA head's whole-vector digit planes, for every code width."""
     return dm.head_scores(codes, scales, x)
 
 
 @pytest.mark.parametrize("qtype", [Q8, Q4, Q6], ids=["q8", "q4", "q6"])
 def test_matvec_argmax(ctx, orc, rng, qtype):
-    """The greedy head computes codes · digits of x (three byte planes: one
-    power-of-two scale for the vector in the MFMA head, one per 16 columns in
-    the Q6 GEMV head; restated in tests/digit_model.py) up to its f32 steps;
+    """The greedy head computes codes · digits of x (three byte planes under
+    one power-of-two scale for the vector, on the matrix cores for Q4, Q8 and
+    Q6; restated in tests/digit_model.py) up to its f32 steps;
     its choice is the exact argmax unless the exact top scores lie within the
     digits' actual deviation plus those f32 steps."""
     q = _qmat(rng, 103424, 1024, qtype)
@@ -181,6 +179,32 @@ def test_lm_head_rows_on_matrix_cores(ctx, orc, qtype, m):
         assert got[i][idx] == np.float32(score), i
 
 
+@pytest.mark.parametrize("m", [2, 4, 16, 17])
+def test_lm_head_rows_q6(ctx, orc, m):
+    """The Q6 103424×1024 LM head at M rows of x (config 2's Q6 head cells):
+    every row's scores against the oracle at the f32 matvec bar, and every
+    row's greedy pick (pocr_matvec_argmax: the MFMA head, one vector) is that
+    row's best exact score up to the digits' and f32 steps' bounds."""
+    rng = np.random.default_rng(70 + m)
+    q = _qmat(rng, 103424, 1024, Q6)
+    w = ctx.upload(q)
+    codes = lib.unpack_rows(Q6, q.packed, q.cols)
+    x = rng.standard_normal((m, 1024)).astype(np.float32)
+    x[1] *= np.float32(1e-3)
+    got = ctx.matvec(w, x)
+    for i in range(m):
+        _close(got[i], orc.matvec(Q6, q.scales, q.packed, x[i]))
+    for i in (0, 1, m - 1):
+        exact, _ = dm.scores(Q6, codes, q.scales, x[i])
+        dig, mag = head_model(Q6, codes, q.scales, x[i])
+        f32b = F32_STEPS[Q6] * mag
+        dev = np.abs(dig - exact)
+        idx, score = ctx.matvec_argmax(w, x[i])
+        assert abs(score - dig[idx]) <= f32b[idx], i
+        best = int(np.argmax(exact))
+        assert exact[best] - exact[idx] <= dev[best] + dev[idx] + f32b[best] + f32b[idx], i
+
+
 def test_argmax_ties_pick_lowest_index(ctx):
     # identical rows give bit-identical scores: ties → lowest index
     w = np.zeros((64, 32), np.float32)
@@ -219,6 +243,74 @@ def test_swiglu_gate_up(ctx, orc, rng, qtype):
     uu = orc.matvec(qtype, u.scales, u.packed, x)
     want = np.array([orc.silu(float(a)) for a in gg], np.float32) * uu
     _close(got, want)
+
+
+def test_swiglu_fast_exp_wrap(ctx, orc):
+    """SiLU is x / (1 + FastExp(-x)) with the reference's FastExp, whose
+    exponent add wraps below about -88.7 (ops.go:1099-1112): for a gate of 90
+    FastExp(-90) is -9.5e37, so SiLU(90) is about -9.5e-37, not 90. The
+    device reproduces that bit for bit. Inputs are exact (integer x, scales
+    of 1), so gate and up are exact integers on both sides:
+    gate_r = 2·g_r, up = 2·3."""
+    gs = [3, 40, 43, 44, 45, 50, 60, 100, 127, -20, -44, -45, -50, -127]
+    cols = 64
+    wg = np.zeros((len(gs), cols), np.float32)
+    wu = np.zeros((len(gs), cols), np.float32)
+    wg[:, 0] = wu[:, 0] = 127.0
+    wg[:, 1] = gs
+    wu[:, 1] = 3.0
+    x = np.zeros(cols, np.float32)
+    x[1] = 2.0
+    g, u = lib.QMatrix.quantize(wg, Q8), lib.QMatrix.quantize(wu, Q8)
+    assert np.all(g.scales == 1.0) and np.all(u.scales == 1.0)
+    got = ctx.swiglu_gate_up(ctx.upload(g), ctx.upload(u), x)
+    gate = np.float32(2) * np.array(gs, np.float32)
+    want = np.array([orc.silu(float(a)) for a in gate], np.float32) * np.float32(6)
+    assert np.array_equal(got, want)
+    # what the wrap gives: gates 90, 100, 120 come out as tiny negatives
+    # (FastExp(-g) negative and huge), gates -90 and -100 as the gate itself
+    # (FastExp(g) wraps to about 0), while 200 and 254 land back in range;
+    # below |g| = 88 it is the textbook SiLU
+    by_gate = dict(zip(gate.tolist(), got.tolist()))
+    for gv in (90.0, 100.0, 120.0):
+        assert -1e-20 < by_gate[gv] <= 0.0
+    for gv in (-90.0, -100.0):
+        assert by_gate[gv] == gv * 6
+    silu64 = gate.astype(np.float64) / (1 + np.exp(-gate.astype(np.float64))) * 6
+    small = np.abs(gate) < 88
+    assert np.all(np.abs(got[small] - silu64[small]) <= 1e-5 * np.maximum(np.abs(silu64[small]), 1e-30))
+
+
+def test_attention_score_gap_beyond_fast_exp_range(ctx, orc):
+    """A score gap above 88 is where the reference's one-pass softmax takes
+    FastExp into its wrap: with row 0 at score 0 and rows 1..63 at -100, each
+    far row's weight is FastExp(-100) = -4.3e33, the sum is negative and huge,
+    and the normalised weights become ≈ 0 for row 0 and 1/63 for each far row:
+    the reference returns the mean of the far rows' values. The split decode
+    attention cannot form those weights (it rescales per-split sums by
+    exp(m_split - m), which the reference never computes), so it clamps
+    FastExp's input at -87 and returns the softmax itself: row 0's values.
+    Both behaviours are stated here; the greedy streams never reach such
+    gaps (scores of |q·k|/√128 ≤ 88 hold for every test model)."""
+    L, heads, kvh, dim = 64, 16, 2, 128
+    q = np.zeros((heads, dim), np.float32)
+    q[:, 0] = 40.0
+    kc = np.zeros((L, kvh, dim), np.float32)
+    # score = 40·k0 / sqrt(128): -100 at k0 = -100·sqrt(128)/40
+    kc[1:, :, 0] = np.float32(-100.0 * math.sqrt(128.0) / 40.0)
+    rng = np.random.default_rng(5)
+    vc = rng.standard_normal((L, kvh, dim)).astype(np.float32)
+    got = ctx.text_attention(q.ravel(), kc.ravel(), vc.ravel(), L, heads, kvh, dim).reshape(heads, dim)
+    ref = orc.cache_attention(q.ravel(), kc.ravel(), vc.ravel(), L, heads, kvh, dim).reshape(heads, dim)
+    grp = np.arange(heads) // (heads // kvh)
+    assert np.max(np.abs(got - vc[0, grp])) < 1e-6
+    assert np.max(np.abs(ref - vc[1:, :, :].mean(axis=0)[grp])) < 1e-4
+    assert np.max(np.abs(ref - vc[0, grp])) > 0.1
+    # up to a gap of 87 both sides are the softmax
+    kc[1:, :, 0] = np.float32(-80.0 * math.sqrt(128.0) / 40.0)
+    got = ctx.text_attention(q.ravel(), kc.ravel(), vc.ravel(), L, heads, kvh, dim)
+    ref = orc.cache_attention(q.ravel(), kc.ravel(), vc.ravel(), L, heads, kvh, dim)
+    assert np.max(np.abs(got - ref)) < 2e-5
 
 
 @pytest.mark.parametrize("qtype", [Q8, Q4, Q6], ids=["q8", "q4", "q6"])

@@ -148,6 +148,105 @@ def test_generate_eos(orc, ctx):
     assert len(s) == ids.size + len(got)
 
 
+def _eos_list(stream, cut, n_ids, vocab):
+    """An EOS list of n_ids ids whose only id the stream takes is
+    stream[cut], placed last (past the 16 ids the step state holds): the
+    fillers are ids the stream never takes before cut, and ids at or past
+    the vocabulary, which no step can take."""
+    used = set(int(t) for t in stream[:cut + 1])
+    fill = [t for t in range(vocab) if t not in used][: max(0, (n_ids - 1) // 2)]
+    fill += list(range(vocab, vocab + (n_ids - 1 - len(fill))))
+    return fill + [int(stream[cut])]
+
+
+@pytest.mark.parametrize("n_ids", [1, 16, 17, 40, 1024])
+def test_generate_long_eos_lists(orc, ctx, n_ids):
+    """Up to maxEOSTokenIDs (1,024, model.go:432) ids; the device loop itself
+    stops at the EOS (it took 6 tokens, not its chunk of 16), as with a short
+    list, and the oracle stops at the same token."""
+    w, om, gm = _pair(orc, ctx, MID, Q4)
+    ids = synth.prompt_ids(8, seed=9, high=MID.vocab)
+    full = om.generate(ids, 24, eos=())
+    cut = 5
+    assert int(full[cut]) not in set(int(t) for t in full[:cut])
+    eos = _eos_list(full, cut, n_ids, MID.vocab)
+    assert len(eos) == n_ids
+    want = om.generate(ids, 24, eos=tuple(eos))
+    assert list(want) == list(full[:cut + 1])
+    s = gm.seq(64)
+    got = s.generate(ids, 24, eos=eos)
+    assert list(got) == list(want)
+    assert s.device_tokens() == cut + 1
+    assert len(s) == ids.size + cut
+    # decode_greedy from the same state takes the same list
+    s2 = gm.seq(64)
+    first = int(s2.generate(ids, 1, eos=())[0])
+    assert list(s2.decode_greedy(first, ids.size, 24, eos=eos)) == list(want)
+    assert s2.device_tokens() == cut + 1
+
+
+def test_eos_list_limits(ctx):
+    """ValidateGenerateOptions (model.go:461-467): more than 1,024 ids or a
+    negative id is an argument error, checked before anything runs; the
+    sequence stays usable."""
+    w = synth.make_weights(TINY, Q4, seed=1)
+    gm = lib.Model(ctx, TINY)
+    gm.load_weights(w)
+    ids = synth.prompt_ids(6, seed=4, high=TINY.vocab)
+    s = gm.seq(64)
+    bad = [list(range(1025)), [3, -1], [-(1 << 30)]]
+    for eos in bad:
+        with pytest.raises(lib.PocrError) as e:
+            s.generate(ids, 8, eos=eos)
+        assert e.value.code == lib.POCR_ERR_ARG
+        assert len(s) == 0
+        with pytest.raises(lib.PocrError) as e:
+            s.decode_greedy(1, 0, 5, eos=eos)
+        assert e.value.code == lib.POCR_ERR_ARG
+        with pytest.raises(lib.PocrError) as e:
+            lib.decode_batch([s], [1], [0], 5, eos=eos)
+        assert e.value.code == lib.POCR_ERR_ARG
+        b = lib.Batch(gm)
+        with pytest.raises(lib.PocrError) as e:
+            b.join(s, 1, 0, 5, eos=eos)
+        assert e.value.code == lib.POCR_ERR_ARG
+        b.close()
+    ok = list(s.generate(ids, 8, eos=list(range(TINY.vocab, TINY.vocab + 1024))))
+    assert len(ok) == 8
+
+
+def test_decode_batch_long_eos_list(ctx):
+    """The batched decode stops each member on the device at the first id of
+    a 40-id list it takes."""
+    cfg = MID
+    gm = lib.Model(ctx, cfg)
+    gm.load_weights(synth.make_weights(cfg, Q4, seed=21))
+    prompts = [synth.prompt_ids(n, seed=60 + n, high=cfg.vocab) for n in (17, 30, 9)]
+    streams = []
+    for ids in prompts:
+        s = gm.seq(len(ids) + 40)
+        streams.append([int(t) for t in s.generate(ids, 24, eos=(), use_prefill=True)])
+        s.close()
+    eos = _eos_list(streams[0], 4, 39, cfg.vocab) + [streams[1][9]]
+    eset = set(eos)
+    cuts = [next((i for i, t in enumerate(st) if t in eset), None) for st in streams]
+    seqs = [gm.seq(len(ids) + 40) for ids in prompts]
+    firsts = [int(s.generate(ids, 1, eos=(), use_prefill=True)[0]) for s, ids in zip(seqs, prompts)]
+    got = [list(t) for t in lib.decode_batch(seqs, firsts, [len(i) for i in prompts], 24, eos=eos)]
+    for st, cut, g, s, ids in zip(streams, cuts, got, seqs, prompts):
+        if cut is None:
+            assert g == st
+            assert s.device_tokens() == 23
+        else:
+            assert g == st[:cut + 1]
+            assert s.device_tokens() == cut + 1
+            assert len(s) == len(ids) + cut
+    assert cuts[0] is not None and cuts[0] <= 4
+    for s in seqs:
+        s.close()
+    gm.close()
+
+
 @pytest.mark.parametrize("qtype", [Q4, Q6], ids=["q4", "q6"])
 def test_generate_with_image(orc, ctx, qtype):
     w, om, gm = _pair(orc, ctx, MID, qtype)
