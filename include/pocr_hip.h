@@ -289,7 +289,9 @@ int pocr_model_set_residual_quirk(pocr_model *m, int on);
  * row sums it needs, quant.go:2325); default off (plain mode).  Set it before
  * the model's first sequence (POCR_ERR_ARG after).  In this mode prompts run
  * token by token (pocr_prefill and pocr_generate take their rows as token
- * steps; the batched decode returns POCR_ERR_UNSUPPORTED).  The ops around
+ * steps), and the batched decode (pocr_decode_batch, the continuous batch)
+ * steps each member with the mode's single-sequence step: every member's
+ * stream is what decoding it alone gives.  The ops around
  * the matvecs keep the portable scalar accumulation orders
  * (sumSquaresScalar, dotF32's running sums); an x86-64 host takes its
  * FMA/AVX kernels for those (dot_amd64.go:11), so steps are bit-identical to

@@ -2926,7 +2926,6 @@ extern "C" int pocr_decode_batch(pocr_seq *const *seqs, int n_seq, const int32_t
     for (int i = 0; i < n_seq; ++i) out_counts[i] = 0;
     if (max_new <= 0) return POCR_OK;
     RC(model_ready(m));
-    if (m->vnni) return fail(POCR_ERR_UNSUPPORTED, "pocr_decode_batch: the batched kernels compute plain mode only");
     CHECK_INJECT("decode_batch");
     std::lock_guard<std::mutex> lk(m->ctx->mu);
     for (int i = 0; i < n_seq; ++i) RC(seq_idle(seqs[i], "pocr_decode_batch"));
@@ -2936,6 +2935,19 @@ extern "C" int pocr_decode_batch(pocr_seq *const *seqs, int n_seq, const int32_t
     for (int i = 0; i < n_seq; ++i)
         if (seqs[i]->len + steps_needed > seqs[i]->cap || max_new > seqs[i]->max_tokens)
             return fail(POCR_ERR_ARG, "pocr_decode_batch: sequence %d: %d steps exceed capacity", i, steps_needed);
+    // VNNI mode: each member runs its own decode loop of the mode's
+    // single-sequence step (the members are independent, so their streams
+    // are what decoding each alone gives, as the reference's server computes
+    // them: one request per goroutine)
+    if (m->vnni) {
+        for (int i = 0; i < n_seq; ++i) {
+            const int n = decode_locked(seqs[i], first_tokens[i], first_positions[i], max_new, eos, n_eos,
+                                        out_tokens + (size_t)i * max_new);
+            if (n < 0) return n;
+            out_counts[i] = n;
+        }
+        return POCR_OK;
+    }
     DecodeBatch b;
     b.m = m;
     b.n = n_seq;
@@ -3094,7 +3106,6 @@ extern "C" int pocr_batch_join(pocr_batch *b, pocr_seq *s, int32_t first_token, 
     if (s->m != b->m) return fail(POCR_ERR_ARG, "pocr_batch_join: the sequence belongs to another model");
     if (first_token < 0 || first_token >= b->m->cfg.vocab) return fail(POCR_ERR_ARG, "pocr_batch_join: token out of vocab");
     RC(model_ready(b->m));
-    if (b->m->vnni) return fail(POCR_ERR_UNSUPPORTED, "pocr_batch_join: the batched kernels compute plain mode only");
     CHECK_INJECT("batch_join");
     std::lock_guard<std::mutex> lk(b->m->ctx->mu);
     HIP_TRY(hipSetDevice(b->m->ctx->device));
@@ -3170,11 +3181,25 @@ extern "C" int pocr_batch_step(pocr_batch *b, int max_steps) {
             ++decoding;
         }
     if (decoding == 0) return 0;
-    if (!b->cur) RC(batch_capture(b));
     hipStream_t st = b->m->ctx->stream;
-    for (int i = 0; i < k; ++i) {
-        if (b->use_graph) HIP_TRY(hipGraphLaunch(b->cur->exec, st));
-        else RC(enqueue_batch_step(*b->cur));
+    if (b->m->vnni) {
+        // VNNI mode: every decoding member takes k steps of the mode's
+        // single-sequence step graph (its state and token list advance as
+        // under the batched step)
+        for (auto &mb : b->members) {
+            if (mb.finished) continue;
+            if (b->use_graph) RC(build_decode_graph(mb.s));
+            for (int i = 0; i < k; ++i) {
+                if (b->use_graph) HIP_TRY(hipGraphLaunch(mb.s->decode_exec, st));
+                else RC(enqueue_step(mb.s, 1, true, false));
+            }
+        }
+    } else {
+        if (!b->cur) RC(batch_capture(b));
+        for (int i = 0; i < k; ++i) {
+            if (b->use_graph) HIP_TRY(hipGraphLaunch(b->cur->exec, st));
+            else RC(enqueue_batch_step(*b->cur));
+        }
     }
     StepState hs;
     std::vector<int32_t> tok;

@@ -145,11 +145,7 @@ def test_vnni_mode_rules(ctx, rng):
     with pytest.raises(lib.PocrError) as e:
         gm.set_vnni(False)
     assert e.value.code == lib.POCR_ERR_ARG
-    # the batched decode computes plain mode only
     s2 = gm.seq(16)
-    with pytest.raises(lib.PocrError) as e:
-        lib.decode_batch([s, s2], [1, 2], [0, 0], 4, eos=())
-    assert e.value.code == lib.POCR_ERR_UNSUPPORTED
     # pocr_prefill takes its rows as token steps: the same cache and logits
     pos = np.array([[p, p, p] for p in range(3)], np.int32)
     tok, lp = s.prefill(w["embed"][[5, 6, 7]], pos, want_logits=True)
@@ -161,6 +157,68 @@ def test_vnni_mode_rules(ctx, rng):
             assert np.array_equal(a, b)
     s.close()
     s2.close()
+    gm.close()
+
+
+def _prefilled(gm, ids, budget):
+    """A sequence holding the prompt, and the first token the prompt chose."""
+    s = gm.seq(ids.size + budget)
+    first = int(s.generate(ids, 1, eos=(), use_prefill=True)[0])
+    return s, first
+
+
+@pytest.mark.parametrize("qtype", [Q4, Q6], ids=["q4", "q6"])
+def test_vnni_decode_batch(orc, ctx, qtype):
+    """pocr_decode_batch in the VNNI mode: four sequences, each stream
+    bit-identical to the oracle's VNNI-mode stream of that sequence alone
+    (the reference serves each request on its own), one of them cut by an
+    EOS id."""
+    w, om, gm = _pair(orc, ctx, MID, qtype, seed=9)
+    prompts = [synth.prompt_ids(n, seed=90 + n, high=MID.vocab) for n in (13, 27, 8, 20)]
+    full = [list(om.generate(ids, 14, eos=())) for ids in prompts]
+    stop = full[2][6]
+    want = [f[: f.index(stop) + 1] if stop in f else f for f in full]
+    seqs = [_prefilled(gm, ids, 14) for ids in prompts]
+    got = [list(t) for t in lib.decode_batch([s for s, _ in seqs], [f for _, f in seqs],
+                                             [ids.size for ids in prompts], 14, eos=(stop,))]
+    assert got == want
+    for (s, _), ids, g in zip(seqs, prompts, got):
+        assert len(s) == ids.size + len(g) - 1
+        s.close()
+    gm.close()
+
+
+def test_vnni_continuous_batch(orc, ctx):
+    """Continuous batching in the VNNI mode: members join at different token
+    steps with different budgets and leave when done; every stream is the
+    oracle's VNNI-mode stream of that sequence alone."""
+    w, om, gm = _pair(orc, ctx, MID, Q4, seed=11)
+    lens, budgets = [11, 26, 7, 19], [12, 7, 15, 9]
+    prompts = [synth.prompt_ids(n, seed=70 + i, high=MID.vocab) for i, n in enumerate(lens)]
+    want = [list(om.generate(ids, bud, eos=())) for ids, bud in zip(prompts, budgets)]
+    b = lib.Batch(gm)
+    seqs = [_prefilled(gm, ids, bud) for ids, bud in zip(prompts, budgets)]
+    b.join(seqs[0][0], seqs[0][1], lens[0], budgets[0], eos=())
+    assert b.step(3) == 1
+    b.join(seqs[1][0], seqs[1][1], lens[1], budgets[1], eos=())
+    b.join(seqs[2][0], seqs[2][1], lens[2], budgets[2], eos=())
+    assert b.step(2) == 3
+    b.join(seqs[3][0], seqs[3][1], lens[3], budgets[3], eos=())
+    got, pending = {}, [0, 1, 2, 3]
+    for _ in range(100):
+        b.step(4)
+        for i in list(pending):
+            n, done = b.poll(seqs[i][0])
+            if done:
+                got[i] = list(b.leave(seqs[i][0]))
+                pending.remove(i)
+        if not pending:
+            break
+    assert [got[i] for i in range(4)] == want
+    for i in range(4):
+        assert len(seqs[i][0]) == lens[i] + budgets[i] - 1
+        seqs[i][0].close()
+    b.close()
     gm.close()
 
 
