@@ -400,11 +400,12 @@ constexpr int kHeadWideVec = 16;
 template <int QT, int NS>
 struct HeadWideShape {
     static constexpr int COLS = 256 * NS;
-    static constexpr int ROW_BYTES = QT == QT_Q4 ? COLS / 2 : COLS;
-    static constexpr int LINES = ROW_BYTES / 128;  // 128-byte lines per row
+    static constexpr int ROW_BYTES = QT == QT_Q4 ? COLS / 2 : (QT == QT_Q6 ? COLS / 4 * 3 : COLS);
+    static constexpr int LINES = ROW_BYTES / 128;  // 128-byte lines per row (Q4, Q8)
     static constexpr int CP = QT == QT_Q4 ? 32 : 16;  // codes per 16-byte piece
     static constexpr int SPL = head_steps_per_load<QT>();
-    static constexpr int STEPS = LINES * 2 * SPL;  // MFMA steps of 64 columns
+    // MFMA steps of 64 columns
+    static constexpr int STEPS = QT == QT_Q6 ? COLS / 64 : LINES * 2 * SPL;
     static constexpr int PLANE_BYTES = STEPS * 3 * 4 * kHeadWideVec * 16;
     static constexpr int R0 = POCR_HEAD_WIDE_LANE_BYTES * 4 / ROW_BYTES;
     static constexpr int R = R0 > 1 ? R0 : 1;  // row blocks per wave
@@ -417,6 +418,10 @@ struct HeadWideShape {
 template <int QT, int NS>
 __device__ __forceinline__ int head_plane_off(int c, int pl, int v) {
     using SH = HeadWideShape<QT, NS>;
+    if constexpr (QT == QT_Q6) {
+        // k_head_wide_q6: step c/64, lane group (c%64)/16, natural order
+        return (((c / 64) * 3 + pl) * 4 + (c % 64) / 16) * 256 + v * 16 + c % 16;
+    }
     const int ln = c / (8 * SH::CP), rem = c % (8 * SH::CP);
     const int g = rem / (2 * SH::CP), rem2 = rem % (2 * SH::CP);
     const int par = rem2 / SH::CP, h = (rem2 % SH::CP) / 16;
@@ -692,6 +697,165 @@ __global__ void __launch_bounds__(kThreads, 2) k_head_wide(HeadWideParams p) {
         }
     }
     // the best key of vector lr over the four lane groups, then the waves
+    {
+        const unsigned long long o16 = shfl_xor_u64(key, 16);
+        key = o16 > key ? o16 : key;
+        const unsigned long long o32 = shfl_xor_u64(key, 32);
+        key = o32 > key ? o32 : key;
+    }
+    if (lg == 0) kred[lr][wave] = key;
+    __syncthreads();
+    if ((int)threadIdx.x < nvec) {
+        const int vv = threadIdx.x;
+        unsigned long long m = kred[vv][0];
+#pragma unroll
+        for (int w = 1; w < kWaves; ++w) m = kred[vv][w] > m ? kred[vv][w] : m;
+        StepState *st = p.st[0];
+#pragma unroll
+        for (int u = 1; u < NV; ++u) st = vv == u ? p.st[u] : st;
+        if (m && st) atomicMax(&st->argmax_slot[(blockIdx.x % kArgSlots) * kSlotPitch], m);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// k_head_wide_q6: the 2-to-16-vector head for Q6 rows.  Q6 rows (3 bytes per
+// 4 codes) do not fall on 128-byte lines, so instead of k_head_wide's line
+// halves every load instruction reads 16 rows × 48 bytes: lane (lr, lg) takes
+// the 12 bytes (16 codes) at 48·step + 12·lg of row lr, which is exactly its
+// A operand for MFMA step `step` (64 columns).  The four loads of a 192-byte
+// stretch of the 16 rows follow each other, so each line is fetched once.
+// B column lr = vector lr (one tile per digit plane); a wave owns R blocks of
+// 16 rows over all the columns, so no cross-wave sums.  Scores, argmax and
+// digit planes (k_head_digits, Q6 plane order) as k_head_wide.
+// ---------------------------------------------------------------------------
+template <int NS>
+__global__ void __launch_bounds__(kThreads, 2) k_head_wide_q6(HeadWideParams p) {
+    using SH = HeadWideShape<QT_Q6, NS>;
+    constexpr int STEPS = SH::STEPS, R = SH::R;
+    constexpr int NV = kHeadWideVec;
+    static_assert(R >= 1, "at least one block of 16 rows per wave");
+    static_assert(SH::PLANE_BYTES % (16 * NV) == 0, "planes in 16-vector groups of 16 bytes");
+    __shared__ __attribute__((aligned(16))) int8_t xdig[SH::PLANE_BYTES];
+    __shared__ unsigned long long kred[NV][kWaves];
+    asm volatile("" ::"s"(p.m.data), "s"(p.m.scale), "s"(p.planes), "s"(p.vscale), "s"(p.vbias), "s"(p.out),
+                 "s"(p.rows), "s"(p.m.row_bytes), "s"(p.out_stride), "s"(p.nvec), "s"(p.out_vec4));
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lr = lane & 15, lg = lane >> 4;
+    const int rows = p.rows;
+    const int nvec = p.nvec;
+    const int r0 = (blockIdx.x * kWaves + wave) * 16 * R;  // this wave's first row
+
+    // 1. the live vectors' digit pieces, requested first
+    constexpr int GROUPS = SH::PLANE_BYTES / (16 * NV);
+    constexpr int MAXK = (GROUPS * NV + kThreads - 1) / kThreads;
+    const int npieces = GROUPS * nvec;
+    v4i piece[MAXK];
+#pragma unroll
+    for (int k = 0; k < MAXK; ++k) {
+        const int id = (int)threadIdx.x + k * kThreads;
+        if (id < npieces) {
+            const int off = (id / nvec) * 256 + (id % nvec) * 16;
+            piece[k] = *reinterpret_cast<const v4i *>(p.planes + off);
+        }
+    }
+    asm volatile("" ::: "memory");  // the weight requests stay behind the pieces
+
+    // 2. every weight byte of the wave's rows (past the end: the last row,
+    // loaded and never scored), in the order the MFMAs consume them
+    uint32_t raw[R][STEPS][3];
+    const uint8_t *wrow[R];
+#pragma unroll
+    for (int rb = 0; rb < R; ++rb)
+        wrow[rb] = p.m.data + (size_t)min(r0 + 16 * rb + lr, rows - 1) * p.m.row_bytes + 12 * lg;
+#pragma unroll
+    for (int st = 0; st < STEPS; ++st)
+#pragma unroll
+        for (int rb = 0; rb < R; ++rb) {
+            const uint32_t *q = reinterpret_cast<const uint32_t *>(wrow[rb] + 48 * st);
+#pragma unroll
+            for (int w = 0; w < 3; ++w) raw[rb][st][w] = __builtin_nontemporal_load(q + w);
+        }
+#pragma unroll
+    for (int k = 0; k < MAXK; ++k) {
+        const int id = (int)threadIdx.x + k * kThreads;
+        if (id < npieces) {
+            const int off = (id / nvec) * 256 + (id % nvec) * 16;
+            *reinterpret_cast<v4i *>(xdig + off) = piece[k];
+        }
+    }
+    float rsc[R][4];  // row scales, first used after the MFMAs
+#pragma unroll
+    for (int rb = 0; rb < R; ++rb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) rsc[rb][i] = p.m.scale[min(r0 + 16 * rb + 4 * lg + i, rows - 1)];
+    __syncthreads();
+
+    // 3. the MFMAs: A = row lr's codes of step st, K slice lg; B column lr =
+    // vector lr's digits of the same 16 columns
+    v4i acc[R][3];
+#pragma unroll
+    for (int rb = 0; rb < R; ++rb)
+#pragma unroll
+        for (int pl = 0; pl < 3; ++pl) acc[rb][pl] = v4i{0, 0, 0, 0};
+#pragma unroll
+    for (int st = 0; st < STEPS; ++st) {
+        v4i b[3];
+#pragma unroll
+        for (int pl = 0; pl < 3; ++pl) b[pl] = *reinterpret_cast<const v4i *>(xdig + (st * 3 + pl) * 1024 + 16 * lane);
+#pragma unroll
+        for (int rb = 0; rb < R; ++rb) {
+            RawCodes<QT_Q6> rc;
+#pragma unroll
+            for (int w = 0; w < 3; ++w) rc.d[w] = raw[rb][st][w];
+            const v4i a = unpack_codes16<QT_Q6>(rc);
+#pragma unroll
+            for (int pl = 0; pl < 3; ++pl)
+                acc[rb][pl] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b[pl], acc[rb][pl], 0, 0, 0);
+        }
+    }
+
+    // 4. lane (lr, lg) holds C[4lg + i][lr]: rows r0 + 16rb + 4lg + i of
+    // vector lr.  Scores as k_head_mfma forms them.
+    const int v = lr;
+    const bool live = v < nvec;
+    int b0 = 0, b1 = 0, b2 = 0;
+    float my_sx = 1.0f;
+    if (live) {
+        b0 = p.vbias[v * 3];
+        b1 = p.vbias[v * 3 + 1];
+        b2 = p.vbias[v * 3 + 2];
+        my_sx = p.vscale[v];
+    }
+    unsigned long long key = 0ull;
+#pragma unroll
+    for (int rb = 0; rb < R; ++rb) {
+        const int rr = r0 + 16 * rb + 4 * lg;
+        float sc[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            // |Σ u·d| < 2^24 per plane (cols ≤ 2048): exact converts
+            const float f0 = (float)(acc[rb][0][i] - b0);
+            const float f1 = (float)(acc[rb][1][i] - b1);
+            const float f2 = (float)(acc[rb][2][i] - b2);
+            sc[i] = fmaf(f2, 1.0f / 16384.0f, fmaf(f1, 1.0f / 128.0f, f0)) * my_sx * rsc[rb][i];
+            if (live && rr + i < rows) {
+                const unsigned long long k = argmax_key(sc[i], rr + i);
+                key = k > key ? k : key;
+            }
+        }
+        if (p.out && live) {
+            float *o = p.out + (size_t)v * p.out_stride + rr;
+            if (p.out_vec4) {
+                if (rr < rows) *reinterpret_cast<float4 *>(o) = make_float4(sc[0], sc[1], sc[2], sc[3]);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    if (rr + i < rows) o[i] = sc[i];
+            }
+        }
+    }
     {
         const unsigned long long o16 = shfl_xor_u64(key, 16);
         key = o16 > key ? o16 : key;

@@ -445,8 +445,9 @@ static int launch_head(hipStream_t s, const void *fn, const GemvParams &p, int p
     return POCR_OK;
 }
 
-// The head for 2 to 16 vectors (head.hpp: k_head_digits, then k_head_wide):
-// Q4 or Q8 rows of 1024 or 2048 columns on 16-byte boundaries.
+// The head for 2 to 16 vectors (head.hpp: k_head_digits, then k_head_wide,
+// or k_head_wide_q6 for Q6 rows): rows of 1024 or 2048 columns on 16-byte
+// boundaries.
 struct HeadWidePlan {
     const void *digits = nullptr, *head = nullptr;
     int rows_per_wg = 0, plane_bytes = 0;
@@ -456,7 +457,8 @@ template <int QT, int NS>
 static HeadWidePlan head_wide_plan() {
     HeadWidePlan h;
     h.digits = reinterpret_cast<const void *>(&k_head_digits<QT, NS>);
-    h.head = reinterpret_cast<const void *>(&k_head_wide<QT, NS>);
+    if constexpr (QT == QT_Q6) h.head = reinterpret_cast<const void *>(&k_head_wide_q6<NS>);
+    else h.head = reinterpret_cast<const void *>(&k_head_wide<QT, NS>);
     h.rows_per_wg = HeadWideShape<QT, NS>::ROWS_PER_WG;
     h.plane_bytes = HeadWideShape<QT, NS>::PLANE_BYTES;
     return h;
@@ -468,6 +470,7 @@ static bool plan_head_wide(const DevMat &m, HeadWidePlan *h) {
     const bool ns4 = m.cols == 1024;
     if (m.qtype == POCR_Q4) *h = ns4 ? head_wide_plan<QT_Q4, 4>() : head_wide_plan<QT_Q4, 8>();
     else if (m.qtype == POCR_Q8) *h = ns4 ? head_wide_plan<QT_Q8, 4>() : head_wide_plan<QT_Q8, 8>();
+    else if (m.qtype == POCR_Q6) *h = ns4 ? head_wide_plan<QT_Q6, 4>() : head_wide_plan<QT_Q6, 8>();
     else return false;
     return true;
 }
