@@ -428,7 +428,11 @@ static const void *plan_head(const GemvParams &p, int nmat, int nv) {
     return nullptr;
 }
 
-static int launch_head(hipStream_t s, const void *fn, const GemvParams &p, int pro, int nv, const GemvNV *q) {
+// argmax: fold each vector's best (score, row) into its step state's slots;
+// otherwise only the scores are written (a sampling head's logits: the slots
+// then carry the drawn token and must not be touched)
+static int launch_head(hipStream_t s, const void *fn, const GemvParams &p, int pro, int nv, const GemvNV *q,
+                       bool argmax) {
     HeadParams h{};
     h.m = p.m[0];
     h.rows = p.rows;
@@ -438,7 +442,8 @@ static int launch_head(hipStream_t s, const void *fn, const GemvParams &p, int p
     h.eps = p.eps;
     h.out = p.out;
     h.out_stride = nv > 1 ? q->o_stride : 0;
-    for (int v = 0; v < kHeadMaxVec; ++v) h.st[v] = v == 0 ? p.st : (v < nv ? q->stv[v - 1] : p.st);
+    for (int v = 0; v < kHeadMaxVec; ++v)
+        h.st[v] = !argmax ? nullptr : (v == 0 ? p.st : (v < nv ? q->stv[v - 1] : p.st));
     const int blocks = (p.rows + 15) / 16;
     void *args[] = {&h};
     HIP_TRY(hipLaunchKernel(fn, dim3((blocks + kHeadRB - 1) / kHeadRB), dim3(kThreads), args, 0, s));
@@ -527,7 +532,12 @@ int pocr::gemv_launch(hipStream_t s, GemvParams p, int nmat, int pro, int epi, i
                       const GemvNV *q) {
     if (nv > 1 && !q) return fail(POCR_ERR_ARG, "gemv: %d vectors need their strides", nv);
     if (epi == EPI_ARGMAX && p.st) {
-        if (const void *fn = plan_head(p, nmat, nv)) return launch_head(s, fn, p, pro, nv, q);
+        if (const void *fn = plan_head(p, nmat, nv)) return launch_head(s, fn, p, pro, nv, q, true);
+    }
+    // every score of an LM-head-sized matrix (the sampling head's logits, a
+    // one-row pocr_matvec): the same kernel with the argmax off
+    if (epi == EPI_PLAIN && nv == 1 && p.out && p.rows >= kHeadWideMinRows && !p.residual) {
+        if (const void *fn = plan_head(p, nmat, nv)) return launch_head(s, fn, p, pro, nv, q, false);
     }
     GemvPlan plan;
     const int nm = nmat == 2 ? 2 : (p.seg_end[0] == p.rows ? 1 : (p.seg_end[1] == p.rows ? 2 : 3));
@@ -1936,11 +1946,13 @@ static int time_matvec_impl(pocr_ctx *ctx, const pocr_weight *const *weights, in
         p.st = ctx->state.as<StepState>();  // argmax slots (the key only grows: no reset needed)
         return p;
     };
-    // the greedy head times the kernel the decode runs: the MFMA head where
-    // the shape allows it
-    const void *hfn = argmax ? plan_head(params(0), 1, 1) : nullptr;
+    // the kernel pocr_matvec / the decode run: the MFMA head for the greedy
+    // argmax and for every score of an LM-head-sized matrix, where the shape
+    // allows it
+    const void *hfn = (argmax || w0->rows >= kHeadWideMinRows) ? plan_head(params(0), 1, 1) : nullptr;
     auto launch = [&](int i) {
-        return hfn ? launch_head(s, hfn, params(i), PRO_COPY, 1, nullptr) : launch_gemv(s, plan, params(i), PRO_COPY, epi);
+        return hfn ? launch_head(s, hfn, params(i), PRO_COPY, 1, nullptr, argmax)
+                   : launch_gemv(s, plan, params(i), PRO_COPY, epi);
     };
     hipEvent_t e0, e1;
     HIP_TRY(hipEventCreate(&e0));
