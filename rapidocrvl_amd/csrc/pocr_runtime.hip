@@ -622,6 +622,17 @@ static int matvec_rows(pocr_ctx *ctx, const pocr_weight *w, const float *x, int 
     hipStream_t s = ctx->stream;
     // LM-head-sized matrices: up to 16 rows of x per weight pass on the matrix
     // cores (one power-of-two digit scale per row of x)
+    // two rows: the 2-vector head (103424x1024 Q4 13.2 us against 19.3 on the
+    // 16-vector kernel; at 4 rows the two tie)
+    if (m == 2 && w->rows >= kHeadWideMinRows) {
+        GemvParams p = gemv_params_1(w);
+        p.x = x;
+        p.out = out;
+        GemvNV q{};
+        q.x_stride = w->cols;
+        q.o_stride = w->rows;
+        if (const void *fn = plan_head(p, 1, m)) return launch_head(s, fn, p, PRO_COPY, m, &q, false);
+    }
     if (m > 1 && w->rows >= kHeadWideMinRows && head_wide_ok(w)) {
         RC(ctx->gxd.ensure(head_wide_plane_bytes(w)));
         RC(ctx->gxs.ensure(kHeadWideVec * sizeof(float)));
