@@ -719,23 +719,32 @@ __global__ void __launch_bounds__(kThreads, 2) k_head_wide(HeadWideParams p) {
 
 // ---------------------------------------------------------------------------
 // k_head_wide_q6: the 2-to-16-vector head for Q6 rows.  Q6 rows (3 bytes per
-// 4 codes) do not fall on 128-byte lines, so instead of k_head_wide's line
-// halves every load instruction reads 16 rows × 48 bytes: lane (lr, lg) takes
-// the 12 bytes (16 codes) at 48·step + 12·lg of row lr, which is exactly its
-// A operand for MFMA step `step` (64 columns).  The four loads of a 192-byte
-// stretch of the 16 rows follow each other, so each line is fetched once.
+// 4 codes) do not fall on 128-byte lines.  Every load instruction reads 4 rows
+// × 192 contiguous bytes (a unit: 256 codes): lane L takes the 12 bytes (16
+// codes) at 12·(L%16) of row L/16 of its row group.  The MFMA wants lane
+// (lr, lg) to hold row lr's 16 codes of K slice lg instead, so each wave
+// passes its units through a wave-private LDS tile (rows padded to 49 dwords
+// against bank conflicts; a wave's LDS accesses stay in order, so no barrier)
+// and reads A back as row lr, piece 4k + lg for MFMA step k of the unit.
+// Loading 16 rows × 48 bytes per instruction, which is the A operand as
+// loaded, streamed at half the rate.
 // B column lr = vector lr (one tile per digit plane); a wave owns R blocks of
 // 16 rows over all the columns, so no cross-wave sums.  Scores, argmax and
-// digit planes (k_head_digits, Q6 plane order) as k_head_wide.
+// digit planes (k_head_digits, Q6 plane order: step c/64, K slice (c%64)/16)
+// as k_head_wide.
 // ---------------------------------------------------------------------------
 template <int NS>
 __global__ void __launch_bounds__(kThreads, 2) k_head_wide_q6(HeadWideParams p) {
     using SH = HeadWideShape<QT_Q6, NS>;
     constexpr int STEPS = SH::STEPS, R = SH::R;
+    constexpr int UNITS = STEPS / 4;  // 192-byte units per row
+    constexpr int TRW = 49;           // dwords per row of the transpose tile (48 + 1 pad)
     constexpr int NV = kHeadWideVec;
     static_assert(R >= 1, "at least one block of 16 rows per wave");
+    static_assert(STEPS % 4 == 0, "whole 192-byte units");
     static_assert(SH::PLANE_BYTES % (16 * NV) == 0, "planes in 16-vector groups of 16 bytes");
     __shared__ __attribute__((aligned(16))) int8_t xdig[SH::PLANE_BYTES];
+    __shared__ uint32_t tr[kWaves][R][16][TRW];
     __shared__ unsigned long long kred[NV][kWaves];
     asm volatile("" ::"s"(p.m.data), "s"(p.m.scale), "s"(p.planes), "s"(p.vscale), "s"(p.vbias), "s"(p.out),
                  "s"(p.rows), "s"(p.m.row_bytes), "s"(p.out_stride), "s"(p.nvec), "s"(p.out_vec4));
@@ -763,20 +772,26 @@ __global__ void __launch_bounds__(kThreads, 2) k_head_wide_q6(HeadWideParams p) 
     asm volatile("" ::: "memory");  // the weight requests stay behind the pieces
 
     // 2. every weight byte of the wave's rows (past the end: the last row,
-    // loaded and never scored), in the order the MFMAs consume them
-    uint32_t raw[R][STEPS][3];
-    const uint8_t *wrow[R];
+    // loaded and never scored), unit by unit in the order the MFMAs consume
+    // them: row group g of block rb is rows 16rb + 4g + L/16
+    uint32_t raw[UNITS][R][4][3];
+    const uint8_t *wrow[R][4];
 #pragma unroll
     for (int rb = 0; rb < R; ++rb)
-        wrow[rb] = p.m.data + (size_t)min(r0 + 16 * rb + lr, rows - 1) * p.m.row_bytes + 12 * lg;
 #pragma unroll
-    for (int st = 0; st < STEPS; ++st)
+        for (int g = 0; g < 4; ++g)
+            wrow[rb][g] = p.m.data + (size_t)min(r0 + 16 * rb + 4 * g + (lane >> 4), rows - 1) * p.m.row_bytes +
+                          12 * (lane & 15);
 #pragma unroll
-        for (int rb = 0; rb < R; ++rb) {
-            const uint32_t *q = reinterpret_cast<const uint32_t *>(wrow[rb] + 48 * st);
+    for (int u = 0; u < UNITS; ++u)
 #pragma unroll
-            for (int w = 0; w < 3; ++w) raw[rb][st][w] = __builtin_nontemporal_load(q + w);
-        }
+        for (int rb = 0; rb < R; ++rb)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const uint32_t *q = reinterpret_cast<const uint32_t *>(wrow[rb][g] + 192 * u);
+#pragma unroll
+                for (int w = 0; w < 3; ++w) raw[u][rb][g][w] = __builtin_nontemporal_load(q + w);
+            }
 #pragma unroll
     for (int k = 0; k < MAXK; ++k) {
         const int id = (int)threadIdx.x + k * kThreads;
@@ -800,20 +815,39 @@ __global__ void __launch_bounds__(kThreads, 2) k_head_wide_q6(HeadWideParams p) 
 #pragma unroll
         for (int pl = 0; pl < 3; ++pl) acc[rb][pl] = v4i{0, 0, 0, 0};
 #pragma unroll
-    for (int st = 0; st < STEPS; ++st) {
-        v4i b[3];
+    for (int u = 0; u < UNITS; ++u) {
+        // this unit of the wave's rows into its LDS tile: row 4g + L/16,
+        // piece L%16 (the previous unit's reads have all been consumed)
 #pragma unroll
-        for (int pl = 0; pl < 3; ++pl) b[pl] = *reinterpret_cast<const v4i *>(xdig + (st * 3 + pl) * 1024 + 16 * lane);
+        for (int rb = 0; rb < R; ++rb)
 #pragma unroll
-        for (int rb = 0; rb < R; ++rb) {
-            RawCodes<QT_Q6> rc;
+            for (int g = 0; g < 4; ++g) {
+                uint32_t *d = &tr[wave][rb][4 * g + (lane >> 4)][3 * (lane & 15)];
 #pragma unroll
-            for (int w = 0; w < 3; ++w) rc.d[w] = raw[rb][st][w];
-            const v4i a = unpack_codes16<QT_Q6>(rc);
+                for (int w = 0; w < 3; ++w) d[w] = raw[u][rb][g][w];
+            }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int st = 4 * u + k;
+            v4i b[3];
 #pragma unroll
             for (int pl = 0; pl < 3; ++pl)
-                acc[rb][pl] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b[pl], acc[rb][pl], 0, 0, 0);
+                b[pl] = *reinterpret_cast<const v4i *>(xdig + (st * 3 + pl) * 1024 + 16 * lane);
+#pragma unroll
+            for (int rb = 0; rb < R; ++rb) {
+                // row lr, piece 4k + lg: columns 64·st + 16·lg .. +15
+                const uint32_t *a3 = &tr[wave][rb][lr][12 * k + 3 * lg];
+                RawCodes<QT_Q6> rc;
+#pragma unroll
+                for (int w = 0; w < 3; ++w) rc.d[w] = a3[w];
+                const v4i a = unpack_codes16<QT_Q6>(rc);
+#pragma unroll
+                for (int pl = 0; pl < 3; ++pl)
+                    acc[rb][pl] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b[pl], acc[rb][pl], 0, 0, 0);
+            }
         }
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
 
     // 4. lane (lr, lg) holds C[4lg + i][lr]: rows r0 + 16rb + 4lg + i of
