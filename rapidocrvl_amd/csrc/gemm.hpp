@@ -164,6 +164,115 @@ static __global__ void __launch_bounds__(kThreads) k_digitize(DigitizeParams p) 
     if (t == 0) p.xs[n] = S * factor;
 }
 
+// The same digit planes with one wave per token (four tokens per workgroup)
+// for K ≤ 1024·J: lane l of the token's wave takes the 16-column groups
+// 64j + l, j < ⌈K/1024⌉, which k_digitize gives thread 64j + l, and reduces
+// each j's partials with the same wave sum before adding them in j order, so
+// Σx², the maximum, the digits and the plane sums are bit-identical to
+// k_digitize's.  No barrier: at K = 1024, k_digitize keeps three of its four
+// waves idle through three workgroup barriers per token.
+template <int QT, int J>
+static __global__ void __launch_bounds__(kThreads) k_digitize_w(DigitizeParams p, int ntok) {
+    static_assert(J >= 1 && J <= 4, "1024-column slices, K ≤ 1024·J ≤ 4096");
+    const int lane = threadIdx.x & 63;
+    const int n = blockIdx.x * kWaves + (threadIdx.x >> 6);
+    if (n >= ntok) return;  // wave-uniform; no barrier below
+    float y[J][16];
+    bool valid[J];
+    int c0[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        c0[j] = 16 * (64 * j + lane);
+        valid[j] = c0[j] < p.K;
+        const int cl = valid[j] ? c0[j] : p.K - 16;  // clamped, never written
+        const float *xr = p.x + (size_t)n * p.x_stride + cl;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float4 v = reinterpret_cast<const float4 *>(xr)[i];
+            y[j][4 * i] = v.x;
+            y[j][4 * i + 1] = v.y;
+            y[j][4 * i + 2] = v.z;
+            y[j][4 * i + 3] = v.w;
+        }
+    }
+    float factor = 1.0f;
+    if (p.norm_w) {
+        // k_digitize adds its idle waves' zero partials after these: +0
+        // changes nothing
+        float tot = 0.0f;
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            float sg = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) sg = fmaf(y[j][i], y[j][i], sg);
+            const float pj = wave_sum(valid[j] ? sg : 0.0f);
+            tot = j == 0 ? pj : tot + pj;
+        }
+        factor = fast_rsqrt_ref(tot / (float)p.K + p.eps);
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            const int cl = valid[j] ? c0[j] : p.K - 16;
+            float w[16];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float4 v = reinterpret_cast<const float4 *>(p.norm_w + cl)[i];
+                w[4 * i] = v.x;
+                w[4 * i + 1] = v.y;
+                w[4 * i + 2] = v.z;
+                w[4 * i + 3] = v.w;
+            }
+#pragma unroll
+            for (int i = 0; i < 16; ++i) y[j][i] = y[j][i] * w[i];  // a lone product: nothing to contract
+        }
+    }
+    float m = 0.0f;
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) m = valid[j] ? fmaxf(m, fabsf(y[j][i])) : m;
+    m = wave_max(m);
+    int ex = 0;
+    (void)frexpf(m * (1.0f / 127.0f), &ex);  // m/127 < 2^ex; m = 0 → ex = 0
+    const float S = m > 0.0f ? ldexpf(1.0f, ex) : 1.0f;
+    int sd[3] = {0, 0, 0};
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        int d[3][16];
+        int sg[3] = {0, 0, 0};
+#pragma unroll
+        for (int c = 0; c < 16; ++c) {
+            const float tt = ldexpf(y[j][c], -ex);  // exact (no overflow of 2^-ex for tiny rows)
+            const float a = rintf(tt);
+            const float t1 = (tt - a) * 128.0f;
+            const float b = rintf(t1);
+            const int d2 = (int)rintf((t1 - b) * 128.0f);
+            const int pos = digit_pos16<QT>(c);
+            d[0][pos] = (int)a;
+            d[1][pos] = (int)b;
+            d[2][pos] = d2;
+            sg[0] += (int)a;
+            sg[1] += (int)b;
+            sg[2] += d2;
+        }
+        if (valid[j]) {
+#pragma unroll
+            for (int pl = 0; pl < 3; ++pl) {
+                *reinterpret_cast<int4 *>(p.xd + pl * p.plane_stride + (size_t)n * p.K + c0[j]) =
+                    make_int4(pack4(d[pl][0], d[pl][1], d[pl][2], d[pl][3]),
+                              pack4(d[pl][4], d[pl][5], d[pl][6], d[pl][7]),
+                              pack4(d[pl][8], d[pl][9], d[pl][10], d[pl][11]),
+                              pack4(d[pl][12], d[pl][13], d[pl][14], d[pl][15]));
+                sd[pl] += sg[pl];
+            }
+        }
+    }
+    int tot[3];
+#pragma unroll
+    for (int pl = 0; pl < 3; ++pl) tot[pl] = (int)wave_sum((float)sd[pl]);  // |Σ| ≤ 4096·127: exact in f32
+    if (lane < 3) p.xb[n * 4 + lane] = lane == 0 ? tot[0] : (lane == 1 ? tot[1] : tot[2]);
+    if (lane == 0) p.xs[n] = S * factor;
+}
+
 // ---------------------------------------------------------------------------
 // MFMA GEMM: Y[n][r] = epilogue(scale[r]·xs[n]·(D0 + D1/2^7 + D2/2^14)),
 // D_p = Σ_k u[r][k]·d_p[n][k] − IBIAS·Σ_k d_p[n][k].  Workgroup: 256 rows ×
