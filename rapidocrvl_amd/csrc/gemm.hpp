@@ -37,11 +37,25 @@ struct DigitizeParams {
     const float *norm_w;   // null → no RMSNorm
     float eps;
     int K;                 // multiple of 16, ≤ 8192
-    int8_t *xd;            // planes [3][npad][K]
+    int8_t *xd;            // planes [3][npad][K], or the tile layout below
     size_t plane_stride;   // npad·K
     float *xs;             // [n] row scale
     int *xb;               // [n][4] Σd per plane (4th unused)
+    int tiled;             // 1: the prefill GEMM's tile layout (K a multiple of 128)
 };
+
+// Byte offset of the 16-column group at column c0 (a multiple of 16) of token
+// n, digit plane pl.  Plane layout: [pl][npad][K].  Tile layout (the operand
+// order of k_gemm_lds, so each of its loads reads 1 KB of consecutive bytes):
+// [token tile n/32][stage c0/128][chunk j][lane][16 B], where in stage u the
+// MFMA step s, plane pl and token block tb form chunk j = (3s + pl)·2 + tb and
+// lane lr + 16·lg holds token 16tb + lr, columns 128u + 32lg + 16s .. +15.
+__device__ __forceinline__ size_t digit_off(const DigitizeParams &p, int pl, int n, int c0) {
+    if (!p.tiled) return pl * p.plane_stride + (size_t)n * p.K + c0;
+    const int g = c0 >> 4, u = g >> 3, gi = g & 7;
+    const int tl = n & 31, j = ((gi & 1) * 3 + pl) * 2 + (tl >> 4), lane = (tl & 15) + 16 * (gi >> 1);
+    return ((size_t)((n >> 5) * (p.K >> 7) + u) * 12 + j) * 1024 + lane * 16;
+}
 
 template <int QT, int G>
 static __global__ void __launch_bounds__(kThreads) k_digitize(DigitizeParams p) {
@@ -139,7 +153,7 @@ static __global__ void __launch_bounds__(kThreads) k_digitize(DigitizeParams p) 
         if (valid[g]) {
 #pragma unroll
             for (int pl = 0; pl < 3; ++pl) {
-                *reinterpret_cast<int4 *>(p.xd + pl * p.plane_stride + (size_t)n * p.K + c0[g]) =
+                *reinterpret_cast<int4 *>(p.xd + digit_off(p, pl, n, c0[g])) =
                     make_int4(pack4(d[pl][0], d[pl][1], d[pl][2], d[pl][3]),
                               pack4(d[pl][4], d[pl][5], d[pl][6], d[pl][7]),
                               pack4(d[pl][8], d[pl][9], d[pl][10], d[pl][11]),
@@ -257,7 +271,7 @@ static __global__ void __launch_bounds__(kThreads) k_digitize_w(DigitizeParams p
         if (valid[j]) {
 #pragma unroll
             for (int pl = 0; pl < 3; ++pl) {
-                *reinterpret_cast<int4 *>(p.xd + pl * p.plane_stride + (size_t)n * p.K + c0[j]) =
+                *reinterpret_cast<int4 *>(p.xd + digit_off(p, pl, n, c0[j])) =
                     make_int4(pack4(d[pl][0], d[pl][1], d[pl][2], d[pl][3]),
                               pack4(d[pl][4], d[pl][5], d[pl][6], d[pl][7]),
                               pack4(d[pl][8], d[pl][9], d[pl][10], d[pl][11]),
@@ -413,6 +427,7 @@ __device__ __forceinline__ void gemm_store(const GemmParams &p, int epi, int n, 
 // for the small kernel, of 64 for the prefill one)
 struct GemmSeg {
     const uint8_t *base[2];
+    const uint8_t *tiled[2];
     const float *scale[2];
     int start;
 };
@@ -420,24 +435,19 @@ template <int NMAT>
 __device__ __forceinline__ GemmSeg gemm_seg(const GemmParams &p, int r0) {
     GemmSeg g;
     g.base[1] = nullptr;
+    g.tiled[1] = nullptr;
     g.scale[1] = nullptr;
     g.start = 0;
+    const int i = NMAT == 2 ? 0 : (r0 >= p.seg_end[1] ? 2 : (r0 >= p.seg_end[0] ? 1 : 0));
+    g.base[0] = p.m[i].data;
+    g.tiled[0] = p.m[i].tiled;
+    g.scale[0] = p.m[i].scale;
     if (NMAT == 2) {
-        g.base[0] = p.m[0].data;
         g.base[1] = p.m[1].data;
-        g.scale[0] = p.m[0].scale;
+        g.tiled[1] = p.m[1].tiled;
         g.scale[1] = p.m[1].scale;
-    } else if (r0 >= p.seg_end[1]) {
-        g.base[0] = p.m[2].data;
-        g.scale[0] = p.m[2].scale;
-        g.start = p.seg_end[1];
-    } else if (r0 >= p.seg_end[0]) {
-        g.base[0] = p.m[1].data;
-        g.scale[0] = p.m[1].scale;
-        g.start = p.seg_end[0];
-    } else {
-        g.base[0] = p.m[0].data;
-        g.scale[0] = p.m[0].scale;
+    } else if (i > 0) {
+        g.start = p.seg_end[i - 1];
     }
     return g;
 }
@@ -590,9 +600,10 @@ __device__ __forceinline__ int2 xcd_tile() {
 // ---------------------------------------------------------------------------
 // Prefill GEMM with both operands streamed into LDS by direct loads
 // (global_load_lds: HBM → LDS with no staging registers) through a ring of
-// NST stages of 128 columns.  Workgroup: 4 waves along the rows (256 rows, or
-// 128 gate + 128 up rows) × 32 tokens; wave tile 64 rows × 32 tokens, 24
-// MFMAs (4 row blocks × 2 token blocks × 3 digit planes) per 64 columns.
+// NST stages of 128 columns.  Workgroup: 4 waves along the rows × 32 tokens;
+// a wave owns RB blocks of 16 rows of each of its NMAT matrices (gate and up
+// side by side) × 32 tokens: NMAT·RB·2·3 MFMAs (row blocks × 2 token blocks ×
+// 3 digit planes) per 64 columns.
 //
 // K order of the MFMA operands: in stage u, MFMA step s, lane group lg takes
 // columns 128u + 32lg + 16s .. +15 (A and B alike; inside a 16-column group
@@ -602,8 +613,14 @@ __device__ __forceinline__ int2 xcd_tile() {
 // decouples the loads from the MFMAs (no register cost for the prefetch).
 // The digit planes are shared by the 4 waves.
 //
-// Per stage and wave: B 3 loads (1 KB each: 12 per workgroup), A 4 (Q4) or
-// 8 (Q8, Q6) loads.  One barrier per stage: at its top every wave has waited
+// Both operands are read from HBM images in this load order (the digitizer's
+// tile layout, digit_off; the weight image, k_tile_weight), so each direct
+// load reads 64 lanes × 16 (or 12) consecutive bytes.  From the row-major
+// weights and [pl][n][K] planes a load touched 16 rows × 64 B, half of each
+// 128-byte line, and the loads took 2.5× as long.
+//
+// Per stage and wave: B 3 loads (1 KB each: 12 per workgroup), A NMAT·RB
+// (Q4) or 2·NMAT·RB (Q8, Q6) loads.  One barrier per stage: at its top every wave has waited
 // for its own loads of this stage, and every wave has finished the previous
 // stage, whose slot is then refilled NST−1 stages ahead.
 // ---------------------------------------------------------------------------
@@ -614,13 +631,39 @@ struct ALds {
     static constexpr int chunks = QT == QT_Q4 ? 1 : 2;       // loads per (matrix, row block) and stage
     static constexpr int bytes = QT == QT_Q6 ? 12 : 16;      // bytes per lane and load
     static constexpr int lane_words = QT == QT_Q4 ? 4 : (QT == QT_Q8 ? 8 : 6);
+    static constexpr int stage_row = QT == QT_Q4 ? 64 : (QT == QT_Q8 ? 128 : 96);  // row bytes per stage
+    static constexpr int block_stage = chunks * 64 * bytes;  // image bytes per 16-row block and stage (16·stage_row)
 };
+
+// Weight image of the prefill GEMM: for 16-row block rb, stage u, load c and
+// lane lr + 16·lg, the `bytes` that row 16rb + lr holds at stage_row·u +
+// lg·stage_row/4 + c·bytes, stored at (((rb·nst + u)·chunks + c)·64 + lane)·
+// bytes.  A permutation of the row-major bytes (rows a multiple of 16, K of
+// 128); one thread per lane-load.
+template <int QT>
+static __global__ void __launch_bounds__(kThreads) k_tile_weight(const uint8_t *src, int row_bytes, int rows, int nst,
+                                                                 uint8_t *dst) {
+    using A = ALds<QT>;
+    const size_t i = (size_t)blockIdx.x * kThreads + threadIdx.x;
+    const size_t total = (size_t)(rows / 16) * nst * A::chunks * 64;
+    if (i >= total) return;
+    const int lane = (int)(i % 64);
+    const size_t t = i / 64;
+    const int c = (int)(t % A::chunks);
+    const int u = (int)((t / A::chunks) % nst);
+    const size_t rb = t / A::chunks / nst;
+    const uint32_t *sp = reinterpret_cast<const uint32_t *>(
+        src + (16 * rb + (lane & 15)) * (size_t)row_bytes + A::stage_row * u + (lane >> 4) * (A::stage_row / 4) + c * A::bytes);
+    uint32_t *dp = reinterpret_cast<uint32_t *>(dst + i * A::bytes);
+#pragma unroll
+    for (int w = 0; w < A::bytes / 4; ++w) dp[w] = sp[w];
+}
 // the direct load places lane i's bytes at 16·i for 12- and 16-byte loads alike
 constexpr int kLdsLaneStride = 16;
 
-template <int QT, int NMAT, int NST>
+template <int QT, int NMAT, int NST, int RB_>
 struct GemmLdsLayout {
-    static constexpr int RB = 4 / NMAT;
+    static constexpr int RB = RB_;
     static constexpr int b_bytes = 2 * 3 * 2 * 64 * 16;                                       // [s][pl][tb][lane]
     static constexpr int a_wave = NMAT * RB * ALds<QT>::chunks * 64 * kLdsLaneStride;        // [mi][rb][c][lane]
     static constexpr int stage = b_bytes + kWaves * a_wave;
@@ -656,11 +699,11 @@ __device__ __forceinline__ void lds_barrier() {
     asm volatile("s_barrier" ::: "memory");
 }
 
-template <int QT, int NMAT, int NST>
+template <int QT, int NMAT, int NST, int RB>
 static __global__ void __launch_bounds__(kThreads) k_gemm_lds(GemmParams p, int epi) {
     static_assert(NST == 2 || NST == 3, "the main loop is unrolled over two or three slots");
-    using Lay = GemmLdsLayout<QT, NMAT, NST>;
-    constexpr int RB = Lay::RB;
+    static_assert(NMAT * RB <= 4, "at most four row blocks per wave");
+    using Lay = GemmLdsLayout<QT, NMAT, NST, RB>;
     constexpr int WR = 16 * RB;                 // rows per matrix and wave
     constexpr int TB = 2;
     constexpr int CH = ALds<QT>::chunks, AB = ALds<QT>::bytes;
@@ -679,37 +722,35 @@ static __global__ void __launch_bounds__(kThreads) k_gemm_lds(GemmParams p, int 
     const int nst = p.K / kStageCols;
 
     const GemmSeg sg = gemm_seg<NMAT>(p, rc);
-    const int row_bytes = p.m[0].row_bytes;
-    constexpr int stage_row = QT == QT_Q4 ? 64 : (QT == QT_Q8 ? 128 : 96);  // row bytes per stage
-    // this lane's A source: row rc+16rb+lr, bytes lg·(stage_row/4) + c·AB of the stage slice
+    constexpr int BS = ALds<QT>::block_stage;
+    // this lane's A source in the weight image: 16-row block (rc − start)/16 + rb, stage 0, load 0
     const uint8_t *asrc[NMAT][RB];
 #pragma unroll
     for (int mi = 0; mi < NMAT; ++mi)
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb)
-            asrc[mi][rb] = sg.base[mi] + (size_t)(rc + 16 * rb + lr - sg.start) * row_bytes + lg * (stage_row / 4);
-    // this wave's 3 B loads: chunk j = 3·wave + i → (s, pl, tb); lane: token 16tb+lr, columns 32lg + 16s
+            asrc[mi][rb] = sg.tiled[mi] + (size_t)((rc - sg.start) / 16 + rb) * nst * BS + lane * AB;
+    // this wave's 3 B loads: chunks j = 3·wave + i of the token tile's stages (digit_off)
     const int8_t *bsrc[3];
     int boff[3];
 #pragma unroll
     for (int i = 0; i < 3; ++i) {
         const int j = 3 * wave + i;
-        const int tb = j % 2, pl = (j / 2) % 3, s = j / 6;
-        bsrc[i] = p.xd + pl * p.plane_stride + (size_t)(n0 + 16 * tb + lr) * p.K + 32 * lg + 16 * s;
+        bsrc[i] = p.xd + ((size_t)tile.y * nst * 12 + j) * 1024 + lane * 16;
         boff[i] = j * 1024;
     }
     const int aoff = Lay::b_bytes + wave * Lay::a_wave;
 
     auto issue = [&](int u, uint8_t *st) {
 #pragma unroll
-        for (int i = 0; i < 3; ++i) lds_load<16>(bsrc[i] + kStageCols * u, st + boff[i]);
+        for (int i = 0; i < 3; ++i) lds_load<16>(bsrc[i] + (size_t)12 * 1024 * u, st + boff[i]);
 #pragma unroll
         for (int mi = 0; mi < NMAT; ++mi)
 #pragma unroll
             for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
                 for (int c = 0; c < CH; ++c)
-                    lds_load<AB>(asrc[mi][rb] + stage_row * u + c * AB,
+                    lds_load<AB>(asrc[mi][rb] + (size_t)BS * u + c * 64 * AB,
                                  st + aoff + ((mi * RB + rb) * CH + c) * 64 * kLdsLaneStride);
     };
 

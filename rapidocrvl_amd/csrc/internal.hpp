@@ -88,6 +88,7 @@ struct pocr_weight {
     void *base = nullptr;
     const float *scale = nullptr;
     const uint8_t *data = nullptr;
+    uint8_t *tiled = nullptr;  // the prefill GEMM's copy in its load order, when weight_tiles_ok
 };
 
 struct LayerW {
@@ -206,6 +207,12 @@ struct DigitizeParams;
 struct GemmParams;
 int digitize_rows(hipStream_t s, int qtype, const DigitizeParams &p, int n);
 int gemm_rows(hipStream_t s, int qtype, int nmat, const GemmParams &p, int epi, int npad);
+// gemm_rows over K columns reads digit planes in the tile layout
+// (DigitizeParams::tiled) and the weights' tile images
+bool gemm_tiled(int K);
+// weights of this shape get a tile image at upload (k_tile_weight)
+bool weight_tiles_ok(int rows, int cols);
+int tile_weight(hipStream_t s, int qtype, const uint8_t *src, int row_bytes, int rows, int cols, uint8_t *dst);
 // the small MFMA GEMM over at most 16 rows (digit planes of 16 rows)
 bool gemm_small_ok(int rows, int K);
 int gemm_small_rows(hipStream_t s, int qtype, int nmat, const GemmParams &p, int epi);

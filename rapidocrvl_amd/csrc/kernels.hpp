@@ -27,6 +27,7 @@ constexpr int kMaxCols = 4096; // widest input of the streaming GEMV kernel
 struct DevMat {
     const float *scale;    // [rows]
     const uint8_t *data;   // rows * row_bytes, 256-byte aligned base
+    const uint8_t *tiled;  // the same bytes in the prefill GEMM's operand order (weight_tile_off), or null
     int rows;
     int cols;
     int row_bytes;

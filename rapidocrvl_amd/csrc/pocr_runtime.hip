@@ -186,6 +186,21 @@ extern "C" int pocr_weight_upload(pocr_ctx *ctx, int qtype, int rows, int cols, 
         (void)hipFree(base);
         return fail(POCR_ERR_DEVICE, "weight upload copy: %s", hipGetErrorString(e));
     }
+    // the prefill GEMM's image of the same bytes (k_tile_weight)
+    uint8_t *tiled = nullptr;
+    if (weight_tiles_ok(rows, cols)) {
+        e = hipMalloc(&tiled, data_bytes);
+        int rc = e == hipSuccess ? POCR_OK : fail(POCR_ERR_DEVICE, "weight tile image: %s", hipGetErrorString(e));
+        if (rc == POCR_OK)
+            rc = tile_weight(ctx->stream, qtype, (const uint8_t *)base + scale_bytes, (int)rb, rows, cols, tiled);
+        if (rc == POCR_OK && (e = hipStreamSynchronize(ctx->stream)) != hipSuccess)
+            rc = fail(POCR_ERR_DEVICE, "weight tile image: %s", hipGetErrorString(e));
+        if (rc != POCR_OK) {
+            if (tiled) (void)hipFree(tiled);
+            (void)hipFree(base);
+            return rc;
+        }
+    }
     pocr_weight *w = new pocr_weight();
     ctx->refs.fetch_add(1);
     w->ctx = ctx;
@@ -196,6 +211,7 @@ extern "C" int pocr_weight_upload(pocr_ctx *ctx, int qtype, int rows, int cols, 
     w->base = base;
     w->scale = (const float *)base;
     w->data = (const uint8_t *)base + scale_bytes;
+    w->tiled = tiled;
     *out = w;
     return POCR_OK;
 }
@@ -213,6 +229,7 @@ void pocr::weight_release(const pocr_weight *cw) {
         (void)hipSetDevice(ctx->device);
         (void)hipStreamSynchronize(ctx->stream);
         free_dev(w->base);
+        free_dev(w->tiled);
     }
     delete w;
     ctx_release(ctx);
@@ -224,6 +241,7 @@ DevMat pocr::dev_mat(const pocr_weight *w) {
     DevMat m;
     m.scale = w->scale;
     m.data = w->data;
+    m.tiled = w->tiled;
     m.rows = w->rows;
     m.cols = w->cols;
     m.row_bytes = (int)w->row_bytes;

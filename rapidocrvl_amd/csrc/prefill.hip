@@ -83,33 +83,67 @@ int launch_gemm_small_t(hipStream_t s, int qtype, const GemmParams &p, int epi) 
 
 bool small_shape_ok(int rows, int K) { return rows % 16 == 0 && K % (kGemmK * kWaves) == 0 && K <= kMaxCols; }
 
-template <int NMAT>
-int launch_gemm_lds_t(hipStream_t s, int qtype, const GemmParams &p, int epi, int npad) {
-    const dim3 grid((p.rows + kGemmRows / NMAT - 1) / (kGemmRows / NMAT), npad / 32);
+// One, two or four 16-row blocks per wave (64, 128 or 256 rows of each matrix
+// per workgroup), two-slot ring.  These kernels are latency-bound: the more
+// workgroups share a CU, the better their loads and barriers overlap, so the
+// row tile shrinks until the grid holds about three workgroups per CU.
+// Measured on the MI355X at 1,345 tokens (Q4, µs; 256 / 128 / 64-row tiles):
+// QKV 2560×1024 15.3 / 14.1 / 15.2; o_proj 1024×2048 16.5 / 13.5 / 12.3;
+// down 1024×3072 22.0 / 18.5 / 16.4; gate/up 2×3072×1024 – / 28.0 / 23.0.
+template <int NMAT, int RB>
+int launch_gemm_lds_rb(hipStream_t s, int qtype, const GemmParams &p, int epi, int npad) {
+    const dim3 grid((p.rows + 64 * RB - 1) / (64 * RB), npad / 32);
     switch (qtype) {
-    case QT_Q8: hipLaunchKernelGGL((k_gemm_lds<QT_Q8, NMAT, 3>), grid, dim3(kThreads), 0, s, p, epi); break;
-    // Q4 gate/up: a two-slot ring (56 KB of LDS) fits two workgroups per CU,
-    // which pays for its shallower prefetch; the single-matrix products keep
-    // three slots
-    case QT_Q4:
-        hipLaunchKernelGGL((k_gemm_lds<QT_Q4, NMAT, NMAT == 2 ? 2 : 3>), grid, dim3(kThreads), 0, s, p, epi);
-        break;
-    case QT_Q6: hipLaunchKernelGGL((k_gemm_lds<QT_Q6, NMAT, 3>), grid, dim3(kThreads), 0, s, p, epi); break;
+    case QT_Q8: hipLaunchKernelGGL((k_gemm_lds<QT_Q8, NMAT, 2, RB>), grid, dim3(kThreads), 0, s, p, epi); break;
+    case QT_Q4: hipLaunchKernelGGL((k_gemm_lds<QT_Q4, NMAT, 2, RB>), grid, dim3(kThreads), 0, s, p, epi); break;
+    case QT_Q6: hipLaunchKernelGGL((k_gemm_lds<QT_Q6, NMAT, 2, RB>), grid, dim3(kThreads), 0, s, p, epi); break;
     default: return fail(POCR_ERR_UNSUPPORTED, "gemm: qtype %d", qtype);
     }
     HIP_TRY(hipGetLastError());
     return POCR_OK;
 }
 
-// the LDS-ring kernel takes K in whole 128-column stages
-bool lds_gemm_ok(int K) {
+constexpr int kGemmTargetGroups = 768;  // about three workgroups per CU
+
+template <int NMAT>
+int launch_gemm_lds_t(hipStream_t s, int qtype, const GemmParams &p, int epi, int npad) {
+    if (NMAT == 1 && p.rows % 128 == 0 && (p.rows / 128) * (npad / 32) >= kGemmTargetGroups)
+        return launch_gemm_lds_rb<1, 2>(s, qtype, p, epi, npad);
+    return launch_gemm_lds_rb<NMAT, 1>(s, qtype, p, epi, npad);
+}
+
+}  // namespace
+
+// the LDS-ring kernel takes K in whole 128-column stages; its digit planes
+// are written in the tile layout
+bool pocr::gemm_tiled(int K) {
     const char *env = getenv("POCR_PREFILL_GEMM");
     return K % kStageCols == 0 && !(env && env[0] == 'd');
 }
 
+bool pocr::weight_tiles_ok(int rows, int cols) { return rows % 16 == 0 && cols % kStageCols == 0; }
+
+int pocr::tile_weight(hipStream_t s, int qtype, const uint8_t *src, int row_bytes, int rows, int cols, uint8_t *dst) {
+    const int nst = cols / kStageCols;
+    const size_t loads = (size_t)(rows / 16) * nst * 64 * (qtype == QT_Q4 ? 1 : 2);
+    const dim3 grid((unsigned)((loads + kThreads - 1) / kThreads));
+    switch (qtype) {
+    case QT_Q8: hipLaunchKernelGGL(k_tile_weight<QT_Q8>, grid, dim3(kThreads), 0, s, src, row_bytes, rows, nst, dst); break;
+    case QT_Q4: hipLaunchKernelGGL(k_tile_weight<QT_Q4>, grid, dim3(kThreads), 0, s, src, row_bytes, rows, nst, dst); break;
+    case QT_Q6: hipLaunchKernelGGL(k_tile_weight<QT_Q6>, grid, dim3(kThreads), 0, s, src, row_bytes, rows, nst, dst); break;
+    default: return fail(POCR_ERR_UNSUPPORTED, "tile_weight: qtype %d", qtype);
+    }
+    HIP_TRY(hipGetLastError());
+    return POCR_OK;
+}
+
+namespace {
+
 // npad: token rows of the digit planes, a multiple of 32
 int launch_gemm(hipStream_t s, int qtype, int nmat, const GemmParams &p, int epi, int npad) {
-    if (lds_gemm_ok(p.K)) {
+    if (gemm_tiled(p.K)) {
+        for (int i = 0; i < (nmat == 2 ? 2 : 3); ++i)
+            if (!p.m[i].tiled) return fail(POCR_ERR_UNSUPPORTED, "gemm: %dx%d weight has no tile image", p.m[i].rows, p.K);
         if (nmat == 2) return launch_gemm_lds_t<2>(s, qtype, p, epi, npad);
         return launch_gemm_lds_t<1>(s, qtype, p, epi, npad);
     }
@@ -223,6 +257,7 @@ int batched_gemv(pocr_ctx *ctx, const DevMat &w, const float *x, int m, float *o
     d.plane_stride = (size_t)npad * w.cols;
     d.xs = ctx->gxs.as<float>();
     d.xb = ctx->gxb.as<int>();
+    d.tiled = !small && gemm_tiled(w.cols);
     RC(launch_digitize(s, w.qtype, d, m));
     GemmParams p{};
     p.m[0] = p.m[1] = p.m[2] = w;
@@ -335,6 +370,7 @@ int prefill_run(pocr_seq *s, int n, const int32_t *pos3, float *logits, int32_t 
         d.plane_stride = (size_t)npad * K;
         d.xs = b.xs;
         d.xb = b.xb;
+        d.tiled = gemm_tiled(K);
         return launch_digitize(st, qt, d, n);
     };
     auto gemm_in = [&](GemmParams &p) {

@@ -151,6 +151,7 @@ int digitize(const pocr_projector *p, const float *x, int n, int npad) {
     d.plane_stride = (size_t)npad * d.K;
     d.xs = p->xs;
     d.xb = p->xb;
+    d.tiled = gemm_tiled(d.K);
     return digitize_rows(p->ctx->stream, QT_Q8, d, n);
 }
 
