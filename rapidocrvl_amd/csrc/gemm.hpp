@@ -1016,7 +1016,7 @@ static __global__ void __launch_bounds__(kThreads) k_rope_append(float *qkv, int
 // Pᵀ feeds the second product straight from the first one's accumulators: MFMA
 // step element e of lane group lg is key 4lg+e (e < 4) or 16+4lg+(e−4), the
 // rows that lane already holds, and Vᵀ is read in the same key order.
-// Online softmax per token (max, Σexp) with FastExp; token n attends cache
+// Online softmax per token (max, Σexp) with exp_hw; token n attends cache
 // rows [0, clen0+n]; scores dot·f32(1/√128) (model.go:4623-4795, 7391).
 // ---------------------------------------------------------------------------
 typedef float v4f __attribute__((ext_vector_type(4)));
@@ -1026,6 +1026,14 @@ constexpr int kPfTok = 16;                  // query tokens per tile
 constexpr int kPfKeys = 32;                 // keys per block
 constexpr int kPfKPlane = kPfKeys * kHD;    // bf16 per K plane of a block image
 constexpr int kPfImage = 4 * kPfKPlane * 2; // bytes per block image (K and Vᵀ, hi and lo): 32 KB
+
+// e^x from the hardware base-2 exponential (v_exp_f32, about 1 ulp), for the
+// prefill attention's weights, rescales and parity merge: the weights enter
+// split-bf16 products (2^-16 relative), so FastExpF32's own ~1e-7 departure
+// from e^x is far below what the products keep, and the hardware form costs
+// 3 VALU issues against about 20 for the restated polynomial, which made this
+// kernel VALU-bound (57.1 → 50.3 µs per layer at 1,345 tokens)
+__device__ __forceinline__ float exp_hw(float x) { return __builtin_amdgcn_exp2f(x * 1.4426950408889634f); }
 
 __device__ __forceinline__ void split_bf16(float x, __bf16 &hi, __bf16 &lo) {
     hi = (__bf16)x;
@@ -1208,7 +1216,7 @@ static __global__ void __launch_bounds__(kPfThreads) k_attn_prefill(const float 
             v8bf ph, pl;
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                const float ex = fast_exp_ref(sv[e] - mx);
+                const float ex = exp_hw(sv[e] - mx);
                 const float p = vis[e] ? ex : 0.0f;
                 ps += p;
                 __bf16 a, c;
@@ -1217,10 +1225,10 @@ static __global__ void __launch_bounds__(kPfThreads) k_attn_prefill(const float 
                 pl[e] = c;
             }
             ps = groups4_sum(ps);
-            // rescale only when a column's maximum moved (FastExp(0) is exactly
+            // rescale only when a column's maximum moved (exp_hw(0) is exactly
             // 1, so skipping is exact)
             if (__builtin_amdgcn_ballot_w64(mb != m)) {
-                const float fe = fast_exp_ref(m - mx);
+                const float fe = exp_hw(m - mx);
                 const float f = m == -INFINITY ? 0.0f : fe;
                 lsum *= f;
 #pragma unroll
@@ -1275,8 +1283,8 @@ static __global__ void __launch_bounds__(kPfThreads) k_attn_prefill(const float 
         if (par == 0 && wave_on && q0 + lr < ntok) {
             const float m1 = mrg[0], l1 = mrg[1];
             const float M = fmaxf(m, m1);  // finite: key 0 is in block 0
-            const float f0 = m == -INFINITY ? 0.0f : fast_exp_ref(m - M);
-            const float f1 = m1 == -INFINITY ? 0.0f : fast_exp_ref(m1 - M);
+            const float f0 = m == -INFINITY ? 0.0f : exp_hw(m - M);
+            const float f1 = m1 == -INFINITY ? 0.0f : exp_hw(m1 - M);
             const float inv = 1.0f / (lsum * f0 + l1 * f1);
             float *dst = out + (size_t)(q0 + lr) * out_stride + (size_t)hh * kHD + 4 * lg;
 #pragma unroll

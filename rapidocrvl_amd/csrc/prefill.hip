@@ -46,11 +46,12 @@ int launch_digitize_w(hipStream_t s, int qtype, const DigitizeParams &p, int n) 
 int launch_digitize(hipStream_t s, int qtype, const DigitizeParams &p, int n) {
     if (p.K % 16 || p.K > 2 * 16 * kThreads) return fail(POCR_ERR_UNSUPPORTED, "digitize: K %d", p.K);
     if (p.K > 16 * kThreads) return launch_digitize_g<2>(s, qtype, p, n);
-    // up to 2048 columns: one wave per token, the same bytes (1345 tokens of
-    // 1024 / 2048 columns: 6.3 / 6.9 µs against 7.7; at 3072 columns the
-    // wave's three serial slices make it slower, 9.3 µs)
+    // up to 3072 columns: one wave per token, the same bytes (1345 tokens of
+    // 1024 / 2048 / 3072 columns, planes in the tile layout: 6.9 / 7.6 / 10.2
+    // µs; a workgroup per token with three barriers took 14 µs at 3072)
     if (p.K <= 1024) return launch_digitize_w<1>(s, qtype, p, n);
     if (p.K <= 2048) return launch_digitize_w<2>(s, qtype, p, n);
+    if (p.K <= 3072) return launch_digitize_w<3>(s, qtype, p, n);
     return launch_digitize_g<1>(s, qtype, p, n);
 }
 
