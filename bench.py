@@ -458,17 +458,25 @@ def roofline_only(args):
                       "frac_of_stream_read": round(stream_us / us, 4)}), flush=True)
 
 
-def vnni_decode(ctx, cfg, weights, seq, first_tok, first_pos, n_prefix, n_tokens, steps):
+def vnni_decode(ctx, cfg, weights, seq, first_tok, first_pos, n_prefix, n_tokens, steps, prompt=None):
     """The same Q4 greedy decode in the reference's VNNI activation mode
     (pocr_model_set_vnni: u8 activations for every Q4 matvec, the
     reference's VNNI matvec arithmetic, with the portable scalar orders
     around it), from the same
-    1345-row KV state, on its own copy of the weights."""
+    1345-row KV state, on its own copy of the weights.  With prompt = (ids,
+    image rows), the same prompt's prefill in that mode is timed too (the
+    mode's batched prefill, bit-identical to its token steps)."""
     from rapidocrvl_amd import lib
 
     m = lib.Model(ctx, cfg)
     m.load_weights(weights)
     m.set_vnni(True)
+    extra = {}
+    if prompt is not None:
+        sp = m.seq(n_prefix + 8)
+        tok, t_pf = prefill(sp, prompt[0], prompt[1], reps=3)
+        sp.close()
+        extra = {"prefill_ms": round(t_pf * 1e3, 3), "prefill_first_token": tok}
     s = m.seq(n_prefix + n_tokens + 8)
     rows = n_prefix * cfg.kv_heads * cfg.head_dim
     for li in range(cfg.layers):
@@ -479,7 +487,7 @@ def vnni_decode(ctx, cfg, weights, seq, first_tok, first_pos, n_prefix, n_tokens
     m.close()
     computed = n_tokens - 1
     return {"value": round(computed * steps / dt, 1), "unit": "tok/s",
-            "us_per_token": round(dt / steps / computed * 1e6, 1)}, [int(t) for t in toks]
+            "us_per_token": round(dt / steps / computed * 1e6, 1), **extra}, [int(t) for t in toks]
 
 
 def cpu_baseline(cfg, weights, gpu_seq, first_tok, first_pos, gpu_tokens, n_prefix, budget_s=12.0,
@@ -786,7 +794,7 @@ def main():
         return
     if args.vnni_only:
         vd, _ = vnni_decode(ctx, cfg, weights, seq, first_tok, first_pos, n_prefix, args.decode_tokens,
-                            max(1, args.steps // 2))
+                            max(1, args.steps // 2), prompt=(ids, img))
         print(json.dumps({"workload": f"q4 greedy decode in the VNNI activation mode, {args.decode_tokens - 1} token "
                                       f"steps after a {n_prefix}-token prefill", **vd}), flush=True)
         return
@@ -824,7 +832,7 @@ def main():
 
     extra = {}
     extra["vnni_decode"], vnni_toks = vnni_decode(ctx, cfg, weights, seq, first_tok, first_pos, n_prefix,
-                                                  args.decode_tokens, max(1, args.steps // 2))
+                                                  args.decode_tokens, max(1, args.steps // 2), prompt=(ids, img))
     log(f"[bench] q4 decode in the VNNI activation mode {extra['vnni_decode']}")
     cpu = None
     if not args.no_cpu:

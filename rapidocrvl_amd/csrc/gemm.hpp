@@ -40,21 +40,24 @@ struct DigitizeParams {
     int8_t *xd;            // planes [3][npad][K], or the tile layout below
     size_t plane_stride;   // npad·K
     float *xs;             // [n] row scale
-    int *xb;               // [n][4] Σd per plane (4th unused)
+    int *xb;               // [n][4] Σd per plane (4th unused); VNNI: [n][4] with Σq first
     int tiled;             // 1: the prefill GEMM's tile layout (K a multiple of 128)
+    int vnni;              // 1: one plane of VNNI activation bytes (k_digitize_vnni, tile layout only)
 };
 
 // Byte offset of the 16-column group at column c0 (a multiple of 16) of token
 // n, digit plane pl.  Plane layout: [pl][npad][K].  Tile layout (the operand
-// order of k_gemm_lds, so each of its loads reads 1 KB of consecutive bytes):
+// order of k_gemm_lds, so each of its loads reads 1 KB of consecutive bytes),
+// with NPL planes (3, or 1 in the VNNI mode):
 // [token tile n/32][stage c0/128][chunk j][lane][16 B], where in stage u the
-// MFMA step s, plane pl and token block tb form chunk j = (3s + pl)·2 + tb and
-// lane lr + 16·lg holds token 16tb + lr, columns 128u + 32lg + 16s .. +15.
+// MFMA step s, plane pl and token block tb form chunk j = (NPL·s + pl)·2 + tb
+// and lane lr + 16·lg holds token 16tb + lr, columns 128u + 32lg + 16s .. +15.
 __device__ __forceinline__ size_t digit_off(const DigitizeParams &p, int pl, int n, int c0) {
     if (!p.tiled) return pl * p.plane_stride + (size_t)n * p.K + c0;
+    const int npl = p.vnni ? 1 : 3;
     const int g = c0 >> 4, u = g >> 3, gi = g & 7;
-    const int tl = n & 31, j = ((gi & 1) * 3 + pl) * 2 + (tl >> 4), lane = (tl & 15) + 16 * (gi >> 1);
-    return ((size_t)((n >> 5) * (p.K >> 7) + u) * 12 + j) * 1024 + lane * 16;
+    const int tl = n & 31, j = ((gi & 1) * npl + pl) * 2 + (tl >> 4), lane = (tl & 15) + 16 * (gi >> 1);
+    return ((size_t)((n >> 5) * (p.K >> 7) + u) * 4 * npl + j) * 1024 + lane * 16;
 }
 
 template <int QT, int G>
@@ -287,6 +290,145 @@ static __global__ void __launch_bounds__(kThreads) k_digitize_w(DigitizeParams p
     if (lane == 0) p.xs[n] = S * factor;
 }
 
+// The VNNI mode's activation bytes (quantizeXForVNNI, internal/tensor/
+// quant.go:2087-2115; dot_amd64.go:228-252), one wave per token, as the VNNI
+// GEMV's prologue forms them for one vector, so each token's bytes are the
+// token step's:
+// * with norm_w, RMSNorm first: Σx² in sumSquaresScalar's order (ops.go:
+//   1039-1058; K a multiple of 8: eight running sums over the columns ≡ j mod
+//   8, lanes 0-7, then ((s0+s1)+(s2+s3))+((s4+s5)+(s6+s7))), factor =
+//   fastRsqrt(Σ/K + eps), y = (x·factor)·w;
+// * m = max|y|, sx = m/127 (1 for m = 0), inv = 1/sx, q = clamp(RNE(y·inv) +
+//   128, 0, 255), every q = 128 for m = 0.
+// The tile layout's one plane holds d = q − 128 (the GEMM's B operand) in the
+// weight codes' order; xs = sx, xb[0] = Σq.
+template <int QT, int J>
+static __global__ void __launch_bounds__(kThreads) k_digitize_vnni(DigitizeParams p, int ntok) {
+#pragma clang fp contract(off)
+    static_assert(J >= 1 && J <= 4, "1024-column slices, K ≤ 1024·J ≤ 4096");
+    const int lane = threadIdx.x & 63;
+    const int n = blockIdx.x * kWaves + (threadIdx.x >> 6);
+    if (n >= ntok) return;  // wave-uniform; no barrier below
+    const float *xr = p.x + (size_t)n * p.x_stride;
+    float y[J][16];
+    bool valid[J];
+    int c0[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        c0[j] = 16 * (64 * j + lane);
+        valid[j] = c0[j] < p.K;
+        const int cl = valid[j] ? c0[j] : p.K - 16;  // clamped, never written
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float4 v = reinterpret_cast<const float4 *>(xr + cl)[i];
+            y[j][4 * i] = v.x;
+            y[j][4 * i + 1] = v.y;
+            y[j][4 * i + 2] = v.z;
+            y[j][4 * i + 3] = v.w;
+        }
+    }
+    if (p.norm_w) {
+        float s = 0.0f;
+        if (lane < 8) {  // running sum `lane`: columns lane, lane + 8, … in order, 16 reads in flight
+            int i = lane;
+            for (; i + 8 * 15 < p.K; i += 8 * 16) {
+                float v[16];
+#pragma unroll
+                for (int k = 0; k < 16; ++k) v[k] = xr[i + 8 * k];
+#pragma unroll
+                for (int k = 0; k < 16; ++k) s = s + v[k] * v[k];
+            }
+            for (; i < p.K; i += 8) s = s + xr[i] * xr[i];
+        }
+        float r[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) r[k] = __shfl(s, k, 64);
+        const float ss = ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));
+        const float factor = fast_rsqrt_ref(ss / (float)p.K + p.eps);
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            const int cl = valid[j] ? c0[j] : p.K - 16;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float4 w = reinterpret_cast<const float4 *>(p.norm_w + cl)[i];
+                y[j][4 * i] = y[j][4 * i] * factor * w.x;
+                y[j][4 * i + 1] = y[j][4 * i + 1] * factor * w.y;
+                y[j][4 * i + 2] = y[j][4 * i + 2] * factor * w.z;
+                y[j][4 * i + 3] = y[j][4 * i + 3] * factor * w.w;
+            }
+        }
+    }
+    float m = 0.0f;
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) m = valid[j] ? fmaxf(m, fabsf(y[j][i])) : m;
+    m = wave_max(m);
+    const float sx = m == 0.0f ? 1.0f : m / 127.0f;
+    const float inv = 1.0f / sx;
+    int sq = 0;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        int d[16];
+        int sg = 0;
+#pragma unroll
+        for (int c = 0; c < 16; ++c) {
+            int q = 128;
+            if (m != 0.0f) {
+                float v = rintf(y[j][c] * inv) + 128.0f;
+                v = fminf(fmaxf(v, 0.0f), 255.0f);
+                q = (int)v;
+            }
+            d[digit_pos16<QT>(c)] = q - 128;
+            sg += q;
+        }
+        if (valid[j]) {
+            *reinterpret_cast<int4 *>(p.xd + digit_off(p, 0, n, c0[j])) =
+                make_int4(pack4(d[0], d[1], d[2], d[3]), pack4(d[4], d[5], d[6], d[7]),
+                          pack4(d[8], d[9], d[10], d[11]), pack4(d[12], d[13], d[14], d[15]));
+            sq += sg;
+        }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) sq += __shfl_xor(sq, off, 64);
+    if (lane == 0) {
+        p.xb[n * 4] = sq;
+        p.xs[n] = sx;
+    }
+}
+
+// Σ of the stored codes of each row (Q4 nibbles, Q6 fields; cols a multiple of
+// 16), one wave per row: the VNNI mode's row sum is Σu − IBIAS·cols.
+template <int QT>
+static __global__ void __launch_bounds__(kThreads) k_row_usum(const uint8_t *data, int row_bytes, int rows, int cols,
+                                                              int *out) {
+    const int lane = threadIdx.x & 63;
+    const int r = blockIdx.x * kWaves + (threadIdx.x >> 6);
+    if (r >= rows) return;
+    const uint8_t *row = data + (size_t)r * row_bytes;
+    int u = 0;
+    if constexpr (QT == QT_Q4) {
+        for (int b = 4 * lane; b < cols / 2; b += 4 * 64) {
+            const uint32_t w = *reinterpret_cast<const uint32_t *>(row + b);
+            u += (int)((w & 15u) + ((w >> 4) & 15u) + ((w >> 8) & 15u) + ((w >> 12) & 15u) +
+                                                ((w >> 16) & 15u) + ((w >> 20) & 15u) + ((w >> 24) & 15u) + (w >> 28));
+        }
+    } else {
+        for (int c = lane; c < cols / 16; c += 64) {
+            const uint32_t *q = reinterpret_cast<const uint32_t *>(row + 12 * (size_t)c);
+            const uint32_t w0 = q[0], w1 = q[1], w2 = q[2];
+            const uint32_t g[4] = {w0 & 0xFFFFFFu, (w0 >> 24) | ((w1 & 0xFFFFu) << 8), (w1 >> 16) | ((w2 & 0xFFu) << 16),
+                                   w2 >> 8};
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                u += (int)((g[k] & 63u) + ((g[k] >> 6) & 63u) + ((g[k] >> 12) & 63u) + (g[k] >> 18));
+        }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) u += __shfl_xor(u, off, 64);
+    if (lane == 0) out[r] = u;
+}
+
 // ---------------------------------------------------------------------------
 // MFMA GEMM: Y[n][r] = epilogue(scale[r]·xs[n]·(D0 + D1/2^7 + D2/2^14)),
 // D_p = Σ_k u[r][k]·d_p[n][k] − IBIAS·Σ_k d_p[n][k].  Workgroup: 256 rows ×
@@ -315,6 +457,7 @@ struct GemmParams {
     StepState *const *rst; // [n] step state of row n (batched decode: rows are sequences), or null
     int last;              // DOWN: last layer → vbuf = h + y (h untouched)
     const float *bias;     // BIAS / BIAS_GELU: [rows]
+    int vnni;              // one plane of VNNI bytes (xs = scaleX, xb[0] = Σq): the VNNI finalize
 };
 
 // 16 weight codes of row `row` at columns k..k+15 (k multiple of 16) as the
@@ -423,12 +566,41 @@ __device__ __forceinline__ void gemm_store(const GemmParams &p, int epi, int n, 
     gemm_store_y<NMAT>(p, epi, n, rr, y);
 }
 
+// The VNNI mode's epilogue of rows rr..rr+3 for token n from the int32 Σu·d of
+// each row (u the stored code, d = q − 128), as the VNNI GEMV finishes a row
+// (finalizeDotQ8VNNI, dot_vnni_amd64.s:1043-1080; rows in whole 16-row blocks):
+//   dot = Σu·d + 128·Σu − IBIAS·Σq = Σ code·q,  rowSum = Σu − IBIAS·K,
+//   y = ((f32(dot) − f32(rowSum)·128)·scaleX)·scale[r].
+template <int QT, int NMAT>
+__device__ __forceinline__ void gemm_store_vnni(const GemmParams &p, int epi, int n, int rr,
+                                                const float *const (&scl)[2], const int *const (&us)[2],
+                                                const v4i (&a)[NMAT]) {
+#pragma clang fp contract(off)
+    constexpr int IB = DigitTraits<QT>::IBIAS;
+    const float sx = p.xs[n];
+    const int sq = p.xb[4 * n];
+    float y[NMAT][4];
+#pragma unroll
+    for (int mi = 0; mi < NMAT; ++mi) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int u = us[mi][i];
+            const int dot = a[mi][i] + 128 * u - IB * sq;
+            const int rowsum = u - IB * p.K;
+            const float v = (float)dot - (float)rowsum * 128.0f;
+            y[mi][i] = v * sx * scl[mi][i];
+        }
+    }
+    gemm_store_y<NMAT>(p, epi, n, rr, y);
+}
+
 // the wave's rows lie in one segment (segment ends are multiples of 16 rows
 // for the small kernel, of 64 for the prefill one)
 struct GemmSeg {
     const uint8_t *base[2];
     const uint8_t *tiled[2];
     const float *scale[2];
+    const int *usum[2];
     int start;
 };
 template <int NMAT>
@@ -437,15 +609,18 @@ __device__ __forceinline__ GemmSeg gemm_seg(const GemmParams &p, int r0) {
     g.base[1] = nullptr;
     g.tiled[1] = nullptr;
     g.scale[1] = nullptr;
+    g.usum[1] = nullptr;
     g.start = 0;
     const int i = NMAT == 2 ? 0 : (r0 >= p.seg_end[1] ? 2 : (r0 >= p.seg_end[0] ? 1 : 0));
     g.base[0] = p.m[i].data;
     g.tiled[0] = p.m[i].tiled;
     g.scale[0] = p.m[i].scale;
+    g.usum[0] = p.m[i].usum;
     if (NMAT == 2) {
         g.base[1] = p.m[1].data;
         g.tiled[1] = p.m[1].tiled;
         g.scale[1] = p.m[1].scale;
+        g.usum[1] = p.m[1].usum;
     } else if (i > 0) {
         g.start = p.seg_end[i - 1];
     }
@@ -661,10 +836,10 @@ static __global__ void __launch_bounds__(kThreads) k_tile_weight(const uint8_t *
 // the direct load places lane i's bytes at 16·i for 12- and 16-byte loads alike
 constexpr int kLdsLaneStride = 16;
 
-template <int QT, int NMAT, int NST, int RB_>
+template <int QT, int NMAT, int NST, int RB_, int NPL = 3>
 struct GemmLdsLayout {
     static constexpr int RB = RB_;
-    static constexpr int b_bytes = 2 * 3 * 2 * 64 * 16;                                       // [s][pl][tb][lane]
+    static constexpr int b_bytes = 2 * NPL * 2 * 64 * 16;                                     // [s][pl][tb][lane]
     static constexpr int a_wave = NMAT * RB * ALds<QT>::chunks * 64 * kLdsLaneStride;        // [mi][rb][c][lane]
     static constexpr int stage = b_bytes + kWaves * a_wave;
     static constexpr int total = NST * stage;
@@ -699,15 +874,16 @@ __device__ __forceinline__ void lds_barrier() {
     asm volatile("s_barrier" ::: "memory");
 }
 
-template <int QT, int NMAT, int NST, int RB>
+template <int QT, int NMAT, int NST, int RB, int NPL = 3>
 static __global__ void __launch_bounds__(kThreads) k_gemm_lds(GemmParams p, int epi) {
     static_assert(NST == 2 || NST == 3, "the main loop is unrolled over two or three slots");
     static_assert(NMAT * RB <= 4, "at most four row blocks per wave");
-    using Lay = GemmLdsLayout<QT, NMAT, NST, RB>;
+    static_assert(NPL == 3 || (NPL == 1 && QT != QT_Q8), "three digit planes, or one plane of VNNI bytes (Q4, Q6)");
+    using Lay = GemmLdsLayout<QT, NMAT, NST, RB, NPL>;
     constexpr int WR = 16 * RB;                 // rows per matrix and wave
     constexpr int TB = 2;
     constexpr int CH = ALds<QT>::chunks, AB = ALds<QT>::bytes;
-    constexpr int LPS = 3 + NMAT * RB * CH;     // loads per stage and wave
+    constexpr int LPS = NPL + NMAT * RB * CH;   // loads per stage and wave
     __shared__ __attribute__((aligned(16))) uint8_t slot0[Lay::stage];
     __shared__ __attribute__((aligned(16))) uint8_t slot1[Lay::stage];
     __shared__ __attribute__((aligned(16))) uint8_t slot2[NST == 3 ? Lay::stage : 16];
@@ -730,20 +906,20 @@ static __global__ void __launch_bounds__(kThreads) k_gemm_lds(GemmParams p, int 
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb)
             asrc[mi][rb] = sg.tiled[mi] + (size_t)((rc - sg.start) / 16 + rb) * nst * BS + lane * AB;
-    // this wave's 3 B loads: chunks j = 3·wave + i of the token tile's stages (digit_off)
-    const int8_t *bsrc[3];
-    int boff[3];
+    // this wave's NPL B loads: chunks j = NPL·wave + i of the token tile's stages (digit_off)
+    const int8_t *bsrc[NPL];
+    int boff[NPL];
 #pragma unroll
-    for (int i = 0; i < 3; ++i) {
-        const int j = 3 * wave + i;
-        bsrc[i] = p.xd + ((size_t)tile.y * nst * 12 + j) * 1024 + lane * 16;
+    for (int i = 0; i < NPL; ++i) {
+        const int j = NPL * wave + i;
+        bsrc[i] = p.xd + ((size_t)tile.y * nst * 4 * NPL + j) * 1024 + lane * 16;
         boff[i] = j * 1024;
     }
     const int aoff = Lay::b_bytes + wave * Lay::a_wave;
 
     auto issue = [&](int u, uint8_t *st) {
 #pragma unroll
-        for (int i = 0; i < 3; ++i) lds_load<16>(bsrc[i] + (size_t)12 * 1024 * u, st + boff[i]);
+        for (int i = 0; i < NPL; ++i) lds_load<16>(bsrc[i] + (size_t)4 * NPL * 1024 * u, st + boff[i]);
 #pragma unroll
         for (int mi = 0; mi < NMAT; ++mi)
 #pragma unroll
@@ -754,7 +930,7 @@ static __global__ void __launch_bounds__(kThreads) k_gemm_lds(GemmParams p, int 
                                  st + aoff + ((mi * RB + rb) * CH + c) * 64 * kLdsLaneStride);
     };
 
-    v4i acc[NMAT][RB][TB][3];
+    v4i acc[NMAT][RB][TB][NPL];
 #pragma unroll
     for (int mi = 0; mi < NMAT; ++mi)
 #pragma unroll
@@ -762,7 +938,7 @@ static __global__ void __launch_bounds__(kThreads) k_gemm_lds(GemmParams p, int 
 #pragma unroll
             for (int tb = 0; tb < TB; ++tb)
 #pragma unroll
-                for (int pl = 0; pl < 3; ++pl) acc[mi][rb][tb][pl] = v4i{0, 0, 0, 0};
+                for (int pl = 0; pl < NPL; ++pl) acc[mi][rb][tb][pl] = v4i{0, 0, 0, 0};
 
     auto compute = [&](const uint8_t *st) {
         const v4i *bl = reinterpret_cast<const v4i *>(st);
@@ -785,11 +961,11 @@ static __global__ void __launch_bounds__(kThreads) k_gemm_lds(GemmParams p, int 
                 }
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
-            v4i b[TB][3];
+            v4i b[TB][NPL];
 #pragma unroll
             for (int tb = 0; tb < TB; ++tb)
 #pragma unroll
-                for (int pl = 0; pl < 3; ++pl) b[tb][pl] = bl[((s * 3 + pl) * TB + tb) * 64 + lane];
+                for (int pl = 0; pl < NPL; ++pl) b[tb][pl] = bl[((s * NPL + pl) * TB + tb) * 64 + lane];
 #pragma unroll
             for (int mi = 0; mi < NMAT; ++mi)
 #pragma unroll
@@ -802,7 +978,7 @@ static __global__ void __launch_bounds__(kThreads) k_gemm_lds(GemmParams p, int 
 #pragma unroll
                     for (int tb = 0; tb < TB; ++tb)
 #pragma unroll
-                        for (int pl = 0; pl < 3; ++pl)
+                        for (int pl = 0; pl < NPL; ++pl)
                             acc[mi][rb][tb][pl] =
                                 __builtin_amdgcn_mfma_i32_16x16x64_i8(av, b[tb][pl], acc[mi][rb][tb][pl], 0, 0, 0);
                 }
@@ -855,12 +1031,21 @@ static __global__ void __launch_bounds__(kThreads) k_gemm_lds(GemmParams p, int 
             const int rr = r0 + 16 * rb + 4 * lg;
             const float *const scl[2] = {sg.scale[0] + (rr - sg.start),
                                          NMAT == 2 ? sg.scale[1] + (rr - sg.start) : nullptr};
-            v4i a3[NMAT][3];
+            if constexpr (NPL == 1) {
+                const int *const us[2] = {sg.usum[0] + (rr - sg.start),
+                                          NMAT == 2 ? sg.usum[1] + (rr - sg.start) : nullptr};
+                v4i a1[NMAT];
 #pragma unroll
-            for (int mi = 0; mi < NMAT; ++mi)
+                for (int mi = 0; mi < NMAT; ++mi) a1[mi] = acc[mi][rb][tb][0];
+                gemm_store_vnni<QT, NMAT>(p, epi, n, rr, scl, us, a1);
+            } else {
+                v4i a3[NMAT][3];
 #pragma unroll
-                for (int pl = 0; pl < 3; ++pl) a3[mi][pl] = acc[mi][rb][tb][pl];
-            gemm_store<QT, NMAT>(p, epi, n, rr, scl, a3);
+                for (int mi = 0; mi < NMAT; ++mi)
+#pragma unroll
+                    for (int pl = 0; pl < 3; ++pl) a3[mi][pl] = acc[mi][rb][tb][pl];
+                gemm_store<QT, NMAT>(p, epi, n, rr, scl, a3);
+            }
         }
     }
 }

@@ -89,6 +89,7 @@ struct pocr_weight {
     const float *scale = nullptr;
     const uint8_t *data = nullptr;
     uint8_t *tiled = nullptr;  // the prefill GEMM's copy in its load order, when weight_tiles_ok
+    int *usum = nullptr;       // Q4/Q6 with a tile image: Σ of each row's stored codes (row_usum)
 };
 
 struct LayerW {
@@ -194,6 +195,10 @@ int seq_idle(const pocr_seq *s, const char *op);
 // sampling head (logits, top-k, one draw into argmax slot 0) when the
 // sequence samples
 int enqueue_lm_head(pocr_seq *s, const float *x, bool want_logits);
+// the VNNI mode's ordered attention for the n rows of a batched prompt
+// (k_attn_ordered_rows): q heads × n workgroups, cache rows [0, clen0 + i]
+int launch_attn_ordered_rows(hipStream_t s, const float *qkv, int stride, const float *kc, const float *vc,
+                             int heads, int kvh, int n, int clen0, float scale, float *out, int out_stride);
 // the matrix-core head for 2 to 16 vectors (head.hpp, k_head_wide)
 constexpr int kHeadWideMinRows = 16384;  // plain scores of fewer rows stay on the GEMV
 bool head_wide_ok(const pocr_weight *w);
@@ -213,6 +218,8 @@ bool gemm_tiled(int K);
 // weights of this shape get a tile image at upload (k_tile_weight)
 bool weight_tiles_ok(int rows, int cols);
 int tile_weight(hipStream_t s, int qtype, const uint8_t *src, int row_bytes, int rows, int cols, uint8_t *dst);
+// Σ of each row's stored codes (Q4, Q6), for the VNNI-mode GEMM epilogue
+int row_usum(hipStream_t s, int qtype, const uint8_t *src, int row_bytes, int rows, int cols, int *dst);
 // the small MFMA GEMM over at most 16 rows (digit planes of 16 rows)
 bool gemm_small_ok(int rows, int K);
 int gemm_small_rows(hipStream_t s, int qtype, int nmat, const GemmParams &p, int epi);

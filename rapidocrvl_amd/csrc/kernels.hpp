@@ -27,7 +27,8 @@ constexpr int kMaxCols = 4096; // widest input of the streaming GEMV kernel
 struct DevMat {
     const float *scale;    // [rows]
     const uint8_t *data;   // rows * row_bytes, 256-byte aligned base
-    const uint8_t *tiled;  // the same bytes in the prefill GEMM's operand order (weight_tile_off), or null
+    const uint8_t *tiled;  // the same bytes in the prefill GEMM's operand order (k_tile_weight), or null
+    const int *usum;       // Q4/Q6 with a tile image: Σ of the row's stored codes (k_row_usum), else null
     int rows;
     int cols;
     int row_bytes;
@@ -1394,6 +1395,7 @@ static __global__ void __launch_bounds__(kThreads) k_step_begin_multi(StepBatch 
 // ---------------------------------------------------------------------------
 constexpr int kHD = 128;
 constexpr int kMaxGroup = 8;
+constexpr int kOrdMaxRows = 8192;  // cache rows of the VNNI mode's ordered attention (scores in LDS)
 constexpr int kMaxChunk = 64;  // cache rows per workgroup (RPW 16)
 constexpr int kRec = kHD + 4;  // partial record per head: m, l, 2 pad, acc[128] (16-byte aligned)
 

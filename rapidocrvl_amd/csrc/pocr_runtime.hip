@@ -186,17 +186,22 @@ extern "C" int pocr_weight_upload(pocr_ctx *ctx, int qtype, int rows, int cols, 
         (void)hipFree(base);
         return fail(POCR_ERR_DEVICE, "weight upload copy: %s", hipGetErrorString(e));
     }
-    // the prefill GEMM's image of the same bytes (k_tile_weight)
+    // the prefill GEMM's image of the same bytes (k_tile_weight), and for Q4/Q6
+    // the rows' code sums of its VNNI mode
     uint8_t *tiled = nullptr;
+    int *usum = nullptr;
     if (weight_tiles_ok(rows, cols)) {
+        const uint8_t *src = (const uint8_t *)base + scale_bytes;
         e = hipMalloc(&tiled, data_bytes);
+        if (e == hipSuccess && qtype != POCR_Q8) e = hipMalloc(&usum, (size_t)rows * sizeof(int));
         int rc = e == hipSuccess ? POCR_OK : fail(POCR_ERR_DEVICE, "weight tile image: %s", hipGetErrorString(e));
-        if (rc == POCR_OK)
-            rc = tile_weight(ctx->stream, qtype, (const uint8_t *)base + scale_bytes, (int)rb, rows, cols, tiled);
+        if (rc == POCR_OK) rc = tile_weight(ctx->stream, qtype, src, (int)rb, rows, cols, tiled);
+        if (rc == POCR_OK && usum) rc = row_usum(ctx->stream, qtype, src, (int)rb, rows, cols, usum);
         if (rc == POCR_OK && (e = hipStreamSynchronize(ctx->stream)) != hipSuccess)
             rc = fail(POCR_ERR_DEVICE, "weight tile image: %s", hipGetErrorString(e));
         if (rc != POCR_OK) {
-            if (tiled) (void)hipFree(tiled);
+            free_dev(usum);
+            free_dev(tiled);
             (void)hipFree(base);
             return rc;
         }
@@ -212,6 +217,7 @@ extern "C" int pocr_weight_upload(pocr_ctx *ctx, int qtype, int rows, int cols, 
     w->scale = (const float *)base;
     w->data = (const uint8_t *)base + scale_bytes;
     w->tiled = tiled;
+    w->usum = usum;
     *out = w;
     return POCR_OK;
 }
@@ -230,6 +236,7 @@ void pocr::weight_release(const pocr_weight *cw) {
         (void)hipStreamSynchronize(ctx->stream);
         free_dev(w->base);
         free_dev(w->tiled);
+        free_dev(w->usum);
     }
     delete w;
     ctx_release(ctx);
@@ -242,6 +249,7 @@ DevMat pocr::dev_mat(const pocr_weight *w) {
     m.scale = w->scale;
     m.data = w->data;
     m.tiled = w->tiled;
+    m.usum = w->usum;
     m.rows = w->rows;
     m.cols = w->cols;
     m.row_bytes = (int)w->row_bytes;
@@ -2351,6 +2359,15 @@ static int enqueue_layer(pocr_seq *s, int li, bool last, bool kv_only) {
     return POCR_OK;
 }
 
+int pocr::launch_attn_ordered_rows(hipStream_t s, const float *qkv, int stride, const float *kc, const float *vc,
+                                   int heads, int kvh, int n, int clen0, float scale, float *out, int out_stride) {
+    if (clen0 + n > kOrdMaxRows) return fail(POCR_ERR_UNSUPPORTED, "ordered attention: %d rows", clen0 + n);
+    hipLaunchKernelGGL(k_attn_ordered_rows, dim3(heads, n), dim3(kThreads), (size_t)(clen0 + n) * 4, s, qkv, stride, kc,
+                       vc, heads, kvh, clen0, scale, out, out_stride);
+    HIP_TRY(hipGetLastError());
+    return POCR_OK;
+}
+
 int pocr::enqueue_lm_head(pocr_seq *s, const float *x, bool want_logits) {
     pocr_model *m = s->m;
     hipStream_t st = m->ctx->stream;
@@ -3310,17 +3327,6 @@ extern "C" int pocr_prefill(pocr_seq *s, int n, const float *emb, const int32_t 
     RC(seq_idle(s, "pocr_prefill"));
     HIP_TRY(hipSetDevice(s->m->ctx->device));
     if (s->len + n > s->cap) return fail(POCR_ERR_ARG, "pocr_prefill: %d rows exceed capacity", n);
-    if (s->m->vnni) {
-        // VNNI mode: the rows go through token steps (the batched prefill
-        // computes plain mode), as the reference's CPU path takes a prompt
-        const int H = s->m->cfg.hidden;
-        for (int i = 0; i < n; ++i) {
-            const bool last = i == n - 1;
-            RC(step_locked(s, emb + (size_t)i * H, pos3 + 3 * i, last, last ? logits : nullptr,
-                           last ? token : nullptr));
-        }
-        return POCR_OK;
-    }
     return prefill_locked(s, n, emb, pos3, logits, token);
 }
 
@@ -3366,9 +3372,6 @@ int pocr::generate_locked(pocr_seq *s, const int32_t *ids, int n_ids, const floa
     if (n_ids + max_new - 1 > s->cap) return fail(POCR_ERR_ARG, "pocr_generate: capacity %d too small", s->cap);
     if (s->sampling) RC(seed_sampler(s));  // one generator per generation call
     int32_t next = -1;
-    // VNNI mode: the prompt goes token by token, as the reference's CPU path
-    // takes it (the batched prefill computes plain mode only)
-    if (m->vnni) use_prefill = 0;
     if (use_prefill) {
         const int rc = prefill_ids_locked(s, ids, n_ids, n_image > 0 ? image_embeds : nullptr,
                                           n_image > 0 ? image_token_id : -1, pos.data(), nullptr, &next, image_dev);

@@ -43,7 +43,29 @@ int launch_digitize_w(hipStream_t s, int qtype, const DigitizeParams &p, int n) 
     return POCR_OK;
 }
 
+template <int J>
+int launch_digitize_vnni_j(hipStream_t s, int qtype, const DigitizeParams &p, int n) {
+    const dim3 grid((n + kWaves - 1) / kWaves);
+    switch (qtype) {
+    case QT_Q4: hipLaunchKernelGGL((k_digitize_vnni<QT_Q4, J>), grid, dim3(kThreads), 0, s, p, n); break;
+    case QT_Q6: hipLaunchKernelGGL((k_digitize_vnni<QT_Q6, J>), grid, dim3(kThreads), 0, s, p, n); break;
+    default: return fail(POCR_ERR_UNSUPPORTED, "VNNI digitize: qtype %d", qtype);
+    }
+    HIP_TRY(hipGetLastError());
+    return POCR_OK;
+}
+
+// the VNNI mode's bytes: tile layout only, K a multiple of 128 up to 4096
+int launch_digitize_vnni(hipStream_t s, int qtype, const DigitizeParams &p, int n) {
+    if (!p.tiled || p.K % kStageCols || p.K > 4096) return fail(POCR_ERR_UNSUPPORTED, "VNNI digitize: K %d", p.K);
+    if (p.K <= 1024) return launch_digitize_vnni_j<1>(s, qtype, p, n);
+    if (p.K <= 2048) return launch_digitize_vnni_j<2>(s, qtype, p, n);
+    if (p.K <= 3072) return launch_digitize_vnni_j<3>(s, qtype, p, n);
+    return launch_digitize_vnni_j<4>(s, qtype, p, n);
+}
+
 int launch_digitize(hipStream_t s, int qtype, const DigitizeParams &p, int n) {
+    if (p.vnni) return launch_digitize_vnni(s, qtype, p, n);
     if (p.K % 16 || p.K > 2 * 16 * kThreads) return fail(POCR_ERR_UNSUPPORTED, "digitize: K %d", p.K);
     if (p.K > 16 * kThreads) return launch_digitize_g<2>(s, qtype, p, n);
     // up to 3072 columns: one wave per token, the same bytes (1345 tokens of
@@ -94,6 +116,15 @@ bool small_shape_ok(int rows, int K) { return rows % 16 == 0 && K % (kGemmK * kW
 template <int NMAT, int RB>
 int launch_gemm_lds_rb(hipStream_t s, int qtype, const GemmParams &p, int epi, int npad) {
     const dim3 grid((p.rows + 64 * RB - 1) / (64 * RB), npad / 32);
+    if (p.vnni) {  // one plane of VNNI bytes (Q4, Q6)
+        switch (qtype) {
+        case QT_Q4: hipLaunchKernelGGL((k_gemm_lds<QT_Q4, NMAT, 2, RB, 1>), grid, dim3(kThreads), 0, s, p, epi); break;
+        case QT_Q6: hipLaunchKernelGGL((k_gemm_lds<QT_Q6, NMAT, 2, RB, 1>), grid, dim3(kThreads), 0, s, p, epi); break;
+        default: return fail(POCR_ERR_UNSUPPORTED, "VNNI gemm: qtype %d", qtype);
+        }
+        HIP_TRY(hipGetLastError());
+        return POCR_OK;
+    }
     switch (qtype) {
     case QT_Q8: hipLaunchKernelGGL((k_gemm_lds<QT_Q8, NMAT, 2, RB>), grid, dim3(kThreads), 0, s, p, epi); break;
     case QT_Q4: hipLaunchKernelGGL((k_gemm_lds<QT_Q4, NMAT, 2, RB>), grid, dim3(kThreads), 0, s, p, epi); break;
@@ -138,13 +169,28 @@ int pocr::tile_weight(hipStream_t s, int qtype, const uint8_t *src, int row_byte
     return POCR_OK;
 }
 
+int pocr::row_usum(hipStream_t s, int qtype, const uint8_t *src, int row_bytes, int rows, int cols, int *dst) {
+    if (cols % 16) return fail(POCR_ERR_UNSUPPORTED, "row_usum: %d columns", cols);
+    const dim3 grid((rows + kWaves - 1) / kWaves);
+    switch (qtype) {
+    case QT_Q4: hipLaunchKernelGGL(k_row_usum<QT_Q4>, grid, dim3(kThreads), 0, s, src, row_bytes, rows, cols, dst); break;
+    case QT_Q6: hipLaunchKernelGGL(k_row_usum<QT_Q6>, grid, dim3(kThreads), 0, s, src, row_bytes, rows, cols, dst); break;
+    default: return fail(POCR_ERR_UNSUPPORTED, "row_usum: qtype %d", qtype);
+    }
+    HIP_TRY(hipGetLastError());
+    return POCR_OK;
+}
+
 namespace {
 
 // npad: token rows of the digit planes, a multiple of 32
 int launch_gemm(hipStream_t s, int qtype, int nmat, const GemmParams &p, int epi, int npad) {
+    if (p.vnni && !gemm_tiled(p.K)) return fail(POCR_ERR_UNSUPPORTED, "VNNI gemm: K %d", p.K);
     if (gemm_tiled(p.K)) {
-        for (int i = 0; i < (nmat == 2 ? 2 : 3); ++i)
+        for (int i = 0; i < (nmat == 2 ? 2 : 3); ++i) {
             if (!p.m[i].tiled) return fail(POCR_ERR_UNSUPPORTED, "gemm: %dx%d weight has no tile image", p.m[i].rows, p.K);
+            if (p.vnni && !p.m[i].usum) return fail(POCR_ERR_UNSUPPORTED, "VNNI gemm: %dx%d weight has no row sums", p.m[i].rows, p.K);
+        }
         if (nmat == 2) return launch_gemm_lds_t<2>(s, qtype, p, epi, npad);
         return launch_gemm_lds_t<1>(s, qtype, p, epi, npad);
     }
@@ -282,9 +328,22 @@ int batched_gemv(pocr_ctx *ctx, const DevMat &w, const float *x, int m, float *o
 // match n sequential steps (model.go:1514-1536, 3475-3643).
 namespace {
 
-bool batched_prefill_on(const pocr_model *m) {
+// The VNNI mode's batched prompt (vnni.hpp): Q4/Q6 layers (Q8 keeps plain
+// matvecs in that mode), every GEMM on the tile layout with K ≤ 4096 (one
+// wave per token forms the bytes), and the ordered attention's row limit.
+bool vnni_prefill_ok(const pocr_seq *s) {
+    const pocr_model *m = s->m;
+    const pocr_config &c = m->cfg;
+    if (m->layers[0].w[POCR_W_Q]->qtype == POCR_Q8) return false;
+    for (const int K : {c.hidden, c.heads * c.head_dim, c.intermediate})
+        if (!gemm_tiled(K) || K > 4096) return false;
+    return c.head_dim == kHD && s->cap <= kOrdMaxRows;
+}
+
+bool batched_prefill_on(const pocr_seq *s) {
     const char *env = getenv("POCR_BATCHED_PREFILL");
-    return !(env && env[0] == '0') && prefill_supported(m);
+    if ((env && env[0] == '0') || !prefill_supported(s->m)) return false;
+    return !s->m->vnni || vnni_prefill_ok(s);
 }
 
 // text rows of the prompt from the device embedding table; image rows
@@ -303,7 +362,7 @@ int prefill_run(pocr_seq *s, int n, const int32_t *pos3, float *logits, int32_t 
 }  // namespace
 
 int prefill_locked(pocr_seq *s, int n, const float *emb, const int32_t *pos3, float *logits, int32_t *token) {
-    if (!batched_prefill_on(s->m)) return prefill_tokenwise(s, n, emb, pos3, logits, token);
+    if (!batched_prefill_on(s)) return prefill_tokenwise(s, n, emb, pos3, logits, token);
     if (s->len + n > s->cap) return fail(POCR_ERR_ARG, "prefill: %d rows exceed capacity", n);
     RC(ensure_bufs(s, round_up(n, 32)));
     RC(upload_staged(s->m->ctx, s->pf.h, emb, (size_t)n * s->m->cfg.hidden * 4));
@@ -313,7 +372,7 @@ int prefill_locked(pocr_seq *s, int n, const float *emb, const int32_t *pos3, fl
 int prefill_ids_locked(pocr_seq *s, const int32_t *ids, int n, const float *image, int32_t image_token,
                        const int32_t *pos3, float *logits, int32_t *token, bool image_on_device) {
     pocr_model *m = s->m;
-    if (!batched_prefill_on(m) || m->cfg.hidden % 4) return POCR_ERR_UNSUPPORTED;
+    if (!batched_prefill_on(s) || m->cfg.hidden % 4) return POCR_ERR_UNSUPPORTED;
     if (s->len + n > s->cap) return fail(POCR_ERR_ARG, "prefill: %d rows exceed capacity", n);
     const int H = m->cfg.hidden;
     RC(ensure_bufs(s, round_up(n, 32)));
@@ -359,6 +418,11 @@ int prefill_run(pocr_seq *s, int n, const int32_t *pos3, float *logits, int32_t 
     const float eps = c.rms_norm_eps;
     const float scale = (float)(1.0 / std::sqrt((double)c.head_dim));
     const int qt = m->layers[0].w[POCR_W_Q]->qtype;
+    // VNNI mode (vnni.hpp): one plane of activation bytes per token and the
+    // mode's integer finish in every GEMM, the ordered attention per (head,
+    // token); every step is exact or in the token step's order, so the rows
+    // are the token steps' to the bit
+    const int vnni = m->vnni ? 1 : 0;
 
     auto digitize = [&](const float *x, int stride, const float *norm_w, int K) {
         DigitizeParams d{};
@@ -372,6 +436,7 @@ int prefill_run(pocr_seq *s, int n, const int32_t *pos3, float *logits, int32_t 
         d.xs = b.xs;
         d.xb = b.xb;
         d.tiled = gemm_tiled(K);
+        d.vnni = vnni;
         return launch_digitize(st, qt, d, n);
     };
     auto gemm_in = [&](GemmParams &p) {
@@ -381,6 +446,7 @@ int prefill_run(pocr_seq *s, int n, const int32_t *pos3, float *logits, int32_t 
         p.xb = b.xb;
         p.ntok = n;
         p.clen0 = clen0;
+        p.vnni = vnni;
     };
 
     for (int li = 0; li < c.layers; ++li) {
@@ -404,13 +470,19 @@ int prefill_run(pocr_seq *s, int n, const int32_t *pos3, float *logits, int32_t 
         // 2. per-token RoPE, K/V append at rows clen0.., causal attention
         hipLaunchKernelGGL(k_rope_append, dim3(n), dim3(kThreads), 0, st, b.qkv, QKV, b.pos, m->freq, m->axis,
                            c.heads, c.kv_heads, c.head_dim, layer_k(s, li), layer_v(s, li), clen0);
-        const int ntiles = (n + kPfTok - 1) / kPfTok, quads = (c.heads / c.kv_heads + 3) / 4;
-        const int nblk = (clen0 + n + kPfKeys - 1) / kPfKeys;
-        hipLaunchKernelGGL(k_kv_blocks, dim3(nblk, c.kv_heads), dim3(kThreads), 0, st, layer_k(s, li), layer_v(s, li),
-                           c.kv_heads, clen0 + n, nblk, b.kvimg);
-        hipLaunchKernelGGL(k_attn_prefill, dim3(c.kv_heads * quads, (ntiles + 1) / 2), dim3(kPfThreads), 0, st, b.qkv,
-                           QKV, b.kvimg, nblk, c.heads, c.kv_heads, n, clen0, scale, b.ho, Q);
-        HIP_TRY(hipGetLastError());
+        if (vnni) {
+            HIP_TRY(hipGetLastError());
+            RC(launch_attn_ordered_rows(st, b.qkv, QKV, layer_k(s, li), layer_v(s, li), c.heads, c.kv_heads, n, clen0,
+                                        scale, b.ho, Q));
+        } else {
+            const int ntiles = (n + kPfTok - 1) / kPfTok, quads = (c.heads / c.kv_heads + 3) / 4;
+            const int nblk = (clen0 + n + kPfKeys - 1) / kPfKeys;
+            hipLaunchKernelGGL(k_kv_blocks, dim3(nblk, c.kv_heads), dim3(kThreads), 0, st, layer_k(s, li),
+                               layer_v(s, li), c.kv_heads, clen0 + n, nblk, b.kvimg);
+            hipLaunchKernelGGL(k_attn_prefill, dim3(c.kv_heads * quads, (ntiles + 1) / 2), dim3(kPfThreads), 0, st,
+                               b.qkv, QKV, b.kvimg, nblk, c.heads, c.kv_heads, n, clen0, scale, b.ho, Q);
+            HIP_TRY(hipGetLastError());
+        }
         // 3. o_proj + residual (+ the Q4/Q6 behaviour per token) → v; h if in place
         RC(digitize(b.ho, Q, nullptr, Q));
         GemmParams o = gemm_params_1(L.w[POCR_W_O]);

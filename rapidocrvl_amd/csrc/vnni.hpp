@@ -242,39 +242,16 @@ __global__ void __launch_bounds__(kThreads) k_gemv_vnni(GemvParams p, int pro, i
 //   more rows by one running sum in row order; weights = e·(1/sum);
 // * out[d] = p0·v0[d], then out[d] += p_t·v_t[d] in row order.
 // One workgroup per q head; the previous kernel (the split attention) has
-// appended this step's rotated K/V row.  Scores live in LDS (len floats).
-constexpr int kOrdMaxRows = 8192;
+// appended this step's rotated K/V row.  Scores live in LDS (len floats, at
+// most kOrdMaxRows).
 
-__global__ void __launch_bounds__(kThreads) k_attn_ordered(AttnParams a) {
+// One q head over len ≥ 2 cache rows in that order; the whole workgroup
+// calls it.  qs (LDS) holds the rotated q, kc / vc point at the KV head's
+// columns of row 0 (row stride kvd), sc is LDS of len floats.
+__device__ __forceinline__ void attn_ordered_head(const float *qs, const float *kc, const float *vc, size_t kvd,
+                                                  int len, float scale, float *out, float *sc, float *red,
+                                                  float *s_inv) {
 #pragma clang fp contract(off)
-    const StepState *st = a.st;
-    if (st->err) return;
-    extern __shared__ float sc[];
-    __shared__ float qs[128];
-    __shared__ float red[kWaves];
-    __shared__ float s_inv;
-    const int len = st->len;
-    const int h = blockIdx.x, kvh = h / (a.heads / a.kvh);
-    const size_t kvd = (size_t)a.kvh * 128;
-    const float *kc = a.kc + (size_t)kvh * 128, *vc = a.vc + (size_t)kvh * 128;
-    float *out = a.head_out + (size_t)h * 128;
-    if (len == 1) {  // attendHead's single row: V itself
-        if (threadIdx.x < 128) out[threadIdx.x] = vc[threadIdx.x];
-        return;
-    }
-    if (threadIdx.x < 64) {  // applyRoPE's pairs (i, 64 + i)
-        const int i = threadIdx.x;
-        const float q0 = a.q[(size_t)h * 128 + i], q1 = a.q[(size_t)h * 128 + 64 + i];
-        if (st->has_rope) {
-            const float cs = st->cos_t[i], sn = st->sin_t[i];
-            qs[i] = q0 * cs - q1 * sn;
-            qs[64 + i] = q1 * cs + q0 * sn;
-        } else {
-            qs[i] = q0;
-            qs[64 + i] = q1;
-        }
-    }
-    __syncthreads();
     for (int t = threadIdx.x; t < len; t += kThreads) {
         const float *k = kc + (size_t)t * kvd;
         float s[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
@@ -290,7 +267,7 @@ __global__ void __launch_bounds__(kThreads) k_attn_ordered(AttnParams a) {
             s[6] = s[6] + qs[i + 6] * k1.z;
             s[7] = s[7] + qs[i + 7] * k1.w;
         }
-        sc[t] = (((s[0] + s[1]) + (s[2] + s[3])) + ((s[4] + s[5]) + (s[6] + s[7]))) * a.scale;
+        sc[t] = (((s[0] + s[1]) + (s[2] + s[3])) + ((s[4] + s[5]) + (s[6] + s[7]))) * scale;
     }
     __syncthreads();
     // the maximum (order-free)
@@ -335,10 +312,10 @@ __global__ void __launch_bounds__(kThreads) k_attn_ordered(AttnParams a) {
                 }
                 for (; t < len; ++t) sum = sum + sc[t];
             }
-            s_inv = 1.0f / sum;
+            *s_inv = 1.0f / sum;
         }
         __syncthreads();
-        const float inv = s_inv;
+        const float inv = *s_inv;
         for (int t = threadIdx.x; t < len; t += kThreads) sc[t] = sc[t] * inv;
     }
     __syncthreads();
@@ -356,6 +333,65 @@ __global__ void __launch_bounds__(kThreads) k_attn_ordered(AttnParams a) {
         for (; t < len; ++t) acc = acc + sc[t] * vc[(size_t)t * kvd + d];
         out[d] = acc;
     }
+}
+
+static __global__ void __launch_bounds__(kThreads) k_attn_ordered(AttnParams a) {
+#pragma clang fp contract(off)
+    const StepState *st = a.st;
+    if (st->err) return;
+    extern __shared__ float sc[];
+    __shared__ float qs[128];
+    __shared__ float red[kWaves];
+    __shared__ float s_inv;
+    const int len = st->len;
+    const int h = blockIdx.x, kvh = h / (a.heads / a.kvh);
+    const size_t kvd = (size_t)a.kvh * 128;
+    const float *kc = a.kc + (size_t)kvh * 128, *vc = a.vc + (size_t)kvh * 128;
+    float *out = a.head_out + (size_t)h * 128;
+    if (len == 1) {  // attendHead's single row: V itself
+        if (threadIdx.x < 128) out[threadIdx.x] = vc[threadIdx.x];
+        return;
+    }
+    if (threadIdx.x < 64) {  // applyRoPE's pairs (i, 64 + i)
+        const int i = threadIdx.x;
+        const float q0 = a.q[(size_t)h * 128 + i], q1 = a.q[(size_t)h * 128 + 64 + i];
+        if (st->has_rope) {
+            const float cs = st->cos_t[i], sn = st->sin_t[i];
+            qs[i] = q0 * cs - q1 * sn;
+            qs[64 + i] = q1 * cs + q0 * sn;
+        } else {
+            qs[i] = q0;
+            qs[64 + i] = q1;
+        }
+    }
+    __syncthreads();
+    attn_ordered_head(qs, kc, vc, kvd, len, a.scale, out, sc, red, &s_inv);
+}
+
+// The same for the rows of a batched prompt: workgroup (q head h, token i)
+// attends cache rows [0, clen0 + i] with token i's q, already rotated in the
+// qkv rows (k_rope_append, the same pair formula), and writes its head of
+// out row i.  Token i's result is the one its token step computes.
+static __global__ void __launch_bounds__(kThreads) k_attn_ordered_rows(const float *qkv, int stride, const float *kc,
+                                                                       const float *vc, int heads, int kvh, int clen0,
+                                                                       float scale, float *out, int out_stride) {
+    extern __shared__ float sc[];
+    __shared__ float qs[128];
+    __shared__ float red[kWaves];
+    __shared__ float s_inv;
+    const int h = blockIdx.x, i = blockIdx.y;
+    const int len = clen0 + i + 1;
+    const int g = h / (heads / kvh);
+    const size_t kvd = (size_t)kvh * 128;
+    const float *kh = kc + (size_t)g * 128, *vh = vc + (size_t)g * 128;
+    float *o = out + (size_t)i * out_stride + (size_t)h * 128;
+    if (len == 1) {
+        if (threadIdx.x < 128) o[threadIdx.x] = vh[threadIdx.x];
+        return;
+    }
+    if (threadIdx.x < 128) qs[threadIdx.x] = qkv[(size_t)i * stride + (size_t)h * 128 + threadIdx.x];
+    __syncthreads();
+    attn_ordered_head(qs, kh, vh, kvd, len, scale, o, sc, red, &s_inv);
 }
 
 }  // namespace pocr

@@ -119,8 +119,8 @@ def test_vnni_steps_match_oracle(orc, ctx, qtype, seed):
 @pytest.mark.parametrize("qtype", [Q4, Q6], ids=["q4", "q6"])
 def test_vnni_generation_ernie(orc, ctx, qtype):
     """The 0.3B decoder, 64 prompt ids from [0, 100000) with seed 0, 16 greedy
-    tokens in VNNI mode: the oracle's stream in the same mode (the prompt goes
-    token by token in this mode, even when the prefill is asked for)."""
+    tokens in VNNI mode: the oracle's stream in the same mode (the prompt
+    through the mode's batched prefill)."""
     cfg = ERNIE_0P3B
     w, om, gm = _pair(orc, ctx, cfg, qtype, seed=0)
     ids = synth.prompt_ids(64, seed=0)
@@ -130,6 +130,67 @@ def test_vnni_generation_ernie(orc, ctx, qtype):
     assert list(got) == list(want)
     assert len(s) == 64 + 15
     s.close()
+    gm.close()
+
+
+@pytest.mark.parametrize("qtype", [Q4, Q6], ids=["q4", "q6"])
+def test_vnni_batched_prefill_bit_exact(orc, ctx, qtype):
+    """The VNNI mode's batched prompt (one plane of activation bytes per token,
+    the mode's integer finish in the MFMA GEMMs, the ordered attention per
+    head and token) against the oracle's VNNI token steps: the last token's
+    logits and every K/V row to the bit, through the first-token, 1..5 and >= 6
+    residual branches, then a second prompt on top of the cache (rows from
+    clen0 = 13)."""
+    w, om, gm = _pair(orc, ctx, MID, qtype, seed=5)
+    os_, gs = om.seq(40), gm.seq(40)
+    embs = w["embed"][[(11 * p + 2) % MID.vocab for p in range(21)]]
+    pos = np.array([[p, p, p] for p in range(21)], np.int32)
+    for lo, hi in ((0, 13), (13, 21)):
+        for p in range(lo, hi):
+            ot, ol, _ = os_.step(embs[p], tuple(pos[p]))
+        gt, gl = gs.prefill(embs[lo:hi], pos[lo:hi], want_logits=True)
+        assert gt == ot
+        assert np.array_equal(gl, ol), (lo, float(np.max(np.abs(gl - ol))))
+    assert len(gs) == 21
+    for li in range(MID.layers):
+        gk, gv = gs.read_kv(li)
+        ok, ov = os_.kv(li)
+        assert np.array_equal(gk.reshape(21, -1), ok.reshape(21, -1)), li
+        assert np.array_equal(gv.reshape(21, -1), ov.reshape(21, -1)), li
+    gs.close()
+    gm.close()
+
+
+def test_vnni_batched_prefill_runs_batched(ctx, monkeypatch):
+    """A 256-row VNNI prompt through the batched prefill and through token
+    steps (POCR_BATCHED_PREFILL=0): the same bits, and the batched form is
+    the fast one (tens of launches per layer instead of 256 token steps)."""
+    import time
+    cfg = ERNIE_0P3B
+    w = synth.make_weights(cfg, Q4, seed=2)
+    gm = lib.Model(ctx, cfg)
+    gm.load_weights(w)
+    gm.set_vnni(True)
+    embs = w["embed"][synth.prompt_ids(256, seed=3)]
+    pos = np.array([[p, p, p] for p in range(256)], np.int32)
+
+    def run():
+        s = gm.seq(260)
+        s.prefill(embs[:8], pos[:8])  # warm-up: buffers and first launches
+        t0 = time.perf_counter()
+        tok, lg = s.prefill(embs[8:], pos[8:], want_logits=True)
+        dt = time.perf_counter() - t0
+        kv = s.read_kv(cfg.layers - 1)
+        s.close()
+        return tok, lg, kv, dt
+
+    tb, lb, kvb, dtb = run()
+    monkeypatch.setenv("POCR_BATCHED_PREFILL", "0")
+    tt, lt, kvt, dtt = run()
+    monkeypatch.delenv("POCR_BATCHED_PREFILL")
+    assert tb == tt and np.array_equal(lb, lt)
+    assert np.array_equal(kvb[0], kvt[0]) and np.array_equal(kvb[1], kvt[1])
+    assert dtb * 5 < dtt, (dtb, dtt)
     gm.close()
 
 
@@ -146,7 +207,8 @@ def test_vnni_mode_rules(ctx, rng):
         gm.set_vnni(False)
     assert e.value.code == lib.POCR_ERR_ARG
     s2 = gm.seq(16)
-    # pocr_prefill takes its rows as token steps: the same cache and logits
+    # 192 intermediate columns are off the batched prefill's 128-column tiles:
+    # pocr_prefill takes these rows as token steps, the same cache and logits
     pos = np.array([[p, p, p] for p in range(3)], np.int32)
     tok, lp = s.prefill(w["embed"][[5, 6, 7]], pos, want_logits=True)
     for p in range(3):
