@@ -111,7 +111,11 @@ int pocr_quantize_rows(int qtype, int tie_mode, const float *w, int rows, int co
 int pocr_unpack_rows(int qtype, const uint8_t *packed, int rows, int cols, int8_t *out);
 
 /* ---------------- weights ---------------- */
-/* upload one Q*_ROW tensor (scales f32[rows] + packed rows) into HBM */
+/* upload one Q*_ROW tensor (scales f32[rows] + packed rows) into HBM.  A
+ * tensor of rows a multiple of 16 and cols a multiple of 128 also gets the
+ * prefill GEMM's tile image of the same bytes (and, for Q4/Q6, each row's sum
+ * of stored codes for the VNNI mode), built on the device here: its HBM
+ * footprint is then about twice the packed bytes. */
 int pocr_weight_upload(pocr_ctx *ctx, int qtype, int rows, int cols, const float *scales,
                        const uint8_t *packed, pocr_weight **out);
 void pocr_weight_free(pocr_weight *w);
