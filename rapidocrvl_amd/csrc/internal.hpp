@@ -196,7 +196,8 @@ int seq_idle(const pocr_seq *s, const char *op);
 // sequence samples
 int enqueue_lm_head(pocr_seq *s, const float *x, bool want_logits);
 // the VNNI mode's ordered attention for the n rows of a batched prompt
-// (k_attn_ordered_rows): q heads × n workgroups, cache rows [0, clen0 + i]
+// (k_attn_ordered_rows): workgroups of up to 8 q heads of one KV head × n
+// tokens, token i over cache rows [0, clen0 + i]
 int launch_attn_ordered_rows(hipStream_t s, const float *qkv, int stride, const float *kc, const float *vc,
                              int heads, int kvh, int n, int clen0, float scale, float *out, int out_stride);
 // the matrix-core head for 2 to 16 vectors (head.hpp, k_head_wide)

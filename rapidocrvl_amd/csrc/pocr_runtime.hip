@@ -2361,9 +2361,24 @@ static int enqueue_layer(pocr_seq *s, int li, bool last, bool kv_only) {
 
 int pocr::launch_attn_ordered_rows(hipStream_t s, const float *qkv, int stride, const float *kc, const float *vc,
                                    int heads, int kvh, int n, int clen0, float scale, float *out, int out_stride) {
-    if (clen0 + n > kOrdMaxRows) return fail(POCR_ERR_UNSUPPORTED, "ordered attention: %d rows", clen0 + n);
-    hipLaunchKernelGGL(k_attn_ordered_rows, dim3(heads, n), dim3(kThreads), (size_t)(clen0 + n) * 4, s, qkv, stride, kc,
-                       vc, heads, kvh, clen0, scale, out, out_stride);
+    const int rows = clen0 + n, group = heads / kvh;
+    if (rows > kOrdMaxRows) return fail(POCR_ERR_UNSUPPORTED, "ordered attention: %d rows", rows);
+    // q heads per workgroup: as many of the group as keep the scores within
+    // 56 KB of LDS (with the q rows under 64 KB; two workgroups per CU or more)
+    int hpw = 1;
+    for (const int c : {8, 4, 2})
+        if (group % c == 0 && (size_t)c * rows * 4 <= 56 * 1024) {
+            hpw = c;
+            break;
+        }
+    const dim3 grid(kvh * (group / hpw), n);
+    const size_t lds = (size_t)hpw * rows * 4;
+    switch (hpw) {
+    case 8: hipLaunchKernelGGL(k_attn_ordered_rows<8>, grid, dim3(kThreads), lds, s, qkv, stride, kc, vc, heads, kvh, clen0, scale, out, out_stride); break;
+    case 4: hipLaunchKernelGGL(k_attn_ordered_rows<4>, grid, dim3(kThreads), lds, s, qkv, stride, kc, vc, heads, kvh, clen0, scale, out, out_stride); break;
+    case 2: hipLaunchKernelGGL(k_attn_ordered_rows<2>, grid, dim3(kThreads), lds, s, qkv, stride, kc, vc, heads, kvh, clen0, scale, out, out_stride); break;
+    default: hipLaunchKernelGGL(k_attn_ordered_rows<1>, grid, dim3(kThreads), lds, s, qkv, stride, kc, vc, heads, kvh, clen0, scale, out, out_stride);
+    }
     HIP_TRY(hipGetLastError());
     return POCR_OK;
 }

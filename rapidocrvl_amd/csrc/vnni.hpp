@@ -368,30 +368,170 @@ static __global__ void __launch_bounds__(kThreads) k_attn_ordered(AttnParams a) 
     attn_ordered_head(qs, kc, vc, kvd, len, a.scale, out, sc, red, &s_inv);
 }
 
-// The same for the rows of a batched prompt: workgroup (q head h, token i)
-// attends cache rows [0, clen0 + i] with token i's q, already rotated in the
-// qkv rows (k_rope_append, the same pair formula), and writes its head of
-// out row i.  Token i's result is the one its token step computes.
+// The same for the rows of a batched prompt.  Workgroup (KV head g, head
+// group hg, token i) takes HPW q heads of g's group for token i over cache rows
+// [0, len), len = clen0 + i + 1, with token i's q already rotated in the qkv
+// rows (k_rope_append, the token step's pair formula).  Each K and V row is
+// read once for the HPW heads; every (head, token) result is formed exactly as
+// attn_ordered_head forms it:
+// * score t: dotF32's eight running sums over the dims in order (s_k over
+//   dims ≡ k mod 8), the tree, times the scale;
+// * the maximum (order-free), FastExp of s − max (the wrapped form), the pair
+//   form for two rows; Σ by the fixed trees up to 8 rows, else one running
+//   sum in row order (one thread per head); weights e·(1/Σ);
+// * out[d] = p0·v0[d], then + p_t·v_t[d] in row order (one chain per head and
+//   dim; a thread keeps HPW/2 chains of one dim, one V load for all of them).
+// LDS: the HPW rotated q rows and HPW·len scores (dynamic).
+template <int HPW>
 static __global__ void __launch_bounds__(kThreads) k_attn_ordered_rows(const float *qkv, int stride, const float *kc,
                                                                        const float *vc, int heads, int kvh, int clen0,
                                                                        float scale, float *out, int out_stride) {
-    extern __shared__ float sc[];
-    __shared__ float qs[128];
-    __shared__ float red[kWaves];
-    __shared__ float s_inv;
-    const int h = blockIdx.x, i = blockIdx.y;
+#pragma clang fp contract(off)
+    static_assert(HPW == 1 || HPW == 2 || HPW == 4 || HPW == 8, "q heads per workgroup");
+    extern __shared__ float sc_all[];
+    __shared__ float qs[HPW][128];
+    __shared__ float red[kWaves][HPW];
+    __shared__ float s_inv[HPW];
+    const int group = heads / kvh;
+    const int ngrp = group / HPW;
+    const int g = blockIdx.x / ngrp, h0 = g * group + (blockIdx.x % ngrp) * HPW;
+    const int i = blockIdx.y;
     const int len = clen0 + i + 1;
-    const int g = h / (heads / kvh);
     const size_t kvd = (size_t)kvh * 128;
     const float *kh = kc + (size_t)g * 128, *vh = vc + (size_t)g * 128;
-    float *o = out + (size_t)i * out_stride + (size_t)h * 128;
-    if (len == 1) {
-        if (threadIdx.x < 128) o[threadIdx.x] = vh[threadIdx.x];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if (len == 1) {  // attendHead's single row: V itself
+        for (int e = tid; e < HPW * 128; e += kThreads)
+            out[(size_t)i * out_stride + (size_t)(h0 + e / 128) * 128 + e % 128] = vh[e % 128];
         return;
     }
-    if (threadIdx.x < 128) qs[threadIdx.x] = qkv[(size_t)i * stride + (size_t)h * 128 + threadIdx.x];
+    for (int e = tid; e < HPW * 128; e += kThreads)
+        qs[e / 128][e % 128] = qkv[(size_t)i * stride + (size_t)(h0 + e / 128) * 128 + e % 128];
     __syncthreads();
-    attn_ordered_head(qs, kh, vh, kvd, len, scale, o, sc, red, &s_inv);
+    // scores: thread → rows t, the row's dims 8 at a time for all HPW heads
+    for (int t = tid; t < len; t += kThreads) {
+        const float *k = kh + (size_t)t * kvd;
+        float s[HPW][8];
+#pragma unroll
+        for (int h = 0; h < HPW; ++h)
+#pragma unroll
+            for (int c = 0; c < 8; ++c) s[h][c] = 0.0f;
+        for (int d = 0; d < 128; d += 8) {
+            const float4 k0 = *reinterpret_cast<const float4 *>(k + d);
+            const float4 k1 = *reinterpret_cast<const float4 *>(k + d + 4);
+            const float kv[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+#pragma unroll
+            for (int h = 0; h < HPW; ++h)
+#pragma unroll
+                for (int c = 0; c < 8; ++c) s[h][c] = s[h][c] + qs[h][d + c] * kv[c];
+        }
+#pragma unroll
+        for (int h = 0; h < HPW; ++h)
+            sc_all[(size_t)h * len + t] =
+                (((s[h][0] + s[h][1]) + (s[h][2] + s[h][3])) + ((s[h][4] + s[h][5]) + (s[h][6] + s[h][7]))) * scale;
+    }
+    __syncthreads();
+    // the maxima (order-free)
+    {
+        float mx[HPW];
+#pragma unroll
+        for (int h = 0; h < HPW; ++h) {
+            mx[h] = -INFINITY;
+            for (int t = tid; t < len; t += kThreads) mx[h] = fmaxf(mx[h], sc_all[(size_t)h * len + t]);
+            mx[h] = wave_max(mx[h]);
+        }
+        if (lane == 0) {
+#pragma unroll
+            for (int h = 0; h < HPW; ++h) red[wave][h] = mx[h];
+        }
+    }
+    __syncthreads();
+    if (len == 2) {
+        if (tid < HPW) {
+            float *sc = sc_all + (size_t)tid * len;
+            const float x0 = sc[0], x1 = sc[1];
+            const float e = x0 >= x1 ? fast_exp_wrap(x1 - x0) : fast_exp_wrap(x0 - x1);
+            const float inv = 1.0f / (1.0f + e);
+            sc[0] = x0 >= x1 ? inv : e * inv;
+            sc[1] = x0 >= x1 ? e * inv : inv;
+        }
+    } else {
+        float m[HPW];
+#pragma unroll
+        for (int h = 0; h < HPW; ++h) {
+            m[h] = red[0][h];
+#pragma unroll
+            for (int w = 1; w < kWaves; ++w) m[h] = fmaxf(m[h], red[w][h]);
+        }
+#pragma unroll
+        for (int h = 0; h < HPW; ++h)
+            for (int t = tid; t < len; t += kThreads) {
+                float *e = sc_all + (size_t)h * len + t;
+                *e = fast_exp_wrap(*e - m[h]);
+            }
+        __syncthreads();
+        if (tid < HPW) {  // thread h: head h's sum, in Softmax's order
+            const float *sc = sc_all + (size_t)tid * len;
+            float sum;
+            if (len <= 8) {
+                sum = sc[0] + sc[1];
+                if (len == 3) sum = sum + sc[2];
+                if (len >= 4) sum = sum + (sc[2] + sc[3]);
+                if (len == 5) sum = sum + sc[4];
+                if (len >= 6) sum = sum + (sc[4] + sc[5]);
+                if (len == 7) sum = sum + sc[6];
+                if (len == 8) sum = sum + (sc[6] + sc[7]);
+            } else {
+                sum = 0.0f;
+                int t = 0;
+                for (; t + 16 <= len; t += 16) {
+                    float v[16];
+#pragma unroll
+                    for (int k = 0; k < 16; ++k) v[k] = sc[t + k];
+#pragma unroll
+                    for (int k = 0; k < 16; ++k) sum = sum + v[k];
+                }
+                for (; t < len; ++t) sum = sum + sc[t];
+            }
+            s_inv[tid] = 1.0f / sum;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int h = 0; h < HPW; ++h) {
+            const float inv = s_inv[h];
+            for (int t = tid; t < len; t += kThreads) {
+                float *e = sc_all + (size_t)h * len + t;
+                *e = *e * inv;
+            }
+        }
+    }
+    __syncthreads();
+    // Σ p·V: thread (dim d, half hf) keeps the chains of heads hf, hf + 2, …
+    constexpr int CH = HPW >= 2 ? HPW / 2 : 1;
+    const int d = tid & 127, hf = tid >> 7;
+    if (HPW >= 2 || hf == 0) {
+        float acc[CH];
+        const float v0 = vh[d];
+#pragma unroll
+        for (int c = 0; c < CH; ++c) acc[c] = sc_all[(size_t)(hf + 2 * c) * len] * v0;
+        int t = 1;
+        for (; t + 32 <= len; t += 32) {  // 32 value rows in flight, added in row order
+            float v[32];
+#pragma unroll
+            for (int k = 0; k < 32; ++k) v[k] = vh[(size_t)(t + k) * kvd + d];
+#pragma unroll
+            for (int k = 0; k < 32; ++k)
+#pragma unroll
+                for (int c = 0; c < CH; ++c) acc[c] = acc[c] + sc_all[(size_t)(hf + 2 * c) * len + t + k] * v[k];
+        }
+        for (; t < len; ++t) {
+            const float v = vh[(size_t)t * kvd + d];
+#pragma unroll
+            for (int c = 0; c < CH; ++c) acc[c] = acc[c] + sc_all[(size_t)(hf + 2 * c) * len + t] * v;
+        }
+#pragma unroll
+        for (int c = 0; c < CH; ++c) out[(size_t)i * out_stride + (size_t)(h0 + hf + 2 * c) * 128 + d] = acc[c];
+    }
 }
 
 }  // namespace pocr
