@@ -30,6 +30,9 @@ constexpr int kHeadMaxVec = 4;  // vectors per launch (two per 16-column B tile)
 #ifndef POCR_HEAD_RB
 #define POCR_HEAD_RB 4
 #endif
+// 12 bytes on a 4-byte boundary: one global_load_dwordx3
+typedef uint32_t U3v __attribute__((ext_vector_type(3), aligned(4)));
+
 constexpr int kHeadRB = POCR_HEAD_RB;  // row blocks (16 rows) per workgroup, a multiple of kWaves
 static_assert(kHeadRB % kWaves == 0, "wave w finishes blocks w, w + 4, …");
 
@@ -149,8 +152,8 @@ __global__ void __launch_bounds__(kThreads) k_head_mfma(HeadParams p) {
     // 2. this wave's weight lines: row block rb, row group g (16/NP rows),
     // line or unit l
     typedef unsigned u4v __attribute__((ext_vector_type(4)));
-    // Q6 pieces: 12 bytes on 4-byte boundaries, three dword loads (a 3-wide
-    // vector type is padded to 16 bytes and could read past the last row)
+    // Q6 pieces: 12 bytes on 4-byte boundaries, one global_load_dwordx3 each
+    // (a 3-vector of dword alignment: 12 bytes read, none past the piece)
     struct U3 {
         uint32_t d[3];
         __device__ __forceinline__ uint32_t operator[](int i) const { return d[i]; }
@@ -172,15 +175,23 @@ __global__ void __launch_bounds__(kThreads) k_head_mfma(HeadParams p) {
 #pragma unroll
                 for (int l = 0; l < LINES; ++l) {
                     if constexpr (Q6) {
-                        const uint32_t *q = reinterpret_cast<const uint32_t *>(row + STRIDE * l);
-#pragma unroll
-                        for (int w = 0; w < 3; ++w) raw[rb][g][l].d[w] = __builtin_nontemporal_load(q + w);
+                        const U3v q = __builtin_nontemporal_load(reinterpret_cast<const U3v *>(row + STRIDE * l));
+                        raw[rb][g][l].d[0] = q.x;
+                        raw[rb][g][l].d[1] = q.y;
+                        raw[rb][g][l].d[2] = q.z;
                     } else {
                         raw[rb][g][l] = __builtin_nontemporal_load(reinterpret_cast<const u4v *>(row + STRIDE * l));
                     }
                 }
             }
     }
+
+    // the row scales the finish needs, requested with the weights (a load at
+    // the finish would add a memory round trip to every workgroup's tail)
+    constexpr int FIN = RB / kWaves;
+    float rsc[FIN];
+#pragma unroll
+    for (int f = 0; f < FIN; ++f) rsc[f] = p.m.scale[min(16 * (rb0 + wave + kWaves * f) + lr, rows - 1)];
 
     // 3. prologue: digits of every vector
     float y[NV][PER_T];
@@ -312,7 +323,6 @@ __global__ void __launch_bounds__(kThreads) k_head_mfma(HeadParams p) {
 
     // 6. wave w finishes blocks w, w + 4, …: lane (row lr, vector lg) adds the
     // halves and the waves' quarters of its three plane sums
-    constexpr int FIN = RB / kWaves;
     const int v = lg;  // lanes of vectors past NV idle
     int b0 = 0, b1 = 0, b2 = 0;
     float sv = sx[0];
@@ -328,7 +338,6 @@ __global__ void __launch_bounds__(kThreads) k_head_mfma(HeadParams p) {
     for (int f = 0; f < FIN; ++f) {
         const int rb = wave + kWaves * f;
         const int r = 16 * (rb0 + rb) + lr;
-        const float rsc = p.m.scale[min(r, rows - 1)];
         if (v < NV) {
             int c0 = 0, c1 = 0, c2 = 0;
 #pragma unroll
@@ -343,7 +352,7 @@ __global__ void __launch_bounds__(kThreads) k_head_mfma(HeadParams p) {
             const float f0 = (float)(c0 - b0);
             const float f1 = (float)(c1 - b1);
             const float f2 = (float)(c2 - b2);
-            const float s = fmaf(f2, 1.0f / 16384.0f, fmaf(f1, 1.0f / 128.0f, f0)) * sv * rsc;
+            const float s = fmaf(f2, 1.0f / 16384.0f, fmaf(f1, 1.0f / 128.0f, f0)) * sv * rsc[f];
             if (r < rows) {
                 if (p.out) p.out[(size_t)v * p.out_stride + r] = s;
                 const unsigned long long k = argmax_key(s, r);
@@ -788,9 +797,10 @@ __global__ void __launch_bounds__(kThreads, 2) k_head_wide_q6(HeadWideParams p) 
         for (int rb = 0; rb < R; ++rb)
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
-                const uint32_t *q = reinterpret_cast<const uint32_t *>(wrow[rb][g] + 192 * u);
-#pragma unroll
-                for (int w = 0; w < 3; ++w) raw[u][rb][g][w] = __builtin_nontemporal_load(q + w);
+                const U3v q = __builtin_nontemporal_load(reinterpret_cast<const U3v *>(wrow[rb][g] + 192 * u));
+                raw[u][rb][g][0] = q.x;
+                raw[u][rb][g][1] = q.y;
+                raw[u][rb][g][2] = q.z;
             }
 #pragma unroll
     for (int k = 0; k < MAXK; ++k) {

@@ -348,11 +348,10 @@ __device__ __forceinline__ void dotp(int code4, const int (&x)[3], int (&a)[3]) 
 
 // six-bit fields of one 24-bit group spread into the four bytes of a dword
 __device__ __forceinline__ int spread6(uint32_t g) {
-    uint32_t r = g & 0x3Fu;
-    r |= (g << 2) & 0x3F00u;
-    r |= (g << 4) & 0x3F0000u;
-    r |= (g << 6) & 0x3F000000u;
-    return (int)r;
+    // fields 0-1 stay in bits 0-11, fields 2-3 move to bits 16-27; then each
+    // 12-bit pair splits into two bytes
+    const uint32_t t = (g & 0xFFFu) | ((g << 4) & 0xFFF0000u);
+    return (int)((t & 0x3F003Fu) | ((t << 2) & 0x3F003F00u));
 }
 
 template <int QT, int CPL, int NPL = 3>
