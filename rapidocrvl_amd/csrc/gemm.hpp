@@ -1193,8 +1193,10 @@ static __global__ void __launch_bounds__(kThreads) k_rope_append(float *qkv, int
 //
 // k_attn_prefill — workgroup: one KV head, 4 query heads of its group (one per
 // wave) and two 16-token tiles, i and NT−1−i, so every workgroup meets the
-// same number of key blocks under the causal mask.  Block images stream
-// HBM → LDS by direct loads through a ring of 3 slots; per block each wave runs
+// same number of key blocks under the causal mask.  Both tiles go in one pass
+// over the longer one's key blocks: each block image is loaded once for both
+// (HBM → LDS by direct loads, two slots of two blocks); per block and tile
+// each wave runs
 //   Sᵀ (keys × tokens) = K · Qᵀ     2 key tiles × 4 dim chunks × 3 MFMAs
 //   online softmax per token column (the column's keys sit in 4 lane groups)
 //   Oᵀ (dims × tokens) += Vᵀ · Pᵀ   8 dim tiles × 3 MFMAs, K index = keys
@@ -1329,154 +1331,177 @@ static __global__ void __launch_bounds__(kPfThreads) k_attn_prefill(const float 
         }
     };
 
-    for (int pass = 0; pass < 2; ++pass) {
-        const int tile = pass == 0 ? (int)blockIdx.y : nt - 1 - (int)blockIdx.y;
-        if (pass == 1 && tile <= (int)blockIdx.y) break;  // uniform
-        const int q0 = tile * kPfTok;
-        const int tq = min(q0 + lr, ntok - 1);    // this lane's token (clamped; stored only if < ntok)
-        const int last_key = clen0 + min(q0 + kPfTok, ntok) - 1;
-        const int my_last = clen0 + tq;
-        const int nblk = last_key / kPfKeys + 1;
-        const int nstage = (nblk + 1) / 2;
+    // the causal pair: tile 0 = blockIdx.y (the shorter), tile 1 = nt − 1 −
+    // blockIdx.y, both in one pass over the longer one's key blocks, so each
+    // block is loaded once and its operands are read from LDS once for both
+    const int tq0 = (int)blockIdx.y, tq1 = nt - 1 - (int)blockIdx.y;
+    const bool pair = tq1 > tq0;                  // uniform; the middle tile of an odd count is alone
+    int q0[2], my_last[2], nblk[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        q0[u] = (u == 0 ? tq0 : tq1) * kPfTok;
+        const int tq = min(q0[u] + lr, ntok - 1);  // this lane's token (clamped; stored only if < ntok)
+        my_last[u] = clen0 + tq;
+        nblk[u] = (clen0 + min(q0[u] + kPfTok, ntok) - 1) / kPfKeys + 1;
+    }
+    const int nblk_all = pair ? nblk[1] : nblk[0];
+    const int nstage = (nblk_all + 1) / 2;
 
-        // Qᵀ operand of the first product: token lr, dims 32c + 8lg + e
-        v8bf qh[4], ql[4];
-        {
-            const float *qs = qkv + (size_t)tq * stride + (size_t)hh * kHD + 8 * lg;
+    // Qᵀ operands of the first product: token lr, dims 32c + 8lg + e
+    v8bf qh[2][4], ql[2][4];
 #pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const float4 a = *reinterpret_cast<const float4 *>(qs + 32 * c);
-                const float4 b = *reinterpret_cast<const float4 *>(qs + 32 * c + 4);
-                const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    for (int u = 0; u < 2; ++u) {
+        const float *qs = qkv + (size_t)min(q0[u] + lr, ntok - 1) * stride + (size_t)hh * kHD + 8 * lg;
 #pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    __bf16 h, lo;
-                    split_bf16(x[e], h, lo);
-                    qh[c][e] = h;
-                    ql[c][e] = lo;
-                }
-            }
-        }
-        v4f o[8];
-#pragma unroll
-        for (int dt = 0; dt < 8; ++dt) o[dt] = v4f{0.f, 0.f, 0.f, 0.f};
-        float m = -INFINITY, lsum = 0.0f;
-
-        auto compute = [&](int b, const uint8_t *slot) {
-            // scores are rounded (s·scale) before the max is subtracted
-#pragma clang fp contract(off)
-            const __bf16 *im = reinterpret_cast<const __bf16 *>(slot);
-            const int k0 = b * kPfKeys;
-            v4f sT[2];
-#pragma unroll
-            for (int kt = 0; kt < 2; ++kt) {
-                sT[kt] = v4f{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int c = 0; c < 4; ++c) {
-                    const v8bf kh = *reinterpret_cast<const v8bf *>(im + pf_k_at(0, 16 * kt + lr, 4 * c + lg));
-                    const v8bf kl = *reinterpret_cast<const v8bf *>(im + pf_k_at(1, 16 * kt + lr, 4 * c + lg));
-                    sT[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, qh[c], sT[kt], 0, 0, 0);
-                    sT[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, ql[c], sT[kt], 0, 0, 0);
-                    sT[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kl, qh[c], sT[kt], 0, 0, 0);
-                }
-            }
-            // online softmax of token column lr (branch-free: masked keys get
-            // p = 0 by selection after an exp of a clamped argument)
-            float sv[8];
-            bool vis[8];
-            float mb = m;
-#pragma unroll
-            for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    vis[4 * kt + i] = k0 + 16 * kt + 4 * lg + i <= my_last;
-                    sv[4 * kt + i] = vis[4 * kt + i] ? sT[kt][i] * scale : -INFINITY;
-                    mb = fmaxf(mb, sv[4 * kt + i]);
-                }
-            mb = groups4_max(mb);
-            // a column may have seen no visible key yet on this parity (mb = −∞):
-            // its p are all 0 and its running sums stay 0
-            const float mx = mb == -INFINITY ? 0.0f : mb;
-            float ps = 0.0f;
-            v8bf ph, pl;
+        for (int c = 0; c < 4; ++c) {
+            const float4 a4 = *reinterpret_cast<const float4 *>(qs + 32 * c);
+            const float4 b4 = *reinterpret_cast<const float4 *>(qs + 32 * c + 4);
+            const float x[8] = {a4.x, a4.y, a4.z, a4.w, b4.x, b4.y, b4.z, b4.w};
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                const float ex = exp_hw(sv[e] - mx);
-                const float p = vis[e] ? ex : 0.0f;
-                ps += p;
-                __bf16 a, c;
-                split_bf16(p, a, c);
-                ph[e] = a;
-                pl[e] = c;
+                __bf16 h, lo;
+                split_bf16(x[e], h, lo);
+                qh[u][c][e] = h;
+                ql[u][c][e] = lo;
             }
-            ps = groups4_sum(ps);
-            // rescale only when a column's maximum moved (exp_hw(0) is exactly
-            // 1, so skipping is exact)
-            if (__builtin_amdgcn_ballot_w64(mb != m)) {
-                const float fe = exp_hw(m - mx);
-                const float f = m == -INFINITY ? 0.0f : fe;
-                lsum *= f;
-#pragma unroll
-                for (int dt = 0; dt < 8; ++dt) o[dt] *= f;
-            }
-            lsum += ps;
-            m = mb;
-#pragma unroll
-            for (int dt = 0; dt < 8; ++dt) {
-                const int d = 16 * dt + lr;
-                const v4bf ah0 = *reinterpret_cast<const v4bf *>(im + pf_v_at(0, d, lg));
-                const v4bf ah1 = *reinterpret_cast<const v4bf *>(im + pf_v_at(0, d, 4 + lg));
-                const v4bf al0 = *reinterpret_cast<const v4bf *>(im + pf_v_at(1, d, lg));
-                const v4bf al1 = *reinterpret_cast<const v4bf *>(im + pf_v_at(1, d, 4 + lg));
-                const v8bf vh = __builtin_shufflevector(ah0, ah1, 0, 1, 2, 3, 4, 5, 6, 7);
-                const v8bf vl = __builtin_shufflevector(al0, al1, 0, 1, 2, 3, 4, 5, 6, 7);
-                o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vh, ph, o[dt], 0, 0, 0);
-                o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vh, pl, o[dt], 0, 0, 0);
-                o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vl, ph, o[dt], 0, 0, 0);
-            }
-        };
-        // stage s: wait for this wave's loads of s, barrier (every wave's loads
-        // of s have landed; every wave is done with s−1, whose buffer takes
-        // s+1), then this wave's block 2s + parity
-        auto body = [&](int s, const uint8_t *cur, uint8_t *next) {
-            wait_vm<0>();
-            lds_barrier();
-            if (s + 1 < nstage) issue(s + 1, nblk, next);
-            const int b = 2 * s + par;
-            if (wave_on && b < nblk) compute(b, cur + par * kPfImage);
-        };
-        lds_barrier();  // the previous tile's stages are read
-        issue(0, nblk, stage0);
-        for (int s = 0; s < nstage; s += 2) {
-            body(s, stage0, stage1);
-            if (s + 1 < nstage) body(s + 1, stage1, stage0);
         }
+    }
+    v4f o[2][8];
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) o[u][dt] = v4f{0.f, 0.f, 0.f, 0.f};
+    float m[2] = {-INFINITY, -INFINITY}, lsum[2] = {0.0f, 0.0f};
 
-        // merge the two parities of each head through LDS (stage0 is free
-        // after the barrier: no loads are in flight)
+    // block b for tile U (a compile-time index, so the tile's registers stay
+    // registers): Sᵀ, the online softmax of token column lr, Oᵀ += Vᵀ·Pᵀ
+    auto compute = [&](int b, const uint8_t *slot, auto tile) {
+        // scores are rounded (s·scale) before the max is subtracted
+#pragma clang fp contract(off)
+        constexpr int U = decltype(tile)::value;
+        const __bf16 *im = reinterpret_cast<const __bf16 *>(slot);
+        const int k0 = b * kPfKeys;
+        v4f sT[2];
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+            sT[kt] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const v8bf kh = *reinterpret_cast<const v8bf *>(im + pf_k_at(0, 16 * kt + lr, 4 * c + lg));
+                const v8bf kl = *reinterpret_cast<const v8bf *>(im + pf_k_at(1, 16 * kt + lr, 4 * c + lg));
+                sT[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, qh[U][c], sT[kt], 0, 0, 0);
+                sT[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, ql[U][c], sT[kt], 0, 0, 0);
+                sT[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kl, qh[U][c], sT[kt], 0, 0, 0);
+            }
+        }
+        // online softmax of token column lr (branch-free: masked keys get
+        // p = 0 by selection after an exp of a clamped argument)
+        float sv[8];
+        bool vis[8];
+        float mb = m[U];
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                vis[4 * kt + i] = k0 + 16 * kt + 4 * lg + i <= my_last[U];
+                sv[4 * kt + i] = vis[4 * kt + i] ? sT[kt][i] * scale : -INFINITY;
+                mb = fmaxf(mb, sv[4 * kt + i]);
+            }
+        mb = groups4_max(mb);
+        // a column may have seen no visible key yet on this parity (mb = −∞):
+        // its p are all 0 and its running sums stay 0
+        const float mx = mb == -INFINITY ? 0.0f : mb;
+        float ps = 0.0f;
+        v8bf ph, pl;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float ex = exp_hw(sv[e] - mx);
+            const float p = vis[e] ? ex : 0.0f;
+            ps += p;
+            __bf16 a, c;
+            split_bf16(p, a, c);
+            ph[e] = a;
+            pl[e] = c;
+        }
+        ps = groups4_sum(ps);
+        // rescale only when a column's maximum moved (exp_hw(0) is exactly
+        // 1, so skipping is exact)
+        if (__builtin_amdgcn_ballot_w64(mb != m[U])) {
+            const float fe = exp_hw(m[U] - mx);
+            const float f = m[U] == -INFINITY ? 0.0f : fe;
+            lsum[U] *= f;
+#pragma unroll
+            for (int dt = 0; dt < 8; ++dt) o[U][dt] *= f;
+        }
+        lsum[U] += ps;
+        m[U] = mb;
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) {
+            const int d = 16 * dt + lr;
+            const v4bf ah0 = *reinterpret_cast<const v4bf *>(im + pf_v_at(0, d, lg));
+            const v4bf ah1 = *reinterpret_cast<const v4bf *>(im + pf_v_at(0, d, 4 + lg));
+            const v4bf al0 = *reinterpret_cast<const v4bf *>(im + pf_v_at(1, d, lg));
+            const v4bf al1 = *reinterpret_cast<const v4bf *>(im + pf_v_at(1, d, 4 + lg));
+            const v8bf vh = __builtin_shufflevector(ah0, ah1, 0, 1, 2, 3, 4, 5, 6, 7);
+            const v8bf vl = __builtin_shufflevector(al0, al1, 0, 1, 2, 3, 4, 5, 6, 7);
+            o[U][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vh, ph, o[U][dt], 0, 0, 0);
+            o[U][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vh, pl, o[U][dt], 0, 0, 0);
+            o[U][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vl, ph, o[U][dt], 0, 0, 0);
+        }
+    };
+    // stage s: wait for this wave's loads of s, barrier (every wave's loads
+    // of s have landed; every wave is done with s−1, whose buffer takes
+    // s+1), then this wave's block 2s + parity
+    auto body = [&](int s, const uint8_t *cur, uint8_t *next) {
+        wait_vm<0>();
         lds_barrier();
-        float *mrg = reinterpret_cast<float *>(stage0) + (size_t)((wave & 3) * 64 + l) * 34;
-        if (par == 1) {
-            mrg[0] = m;
-            mrg[1] = lsum;
+        if (s + 1 < nstage) issue(s + 1, nblk_all, next);
+        const int b = 2 * s + par;
+        if (!wave_on || b >= nblk_all) return;
+        const uint8_t *slot = cur + par * kPfImage;
+        // the shorter tile's keys end at block nblk[0]; the middle tile of an
+        // odd count is tile 0 alone
+        if (b < nblk[0]) compute(b, slot, std::integral_constant<int, 0>{});
+        if (pair) compute(b, slot, std::integral_constant<int, 1>{});
+    };
+    issue(0, nblk_all, stage0);
+    for (int s = 0; s < nstage; s += 2) {
+        body(s, stage0, stage1);
+        if (s + 1 < nstage) body(s + 1, stage1, stage0);
+    }
+
+    // merge the two parities of each head through LDS, tile u in stage u
+    // (free after the barrier: no loads are in flight)
+    lds_barrier();
+    if (par == 1) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            float *mrg = reinterpret_cast<float *>(u == 0 ? stage0 : stage1) + (size_t)((wave & 3) * 64 + l) * 34;
+            mrg[0] = m[u];
+            mrg[1] = lsum[u];
 #pragma unroll
             for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) mrg[2 + 4 * dt + i] = o[dt][i];
+                for (int i = 0; i < 4; ++i) mrg[2 + 4 * dt + i] = o[u][dt][i];
         }
-        lds_barrier();
-        if (par == 0 && wave_on && q0 + lr < ntok) {
+    }
+    lds_barrier();
+    if (par == 0 && wave_on) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            if ((u == 1 && !pair) || q0[u] + lr >= ntok) continue;
+            const float *mrg = reinterpret_cast<const float *>(u == 0 ? stage0 : stage1) + (size_t)((wave & 3) * 64 + l) * 34;
             const float m1 = mrg[0], l1 = mrg[1];
-            const float M = fmaxf(m, m1);  // finite: key 0 is in block 0
-            const float f0 = m == -INFINITY ? 0.0f : exp_hw(m - M);
+            const float M = fmaxf(m[u], m1);  // finite: key 0 is in block 0
+            const float f0 = m[u] == -INFINITY ? 0.0f : exp_hw(m[u] - M);
             const float f1 = m1 == -INFINITY ? 0.0f : exp_hw(m1 - M);
-            const float inv = 1.0f / (lsum * f0 + l1 * f1);
-            float *dst = out + (size_t)(q0 + lr) * out_stride + (size_t)hh * kHD + 4 * lg;
+            const float inv = 1.0f / (lsum[u] * f0 + l1 * f1);
+            float *dst = out + (size_t)(q0[u] + lr) * out_stride + (size_t)hh * kHD + 4 * lg;
 #pragma unroll
             for (int dt = 0; dt < 8; ++dt) {
                 float r[4];
 #pragma unroll
-                for (int i = 0; i < 4; ++i) r[i] = (o[dt][i] * f0 + mrg[2 + 4 * dt + i] * f1) * inv;
+                for (int i = 0; i < 4; ++i) r[i] = (o[u][dt][i] * f0 + mrg[2 + 4 * dt + i] * f1) * inv;
                 *reinterpret_cast<float4 *>(dst + 16 * dt) = make_float4(r[0], r[1], r[2], r[3]);
             }
         }
