@@ -137,3 +137,34 @@ def test_batched_matvec_mfma_shapes(ctx, orc, rng, qtype, m):
         for i in range(m):
             want = orc.matvec(qtype, q.scales, q.packed, x[i])
             assert np.max(np.abs(got[i] - want)) <= 5e-5 * max(1.0, float(np.max(np.abs(want))))
+
+
+@pytest.mark.parametrize("qtype", [Q4, Q6, Q8], ids=["q4", "q6", "q8"])
+def test_prefill_gemm_layouts_agree(ctx, qtype, monkeypatch):
+    """The LDS-ring GEMM reads the digit planes in its tile layout and the
+    weights' tile images; the register-operand GEMM (POCR_PREFILL_GEMM=d)
+    reads row-major planes and weights.  Both sum the same exact int32
+    products, so a prefill gives the same bits either way: logits of the last
+    token and every K/V row."""
+    w = synth.make_weights(MID, qtype, seed=21)
+    gm = lib.Model(ctx, MID)
+    gm.load_weights(w)
+    ids = synth.prompt_ids(45, seed=22, high=MID.vocab)
+    embs = w["embed"][ids]
+    pos = np.array([[p, p, p] for p in range(ids.size)], np.int32)
+
+    def run():
+        s = gm.seq(64)
+        tok, lg = s.prefill(embs, pos, want_logits=True)
+        kv = [s.read_kv(li) for li in range(MID.layers)]
+        s.close()
+        return tok, lg, kv
+
+    tt, lt, kvt = run()
+    monkeypatch.setenv("POCR_PREFILL_GEMM", "d")
+    tr, lr, kvr = run()
+    monkeypatch.delenv("POCR_PREFILL_GEMM")
+    assert tt == tr and np.array_equal(lt, lr)
+    for (a, b), (c, d) in zip(kvt, kvr):
+        assert np.array_equal(a, c) and np.array_equal(b, d)
+    gm.close()
