@@ -22,6 +22,11 @@
 namespace pocr {
 int fail(int code, const char *fmt, ...);
 bool injected(const char *op);
+// greedy decode loop: steps per graph replay, and steps between the host's
+// reads of the step state and tokens (a multiple of the former)
+constexpr int kDecodeGraphSteps = 4;
+constexpr int kDecodeSyncSteps = 16;
+static_assert(kDecodeSyncSteps % kDecodeGraphSteps == 0, "whole graph replays per read-back");
 }  // namespace pocr
 
 #define HIP_TRY(expr)                                                                                     \
@@ -78,6 +83,9 @@ struct pocr_ctx {
     uint8_t *pin = nullptr;
     size_t pin_half = 0;
     hipEvent_t pin_ev[2] = {nullptr, nullptr};
+    // pinned host read-back of the greedy decode loop: the step state and the
+    // tokens of one batch of steps, fetched with one synchronization
+    uint8_t *readback = nullptr;
 };
 
 struct pocr_weight {
@@ -155,8 +163,10 @@ struct pocr_seq {
     pocr::SampleState *samp = nullptr;
     unsigned long long *topk_part = nullptr;  // [kTopKMaxParts][kTopKMax] keys
     DevBuf wide;                              // wide sampler buffers (top_k 0 or > 64)
-    hipGraphExec_t decode_exec = nullptr;
+    hipGraphExec_t decode_exec = nullptr;    // one greedy (or sampled) decode step
     hipGraph_t decode_graph = nullptr;
+    hipGraphExec_t decode_exec_n = nullptr;  // pocr::kDecodeGraphSteps of them in one replay
+    hipGraph_t decode_graph_n = nullptr;
     PrefillBufs pf;
     ~pocr_seq();
 };

@@ -71,6 +71,8 @@ struct StepState {
 // kernels read len, clen, cap and err as one 16-byte load
 static_assert(offsetof(StepState, len) == 0 && offsetof(StepState, clen) == 4 && offsetof(StepState, err) == 12,
               "step state header layout");
+static_assert(offsetof(StepState, eos) % 16 == 0 && kMaxEos % 4 == 0, "the step prologue reads eos[] as int4");
+static_assert(kMaxHalf <= kThreads && kArgSlots <= 64, "the step prologue: one table entry per thread, slots in wave 0");
 
 // ---------------------------------------------------------------------------
 // reference numerics (internal/tensor/ops.go)
@@ -1269,75 +1271,119 @@ static __global__ void __launch_bounds__(kThreads) k_rope(float *q, float *k, co
 // mode 0: h and pos were written by the host.  mode 1: greedy decode — the
 // token is the previous step's argmax, its embedding row is copied into h and
 // the position is next_pos (decode position len(out)-1+ropeDelta, model.go:1695).
+// Everything that does not wait for the chosen token is requested at entry in
+// one round trip (the argmax slots, thread 0's state fields, the position),
+// and the table entry is computed while the slots are reduced; the token's
+// embedding row is requested while thread 0 settles the state.  Results are
+// stored only once the step is known to go ahead.
+constexpr int kStepEmb = 4;  // embedding floats a thread holds across the state barrier
 __device__ __forceinline__ void step_begin_body(StepState *st, const float *embed, float *h, int hidden, int vocab,
                                                 const double *freq, const uint8_t *axis, int mode, int32_t *tokens,
                                                 int max_tokens) {
-    __shared__ int s_tok, s_err, s_pos[3];
+    __shared__ int s_err;
     __shared__ unsigned long long s_key;
-    if (threadIdx.x < 64) {  // wave 0: max over the argmax slots
-        unsigned long long k = st->argmax_slot[threadIdx.x * kSlotPitch];
+    const int t = threadIdx.x;
+    unsigned long long k = 0ull;
+    if (t < kArgSlots) k = st->argmax_slot[t * kSlotPitch];
+    int4 hdr = make_int4(0, 0, 0, 0);  // len, clen, cap, err
+    int n_out = 0, n_eos = 0;
+    const uint32_t *bits = nullptr;
+    int4 eos4[kMaxEos / 4];
+    if (t == 0) {
+        hdr = *reinterpret_cast<const int4 *>(st);
+        n_out = st->n_out;
+        n_eos = st->n_eos;
+        bits = st->eos_bits;
+#pragma unroll
+        for (int i = 0; i < kMaxEos / 4; ++i) eos4[i] = reinterpret_cast<const int4 *>(st->eos)[i];
+    }
+    // this step's position: the decode counter (mode 1) or the host's (mode 0)
+    int pos[3];
+    if (mode == 1) {
+        pos[0] = pos[1] = pos[2] = st->next_pos;
+    } else {
+        pos[0] = st->pos[0];
+        pos[1] = st->pos[1];
+        pos[2] = st->pos[2];
+    }
+    const int half = st->half;  // ≤ kMaxHalf ≤ kThreads: one table entry per thread
+    float ct = 0.0f, sn = 0.0f;
+    if (t < half) {
+        const int a = axis[t];
+        const int p = a == 0 ? pos[0] : (a == 1 ? pos[1] : pos[2]);
+        const double ang = (double)p * freq[t];
+        ct = (float)cos(ang);
+        sn = (float)sin(ang);
+    }
+    if (t < kArgSlots) {  // wave 0: max over the argmax slots
 #pragma unroll
         for (int off = 32; off > 0; off >>= 1) {
             const unsigned long long o = __shfl_xor(k, off, 64);
             k = o > k ? o : k;
         }
-        if (threadIdx.x == 0) s_key = k;
+        if (t == 0) s_key = k;
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
-        int err = st->err;
-        int tok = -1;
-        if (!err && st->len >= st->cap) err = 1;
+    const unsigned long long key = s_key;
+    const int tok = (int)(0xFFFFFFFFu - (uint32_t)(key & 0xFFFFFFFFull));
+    const bool take = mode == 1 && key != 0ull && tok >= 0 && tok < vocab;
+    float e[kStepEmb];
+    if (take) {
+        const float *src = embed + (size_t)tok * hidden;
+#pragma unroll
+        for (int j = 0; j < kStepEmb; ++j) {
+            const int i = t + j * kThreads;
+            e[j] = i < hidden ? src[i] : 0.0f;
+        }
+    }
+    if (t == 0) {
+        int err = hdr.w;
+        if (!err && hdr.x >= hdr.z) err = 1;  // len ≥ cap
         if (!err && mode == 1) {
-            const unsigned long long key = s_key;
             if (key == 0ull) err = 2;
-            tok = (int)(0xFFFFFFFFu - (uint32_t)(key & 0xFFFFFFFFull));
             if (tok < 0 || tok >= vocab) err = 3;
-            if (!err && st->n_out >= max_tokens) err = 4;
+            if (!err && n_out >= max_tokens) err = 4;
             if (!err) {
-                tokens[st->n_out] = tok;
-                st->n_out = st->n_out + 1;
-                const int p = st->next_pos;
-                st->next_pos = p + 1;
-                st->pos[0] = st->pos[1] = st->pos[2] = p;
+                tokens[n_out] = tok;
+                st->n_out = n_out + 1;
+                st->next_pos = pos[0] + 1;
+                st->pos[0] = st->pos[1] = st->pos[2] = pos[0];
                 // the generation loop stops at an EOS token once it is in the
                 // output, before any step for it (model.go:1545-1548)
-                const uint32_t *bits = st->eos_bits;
                 if (bits) {
                     if ((bits[tok >> 5] >> (tok & 31)) & 1u) err = kErrStopped;
                 } else {
-                    const int ne = min(st->n_eos, kMaxEos);
-                    for (int i = 0; i < ne; ++i)
-                        if (st->eos[i] == tok) err = kErrStopped;
+                    const int ne = min(n_eos, kMaxEos);
+                    const int *ev = reinterpret_cast<const int *>(eos4);
+#pragma unroll
+                    for (int i = 0; i < kMaxEos; ++i)
+                        if (i < ne && ev[i] == tok) err = kErrStopped;
                 }
             }
         }
         if (!err) {
-            st->clen = st->len;
-            st->len = st->len + 1;
-            st->has_rope = (st->pos[0] != 0 || st->pos[1] != 0 || st->pos[2] != 0) ? 1 : 0;
+            st->clen = hdr.x;
+            st->len = hdr.x + 1;
+            st->has_rope = (pos[0] != 0 || pos[1] != 0 || pos[2] != 0) ? 1 : 0;
         }
         st->err = err;
         s_err = err;
-        s_tok = tok;
-        s_pos[0] = st->pos[0];
-        s_pos[1] = st->pos[1];
-        s_pos[2] = st->pos[2];
     }
     __syncthreads();
-    if (!s_err && threadIdx.x < kArgSlots) st->argmax_slot[threadIdx.x * kSlotPitch] = 0ull;
+    if (!s_err && t < kArgSlots) st->argmax_slot[t * kSlotPitch] = 0ull;
     if (s_err) return;
-    const int half = st->half;
-    for (int i = threadIdx.x; i < half; i += kThreads) {
-        const int a = axis[i];
-        const int p = a == 0 ? s_pos[0] : (a == 1 ? s_pos[1] : s_pos[2]);
-        const double ang = (double)p * freq[i];
-        st->cos_t[i] = (float)cos(ang);
-        st->sin_t[i] = (float)sin(ang);
+    if (t < half) {
+        st->cos_t[t] = ct;
+        st->sin_t[t] = sn;
     }
     if (mode == 1) {
-        const float *src = embed + (size_t)s_tok * hidden;
-        for (int i = threadIdx.x; i < hidden; i += kThreads) h[i] = src[i];
+#pragma unroll
+        for (int j = 0; j < kStepEmb; ++j) {
+            const int i = t + j * kThreads;
+            if (i < hidden) h[i] = e[j];
+        }
+        const float *src = embed + (size_t)tok * hidden;
+        for (int i = t + kStepEmb * kThreads; i < hidden; i += kThreads) h[i] = src[i];
     }
 }
 

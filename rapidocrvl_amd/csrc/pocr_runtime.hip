@@ -48,9 +48,17 @@ static void free_dev(void *p) {
     if (p) (void)hipFree(p);
 }
 
+static void drop_decode_graphs(pocr_seq *s) {
+    if (s->decode_exec) (void)hipGraphExecDestroy(s->decode_exec);
+    if (s->decode_graph) (void)hipGraphDestroy(s->decode_graph);
+    if (s->decode_exec_n) (void)hipGraphExecDestroy(s->decode_exec_n);
+    if (s->decode_graph_n) (void)hipGraphDestroy(s->decode_graph_n);
+    s->decode_exec = s->decode_exec_n = nullptr;
+    s->decode_graph = s->decode_graph_n = nullptr;
+}
+
 pocr_seq::~pocr_seq() {
-    if (decode_exec) (void)hipGraphExecDestroy(decode_exec);
-    if (decode_graph) (void)hipGraphDestroy(decode_graph);
+    drop_decode_graphs(this);
     free_dev(kv);
     free_dev(h);
     free_dev(qkv);
@@ -132,6 +140,7 @@ void pocr::ctx_release(pocr_ctx *ctx) {
     for (hipEvent_t &e : ctx->pin_ev)
         if (e) (void)hipEventDestroy(e);
     if (ctx->pin) (void)hipHostFree(ctx->pin);
+    if (ctx->readback) (void)hipHostFree(ctx->readback);
     delete ctx;
 }
 
@@ -1905,10 +1914,7 @@ extern "C" int pocr_seq_set_sampling(pocr_seq *s, double temperature, int top_k,
     }
     if (s->sampling != !greedy || (!greedy && s->top_k != top_k)) {
         // the captured step ends in the other LM head: capture again
-        if (s->decode_exec) (void)hipGraphExecDestroy(s->decode_exec);
-        if (s->decode_graph) (void)hipGraphDestroy(s->decode_graph);
-        s->decode_exec = nullptr;
-        s->decode_graph = nullptr;
+        drop_decode_graphs(s);
     }
     s->sampling = !greedy;
     s->temperature = temperature;
@@ -2466,11 +2472,12 @@ extern "C" int pocr_step(pocr_seq *s, const float *emb, const int32_t pos3[3], i
     return step_locked(s, emb, pos3, need_logits, logits, token);
 }
 
-static int build_decode_graph(pocr_seq *s) {
-    if (s->decode_exec) return POCR_OK;
+// `steps` decode steps (mode 1) captured as one graph
+static int capture_decode_steps(pocr_seq *s, int steps, hipGraph_t *graph_out, hipGraphExec_t *exec_out) {
     hipStream_t st = s->m->ctx->stream;
     HIP_TRY(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
-    int rc = enqueue_step(s, 1, true, false);
+    int rc = POCR_OK;
+    for (int i = 0; i < steps && rc == POCR_OK; ++i) rc = enqueue_step(s, 1, true, false);
     hipGraph_t graph = nullptr;
     hipError_t e = hipStreamEndCapture(st, &graph);
     if (rc != POCR_OK) {
@@ -2478,13 +2485,28 @@ static int build_decode_graph(pocr_seq *s) {
         return rc;
     }
     if (e != hipSuccess) return fail(POCR_ERR_DEVICE, "graph capture: %s", hipGetErrorString(e));
-    e = hipGraphInstantiate(&s->decode_exec, graph, nullptr, nullptr, 0);
+    e = hipGraphInstantiate(exec_out, graph, nullptr, nullptr, 0);
     if (e != hipSuccess) {
         (void)hipGraphDestroy(graph);
         return fail(POCR_ERR_DEVICE, "graph instantiate: %s", hipGetErrorString(e));
     }
-    s->decode_graph = graph;
+    *graph_out = graph;
     return POCR_OK;
+}
+
+static int build_decode_graph(pocr_seq *s) {
+    if (s->decode_exec) return POCR_OK;
+    return capture_decode_steps(s, 1, &s->decode_graph, &s->decode_exec);
+}
+
+// The decode loop replays kDecodeGraphSteps steps per graph launch: each
+// launch costs about 5 µs on the device beyond its kernels, against 390 µs
+// per step (capture and instantiation take about 0.25 ms per step, once per
+// sequence).
+static int build_decode_graph_n(pocr_seq *s) {
+    RC(build_decode_graph(s));
+    if (s->decode_exec_n) return POCR_OK;
+    return capture_decode_steps(s, kDecodeGraphSteps, &s->decode_graph_n, &s->decode_exec_n);
 }
 
 static bool is_eos(int32_t t, const int32_t *eos, int n) {
@@ -2557,7 +2579,10 @@ static int decode_locked(pocr_seq *s, int32_t first_token, int32_t first_pos, in
     // (profilers that cannot follow graph launches)
     const char *g_env = getenv("POCR_HIP_GRAPH");
     const bool use_graph = !(g_env && g_env[0] == '0');
-    if (use_graph) RC(build_decode_graph(s));
+    if (use_graph) RC(build_decode_graph_n(s));
+    pocr_ctx *ctx = m->ctx;
+    if (!ctx->readback)
+        HIP_TRY(hipHostMalloc((void **)&ctx->readback, sizeof(StepState) + kDecodeSyncSteps * 4, hipHostMallocDefault));
     StepState hs;
     RC(read_state(s, &hs));
     const int start_len = hs.len;
@@ -2571,24 +2596,34 @@ static int decode_locked(pocr_seq *s, int32_t first_token, int32_t first_pos, in
     HIP_TRY(hipStreamSynchronize(st));  // hs is reused as a read-back target below
     int produced = 0;  // tokens known on the host
     int launched = 0;
-    const int batch = 16;
-    std::vector<int32_t> tok;
     s->device_tokens = 0;
+    StepState *rb_state = reinterpret_cast<StepState *>(ctx->readback);
+    int32_t *rb_tok = reinterpret_cast<int32_t *>(ctx->readback + sizeof(StepState));
     while (launched < steps_needed) {
-        const int n = std::min(batch, steps_needed - launched);
-        for (int i = 0; i < n; ++i) {
-            if (use_graph) HIP_TRY(hipGraphLaunch(s->decode_exec, st));
-            else RC(enqueue_step(s, 1, true, false));
+        const int n = std::min(kDecodeSyncSteps, steps_needed - launched);
+        int i = 0;
+        if (use_graph) {
+            for (; i + kDecodeGraphSteps <= n; i += kDecodeGraphSteps) HIP_TRY(hipGraphLaunch(s->decode_exec_n, st));
+            for (; i < n; ++i) HIP_TRY(hipGraphLaunch(s->decode_exec, st));
+        } else {
+            for (; i < n; ++i) RC(enqueue_step(s, 1, true, false));
         }
         launched += n;
-        RC(read_state(s, &hs));
+        // the state and the tokens this batch can have taken (step j takes
+        // token j at most: tokens [produced, launched)), one synchronization
+        const int span = std::min(launched, s->max_tokens) - produced;
+        if (span > kDecodeSyncSteps) return fail(POCR_ERR_DEVICE, "decode: %d tokens pending", span);
+        HIP_TRY(hipMemcpyAsync(rb_state, s->st, sizeof(StepState), hipMemcpyDeviceToHost, st));
+        if (span > 0)
+            HIP_TRY(hipMemcpyAsync(rb_tok, s->tokens + produced, (size_t)span * 4, hipMemcpyDeviceToHost, st));
+        HIP_TRY(hipStreamSynchronize(st));
+        std::memcpy(&hs, rb_state, sizeof(StepState));
         s->device_tokens = hs.n_out;
         if (state_failed(hs)) return fail(POCR_ERR_DEVICE, "decode: device state error %d", hs.err);
-        tok.resize(hs.n_out);
-        HIP_TRY(hipMemcpy(tok.data(), s->tokens, (size_t)hs.n_out * 4, hipMemcpyDeviceToHost));
-        for (; produced < hs.n_out; ++produced) {
-            out_tokens[produced] = tok[produced];
-            if (is_eos(tok[produced], eos, n_eos)) {
+        if (hs.n_out - produced > span) return fail(POCR_ERR_DEVICE, "decode: %d tokens after %d steps", hs.n_out, launched);
+        for (int j = 0; produced < hs.n_out; ++produced, ++j) {
+            out_tokens[produced] = rb_tok[j];
+            if (is_eos(rb_tok[j], eos, n_eos)) {
                 RC(end_at_eos(s, start_len, produced));
                 return produced + 1;
             }
