@@ -193,8 +193,12 @@ __global__ void __launch_bounds__(kThreads) k_head_mfma(HeadParams p) {
 #pragma unroll
     for (int f = 0; f < FIN; ++f) rsc[f] = p.m.scale[min(16 * (rb0 + wave + kWaves * f) + lr, rows - 1)];
 
-    // 3. prologue: digits of every vector
+    // 3. prologue: digits of every vector.  Only the scale S (the largest
+    // |y|) stands between the activations and the MFMAs; the thread's Σx² and
+    // plane sums wait in registers and are reduced after the MFMAs, in the
+    // same order, before the finish's barrier.
     float y[NV][PER_T];
+    float ssk[NV];
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
         float ss = 0.0f, mx = 0.0f;
@@ -204,33 +208,26 @@ __global__ void __launch_bounds__(kThreads) k_head_mfma(HeadParams p) {
             y[v][i] = norm ? xr[v][i] * nw[i] : xr[v][i];  // a lone product: nothing to contract
             mx = fmaxf(mx, fabsf(y[v][i]));
         }
-        ss = wave_sum(ss);
+        ssk[v] = ss;
         mx = wave_max(mx);
-        if (lane == 0) {
-            redf[0][v][wave] = mx;
-            redf[1][v][wave] = ss;
-        }
+        if (lane == 0) redf[0][v][wave] = mx;
     }
     __syncthreads();
-    int ex[NV];
-    float sx[NV];  // S·(RMSNorm factor): the vector's score scale
+    float sx[NV];  // S, and after the finish's barrier S·(RMSNorm factor): the vector's score scale
+    int sdk[NV][3];
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
-        float m = redf[0][v][0], tot = redf[1][v][0];
+        float m = redf[0][v][0];
 #pragma unroll
-        for (int w = 1; w < kWaves; ++w) {
-            m = fmaxf(m, redf[0][v][w]);
-            tot += redf[1][v][w];
-        }
-        ex[v] = 0;
-        (void)frexpf(m * (1.0f / 127.0f), &ex[v]);  // m/127 < 2^ex; m = 0 → ex = 0
-        const float S = m > 0.0f ? ldexpf(1.0f, ex[v]) : 1.0f;
-        sx[v] = norm ? S * fast_rsqrt_ref(tot / (float)COLS + p.eps) : S;
+        for (int w = 1; w < kWaves; ++w) m = fmaxf(m, redf[0][v][w]);
+        int ex = 0;
+        (void)frexpf(m * (1.0f / 127.0f), &ex);  // m/127 < 2^ex; m = 0 → ex = 0
+        sx[v] = m > 0.0f ? ldexpf(1.0f, ex) : 1.0f;
         int sd[3] = {0, 0, 0};
 #pragma unroll
         for (int i = 0; i < PER_T; ++i) {
             const int c = cb + i;
-            const float t = ldexpf(y[v][i], -ex[v]);  // exact
+            const float t = ldexpf(y[v][i], -ex);  // exact
             const float a = rintf(t);
             const float t1 = (t - a) * 128.0f;        // exact: |t − a| ≤ 1/2
             const float b = rintf(t1);
@@ -244,10 +241,7 @@ __global__ void __launch_bounds__(kThreads) k_head_mfma(HeadParams p) {
             sd[2] += d2;
         }
 #pragma unroll
-        for (int pl = 0; pl < 3; ++pl) {
-            const int s = (int)wave_sum((float)sd[pl]);  // |Σ| ≤ 512·127: exact in f32
-            if (lane == 0) redi[pl][v][wave] = s;
-        }
+        for (int pl = 0; pl < 3; ++pl) sdk[v][pl] = sd[pl];
     }
     __syncthreads();
 
@@ -319,7 +313,28 @@ __global__ void __launch_bounds__(kThreads) k_head_mfma(HeadParams p) {
                 }
             }
         }
+    // the deferred sums: each vector's plane sums (|Σ| ≤ 512·127: exact in
+    // f32) and Σx², per wave
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+#pragma unroll
+        for (int pl = 0; pl < 3; ++pl) {
+            const int s = (int)wave_sum((float)sdk[v][pl]);
+            if (lane == 0) redi[pl][v][wave] = s;
+        }
+        const float ss = wave_sum(ssk[v]);
+        if (lane == 0) redf[1][v][wave] = ss;
+    }
     __syncthreads();
+    if (norm) {
+#pragma unroll
+        for (int v = 0; v < NV; ++v) {
+            float tot = redf[1][v][0];
+#pragma unroll
+            for (int w = 1; w < kWaves; ++w) tot += redf[1][v][w];
+            sx[v] *= fast_rsqrt_ref(tot / (float)COLS + p.eps);
+        }
+    }
 
     // 6. wave w finishes blocks w, w + 4, …: lane (row lr, vector lg) adds the
     // halves and the waves' quarters of its three plane sums
