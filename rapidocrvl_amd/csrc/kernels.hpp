@@ -1783,7 +1783,11 @@ constexpr int kMergeGroups = kMergeThreads / 32;
 
 // Returns false when the step has failed (nothing written).  The merged head
 // (128 floats, 16-byte aligned) goes to dst, by default its head_out slot.
+// B: acc vectors each split group requests up front, 8 (splits < 64 in one
+// round trip) or 16 (< 128; the host picks 16 above 64 splits)
+template <int B = 8>
 __device__ __forceinline__ bool attn_merge_body(AttnParams p, float *dst = nullptr) {
+    static_assert(B == 8 || B == 16, "8 or 16 acc vectors per split group");
     __shared__ float e_lds[kMaxSplits];
     __shared__ float4 o_lds[kMergeGroups][32];
     __shared__ float l_lds;
@@ -1799,29 +1803,35 @@ __device__ __forceinline__ bool attn_merge_body(AttnParams p, float *dst = nullp
     // the step state's header first (len, clen, cap, err; without a step
     // state a readable stand-in), so waiting for it waits for nothing else
     int4 st4 = *reinterpret_cast<const int4 *>(p.st ? reinterpret_cast<const float *>(p.st) : p.part);
-    // then (max, Σexp) of splits lane, lane + 64 (every wave loads them, only
-    // wave 0 uses them: no load inside a branch), then the acc vectors
+    // then (max, Σexp) of split lane (and lane + 64 with B = 16; every wave
+    // loads them, only wave 0 uses them: no load inside a branch), then the
+    // acc vectors of splits sg + 8b, b < B: with B = 16 every record of up to
+    // 128 splits (8,192 rows at 64 rows per split) arrives in one round trip
     const float2 ml = *reinterpret_cast<const float2 *>(base + min(lane, p.nsplit - 1) * RS);
+    float2 ml2 = ml;
+    if constexpr (B == 16) ml2 = *reinterpret_cast<const float2 *>(base + min(lane + 64, p.nsplit - 1) * RS);
     asm volatile("" ::: "memory");
-    constexpr int B = 8;  // acc vectors requested up front (splits sg + 8b)
     float4 av[B];
 #pragma unroll
     for (int b = 0; b < B; ++b) av[b] = acc(min(sg + kMergeGroups * b, p.nsplit - 1));
-    const float m0 = ml.x, l0 = ml.y;
     asm volatile("" : "+v"(st4.x), "+v"(st4.y), "+v"(st4.z), "+v"(st4.w)::"memory");  // requests above, uses below
     if (p.st && st4.w) return false;  // err
     const int L = p.st ? st4.x : p.len;
     const int used = min(p.nsplit, (L + p.chunk - 1) / p.chunk);  // ≥ 1 for L ≥ 1
     if (wave0) {  // split weights, lane s + 64k ↔ split
-        float M = lane < used ? m0 : -INFINITY;
-        for (int s = 64 + lane; s - lane < used; s += 64) M = fmaxf(M, s < used ? base[s * RS] : -INFINITY);
+        // (m, l) of split s: the registers for s < 128, else a load
+        constexpr int HELD = B == 16 ? 128 : 64;  // splits whose (m, l) arrived with the requests above
+        auto ms_of = [&](int s) { return s < 64 ? ml.x : (s < HELD ? ml2.x : base[s * RS]); };
+        auto ls_of = [&](int s) { return s < 64 ? ml.y : (s < HELD ? ml2.y : base[s * RS + 1]); };
+        float M = lane < used ? ml.x : -INFINITY;
+        for (int s = 64 + lane; s - lane < used; s += 64) M = fmaxf(M, s < used ? ms_of(s) : -INFINITY);
         M = wave_max(M);
         float ls = 0.0f;
         for (int s = lane; s - lane < used; s += 64) {
             float e = 0.0f, lv = 0.0f;
             if (s < used) {
-                const float ms = s < 64 ? m0 : base[s * RS];
-                lv = s < 64 ? l0 : base[s * RS + 1];
+                const float ms = ms_of(s);
+                lv = ls_of(s);
                 e = fast_exp_ref(ms - M);
                 e_lds[s] = e;
             }
@@ -1869,11 +1879,14 @@ __global__ void __launch_bounds__(kThreads) k_attn_decode(AttnParams args) {
     pin_args(p);
     attn_decode_body<RPW>(p);
 }
-static __global__ void __launch_bounds__(kMergeThreads) k_attn_merge(AttnParams args) {
+template <int B>
+__global__ void __launch_bounds__(kMergeThreads) k_attn_merge(AttnParams args) {
     AttnParams p = args;
     pin_args(p);
-    attn_merge_body(p);
+    attn_merge_body<B>(p);
 }
+// acc vectors per split group requested up front for nsplit splits
+__host__ __device__ constexpr int merge_prefetch(int nsplit) { return nsplit > 64 ? 16 : 8; }
 
 // ---------------------------------------------------------------------------
 // The merge with o_proj folded in, as a split over heads.  Workgroup (q head
@@ -1893,7 +1906,7 @@ struct OprojParts {
     float *part;   // [heads][rows]
 };
 
-template <int QT>
+template <int QT, int B>
 __global__ void __launch_bounds__(kMergeThreads) k_attn_merge_oproj(AttnParams args, OprojParts op) {
     constexpr int LPROW = 128 / QTraits<QT>::W;  // lanes per row: one chunk each (Q4 4, Q8/Q6 8)
     constexpr int ROWS_PASS = kMergeThreads / LPROW;
@@ -1926,7 +1939,7 @@ __global__ void __launch_bounds__(kMergeThreads) k_attn_merge_oproj(AttnParams a
                                (size_t)(hq * LPROW + j) * QTraits<QT>::CB);
         sc[ps] = op.w.scale[r];
     }
-    if (!attn_merge_body(p, merged)) return;
+    if (!attn_merge_body<B>(p, merged)) return;
     __syncthreads();
     // digit records of the head's 128 values (threads 0..15 hold 8 columns each)
     XRegs xr;
@@ -1980,10 +1993,11 @@ __global__ void __launch_bounds__(kThreads) k_attn_decode_multi(AttnMulti b) {
     attn_decode_body<RPW>(p);
 #endif
 }
-static __global__ void __launch_bounds__(kMergeThreads) k_attn_merge_multi(AttnMulti b) {
+template <int B>
+__global__ void __launch_bounds__(kMergeThreads) k_attn_merge_multi(AttnMulti b) {
     (void)b;
 #if defined(__HIP_DEVICE_COMPILE__)
-    attn_merge_body(((KernargAttn *)__builtin_amdgcn_kernarg_segment_ptr())[blockIdx.z]);
+    attn_merge_body<B>(((KernargAttn *)__builtin_amdgcn_kernarg_segment_ptr())[blockIdx.z]);
 #endif
 }
 

@@ -1365,6 +1365,17 @@ static void attn_shape(AttnParams &a, int cap, int rpw) {
     a.chunk = attn_chunk(cap, a.nsplit, 4 * rpw);
 }
 
+// the split merge with its records requested in one round trip for up to
+// 64 (or, above 64 splits, 128) splits
+static void launch_attn_merge(hipStream_t s, dim3 grid, const AttnParams &a) {
+    if (merge_prefetch(a.nsplit) == 16) hipLaunchKernelGGL(k_attn_merge<16>, grid, dim3(kMergeThreads), 0, s, a);
+    else hipLaunchKernelGGL(k_attn_merge<8>, grid, dim3(kMergeThreads), 0, s, a);
+}
+static void launch_attn_merge_multi(hipStream_t s, dim3 grid, int max_split, const AttnMulti &am) {
+    if (merge_prefetch(max_split) == 16) hipLaunchKernelGGL(k_attn_merge_multi<16>, grid, dim3(kMergeThreads), 0, s, am);
+    else hipLaunchKernelGGL(k_attn_merge_multi<8>, grid, dim3(kMergeThreads), 0, s, am);
+}
+
 static void launch_attn_decode(hipStream_t s, int rpw, dim3 grid, const AttnParams &a) {
     if (rpw == 8) hipLaunchKernelGGL(k_attn_decode<8>, grid, dim3(kThreads), 0, s, a);
     else hipLaunchKernelGGL(k_attn_decode<16>, grid, dim3(kThreads), 0, s, a);
@@ -1404,7 +1415,7 @@ static int text_attention_dev(pocr_ctx *ctx, const float *q, const float *k_cach
         attn_shape(p, cache_len, rpw);
         p.scale = scale;
         launch_attn_decode(s, rpw, dim3(kv_heads, nsplit), p);
-        hipLaunchKernelGGL(k_attn_merge, dim3(heads), dim3(kMergeThreads), 0, s, p);
+        launch_attn_merge(s, dim3(heads), p);
     } else {
         if ((size_t)cache_len * 4 > 60 * 1024) return fail(POCR_ERR_UNSUPPORTED, "text_attention: cache too long");
         hipLaunchKernelGGL(k_attn_small, dim3(heads), dim3(kThreads), (size_t)cache_len * 4, s, ctx->x.as<float>(),
@@ -1528,7 +1539,7 @@ extern "C" int pocr_text_attention_noalloc(pocr_ctx *ctx, const float *q_dev, co
         attn_shape(p, cache_len, rpw);
         p.scale = scale;
         launch_attn_decode(s, rpw, dim3(kv_heads, nsplit), p);
-        hipLaunchKernelGGL(k_attn_merge, dim3(heads), dim3(kMergeThreads), 0, s, p);
+        launch_attn_merge(s, dim3(heads), p);
     } else {
         if ((size_t)cache_len * 4 > 60 * 1024)
             return fail(POCR_ERR_UNSUPPORTED, "pocr_text_attention_noalloc: cache too long for this head shape");
@@ -2109,7 +2120,7 @@ extern "C" int pocr_time_attention(pocr_ctx *ctx, int heads, int kv_heads, int h
         a.kc = ctx->kc.as<float>() + layer * layer_floats;
         a.vc = a.kc + (size_t)cache_len * kvd;
         launch_attn_decode(s, rpw, dim3(kv_heads, nsplit), a);
-        hipLaunchKernelGGL(k_attn_merge, dim3(heads), dim3(kMergeThreads), 0, s, a);
+        launch_attn_merge(s, dim3(heads), a);
     };
     for (int l = 0; l < n_layers; ++l) launch(l);
     HIP_TRY(hipGetLastError());
@@ -2243,10 +2254,20 @@ static bool fused_oproj(const pocr_model *m, const LayerW &L) {
 static int launch_merge_oproj(hipStream_t st, const AttnParams &a, const pocr_weight *wo, float *part, int heads) {
     OprojParts op{dev_mat(wo), part};
     const dim3 grid(heads, kOprojSlices);
+    const bool wide = merge_prefetch(a.nsplit) == 16;
     switch (wo->qtype) {
-    case POCR_Q4: hipLaunchKernelGGL(k_attn_merge_oproj<QT_Q4>, grid, dim3(kMergeThreads), 0, st, a, op); break;
-    case POCR_Q8: hipLaunchKernelGGL(k_attn_merge_oproj<QT_Q8>, grid, dim3(kMergeThreads), 0, st, a, op); break;
-    default: hipLaunchKernelGGL(k_attn_merge_oproj<QT_Q6>, grid, dim3(kMergeThreads), 0, st, a, op); break;
+    case POCR_Q4:
+        if (wide) hipLaunchKernelGGL((k_attn_merge_oproj<QT_Q4, 16>), grid, dim3(kMergeThreads), 0, st, a, op);
+        else hipLaunchKernelGGL((k_attn_merge_oproj<QT_Q4, 8>), grid, dim3(kMergeThreads), 0, st, a, op);
+        break;
+    case POCR_Q8:
+        if (wide) hipLaunchKernelGGL((k_attn_merge_oproj<QT_Q8, 16>), grid, dim3(kMergeThreads), 0, st, a, op);
+        else hipLaunchKernelGGL((k_attn_merge_oproj<QT_Q8, 8>), grid, dim3(kMergeThreads), 0, st, a, op);
+        break;
+    default:
+        if (wide) hipLaunchKernelGGL((k_attn_merge_oproj<QT_Q6, 16>), grid, dim3(kMergeThreads), 0, st, a, op);
+        else hipLaunchKernelGGL((k_attn_merge_oproj<QT_Q6, 8>), grid, dim3(kMergeThreads), 0, st, a, op);
+        break;
     }
     HIP_TRY(hipGetLastError());
     return POCR_OK;
@@ -2330,7 +2351,7 @@ static int enqueue_layer(pocr_seq *s, int li, bool last, bool kv_only) {
         // the reference's summation order (vnni.hpp): the split records are unused
         if (!kv_only) hipLaunchKernelGGL(k_attn_ordered, dim3(c.heads), dim3(kThreads), (size_t)s->cap * 4, st, a);
     } else {
-        hipLaunchKernelGGL(k_attn_merge, dim3(c.heads), dim3(kMergeThreads), 0, st, a);
+        launch_attn_merge(st, dim3(c.heads), a);
     }
     HIP_TRY(hipGetLastError());
     if (kv_only) return POCR_OK;
@@ -2794,7 +2815,7 @@ int batch_layer_wide(DecodeBatch &b, const LayerW &L, int li, bool last, int rpw
     const dim3 ag(c.kv_heads, max_split, b.n);
     if (rpw == 8) hipLaunchKernelGGL(k_attn_decode_multi<8>, ag, dim3(kThreads), 0, st, am);
     else hipLaunchKernelGGL(k_attn_decode_multi<16>, ag, dim3(kThreads), 0, st, am);
-    hipLaunchKernelGGL(k_attn_merge_multi, dim3(c.heads, 1, b.n), dim3(kMergeThreads), 0, st, am);
+    launch_attn_merge_multi(st, dim3(c.heads, 1, b.n), max_split, am);
     HIP_TRY(hipGetLastError());
     // 3. o_proj + residual (+ the Q4/Q6 behaviour by each sequence's clen)
     const pocr_weight *wo = L.w[POCR_W_O];
@@ -2889,7 +2910,7 @@ int enqueue_batch_step(DecodeBatch &b) {
         const dim3 ag(c.kv_heads, max_split, b.n);
         if (rpw == 8) hipLaunchKernelGGL(k_attn_decode_multi<8>, ag, dim3(kThreads), 0, st, am);
         else hipLaunchKernelGGL(k_attn_decode_multi<16>, ag, dim3(kThreads), 0, st, am);
-        hipLaunchKernelGGL(k_attn_merge_multi, dim3(c.heads, 1, b.n), dim3(kMergeThreads), 0, st, am);
+        launch_attn_merge_multi(st, dim3(c.heads, 1, b.n), max_split, am);
         HIP_TRY(hipGetLastError());
         // 3. o_proj + residual (+ the Q4/Q6 behaviour per sequence)
         const pocr_weight *wo = L.w[POCR_W_O];
