@@ -121,6 +121,35 @@ def test_generate_token_stream(orc, ctx, qtype):
     assert list(got2) == list(want)
 
 
+def test_decode_lengths_across_graph_replays(orc, ctx):
+    """The greedy loop replays four token steps per graph launch and reads
+    the state back every 16 steps, with single-step replays for the rest:
+    every length from 1 to 40 tokens (ends inside a four-step replay, at a
+    read-back, one past it) and an EOS inside a replay give the oracle's
+    stream, and the cache keeps exactly the rows of the tokens before the
+    stop (a second decode continues the oracle's stream)."""
+    w, om, gm = _pair(orc, ctx, MID, Q4)
+    ids = synth.prompt_ids(11, seed=31, high=MID.vocab)
+    want = list(om.generate(ids, 40, eos=()))
+    s = gm.seq(64)
+    for n in (1, 2, 3, 4, 5, 7, 8, 15, 16, 17, 18, 20, 31, 33, 40):
+        s.reset()
+        assert list(s.generate(ids, n, eos=())) == want[:n], n
+    for k in (2, 6, 13, 17):  # EOS as the (k+1)-th token: mid-replay and past a read-back
+        eos = want[k]
+        if eos in want[:k]:
+            continue
+        s.reset()
+        got = list(s.generate(ids, 40, eos=(eos,)))
+        assert got == want[:k + 1], k
+        # the stop keeps the rows of the tokens before it: decoding on from the
+        # EOS token continues the oracle's stream
+        more = list(s.decode_greedy(eos, len(ids) + k, 6, eos=()))
+        assert more == want[k:k + 6], k
+    s.close()
+    gm.close()
+
+
 def test_generate_eos(orc, ctx):
     w, om, gm = _pair(orc, ctx, MID, Q4)
     ids = synth.prompt_ids(8, seed=9, high=MID.vocab)
