@@ -285,7 +285,9 @@ int pocr_model_set_norm(pocr_model *m, int layer, int role, const float *w);
 /* copies the f32 embed_tokens table [vocab][hidden] to HBM */
 int pocr_model_set_embed(pocr_model *m, const float *embed);
 /* reproduce the reference's Q4/Q6 attention-residual behaviour
- * (internal/model/model.go:3895-3902, 4051-4057); default on */
+ * (internal/model/model.go:3895-3902, 4051-4057); default on.  Set it before
+ * the model's first sequence: changing it while sequences exist returns
+ * POCR_ERR_ARG (their captured decode graphs hold the rule). */
 int pocr_model_set_residual_quirk(pocr_model *m, int on);
 /* Every Q4/Q6 matvec of the model's decode steps and LM head in the VNNI
  * activation mode above, as the reference's CPU path runs on an

@@ -1756,9 +1756,14 @@ extern "C" int pocr_model_load_gguf(pocr_ctx *ctx, const pocr_config *cfg, const
     return POCR_OK;
 }
 
+// Fixed once the model has sequences, like the activation mode: their
+// captured decode graphs hold the o_proj epilogue's residual rule.
 extern "C" int pocr_model_set_residual_quirk(pocr_model *m, int on) {
     if (!m) return fail(POCR_ERR_ARG, "pocr_model_set_residual_quirk: null model");
-    m->quirk = on ? 1 : 0;
+    const int q = on ? 1 : 0;
+    if (q != m->quirk && m->refs.load() != 1)
+        return fail(POCR_ERR_ARG, "pocr_model_set_residual_quirk: set the behaviour before creating sequences");
+    m->quirk = q;
     return POCR_OK;
 }
 

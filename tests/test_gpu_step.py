@@ -287,6 +287,23 @@ def test_generate_with_image(orc, ctx, qtype):
     assert list(got) == list(want)
 
 
+def test_residual_rule_fixed_once_sequences_exist(ctx):
+    """A sequence's captured decode graphs hold the o_proj epilogue's residual
+    rule, so the model refuses to change it while sequences exist (setting
+    the value it already has is fine) and accepts it again once they are
+    closed."""
+    gm = lib.Model(ctx, TINY)
+    gm.load_weights(synth.make_weights(TINY, Q4, seed=3))
+    gm.set_residual_quirk(False)
+    s = gm.seq(16)
+    gm.set_residual_quirk(False)
+    with pytest.raises(lib.PocrError):
+        gm.set_residual_quirk(True)
+    s.close()
+    gm.set_residual_quirk(True)
+    gm.close()
+
+
 def test_capacity_is_enforced(ctx):
     w = synth.make_weights(TINY, Q4, seed=1)
     gm = lib.Model(ctx, TINY)
