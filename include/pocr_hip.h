@@ -278,7 +278,11 @@ int pocr_time_stream_read(pocr_ctx *ctx, int64_t bytes, int n_buffers, int iters
 /* ---------------- model / step level (device-resident) ---------------- */
 int pocr_model_create(pocr_ctx *ctx, const pocr_config *cfg, pocr_model **out);
 void pocr_model_destroy(pocr_model *m);
-/* borrow an uploaded weight; layer -1 with POCR_W_LM_HEAD for the head */
+/* borrow an uploaded weight; layer -1 with POCR_W_LM_HEAD for the head.
+ * Set the matrices before the model's first sequence: while sequences exist
+ * this returns POCR_ERR_ARG (their captured decode graphs hold the weights'
+ * device addresses).  Norms and the embedding table may be rewritten any time
+ * (in place). */
 int pocr_model_set_weight(pocr_model *m, int layer, int role, const pocr_weight *w);
 /* copies hidden floats to HBM; layer -1 with POCR_N_FINAL for the final norm */
 int pocr_model_set_norm(pocr_model *m, int layer, int role, const float *w);

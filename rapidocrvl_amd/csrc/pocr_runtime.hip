@@ -1632,9 +1632,13 @@ void pocr::model_release(pocr_model *m) {
 
 extern "C" void pocr_model_destroy(pocr_model *m) { model_release(m); }
 
+// Matrices are fixed once the model has sequences: their captured decode
+// graphs hold the weights' device addresses (a replaced weight may be freed).
 extern "C" int pocr_model_set_weight(pocr_model *m, int layer, int role, const pocr_weight *w) {
     if (!m || !w) return fail(POCR_ERR_ARG, "pocr_model_set_weight: null argument");
     if (w->ctx != m->ctx) return fail(POCR_ERR_ARG, "pocr_model_set_weight: weight from another context");
+    if (m->refs.load() != 1)
+        return fail(POCR_ERR_ARG, "pocr_model_set_weight: set the weights before creating sequences");
     const pocr_config &c = m->cfg;
     const int q_rows = c.heads * c.head_dim, kv_rows = c.kv_heads * c.head_dim;
     if (layer == -1 && role == POCR_W_LM_HEAD) {

@@ -287,11 +287,11 @@ def test_generate_with_image(orc, ctx, qtype):
     assert list(got) == list(want)
 
 
-def test_residual_rule_fixed_once_sequences_exist(ctx):
+def test_residual_rule_and_weights_fixed_once_sequences_exist(ctx):
     """A sequence's captured decode graphs hold the o_proj epilogue's residual
-    rule, so the model refuses to change it while sequences exist (setting
-    the value it already has is fine) and accepts it again once they are
-    closed."""
+    rule and the weights' device addresses, so the model refuses to change
+    either while sequences exist (setting the rule it already has is fine)
+    and accepts both again once they are closed."""
     gm = lib.Model(ctx, TINY)
     gm.load_weights(synth.make_weights(TINY, Q4, seed=3))
     gm.set_residual_quirk(False)
@@ -299,8 +299,12 @@ def test_residual_rule_fixed_once_sequences_exist(ctx):
     gm.set_residual_quirk(False)
     with pytest.raises(lib.PocrError):
         gm.set_residual_quirk(True)
+    # the matrices likewise (a replaced weight could be freed under the graphs)
+    with pytest.raises(lib.PocrError):
+        gm.load_weights(synth.make_weights(TINY, Q4, seed=4))
     s.close()
     gm.set_residual_quirk(True)
+    gm.load_weights(synth.make_weights(TINY, Q4, seed=4))
     gm.close()
 
 
