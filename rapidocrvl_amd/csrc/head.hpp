@@ -70,6 +70,41 @@ constexpr int head_steps_per_load() { return QT == QT_Q4 ? 2 : 1; }
 // parts (Q6)
 template <int QT>
 constexpr int head_parts() { return QT == QT_Q6 ? 4 : 2; }
+// Q6 head image.  The 12-byte pieces of a 192-byte unit straddle 128-byte
+// lines (a wave's unit shares lines with its neighbours'), which streams at
+// about 0.9 of whole lines.  So Q6 matrices of LM-head size also keep their
+// rows in the load order of the heads: unit (b, w, g, l) — block b of 16
+// rows, column quarter w, row group g (rows 16b + 4g … + 3), unit l of the
+// quarter — is 768 consecutive bytes at ((4b + w)·4 + g)·LINES + l times 768,
+// slot L (= lr + 16·lg) holding what lane L of k_head_mfma loads: the 12
+// bytes at w·row_bytes/4 + 192·l + 48·(lr/4) + 12·lg of row 16b + 4g + lr%4
+// (rows past the end: the last row).  nblk = ⌈rows/16⌉ blocks, nblk·16 rows
+// of bytes in all.
+__device__ __forceinline__ size_t head_img_unit_q6(int b, int w, int g, int l, int lines) {
+    return ((((size_t)b * kWaves + w) * 4 + g) * lines + l) * 768;
+}
+
+// one thread per (unit, slot): 3 dwords
+static __global__ void __launch_bounds__(kThreads) k_head_image_q6(const uint8_t *src, int row_bytes, int rows,
+                                                                 int nblk, uint8_t *dst) {
+    const int lines = row_bytes / 768;
+    const size_t id = (size_t)blockIdx.x * kThreads + threadIdx.x;
+    const size_t units = (size_t)nblk * 16 * lines;
+    if (id >= units * 64) return;
+    const int L = (int)(id % 64);
+    const size_t u = id / 64;
+    const int l = (int)(u % lines), g = (int)(u / lines % 4), w = (int)(u / lines / 4 % kWaves);
+    const int b = (int)(u / lines / 4 / kWaves);
+    const int lr = L & 15, lg = L >> 4;
+    const int r = min(16 * b + 4 * g + (lr & 3), rows - 1);
+    const uint32_t *s = reinterpret_cast<const uint32_t *>(src + (size_t)r * row_bytes + w * (row_bytes / 4) + 192 * l +
+                                                           48 * (lr >> 2) + 12 * lg);
+    uint32_t *d = reinterpret_cast<uint32_t *>(dst + head_img_unit_q6(b, w, g, l, lines) + 12 * L);
+    d[0] = s[0];
+    d[1] = s[1];
+    d[2] = s[2];
+}
+
 // first column (relative to the wave's quarter) of step h of line ℓ, half hb,
 // lane group lg: 16 columns in the MFMA K order (digit_pos16)
 template <int QT>
@@ -116,6 +151,7 @@ __global__ void __launch_bounds__(kThreads) k_head_mfma(HeadParams p) {
     // every kernel argument live up front: one kernel-argument round trip
     asm volatile("" ::"s"(p.m.data), "s"(p.m.scale), "s"(p.x), "s"(p.norm_w), "s"(p.out), "s"(p.rows),
                  "s"(p.m.row_bytes), "s"(p.x_stride), "s"(p.out_stride), "s"(p.eps));
+    if constexpr (QT == QT_Q6) asm volatile("" ::"s"(p.m.head_img));
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -165,6 +201,7 @@ __global__ void __launch_bounds__(kThreads) k_head_mfma(HeadParams p) {
         const int qbyte = Q6 ? kbeg / 4 * 3 : (QT == QT_Q4 ? kbeg / 2 : kbeg);
         const int lb = Q6 ? 48 * (lr >> 2) + 12 * lg : 64 * (lr >> 3) + 16 * lg;
         constexpr int STRIDE = Q6 ? 192 : 128;
+        const int nblk = (rows + 15) / 16;
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
@@ -175,7 +212,12 @@ __global__ void __launch_bounds__(kThreads) k_head_mfma(HeadParams p) {
 #pragma unroll
                 for (int l = 0; l < LINES; ++l) {
                     if constexpr (Q6) {
-                        const U3v q = __builtin_nontemporal_load(reinterpret_cast<const U3v *>(row + STRIDE * l));
+                        // the same 12 bytes from the head image when there is one
+                        const uint8_t *src =
+                            p.m.head_img ? p.m.head_img + head_img_unit_q6(min(rb0 + rb, nblk - 1), wave, g, l, LINES) +
+                                               12 * lane
+                                         : row + STRIDE * l;
+                        const U3v q = __builtin_nontemporal_load(reinterpret_cast<const U3v *>(src));
                         raw[rb][g][l].d[0] = q.x;
                         raw[rb][g][l].d[1] = q.y;
                         raw[rb][g][l].d[2] = q.z;
@@ -765,7 +807,7 @@ __global__ void __launch_bounds__(kThreads, 2) k_head_wide_q6(HeadWideParams p) 
     constexpr int TRW = 49;           // dwords per row of the transpose tile (48 + 1 pad)
     constexpr int NV = kHeadWideVec;
     static_assert(R >= 1, "at least one block of 16 rows per wave");
-    static_assert(STEPS % 4 == 0, "whole 192-byte units");
+    static_assert(STEPS % 16 == 0, "whole 192-byte units in every column quarter");
     static_assert(SH::PLANE_BYTES % (16 * NV) == 0, "planes in 16-vector groups of 16 bytes");
     __shared__ __attribute__((aligned(16))) int8_t xdig[SH::PLANE_BYTES];
     __shared__ uint32_t tr[kWaves][R][16][TRW];
@@ -797,9 +839,15 @@ __global__ void __launch_bounds__(kThreads, 2) k_head_wide_q6(HeadWideParams p) 
 
     // 2. every weight byte of the wave's rows (past the end: the last row,
     // loaded and never scored), unit by unit in the order the MFMAs consume
-    // them: row group g of block rb is rows 16rb + 4g + L/16
+    // them: row group g of block rb is rows 16rb + 4g + L/16.  With a head
+    // image, lane L's piece L%16 of row L/16 sits in slot 4·(k/4) + L/16 +
+    // 16·(k%4), k = L%16, of the unit (k_head_mfma's lane order)
     uint32_t raw[UNITS][R][4][3];
     const uint8_t *wrow[R][4];
+    const bool img = p.m.head_img != nullptr;  // uniform
+    constexpr int LINES = UNITS / 4;           // units per column quarter
+    const int nblk = (rows + 15) / 16;
+    const int slot = 4 * ((lane & 15) >> 2) + (lane >> 4) + 16 * (lane & 3);
 #pragma unroll
     for (int rb = 0; rb < R; ++rb)
 #pragma unroll
@@ -812,7 +860,11 @@ __global__ void __launch_bounds__(kThreads, 2) k_head_wide_q6(HeadWideParams p) 
         for (int rb = 0; rb < R; ++rb)
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
-                const U3v q = __builtin_nontemporal_load(reinterpret_cast<const U3v *>(wrow[rb][g] + 192 * u));
+                const uint8_t *src =
+                    img ? p.m.head_img + head_img_unit_q6(min(r0 / 16 + rb, nblk - 1), u / LINES, g, u % LINES, LINES) +
+                              12 * slot
+                        : wrow[rb][g] + 192 * u;
+                const U3v q = __builtin_nontemporal_load(reinterpret_cast<const U3v *>(src));
                 raw[u][rb][g][0] = q.x;
                 raw[u][rb][g][1] = q.y;
                 raw[u][rb][g][2] = q.z;

@@ -98,6 +98,7 @@ struct pocr_weight {
     const uint8_t *data = nullptr;
     uint8_t *tiled = nullptr;  // the prefill GEMM's copy in its load order, when weight_tiles_ok
     int *usum = nullptr;       // Q4/Q6 with a tile image: Σ of each row's stored codes (row_usum)
+    uint8_t *head_img = nullptr;  // Q6 heads: the rows in the head kernels' load order, when head_image_ok
 };
 
 struct LayerW {

@@ -29,6 +29,7 @@ struct DevMat {
     const uint8_t *data;   // rows * row_bytes, 256-byte aligned base
     const uint8_t *tiled;  // the same bytes in the prefill GEMM's operand order (k_tile_weight), or null
     const int *usum;       // Q4/Q6 with a tile image: Σ of the row's stored codes (k_row_usum), else null
+    const uint8_t *head_img;  // Q6 LM-head-sized rows in the greedy head's load order (k_head_image_q6), or null
     int rows;
     int cols;
     int row_bytes;

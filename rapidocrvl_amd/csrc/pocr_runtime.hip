@@ -174,6 +174,21 @@ extern "C" void pocr_ctx_destroy(pocr_ctx *ctx) { ctx_release(ctx); }
 // ---------------------------------------------------------------------------
 static bool valid_qtype(int q) { return q == POCR_Q8 || q == POCR_Q4 || q == POCR_Q6; }
 
+// Q6 matrices of LM-head size (the shapes the greedy heads take) also keep
+// their rows in the heads' load order (head.hpp, k_head_image_q6)
+static bool head_image_ok(int qtype, int rows, int cols) {
+    return qtype == POCR_Q6 && (cols == 1024 || cols == 2048) && rows >= kHeadWideMinRows;
+}
+static size_t head_image_bytes(int rows, size_t row_bytes) { return (size_t)(rows + 15) / 16 * 16 * row_bytes; }
+static int head_image_q6(hipStream_t s, const uint8_t *src, int row_bytes, int rows, uint8_t *dst) {
+    const int nblk = (rows + 15) / 16;
+    const size_t threads = (size_t)nblk * 16 * (row_bytes / 768) * 64;
+    hipLaunchKernelGGL(k_head_image_q6, dim3((unsigned)((threads + kThreads - 1) / kThreads)), dim3(kThreads), 0, s, src,
+                       row_bytes, rows, nblk, dst);
+    HIP_TRY(hipGetLastError());
+    return POCR_OK;
+}
+
 extern "C" int pocr_weight_upload(pocr_ctx *ctx, int qtype, int rows, int cols, const float *scales,
                                   const uint8_t *packed, pocr_weight **out) {
     if (!ctx || !out || !scales || !packed) return fail(POCR_ERR_ARG, "pocr_weight_upload: null argument");
@@ -197,8 +212,21 @@ extern "C" int pocr_weight_upload(pocr_ctx *ctx, int qtype, int rows, int cols, 
     }
     // the prefill GEMM's image of the same bytes (k_tile_weight), and for Q4/Q6
     // the rows' code sums of its VNNI mode
-    uint8_t *tiled = nullptr;
+    uint8_t *tiled = nullptr, *head_img = nullptr;
     int *usum = nullptr;
+    if (head_image_ok(qtype, rows, cols)) {
+        e = hipMalloc(&head_img, head_image_bytes(rows, rb));
+        int rc = e == hipSuccess ? POCR_OK : fail(POCR_ERR_DEVICE, "weight head image: %s", hipGetErrorString(e));
+        if (rc == POCR_OK)
+            rc = head_image_q6(ctx->stream, (const uint8_t *)base + scale_bytes, (int)rb, rows, head_img);
+        if (rc == POCR_OK && (e = hipStreamSynchronize(ctx->stream)) != hipSuccess)
+            rc = fail(POCR_ERR_DEVICE, "weight head image: %s", hipGetErrorString(e));
+        if (rc != POCR_OK) {
+            free_dev(head_img);
+            (void)hipFree(base);
+            return rc;
+        }
+    }
     if (weight_tiles_ok(rows, cols)) {
         const uint8_t *src = (const uint8_t *)base + scale_bytes;
         e = hipMalloc(&tiled, data_bytes);
@@ -211,6 +239,7 @@ extern "C" int pocr_weight_upload(pocr_ctx *ctx, int qtype, int rows, int cols, 
         if (rc != POCR_OK) {
             free_dev(usum);
             free_dev(tiled);
+            free_dev(head_img);
             (void)hipFree(base);
             return rc;
         }
@@ -227,6 +256,7 @@ extern "C" int pocr_weight_upload(pocr_ctx *ctx, int qtype, int rows, int cols, 
     w->data = (const uint8_t *)base + scale_bytes;
     w->tiled = tiled;
     w->usum = usum;
+    w->head_img = head_img;
     *out = w;
     return POCR_OK;
 }
@@ -246,6 +276,7 @@ void pocr::weight_release(const pocr_weight *cw) {
         free_dev(w->base);
         free_dev(w->tiled);
         free_dev(w->usum);
+        free_dev(w->head_img);
     }
     delete w;
     ctx_release(ctx);
@@ -259,6 +290,7 @@ DevMat pocr::dev_mat(const pocr_weight *w) {
     m.data = w->data;
     m.tiled = w->tiled;
     m.usum = w->usum;
+    m.head_img = w->head_img;
     m.rows = w->rows;
     m.cols = w->cols;
     m.row_bytes = (int)w->row_bytes;

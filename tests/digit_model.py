@@ -84,10 +84,10 @@ def head_scores(codes, scales, x, rows_per_block=8192):
 def head_scores_rows(codes, scales, X):
     """head_scores for every row of X at once: ([m, rows], [m, rows]).  The
     integer plane sums are formed in f32, exact while |Σ| < 2^24 (codes ≤ 128
-    in magnitude, digits ≤ 127, 1024 columns)."""
+    in magnitude, digits ≤ 127, 1024 columns; Q6 codes ≤ 32 also at 2048)."""
     X = np.asarray(X, np.float32)
     m, cols = X.shape
-    assert cols <= 1024
+    assert int(np.abs(codes).max()) * 127 * cols < 2 ** 24
     S = np.zeros(m)
     D = np.zeros((cols, 3 * m), np.float32)
     for i in range(m):

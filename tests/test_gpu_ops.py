@@ -205,6 +205,35 @@ def test_lm_head_rows_q6(ctx, orc, m):
         assert exact[best] - exact[idx] <= dev[best] + dev[idx] + f32b[best] + f32b[idx], i
 
 
+@pytest.mark.parametrize("cols", [1024, 2048])
+@pytest.mark.parametrize("m", [1, 5])
+def test_q6_head_image_ragged_rows(ctx, orc, cols, m):
+    """Q6 matrices of LM-head size are read through the head image (rows in
+    the heads' load order, built at upload).  16,421 rows leave a partial last
+    block of 16 and a partial last workgroup of blocks: every row's scores are
+    the digit model's up to the f32 steps and within the oracle's f32 bar, and
+    every vector's greedy pick is that of the one-vector head, to the bit."""
+    rows = 16421
+    rng = np.random.default_rng(cols + m)
+    q = _qmat(rng, rows, cols, Q6)
+    w = ctx.upload(q)
+    codes = lib.unpack_rows(Q6, q.packed, q.cols)
+    x = rng.standard_normal((m, cols)).astype(np.float32)
+    if m > 1:
+        x[1] *= np.float32(1e-3)
+    got = ctx.matvec(w, x if m > 1 else x[0])
+    got = got.reshape(m, rows)
+    dig, mag = dm.head_scores_rows(codes, q.scales, x)
+    for i in range(m):
+        _close(got[i], orc.matvec(Q6, q.scales, q.packed, x[i]))
+        assert np.all(np.abs(got[i] - dig[i]) <= F32_STEPS[Q6] * mag[i]), i
+        idx, score = ctx.matvec_argmax(w, x[i])
+        assert int(np.argmax(got[i])) == idx, i
+        assert got[i][idx] == np.float32(score), i
+    # the last rows (the partial block) are scored like every other row
+    assert np.all(np.isfinite(got[:, -5:]))
+
+
 def test_argmax_ties_pick_lowest_index(ctx):
     # identical rows give bit-identical scores: ties → lowest index
     w = np.zeros((64, 32), np.float32)
