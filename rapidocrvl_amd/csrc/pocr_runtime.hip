@@ -214,11 +214,13 @@ extern "C" int pocr_weight_upload(pocr_ctx *ctx, int qtype, int rows, int cols, 
     // the rows' code sums of its VNNI mode
     uint8_t *tiled = nullptr, *head_img = nullptr;
     int *usum = nullptr;
-    if (head_image_ok(qtype, rows, cols)) {
-        e = hipMalloc(&head_img, head_image_bytes(rows, rb));
-        int rc = e == hipSuccess ? POCR_OK : fail(POCR_ERR_DEVICE, "weight head image: %s", hipGetErrorString(e));
-        if (rc == POCR_OK)
-            rc = head_image_q6(ctx->stream, (const uint8_t *)base + scale_bytes, (int)rb, rows, head_img);
+    // the image is an optional copy: without room for it the heads read the rows
+    if (head_image_ok(qtype, rows, cols) && hipMalloc(&head_img, head_image_bytes(rows, rb)) != hipSuccess) {
+        (void)hipGetLastError();
+        head_img = nullptr;
+    }
+    if (head_img) {
+        int rc = head_image_q6(ctx->stream, (const uint8_t *)base + scale_bytes, (int)rb, rows, head_img);
         if (rc == POCR_OK && (e = hipStreamSynchronize(ctx->stream)) != hipSuccess)
             rc = fail(POCR_ERR_DEVICE, "weight head image: %s", hipGetErrorString(e));
         if (rc != POCR_OK) {
