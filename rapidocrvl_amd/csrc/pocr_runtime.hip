@@ -2722,6 +2722,10 @@ extern "C" int pocr_decode_greedy(pocr_seq *s, int32_t first_token, int32_t firs
 // ---------------------------------------------------------------------------
 namespace {
 
+// greedy sequences from which the LM head takes the digit-plane launch and the
+// 16-vector head (k_head_digits + k_head_wide) instead of a 4-vector pass
+constexpr int kBatchWideHeadMin = 3;
+
 struct DecodeBatch {
     pocr_model *m = nullptr;
     int n = 0;    // sequences: the ng greedy ones first, then the sampling ones
@@ -2731,8 +2735,9 @@ struct DecodeBatch {
     pocr_seq *seq[kMaxBatch] = {};
     float *h = nullptr, *v = nullptr, *qkv = nullptr, *ho = nullptr, *g = nullptr;
     StepState *pad = nullptr;  // step state of the padding vectors
-    // wide step (n > 4): digit planes of 16 rows, row scales and sums, and the
-    // rows' step states (the o_proj epilogue reads each sequence's clen)
+    // digit planes of 16 rows, row scales and sums (the wide step, n > 4, and
+    // the wide LM head from kBatchWideHeadMin rows), and the wide step's row
+    // step states (the o_proj epilogue reads each sequence's clen)
     int8_t *xd = nullptr;
     float *xs = nullptr;
     int *xb = nullptr;
@@ -2986,12 +2991,15 @@ int enqueue_batch_step(DecodeBatch &b) {
         RC(gemv_launch(st, d, 1, PRO_COPY, EPI_DOWN, kBigGrid, b.nv, &q));
     }
     // LM head on RMSNorm(v)·final_norm.  Greedy sequences: argmax into each
-    // one's state — more than 4 of them (and a vocabulary in 16-row blocks):
-    // digit planes, the small MFMA GEMM into logits rows and a per-row argmax;
-    // otherwise one GEMV pass per 4 of them (the last pass padded to 1, 2 or 4
-    // vectors).  Sampling sequences: each its own logits, top-k and draw (the
-    // draw lands in argmax slot 0, where the next step reads it).
-    if (wide && b.ng > kMaxNV && head_wide_ok(m->lm)) {
+    // one's state — from kBatchWideHeadMin of them and a head the wide kernels
+    // take: one digit-plane launch and one 16-vector head for all; more than 4
+    // of them otherwise (and a vocabulary in 16-row blocks): digit planes, the
+    // small MFMA GEMM into logits rows and a per-row argmax; otherwise one GEMV
+    // pass per 4 of them (the last pass padded to 1, 2 or 4 vectors).
+    // Sampling sequences: each its own logits, top-k and draw (the draw lands
+    // in argmax slot 0, where the next step reads it).
+    const bool head_wide = b.ng >= kBatchWideHeadMin && b.xd && head_wide_ok(m->lm);
+    if (head_wide) {
         // one launch for every greedy sequence (rows 0..ng-1 of v)
         StepState *sts[kHeadWideVec];
         for (int i = 0; i < b.ng; ++i) sts[i] = b.seq[i]->st;
@@ -3009,8 +3017,7 @@ int enqueue_batch_step(DecodeBatch &b) {
                            kSlice, b.rst);
         HIP_TRY(hipGetLastError());
     }
-    for (int base = 0; base < b.ng && !(wide && b.ng > kMaxNV && (b.logits || head_wide_ok(m->lm)));
-         base += kMaxNV) {
+    for (int base = 0; base < b.ng && !head_wide && !(wide && b.ng > kMaxNV && b.logits); base += kMaxNV) {
         const int left = b.ng - base;
         const int nv = left == 1 ? 1 : (left == 2 ? 2 : 4);
         GemvParams lm = gemv_params_1(m->lm);
@@ -3045,8 +3052,8 @@ int32_t pending_token(const StepState &hs) {
     return (int32_t)(0xFFFFFFFFu - (uint32_t)(argmax_of(hs) & 0xFFFFFFFFull));
 }
 
-// vector buffers for b.cap rows; with cap > 4 also the wide step's digit
-// planes (16 rows of the widest input) and row-state table
+// vector buffers for b.cap rows; from kBatchWideHeadMin rows also digit planes
+// (16 rows of the widest input), with cap > 4 the wide step's row-state table
 int batch_alloc(DecodeBatch &b) {
     const pocr_config &c = b.m->cfg;
     const size_t H = c.hidden, Q = (size_t)c.heads * c.head_dim, KV = (size_t)c.kv_heads * c.head_dim;
@@ -3060,12 +3067,14 @@ int batch_alloc(DecodeBatch &b) {
     }
     HIP_TRY(hipMalloc(&b.pad, sizeof(StepState)));
     HIP_TRY(hipMemsetAsync(b.pad, 0, sizeof(StepState), s));
-    if (rows > (size_t)kMaxNV) {
+    if (rows >= (size_t)kBatchWideHeadMin) {
         const size_t kmax = std::max(std::max(H, Q), (size_t)c.intermediate);
         HIP_TRY(hipMalloc(&b.xd, 3 * 16 * kmax));
         HIP_TRY(hipMemsetAsync(b.xd, 0, 3 * 16 * kmax, s));
         HIP_TRY(hipMalloc(&b.xs, 16 * sizeof(float)));
         HIP_TRY(hipMalloc(&b.xb, 16 * 4 * sizeof(int)));
+    }
+    if (rows > (size_t)kMaxNV) {
         HIP_TRY(hipMalloc(&b.rst, kMaxBatch * sizeof(StepState *)));
         if (gemm_small_ok(c.vocab, c.hidden)) HIP_TRY(hipMalloc(&b.logits, (size_t)16 * c.vocab * 4));
     }
