@@ -595,7 +595,10 @@ struct HeadWideParams {
     StepState *st[kHeadWideVec];  // argmax slots of vector v (null: no argmax)
 };
 
-template <int QT, int NS>
+// PK (up to 5 vectors): one B tile holds every (vector, plane) pair, column
+// 3v + pl, so one MFMA per A operand instead of one per plane; the lane of
+// column 3v gathers planes 1 and 2 from its two neighbours for the finish.
+template <int QT, int NS, bool PK>
 __global__ void __launch_bounds__(kThreads, 2) k_head_wide(HeadWideParams p) {
     static_assert(QT == QT_Q4 || QT == QT_Q8, "codes in 16-byte pieces of 16 or 32 columns");
     using SH = HeadWideShape<QT, NS>;
@@ -676,12 +679,16 @@ __global__ void __launch_bounds__(kThreads, 2) k_head_wide(HeadWideParams p) {
     // the rotated other half elsewhere, and K slice lg of set par is piece
     // 2·lg + par: columns 8·CP·ln + 2·CP·lg + CP·par + 16·h for step h.
     // B column lr = vector lr.
-    v4i acc[R][3];
+    constexpr int NA = PK ? 1 : 3;  // accumulators (B tiles) per row block
+    v4i acc[R][NA];
 #pragma unroll
     for (int rb = 0; rb < R; ++rb)
 #pragma unroll
-        for (int pl = 0; pl < 3; ++pl) acc[rb][pl] = v4i{0, 0, 0, 0};
+        for (int pl = 0; pl < NA; ++pl) acc[rb][pl] = v4i{0, 0, 0, 0};
     const int bit3 = (lane >> 3) & 1;
+    // PK: column lr = vector lr/3, plane lr%3 (column 15 repeats column 14 and
+    // is never read into a score)
+    const int pk_off = ((min(lr, 14) % 3) * 4 + lg) * 256 + (min(lr, 14) / 3) * 16;
 #pragma unroll
     for (int ln = 0; ln < LINES; ++ln)
 #pragma unroll
@@ -700,10 +707,14 @@ __global__ void __launch_bounds__(kThreads, 2) k_head_wide(HeadWideParams p) {
 #pragma unroll
             for (int h = 0; h < SPL; ++h) {
                 const int st = (ln * 2 + par) * SPL + h;
-                v4i b[3];  // lane (lr, lg): vector lr's K slice lg, 16 consecutive bytes per lane
+                v4i b[NA];  // lane (lr, lg): vector lr's K slice lg, 16 consecutive bytes per lane
+                if constexpr (PK) {
+                    b[0] = *reinterpret_cast<const v4i *>(xdig + st * 3 * 1024 + pk_off);
+                } else {
 #pragma unroll
-                for (int pl = 0; pl < 3; ++pl)
-                    b[pl] = *reinterpret_cast<const v4i *>(xdig + (st * 3 + pl) * 1024 + 16 * lane);
+                    for (int pl = 0; pl < 3; ++pl)
+                        b[pl] = *reinterpret_cast<const v4i *>(xdig + (st * 3 + pl) * 1024 + 16 * lane);
+                }
 #pragma unroll
                 for (int rb = 0; rb < R; ++rb) {
                     RawCodes<QT> rc;
@@ -716,16 +727,32 @@ __global__ void __launch_bounds__(kThreads, 2) k_head_wide(HeadWideParams p) {
                     }
                     const v4i a = unpack_codes16<QT>(rc);
 #pragma unroll
-                    for (int pl = 0; pl < 3; ++pl)
+                    for (int pl = 0; pl < NA; ++pl)
                         acc[rb][pl] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b[pl], acc[rb][pl], 0, 0, 0);
                 }
             }
         }
 
     // 4. lane (lr, lg) holds C[4lg + i][lr]: rows r0 + 16rb + 4lg + i of
-    // vector lr.  Scores as k_head_mfma forms them.
-    const int v = lr;
-    const bool live = v < nvec;
+    // vector lr (PK: of vector lr/3, plane lr%3; the lane of plane 0 takes
+    // planes 1 and 2 from lanes lane + 1 and lane + 2).  Scores as k_head_mfma
+    // forms them.
+    int pls[R][3][4];
+#pragma unroll
+    for (int rb = 0; rb < R; ++rb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if constexpr (PK) {
+                pls[rb][0][i] = acc[rb][0][i];
+                pls[rb][1][i] = __shfl(acc[rb][0][i], min(lane + 1, 63), 64);
+                pls[rb][2][i] = __shfl(acc[rb][0][i], min(lane + 2, 63), 64);
+            } else {
+#pragma unroll
+                for (int pl = 0; pl < 3; ++pl) pls[rb][pl][i] = acc[rb][pl < NA ? pl : 0][i];
+            }
+        }
+    const int v = PK ? lr / 3 : lr;
+    const bool live = v < nvec && (!PK || (lr % 3 == 0 && lr < 15));
     int b0 = 0, b1 = 0, b2 = 0;
     float my_sx = 1.0f;
     if (live) {
@@ -742,9 +769,9 @@ __global__ void __launch_bounds__(kThreads, 2) k_head_wide(HeadWideParams p) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             // |Σ u·d| < 2^24 per plane (cols ≤ 2048): exact converts
-            const float f0 = (float)(acc[rb][0][i] - b0);
-            const float f1 = (float)(acc[rb][1][i] - b1);
-            const float f2 = (float)(acc[rb][2][i] - b2);
+            const float f0 = (float)(pls[rb][0][i] - b0);
+            const float f1 = (float)(pls[rb][1][i] - b1);
+            const float f2 = (float)(pls[rb][2][i] - b2);
             sc[i] = fmaf(f2, 1.0f / 16384.0f, fmaf(f1, 1.0f / 128.0f, f0)) * my_sx * rsc[rb][i];
             if (live && rr + i < rows) {
                 const unsigned long long k = argmax_key(sc[i], rr + i);
@@ -769,7 +796,7 @@ __global__ void __launch_bounds__(kThreads, 2) k_head_wide(HeadWideParams p) {
         const unsigned long long o32 = shfl_xor_u64(key, 32);
         key = o32 > key ? o32 : key;
     }
-    if (lg == 0) kred[lr][wave] = key;
+    if (lg == 0 && (!PK || (lr % 3 == 0 && lr < 15))) kred[v][wave] = key;
     __syncthreads();
     if ((int)threadIdx.x < nvec) {
         const int vv = threadIdx.x;

@@ -524,15 +524,21 @@ static int launch_head(hipStream_t s, const void *fn, const GemvParams &p, int p
 // boundaries.
 struct HeadWidePlan {
     const void *digits = nullptr, *head = nullptr;
+    const void *head_few = nullptr;  // up to kHeadPackedVec vectors (Q4/Q8: one B tile for all planes)
     int rows_per_wg = 0, plane_bytes = 0;
 };
+constexpr int kHeadPackedVec = 5;  // (vector, plane) pairs in one 16-column B tile
 
 template <int QT, int NS>
 static HeadWidePlan head_wide_plan() {
     HeadWidePlan h;
     h.digits = reinterpret_cast<const void *>(&k_head_digits<QT, NS>);
-    if constexpr (QT == QT_Q6) h.head = reinterpret_cast<const void *>(&k_head_wide_q6<NS>);
-    else h.head = reinterpret_cast<const void *>(&k_head_wide<QT, NS>);
+    if constexpr (QT == QT_Q6) {
+        h.head = h.head_few = reinterpret_cast<const void *>(&k_head_wide_q6<NS>);
+    } else {
+        h.head = reinterpret_cast<const void *>(&k_head_wide<QT, NS, false>);
+        h.head_few = reinterpret_cast<const void *>(&k_head_wide<QT, NS, true>);
+    }
     h.rows_per_wg = HeadWideShape<QT, NS>::ROWS_PER_WG;
     h.plane_bytes = HeadWideShape<QT, NS>::PLANE_BYTES;
     return h;
@@ -592,8 +598,8 @@ int pocr::launch_head_wide(hipStream_t s, const pocr_weight *w, const float *x, 
     h.out_vec4 = out && ((uintptr_t)out % 16 == 0) && out_stride % 4 == 0 && h.rows % 16 == 0;
     for (int v = 0; v < kHeadWideVec; ++v) h.st[v] = (st && v < nvec) ? st[v] : nullptr;
     void *args[] = {&h};
-    HIP_TRY(hipLaunchKernel(plan.head, dim3((h.rows + plan.rows_per_wg - 1) / plan.rows_per_wg), dim3(kThreads), args,
-                            0, s));
+    HIP_TRY(hipLaunchKernel(nvec <= kHeadPackedVec ? plan.head_few : plan.head,
+                            dim3((h.rows + plan.rows_per_wg - 1) / plan.rows_per_wg), dim3(kThreads), args, 0, s));
     return POCR_OK;
 }
 

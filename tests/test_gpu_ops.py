@@ -151,7 +151,7 @@ def test_matvec_argmax_planted_near_tie(ctx, orc, qtype):
 
 
 @pytest.mark.parametrize("qtype", [Q8, Q4, Q6], ids=["q8", "q4", "q6"])
-@pytest.mark.parametrize("m", [2, 3, 5, 16, 17])
+@pytest.mark.parametrize("m", [2, 3, 4, 5, 6, 16, 17])
 def test_lm_head_rows_on_matrix_cores(ctx, orc, qtype, m):
     """M rows of x against the 103424×1024 LM head: up to 16 rows per weight
     pass on the matrix cores.  Each row's scores are what the MFMA greedy head
