@@ -821,12 +821,13 @@ __global__ void __launch_bounds__(kThreads, 2) k_head_wide(HeadWideParams p) {
 // and reads A back as row lr, piece 4k + lg for MFMA step k of the unit.
 // Loading 16 rows × 48 bytes per instruction, which is the A operand as
 // loaded, streamed at half the rate.
-// B column lr = vector lr (one tile per digit plane); a wave owns R blocks of
-// 16 rows over all the columns, so no cross-wave sums.  Scores, argmax and
+// B column lr = vector lr (one tile per digit plane), or with PK (up to 5
+// vectors) column 3v + pl in one tile, as in k_head_wide; a wave owns R blocks
+// of 16 rows over all the columns, so no cross-wave sums.  Scores, argmax and
 // digit planes (k_head_digits, Q6 plane order: step c/64, K slice (c%64)/16)
 // as k_head_wide.
 // ---------------------------------------------------------------------------
-template <int NS>
+template <int NS, bool PK>
 __global__ void __launch_bounds__(kThreads, 2) k_head_wide_q6(HeadWideParams p) {
     using SH = HeadWideShape<QT_Q6, NS>;
     constexpr int STEPS = SH::STEPS, R = SH::R;
@@ -913,11 +914,13 @@ __global__ void __launch_bounds__(kThreads, 2) k_head_wide_q6(HeadWideParams p) 
 
     // 3. the MFMAs: A = row lr's codes of step st, K slice lg; B column lr =
     // vector lr's digits of the same 16 columns
-    v4i acc[R][3];
+    constexpr int NA = PK ? 1 : 3;  // accumulators (B tiles) per row block, as in k_head_wide
+    v4i acc[R][NA];
 #pragma unroll
     for (int rb = 0; rb < R; ++rb)
 #pragma unroll
-        for (int pl = 0; pl < 3; ++pl) acc[rb][pl] = v4i{0, 0, 0, 0};
+        for (int pl = 0; pl < NA; ++pl) acc[rb][pl] = v4i{0, 0, 0, 0};
+    const int pk_off = ((min(lr, 14) % 3) * 4 + lg) * 256 + (min(lr, 14) / 3) * 16;
 #pragma unroll
     for (int u = 0; u < UNITS; ++u) {
         // this unit of the wave's rows into its LDS tile: row 4g + L/16,
@@ -934,10 +937,14 @@ __global__ void __launch_bounds__(kThreads, 2) k_head_wide_q6(HeadWideParams p) 
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             const int st = 4 * u + k;
-            v4i b[3];
+            v4i b[NA];
+            if constexpr (PK) {
+                b[0] = *reinterpret_cast<const v4i *>(xdig + st * 3 * 1024 + pk_off);
+            } else {
 #pragma unroll
-            for (int pl = 0; pl < 3; ++pl)
-                b[pl] = *reinterpret_cast<const v4i *>(xdig + (st * 3 + pl) * 1024 + 16 * lane);
+                for (int pl = 0; pl < 3; ++pl)
+                    b[pl] = *reinterpret_cast<const v4i *>(xdig + (st * 3 + pl) * 1024 + 16 * lane);
+            }
 #pragma unroll
             for (int rb = 0; rb < R; ++rb) {
                 // row lr, piece 4k + lg: columns 64·st + 16·lg .. +15
@@ -947,7 +954,7 @@ __global__ void __launch_bounds__(kThreads, 2) k_head_wide_q6(HeadWideParams p) 
                 for (int w = 0; w < 3; ++w) rc.d[w] = a3[w];
                 const v4i a = unpack_codes16<QT_Q6>(rc);
 #pragma unroll
-                for (int pl = 0; pl < 3; ++pl)
+                for (int pl = 0; pl < NA; ++pl)
                     acc[rb][pl] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b[pl], acc[rb][pl], 0, 0, 0);
             }
         }
@@ -955,9 +962,24 @@ __global__ void __launch_bounds__(kThreads, 2) k_head_wide_q6(HeadWideParams p) 
     }
 
     // 4. lane (lr, lg) holds C[4lg + i][lr]: rows r0 + 16rb + 4lg + i of
-    // vector lr.  Scores as k_head_mfma forms them.
-    const int v = lr;
-    const bool live = v < nvec;
+    // vector lr (PK: vector lr/3, plane lr%3, gathered as in k_head_wide).
+    // Scores as k_head_mfma forms them.
+    int pls[R][3][4];
+#pragma unroll
+    for (int rb = 0; rb < R; ++rb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if constexpr (PK) {
+                pls[rb][0][i] = acc[rb][0][i];
+                pls[rb][1][i] = __shfl(acc[rb][0][i], min(lane + 1, 63), 64);
+                pls[rb][2][i] = __shfl(acc[rb][0][i], min(lane + 2, 63), 64);
+            } else {
+#pragma unroll
+                for (int pl = 0; pl < 3; ++pl) pls[rb][pl][i] = acc[rb][pl < NA ? pl : 0][i];
+            }
+        }
+    const int v = PK ? lr / 3 : lr;
+    const bool live = v < nvec && (!PK || (lr % 3 == 0 && lr < 15));
     int b0 = 0, b1 = 0, b2 = 0;
     float my_sx = 1.0f;
     if (live) {
@@ -974,9 +996,9 @@ __global__ void __launch_bounds__(kThreads, 2) k_head_wide_q6(HeadWideParams p) 
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             // |Σ u·d| < 2^24 per plane (cols ≤ 2048): exact converts
-            const float f0 = (float)(acc[rb][0][i] - b0);
-            const float f1 = (float)(acc[rb][1][i] - b1);
-            const float f2 = (float)(acc[rb][2][i] - b2);
+            const float f0 = (float)(pls[rb][0][i] - b0);
+            const float f1 = (float)(pls[rb][1][i] - b1);
+            const float f2 = (float)(pls[rb][2][i] - b2);
             sc[i] = fmaf(f2, 1.0f / 16384.0f, fmaf(f1, 1.0f / 128.0f, f0)) * my_sx * rsc[rb][i];
             if (live && rr + i < rows) {
                 const unsigned long long k = argmax_key(sc[i], rr + i);
@@ -1000,7 +1022,7 @@ __global__ void __launch_bounds__(kThreads, 2) k_head_wide_q6(HeadWideParams p) 
         const unsigned long long o32 = shfl_xor_u64(key, 32);
         key = o32 > key ? o32 : key;
     }
-    if (lg == 0) kred[lr][wave] = key;
+    if (lg == 0 && (!PK || (lr % 3 == 0 && lr < 15))) kred[v][wave] = key;
     __syncthreads();
     if ((int)threadIdx.x < nvec) {
         const int vv = threadIdx.x;

@@ -524,7 +524,7 @@ static int launch_head(hipStream_t s, const void *fn, const GemvParams &p, int p
 // boundaries.
 struct HeadWidePlan {
     const void *digits = nullptr, *head = nullptr;
-    const void *head_few = nullptr;  // up to kHeadPackedVec vectors (Q4/Q8: one B tile for all planes)
+    const void *head_few = nullptr;  // up to kHeadPackedVec vectors: one B tile for all planes
     int rows_per_wg = 0, plane_bytes = 0;
 };
 constexpr int kHeadPackedVec = 5;  // (vector, plane) pairs in one 16-column B tile
@@ -534,7 +534,8 @@ static HeadWidePlan head_wide_plan() {
     HeadWidePlan h;
     h.digits = reinterpret_cast<const void *>(&k_head_digits<QT, NS>);
     if constexpr (QT == QT_Q6) {
-        h.head = h.head_few = reinterpret_cast<const void *>(&k_head_wide_q6<NS>);
+        h.head = reinterpret_cast<const void *>(&k_head_wide_q6<NS, false>);
+        h.head_few = reinterpret_cast<const void *>(&k_head_wide_q6<NS, true>);
     } else {
         h.head = reinterpret_cast<const void *>(&k_head_wide<QT, NS, false>);
         h.head_few = reinterpret_cast<const void *>(&k_head_wide<QT, NS, true>);
