@@ -175,8 +175,12 @@ extern "C" void pocr_ctx_destroy(pocr_ctx *ctx) { ctx_release(ctx); }
 static bool valid_qtype(int q) { return q == POCR_Q8 || q == POCR_Q4 || q == POCR_Q6; }
 
 // Q6 matrices of LM-head size (the shapes the greedy heads take) also keep
-// their rows in the heads' load order (head.hpp, k_head_image_q6)
+// their rows in the heads' load order (head.hpp, k_head_image_q6);
+// POCR_HEAD_IMAGE=0 at upload leaves a weight without it (the heads then read
+// the rows)
 static bool head_image_ok(int qtype, int rows, int cols) {
+    const char *env = getenv("POCR_HEAD_IMAGE");
+    if (env && env[0] == '0') return false;
     return qtype == POCR_Q6 && (cols == 1024 || cols == 2048) && rows >= kHeadWideMinRows;
 }
 static size_t head_image_bytes(int rows, size_t row_bytes) { return (size_t)(rows + 15) / 16 * 16 * row_bytes; }

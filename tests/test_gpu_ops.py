@@ -234,6 +234,26 @@ def test_q6_head_image_ragged_rows(ctx, orc, cols, m):
     assert np.all(np.isfinite(got[:, -5:]))
 
 
+def test_q6_head_image_matches_rows(ctx, monkeypatch):
+    """The Q6 heads read the same bytes from the upload-time image as from the
+    rows (POCR_HEAD_IMAGE=0 uploads without the image): scores and greedy picks
+    at M = 1, 4 and 16 agree to the bit, for 1024 and 2048 columns."""
+    for cols in (1024, 2048):
+        rng = np.random.default_rng(cols)
+        q = _qmat(rng, 16400, cols, Q6)
+        x = rng.standard_normal((16, cols)).astype(np.float32)
+        monkeypatch.setenv("POCR_HEAD_IMAGE", "0")
+        w_rows = ctx.upload(q)
+        monkeypatch.delenv("POCR_HEAD_IMAGE")
+        w_img = ctx.upload(q)
+        for m in (1, 4, 16):
+            a = ctx.matvec(w_rows, x[:m])
+            b = ctx.matvec(w_img, x[:m])
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), (cols, m)
+        for i in range(2):
+            assert ctx.matvec_argmax(w_rows, x[i]) == ctx.matvec_argmax(w_img, x[i]), (cols, i)
+
+
 def test_argmax_ties_pick_lowest_index(ctx):
     # identical rows give bit-identical scores: ties → lowest index
     w = np.zeros((64, 32), np.float32)
