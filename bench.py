@@ -369,13 +369,28 @@ def attention_sweep(ctx, cfg):
     return out
 
 
-def lm_head_q4(cfg, seed=0):
-    """The Q4 LM head of the synthetic 0.3B weights (same draw as make_weights)."""
+def lm_head_q4(cfg, seed=0, qtype=None):
+    """The Q4 (or qtype) LM head of the synthetic 0.3B weights (same draw as make_weights)."""
     from rapidocrvl_amd import lib, synth
 
+    qt = lib.Q4 if qtype is None else qtype
     lm = synth.normal((cfg.vocab, cfg.hidden), [seed, 1000, 0])
-    s, p = lib.quantize_rows(lib.Q4, lm)
-    return lib.QMatrix(lib.Q4, cfg.vocab, cfg.hidden, s, p)
+    s, p = lib.quantize_rows(qt, lm)
+    return lib.QMatrix(qt, cfg.vocab, cfg.hidden, s, p)
+
+
+def q6_head(ctx, cfg):
+    """The Q6 greedy LM head (the 4-sequence Q6 decode's head at M = 1), timed as
+    the Q4 roofline kernel is, with the lean read of the same bytes beside it."""
+    from rapidocrvl_amd import lib
+
+    lmq = lm_head_q4(cfg, qtype=lib.Q6)
+    us, alg, achieved = lm_head_roofline(ctx, lmq)
+    stream_us = stream_read_ceiling(ctx, int(alg))
+    return {"kernel": "k_head_mfma: q6 lm_head greedy head 103424x1024 m=1 (rows from the head image)",
+            "us_per_launch": round(us, 3), "algorithmic_bytes": int(alg), "achieved_GB_s": round(achieved, 1),
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "stream_read_us": round(stream_us, 3),
+            "frac_of_stream_read": round(stream_us / us, 4)}
 
 
 def lm_head_roofline(ctx, lmq, target_bytes=600 << 20):
@@ -722,6 +737,7 @@ def main():
     ap.add_argument("--no-q8", action="store_true")
     ap.add_argument("--roofline-only", action="store_true", help="time only the Q4 LM-head GEMV rotation")
     ap.add_argument("--calibrate-copy", action="store_true", help="with --roofline-only: add a 512 MiB copy")
+    ap.add_argument("--q6-head-only", action="store_true", help="time only the Q6 greedy LM head and its lean read")
     ap.add_argument("--prefill-only", action="store_true", help="time only the 1345-token Q4 image prefill")
     ap.add_argument("--decode-only", action="store_true",
                     help="time only the prefill and the Q4 greedy decode (the kernel sequence the profiles trace)")
@@ -749,6 +765,12 @@ def main():
         sys.exit(2)
     if args.roofline_only:
         roofline_only(args)
+        return
+    if args.q6_head_only:
+        from rapidocrvl_amd import lib
+        from rapidocrvl_amd.config import ERNIE_0P3B as cfg
+
+        print(json.dumps(q6_head(lib.Context(0), cfg)), flush=True)
         return
 
     from rapidocrvl_amd import lib, synth
@@ -894,6 +916,8 @@ def main():
     if not args.no_sweep:
         extra["gemv_sweep"] = gemv_sweep(ctx, np.random.default_rng(0))
         extra["attention_sweep"] = attention_sweep(ctx, cfg)
+        extra["q6_lm_head"] = q6_head(ctx, cfg)
+        log(f"[bench] q6 lm_head {extra['q6_lm_head']}")
 
     per_token_bytes = 181_542_912 + 36_864 * (n_prefix + args.decode_tokens // 2)
     result = {
