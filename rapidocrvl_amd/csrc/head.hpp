@@ -463,7 +463,8 @@ constexpr int kHeadWideVec = 16;
 #define POCR_HEAD_WIDE_LANE_BYTES 512  // weight bytes a lane requests at once
 #endif
 
-template <int QT, int NS>
+// LB: weight bytes a lane requests at once (R row blocks of 16 rows per wave)
+template <int QT, int NS, int LB = POCR_HEAD_WIDE_LANE_BYTES>
 struct HeadWideShape {
     static constexpr int COLS = 256 * NS;
     static constexpr int ROW_BYTES = QT == QT_Q4 ? COLS / 2 : (QT == QT_Q6 ? COLS / 4 * 3 : COLS);
@@ -473,7 +474,7 @@ struct HeadWideShape {
     // MFMA steps of 64 columns
     static constexpr int STEPS = QT == QT_Q6 ? COLS / 64 : LINES * 2 * SPL;
     static constexpr int PLANE_BYTES = STEPS * 3 * 4 * kHeadWideVec * 16;
-    static constexpr int R0 = POCR_HEAD_WIDE_LANE_BYTES * 4 / ROW_BYTES;
+    static constexpr int R0 = LB * 4 / ROW_BYTES;
     static constexpr int R = R0 > 1 ? R0 : 1;  // row blocks per wave
     static constexpr int ROWS_PER_WG = 16 * R * kWaves;
 };
@@ -598,10 +599,21 @@ struct HeadWideParams {
 // PK (up to 5 vectors): one B tile holds every (vector, plane) pair, column
 // 3v + pl, so one MFMA per A operand instead of one per plane; the lane of
 // column 3v gathers planes 1 and 2 from its two neighbours for the finish.
+// Row blocks per wave: with few vectors the finish is short, so the Q4 head of
+// 1024 columns takes 2 blocks per wave (twice the workgroups; M = 3-5 on the
+// 103424-row head 19.1-19.4 -> 18.1-18.5 us), and 4 otherwise (M = 16: 22.5
+// against 23.2 us with 2).
+template <int QT, int NS, bool PK>
+constexpr int head_wide_lane_bytes() {
+    return (PK && QT == QT_Q4 && NS == 4) ? POCR_HEAD_WIDE_LANE_BYTES / 2 : POCR_HEAD_WIDE_LANE_BYTES;
+}
+template <int QT, int NS, bool PK>
+using HeadWideShapeK = HeadWideShape<QT, NS, head_wide_lane_bytes<QT, NS, PK>()>;
+
 template <int QT, int NS, bool PK>
 __global__ void __launch_bounds__(kThreads, 2) k_head_wide(HeadWideParams p) {
     static_assert(QT == QT_Q4 || QT == QT_Q8, "codes in 16-byte pieces of 16 or 32 columns");
-    using SH = HeadWideShape<QT, NS>;
+    using SH = HeadWideShapeK<QT, NS, PK>;
     constexpr int LINES = SH::LINES, R = SH::R, CP = SH::CP, SPL = SH::SPL;
     constexpr int NV = kHeadWideVec;
     static_assert(R >= 1 && LINES >= 1, "rows of whole 128-byte lines");

@@ -529,7 +529,7 @@ static int launch_head(hipStream_t s, const void *fn, const GemvParams &p, int p
 struct HeadWidePlan {
     const void *digits = nullptr, *head = nullptr;
     const void *head_few = nullptr;  // up to kHeadPackedVec vectors: one B tile for all planes
-    int rows_per_wg = 0, plane_bytes = 0;
+    int rows_per_wg = 0, rows_per_wg_few = 0, plane_bytes = 0;
 };
 constexpr int kHeadPackedVec = 5;  // (vector, plane) pairs in one 16-column B tile
 
@@ -544,7 +544,12 @@ static HeadWidePlan head_wide_plan() {
         h.head = reinterpret_cast<const void *>(&k_head_wide<QT, NS, false>);
         h.head_few = reinterpret_cast<const void *>(&k_head_wide<QT, NS, true>);
     }
-    h.rows_per_wg = HeadWideShape<QT, NS>::ROWS_PER_WG;
+    if constexpr (QT == QT_Q6) {
+        h.rows_per_wg = h.rows_per_wg_few = HeadWideShape<QT, NS>::ROWS_PER_WG;
+    } else {
+        h.rows_per_wg = HeadWideShapeK<QT, NS, false>::ROWS_PER_WG;
+        h.rows_per_wg_few = HeadWideShapeK<QT, NS, true>::ROWS_PER_WG;
+    }
     h.plane_bytes = HeadWideShape<QT, NS>::PLANE_BYTES;
     return h;
 }
@@ -603,8 +608,10 @@ int pocr::launch_head_wide(hipStream_t s, const pocr_weight *w, const float *x, 
     h.out_vec4 = out && ((uintptr_t)out % 16 == 0) && out_stride % 4 == 0 && h.rows % 16 == 0;
     for (int v = 0; v < kHeadWideVec; ++v) h.st[v] = (st && v < nvec) ? st[v] : nullptr;
     void *args[] = {&h};
-    HIP_TRY(hipLaunchKernel(nvec <= kHeadPackedVec ? plan.head_few : plan.head,
-                            dim3((h.rows + plan.rows_per_wg - 1) / plan.rows_per_wg), dim3(kThreads), args, 0, s));
+    const bool few = nvec <= kHeadPackedVec;
+    const int rows_per_wg = few ? plan.rows_per_wg_few : plan.rows_per_wg;
+    HIP_TRY(hipLaunchKernel(few ? plan.head_few : plan.head, dim3((h.rows + rows_per_wg - 1) / rows_per_wg),
+                            dim3(kThreads), args, 0, s));
     return POCR_OK;
 }
 
