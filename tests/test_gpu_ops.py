@@ -234,6 +234,32 @@ def test_q6_head_image_ragged_rows(ctx, orc, cols, m):
     assert np.all(np.isfinite(got[:, -5:]))
 
 
+@pytest.mark.parametrize("qtype", [Q8, Q4, Q6], ids=["q8", "q4", "q6"])
+@pytest.mark.parametrize("m", [3, 5, 16])
+def test_lm_head_rows_2048_columns(ctx, orc, qtype, m):
+    """The M-row heads at 2,048 columns (the 16-vector tiles and, up to 5
+    rows, the packed one): every row within the oracle's f32 bar, each row's
+    best score and row those of the single-vector head to the bit, and, where
+    the digit model's f32 plane sums are exact (Q4, Q6), the scores it gives."""
+    rng = np.random.default_rng(90 + m)
+    q = _qmat(rng, 16400, 2048, qtype)
+    w = ctx.upload(q)
+    x = rng.standard_normal((m, 2048)).astype(np.float32)
+    x[1] *= np.float32(1e-3)
+    got = ctx.matvec(w, x)
+    codes = lib.unpack_rows(qtype, q.packed, q.cols)
+    exact_model = qtype != Q8
+    if exact_model:
+        dig, mag = dm.head_scores_rows(codes, q.scales, x)
+    for i in range(m):
+        _close(got[i], orc.matvec(qtype, q.scales, q.packed, x[i]))
+        if exact_model:
+            assert np.all(np.abs(got[i] - dig[i]) <= F32_STEPS[qtype] * mag[i]), i
+        idx, score = ctx.matvec_argmax(w, x[i])
+        assert int(np.argmax(got[i])) == idx, i
+        assert got[i][idx] == np.float32(score), i
+
+
 def test_q6_head_image_matches_rows(ctx, monkeypatch):
     """The Q6 heads read the same bytes from the upload-time image as from the
     rows (POCR_HEAD_IMAGE=0 uploads without the image): scores and greedy picks
